@@ -1,0 +1,154 @@
+/*
+ * dsa_mi355x.h - C ABI of the MI355X (gfx950) DeepSeek sparse-attention (DSA) kernels.
+ *
+ * Every entry point takes raw device pointers, int64 sizes, scalar parameters and a
+ * hipStream_t passed as void*.  It enqueues work asynchronously on that stream and
+ * returns DSA_OK (0) or a non-zero dsa_status; it never throws.  On error the message
+ * is available from dsa_last_error() (thread-local).  The caller owns every buffer.
+ * Tensors are dense row-major ("BSND" in the reference's terms) unless a leading
+ * dimension argument says otherwise.
+ *
+ * Reference interfaces each entry point replaces (paths relative to the
+ * torchtitan-npu reference repository):
+ *   dsa_indexer_fwd + dsa_topk   torch_npu.npu_lightning_indexer
+ *                                (converters/kernels/dsa.py:217-226;
+ *                                 ops/aclnn/lightning_indexer/binding.cpp:12-36)
+ *   dsa_sparse_mla_fwd           torch_npu.npu_sparse_flash_attention, attention_mode=2
+ *                                (converters/kernels/dsa.py:238-253;
+ *                                 ops/aclnn/sparse_attn_sharedkv/binding.cpp:30-60)
+ *   dsa_sparse_mla_bwd           its autograd backward / npu_sparse_attn_sharedkv_grad
+ *                                (ops/aclnn/sparse_attn_sharedkv/binding.cpp:62-88)
+ *   dsa_attn_mass +
+ *   dsa_indexer_kl_grad          torch_npu.npu_sparse_lightning_indexer_grad_kl_loss
+ *                                (converters/kernels/dsa.py:159-177;
+ *                                 ops/aclnn/sparse_lightning_indexer_grad_kl_loss/binding.cpp:12-36)
+ *   dsa_compressor_fwd           Compressor._forward_bsnd pooling + RMSNorm
+ *                                (models/deepseek_v4/model.py:183-221; torch-only in the reference)
+ */
+#ifndef DSA_MI355X_H
+#define DSA_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum dsa_dtype { DSA_F32 = 0, DSA_BF16 = 1, DSA_FP8_E4M3 = 2 };
+
+enum dsa_status {
+  DSA_OK = 0,
+  DSA_ERR_INVALID_ARG = 1,   /* null pointer, bad size, unsupported combination */
+  DSA_ERR_LAUNCH = 2,        /* the HIP runtime reported an error */
+  DSA_ERR_UNSUPPORTED = 3    /* valid request this build does not implement */
+};
+
+/* Thread-local text of the last error (empty string if none). */
+const char* dsa_last_error(void);
+/* ABI version of this library (bumped on any signature change). */
+int dsa_abi_version(void);
+
+/*
+ * Lightning-indexer scores (reference: bf16_index, models/deepseek_v32/model.py:224-236;
+ * LiCompute, models/deepseek_v4/model.py:647-652).
+ *   scores[b, s, t] = k_scale[b,t] * sum_h w[b,s,h] * q_scale[b,s,h] * relu(q[b,s,h,:] . k[b,t,:])
+ * for t < (s + q_offset + 1) / cmp_ratio, and -inf for every other t < s_k.
+ *   q        [B, S, H_I, D_I]   bf16 or fp8-e4m3 (q_dtype)
+ *   q_scale  [B, S, H_I] fp32 or NULL (== 1)
+ *   k        [B, S_k, D_I]      same dtype as q
+ *   k_scale  [B, S_k] fp32 or NULL (== 1)
+ *   w        [B, S, H_I] fp32
+ *   scores   [B, S, ld_scores] fp32, ld_scores >= S_k
+ * D_I must be 128 (MFMA path) ; H_I a multiple of 16 and <= 128.
+ */
+int dsa_indexer_fwd(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
+                    float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                    int64_t head_dim, int64_t ld_scores, int64_t q_offset, int64_t cmp_ratio, void* stream);
+
+/*
+ * Per-row top-k of fp32 scores (reference: DSV32_SDPA.forward topk,
+ * models/deepseek_v32/model.py:389-395; LiCompute, models/deepseek_v4/model.py:653-655).
+ * Row (b, s) considers candidates t < min(s_k, (s + q_offset + 1) / cmp_ratio) whose score is
+ * not NaN; it keeps the first k of a stable descending order by (score, lower index) with
+ * -0.0 == +0.0.  indices[b, s, :] receive the chosen t + index_offset in ascending t order,
+ * padded with -1; values (optional) the matching scores, -inf in padded slots.
+ *   scores  [B, S, ld_scores] fp32; indices [B, S, k] int32; values [B, S, k] fp32 or NULL.
+ * k <= 4096.
+ */
+int dsa_topk(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
+             int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset,
+             void* stream);
+
+/*
+ * Gathered sparse MLA attention forward (reference: npu_sparse_flash_attention with
+ * attention_mode=2, converters/kernels/dsa.py:238-253; torch-native semantics
+ * models/deepseek_v32/model.py:391-404).
+ *   q        [B, S, H, D_qk]   (D_qk = latent D_v + rope)
+ *   kv       [B, S_kv, D_qk]   one shared latent KV head; v = kv[..., :D_v]
+ *   indices  [B, S, K] int32; slot j of row s is used iff 0 <= idx <= s + q_offset and idx < S_kv
+ *   out      [B, S, H, D_v]
+ *   softmax_max [B, S, H] fp32: max_j scale*q.k_j (natural-log units), -inf if no valid slot
+ *   softmax_sum [B, S, H] fp32: sum_j exp(scale*q.k_j - softmax_max)
+ * dtype DSA_BF16: MFMA path (requires D_qk = 576, D_v = 512); DSA_F32: exact fp32 path.
+ */
+int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, void* out, float* softmax_max,
+                       float* softmax_sum, int dtype, int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
+                       int64_t d_qk, int64_t d_v, int64_t topk, float scale, int64_t q_offset, void* stream);
+
+/*
+ * Backward of dsa_sparse_mla_fwd (reference: SparseAttnSharedKV.backward,
+ * converters/kernels/npu_smla.py:303-348 -> sparse_attn_sharedkv/binding.cpp:62-88).
+ *   dq        [B, S, H, D_qk]  same dtype as q (written)
+ *   dkv_accum [B, S_kv, D_qk]  fp32, ACCUMULATED into (caller zeroes it); latent alias:
+ *             dkv[:, :D_v] = dK_nope + dV, dkv[:, D_v:] = dK_rope
+ *   workspace fp32, at least dsa_sparse_mla_bwd_workspace_size() bytes
+ */
+int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t topk);
+int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out, const void* dout,
+                       const float* softmax_max, const float* softmax_sum, void* dq, float* dkv_accum,
+                       void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
+                       int64_t d_qk, int64_t d_v, int64_t topk, float scale, int64_t q_offset, void* stream);
+
+/*
+ * Head-summed attention probability at each selected slot (reference: get_attn_scores,
+ * models/deepseek_v32/model.py:285-306, gathered/zeroed at :410-413):
+ *   mass[b, s, j] = sum_h exp(scale*q[b,s,h].kv[idx_j] - lse[b,s,h]),  0 for unused slots,
+ * with lse = softmax_max + log(softmax_sum) from dsa_sparse_mla_fwd.
+ */
+int dsa_attn_mass(const void* q, const void* kv, const int32_t* indices, const float* softmax_max,
+                  const float* softmax_sum, float* mass, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
+                  int64_t n_heads, int64_t d_qk, int64_t topk, float scale, int64_t q_offset, void* stream);
+
+/*
+ * Indexer KL loss and its gradients (reference: DSAIndexerLoss.forward,
+ * models/common/dsa_indexer_loss.py:138-160, as fused by
+ * npu_sparse_lightning_indexer_grad_kl_loss, converters/kernels/dsa.py:159-183).
+ * Per row (b,s): I_j = sum_h w[h] relu(q_idx[h].k_idx[idx_j]) over used slots, target
+ * t_j = mass_j / Z with Z = sum_j mass_j (row skipped when Z <= eps), row loss
+ * Z * sum_j t_j (log max(t_j, eps) - log_softmax(I)_j) [t_j > 0], times loss_scale.
+ *   q_idx [B,S,H_I,D_I] bf16, k_idx [B,S_k,D_I] bf16, w [B,S,H_I] fp32, mass [B,S,K] fp32
+ *   dq_idx [B,S,H_I,D_I] fp32 (written), dk_idx_accum [B,S_k,D_I] fp32 (ACCUMULATED),
+ *   dw [B,S,H_I] fp32 (written), loss_rows [B,S] fp32 (written; the op's loss is their sum)
+ * grad_scale multiplies every gradient (the upstream gradient of the summed loss).
+ */
+int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
+                        const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
+                        int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t topk,
+                        int64_t q_offset, float loss_scale, float eps, float grad_scale, void* stream);
+
+/*
+ * Block KV compressor (reference: Compressor._forward_bsnd + overlap_transform,
+ * models/deepseek_v4/model.py:174-221).
+ *   kv, score [B, S, coff*D] fp32 (coff = 2 with overlap, else 1); ape [ratio, coff*D] fp32
+ *   out [B, S/ratio, D]: fp32 pooled values, or, with norm_weight != NULL,
+ *   RMSNorm(bf16(pooled)) * norm_weight written as bf16 (out_dtype selects f32/bf16 output).
+ */
+int dsa_compressor_fwd(const float* kv, const float* score, const float* ape, const float* norm_weight, void* out,
+                       int out_dtype, int64_t batch, int64_t s, int64_t d, int64_t ratio, int overlap,
+                       float norm_eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_MI355X_H */

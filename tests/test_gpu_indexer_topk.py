@@ -1,0 +1,125 @@
+"""Parity of the lightning indexer (dsa_indexer_fwd) and top-k (dsa_topk) HIP kernels.
+
+Top-k is bit-exact: identical fp32 scores must give identical index sets (ties broken by
+lower index, -0.0 == +0.0, NaN excluded).  Indexer scores are fp32 sums of exact
+products (bf16 x bf16 or e4m3 x e4m3), so only the summation order differs from the
+oracle: relative tolerance 1e-5 of the row's magnitude (5e-5 for fp8, whose per-token
+scales are folded into the weights and the final sum with extra fp32 roundings).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _ops():
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    return ops
+
+
+def _oracle_topk(scores, k, q_offset=0, cmp_ratio=1, index_offset=0):
+    S, n = scores.shape[1], scores.shape[2]
+    nv = np.array([O.valid_key_count(s, q_offset, cmp_ratio, n) for s in range(S)])
+    ref = O.topk_select_numpy(scores[0].numpy(), k, nv)
+    ref = np.where(ref >= 0, ref + index_offset, -1)
+    return torch.from_numpy(ref).unsqueeze(0)
+
+
+@pytest.mark.parametrize("S,n,k,q_offset,cmp_ratio", [(64, 64, 16, 0, 1), (300, 300, 64, 0, 1), (128, 512, 100, 384, 1),
+                                                     (256, 64, 32, 0, 4), (40, 20000, 2048, 19960, 1)])
+def test_topk_bit_exact_random(S, n, k, q_offset, cmp_ratio):
+    g = torch.Generator().manual_seed(S + n + k)
+    scores = torch.randn(1, S, n, generator=g)
+    idx, vals = _ops().topk_select(scores.to(DEV), k, q_offset=q_offset, cmp_ratio=cmp_ratio, return_values=True)
+    ref = _oracle_topk(scores, k, q_offset, cmp_ratio)
+    assert torch.equal(idx.cpu(), ref)
+    ref_vals = torch.where(ref >= 0, torch.gather(scores, -1, ref.clamp_min(0).long()), torch.tensor(float("-inf")))
+    assert torch.equal(vals.cpu(), ref_vals)
+
+
+def test_topk_ties_signed_zero_nan_inf():
+    S, n, k = 96, 256, 40
+    g = torch.Generator().manual_seed(3)
+    scores = torch.randint(-3, 4, (1, S, n), generator=g).float()  # heavy ties
+    scores[0, :, ::7] = -0.0
+    scores[0, :, 3::11] = 0.0
+    scores[0, 5:, 1::13] = float("nan")
+    scores[0, 7:, 2::17] = float("inf")
+    scores[0, 9:, 4::19] = float("-inf")
+    idx, _ = _ops().topk_select(scores.to(DEV), k)
+    assert torch.equal(idx.cpu(), _oracle_topk(scores, k))
+
+
+def test_topk_all_equal_and_short_rows():
+    S, n, k = 50, 50, 8
+    scores = torch.zeros(1, S, n)
+    idx, _ = _ops().topk_select(scores.to(DEV), k)
+    ref = _oracle_topk(scores, k)
+    assert torch.equal(idx.cpu(), ref)
+    # rows s < k have s+1 candidates: all chosen, rest -1
+    assert torch.all(idx.cpu()[0, 0, 1:] == -1) and idx.cpu()[0, 0, 0] == 0
+
+
+def test_topk_index_offset():
+    S, n, k = 32, 32, 8
+    scores = torch.randn(1, S, n, generator=torch.Generator().manual_seed(4))
+    idx, _ = _ops().topk_select(scores.to(DEV), k, index_offset=100)
+    assert torch.equal(idx.cpu(), _oracle_topk(scores, k, index_offset=100))
+
+
+@pytest.mark.parametrize("S,H,D,q_offset,cmp_ratio", [(256, 64, 128, 0, 1), (200, 32, 128, 56, 1), (512, 4, 64, 0, 1),
+                                                     (128, 16, 128, 0, 4)])
+def test_indexer_bf16_parity(S, H, D, q_offset, cmp_ratio):
+    g = torch.Generator().manual_seed(S + H)
+    s_k = (S + q_offset) // cmp_ratio
+    q = torch.randn(1, S, H, D, generator=g).bfloat16()
+    k = torch.randn(1, s_k, D, generator=g).bfloat16()
+    w = torch.rand(1, S, H, generator=g) * H ** -0.5 * D ** -0.5
+    got = _ops().indexer_scores(q.to(DEV), k.to(DEV), w.to(DEV), q_offset=q_offset, cmp_ratio=cmp_ratio).cpu()
+    ref = O.indexer_scores(q, k, w, q_offset=q_offset, cmp_ratio=cmp_ratio, dtype=torch.float64)
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got))
+    err = (got.double() - ref).abs().masked_fill(~fin, 0).amax(-1)
+    mag = ref.abs().masked_fill(~fin, 0).amax(-1).clamp_min(1e-6)
+    assert float((err / mag).max()) <= 1e-5
+
+
+def test_indexer_fp8_quantise_dequantise_parity():
+    S, H, D = 256, 64, 128
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(1, S, H, D, generator=g)
+    k = torch.randn(1, S, D, generator=g)
+    w = torch.rand(1, S, H, generator=g) * H ** -0.5 * D ** -0.5
+    q8, qs = O.quantize_e4m3_per_row(q)
+    k8, ks = O.quantize_e4m3_per_row(k)
+    got = _ops().indexer_scores(q8.to(DEV), k8.to(DEV), w.to(DEV), q_scale=qs.to(DEV), k_scale=ks.to(DEV)).cpu()
+    qd = q8.double() * qs.double().unsqueeze(-1)
+    kd = k8.double() * ks.double().unsqueeze(-1)
+    ref = O.indexer_scores(qd, kd, w.double(), dtype=torch.float64)
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got))
+    err = (got.double() - ref).abs().masked_fill(~fin, 0).amax(-1)
+    mag = ref.abs().masked_fill(~fin, 0).amax(-1).clamp_min(1e-6)
+    # the per-token scales are folded into w and the final sum in fp32: a few extra roundings
+    assert float((err / mag).max()) <= 5e-5
+
+
+def test_lightning_indexer_op_end_to_end():
+    """npu_lightning_indexer == oracle top-k applied to the GPU's own fp32 scores (bit-exact)."""
+    S, H, D, K = 300, 64, 128, 64
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(1, S, H, D, generator=g).bfloat16()
+    k = torch.randn(1, S, 1, D, generator=g).bfloat16()
+    w = torch.rand(1, S, H, generator=g) * H ** -0.5 * D ** -0.5
+    ops = _ops()
+    idx, vals = ops.npu_lightning_indexer(q.to(DEV), k.to(DEV), w.to(DEV), sparse_count=K, sparse_mode=3,
+                                          return_value=True)
+    scores = ops.indexer_scores(q.to(DEV), k.to(DEV), w.to(DEV)).cpu()
+    assert idx.shape == (1, S, 1, K)
+    assert torch.equal(idx[:, :, 0].cpu(), _oracle_topk(scores, K))

@@ -1,0 +1,111 @@
+"""ctypes binding of the C ABI in ``include/dsa_mi355x.h``.
+
+The HIP library is the only compute path: if it is not built, or no GPU is visible,
+every op raises instead of falling back to anything else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
+
+DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+_vp = ctypes.c_void_p
+
+# name -> argument types (must match include/dsa_mi355x.h)
+_SIGNATURES = {
+    "dsa_last_error": ([], ctypes.c_char_p),
+    "dsa_abi_version": ([], _i32),
+    "dsa_indexer_fwd": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _i32),
+    "dsa_topk": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _i32),
+    "dsa_sparse_mla_fwd": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _vp],
+        _i32,
+    ),
+    "dsa_sparse_mla_bwd_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _i64], _i64),
+    "dsa_sparse_mla_bwd": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _f32, _i64, _vp],
+        _i32,
+    ),
+    "dsa_attn_mass": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _vp],
+        _i32,
+    ),
+    "dsa_indexer_kl_grad": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32,
+         _vp],
+        _i32,
+    ),
+    "dsa_compressor_fwd": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class DSAError(RuntimeError):
+    """Error reported by the HIP library (status code + dsa_last_error text)."""
+
+
+def load_library(path: Path | None = None):
+    """Load (once) and return the ctypes handle; raises if the library is absent."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path else LIB_PATH
+        if not p.exists():
+            raise DSAError(
+                f"HIP extension {p} is not built; run `python -m torchtitan_npu_simulator_amd.build` "
+                "(there is no CPU fallback)"
+            )
+        lib = ctypes.CDLL(str(p))
+        for name, (argtypes, restype) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _lib = lib
+        return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().dsa_last_error().decode(errors="replace")
+        raise DSAError(f"{what} failed (status {rc}): {msg}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu_tensor(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise DSAError(f"{name} must be a GPU tensor (the DSA ops have no CPU implementation)")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return DSA_BF16
+    if dt == torch.float32:
+        return DSA_F32
+    if dt == torch.float8_e4m3fn:
+        return DSA_FP8_E4M3
+    raise DSAError(f"unsupported dtype {dt}")
