@@ -101,13 +101,18 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, vo
  *   dq        [B, S, H, D_qk]  same dtype as q (written)
  *   dkv_accum [B, S_kv, D_qk]  fp32, ACCUMULATED into (caller zeroes it); latent alias:
  *             dkv[:, :D_v] = dK_nope + dV, dkv[:, D_v:] = dK_rope
- *   workspace fp32, at least dsa_sparse_mla_bwd_workspace_size() bytes
+ *   workspace  device scratch of workspace_bytes (dsa_sparse_mla_bwd_workspace_size() gives the
+ *              default; a smaller one processes query rows in more chunks); fp32 dtype needs none
+ * The bf16 path needs D_qk = 576, D_v = 512, H <= 128.  dKV is reduced per key without
+ * float atomics (bf16 per-(row, slot) contributions summed in fp32 through a key-major CSR).
  */
-int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t topk);
+int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
+                                          int64_t d_qk, int64_t topk);
 int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out, const void* dout,
                        const float* softmax_max, const float* softmax_sum, void* dq, float* dkv_accum,
-                       void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
-                       int64_t d_qk, int64_t d_v, int64_t topk, float scale, int64_t q_offset, void* stream);
+                       void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q,
+                       int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
+                       int64_t q_offset, void* stream);
 
 /*
  * Head-summed attention probability at each selected slot (reference: get_attn_scores,
@@ -124,17 +129,23 @@ int dsa_attn_mass(const void* q, const void* kv, const int32_t* indices, const f
  * models/common/dsa_indexer_loss.py:138-160, as fused by
  * npu_sparse_lightning_indexer_grad_kl_loss, converters/kernels/dsa.py:159-183).
  * Per row (b,s): I_j = sum_h w[h] relu(q_idx[h].k_idx[idx_j]) over used slots, target
- * t_j = mass_j / Z with Z = sum_j mass_j (row skipped when Z <= eps), row loss
- * Z * sum_j t_j (log max(t_j, eps) - log_softmax(I)_j) [t_j > 0], times loss_scale.
+ * t_j = mass_j / Z with Z = sum_j mass_j, row loss
+ * Z * sum_{t_j > 0} t_j (log max(t_j, eps) - log_softmax(I)_j) * loss_scale
+ * (rows with Z <= eps use a zero score vector and get no gradient, as the reference does).
  *   q_idx [B,S,H_I,D_I] bf16, k_idx [B,S_k,D_I] bf16, w [B,S,H_I] fp32, mass [B,S,K] fp32
  *   dq_idx [B,S,H_I,D_I] fp32 (written), dk_idx_accum [B,S_k,D_I] fp32 (ACCUMULATED),
  *   dw [B,S,H_I] fp32 (written), loss_rows [B,S] fp32 (written; the op's loss is their sum)
  * grad_scale multiplies every gradient (the upstream gradient of the summed loss).
+ * H_I = 64, D_I = 128 run on MFMA with a workspace of
+ * dsa_indexer_kl_grad_workspace_size() bytes; other shapes use an exact fp32 kernel.
  */
+int64_t dsa_indexer_kl_grad_workspace_size(int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                                           int64_t head_dim, int64_t topk);
 int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
                         const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
-                        int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t topk,
-                        int64_t q_offset, float loss_scale, float eps, float grad_scale, void* stream);
+                        void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q, int64_t s_k,
+                        int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset, float loss_scale,
+                        float eps, float grad_scale, void* stream);
 
 /*
  * Block KV compressor (reference: Compressor._forward_bsnd + overlap_transform,

@@ -78,6 +78,7 @@ __all__ = [
     "attn_mass",
     "dsa_indexer_loss",
     "indexer_kl_loss_grad",
+    "indexer_kl_from_mass",
     "compressor_pool",
     "window_topk_idxs",
     "compress_topk_idxs",
@@ -381,26 +382,33 @@ def indexer_kl_loss_grad(
     """What npu_sparse_lightning_indexer_grad_kl_loss returns: (dq_idx, dk_idx, dw, loss_sum).
 
     The indexer scores are recomputed at the selected keys, the target is the
-    head-summed main-attention mass at those keys, and the loss is the token
-    SUM of DSAIndexerLoss's per-token term times ``loss_scale``; gradients flow
+    head-summed main-attention mass at those keys, and the loss is the token SUM
+    of DSAIndexerLoss's per-token term times ``loss_scale``; gradients flow
     only into (q_idx, k_idx, weights) (models/deepseek_v32/model.py:407-409).
     """
     mass = attn_mass(q, kv, idx, lse, scale, q_offset=q_offset, dtype=dtype)
-    s_kv = k_idx.shape[-2]
-    valid = _attn_valid(idx.long(), q_offset, s_kv)
+    return indexer_kl_from_mass(q_idx, k_idx, weights, idx, mass, q_offset=q_offset, loss_scale=loss_scale, eps=eps,
+                                dtype=dtype)
+
+
+def indexer_kl_from_mass(q_idx, k_idx, weights, idx, mass, *, q_offset=0, loss_scale=1.0, eps=1e-8,
+                         dtype=torch.float64):
+    """KL loss SUM over tokens and its gradients given the target mass [B,S,K]."""
+    s_k = k_idx.shape[-2] if k_idx.dim() == 3 else k_idx.shape[1]
+    valid = _attn_valid(idx.long(), q_offset, s_k)
     qi = q_idx.detach().to(dtype).requires_grad_(True)
     ki = (k_idx.squeeze(2) if k_idx.dim() == 4 else k_idx).detach().to(dtype).requires_grad_(True)
     w = weights.detach().to(dtype).requires_grad_(True)
-    ii = idx.long().clamp(0, s_kv - 1)
-    B = q.shape[0]
+    ii = idx.long().clamp(0, s_k - 1)
     rows = []
-    for b in range(B):
+    for b in range(q_idx.shape[0]):
         kk = ki[b][ii[b]]  # [S,K,D_I]
         p = torch.einsum("shd,skd->shk", qi[b], kk)
         sc = (torch.relu(p) * w[b].unsqueeze(-1)).sum(dim=1)
         rows.append(sc.masked_fill(~valid[b], float("-inf")))
     index_score = torch.stack(rows)
-    loss = dsa_indexer_loss(mass.masked_fill(~valid, 0.0), index_score, loss_scale, eps=eps, reduction="sum")
+    target = mass.to(dtype).masked_fill(~valid, 0.0)
+    loss = dsa_indexer_loss(target, index_score, loss_scale, eps=eps, reduction="sum")
     dq, dk, dw = torch.autograd.grad(loss, (qi, ki, w), allow_unused=True)
     return dq, dk, dw, loss.detach()
 

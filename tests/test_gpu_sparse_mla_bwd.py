@@ -1,0 +1,105 @@
+"""Parity of dsa_sparse_mla_bwd (dQ, dKV) and dsa_attn_mass (HIP) against the CPU oracle.
+
+Gradients: relative error ||gpu - oracle|| / ||oracle|| <= 2e-2 in bf16 (contract
+tolerance), <= 1e-5 in fp32.  The oracle backward is the closed-form flash-attention
+backward in fp64, itself pinned to torch.autograd (tests/test_oracle.py).
+"""
+
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+from tests.dsa_cases import attn_inputs, rand_indices, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+BF16_TOL = 2e-2
+
+
+def _ops():
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    return ops
+
+
+def _gpu_fwd_bwd(q, kv, idx, dout, scale, q_offset=0, workspace_bytes=None):
+    ops = _ops()
+    qd, kvd, idd, dod = q.to(DEV), kv.to(DEV), idx.to(DEV), dout.to(DEV)
+    out, smax, ssum = ops.sparse_mla_fwd(qd, kvd, idd, scale, q_offset=q_offset)
+    dq, dkv = ops.sparse_mla_bwd(qd, kvd, idd, out, dod, smax, ssum, scale, q_offset=q_offset,
+                                 workspace_bytes=workspace_bytes)
+    torch.cuda.synchronize()
+    return out.cpu(), smax.cpu(), ssum.cpu(), dq.cpu(), dkv.cpu()
+
+
+@pytest.mark.parametrize(
+    "S,H,K,q_offset,seed,shuffle,holes",
+    [
+        (256, 128, 128, 0, 0, False, 0.0),
+        (160, 128, 96, 32, 1, True, 0.2),  # arbitrary slot order, -1 holes, CP shard offset
+        (128, 16, 64, 0, 2, False, 0.0),  # few heads (one partial head group)
+        (96, 72, 40, 0, 3, True, 0.0),  # head count not a multiple of 16
+    ],
+)
+def test_bwd_bf16_parity(S, H, K, q_offset, seed, shuffle, holes):
+    q, kv, dout, scale = attn_inputs(S, H, q_offset=q_offset, seed=seed)
+    idx = rand_indices(S, K, q_offset=q_offset, seed=seed, shuffle=shuffle, holes=holes)
+    out, smax, ssum, dq, dkv = _gpu_fwd_bwd(q, kv, idx, dout, scale, q_offset)
+    ref_out, ref_lse = O.sparse_mla_fwd(q, kv, idx, scale, q_offset=q_offset)
+    # backward of the bf16 forward output, as the GPU sees it
+    rdq, rdkv, _ = O.sparse_mla_bwd_closed_form(q, kv, idx, out, ref_lse, dout, scale, q_offset=q_offset)
+    assert rel_err(dq, rdq) <= BF16_TOL, rel_err(dq, rdq)
+    assert rel_err(dkv, rdkv) <= BF16_TOL, rel_err(dkv, rdkv)
+    # and against autograd of the exact forward
+    adq, adkv = O.sparse_mla_bwd(q, kv, idx, dout, scale, q_offset=q_offset)
+    assert rel_err(dq, adq) <= BF16_TOL and rel_err(dkv, adkv) <= BF16_TOL
+
+
+def test_bwd_bf16_chunked_workspace_matches_single_pass():
+    """A workspace that only fits a few query rows gives the same gradients (row chunking)."""
+    S, H, K = 128, 32, 64
+    q, kv, dout, scale = attn_inputs(S, H, seed=4)
+    idx = rand_indices(S, K, seed=4)
+    *_, dq1, dkv1 = _gpu_fwd_bwd(q, kv, idx, dout, scale)
+    small = (K * (256 * 2 + 576 * 2 + 4)) * 24 + 3 * (S + 1) * 4 + 4096
+    *_, dq2, dkv2 = _gpu_fwd_bwd(q, kv, idx, dout, scale, workspace_bytes=small)
+    assert torch.equal(dq1, dq2)
+    assert rel_err(dkv2, dkv1) <= 1e-6
+
+
+def test_bwd_dense_special_case_matches_sdpa_autograd():
+    S, H = 96, 32
+    q, kv, dout, scale = attn_inputs(S, H, seed=6)
+    idx = rand_indices(S, S, seed=6)
+    _, _, _, dq, dkv = _gpu_fwd_bwd(q, kv, idx, dout, scale)
+    qd = q.double().requires_grad_(True)
+    kvd = kv.double().requires_grad_(True)
+    k = kvd.unsqueeze(1).expand(1, H, S, 576)
+    o = torch.nn.functional.scaled_dot_product_attention(qd.permute(0, 2, 1, 3), k, k[..., :512], is_causal=True,
+                                                         scale=scale)
+    gq, gkv = torch.autograd.grad(o.permute(0, 2, 1, 3), (qd, kvd), dout.double())
+    assert rel_err(dq, gq) <= BF16_TOL and rel_err(dkv, gkv) <= BF16_TOL
+
+
+def test_bwd_fp32_parity():
+    S, H, K = 48, 4, 24
+    q, kv, dout, scale = attn_inputs(S, H, seed=8, dtype=torch.float32)
+    idx = rand_indices(S, K, seed=8)
+    out, smax, ssum, dq, dkv = _gpu_fwd_bwd(q, kv, idx, dout.float(), scale)
+    adq, adkv = O.sparse_mla_bwd(q, kv, idx, dout, scale)
+    assert rel_err(dq, adq) <= 1e-5 and rel_err(dkv, adkv) <= 1e-5
+
+
+@pytest.mark.parametrize("S,H,K,q_offset", [(200, 128, 128, 0), (64, 16, 32, 16), (80, 128, 40, 0)])
+def test_attn_mass_parity(S, H, K, q_offset):
+    q, kv, _, scale = attn_inputs(S, H, q_offset=q_offset, seed=10)
+    idx = rand_indices(S, K, q_offset=q_offset, seed=10, holes=0.1)
+    ops = _ops()
+    out, smax, ssum = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), scale, q_offset=q_offset)
+    mass = ops.attn_mass(q.to(DEV), kv.to(DEV), idx.to(DEV), smax, ssum, scale, q_offset=q_offset).cpu()
+    lse = smax.cpu().double() + torch.log(ssum.cpu().double())
+    ref = O.attn_mass(q, kv, idx, lse, scale, q_offset=q_offset)
+    assert rel_err(mass, ref) <= 1e-4
+    # each head's softmax sums to one over the selected keys
+    rows = torch.isfinite(lse).all(-1)
+    assert torch.allclose(mass.sum(-1)[rows].double(), torch.full_like(mass.sum(-1)[rows].double(), H), rtol=1e-3)

@@ -41,9 +41,10 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _vp],
         _i32,
     ),
+    "dsa_indexer_kl_grad_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _i64], _i64),
     "dsa_indexer_kl_grad": (
-        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32, _f32,
-         _vp],
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+         _f32, _f32, _vp],
         _i32,
     ),
     "dsa_compressor_fwd": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),

@@ -1,0 +1,444 @@
+// Indexer KL loss and gradients at the selected keys (the fused op
+// npu_sparse_lightning_indexer_grad_kl_loss of the reference).
+//
+// Per query row s (one workgroup, 4 waves, wave w owns index heads 16w..16w+15):
+//   phase 1  I_j = sum_h w_h relu(q_h . k_{idx_j}) for every slot j: S = q k^T on
+//            v_mfma_f32_16x16x32_bf16 over 32-slot blocks of gathered key rows (LDS),
+//            relu * w summed in-lane, across lane groups and across waves (LDS adds)
+//   phase 2  row statistics: softmax of I over usable slots, target t = mass / Z, the
+//            row loss Z * sum_{t>0} t (log max(t, eps) - log_softmax(I)) * loss_scale and
+//            g_j = dloss/dI_j = Z * loss_scale * grad_scale * (softmax_j * T - t_j)
+//   phase 3  recompute S; E = g_j w_h [S > 0];  dw_h = sum_j g_j relu(S);
+//            dq^T += k^T E^T (k read transposed with ds_read_tr16_b64);
+//            dk contribution of slot j = sum_h E[h, j] q_h (v_mfma_f32_16x16x16_bf16 per
+//            wave, summed over waves in LDS) written as bf16 and reduced per key through
+//            the shared CSR pass (no float atomics).
+// A generic fp32 kernel (any H, D) handles shapes outside the MFMA tile.
+#include <algorithm>
+
+#include "dsa_common.h"
+#include "dsa_csr.h"
+
+namespace dsa {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kH = 64;
+constexpr int kB = 32;           // slots per block
+constexpr int kRowC = kD / 8;    // 16 chunks per key row
+constexpr int kMaxK = 4096;
+
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef short i16x4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bool ok_slot(int v, int s_k, int64_t limit) {
+  return v >= 0 && v < s_k && (int64_t)v <= limit;
+}
+
+__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float o = __shfl_xor(v, m, 64);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  if ((t & 63) == 0) red[t >> 6] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < 4; ++i) r = is_max ? fmaxf(r, red[i]) : r + red[i];
+  __syncthreads();
+  return r;
+}
+
+__global__ void __launch_bounds__(256, 2)
+indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restrict__ ki, const float* __restrict__ w,
+                       const int32_t* __restrict__ idx, const float* __restrict__ mass, float* __restrict__ dq,
+                       float* __restrict__ dw, float* __restrict__ loss_rows, uint16_t* __restrict__ ck, int S,
+                       int s_k, int K, int64_t q_offset, float loss_scale, float eps, float grad_scale, int row0) {
+  __shared__ u32x4 kt[kB * kRowC];          // gathered key rows [32][16 chunks], XOR-swizzled
+  __shared__ float iv[kMaxK];               // I_j, then g_j
+  __shared__ float dkp[kB][kD + 4];         // dk contributions of one block (fp32, summed over waves)
+  __shared__ uint16_t et[4][16][kB + 8];    // E per wave, [head][slot] (transposed for dq)
+  __shared__ float red[4];
+  __shared__ float stats[4];
+
+  const int lr = blockIdx.x, b = blockIdx.y;
+  const int tok = row0 + lr;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, g = lane >> 4;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int32_t* ridx = idx + row_id * K;
+  const float* mrow = mass + row_id * K;
+  const int64_t limit = tok + q_offset;
+  const uint16_t* kb = ki + (int64_t)b * s_k * kD;
+  const int head_a = 16 * wave + col;  // A-operand row (head) of this lane
+  const int nblocks = (K + kB - 1) / kB;
+
+  // A = q [16 heads x 32 d] per step c: lane (head col, g) holds q[head][32c + 8g .. +8]
+  u32x4 qa[kD / 32];
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(qi + (row_id * kH + head_a) * kD);
+#pragma unroll
+    for (int c = 0; c < kD / 32; ++c) qa[c] = qh[4 * c + g];
+  }
+  // transposed q for the dk contribution (A of 16x16x16: lane (d col, g) holds heads 4g..4g+3)
+  i16x4v qt[kD / 16];
+#pragma unroll
+  for (int dt = 0; dt < kD / 16; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      qt[dt][i] = (short)qi[(row_id * kH + 16 * wave + 4 * g + i) * kD + 16 * dt + col];
+  // C layout of S = q k^T tiles: lane (slot col, g) holds heads 16w + 4g + r
+  float wr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) wr[r] = w[row_id * kH + 16 * wave + 4 * g + r];
+
+  for (int j = tid; j < K; j += 256) iv[j] = 0.f;
+
+  auto gather = [&](int blk) {  // 32 rows x 256 B: 2 DMA instructions per wave
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int J = wave * 2 + i;
+      const int p = J * 64 + lane;
+      const int row = p >> 4, pos = p & 15;
+      const int chunk = pos ^ (row & 7);
+      const int slot = blk * kB + row;
+      int v = ridx[min(slot, K - 1)];
+      if (slot >= K || !ok_slot(v, s_k, limit)) v = 0;
+      __builtin_amdgcn_global_load_lds((const void*)(kb + (int64_t)v * kD + chunk * 8),
+                                       (__attribute__((address_space(3))) void*)&kt[J * 64], 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  };
+  const uint32_t kt_base = (uint32_t)(uintptr_t)(&kt[0]);
+  // S tile (16 heads x 16 slots) for slot tile st of the staged block
+  auto s_tile = [&](int st) -> f32x4 {
+    f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * st + col;
+#pragma unroll
+    for (int c = 0; c < kD / 32; ++c) {
+      const u32x4 bk = *(const lds_u32x4*)(kt_base + 16 * (row * kRowC + ((4 * c + g) ^ (row & 7))));
+      acc = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk), acc);
+    }
+    return acc;
+  };
+
+  // ---------------- phase 1: index scores at the selected slots ----------------
+  __syncthreads();
+  for (int blk = 0; blk < nblocks; ++blk) {
+    gather(blk);
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const f32x4 sv = s_tile(st);
+      float part = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part = fmaf(wr[r], fmaxf(sv[r], 0.f), part);
+      part += __shfl_xor(part, 16, 64);
+      part += __shfl_xor(part, 32, 64);
+      const int slot = blk * kB + 16 * st + col;
+      if (g == 0 && slot < K) atomicAdd(&iv[slot], part);
+    }
+    __syncthreads();
+  }
+
+  // ---------------- phase 2: row statistics ----------------
+  float lmax = -INFINITY, zsum = 0.f;
+  for (int j = tid; j < K; j += 256) {
+    const bool ok = ok_slot(ridx[j], s_k, limit);
+    if (ok) {
+      lmax = fmaxf(lmax, iv[j]);
+      zsum += fmaxf(mrow[j], 0.f);
+    }
+  }
+  const float imax = block_reduce(lmax, red, true);
+  const float Z = block_reduce(zsum, red, false);
+  float esum = 0.f;
+  for (int j = tid; j < K; j += 256)
+    if (ok_slot(ridx[j], s_k, limit)) esum += expf(iv[j] - imax);
+  const float E = block_reduce(esum, red, false);
+  const bool valid_row = Z > eps;
+  const float lse = imax + logf(E);
+  const float zc = fmaxf(Z, eps);
+  // loss terms and T = sum of positive targets
+  float lpart = 0.f, tpos = 0.f;
+  for (int j = tid; j < K; j += 256) {
+    const bool ok = ok_slot(ridx[j], s_k, limit);
+    const float t = ok ? fmaxf(mrow[j], 0.f) / zc : 0.f;
+    if (t > 0.f) {
+      const float ls = valid_row ? (iv[j] - lse) : -logf((float)K);
+      lpart += t * (logf(fmaxf(t, eps)) - ls);
+      tpos += t;
+    }
+  }
+  const float lrow = block_reduce(lpart, red, false);
+  const float T = block_reduce(tpos, red, false);
+  if (tid == 0) loss_rows[row_id] = Z * lrow * loss_scale;
+  const float gs = valid_row ? Z * loss_scale * grad_scale : 0.f;
+  for (int j = tid; j < K; j += 256) {
+    const bool ok = ok_slot(ridx[j], s_k, limit);
+    const float t = ok ? fmaxf(mrow[j], 0.f) / zc : 0.f;
+    const float sm = ok ? expf(iv[j] - lse) : 0.f;
+    iv[j] = gs * (sm * T - t);
+  }
+  __syncthreads();
+
+  // ---------------- phase 3: gradients ----------------
+  f32x4 dqa[kD / 16];
+#pragma unroll
+  for (int t = 0; t < kD / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float dwp[4] = {0.f, 0.f, 0.f, 0.f};
+  uint16_t* ckrow = ck + ((int64_t)b * gridDim.x + lr) * (int64_t)K * kD;
+  // transposed reads of the key tile for dq^T += k^T E^T: group g, source lane col supplies
+  // slot row 8g + col/4 (+4 second read), d columns 16dt + 4(col%4) .. +3
+  const int tr_row = 8 * g + (col >> 2);
+  for (int blk = 0; blk < nblocks; ++blk) {
+    if (gs == 0.f) break;  // block-uniform: no gradient for this row
+    gather(blk);
+    for (int i = tid; i < kB * (kD + 4); i += 256) (&dkp[0][0])[i] = 0.f;
+    __syncthreads();
+    u32x4 eb;  // B operand of dq^T: E^T [32 slots x 16 heads] read back from LDS
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const f32x4 sv = s_tile(st);
+      const int slot = blk * kB + 16 * st + col;
+      const float gj = slot < K ? iv[slot] : 0.f;
+      float e[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        e[r] = sv[r] > 0.f ? gj * wr[r] : 0.f;
+        dwp[r] += gj * fmaxf(sv[r], 0.f);
+        et[wave][4 * g + r][16 * st + col] = f_to_bf16(e[r]);
+      }
+      // dk contribution: C^T[d x 16 slots] = q^T[d x 16 heads] . E[16 heads x 16 slots]
+      i16x4v eo;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) eo[r] = (short)f_to_bf16(e[r]);
+#pragma unroll
+      for (int dt = 0; dt < kD / 16; ++dt) {
+        f32x4 c4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+        c4 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qt[dt], eo, c4, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) atomicAdd(&dkp[16 * st + col][16 * dt + 4 * g + r], c4[r]);
+      }
+    }
+    __syncthreads();
+    {
+      const u32x4* er = reinterpret_cast<const u32x4*>(&et[wave][col][8 * g]);
+      eb = *er;
+    }
+#pragma unroll
+    for (int dt = 0; dt < kD / 16; ++dt) {
+      const int c0 = 2 * dt + ((col & 3) >> 1);
+      const uint32_t a1 = kt_base + 16 * (tr_row * kRowC + (c0 ^ (tr_row & 7))) + 8 * (col & 1);
+      const uint32_t a2 = kt_base + 16 * ((tr_row + 4) * kRowC + (c0 ^ ((tr_row + 4) & 7))) + 8 * (col & 1);
+      const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a1);
+      const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a2);
+      u32x4 av;
+      av[0] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
+      av[1] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
+      av[2] = (uint32_t)(uint16_t)v2[0] | ((uint32_t)(uint16_t)v2[1] << 16);
+      av[3] = (uint32_t)(uint16_t)v2[2] | ((uint32_t)(uint16_t)v2[3] << 16);
+      dqa[dt] = mfma16x16x32(as_bf16x8(av), as_bf16x8(eb), dqa[dt]);
+    }
+    // write the block's dk contributions (bf16 rows of 128)
+    for (int i = tid; i < kB * kRowC; i += 256) {
+      const int row = i >> 4, c = i & 15;
+      const int slot = blk * kB + row;
+      if (slot >= K) continue;
+      u32x4 v;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = pack_bf16x2(dkp[row][8 * c + 2 * r], dkp[row][8 * c + 2 * r + 1]);
+      *reinterpret_cast<u32x4*>(ckrow + (int64_t)slot * kD + 8 * c) = v;
+    }
+    __syncthreads();
+  }
+  if (gs == 0.f) {  // zero contributions so the reduction can read every usable slot
+    for (int i = tid; i < K * kRowC; i += 256) {
+      const int slot = i >> 4, c = i & 15;
+      *reinterpret_cast<u32x4*>(ckrow + (int64_t)slot * kD + 8 * c) = (u32x4){0u, 0u, 0u, 0u};
+    }
+  }
+  // dw: lane (slot col, g) holds partials for heads 16w + 4g + r: sum over the 16 slot lanes
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = dwp[r];
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, 64);
+    dwp[r] = v;
+  }
+  if (col == 0)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dw[row_id * kH + 16 * wave + 4 * g + r] = dwp[r];
+  // dq^T tile dt: lane (head col, g) holds d = 16 dt + 4g + r
+  float* dqrow = dq + (row_id * kH + head_a) * kD;
+#pragma unroll
+  for (int dt = 0; dt < kD / 16; ++dt)
+    *reinterpret_cast<f32x4*>(dqrow + 16 * dt + 4 * g) = dqa[dt];
+}
+
+// --------------------------------------------------------------------------------------
+// generic fp32 path: one workgroup per row; dk by fp32 atomics (small shapes)
+// --------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+indexer_kl_generic_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restrict__ ki,
+                          const float* __restrict__ w, const int32_t* __restrict__ idx,
+                          const float* __restrict__ mass, float* __restrict__ dq, float* __restrict__ dk,
+                          float* __restrict__ dw, float* __restrict__ loss_rows, int S, int s_k, int H, int D, int K,
+                          int64_t q_offset, float loss_scale, float eps, float grad_scale) {
+  extern __shared__ float sh[];  // iv[K]
+  __shared__ float red[4];
+  const int tok = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int32_t* ridx = idx + row_id * K;
+  const float* mrow = mass + row_id * K;
+  const int64_t limit = tok + q_offset;
+  const uint16_t* qrow = qi + row_id * H * D;
+  const uint16_t* kb = ki + (int64_t)b * s_k * D;
+  float* iv = sh;
+  float lmax = -INFINITY, zsum = 0.f;
+  for (int j = tid; j < K; j += 256) {
+    const int v = ridx[j];
+    float x = 0.f;
+    if (ok_slot(v, s_k, limit)) {
+      for (int h = 0; h < H; ++h) {
+        float dot = 0.f;
+        for (int d = 0; d < D; ++d) dot = fmaf(bf16_to_f(qrow[h * D + d]), bf16_to_f(kb[(int64_t)v * D + d]), dot);
+        x = fmaf(w[row_id * H + h], fmaxf(dot, 0.f), x);
+      }
+      lmax = fmaxf(lmax, x);
+      zsum += fmaxf(mrow[j], 0.f);
+    }
+    iv[j] = x;
+  }
+  const float imax = block_reduce(lmax, red, true);
+  const float Z = block_reduce(zsum, red, false);
+  float esum = 0.f;
+  for (int j = tid; j < K; j += 256)
+    if (ok_slot(ridx[j], s_k, limit)) esum += expf(iv[j] - imax);
+  const float E = block_reduce(esum, red, false);
+  const bool valid_row = Z > eps;
+  const float lse = imax + logf(E);
+  const float zc = fmaxf(Z, eps);
+  float lpart = 0.f, tpos = 0.f;
+  for (int j = tid; j < K; j += 256) {
+    const bool ok = ok_slot(ridx[j], s_k, limit);
+    const float t = ok ? fmaxf(mrow[j], 0.f) / zc : 0.f;
+    if (t > 0.f) {
+      const float ls = valid_row ? (iv[j] - lse) : -logf((float)K);
+      lpart += t * (logf(fmaxf(t, eps)) - ls);
+      tpos += t;
+    }
+  }
+  const float lrow = block_reduce(lpart, red, false);
+  const float T = block_reduce(tpos, red, false);
+  if (tid == 0) loss_rows[row_id] = Z * lrow * loss_scale;
+  const float gs = valid_row ? Z * loss_scale * grad_scale : 0.f;
+  __syncthreads();
+  for (int j = tid; j < K; j += 256) {
+    const bool ok = ok_slot(ridx[j], s_k, limit);
+    const float t = ok ? fmaxf(mrow[j], 0.f) / zc : 0.f;
+    const float sm = ok ? expf(iv[j] - lse) : 0.f;
+    iv[j] = gs * (sm * T - t);
+  }
+  __syncthreads();
+  // dq[h][d], dw[h]: thread per (h, d); dk by atomics
+  for (int hd = tid; hd < H * D; hd += 256) {
+    const int h = hd / D, d = hd % D;
+    float acc = 0.f, dwacc = 0.f;
+    for (int j = 0; j < K; ++j) {
+      const float gj = iv[j];
+      if (gj == 0.f) continue;
+      const int v = ridx[j];
+      float dot = 0.f;
+      for (int e = 0; e < D; ++e) dot = fmaf(bf16_to_f(qrow[h * D + e]), bf16_to_f(kb[(int64_t)v * D + e]), dot);
+      if (dot > 0.f) {
+        const float ew = gj * w[row_id * H + h];
+        acc = fmaf(ew, bf16_to_f(kb[(int64_t)v * D + d]), acc);
+        atomicAdd(&dk[((int64_t)b * s_k + v) * D + d], ew * bf16_to_f(qrow[h * D + d]));
+        if (d == 0) dwacc += gj * dot;
+      }
+    }
+    dq[(row_id * H + h) * D + d] = acc;
+    if (d == 0) dw[row_id * H + h] = dwacc;
+  }
+}
+
+struct KlPlan {
+  int64_t rows, ck_bytes, pairs_bytes, csr_bytes, total;
+};
+
+KlPlan plan_kl(int64_t batch, int64_t rows, int64_t s_k, int64_t topk) {
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  KlPlan p{};
+  p.rows = rows;
+  p.ck_bytes = batch * rows * topk * kD * 2;
+  p.pairs_bytes = rows * topk * 4;
+  p.csr_bytes = 3 * (s_k + 1) * 4;
+  p.total = al(p.ck_bytes) + al(p.pairs_bytes) + al(p.csr_bytes);
+  return p;
+}
+
+constexpr int64_t kKlBudget = 8LL << 30;
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int64_t dsa_indexer_kl_grad_workspace_size(int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                                                      int64_t head_dim, int64_t topk) {
+  using namespace dsa;
+  if (batch <= 0 || s_q <= 0 || s_k <= 0 || topk <= 0) return 0;
+  if (!(n_heads == kH && head_dim == kD)) return 0;  // generic path needs no workspace
+  const int64_t per_row = batch * topk * kD * 2 + topk * 4;
+  const int64_t rows = std::max<int64_t>(1, std::min<int64_t>(s_q, kKlBudget / per_row));
+  return plan_kl(batch, rows, s_k, topk).total;
+}
+
+extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
+                                   const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
+                                   void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q, int64_t s_k,
+                                   int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset,
+                                   float loss_scale, float eps, float grad_scale, void* stream) {
+  using namespace dsa;
+  if (!q_idx || !k_idx || !w || !indices || !mass || !dq_idx || !dk_idx_accum || !dw || !loss_rows)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: null pointer");
+  if (batch <= 0 || s_q <= 0 || s_k <= 0 || n_heads <= 0 || head_dim <= 0 || topk <= 0 || topk > kMaxK)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: bad sizes");
+  if (s_q > 2147483647LL || batch > 65535 || s_k > 2147483647LL)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: sizes out of range");
+  hipStream_t st = (hipStream_t)stream;
+  if (!(n_heads == kH && head_dim == kD)) {
+    if (s_q > 2147483647LL) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: sizes out of range");
+    dim3 grid((unsigned)s_q, (unsigned)batch);
+    indexer_kl_generic_kernel<<<grid, 256, topk * 4, st>>>(
+        (const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass, dq_idx, dk_idx_accum, dw, loss_rows,
+        (int)s_q, (int)s_k, (int)n_heads, (int)head_dim, (int)topk, q_offset, loss_scale, eps, grad_scale);
+    return check_launch("dsa_indexer_kl_grad(generic)");
+  }
+  if (!workspace) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: workspace required");
+  const int64_t per_row = batch * topk * kD * 2 + topk * 4;
+  int64_t rows = std::max<int64_t>(1, std::min<int64_t>(s_q, workspace_bytes / per_row));
+  KlPlan plan = plan_kl(batch, rows, s_k, topk);
+  while (plan.total > workspace_bytes && plan.rows > 1) plan = plan_kl(batch, plan.rows - 1, s_k, topk);
+  if (plan.total > workspace_bytes)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: workspace of %lld bytes is too small",
+                     (long long)workspace_bytes);
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  char* ws = (char*)workspace;
+  uint16_t* ck = (uint16_t*)ws;
+  int* pairs = (int*)(ws + al(plan.ck_bytes));
+  int* csr = (int*)(ws + al(plan.ck_bytes) + al(plan.pairs_bytes));
+  for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
+    const int rows_c = (int)std::min<int64_t>(plan.rows, s_q - r0);
+    dim3 grid((unsigned)rows_c, (unsigned)batch);
+    indexer_kl_mfma_kernel<<<grid, 256, 0, st>>>((const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass,
+                                                 dq_idx, dw, loss_rows, ck, (int)s_q, (int)s_k, (int)topk, q_offset,
+                                                 loss_scale, eps, grad_scale, (int)r0);
+    if (int rc = check_launch("dsa_indexer_kl_grad(mfma)")) return rc;
+    for (int b = 0; b < (int)batch; ++b)
+      if (int rc = csr_reduce(indices, ck, dk_idx_accum, pairs, csr, (int)s_q, (int)s_k, (int)topk, q_offset, (int)r0,
+                              rows_c, b, kRowC, st))
+        return rc;
+  }
+  return DSA_OK;
+}

@@ -1,0 +1,516 @@
+// Gathered sparse MLA attention backward for gfx950, without float atomics.
+//
+// fp32 atomics on this part top out near 1.3 TB/s of payload (one dword per L2 channel
+// per clock), far too slow for the dKV scatter-add (576 fp32 per (token, key) pair), so
+// the backward reduces dKV through a key-major pass instead:
+//
+//   (alpha) bwd_dq_kernel, workgroup = (token, 64-head group), 4 waves x 16 heads:
+//           recompute S^T = K Q^T and dP^T = V dO^T on v_mfma_f32_16x16x32_bf16 over the
+//           gathered KV tile, P = exp2(S*scale*log2e - lse2), dS = P (dP - delta);
+//           dQ^T += K^T dS^T (K read transposed with ds_read_tr16_b64) in AGPRs; and
+//           G[token][slot][128 hg + (0..63 | 64..127)] = (dS * scale | P) in bf16.
+//   (beta)  bwd_contrib_kernel, workgroup = (token, 128 slots), 8 waves:
+//           C[token][slot][0..576) = G[slot][0..256) . [Q_token ; dO_token]  (bf16 out),
+//           the dKV contribution of one (token, slot) pair summed over all 128 heads.
+//   (gamma) a CSR of (token, slot) pairs per key (LDS-privatised counting sort), then
+//           dkv[key] += sum of its C rows in fp32, one owner per key (plain stores).
+// Query rows are processed in chunks so the bf16 G / C scratch fits the caller's
+// workspace.
+#include <algorithm>
+
+#include "dsa_common.h"
+#include "dsa_csr.h"
+
+namespace dsa {
+namespace {
+
+constexpr int kDqk = 576;
+constexpr int kDv = 512;
+constexpr int kRowChunks = kDqk / 8;
+constexpr int kRowBytes = kRowChunks * 16;
+constexpr int kBN = 32;
+constexpr int kTileChunks = kBN * kRowChunks;
+constexpr int kTileBytes = kTileChunks * 16;
+constexpr int kTileInstr = kTileChunks / 64;  // 36
+constexpr int kHG = 64;                       // heads per alpha workgroup
+constexpr int kGW = 256;                      // G row width: (dS | P) x 128 heads
+constexpr int kHeadsMax = 128;
+
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
+  return v >= 0 && v < s_kv && (int64_t)v <= limit;
+}
+
+__device__ __forceinline__ u32x4 tr_pair(uint32_t a1, uint32_t a2) {
+  const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a1));
+  const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a2));
+  u32x4 av;
+  av[0] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
+  av[1] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
+  av[2] = (uint32_t)(uint16_t)v2[0] | ((uint32_t)(uint16_t)v2[1] << 16);
+  av[3] = (uint32_t)(uint16_t)v2[2] | ((uint32_t)(uint16_t)v2[3] << 16);
+  return av;
+}
+
+// number of 32-slot blocks up to the last usable slot of a row (block-wide; needs sync)
+__device__ int count_blocks(const int32_t* ridx, int K, int s_kv, int64_t limit, int* sh_last) {
+  if (threadIdx.x == 0) *sh_last = -1;
+  __syncthreads();
+  int last = -1;
+  for (int j = threadIdx.x; j < K; j += blockDim.x)
+    if (slot_ok(ridx[j], s_kv, limit)) last = j;
+  if (last >= 0) atomicMax(sh_last, last);
+  __syncthreads();
+  const int n = (*sh_last + kBN) / kBN;
+  __syncthreads();
+  return n;
+}
+
+// --------------------------------------------------------------------------------------
+// (alpha) dQ and G
+// --------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256, 1)
+bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
+              const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, const float* __restrict__ smax,
+              const float* __restrict__ ssum, uint16_t* __restrict__ dq, uint16_t* __restrict__ gbuf, int S, int s_kv,
+              int H, int K, float scale, int64_t q_offset, int row0) {
+  __shared__ u32x4 tile[2][kTileChunks];
+  __shared__ uint16_t gst[kBN][2 * kHG];  // staged G rows of this head group
+  __shared__ uint32_t vmask[2];
+  __shared__ int sh_last;
+
+  const int tok = row0 + blockIdx.x;  // row within the batch element
+  const int hg = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int col = lane & 15, g = lane >> 4;
+  const int head = hg * kHG + wave * 16 + col;
+  const bool head_ok = head < H;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int32_t* ridx = idx + row_id * K;
+  const int64_t limit = tok + q_offset;
+  const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
+  const int64_t hrow = row_id * H + (head_ok ? head : 0);
+  // G rows of this chunk: [local row][slot][kGW]
+  uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + blockIdx.x) * (int64_t)K * kGW;
+
+  const int nblk = count_blocks(ridx, K, s_kv, limit, &sh_last);
+  if (nblk == 0) {  // no usable key: dQ = 0 (G rows are never read)
+    if (head_ok) {
+      uint32_t* d32 = reinterpret_cast<uint32_t*>(dq + hrow * kDqk);
+      for (int i = g; i < kDqk / 2; i += 4) d32[i] = 0u;
+    }
+    return;
+  }
+
+  // ---- per-head operands: Q (B layout of S^T = K Q^T), dO (B layout of dP^T = V dO^T) ----
+  u32x4 qb[kDqk / 32], db[kDv / 32];
+  float delta, lse2;
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
+    const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
+    const u32x4* oh = reinterpret_cast<const u32x4*>(out + hrow * kDv);
+    float part = 0.f;
+#pragma unroll
+    for (int c = 0; c < kDqk / 32; ++c) qb[c] = head_ok ? qh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int c = 0; c < kDv / 32; ++c) {
+      db[c] = head_ok ? dh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
+      const u32x4 ov = head_ok ? oh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        part += bf16_lo(db[c][r]) * bf16_lo(ov[r]) + bf16_hi(db[c][r]) * bf16_hi(ov[r]);
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    delta = part;
+    const float mx = head_ok ? smax[hrow] : 0.f, sm = head_ok ? ssum[hrow] : 0.f;
+    lse2 = (sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0 (absent head / no key)
+  }
+  const float scale_log2 = scale * kLog2e;
+
+  auto load_block = [&](int blk, int buf) {
+    int v[9], chunk[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      const int J = wave * 9 + i;
+      const int p = J * 64 + lane;
+      const int row = p / kRowChunks, pos = p - row * kRowChunks;
+      chunk[i] = pos ^ (row & 7);
+      const int slot = blk * kBN + row;
+      v[i] = ridx[min(slot, K - 1)];
+      if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      const int J = wave * 9 + i;
+      __builtin_amdgcn_global_load_lds((const void*)(kvb + (int64_t)v[i] * kDqk + chunk[i] * 8),
+                                       (__attribute__((address_space(3))) void*)&tile[buf][J * 64], 16, 0, 0);
+    }
+    if (wave == 0) {
+      const int slot = blk * kBN + lane;
+      const bool ok = lane < kBN && slot < K && slot_ok(ridx[min(slot, K - 1)], s_kv, limit);
+      const uint64_t bal = __ballot(ok);
+      if (lane == 0) vmask[buf] = (uint32_t)bal;
+    }
+  };
+
+  // LDS offsets.  A operand of S^T / dP^T: key row 16kt + col, chunk 4c + g (XOR row & 7).
+  // With c = 2u + c0 the XOR touches only bits 0..2 of 4c + g -> ka_off[kt][c0] + 128 u.
+  const uint32_t tile_base = (uint32_t)(uintptr_t)(&tile[0][0]);
+  uint32_t ka_off[2][2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int c0 = 0; c0 < 2; ++c0) {
+      const int row = 16 * kt + col;
+      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ (row & 7));
+    }
+  // Transposed K reads for dQ^T += K^T dS^T: group g, source lane col supplies key row
+  // 4g + col/4 (+16 for the second read), d columns 16dt + 4(col%4) -> chunk 2dt + (col%4)/2.
+  const int tr_row = 4 * g + (col >> 2);
+  const int tr_x = tr_row & 7;
+  const int tr_c0 = (col & 3) >> 1;
+  uint32_t tr_off[4];  // dt = 4u + d0 -> chunk (8u + 2 d0 + tr_c0) ^ tr_x = 8u + ((2 d0 + tr_c0) ^ tr_x)
+#pragma unroll
+  for (int d0 = 0; d0 < 4; ++d0) tr_off[d0] = tr_row * kRowBytes + 16 * ((2 * d0 + tr_c0) ^ tr_x) + 8 * (col & 1);
+
+  f32x4 dqa[kDqk / 16];
+#pragma unroll
+  for (int t = 0; t < kDqk / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  load_block(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int buf = blk & 1;
+    const bool has_next = blk + 1 < nblk;
+    if (has_next) load_block(blk + 1, buf ^ 1);
+    const uint32_t tb = tile_base + buf * kTileBytes;
+    const uint32_t vm = vmask[buf];
+
+    f32x4 sacc[2], pacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      sacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      pacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kDqk / 32; ++c) {
+        const u32x4 a = *(const lds_u32x4*)(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
+        sacc[kt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(qb[c]), sacc[kt]);
+        if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(db[c]), pacc[kt]);
+      }
+    }
+    // P and dS (lane: head col, keys 16kt + 4g + r)
+    float pv[2][4], dsv[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = 16 * kt + 4 * g + r;
+        const bool ok = (vm >> key) & 1u;
+        const float p = ok ? exp2f(sacc[kt][r] * scale_log2 - lse2) : 0.f;
+        pv[kt][r] = p;
+        dsv[kt][r] = p * (pacc[kt][r] - delta);
+      }
+    // dQ^T += K^T dS^T : B = dS^T, k-slot 8g + t <-> key (t < 4 ? 4g + t : 16 + 4g + t - 4)
+    u32x4 bds;
+    bds[0] = pack_bf16x2(dsv[0][0], dsv[0][1]);
+    bds[1] = pack_bf16x2(dsv[0][2], dsv[0][3]);
+    bds[2] = pack_bf16x2(dsv[1][0], dsv[1][1]);
+    bds[3] = pack_bf16x2(dsv[1][2], dsv[1][3]);
+#pragma unroll
+    for (int dt = 0; dt < kDqk / 16; ++dt) {
+      const uint32_t a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
+      const u32x4 a = tr_pair(a1, a1 + 16 * kRowBytes);
+      dqa[dt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(bds), dqa[dt]);
+    }
+    // stage G = (dS * scale | P) for these 32 slots
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int slot = 16 * kt + 4 * g + r;
+        gst[slot][wave * 16 + col] = f_to_bf16(dsv[kt][r] * scale);
+        gst[slot][kHG + wave * 16 + col] = f_to_bf16(pv[kt][r]);
+      }
+    __syncthreads();
+    for (int i = tid; i < kBN * 16; i += 256) {  // 32 slots x 256 B -> G[slot][128 hg ..]
+      const int slot = i >> 4, part = i & 15;
+      if (blk * kBN + slot >= K) continue;  // the row holds K slots only
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&gst[slot][part * 8]);
+      *reinterpret_cast<u32x4*>(grow + (int64_t)(blk * kBN + slot) * kGW + 2 * kHG * hg + part * 8) = v;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // ---- dQ epilogue: lane (head col, g) holds d = 16 dt + 4 g + r ----
+  if (!head_ok) return;
+  uint2* drow = reinterpret_cast<uint2*>(dq + hrow * kDqk);
+#pragma unroll
+  for (int dt = 0; dt < kDqk / 16; ++dt) {
+    uint2 w;
+    w.x = pack_bf16x2(dqa[dt][0] * scale, dqa[dt][1] * scale);
+    w.y = pack_bf16x2(dqa[dt][2] * scale, dqa[dt][3] * scale);
+    drow[(16 * dt + 4 * g) / 4] = w;
+  }
+}
+
+// --------------------------------------------------------------------------------------
+// (beta) C[token][slot] = G[token][slot] . X_token,  X = [(Q, dO) per head group]
+// rows of X: k = 128 hg + 64 type + i  ->  type 0: q[64hg + i], type 1: dout[64hg + i]
+// --------------------------------------------------------------------------------------
+constexpr int kCT = 128;          // slots per contrib workgroup
+constexpr int kXK = 64;           // X rows per staged chunk
+constexpr int kXChunks = kXK * kRowChunks;  // 4608 16-byte chunks (73.7 KB)
+
+__global__ void __launch_bounds__(512, 1)
+bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ dout,
+                   const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf, uint16_t* __restrict__ cbuf,
+                   int S, int s_kv, int H, int K, int64_t q_offset, int row0, int rows) {
+  __shared__ u32x4 xt[kXChunks];           // X chunk [64 rows][72 chunks], XOR-swizzled
+  __shared__ u32x4 gt[kCT * (kGW / 8)];    // G tile [128 slots][32 chunks], XOR-swizzled
+  __shared__ int sh_last;
+
+  const int lr = blockIdx.x;  // local row in chunk
+  const int tok = row0 + lr, st = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n = lane & 31, hh = lane >> 5;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int32_t* ridx = idx + row_id * K;
+  const int nblk = count_blocks(ridx, K, s_kv, tok + q_offset, &sh_last);
+  const int slot0 = st * kCT;
+  if (slot0 >= nblk * kBN) return;  // block-uniform
+
+  const uint16_t* grow = gbuf + ((int64_t)b * rows + lr) * (int64_t)K * kGW;
+  uint16_t* crow = cbuf + ((int64_t)b * rows + lr) * (int64_t)K * kDqk;
+  const int nheads_g = (H + kHG - 1) / kHG;  // head groups present
+  const int kdim = 2 * kHG * nheads_g;       // stacked rows actually used
+
+  // stage G tile: 128 slots x 256 bf16 (32 chunks per slot), position slot*32 + (c ^ (slot & 7))
+  for (int i = tid; i < kCT * 32; i += 512) {
+    const int slot = i >> 5, c = i & 31;
+    const int gs = slot0 + slot;
+    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+    if (gs < K) v = *reinterpret_cast<const u32x4*>(grow + (int64_t)gs * kGW + c * 8);
+    gt[slot * 32 + (c ^ (slot & 7))] = v;
+  }
+
+  // wave w: slot sub-tile (w & 3) x 32 slots, column half (w >> 2) x 288 columns
+  const int ss = wave & 3, ch = wave >> 2;
+  f32x16 acc[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) acc[t] = (f32x16){0};
+
+  const uint32_t xt_base = (uint32_t)(uintptr_t)(&xt[0]);
+  const uint32_t gt_base = (uint32_t)(uintptr_t)(&gt[0]);
+  const int s16 = lane & 15;
+  // C^T = X^T . G^T : A = X^T (lane: column, k-slots 8hh..+7) via transposed reads of the
+  // row-major X chunk; B = G^T (lane: slot, k-slots 8hh..+7) via b128 reads of the G tile.
+  const int tr_rowo = 8 * hh + (s16 >> 2);  // + 16 kk (+4 for the second read)
+  const int tr_cl = 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
+  for (int kc = 0; kc < kdim / kXK; ++kc) {
+    __syncthreads();  // previous chunk fully consumed (and G tile staged on the first pass)
+    const int hgk = kc >> 1, type = kc & 1;
+    for (int i = tid; i < kXChunks; i += 512) {
+      const int row = i / kRowChunks, c = i - row * kRowChunks;
+      const int head = hgk * kHG + row;
+      u32x4 v = (u32x4){0u, 0u, 0u, 0u};
+      if (head < H) {
+        if (type == 0) v = *reinterpret_cast<const u32x4*>(q + (row_id * H + head) * kDqk + c * 8);
+        else if (c < kDv / 8) v = *reinterpret_cast<const u32x4*>(dout + (row_id * H + head) * kDv + c * 8);
+      }
+      xt[row * kRowChunks + (c ^ (row & 7))] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kXK / 16; ++kk) {
+      // B operand: G[slot = 32 ss + n][64 kc + 16 kk + 8 hh .. +8]
+      const int slot = 32 * ss + n;
+      const int gc = (8 * kc + 2 * kk + hh) ^ (slot & 7);
+      const u32x4 bg = *(const lds_u32x4*)(gt_base + 16 * (slot * 32 + gc));
+      const int row1 = 16 * kk + tr_rowo, row2 = row1 + 4;
+#pragma unroll
+      for (int t = 0; t < 9; ++t) {
+        const int c0 = 288 * ch + 32 * t;  // first column of the tile
+        if (type == 1 && c0 >= kDv) continue;  // dO has no rope columns
+        const int cc = (c0 >> 3) + tr_cl;
+        const uint32_t a1 = xt_base + row1 * kRowBytes + 16 * (cc ^ (row1 & 7)) + 8 * (s16 & 1);
+        const uint32_t a2 = xt_base + row2 * kRowBytes + 16 * (cc ^ (row2 & 7)) + 8 * (s16 & 1);
+        const u32x4 a = tr_pair(a1, a2);
+        acc[t] = mfma32x32x16(as_bf16x8(a), as_bf16x8(bg), acc[t]);
+      }
+    }
+  }
+  // lane (slot n, hh) holds columns c0 + 8i + 4hh + r
+  const int slot = slot0 + 32 * ss + n;
+  if (slot >= K) return;
+  uint16_t* cr = crow + (int64_t)slot * kDqk;
+#pragma unroll
+  for (int t = 0; t < 9; ++t) {
+    const int c0 = 288 * ch + 32 * t;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint2 w;
+      w.x = pack_bf16x2(acc[t][4 * i], acc[t][4 * i + 1]);
+      w.y = pack_bf16x2(acc[t][4 * i + 2], acc[t][4 * i + 3]);
+      *reinterpret_cast<uint2*>(cr + c0 + 8 * i + 4 * hh) = w;
+    }
+  }
+}
+
+// --------------------------------------------------------------------------------------
+// exact fp32 path (any D): one workgroup per (token, head); dkv by fp32 atomics
+// --------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+bwd_exact_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, const int32_t* __restrict__ idx,
+                     const float* __restrict__ out, const float* __restrict__ dout, const float* __restrict__ smax,
+                     const float* __restrict__ ssum, float* __restrict__ dq, float* __restrict__ dkv, int S,
+                     int s_kv, int H, int K, int dqk, int dv, float scale, int64_t q_offset) {
+  extern __shared__ float ds[];  // K
+  __shared__ float red[256];
+  const int tok = blockIdx.x, head = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int64_t hr = row_id * H + head;
+  const int32_t* ridx = idx + row_id * K;
+  const float* qh = q + hr * dqk;
+  const float* doh = dout + hr * dv;
+  const float* kvb = kv + (int64_t)b * s_kv * dqk;
+  const int64_t limit = tok + q_offset;
+  float part = 0.f;
+  for (int d = tid; d < dv; d += 256) part += doh[d] * out[hr * dv + d];
+  red[tid] = part;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (tid < st) red[tid] += red[tid + st];
+    __syncthreads();
+  }
+  const float delta = red[0];
+  const float sm = ssum[hr];
+  const float lse = sm > 0.f ? smax[hr] + logf(sm) : INFINITY;
+  __syncthreads();
+  for (int j = tid; j < K; j += 256) {
+    const int v = ridx[j];
+    float g = 0.f;
+    if (slot_ok(v, s_kv, limit)) {
+      const float* kr = kvb + (int64_t)v * dqk;
+      float s = 0.f, dp = 0.f;
+      for (int d = 0; d < dqk; ++d) s = fmaf(qh[d], kr[d], s);
+      for (int d = 0; d < dv; ++d) dp = fmaf(doh[d], kr[d], dp);
+      const float p = expf(s * scale - lse);
+      g = p * (dp - delta);
+      // dV part (uses p) goes straight out; dK part below
+      for (int d = 0; d < dv; ++d) atomicAdd(&dkv[((int64_t)b * s_kv + v) * dqk + d], p * doh[d]);
+    }
+    ds[j] = g;
+  }
+  __syncthreads();
+  for (int d = tid; d < dqk; d += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < K; ++j) {
+      const float g = ds[j];
+      if (g == 0.f) continue;
+      const int v = ridx[j];
+      acc = fmaf(g, kvb[(int64_t)v * dqk + d], acc);
+      atomicAdd(&dkv[((int64_t)b * s_kv + v) * dqk + d], scale * g * qh[d]);
+    }
+    dq[hr * dqk + d] = scale * acc;
+  }
+}
+
+struct BwdPlan {
+  int64_t rows;  // query rows per chunk
+  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, total;
+};
+
+BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget) {
+  BwdPlan p{};
+  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4);
+  int64_t rows = s_q;
+  if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
+  p.rows = rows;
+  p.g_bytes = batch * rows * topk * kGW * 2;
+  p.c_bytes = batch * rows * topk * kDqk * 2;
+  p.pairs_bytes = rows * topk * 4;
+  p.csr_bytes = (3 * (s_kv + 1)) * 4;
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes);
+  return p;
+}
+
+constexpr int64_t kDefaultBudget = 16LL << 30;  // scratch for the G / C chunks
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
+                                                     int64_t d_qk, int64_t topk) {
+  (void)n_heads;
+  (void)d_qk;
+  if (batch <= 0 || s_q <= 0 || s_kv <= 0 || topk <= 0) return 0;
+  return dsa::plan_bwd(batch, s_q, s_kv, topk, dsa::kDefaultBudget).total;
+}
+
+extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out,
+                                  const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
+                                  float* dkv_accum, void* workspace, int64_t workspace_bytes, int dtype, int64_t batch,
+                                  int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
+                                  int64_t topk, float scale, int64_t q_offset, void* stream) {
+  using namespace dsa;
+  if (!q || !kv || !indices || !out || !dout || !softmax_max || !softmax_sum || !dq || !dkv_accum)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: null pointer");
+  if (batch <= 0 || s_q <= 0 || s_kv <= 0 || n_heads <= 0 || topk <= 0 || d_v <= 0 || d_qk < d_v)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: bad sizes");
+  if (s_q > 2147483647LL || s_kv > 2147483647LL || batch > 65535 || topk > (1 << 20))
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: sizes out of range");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DSA_F32) {
+    if (topk * 4 > 64 * 1024) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: fp32 topk <= 16384");
+    if (s_q > 2147483647LL || n_heads > 65535)
+      return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: sizes out of range");
+    dim3 grid((unsigned)s_q, (unsigned)n_heads, (unsigned)batch);
+    bwd_exact_f32_kernel<<<grid, 256, topk * 4, st>>>(
+        (const float*)q, (const float*)kv, indices, (const float*)out, (const float*)dout, softmax_max, softmax_sum,
+        (float*)dq, dkv_accum, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset);
+    return check_launch("dsa_sparse_mla_bwd(f32)");
+  }
+  if (dtype != DSA_BF16) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: dtype %d", dtype);
+  if (d_qk != kDqk || d_v != kDv)
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: bf16 path needs d_qk=576, d_v=512");
+  if (n_heads > kHeadsMax) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: bf16 path needs H <= 128");
+  if (!workspace) return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: workspace required");
+  // choose the largest chunk whose scratch fits the given workspace
+  BwdPlan plan = plan_bwd(batch, s_q, s_kv, topk, workspace_bytes);
+  while (plan.total > workspace_bytes && plan.rows > 1) plan = plan_bwd(batch, plan.rows - 1, s_kv, topk, 0);
+  if (plan.total > workspace_bytes)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: workspace of %lld bytes is too small",
+                     (long long)workspace_bytes);
+  auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
+  char* ws = (char*)workspace;
+  uint16_t* gbuf = (uint16_t*)ws;
+  uint16_t* cbuf = (uint16_t*)(ws + al(plan.g_bytes));
+  int* pairs = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes));
+  int* counts = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes));
+  const unsigned hgroups = ceil_div(n_heads, kHG);
+
+  for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
+    const int rows = (int)std::min<int64_t>(plan.rows, s_q - r0);
+    dim3 ga((unsigned)rows, hgroups, (unsigned)batch);
+    bwd_dq_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)out,
+                                      (const uint16_t*)dout, softmax_max, softmax_sum, (uint16_t*)dq, gbuf, (int)s_q,
+                                      (int)s_kv, (int)n_heads, (int)topk, scale, q_offset, (int)r0);
+    if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
+    dim3 gb((unsigned)rows, ceil_div(topk, kCT), (unsigned)batch);
+    bwd_contrib_kernel<<<gb, 512, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf, (int)s_q,
+                                           (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0, rows);
+    if (int rc = check_launch("dsa_sparse_mla_bwd(contrib)")) return rc;
+    for (int b = 0; b < (int)batch; ++b)
+      if (int rc = csr_reduce(indices, cbuf, dkv_accum, pairs, counts, (int)s_q, (int)s_kv, (int)topk, q_offset,
+                              (int)r0, rows, b, kRowChunks, st))
+        return rc;
+  }
+  return DSA_OK;
+}

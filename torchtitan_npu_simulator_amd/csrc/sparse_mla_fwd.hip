@@ -291,6 +291,177 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   }
 }
 
+// Head-summed softmax mass at the selected slots (target of the indexer KL loss):
+//   mass[s, j] = sum_h exp2(S[h, j] * scale * log2e - lse2[h]),  lse2 from softmax_max/sum.
+// Same token-per-workgroup gather and pair-split QK as the forward (8 waves, 128 heads);
+// each wave sums P over its 32 heads with a 5-step butterfly (16 shuffles), the four head
+// groups are added in LDS and one 128-byte row segment is stored per block.
+__global__ void __launch_bounds__(kThreads, 1)
+attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv,
+                      const int32_t* __restrict__ idx, const float* __restrict__ smax, const float* __restrict__ ssum,
+                      float* __restrict__ mass, int S, int s_kv, int H, int K, float scale_log2, int64_t q_offset) {
+  __shared__ u32x4 tile[2][kTileChunks];
+  __shared__ u32x4 qpe[kHeadsPerWG][(kDqk - kDv) / 8];
+  __shared__ f32x4 xs[kWaves][4][64];
+  __shared__ float macc[2][kBN];
+  __shared__ uint32_t vmask[2];
+  __shared__ int last_slot;
+
+  const int tok = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, n = lane & 31, hh = lane >> 5;
+  const int grp = wave & 3, half = wave >> 2;
+  const int head = blockIdx.y * kHeadsPerWG + grp * 32 + n;
+  const bool head_ok = head < H;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int32_t* ridx = idx + row_id * K;
+  const int64_t limit = tok + q_offset;
+  const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
+  const int64_t hrow = row_id * H + (head_ok ? head : 0);
+  float* mrow = mass + row_id * K;
+
+  if (tid == 0) last_slot = -1;
+  if (tid < 2 * kBN) macc[tid / kBN][tid % kBN] = 0.f;
+  __syncthreads();
+  {
+    int last = -1;
+    for (int j = tid; j < K; j += kThreads)
+      if (slot_ok(ridx[j], s_kv, limit)) last = j;
+    if (last >= 0) atomicMax(&last_slot, last);
+  }
+  __syncthreads();
+  const int nblk = (last_slot + kBN) / kBN;
+  if (blockIdx.y == 0)  // slots past the last usable block are zero
+    for (int j = nblk * kBN + tid; j < K; j += kThreads) mrow[j] = 0.f;
+  if (nblk == 0) return;
+
+  float lse2;
+  {
+    const float sm = head_ok ? ssum[hrow] : 0.f;
+    lse2 = sm > 0.f ? (smax[hrow] + logf(sm)) * kLog2e : INFINITY;
+  }
+  u32x4 qr[kQSteps];
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
+#pragma unroll
+    for (int c = 0; c < kQSteps; ++c)
+      qr[c] = head_ok ? qh[32 * half + 2 * c + hh] : (u32x4){0u, 0u, 0u, 0u};
+    if (half == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int ch = 2 * c + hh;
+        qpe[grp * 32 + n][ch] = head_ok ? qh[2 * (kDv / 16) + ch] : (u32x4){0u, 0u, 0u, 0u};
+      }
+    }
+  }
+  auto load_block = [&](int blk, int buf) {
+    int v[5], chunk[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int J = wave + kWaves * i;
+      const int p = min(J, kTileInstr - 1) * 64 + lane;
+      const int row = p / kRowChunks, pos = p - row * kRowChunks;
+      chunk[i] = pos ^ (row & 7);
+      const int slot = blk * kBN + row;
+      v[i] = ridx[min(slot, K - 1)];
+      if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int J = wave + kWaves * i;
+      if (J < kTileInstr)
+        __builtin_amdgcn_global_load_lds((const void*)(kvb + (int64_t)v[i] * kDqk + chunk[i] * 8),
+                                         (__attribute__((address_space(3))) void*)&tile[buf][J * 64], 16, 0, 0);
+    }
+    if (wave == 0) {
+      const int slot = blk * kBN + lane;
+      const bool ok = lane < kBN && slot < K && slot_ok(ridx[min(slot, K - 1)], s_kv, limit);
+      const uint64_t bal = __ballot(ok);
+      if (lane == 0) vmask[buf] = (uint32_t)bal;
+    }
+  };
+  const uint32_t tile_base = (uint32_t)(uintptr_t)(&tile[0][0]);
+  const int xsw = n & 7;
+  uint32_t qk_off[4];
+#pragma unroll
+  for (int c4 = 0; c4 < 4; ++c4) qk_off[c4] = n * kRowBytes + 512 * half + 16 * ((2 * c4 + hh) ^ xsw);
+  uint32_t pe_off[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) pe_off[c] = n * kRowBytes + 16 * ((64 + 4 * half + 2 * c + hh) ^ xsw);
+
+  load_block(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int buf = blk & 1;
+    if (blk + 1 < nblk) load_block(blk + 1, buf ^ 1);
+    const uint32_t tb = tile_base + buf * kTileBytes;
+    f32x16 s = (f32x16){0};
+    {
+      u32x4 a = *(const lds_u32x4*)(tb + qk_off[0]);
+#pragma unroll
+      for (int c = 0; c < kQSteps + 2; ++c) {
+        u32x4 an = a;
+        if (c + 1 < kQSteps)
+          an = *(const lds_u32x4*)(tb + qk_off[(c + 1) & 3] + 128 * ((c + 1) >> 2));
+        else if (c + 1 < kQSteps + 2)
+          an = *(const lds_u32x4*)(tb + pe_off[c + 1 - kQSteps]);
+        const u32x4 bq = c < kQSteps ? qr[c] : qpe[grp * 32 + n][4 * half + 2 * (c - kQSteps) + hh];
+        s = mfma32x32x16(as_bf16x8(a), as_bf16x8(bq), s);
+        a = an;
+      }
+    }
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4)
+      xs[wave][r4][lane] = (f32x4){s[4 * r4], s[4 * r4 + 1], s[4 * r4 + 2], s[4 * r4 + 3]};
+    __syncthreads();
+    if (half == 0) {
+      const uint32_t vm = vmask[buf];
+      float v[16];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x4 other = xs[wave ^ 4][r4][lane];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * r4 + u;
+          const int key = 8 * (r >> 2) + 4 * hh + (r & 3);
+          const float x = s[r] + other[u];
+          v[r] = ((vm >> key) & 1u) ? exp2f(x * scale_log2 - lse2) : 0.f;
+        }
+      }
+      // butterfly over the 32 head lanes of this half-wave: after the steps on lane bits
+      // 4,3,2,1 lane l holds the partial for value (l >> 1) & 15; bit 0 completes the sum
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int lb = 4 - st, m = 1 << lb;
+        const bool up = (lane >> lb) & 1;
+        const int nh = 8 >> st;  // values kept after this step
+#pragma unroll
+        for (int j = 0; j < nh; ++j) {
+          const float send = up ? v[j] : v[j + nh];
+          const float keep = up ? v[j + nh] : v[j];
+          v[j] = keep + __shfl_xor(send, m, 64);
+        }
+      }
+      const float tot = v[0] + __shfl_xor(v[0], 1, 64);
+      if ((lane & 1) == 0) {
+        const int r = (lane >> 1) & 15;
+        const int key = 8 * (r >> 2) + 4 * hh + (r & 3);
+        atomicAdd(&macc[buf][key], tot);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid < kBN) {
+      const int slot = blk * kBN + tid;
+      if (slot < K) {
+        if (gridDim.y == 1) mrow[slot] = macc[buf][tid];
+        else atomicAdd(&mrow[slot], macc[buf][tid]);
+      }
+      macc[buf][tid] = 0.f;
+    }
+  }
+}
+
 __device__ __forceinline__ float ld_elem(const float* p, int64_t i) { return p[i]; }
 __device__ __forceinline__ float ld_elem(const uint16_t* p, int64_t i) { return bf16_to_f(p[i]); }
 __device__ __forceinline__ void st_elem(float* p, int64_t i, float v) { p[i] = v; }
@@ -368,9 +539,73 @@ sparse_mla_fwd_exact_kernel(const T* __restrict__ q, const T* __restrict__ kv, c
   }
 }
 
+// exact fp32 mass: one workgroup per token, thread per slot, heads looped
+__global__ void __launch_bounds__(256)
+attn_mass_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, const int32_t* __restrict__ idx,
+                     const float* __restrict__ smax, const float* __restrict__ ssum, float* __restrict__ mass, int S,
+                     int s_kv, int H, int K, int dqk, float scale, int64_t q_offset) {
+  const int tok = blockIdx.x, b = blockIdx.z;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int32_t* ridx = idx + row_id * K;
+  const float* kvb = kv + (int64_t)b * s_kv * dqk;
+  for (int j = threadIdx.x; j < K; j += 256) {
+    const int v = ridx[j];
+    float acc = 0.f;
+    if (slot_ok(v, s_kv, tok + q_offset)) {
+      const float* kr = kvb + (int64_t)v * dqk;
+      for (int h = 0; h < H; ++h) {
+        const int64_t hr = row_id * H + h;
+        const float sm = ssum[hr];
+        if (!(sm > 0.f)) continue;
+        const float* qh = q + hr * dqk;
+        float dot = 0.f;
+        for (int d = 0; d < dqk; ++d) dot = fmaf(qh[d], kr[d], dot);
+        acc += expf(dot * scale - smax[hr] - logf(sm));
+      }
+    }
+    mass[row_id * K + j] = acc;
+  }
+}
+
 }  // namespace
 
 }  // namespace dsa
+
+extern "C" int dsa_attn_mass(const void* q, const void* kv, const int32_t* indices, const float* softmax_max,
+                             const float* softmax_sum, float* mass, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
+                             int64_t n_heads, int64_t d_qk, int64_t topk, float scale, int64_t q_offset,
+                             void* stream) {
+  using namespace dsa;
+  if (!q || !kv || !indices || !softmax_max || !softmax_sum || !mass)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_attn_mass: null pointer");
+  if (batch <= 0 || s_q <= 0 || s_kv <= 0 || n_heads <= 0 || topk <= 0)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_attn_mass: bad sizes");
+  if (s_q > 2147483647LL || batch > 65535 || s_kv > 2147483647LL)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_attn_mass: sizes out of range");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DSA_BF16) {
+    if (d_qk != kDqk) return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: bf16 path needs d_qk=576");
+    const unsigned hgroups = ceil_div(n_heads, kHeadsPerWG);
+    if (hgroups > 1) {  // partial sums from several head groups accumulate into a zeroed buffer
+      if (hipMemsetAsync(mass, 0, (size_t)(batch * s_q * topk) * 4, st) != hipSuccess)
+        return set_error(DSA_ERR_LAUNCH, "dsa_attn_mass: memset failed");
+    }
+    dim3 grid((unsigned)s_q, hgroups, (unsigned)batch);
+    attn_mass_bf16_kernel<<<grid, kThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, softmax_max,
+                                                     softmax_sum, mass, (int)s_q, (int)s_kv, (int)n_heads, (int)topk,
+                                                     scale * kLog2e, q_offset);
+    return check_launch("dsa_attn_mass(bf16)");
+  }
+  if (dtype == DSA_F32) {
+    if (n_heads > 65535) return set_error(DSA_ERR_INVALID_ARG, "dsa_attn_mass: sizes out of range");
+    dim3 grid((unsigned)s_q, 1, (unsigned)batch);
+    attn_mass_f32_kernel<<<grid, 256, 0, st>>>((const float*)q, (const float*)kv, indices, softmax_max, softmax_sum,
+                                               mass, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, scale,
+                                               q_offset);
+    return check_launch("dsa_attn_mass(f32)");
+  }
+  return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: dtype %d", dtype);
+}
 
 extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, void* out, float* softmax_max,
                                   float* softmax_sum, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,

@@ -33,6 +33,7 @@ __all__ = [
     "sparse_mla_fwd",
     "sparse_mla_bwd",
     "attn_mass",
+    "indexer_kl_grad_from_mass",
     "indexer_scores",
     "topk_select",
     "quantize_fp8_per_row",
@@ -192,8 +193,11 @@ def sparse_mla_fwd(q, kv, indices, scale, *, d_v=512, q_offset=0):
     return out, smax, ssum
 
 
-def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0):
-    """(dq like q, dkv fp32 [B,S_kv,D_qk]) from dsa_sparse_mla_bwd."""
+def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, workspace_bytes=None):
+    """(dq like q, dkv fp32 [B,S_kv,D_qk]) from dsa_sparse_mla_bwd.
+
+    ``workspace_bytes`` caps the scratch (fewer bytes -> more query-row chunks).
+    """
     lib = load_library()
     B, S, H, D = q.shape
     s_kv = kv.shape[1]
@@ -204,6 +208,8 @@ def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0):
     dq = torch.empty_like(q)
     dkv = torch.zeros(B, s_kv, D, dtype=torch.float32, device=q.device)
     ws_bytes = int(lib.dsa_sparse_mla_bwd_workspace_size(B, S, s_kv, H, D, K))
+    if workspace_bytes is not None:
+        ws_bytes = int(workspace_bytes)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     check(
         lib.dsa_sparse_mla_bwd(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax), ptr(ssum), ptr(dq),
@@ -356,23 +362,38 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     idx = sparse_indices.reshape(B, S, -1).to(torch.int32).contiguous()
     K = idx.shape[-1]
     mass = attn_mass(q, kv3, idx, softmax_max, softmax_sum, scale_value, q_offset=q_off)
+    dq_i, dk_i, dw, loss_rows = indexer_kl_grad_from_mass(query_index, key_index, weight, idx, mass, q_offset=q_off,
+                                                          loss_scale=loss_scale, eps=eps, grad_scale=grad_scale)
+    return dq_i, dk_i.reshape(key_index.shape), dw, loss_rows.sum().reshape(1)
+
+
+def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, q_offset=0, loss_scale=1.0, eps=1e-8,
+                              grad_scale=1.0):
+    """(dq_idx fp32, dk_idx fp32 [B,S_k,D_I], dw fp32, loss_rows fp32 [B,S]) given the target mass."""
+    lib = load_library()
     ki = key_index.squeeze(2) if key_index.dim() == 4 else key_index
     qi = query_index.to(torch.bfloat16).contiguous()
     ki = ki.to(torch.bfloat16).contiguous()
     w = weight.float().contiguous()
-    HI, DI = qi.shape[2], qi.shape[3]
+    B, S, HI, DI = qi.shape
     s_k = ki.shape[1]
-    dq_i = torch.empty(B, S, HI, DI, dtype=torch.float32, device=q.device)
-    dk_i = torch.zeros(B, s_k, DI, dtype=torch.float32, device=q.device)
-    dw = torch.empty(B, S, HI, dtype=torch.float32, device=q.device)
-    loss_rows = torch.empty(B, S, dtype=torch.float32, device=q.device)
+    idx = indices.reshape(B, S, -1).to(torch.int32).contiguous()
+    K = idx.shape[-1]
+    mass = mass.float().contiguous()
+    dev = qi.device
+    dq_i = torch.empty(B, S, HI, DI, dtype=torch.float32, device=dev)
+    dk_i = torch.zeros(B, s_k, DI, dtype=torch.float32, device=dev)
+    dw = torch.empty(B, S, HI, dtype=torch.float32, device=dev)
+    loss_rows = torch.empty(B, S, dtype=torch.float32, device=dev)
+    ws_bytes = int(lib.dsa_indexer_kl_grad_workspace_size(B, S, s_k, HI, DI, K))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     check(
         lib.dsa_indexer_kl_grad(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i), ptr(dw),
-                                ptr(loss_rows), B, S, s_k, HI, DI, K, q_off, float(loss_scale), float(eps),
-                                float(grad_scale), stream_of(q.device)),
+                                ptr(loss_rows), ptr(ws), ws_bytes, B, S, s_k, HI, DI, K, int(q_offset),
+                                float(loss_scale), float(eps), float(grad_scale), stream_of(dev)),
         "dsa_indexer_kl_grad",
     )
-    return dq_i, dk_i.reshape(key_index.shape), dw, loss_rows.sum().reshape(1)
+    return dq_i, dk_i, dw, loss_rows
 
 
 def default_softmax_scale(d_qk: int) -> float:
