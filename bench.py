@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""DSA sparse-attention fwd+bwd throughput on one MI355X (tokens/s) with roofline accounting.
+
+One step = one pass of the DeepSeek-V3.2 DSA hot path over one synthetic batch
+(config C3 by default: B=1, S=8192, H=128, D_qk=576 / D_v=512, top-k 2048, indexer
+64 heads x 128 with fp8-e4m3 per-token-scaled keys and queries):
+
+  fp8 quantise q_I, k_I -> lightning indexer + top-k -> sparse MLA forward ->
+  attention mass -> indexer KL loss gradients -> sparse MLA backward (dQ, dKV)
+
+Inputs are resident in HBM before the timed region.  Prints ONE JSON line.  The
+``roofline`` object is for the dominant kernel, using the algorithmic byte formulas of
+the DSA path (documented in DESIGN.md) over that kernel's average duration, measured
+with HIP events on the stream the kernel runs on.  ``cpu_baseline`` times the CPU oracle
+(fp32, all host threads) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--seq", type=int, default=8192)
+    p.add_argument("--heads", type=int, default=128)
+    p.add_argument("--topk", type=int, default=2048)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--phases", action="store_true", help="also print per-phase timings to stderr")
+    return p.parse_args()
+
+
+def make_inputs(S, H, topk, seed, device):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    d_qk, d_v, h_i, d_i = 576, 512, 64, 128
+    # fixed draw order: q, kv, q_idx, k_idx, w, dout
+    q = torch.randn(1, S, H, d_qk, generator=g)
+    kv = torch.randn(1, S, d_qk, generator=g)
+    q_idx = torch.randn(1, S, h_i, d_i, generator=g)
+    k_idx = torch.randn(1, S, d_i, generator=g)
+    w = torch.rand(1, S, h_i, generator=g) * h_i ** -0.5 * d_i ** -0.5
+    dout = torch.randn(1, S, H, d_v, generator=g)
+    to = dict(device=device)
+    return dict(
+        q=q.to(torch.bfloat16).to(**to),
+        kv=kv.to(torch.bfloat16).to(**to),
+        q_idx=q_idx.to(torch.bfloat16).to(**to),
+        k_idx=k_idx.to(torch.bfloat16).to(**to),
+        w=w.to(**to),
+        dout=dout.to(torch.bfloat16).to(**to),
+        scale=d_qk ** -0.5,
+        topk=topk,
+    )
+
+
+class PhaseTimer:
+    """HIP events on the current stream around each phase; averages over timed steps."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.events = {}
+        self.enabled = False
+
+    def __call__(self, name):
+        timer = self
+
+        class _Ctx:
+            def __enter__(self_inner):
+                if timer.enabled:
+                    self_inner.e0 = timer.torch.cuda.Event(enable_timing=True)
+                    self_inner.e1 = timer.torch.cuda.Event(enable_timing=True)
+                    self_inner.e0.record()
+
+            def __exit__(self_inner, *exc):
+                if timer.enabled:
+                    self_inner.e1.record()
+                    timer.events.setdefault(name, []).append((self_inner.e0, self_inner.e1))
+
+        return _Ctx()
+
+    def averages_ms(self):
+        out = {}
+        for k, evs in self.events.items():
+            out[k] = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
+        return out
+
+
+def dsa_step(inp, ops, timer):
+    """One DSA layer forward + backward; returns the tensors a trainer would consume."""
+    with timer("quantize"):
+        q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
+        k8, ks = ops.quantize_fp8_per_row(inp["k_idx"])
+    with timer("indexer_topk"):
+        idx, _ = ops.npu_lightning_indexer(q8, k8, inp["w"], sparse_count=inp["topk"], sparse_mode=3,
+                                           query_scale=qs, key_scale=ks)
+        idx = idx[:, :, 0]
+    with timer("attn_fwd"):
+        out, smax, ssum = ops.sparse_mla_fwd(inp["q"], inp["kv"], idx, inp["scale"])
+    with timer("attn_mass"):
+        mass = ops.attn_mass(inp["q"], inp["kv"], idx, smax, ssum, inp["scale"])
+    with timer("indexer_kl_grad"):
+        dq_i, dk_i, dw, loss_rows = ops.indexer_kl_grad_from_mass(inp["q_idx"], inp["k_idx"], inp["w"], idx, mass)
+    with timer("attn_bwd"):
+        dq, dkv = ops.sparse_mla_bwd(inp["q"], inp["kv"], idx, out, inp["dout"], smax, ssum, inp["scale"])
+    return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss_rows)
+
+
+def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128):
+    """Bytes and FLOPs of the DSA path per step (formulas documented in DESIGN.md)."""
+    sum_keff = int((idx >= 0).sum().item())
+    causal_pairs = S * (S + 1) // 2
+    K = topk
+    fwd_bytes = 2 * H * d_qk * S + 2 * d_qk * sum_keff + 4 * K * S + 2 * H * d_v * S + 4 * H * S
+    bwd_bytes = (2 * H * d_qk * S * 2 + 2 * H * d_v * S * 2 + 4 * H * S + 4 * K * S + 2 * d_qk * sum_keff
+                 + 4 * d_qk * sum_keff)
+    return dict(
+        sum_keff=sum_keff,
+        attn_fwd_bytes=fwd_bytes,
+        attn_bwd_bytes=bwd_bytes,
+        attn_fwd_flops=2 * H * (d_qk + d_v) * sum_keff,
+        attn_bwd_flops=2 * H * (3 * d_qk + 2 * d_v) * sum_keff,
+        indexer_flops=2 * h_i * d_i * causal_pairs,
+        topk_bytes=4 * causal_pairs + 4 * K * S,
+    )
+
+
+def cpu_baseline(inp_gpu, S, H, topk, seconds):
+    """Time the CPU oracle (fp32, all host threads) on the last rows of the same workload."""
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import dsa_oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    cpu = {k: (v.cpu() if hasattr(v, "cpu") else v) for k, v in inp_gpu.items()}
+    q, kv, qi, ki, w, do = (cpu[k].float() for k in ("q", "kv", "q_idx", "k_idx", "w", "dout"))
+    qi8, qis = O.quantize_e4m3_per_row(qi)
+    ki8, kis = O.quantize_e4m3_per_row(ki)
+    qid = qi8.float() * qis.unsqueeze(-1)
+    kid = ki8.float() * kis.unsqueeze(-1)
+
+    def run(rows):
+        r0 = S - rows
+        # the last `rows` query rows against the full KV prefix (q_offset = r0)
+        sc = O.indexer_scores(qid[:, r0:], kid, w[:, r0:], q_offset=r0)
+        idx = O.topk_select(sc, topk, q_offset=r0)
+        out, lse = O.sparse_mla_fwd(q[:, r0:], kv, idx, cpu["scale"], q_offset=r0, dtype=torch.float32, chunk=8)
+        O.indexer_kl_loss_grad(q[:, r0:], kv, qi[:, r0:], ki, w[:, r0:], idx, lse, cpu["scale"], q_offset=r0,
+                               dtype=torch.float32)
+        O.sparse_mla_bwd_closed_form(q[:, r0:], kv, idx, out, lse, do[:, r0:], cpu["scale"], q_offset=r0,
+                                     dtype=torch.float32)
+
+    rows = 4
+    run(rows)  # warm-up
+    t0 = time.perf_counter()
+    run(rows)
+    dt = time.perf_counter() - t0
+    rows = max(4, min(256, S, int(rows * seconds / max(dt, 1e-3) / 3)))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run(rows)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[1]
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(
+        value=rows / med,
+        unit="tokens/s",
+        cores=threads,
+        kind="port",
+        sample=(f"fp32 CPU oracle of the full step (fp8-dequantised indexer, top-k, attention fwd, "
+                f"indexer KL grads, attention bwd) on the last {rows} of {S} query rows against the "
+                f"full KV prefix, median of 3 runs; host CPU: {model}"),
+    )
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the DSA path shards by query rows, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    dev = torch.device("cuda:0")
+    S, H, K = args.seq, args.heads, args.topk
+    inp = make_inputs(S, H, K, args.seed, dev)
+    timer = PhaseTimer(torch)
+    for _ in range(args.warmup):
+        res = dsa_step(inp, ops, timer)
+    torch.cuda.synchronize()
+    timer.enabled = True
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(args.steps):
+        res = dsa_step(inp, ops, timer)
+    t1.record()
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    phases = timer.averages_ms()
+    work = algorithmic_work(S, H, K, res["idx"])
+
+    # dominant kernel: the attention backward entry (dQ/G, contribution GEMM, CSR reduce)
+    bwd_ms = phases["attn_bwd"]
+    fwd_ms = phases["attn_fwd"]
+    attn_bytes = work["attn_fwd_bytes"] + work["attn_bwd_bytes"]
+    roof = dict(
+        bound="hbm",
+        kernel="gathered sparse MLA attention fwd+bwd (dsa_sparse_mla_fwd + dsa_sparse_mla_bwd)",
+        achieved=attn_bytes / ((fwd_ms + bwd_ms) * 1e-3) / 1e9,
+        peak=HBM_PEAK_GBPS,
+        unit="GB/s",
+        traffic=None,
+    )
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    idx_ms = phases["indexer_topk"]
+    line = dict(
+        metric="sparse-attn fwd+bwd tokens/s @S=8K,top-k 2048; % HBM / MFMA roofline",
+        value=S / (ms_per_step * 1e-3),
+        unit="tokens/s",
+        n_gpus=1,
+        steps=args.steps,
+        warmup=args.warmup,
+        ms_per_step=ms_per_step,
+        higher_is_better=True,
+        scaling="weak",
+        vs_baseline=None,
+        dtype="bf16 (attention), fp8-e4m3 (indexer)",
+        data="synthetic, seeded N(0,1) inputs",
+        config=dict(workload="C3: DeepSeek-V3.2 DSA layer fwd+bwd", batch=1, seq_len=S, heads=H, d_qk=576, d_v=512,
+                    topk=K, index_heads=64, index_dim=128, sum_k_eff=work["sum_keff"]),
+        roofline=roof,
+        phases_ms={k: round(v, 4) for k, v in phases.items()},
+        indexer_mfma=dict(flops=work["indexer_flops"], ms_with_topk=idx_ms,
+                          tflops_upper_bound=work["indexer_flops"] / (idx_ms * 1e-3) / 1e12,
+                          peak_tflops=FP8_PEAK_TFLOPS),
+        attn_mfma=dict(fwd_tflops=work["attn_fwd_flops"] / (fwd_ms * 1e-3) / 1e12,
+                       bwd_tflops=work["attn_bwd_flops"] / (bwd_ms * 1e-3) / 1e12, peak_tflops=BF16_PEAK_TFLOPS),
+    )
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(inp, S, H, K, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
