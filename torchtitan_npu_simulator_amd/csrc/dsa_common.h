@@ -60,6 +60,12 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// LDS row swizzle for tiles whose rows are a multiple of 128 B apart: 16-byte chunk c of
+// row r lives at chunk c ^ swz8(r).  swz8 maps any 8 consecutive rows to distinct values
+// (8-lane b128 reads of one column are conflict-free) and rows 4k..4k+3 to distinct even
+// values (a 4-row x 32-byte transposed read covers all banks once).
+__device__ __forceinline__ int swz8(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
 inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 
 }  // namespace dsa

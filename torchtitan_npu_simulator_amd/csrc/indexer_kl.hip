@@ -1,18 +1,20 @@
 // Indexer KL loss and gradients at the selected keys (the fused op
 // npu_sparse_lightning_indexer_grad_kl_loss of the reference).
 //
-// Per query row s (one workgroup, 4 waves, wave w owns index heads 16w..16w+15):
-//   phase 1  I_j = sum_h w_h relu(q_h . k_{idx_j}) for every slot j: S = q k^T on
-//            v_mfma_f32_16x16x32_bf16 over 32-slot blocks of gathered key rows (LDS),
-//            relu * w summed in-lane, across lane groups and across waves (LDS adds)
+// Per query row s (one workgroup, 4 waves, wave w owns index heads 16w..16w+15), over
+// blocks of 64 selected slots whose key rows are DMA'd into a double-buffered LDS tile:
+//   phase 1  I_j = sum_h w_h relu(q_h . k_{idx_j}): S = q k^T on v_mfma_f32_16x16x32_bf16,
+//            relu * w summed in-lane and across lane groups; the four per-wave partials
+//            are written to LDS and added by one thread per slot (no LDS atomics)
 //   phase 2  row statistics: softmax of I over usable slots, target t = mass / Z, the
 //            row loss Z * sum_{t>0} t (log max(t, eps) - log_softmax(I)) * loss_scale and
 //            g_j = dloss/dI_j = Z * loss_scale * grad_scale * (softmax_j * T - t_j)
-//   phase 3  recompute S; E = g_j w_h [S > 0];  dw_h = sum_j g_j relu(S);
-//            dq^T += k^T E^T (k read transposed with ds_read_tr16_b64);
-//            dk contribution of slot j = sum_h E[h, j] q_h (v_mfma_f32_16x16x16_bf16 per
-//            wave, summed over waves in LDS) written as bf16 and reduced per key through
-//            the shared CSR pass (no float atomics).
+//   phase 3  recompute S; E = g_j w_h [S > 0] staged in LDS as [slot][head] and
+//            [head][slot]; dw_h = sum_j g_j relu(S);
+//            dq^T[d x 16 heads] += k^T E^T (k read transposed with ds_read_tr16_b64);
+//            dk^T[32 d of wave w x slots] = q^T E over all 64 heads, written as bf16 and
+//            reduced per key by the shared CSR pass (no float atomics anywhere).
+// LDS key rows use the swz8 chunk swizzle (conflict-free b128 and transposed reads).
 // A generic fp32 kernel (any H, D) handles shapes outside the MFMA tile.
 #include <algorithm>
 
@@ -24,8 +26,9 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kH = 64;
-constexpr int kB = 32;           // slots per block
+constexpr int kB = 64;           // slots per block
 constexpr int kRowC = kD / 8;    // 16 chunks per key row
+constexpr int kTileC = kB * kRowC;  // 1024 chunks (16 KB)
 constexpr int kMaxK = 4096;
 
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
@@ -56,12 +59,12 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
                        const int32_t* __restrict__ idx, const float* __restrict__ mass, float* __restrict__ dq,
                        float* __restrict__ dw, float* __restrict__ loss_rows, uint16_t* __restrict__ ck, int S,
                        int s_k, int K, int64_t q_offset, float loss_scale, float eps, float grad_scale, int row0) {
-  __shared__ u32x4 kt[kB * kRowC];          // gathered key rows [32][16 chunks], XOR-swizzled
+  __shared__ u32x4 kt[2][kTileC];           // gathered key rows [64][16 chunks], swizzled
   __shared__ float iv[kMaxK];               // I_j, then g_j
-  __shared__ float dkp[kB][kD + 4];         // dk contributions of one block (fp32, summed over waves)
-  __shared__ uint16_t et[4][16][kB + 8];    // E per wave, [head][slot] (transposed for dq)
+  __shared__ float ip[4][kB];               // per-wave partial I of one block
+  __shared__ uint16_t es[kB][kH + 8];       // E as [slot][head]
+  __shared__ uint16_t eh[kH][kB + 8];       // E as [head][slot]
   __shared__ float red[4];
-  __shared__ float stats[4];
 
   const int lr = blockIdx.x, b = blockIdx.y;
   const int tok = row0 + lr;
@@ -81,72 +84,86 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
 #pragma unroll
     for (int c = 0; c < kD / 32; ++c) qa[c] = qh[4 * c + g];
   }
-  // transposed q for the dk contribution (A of 16x16x16: lane (d col, g) holds heads 4g..4g+3)
-  i16x4v qt[kD / 16];
+  // q^T for dk (A of 16x16x32 over heads): wave w covers d = 32w + 16 dt + col, k-step ks covers
+  // heads 32 ks + 8g .. +7
+  u32x4 qtr[2][2];
 #pragma unroll
-  for (int dt = 0; dt < kD / 16; ++dt)
+  for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      qt[dt][i] = (short)qi[(row_id * kH + 16 * wave + 4 * g + i) * kD + 16 * dt + col];
+    for (int ks = 0; ks < 2; ++ks) {
+      const int d = 32 * wave + 16 * dt + col;
+      uint32_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h0 = 32 * ks + 8 * g + 2 * i;
+        v[i] = (uint32_t)qi[(row_id * kH + h0) * kD + d] | ((uint32_t)qi[(row_id * kH + h0 + 1) * kD + d] << 16);
+      }
+      qtr[dt][ks] = (u32x4){v[0], v[1], v[2], v[3]};
+    }
   // C layout of S = q k^T tiles: lane (slot col, g) holds heads 16w + 4g + r
   float wr[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) wr[r] = w[row_id * kH + 16 * wave + 4 * g + r];
 
-  for (int j = tid; j < K; j += 256) iv[j] = 0.f;
-
-  auto gather = [&](int blk) {  // 32 rows x 256 B: 2 DMA instructions per wave
+  auto gather = [&](int blk, int buf) {  // 64 rows x 256 B: 4 DMA instructions per wave
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int J = wave * 2 + i;
+    for (int i = 0; i < 4; ++i) {
+      const int J = wave * 4 + i;
       const int p = J * 64 + lane;
       const int row = p >> 4, pos = p & 15;
-      const int chunk = pos ^ (row & 7);
+      const int chunk = pos ^ swz8(row);
       const int slot = blk * kB + row;
       int v = ridx[min(slot, K - 1)];
       if (slot >= K || !ok_slot(v, s_k, limit)) v = 0;
       __builtin_amdgcn_global_load_lds((const void*)(kb + (int64_t)v * kD + chunk * 8),
-                                       (__attribute__((address_space(3))) void*)&kt[J * 64], 16, 0, 0);
+                                       (__attribute__((address_space(3))) void*)&kt[buf][J * 64], 16, 0, 0);
     }
-    __builtin_amdgcn_s_waitcnt(0);
   };
-  const uint32_t kt_base = (uint32_t)(uintptr_t)(&kt[0]);
-  // S tile (16 heads x 16 slots) for slot tile st of the staged block
-  auto s_tile = [&](int st) -> f32x4 {
+  const uint32_t kt_base = (uint32_t)(uintptr_t)(&kt[0][0]);
+  auto s_tile = [&](uint32_t tb, int st) -> f32x4 {  // S tile (16 heads x 16 slots) of slot tile st
     f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
     const int row = 16 * st + col;
+    u32x4 bk[kD / 32];
 #pragma unroll
-    for (int c = 0; c < kD / 32; ++c) {
-      const u32x4 bk = *(const lds_u32x4*)(kt_base + 16 * (row * kRowC + ((4 * c + g) ^ (row & 7))));
-      acc = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk), acc);
-    }
+    for (int c = 0; c < kD / 32; ++c)
+      bk[c] = *(const lds_u32x4*)(uintptr_t)(tb + 16 * (row * kRowC + ((4 * c + g) ^ swz8(row))));
+#pragma unroll
+    for (int c = 0; c < kD / 32; ++c) acc = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk[c]), acc);
     return acc;
   };
 
   // ---------------- phase 1: index scores at the selected slots ----------------
-  __syncthreads();
+  gather(0, 0);
   for (int blk = 0; blk < nblocks; ++blk) {
-    gather(blk);
-    __syncthreads();
+    const int buf = blk & 1;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // tile[buf] landed for every wave; ip free
+    if (blk + 1 < nblocks) gather(blk + 1, buf ^ 1);
+    const uint32_t tb = kt_base + buf * (kTileC * 16);
+    f32x4 sv[4];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const f32x4 sv = s_tile(st);
+    for (int st = 0; st < 4; ++st) sv[st] = s_tile(tb, st);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
       float part = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) part = fmaf(wr[r], fmaxf(sv[r], 0.f), part);
+      for (int r = 0; r < 4; ++r) part = fmaf(wr[r], fmaxf(sv[st][r], 0.f), part);
       part += __shfl_xor(part, 16, 64);
       part += __shfl_xor(part, 32, 64);
-      const int slot = blk * kB + 16 * st + col;
-      if (g == 0 && slot < K) atomicAdd(&iv[slot], part);
+      if (g == 0) ip[wave][16 * st + col] = part;
     }
     __syncthreads();
+    if (tid < kB) {
+      const int slot = blk * kB + tid;
+      if (slot < K) iv[slot] = (ip[0][tid] + ip[1][tid]) + (ip[2][tid] + ip[3][tid]);
+    }
   }
+  __syncthreads();
 
   // ---------------- phase 2: row statistics ----------------
   float lmax = -INFINITY, zsum = 0.f;
   for (int j = tid; j < K; j += 256) {
-    const bool ok = ok_slot(ridx[j], s_k, limit);
-    if (ok) {
+    if (ok_slot(ridx[j], s_k, limit)) {
       lmax = fmaxf(lmax, iv[j]);
       zsum += fmaxf(mrow[j], 0.f);
     }
@@ -160,7 +177,6 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const bool valid_row = Z > eps;
   const float lse = imax + logf(E);
   const float zc = fmaxf(Z, eps);
-  // loss terms and T = sum of positive targets
   float lpart = 0.f, tpos = 0.f;
   for (int j = tid; j < K; j += 256) {
     const bool ok = ok_slot(ridx[j], s_k, limit);
@@ -181,7 +197,6 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     const float sm = ok ? expf(iv[j] - lse) : 0.f;
     iv[j] = gs * (sm * T - t);
   }
-  __syncthreads();
 
   // ---------------- phase 3: gradients ----------------
   f32x4 dqa[kD / 16];
@@ -189,71 +204,79 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   for (int t = 0; t < kD / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
   float dwp[4] = {0.f, 0.f, 0.f, 0.f};
   uint16_t* ckrow = ck + ((int64_t)b * gridDim.x + lr) * (int64_t)K * kD;
-  // transposed reads of the key tile for dq^T += k^T E^T: group g, source lane col supplies
-  // slot row 8g + col/4 (+4 second read), d columns 16dt + 4(col%4) .. +3
+  // transposed key reads for dq^T += k^T E^T over a 32-slot k-step ks: group g, source lane
+  // col supplies slot row 32 ks + 8g + col/4 (+4 second read), d columns 16dt + 4(col%4)
   const int tr_row = 8 * g + (col >> 2);
-  for (int blk = 0; blk < nblocks; ++blk) {
-    if (gs == 0.f) break;  // block-uniform: no gradient for this row
-    gather(blk);
-    for (int i = tid; i < kB * (kD + 4); i += 256) (&dkp[0][0])[i] = 0.f;
+  if (gs != 0.f) {  // block-uniform
     __syncthreads();
-    u32x4 eb;  // B operand of dq^T: E^T [32 slots x 16 heads] read back from LDS
+    gather(0, 0);
+    for (int blk = 0; blk < nblocks; ++blk) {
+      const int buf = blk & 1;
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();  // tile[buf] landed; es / eh free
+      if (blk + 1 < nblocks) gather(blk + 1, buf ^ 1);
+      const uint32_t tb = kt_base + buf * (kTileC * 16);
+      f32x4 sv[4];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const f32x4 sv = s_tile(st);
-      const int slot = blk * kB + 16 * st + col;
-      const float gj = slot < K ? iv[slot] : 0.f;
-      float e[4];
+      for (int st = 0; st < 4; ++st) sv[st] = s_tile(tb, st);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        e[r] = sv[r] > 0.f ? gj * wr[r] : 0.f;
-        dwp[r] += gj * fmaxf(sv[r], 0.f);
-        et[wave][4 * g + r][16 * st + col] = f_to_bf16(e[r]);
+      for (int st = 0; st < 4; ++st) {
+        const int sl = 16 * st + col;
+        const int slot = blk * kB + sl;
+        const float gj = slot < K ? iv[slot] : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = sv[st][r] > 0.f ? gj * wr[r] : 0.f;
+          dwp[r] += gj * fmaxf(sv[st][r], 0.f);
+          const uint16_t eb = f_to_bf16(e);
+          es[sl][16 * wave + 4 * g + r] = eb;
+          eh[16 * wave + 4 * g + r][sl] = eb;
+        }
       }
-      // dk contribution: C^T[d x 16 slots] = q^T[d x 16 heads] . E[16 heads x 16 slots]
-      i16x4v eo;
+      __syncthreads();
+      // dq^T[16 d x 16 heads] += k^T[16 d x 32 slots] E^T[32 slots x 16 heads], two k-steps
 #pragma unroll
-      for (int r = 0; r < 4; ++r) eo[r] = (short)f_to_bf16(e[r]);
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x4 eb = *reinterpret_cast<const u32x4*>(&eh[head_a][32 * ks + 8 * g]);
+        const int r1 = 32 * ks + tr_row, r2 = r1 + 4;
 #pragma unroll
-      for (int dt = 0; dt < kD / 16; ++dt) {
-        f32x4 c4 = (f32x4){0.f, 0.f, 0.f, 0.f};
-        c4 = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qt[dt], eo, c4, 0, 0, 0);
+        for (int dt = 0; dt < kD / 16; ++dt) {
+          const int c0 = 2 * dt + ((col & 3) >> 1);
+          const uint32_t a1 = tb + 16 * (r1 * kRowC + (c0 ^ swz8(r1))) + 8 * (col & 1);
+          const uint32_t a2 = tb + 16 * (r2 * kRowC + (c0 ^ swz8(r2))) + 8 * (col & 1);
+          const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a1);
+          const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a2);
+          u32x4 av;
+          av[0] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
+          av[1] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
+          av[2] = (uint32_t)(uint16_t)v2[0] | ((uint32_t)(uint16_t)v2[1] << 16);
+          av[3] = (uint32_t)(uint16_t)v2[2] | ((uint32_t)(uint16_t)v2[3] << 16);
+          dqa[dt] = mfma16x16x32(as_bf16x8(av), as_bf16x8(eb), dqa[dt]);
+        }
+      }
+      // dk^T[32 d of this wave x 64 slots] = q^T[d x 64 heads] . E[64 heads x slots]
 #pragma unroll
-        for (int r = 0; r < 4; ++r) atomicAdd(&dkp[16 * st + col][16 * dt + 4 * g + r], c4[r]);
+      for (int st = 0; st < 4; ++st) {
+        const int sl = 16 * st + col;
+        const int slot = blk * kB + sl;
+        u32x4 eo[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) eo[ks] = *reinterpret_cast<const u32x4*>(&es[sl][32 * ks + 8 * g]);
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          f32x4 c4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) c4 = mfma16x16x32(as_bf16x8(qtr[dt][ks]), as_bf16x8(eo[ks]), c4);
+          if (slot < K) {  // lane (slot, g) holds d = 32w + 16dt + 4g + r
+            uint2 wv;
+            wv.x = pack_bf16x2(c4[0], c4[1]);
+            wv.y = pack_bf16x2(c4[2], c4[3]);
+            *reinterpret_cast<uint2*>(ckrow + (int64_t)slot * kD + 32 * wave + 16 * dt + 4 * g) = wv;
+          }
+        }
       }
     }
-    __syncthreads();
-    {
-      const u32x4* er = reinterpret_cast<const u32x4*>(&et[wave][col][8 * g]);
-      eb = *er;
-    }
-#pragma unroll
-    for (int dt = 0; dt < kD / 16; ++dt) {
-      const int c0 = 2 * dt + ((col & 3) >> 1);
-      const uint32_t a1 = kt_base + 16 * (tr_row * kRowC + (c0 ^ (tr_row & 7))) + 8 * (col & 1);
-      const uint32_t a2 = kt_base + 16 * ((tr_row + 4) * kRowC + (c0 ^ ((tr_row + 4) & 7))) + 8 * (col & 1);
-      const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a1);
-      const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a2);
-      u32x4 av;
-      av[0] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
-      av[1] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
-      av[2] = (uint32_t)(uint16_t)v2[0] | ((uint32_t)(uint16_t)v2[1] << 16);
-      av[3] = (uint32_t)(uint16_t)v2[2] | ((uint32_t)(uint16_t)v2[3] << 16);
-      dqa[dt] = mfma16x16x32(as_bf16x8(av), as_bf16x8(eb), dqa[dt]);
-    }
-    // write the block's dk contributions (bf16 rows of 128)
-    for (int i = tid; i < kB * kRowC; i += 256) {
-      const int row = i >> 4, c = i & 15;
-      const int slot = blk * kB + row;
-      if (slot >= K) continue;
-      u32x4 v;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = pack_bf16x2(dkp[row][8 * c + 2 * r], dkp[row][8 * c + 2 * r + 1]);
-      *reinterpret_cast<u32x4*>(ckrow + (int64_t)slot * kD + 8 * c) = v;
-    }
-    __syncthreads();
-  }
-  if (gs == 0.f) {  // zero contributions so the reduction can read every usable slot
+  } else {  // zero contributions so the reduction can read every usable slot
     for (int i = tid; i < K * kRowC; i += 256) {
       const int slot = i >> 4, c = i & 15;
       *reinterpret_cast<u32x4*>(ckrow + (int64_t)slot * kD + 8 * c) = (u32x4){0u, 0u, 0u, 0u};
@@ -273,8 +296,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   // dq^T tile dt: lane (head col, g) holds d = 16 dt + 4g + r
   float* dqrow = dq + (row_id * kH + head_a) * kD;
 #pragma unroll
-  for (int dt = 0; dt < kD / 16; ++dt)
-    *reinterpret_cast<f32x4*>(dqrow + 16 * dt + 4 * g) = dqa[dt];
+  for (int dt = 0; dt < kD / 16; ++dt) *reinterpret_cast<f32x4*>(dqrow + 16 * dt + 4 * g) = dqa[dt];
 }
 
 // --------------------------------------------------------------------------------------

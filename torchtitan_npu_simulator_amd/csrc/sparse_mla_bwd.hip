@@ -137,7 +137,7 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
       const int J = wave * 9 + i;
       const int p = J * 64 + lane;
       const int row = p / kRowChunks, pos = p - row * kRowChunks;
-      chunk[i] = pos ^ (row & 7);
+      chunk[i] = pos ^ swz8(row);
       const int slot = blk * kBN + row;
       v[i] = ridx[min(slot, K - 1)];
       if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;
@@ -156,7 +156,7 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     }
   };
 
-  // LDS offsets.  A operand of S^T / dP^T: key row 16kt + col, chunk 4c + g (XOR row & 7).
+  // LDS offsets.  A operand of S^T / dP^T: key row 16kt + col, chunk 4c + g (XOR swz8(row)).
   // With c = 2u + c0 the XOR touches only bits 0..2 of 4c + g -> ka_off[kt][c0] + 128 u.
   const uint32_t tile_base = (uint32_t)(uintptr_t)(&tile[0][0]);
   uint32_t ka_off[2][2];
@@ -165,12 +165,12 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
     for (int c0 = 0; c0 < 2; ++c0) {
       const int row = 16 * kt + col;
-      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ (row & 7));
+      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ swz8(row));
     }
   // Transposed K reads for dQ^T += K^T dS^T: group g, source lane col supplies key row
   // 4g + col/4 (+16 for the second read), d columns 16dt + 4(col%4) -> chunk 2dt + (col%4)/2.
   const int tr_row = 4 * g + (col >> 2);
-  const int tr_x = tr_row & 7;
+  const int tr_x = swz8(tr_row);
   const int tr_c0 = (col & 3) >> 1;
   uint32_t tr_off[4];  // dt = 4u + d0 -> chunk (8u + 2 d0 + tr_c0) ^ tr_x = 8u + ((2 d0 + tr_c0) ^ tr_x)
 #pragma unroll
@@ -271,8 +271,8 @@ __global__ void __launch_bounds__(512, 1)
 bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ dout,
                    const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf, uint16_t* __restrict__ cbuf,
                    int S, int s_kv, int H, int K, int64_t q_offset, int row0, int rows) {
-  __shared__ u32x4 xt[kXChunks];           // X chunk [64 rows][72 chunks], XOR-swizzled
-  __shared__ u32x4 gt[kCT * (kGW / 8)];    // G tile [128 slots][32 chunks], XOR-swizzled
+  __shared__ u32x4 xt[kXChunks];           // X chunk [64 rows][72 chunks], swz8-swizzled
+  __shared__ u32x4 gt[kCT * (kGW / 8)];    // G tile [128 slots][32 chunks], swz8-swizzled
   __shared__ int sh_last;
 
   const int lr = blockIdx.x;  // local row in chunk
@@ -290,13 +290,13 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int nheads_g = (H + kHG - 1) / kHG;  // head groups present
   const int kdim = 2 * kHG * nheads_g;       // stacked rows actually used
 
-  // stage G tile: 128 slots x 256 bf16 (32 chunks per slot), position slot*32 + (c ^ (slot & 7))
+  // stage G tile: 128 slots x 256 bf16 (32 chunks per slot), position slot*32 + (c ^ swz8(slot))
   for (int i = tid; i < kCT * 32; i += 512) {
     const int slot = i >> 5, c = i & 31;
     const int gs = slot0 + slot;
     u32x4 v = (u32x4){0u, 0u, 0u, 0u};
     if (gs < K) v = *reinterpret_cast<const u32x4*>(grow + (int64_t)gs * kGW + c * 8);
-    gt[slot * 32 + (c ^ (slot & 7))] = v;
+    gt[slot * 32 + (c ^ swz8(slot))] = v;
   }
 
   // wave w: slot sub-tile (w & 3) x 32 slots, column half (w >> 2) x 288 columns
@@ -323,14 +323,14 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
         if (type == 0) v = *reinterpret_cast<const u32x4*>(q + (row_id * H + head) * kDqk + c * 8);
         else if (c < kDv / 8) v = *reinterpret_cast<const u32x4*>(dout + (row_id * H + head) * kDv + c * 8);
       }
-      xt[row * kRowChunks + (c ^ (row & 7))] = v;
+      xt[row * kRowChunks + (c ^ swz8(row))] = v;
     }
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < kXK / 16; ++kk) {
       // B operand: G[slot = 32 ss + n][64 kc + 16 kk + 8 hh .. +8]
       const int slot = 32 * ss + n;
-      const int gc = (8 * kc + 2 * kk + hh) ^ (slot & 7);
+      const int gc = (8 * kc + 2 * kk + hh) ^ swz8(slot);
       const u32x4 bg = *(const lds_u32x4*)(gt_base + 16 * (slot * 32 + gc));
       const int row1 = 16 * kk + tr_rowo, row2 = row1 + 4;
 #pragma unroll
@@ -338,8 +338,8 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
         const int c0 = 288 * ch + 32 * t;  // first column of the tile
         if (type == 1 && c0 >= kDv) continue;  // dO has no rope columns
         const int cc = (c0 >> 3) + tr_cl;
-        const uint32_t a1 = xt_base + row1 * kRowBytes + 16 * (cc ^ (row1 & 7)) + 8 * (s16 & 1);
-        const uint32_t a2 = xt_base + row2 * kRowBytes + 16 * (cc ^ (row2 & 7)) + 8 * (s16 & 1);
+        const uint32_t a1 = xt_base + row1 * kRowBytes + 16 * (cc ^ swz8(row1)) + 8 * (s16 & 1);
+        const uint32_t a2 = xt_base + row2 * kRowBytes + 16 * (cc ^ swz8(row2)) + 8 * (s16 & 1);
         const u32x4 a = tr_pair(a1, a2);
         acc[t] = mfma32x32x16(as_bf16x8(a), as_bf16x8(bg), acc[t]);
       }

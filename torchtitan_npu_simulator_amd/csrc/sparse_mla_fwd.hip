@@ -102,13 +102,13 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int ch = 2 * c + hh;  // 0..7
-        qpe[grp * 32 + n][ch] = head_ok ? qh[2 * (kDv / 16) + ch] : (u32x4){0u, 0u, 0u, 0u};
+        qpe[grp * 32 + n][ch ^ (n & 7)] = head_ok ? qh[2 * (kDv / 16) + ch] : (u32x4){0u, 0u, 0u, 0u};
       }
     }
   }
 
   // ---- block loader: direct global->LDS DMA, 16 B per lane.  Instruction J fills tile
-  // positions [64J, 64J+64); position p = row*72 + (chunk ^ (row & 7)).  Wave w issues
+  // positions [64J, 64J+64); position p = row*72 + (chunk ^ swz8(row)).  Wave w issues
   // J = w, w+8, ... (waves 0-3: 5 instructions, waves 4-7: 4). ----
   auto load_block = [&](int blk, int buf) {
     int v[5], chunk[5];
@@ -117,7 +117,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
       const int J = wave + kWaves * i;
       const int p = min(J, kTileInstr - 1) * 64 + lane;
       const int row = p / kRowChunks, pos = p - row * kRowChunks;
-      chunk[i] = pos ^ (row & 7);
+      chunk[i] = pos ^ swz8(row);
       const int slot = blk * kBN + row;
       v[i] = ridx[min(slot, K - 1)];
       if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;  // finite stand-in row, masked later
@@ -138,10 +138,10 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   };
 
   // ---- LDS byte offsets ----
-  // QK A operand: key row n, chunk (32h + 2c + hh) ^ (n & 7) for latent step c; with
+  // QK A operand: key row n, chunk (32h + 2c + hh) ^ swz8(n) for latent step c; with
   // c = 4k + c' the XOR only touches the low 3 bits, so offset = qk_off[c'] + 128 k.
   const uint32_t tile_base = (uint32_t)(uintptr_t)(&tile[0][0]);
-  const int xsw = n & 7;
+  const int xsw = swz8(n);
   uint32_t qk_off[4];
 #pragma unroll
   for (int c4 = 0; c4 < 4; ++c4) qk_off[c4] = n * kRowBytes + 512 * half + 16 * ((2 * c4 + hh) ^ xsw);
@@ -155,7 +155,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   // With t = 2u + t0: tr_off[t0] + 128 u (+ 18432 c, + 9216 for the second read).
   const int s16 = lane & 15;
   const int tr_row0 = 4 * hh + (s16 >> 2);
-  const int tr_swz = tr_row0 & 7;
+  const int tr_swz = swz8(tr_row0);
   const int tr_cl = 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
   uint32_t tr_off[2];
 #pragma unroll
@@ -189,7 +189,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
           an = *(const lds_u32x4*)(tb + qk_off[(c + 1) & 3] + 128 * ((c + 1) >> 2));
         else if (c + 1 < kQSteps + 2)
           an = *(const lds_u32x4*)(tb + pe_off[c + 1 - kQSteps]);
-        const u32x4 bq = c < kQSteps ? qr[c] : qpe[grp * 32 + n][4 * half + 2 * (c - kQSteps) + hh];
+        const u32x4 bq = c < kQSteps ? qr[c] : qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
         s = mfma32x32x16(as_bf16x8(a), as_bf16x8(bq), s);
         a = an;
       }
@@ -349,7 +349,7 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int ch = 2 * c + hh;
-        qpe[grp * 32 + n][ch] = head_ok ? qh[2 * (kDv / 16) + ch] : (u32x4){0u, 0u, 0u, 0u};
+        qpe[grp * 32 + n][ch ^ (n & 7)] = head_ok ? qh[2 * (kDv / 16) + ch] : (u32x4){0u, 0u, 0u, 0u};
       }
     }
   }
@@ -360,7 +360,7 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
       const int J = wave + kWaves * i;
       const int p = min(J, kTileInstr - 1) * 64 + lane;
       const int row = p / kRowChunks, pos = p - row * kRowChunks;
-      chunk[i] = pos ^ (row & 7);
+      chunk[i] = pos ^ swz8(row);
       const int slot = blk * kBN + row;
       v[i] = ridx[min(slot, K - 1)];
       if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;
@@ -380,7 +380,7 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
     }
   };
   const uint32_t tile_base = (uint32_t)(uintptr_t)(&tile[0][0]);
-  const int xsw = n & 7;
+  const int xsw = swz8(n);
   uint32_t qk_off[4];
 #pragma unroll
   for (int c4 = 0; c4 < 4; ++c4) qk_off[c4] = n * kRowBytes + 512 * half + 16 * ((2 * c4 + hh) ^ xsw);
@@ -405,7 +405,7 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
           an = *(const lds_u32x4*)(tb + qk_off[(c + 1) & 3] + 128 * ((c + 1) >> 2));
         else if (c + 1 < kQSteps + 2)
           an = *(const lds_u32x4*)(tb + pe_off[c + 1 - kQSteps]);
-        const u32x4 bq = c < kQSteps ? qr[c] : qpe[grp * 32 + n][4 * half + 2 * (c - kQSteps) + hh];
+        const u32x4 bq = c < kQSteps ? qr[c] : qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
         s = mfma32x32x16(as_bf16x8(a), as_bf16x8(bq), s);
         a = an;
       }
