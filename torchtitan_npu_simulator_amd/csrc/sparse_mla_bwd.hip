@@ -9,7 +9,7 @@
 //           gathered KV tile, P = exp2(S*scale*log2e - lse2), dS = P (dP - delta);
 //           dQ^T += K^T dS^T (K read transposed with ds_read_tr16_b64) in AGPRs; and
 //           G[token][slot][128 hg + (0..63 | 64..127)] = (dS * scale | P) in bf16.
-//   (beta)  bwd_contrib_kernel, workgroup = (token, 128 slots), 8 waves:
+//   (beta)  bwd_contrib_kernel, workgroup = token, 12 waves (X slice in VGPRs, G streamed):
 //           C[token][slot][0..576) = G[slot][0..256) . [Q_token ; dO_token]  (bf16 out),
 //           the dKV contribution of one (token, slot) pair summed over all 128 heads.
 //   (gamma) a CSR of (token, slot) pairs per key (LDS-privatised counting sort), then
@@ -191,16 +191,28 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     const uint32_t tb = tile_base + buf * kTileBytes;
     const uint32_t vm = vmask[buf];
 
+    // S^T and dP^T: operands read in batches of 6 ahead of their MFMAs (the sched_barrier
+    // keeps the batch together so its LDS latency overlaps the previous batch's MFMAs)
     f32x4 sacc[2], pacc[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       sacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
       pacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int c = 0; c < kDqk / 32; ++c) {
-        const u32x4 a = *(const lds_u32x4*)(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
-        sacc[kt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(qb[c]), sacc[kt]);
-        if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(db[c]), pacc[kt]);
+      for (int cb = 0; cb < kDqk / 32; cb += 6) {
+        u32x4 a[6];
+#pragma unroll
+        for (int u = 0; u < 6; ++u) {
+          const int c = cb + u;
+          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 6; ++u) {
+          const int c = cb + u;
+          sacc[kt] = mfma16x16x32(as_bf16x8(a[u]), as_bf16x8(qb[c]), sacc[kt]);
+          if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a[u]), as_bf16x8(db[c]), pacc[kt]);
+        }
       }
     }
     // P and dS (lane: head col, keys 16kt + 4g + r)
@@ -222,10 +234,17 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     bds[2] = pack_bf16x2(dsv[1][0], dsv[1][1]);
     bds[3] = pack_bf16x2(dsv[1][2], dsv[1][3]);
 #pragma unroll
-    for (int dt = 0; dt < kDqk / 16; ++dt) {
-      const uint32_t a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
-      const u32x4 a = tr_pair(a1, a1 + 16 * kRowBytes);
-      dqa[dt] = mfma16x16x32(as_bf16x8(a), as_bf16x8(bds), dqa[dt]);
+    for (int db4 = 0; db4 < kDqk / 16; db4 += 4) {
+      u32x4 a[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int dt = db4 + u;
+        const uint32_t a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
+        a[u] = tr_pair(a1, a1 + 16 * kRowBytes);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) dqa[db4 + u] = mfma16x16x32(as_bf16x8(a[u]), as_bf16x8(bds), dqa[db4 + u]);
     }
     // stage G = (dS * scale | P) for these 32 slots
 #pragma unroll
@@ -262,60 +281,54 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 // --------------------------------------------------------------------------------------
 // (beta) C[token][slot] = G[token][slot] . X_token,  X = [(Q, dO) per head group]
 // rows of X: k = 128 hg + 64 type + i  ->  type 0: q[64hg + i], type 1: dout[64hg + i]
+//
+// One workgroup per token, 12 waves; wave w owns the 48 output columns 48w .. 48w+47
+// (three 16-column MFMA tiles) and keeps its slice of X transposed in VGPRs for the whole
+// token (A operand of C^T = X^T G^T, 96 VGPRs).  G is streamed through a double-buffered
+// LDS tile of 128 slots x 256 (DMA), so G, X and C each cross HBM exactly once.
 // --------------------------------------------------------------------------------------
-constexpr int kCT = 128;          // slots per contrib workgroup
-constexpr int kXK = 64;           // X rows per staged chunk
-constexpr int kXChunks = kXK * kRowChunks;  // 4608 16-byte chunks (73.7 KB)
+constexpr int kCW = 12;                     // waves
+constexpr int kCThreads = kCW * 64;
+constexpr int kCT = 128;                    // slots per G tile
+constexpr int kGTChunks = kCT * (kGW / 8);  // 4096 16-byte chunks (64 KB)
+constexpr int kXK = 64;                     // X rows staged per chunk while loading X
+constexpr int kXChunks = kXK * kRowChunks;  // 4608 chunks (73.7 KB)
 
-__global__ void __launch_bounds__(512, 1)
+__global__ void __launch_bounds__(kCThreads, 1)
 bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ dout,
                    const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf, uint16_t* __restrict__ cbuf,
                    int S, int s_kv, int H, int K, int64_t q_offset, int row0, int rows) {
-  __shared__ u32x4 xt[kXChunks];           // X chunk [64 rows][72 chunks], swz8-swizzled
-  __shared__ u32x4 gt[kCT * (kGW / 8)];    // G tile [128 slots][32 chunks], swz8-swizzled
+  __shared__ u32x4 lds[2 * kGTChunks];  // X staging at start, then two G tiles
   __shared__ int sh_last;
 
   const int lr = blockIdx.x;  // local row in chunk
-  const int tok = row0 + lr, st = blockIdx.y, b = blockIdx.z;
+  const int tok = row0 + lr, b = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n = lane & 31, hh = lane >> 5;
+  const int col = lane & 15, g = lane >> 4;
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
   const int nblk = count_blocks(ridx, K, s_kv, tok + q_offset, &sh_last);
-  const int slot0 = st * kCT;
-  if (slot0 >= nblk * kBN) return;  // block-uniform
-
+  if (nblk == 0) return;
+  const int nslots = min(K, nblk * kBN);
   const uint16_t* grow = gbuf + ((int64_t)b * rows + lr) * (int64_t)K * kGW;
   uint16_t* crow = cbuf + ((int64_t)b * rows + lr) * (int64_t)K * kDqk;
-  const int nheads_g = (H + kHG - 1) / kHG;  // head groups present
-  const int kdim = 2 * kHG * nheads_g;       // stacked rows actually used
+  const int nheads_g = (H + kHG - 1) / kHG;
+  const int ksteps = 4 * nheads_g;  // 32-row k steps of X actually used (<= 8)
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(&lds[0]);
 
-  // stage G tile: 128 slots x 256 bf16 (32 chunks per slot), position slot*32 + (c ^ swz8(slot))
-  for (int i = tid; i < kCT * 32; i += 512) {
-    const int slot = i >> 5, c = i & 31;
-    const int gs = slot0 + slot;
-    u32x4 v = (u32x4){0u, 0u, 0u, 0u};
-    if (gs < K) v = *reinterpret_cast<const u32x4*>(grow + (int64_t)gs * kGW + c * 8);
-    gt[slot * 32 + (c ^ swz8(slot))] = v;
-  }
-
-  // wave w: slot sub-tile (w & 3) x 32 slots, column half (w >> 2) x 288 columns
-  const int ss = wave & 3, ch = wave >> 2;
-  f32x16 acc[9];
+  // ---- X^T slice into VGPRs: xa[t][ks] = X[32 ks + 8g .. +8][48w + 16t + col] ----
+  u32x4 xa[3][8];
 #pragma unroll
-  for (int t = 0; t < 9; ++t) acc[t] = (f32x16){0};
-
-  const uint32_t xt_base = (uint32_t)(uintptr_t)(&xt[0]);
-  const uint32_t gt_base = (uint32_t)(uintptr_t)(&gt[0]);
-  const int s16 = lane & 15;
-  // C^T = X^T . G^T : A = X^T (lane: column, k-slots 8hh..+7) via transposed reads of the
-  // row-major X chunk; B = G^T (lane: slot, k-slots 8hh..+7) via b128 reads of the G tile.
-  const int tr_rowo = 8 * hh + (s16 >> 2);  // + 16 kk (+4 for the second read)
-  const int tr_cl = 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
-  for (int kc = 0; kc < kdim / kXK; ++kc) {
-    __syncthreads();  // previous chunk fully consumed (and G tile staged on the first pass)
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) xa[t][ks] = (u32x4){0u, 0u, 0u, 0u};
+  const int tr_row = 8 * g + (col >> 2);  // source row within a 32-row k step (+4 second read)
+#pragma unroll
+  for (int kc = 0; kc < 4; ++kc) {
+    if (kc / 2 >= nheads_g) continue;  // block-uniform
+    __syncthreads();
     const int hgk = kc >> 1, type = kc & 1;
-    for (int i = tid; i < kXChunks; i += 512) {
+    for (int i = tid; i < kXChunks; i += kCThreads) {
       const int row = i / kRowChunks, c = i - row * kRowChunks;
       const int head = hgk * kHG + row;
       u32x4 v = (u32x4){0u, 0u, 0u, 0u};
@@ -323,41 +336,75 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
         if (type == 0) v = *reinterpret_cast<const u32x4*>(q + (row_id * H + head) * kDqk + c * 8);
         else if (c < kDv / 8) v = *reinterpret_cast<const u32x4*>(dout + (row_id * H + head) * kDv + c * 8);
       }
-      xt[row * kRowChunks + (c ^ swz8(row))] = v;
+      lds[row * kRowChunks + (c ^ swz8(row))] = v;
     }
     __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < kXK / 16; ++kk) {
-      // B operand: G[slot = 32 ss + n][64 kc + 16 kk + 8 hh .. +8]
-      const int slot = 32 * ss + n;
-      const int gc = (8 * kc + 2 * kk + hh) ^ swz8(slot);
-      const u32x4 bg = *(const lds_u32x4*)(gt_base + 16 * (slot * 32 + gc));
-      const int row1 = 16 * kk + tr_rowo, row2 = row1 + 4;
+    for (int kl = 0; kl < 2; ++kl) {  // two 32-row k steps per staged chunk
+      const int ks = 2 * kc + kl;
+      const int r1 = 32 * kl + tr_row, r2 = r1 + 4;
 #pragma unroll
-      for (int t = 0; t < 9; ++t) {
-        const int c0 = 288 * ch + 32 * t;  // first column of the tile
-        if (type == 1 && c0 >= kDv) continue;  // dO has no rope columns
-        const int cc = (c0 >> 3) + tr_cl;
-        const uint32_t a1 = xt_base + row1 * kRowBytes + 16 * (cc ^ swz8(row1)) + 8 * (s16 & 1);
-        const uint32_t a2 = xt_base + row2 * kRowBytes + 16 * (cc ^ swz8(row2)) + 8 * (s16 & 1);
-        const u32x4 a = tr_pair(a1, a2);
-        acc[t] = mfma32x32x16(as_bf16x8(a), as_bf16x8(bg), acc[t]);
+      for (int t = 0; t < 3; ++t) {
+        const int c0 = (48 * wave + 16 * t) / 8 + ((col & 3) >> 1);
+        const uint32_t a1 = lds_base + 16 * (r1 * kRowChunks + (c0 ^ swz8(r1))) + 8 * (col & 1);
+        const uint32_t a2 = lds_base + 16 * (r2 * kRowChunks + (c0 ^ swz8(r2))) + 8 * (col & 1);
+        xa[t][ks] = tr_pair(a1, a2);
       }
     }
   }
-  // lane (slot n, hh) holds columns c0 + 8i + 4hh + r
-  const int slot = slot0 + 32 * ss + n;
-  if (slot >= K) return;
-  uint16_t* cr = crow + (int64_t)slot * kDqk;
+  __syncthreads();
+
+  // ---- stream G tiles; C^T[16 cols x 16 slots] = X^T[16 cols x 256] . G^T[256 x 16 slots] ----
+  const int ntiles = (nslots + kCT - 1) / kCT;
+  auto load_g = [&](int tile, int buf) {  // 64 DMA instructions per tile, J = wave + 12 i
 #pragma unroll
-  for (int t = 0; t < 9; ++t) {
-    const int c0 = 288 * ch + 32 * t;
+    for (int i = 0; i < 6; ++i) {
+      const int J = wave + kCW * i;
+      if (J < kGTChunks / 64) {
+        const int p = J * 64 + lane;
+        const int slot = p >> 5, pos = p & 31;
+        const int c = pos ^ swz8(slot);
+        const int gs = min(tile * kCT + slot, K - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(grow + (int64_t)gs * kGW + c * 8),
+                                         (__attribute__((address_space(3))) void*)&lds[buf * kGTChunks + J * 64], 16,
+                                         0, 0);
+      }
+    }
+  };
+  load_g(0, 0);
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int buf = tile & 1;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // G tile landed for every wave; the other buffer is free
+    if (tile + 1 < ntiles) load_g(tile + 1, buf ^ 1);
+    const uint32_t gb = lds_base + buf * (kGTChunks * 16);
+    for (int st = 0; st < kCT / 16; ++st) {
+      const int sl = 16 * st + col;  // B operand row (slot) of this lane
+      const int slot = tile * kCT + sl;
+      if (tile * kCT + 16 * st >= nslots) break;  // wave-uniform
+      f32x4 acc[3];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint2 w;
-      w.x = pack_bf16x2(acc[t][4 * i], acc[t][4 * i + 1]);
-      w.y = pack_bf16x2(acc[t][4 * i + 2], acc[t][4 * i + 3]);
-      *reinterpret_cast<uint2*>(cr + c0 + 8 * i + 4 * hh) = w;
+      for (int t = 0; t < 3; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        if (ks >= ksteps) continue;  // block-uniform
+        const u32x4 bg = *(const lds_u32x4*)(uintptr_t)(gb + 16 * (sl * 32 + ((4 * ks + g) ^ swz8(sl))));
+        const bool dO_rows = (ks & 2) != 0;  // k = 128 hg + 64 type + i: type 1 when bit 6 of k set
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          if (dO_rows && 48 * wave + 16 * t >= kDv) continue;  // dO has no rope columns
+          acc[t] = mfma16x16x32(as_bf16x8(xa[t][ks]), as_bf16x8(bg), acc[t]);
+        }
+      }
+      if (slot < nslots) {  // lane (slot, g) holds columns 48w + 16t + 4g + r
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          uint2 w2;
+          w2.x = pack_bf16x2(acc[t][0], acc[t][1]);
+          w2.y = pack_bf16x2(acc[t][2], acc[t][3]);
+          *reinterpret_cast<uint2*>(crow + (int64_t)slot * kDqk + 48 * wave + 16 * t + 4 * g) = w2;
+        }
+      }
     }
   }
 }
@@ -503,8 +550,8 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
                                       (const uint16_t*)dout, softmax_max, softmax_sum, (uint16_t*)dq, gbuf, (int)s_q,
                                       (int)s_kv, (int)n_heads, (int)topk, scale, q_offset, (int)r0);
     if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
-    dim3 gb((unsigned)rows, ceil_div(topk, kCT), (unsigned)batch);
-    bwd_contrib_kernel<<<gb, 512, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf, (int)s_q,
+    dim3 gb((unsigned)rows, (unsigned)batch);
+    bwd_contrib_kernel<<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf, (int)s_q,
                                            (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0, rows);
     if (int rc = check_launch("dsa_sparse_mla_bwd(contrib)")) return rc;
     for (int b = 0; b < (int)batch; ++b)

@@ -179,20 +179,26 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
     const uint32_t tb = tile_base + buf * kTileBytes;
 
     // ---- partial S^T over this wave's half of the contraction ----
+    // operands fetched in batches of 6 ahead of their MFMAs (sched_barrier keeps each batch
+    // together so its LDS latency overlaps the previous batch's MFMAs)
     f32x16 s = (f32x16){0};
-    {
-      u32x4 a = *(const lds_u32x4*)(tb + qk_off[0]);
 #pragma unroll
-      for (int c = 0; c < kQSteps + 2; ++c) {
-        u32x4 an = a;
-        if (c + 1 < kQSteps)
-          an = *(const lds_u32x4*)(tb + qk_off[(c + 1) & 3] + 128 * ((c + 1) >> 2));
-        else if (c + 1 < kQSteps + 2)
-          an = *(const lds_u32x4*)(tb + pe_off[c + 1 - kQSteps]);
-        const u32x4 bq = c < kQSteps ? qr[c] : qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
-        s = mfma32x32x16(as_bf16x8(a), as_bf16x8(bq), s);
-        a = an;
+    for (int cb = 0; cb < kQSteps + 2; cb += 6) {
+      u32x4 a[6], bq[6];
+#pragma unroll
+      for (int u = 0; u < 6; ++u) {
+        const int c = cb + u;
+        if (c < kQSteps) {
+          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + qk_off[c & 3] + 128 * (c >> 2));
+          bq[u] = qr[c];
+        } else {
+          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + pe_off[c - kQSteps]);
+          bq[u] = qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 6; ++u) s = mfma32x32x16(as_bf16x8(a[u]), as_bf16x8(bq[u]), s);
     }
     // ---- swap partial S with the other half of the pair ----
 #pragma unroll
@@ -254,14 +260,17 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
     };
     {
       constexpr int kT = kDv / 64;
-      u32x4 av = read_v(0, 0);
 #pragma unroll
-      for (int step = 0; step < 2 * kT; ++step) {
-        const int c = step / kT, t = step % kT;
-        u32x4 nv = av;
-        if (step + 1 < 2 * kT) nv = read_v((step + 1) / kT, (step + 1) % kT);
-        o[t] = mfma32x32x16(as_bf16x8(av), as_bf16x8(c == 0 ? pb0 : pb1), o[t]);
-        av = nv;
+      for (int sb = 0; sb < 2 * kT; sb += 4) {
+        u32x4 av[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) av[u] = read_v((sb + u) / kT, (sb + u) % kT);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = (sb + u) / kT, t = (sb + u) % kT;
+          o[t] = mfma32x32x16(as_bf16x8(av[u]), as_bf16x8(c == 0 ? pb0 : pb1), o[t]);
+        }
       }
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA into buf^1 has landed
@@ -395,20 +404,26 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
     const int buf = blk & 1;
     if (blk + 1 < nblk) load_block(blk + 1, buf ^ 1);
     const uint32_t tb = tile_base + buf * kTileBytes;
+    // operands fetched in batches of 6 ahead of their MFMAs (sched_barrier keeps each batch
+    // together so its LDS latency overlaps the previous batch's MFMAs)
     f32x16 s = (f32x16){0};
-    {
-      u32x4 a = *(const lds_u32x4*)(tb + qk_off[0]);
 #pragma unroll
-      for (int c = 0; c < kQSteps + 2; ++c) {
-        u32x4 an = a;
-        if (c + 1 < kQSteps)
-          an = *(const lds_u32x4*)(tb + qk_off[(c + 1) & 3] + 128 * ((c + 1) >> 2));
-        else if (c + 1 < kQSteps + 2)
-          an = *(const lds_u32x4*)(tb + pe_off[c + 1 - kQSteps]);
-        const u32x4 bq = c < kQSteps ? qr[c] : qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
-        s = mfma32x32x16(as_bf16x8(a), as_bf16x8(bq), s);
-        a = an;
+    for (int cb = 0; cb < kQSteps + 2; cb += 6) {
+      u32x4 a[6], bq[6];
+#pragma unroll
+      for (int u = 0; u < 6; ++u) {
+        const int c = cb + u;
+        if (c < kQSteps) {
+          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + qk_off[c & 3] + 128 * (c >> 2));
+          bq[u] = qr[c];
+        } else {
+          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + pe_off[c - kQSteps]);
+          bq[u] = qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 6; ++u) s = mfma32x32x16(as_bf16x8(a[u]), as_bf16x8(bq[u]), s);
     }
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4)
