@@ -9,9 +9,9 @@ One step = one pass of the DeepSeek-V3.2 DSA hot path over one synthetic batch
   attention mass -> indexer KL loss gradients -> sparse MLA backward (dQ, dKV)
 
 Inputs are resident in HBM before the timed region.  Prints ONE JSON line.  The
-``roofline`` object is for the dominant kernel, using the algorithmic byte formulas of
-the DSA path (documented in DESIGN.md) over that kernel's average duration, measured
-with HIP events on the stream the kernel runs on.  ``cpu_baseline`` times the CPU oracle
+``roofline`` object is for the dominant kernel (the gathered sparse MLA forward):
+its algorithmic bytes per step (Q + gathered KV rows + indices + O + LSE) over its
+average duration, measured with HIP events on the stream the kernel runs on.  ``cpu_baseline`` times the CPU oracle
 (fp32, all host threads) on a bounded sample of the same workload.
 """
 
@@ -40,7 +40,8 @@ def parse_args():
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--phases", action="store_true", help="also print per-phase timings to stderr")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run one 1 GiB device copy first (reference kernel for the PMC byte counters)")
     return p.parse_args()
 
 
@@ -122,7 +123,12 @@ def dsa_step(inp, ops, timer):
 
 
 def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128):
-    """Bytes and FLOPs of the DSA path per step (formulas documented in DESIGN.md)."""
+    """Algorithmic bytes and FLOPs of the DSA path per step.
+
+    sum_keff = number of valid (row, slot) pairs; every head of a row shares its gathered
+    KV rows, so each row's keys are counted once; dKV is counted as an fp32 scatter-add
+    payload (4 bytes per element per pair).
+    """
     sum_keff = int((idx >= 0).sum().item())
     causal_pairs = S * (S + 1) // 2
     K = topk
@@ -140,6 +146,37 @@ def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128):
     )
 
 
+def measured_traffic(kernel, S, H, K):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC summary, or None.
+
+    profiles/hbm_traffic_c3.json holds FETCH_SIZE and WRITE_SIZE per dispatch, each
+    already divided by the factor the same counter reads on a copy of known size.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic_c3.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+    except (OSError, ValueError):
+        return None
+    wl = data.get("workload", {})
+    if (wl.get("seq_len"), wl.get("heads"), wl.get("topk")) != (S, H, K):
+        return None
+    k = data.get("kernels", {}).get(kernel)
+    if not k:
+        return None
+    return k["fetch_bytes"] + k["write_bytes"]
+
+
+def copy_calibration(torch, device, nbytes=1 << 30):
+    """One plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def cpu_baseline(inp_gpu, S, H, topk, seconds):
     """Time the CPU oracle (fp32, all host threads) on the last rows of the same workload."""
     import torch
@@ -147,8 +184,9 @@ def cpu_baseline(inp_gpu, S, H, topk, seconds):
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import dsa_oracle as O
 
-    threads = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
     torch.set_num_threads(threads)
+    threads = torch.get_num_threads()
     cpu = {k: (v.cpu() if hasattr(v, "cpu") else v) for k, v in inp_gpu.items()}
     q, kv, qi, ki, w, do = (cpu[k].float() for k in ("q", "kv", "q_idx", "k_idx", "w", "dout"))
     qi8, qis = O.quantize_e4m3_per_row(qi)
@@ -204,7 +242,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the DSA path shards by query rows, see DESIGN.md)", file=sys.stderr)
+              "(the DSA path shards by query rows; multi-GPU runs are not part of this build)", file=sys.stderr)
         sys.exit(2)
     import torch
 
@@ -213,6 +251,8 @@ def main():
 
     dev = torch.device("cuda:0")
     S, H, K = args.seq, args.heads, args.topk
+    if args.copy_calibration:
+        copy_calibration(torch, dev)
     inp = make_inputs(S, H, K, args.seed, dev)
     timer = PhaseTimer(torch)
     for _ in range(args.warmup):
@@ -231,19 +271,32 @@ def main():
     phases = timer.averages_ms()
     work = algorithmic_work(S, H, K, res["idx"])
 
-    # dominant kernel: the attention backward entry (dQ/G, contribution GEMM, CSR reduce)
-    bwd_ms = phases["attn_bwd"]
+    # Dominant kernel: the gathered sparse MLA forward (sparse_mla_fwd_bf16_kernel; its
+    # row-fixup pass is launched in the same call and is timed with it).  Its algorithmic
+    # bytes are Q + gathered KV rows + indices + O + LSE for one step.
     fwd_ms = phases["attn_fwd"]
-    attn_bytes = work["attn_fwd_bytes"] + work["attn_bwd_bytes"]
+    bwd_ms = phases["attn_bwd"]
     roof = dict(
         bound="hbm",
-        kernel="gathered sparse MLA attention fwd+bwd (dsa_sparse_mla_fwd + dsa_sparse_mla_bwd)",
+        kernel="sparse_mla_fwd_bf16_kernel",
+        achieved=work["attn_fwd_bytes"] / (fwd_ms * 1e-3) / 1e9,
+        peak=HBM_PEAK_GBPS,
+        unit="GB/s",
+        algorithmic_bytes=work["attn_fwd_bytes"],
+        avg_launch_ms=fwd_ms,
+        traffic=measured_traffic("sparse_mla_fwd_bf16_kernel", S, H, K),
+    )
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    attn_bytes = work["attn_fwd_bytes"] + work["attn_bwd_bytes"]
+    roof_pair = dict(
+        bound="hbm",
+        ops="dsa_sparse_mla_fwd + dsa_sparse_mla_bwd",
         achieved=attn_bytes / ((fwd_ms + bwd_ms) * 1e-3) / 1e9,
         peak=HBM_PEAK_GBPS,
         unit="GB/s",
-        traffic=None,
+        algorithmic_bytes=attn_bytes,
     )
-    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof_pair["frac"] = roof_pair["achieved"] / roof_pair["peak"]
     idx_ms = phases["indexer_topk"]
     line = dict(
         metric="sparse-attn fwd+bwd tokens/s @S=8K,top-k 2048; % HBM / MFMA roofline",
@@ -261,6 +314,7 @@ def main():
         config=dict(workload="C3: DeepSeek-V3.2 DSA layer fwd+bwd", batch=1, seq_len=S, heads=H, d_qk=576, d_v=512,
                     topk=K, index_heads=64, index_dim=128, sum_k_eff=work["sum_keff"]),
         roofline=roof,
+        roofline_attention_fwd_bwd=roof_pair,
         phases_ms={k: round(v, 4) for k, v in phases.items()},
         indexer_mfma=dict(flops=work["indexer_flops"], ms_with_topk=idx_ms,
                           tflops_upper_bound=work["indexer_flops"] / (idx_ms * 1e-3) / 1e12,

@@ -1,0 +1,70 @@
+"""The C-ABI library builds for gfx950, loads, and exports every symbol include/dsa_mi355x.h declares.
+
+No compute entry point is called here (there is no GPU in the CPU suite); the host
+op layer is checked to refuse CPU tensors instead of falling back to any CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "dsa_mi355x.h"
+
+
+def header_symbols() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(dsa_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from torchtitan_npu_simulator_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from torchtitan_npu_simulator_amd import build
+
+        build.build()
+    return _lib.load_library()
+
+
+def test_header_declares_the_entry_points():
+    syms = header_symbols()
+    for name in ("dsa_indexer_fwd", "dsa_topk", "dsa_sparse_mla_fwd", "dsa_sparse_mla_bwd",
+                 "dsa_indexer_kl_grad", "dsa_compressor_fwd", "dsa_last_error"):
+        assert name in syms
+
+
+def test_library_exports_every_header_symbol(lib):
+    from torchtitan_npu_simulator_amd import _lib
+
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [s for s in header_symbols() if not hasattr(raw, s)]
+    assert not missing, missing
+    # the ctypes signature table covers exactly the header
+    assert sorted(_lib.exported_symbols()) == header_symbols()
+
+
+def test_abi_version_and_error_text(lib):
+    assert lib.dsa_abi_version() == 1
+    assert isinstance(lib.dsa_last_error(), bytes)
+
+
+def test_ops_refuse_cpu_tensors(lib):
+    from torchtitan_npu_simulator_amd import DSAError
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    q = torch.zeros(1, 4, 2, 576, dtype=torch.bfloat16)
+    kv = torch.zeros(1, 4, 576, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 4, 2, dtype=torch.int32)
+    with pytest.raises(DSAError):
+        ops.sparse_mla_fwd(q, kv, idx, 0.1)
+    with pytest.raises(DSAError):
+        ops.indexer_scores(torch.zeros(1, 4, 2, 8), torch.zeros(1, 4, 8), torch.zeros(1, 4, 2))

@@ -1,0 +1,381 @@
+"""Pins the CPU oracle (oracle/dsa_oracle.py) to checks that do not restate its formulas.
+
+Each test reduces an oracle function to something fixed independently of it: a
+brute-force loop written from the reference's definition, a library routine
+(``F.scaled_dot_product_attention``, ``torch.matmul``, ``torch.sort(stable=True)``,
+``torch.autograd.gradcheck``), a closed form, or an invariant.  A plausible slip in
+the oracle (wrong causal bound, dropped term, transposed operand, wrong tie rule)
+fails at least one of them.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import dsa_oracle as O
+
+
+def _g(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------------------
+# a3 indexer scores
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("q_offset,ratio", [(0, 1), (3, 1), (0, 4), (5, 2)])
+def test_indexer_scores_brute_force(q_offset, ratio):
+    g = _g(1)
+    B, S, H, D = 1, 7, 3, 5
+    s_k = (S + q_offset) // ratio + 1
+    q = torch.randn(B, S, H, D, generator=g)
+    k = torch.randn(B, s_k, D, generator=g)
+    w = torch.rand(B, S, H, generator=g)
+    got = O.indexer_scores(q, k, w, q_offset=q_offset, cmp_ratio=ratio, dtype=torch.float64)
+    for s in range(S):
+        for t in range(s_k):
+            # V3.2: t <= s (+offset); V4: block t valid when t < (s+1)//r
+            valid = t <= s + q_offset if ratio == 1 else t < (s + q_offset + 1) // ratio
+            if not valid:
+                assert got[0, s, t] == float("-inf")
+                continue
+            acc = 0.0
+            for h in range(H):
+                dot = sum(float(q[0, s, h, d]) * float(k[0, t, d]) for d in range(D))
+                acc += float(w[0, s, h]) * max(dot, 0.0)
+            assert abs(float(got[0, s, t]) - acc) < 1e-9 * max(1.0, abs(acc))
+
+
+def test_indexer_scores_matmul_special_case():
+    # one head, w = 1 and non-negative operands: relu is the identity -> a plain matmul
+    g = _g(2)
+    S, D = 9, 16
+    q = torch.rand(1, S, 1, D, generator=g)
+    k = torch.rand(1, S, D, generator=g)
+    got = O.indexer_scores(q, k, torch.ones(1, S, 1), dtype=torch.float64)
+    ref = torch.matmul(q[0, :, 0].double(), k[0].double().T)
+    mask = torch.ones(S, S, dtype=torch.bool).triu(1)
+    torch.testing.assert_close(got[0][~mask], ref[~mask])
+    assert torch.isinf(got[0][mask]).all()
+
+
+def test_fp8_quantise_dequantise_bound():
+    g = _g(3)
+    x = torch.randn(6, 128, generator=g) * 3
+    qx, sc = O.quantize_e4m3_per_row(x)
+    assert qx.dtype == torch.float8_e4m3fn
+    deq = qx.float() * sc.unsqueeze(-1)
+    # e4m3 has 3 mantissa bits: relative rounding error <= 2^-4 for normal values
+    rel = ((deq - x).abs() / x.abs().clamp_min(sc.unsqueeze(-1) * 2 ** -6)).max()
+    assert rel <= 2 ** -4 + 1e-6
+    assert torch.allclose(qx.float().abs().amax(-1), torch.full((6,), 448.0))
+
+
+# ---------------------------------------------------------------------------
+# a4 top-k
+# ---------------------------------------------------------------------------
+def _brute_topk(row, k, n_valid):
+    """Repeated arg-max: highest score first, equal scores -> lower index; -0.0 == +0.0; NaN never chosen."""
+    cand = [t for t in range(n_valid) if not math.isnan(row[t])]
+    chosen = []
+    while cand and len(chosen) < k:
+        best = cand[0]
+        for t in cand[1:]:
+            if row[t] > row[best]:  # strict: ties keep the lower index; -0.0 > +0.0 is False
+                best = t
+        chosen.append(best)
+        cand.remove(best)
+    out = sorted(chosen) + [-1] * (k - len(chosen))
+    return out
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_topk_brute_force_adversarial_ties(seed):
+    rng = np.random.default_rng(seed)
+    rows, n, k = 12, 40, 9
+    pool = np.array([-0.0, 0.0, 1.0, -1.0, 2.5, -np.inf, np.inf, 1e-30, -1e-30, np.nan], dtype=np.float32)
+    scores = pool[rng.integers(0, pool.size, size=(rows, n))]
+    n_valid = rng.integers(0, n + 1, size=rows)
+    got = O.topk_select_numpy(scores, k, n_valid)
+    for r in range(rows):
+        assert list(got[r]) == _brute_topk(scores[r].tolist(), k, int(n_valid[r])), r
+
+
+def test_topk_matches_stable_sort():
+    g = _g(4)
+    scores = torch.randint(-3, 4, (16, 64), generator=g).float()
+    k = 20
+    got = O.topk_select_numpy(scores.numpy(), k)
+    order = torch.sort(scores, dim=-1, descending=True, stable=True).indices[:, :k]
+    ref = torch.sort(order, dim=-1).values.int().numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_topk_causal_masking_and_padding():
+    S, k = 6, 4
+    scores = torch.arange(S * S, dtype=torch.float32).view(1, S, S).flip(-1)  # lower index = higher score
+    got = O.topk_select(scores, k)
+    for s in range(S):
+        exp = list(range(min(k, s + 1))) + [-1] * max(0, k - (s + 1))
+        assert got[0, s].tolist() == exp
+    # V4 compressed keys: valid t < (s+1)//r
+    got4 = O.topk_select(scores[:, :, :3], 2, cmp_ratio=2)
+    assert got4[0, 0].tolist() == [-1, -1]
+    assert got4[0, 1].tolist() == [0, -1]
+    assert got4[0, 5].tolist() == [0, 1]
+
+
+try:
+    from hypothesis import given, settings
+    from hypothesis import strategies as st
+
+    @settings(max_examples=60, deadline=None)
+    @given(
+        st.lists(st.sampled_from([-0.0, 0.0, 1.0, -2.0, 3.0, 0.5, float("-inf")]), min_size=1, max_size=30),
+        st.integers(1, 12),
+    )
+    def test_topk_hypothesis(vals, k):
+        row = np.array(vals, dtype=np.float32)
+        got = O.topk_select_numpy(row[None], k)[0]
+        assert list(got) == _brute_topk(row.tolist(), k, row.size)
+
+except ImportError:  # pragma: no cover
+    pass
+
+
+# ---------------------------------------------------------------------------
+# a5 / a6 gathered attention
+# ---------------------------------------------------------------------------
+def _attn_case(S, H, D, dv, q_offset=0, seed=5):
+    g = _g(seed)
+    q = torch.randn(1, S, H, D, generator=g, dtype=torch.float64)
+    kv = torch.randn(1, S + q_offset, D, generator=g, dtype=torch.float64)
+    return q, kv
+
+
+@pytest.mark.parametrize("q_offset", [0, 4])
+def test_sparse_fwd_full_selection_is_causal_sdpa(q_offset):
+    S, H, D, dv = 10, 3, 24, 16
+    q, kv = _attn_case(S, H, D, dv, q_offset)
+    s_kv = S + q_offset
+    idx = torch.full((1, S, s_kv), -1, dtype=torch.int32)
+    for s in range(S):
+        n = s + q_offset + 1
+        idx[0, s, :n] = torch.arange(n)
+    scale = 0.3
+    out, lse = O.sparse_mla_fwd(q, kv, idx, scale, d_v=dv, q_offset=q_offset)
+    # library routine: SDPA with one KV head broadcast over H heads, bottom-right causal mask
+    mask = torch.ones(S, s_kv, dtype=torch.bool).tril(q_offset)
+    ref = F.scaled_dot_product_attention(
+        q[0].transpose(0, 1), kv[0].unsqueeze(0).expand(H, -1, -1), kv[0, :, :dv].unsqueeze(0).expand(H, -1, -1),
+        attn_mask=mask, scale=scale,
+    ).transpose(0, 1)
+    torch.testing.assert_close(out[0], ref)
+    logits = torch.einsum("shd,td->sht", q[0], kv[0]) * scale
+    logits = logits.masked_fill(~mask.unsqueeze(1), float("-inf"))
+    torch.testing.assert_close(lse[0], torch.logsumexp(logits, dim=-1))
+
+
+def test_sparse_fwd_gathered_equals_dense_mask_form():
+    g = _g(6)
+    S, H, HI, DI, K = 12, 2, 2, 8, 5
+    q = torch.randn(1, H, S, 576, generator=g, dtype=torch.float64) * 0.05
+    k = torch.randn(1, 1, S, 576, generator=g, dtype=torch.float64)
+    v = k[..., :512]
+    qi = torch.randn(1, S, HI, DI, generator=g)
+    ki = torch.randn(1, S, 1, DI, generator=g)
+    w = torch.rand(1, S, HI, generator=g)
+    loss, out, sel, valid = O.dsv32_sdpa_dense(q, k, v, qi, ki, w, K, 0.1)
+    idx = torch.where(valid, sel, torch.full_like(sel, -1)).int()
+    out_g, _ = O.sparse_mla_fwd(q.transpose(1, 2), k[:, 0], idx, 0.1)
+    torch.testing.assert_close(out_g[0], out[0].transpose(0, 1))
+    assert torch.isfinite(loss)
+
+
+def test_sparse_bwd_gradcheck_and_closed_form():
+    S, H, D, dv, K = 6, 2, 8, 5, 3
+    q, kv = _attn_case(S, H, D, dv, seed=7)
+    g = _g(8)
+    idx = torch.full((1, S, K), -1, dtype=torch.int32)
+    for s in range(S):
+        perm = torch.randperm(s + 1, generator=g)[:K]
+        idx[0, s, : perm.numel()] = perm.int()
+    scale = 0.7
+
+    def f(qq, kk):
+        return O._sparse_mla_fwd_autograd(qq, kk, idx, scale, dv, 0)[0]
+
+    assert torch.autograd.gradcheck(f, (q.clone().requires_grad_(True), kv.clone().requires_grad_(True)))
+    dout = torch.randn(1, S, H, dv, generator=g, dtype=torch.float64)
+    dq, dkv = O.sparse_mla_bwd(q, kv, idx, dout, scale, d_v=dv)
+    out, lse = O.sparse_mla_fwd(q, kv, idx, scale, d_v=dv)
+    dq2, dkv2, mass = O.sparse_mla_bwd_closed_form(q, kv, idx, out, lse, dout, scale, d_v=dv)
+    torch.testing.assert_close(dq2, dq)
+    torch.testing.assert_close(dkv2, dkv)
+    # checksum identity: sum_j kv_j . dKV_j = sum q . dQ + sum O . dO (latent alias k_nope == v)
+    lhs = (kv * dkv).sum()
+    rhs = (q * dq).sum() + (out * dout).sum()
+    torch.testing.assert_close(lhs, rhs)
+    torch.testing.assert_close(mass, O.attn_mass(q, kv, idx, lse, scale))
+
+
+def test_attn_mass_full_selection_sums_to_heads():
+    S, H, D = 8, 3, 12
+    q, kv = _attn_case(S, H, D, D, seed=9)
+    idx = torch.full((1, S, S), -1, dtype=torch.int32)
+    for s in range(S):
+        idx[0, s, : s + 1] = torch.arange(s + 1)
+    _, lse = O.sparse_mla_fwd(q, kv, idx, 0.5, d_v=D)
+    m = O.attn_mass(q, kv, idx, lse, 0.5)
+    torch.testing.assert_close(m.sum(-1), torch.full((1, S), float(H), dtype=torch.float64))
+
+
+# ---------------------------------------------------------------------------
+# a7 indexer KL
+# ---------------------------------------------------------------------------
+def test_kl_closed_form_two_keys():
+    # p = (1/4, 3/4), Z = 2 (mass summed over heads), indexer scores (0, 0): KL = sum t log(t / 0.5)
+    target = torch.tensor([[[0.5, 1.5]]], dtype=torch.float64)
+    score = torch.zeros(1, 1, 2, dtype=torch.float64)
+    kl = 0.25 * math.log(0.25 / 0.5) + 0.75 * math.log(0.75 / 0.5)
+    got = O.dsa_indexer_loss(target, score, 1.0, reduction="sum")
+    assert abs(float(got) - 2.0 * kl) < 1e-12
+    # scores equal to log target (+ any constant) -> KL == 0
+    got0 = O.dsa_indexer_loss(target, torch.log(target) + 7.0, 1.0, reduction="sum")
+    assert abs(float(got0)) < 1e-12
+
+
+def test_kl_mean_is_sum_over_tokens_and_scale():
+    g = _g(10)
+    tgt = torch.rand(2, 5, 4, generator=g, dtype=torch.float64)
+    sc = torch.randn(2, 5, 4, generator=g, dtype=torch.float64)
+    s = O.dsa_indexer_loss(tgt, sc, 0.3, reduction="sum")
+    m = O.dsa_indexer_loss(tgt, sc, 0.3, reduction="mean")
+    torch.testing.assert_close(m, s / 10)  # converters/kernels/dsa.py:73 divides the op's sum by B*S
+
+
+def test_kl_zero_when_indexer_matches_target_and_zero_grad():
+    g = _g(11)
+    S, HI, DI, K = 5, 2, 4, 3
+    qi = torch.randn(1, S, HI, DI, generator=g, dtype=torch.float64)
+    ki = torch.randn(1, S, DI, generator=g, dtype=torch.float64)
+    w = torch.rand(1, S, HI, generator=g, dtype=torch.float64)
+    idx = torch.full((1, S, K), -1, dtype=torch.int32)
+    for s in range(S):
+        n = min(K, s + 1)
+        idx[0, s, :n] = torch.arange(n)
+    scores = O.indexer_scores(qi, ki, w, dtype=torch.float64)
+    vals = torch.gather(scores, -1, idx.clamp_min(0).long()).masked_fill(idx < 0, float("-inf"))
+    # target mass proportional to softmax of the indexer scores on the selected set
+    mass = torch.softmax(vals, dim=-1) * 3.0
+    mass = torch.nan_to_num(mass, nan=0.0).masked_fill(idx < 0, 0.0)
+    dq, dk, dw, loss = O.indexer_kl_from_mass(qi, ki, w, idx, mass)
+    assert abs(float(loss)) < 1e-12
+    for gr in (dq, dk, dw):
+        assert gr is None or gr.abs().max() < 1e-10
+
+
+def test_kl_gradcheck():
+    g = _g(12)
+    S, HI, DI, K = 4, 2, 3, 3
+    qi = torch.randn(1, S, HI, DI, generator=g, dtype=torch.float64)
+    ki = torch.randn(1, S, DI, generator=g, dtype=torch.float64)
+    w = torch.rand(1, S, HI, generator=g, dtype=torch.float64)
+    idx = torch.full((1, S, K), -1, dtype=torch.int32)
+    for s in range(S):
+        n = min(K, s + 1)
+        idx[0, s, :n] = torch.arange(n)
+    mass = torch.rand(1, S, K, generator=g, dtype=torch.float64).masked_fill(idx < 0, 0)
+    dq, dk, dw, loss = O.indexer_kl_from_mass(qi, ki, w, idx, mass)
+    # finite differences of the loss SUM against the autograd gradients
+    eps = 1e-6
+    for t, gr in ((qi, dq), (ki, dk), (w, dw)):
+        flat = t.view(-1)
+        for i in range(0, flat.numel(), max(1, flat.numel() // 7)):
+            old = float(flat[i])
+            flat[i] = old + eps
+            lp = O.indexer_kl_from_mass(qi, ki, w, idx, mass)[3]
+            flat[i] = old - eps
+            lm = O.indexer_kl_from_mass(qi, ki, w, idx, mass)[3]
+            flat[i] = old
+            fd = (float(lp) - float(lm)) / (2 * eps)
+            assert abs(fd - float(gr.reshape(-1)[i])) < 1e-6 * max(1.0, abs(fd))
+
+
+# ---------------------------------------------------------------------------
+# a1 compressor
+# ---------------------------------------------------------------------------
+def test_compressor_uniform_gates_mean_pool():
+    g = _g(13)
+    B, S, D, r = 1, 12, 6, 3
+    kv = torch.randn(B, S, D, generator=g)
+    out = O.compressor_pool(kv, torch.zeros(B, S, D), torch.zeros(r, D), r, overlap=False)
+    torch.testing.assert_close(out, kv.view(B, S // r, r, D).mean(2))
+
+
+def test_compressor_overlap_first_block_and_mean():
+    g = _g(14)
+    B, S, D, r = 1, 16, 5, 4
+    kv = torch.randn(B, S, 2 * D, generator=g)
+    out = O.compressor_pool(kv, torch.zeros(B, S, 2 * D), torch.zeros(r, 2 * D), r, overlap=True)
+    blocks = kv.view(B, S // r, r, 2 * D)
+    # first block: overlap slots are empty, so only the current block's features D..2D pool
+    torch.testing.assert_close(out[:, 0], blocks[:, 0, :, D:].mean(1))
+    # later blocks: mean over previous block's features 0..D and current block's D..2D
+    for b in range(1, S // r):
+        ref = torch.cat((blocks[:, b - 1, :, :D], blocks[:, b, :, D:]), dim=1).mean(1)
+        torch.testing.assert_close(out[:, b], ref)
+
+
+def test_compressor_ratio_one_identity_and_brute_softmax():
+    g = _g(15)
+    kv = torch.randn(1, 6, 4, generator=g)
+    sc = torch.randn(1, 6, 4, generator=g)
+    torch.testing.assert_close(O.compressor_pool(kv, sc, torch.zeros(1, 4), 1, overlap=False), kv)
+    r = 3
+    ape = torch.randn(r, 4, generator=g)
+    out = O.compressor_pool(kv, sc, ape, r, overlap=False)
+    for blk in range(2):
+        for f in range(4):
+            e = [math.exp(float(sc[0, blk * r + i, f] + ape[i, f])) for i in range(r)]
+            ref = sum(e[i] * float(kv[0, blk * r + i, f]) for i in range(r)) / sum(e)
+            assert abs(float(out[0, blk, f]) - ref) < 1e-5
+
+
+def test_compressor_rmsnorm_epilogue():
+    g = _g(16)
+    kv = torch.randn(1, 8, 6, generator=g)
+    w = torch.rand(6, generator=g)
+    out = O.compressor_pool(kv, torch.zeros(1, 8, 6), torch.zeros(2, 6), 2, overlap=False, norm_weight=w)
+    pooled = kv.view(1, 4, 2, 6).mean(2)
+    ref = pooled / torch.sqrt(pooled.pow(2).mean(-1, keepdim=True) + 1e-6) * w
+    torch.testing.assert_close(out, ref)
+
+
+# ---------------------------------------------------------------------------
+# V4 index helpers and TND metadata
+# ---------------------------------------------------------------------------
+def test_window_and_compress_idxs_brute_force():
+    W, S, r = 4, 9, 2
+    win = O.window_topk_idxs(W, 1, S)[0]
+    for s in range(S):
+        exp = [t for t in range(max(0, s - W + 1), s + 1)]
+        row = [int(x) for x in win[s] if x >= 0]
+        assert row == exp
+    cmp = O.compress_topk_idxs(r, 1, S, offset=100)[0]
+    for s in range(S):
+        exp = [100 + t for t in range(S // r) if t < (s + 1) // r]
+        assert [int(x) for x in cmp[s] if x >= 0] == exp
+
+
+def test_tnd_known_answers():
+    # tests/unit_tests/models/test_deepseek_v4_tnd.py:65-79 of the reference
+    pos = torch.tensor([0, 1, 2, 3, 0, 1, 2, 3])
+    assert O.tnd_compressed_block_starts(pos, 4).tolist() == [0, 4]
+    assert O.tnd_compressed_block_starts(pos, 128).numel() == 0
+    # :140-165: two requests of lengths 4 and 2 -> cu_seqlens_q [0, 4, 6]
+    assert O.lengths_to_cu_seqlens(torch.tensor([4, 2], dtype=torch.int32)).tolist() == [0, 4, 6]

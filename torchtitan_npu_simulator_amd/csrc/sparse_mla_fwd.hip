@@ -35,6 +35,9 @@ constexpr int kTileInstr = kTileChunks / 64;   // 36 wave-wide DMA instructions 
 constexpr int kHeadsPerWG = 128;
 constexpr int kQSteps = 16;                    // 16-column MFMA steps of latent Q per wave
 constexpr float kHeadroom = 64.0f;             // log2 units of P above the reference max
+constexpr int64_t kMaxGatherRows = (int64_t)UINT32_MAX / kRowBytes - 1;  // 32-bit byte offsets into kv
+constexpr int kQBatch = 3;                     // LDS A-operand loads issued ahead of their MFMAs
+constexpr int kVBatch = 2;                     // transposed V reads issued ahead of their MFMAs
 
 __device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
   return v >= 0 && v < s_kv && (int64_t)v <= limit;
@@ -42,6 +45,85 @@ __device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
 
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// ---- gathered tile loader shared by the forward and mass kernels ----
+// A block tile is kBN rows x 72 16-byte chunks, filled by 36 wave-wide DMA instructions
+// (global_load_lds, 16 B per lane): instruction J covers tile positions [64J, 64J+64),
+// position p = row*72 + (chunk ^ swz8(row)), and wave w issues J = w, w+8, ...
+// The slot indices reach a 4-entry LDS ring two blocks ahead of their DMA: wave 0 loads
+// block b+3's indices into a register while block b computes and stores them into the
+// ring one block later, so neither an index round trip nor a register spill sits in
+// front of a gather (a spill reload would wait for every DMA in flight).
+constexpr int kLoadsPerWave = (kTileInstr + kWaves - 1) / kWaves;  // 5
+constexpr int kIdxRing = 4;
+
+__device__ __forceinline__ int opaque(int x) {
+  // keeps lane-derived addressing inside the loop (recomputed, not hoisted and spilled)
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+__device__ __forceinline__ void issue_block(const uint16_t* kvb, u32x4* tile_buf, uint32_t* vmask_slot,
+                                            const int* sidx, int blk, int K, uint32_t lim, int wave, int lane_in) {
+  // a slot is usable when its index is in [0, lim] (lim = min(causal limit, S_kv - 1);
+  // negative indices wrap to large unsigned values) and it lies before K
+  const int rows_left = K - blk * kBN;
+  const int lane = opaque(lane_in);
+  const char* base = reinterpret_cast<const char*>(kvb);
+  uint32_t raw[kLoadsPerWave];
+#pragma unroll
+  for (int i = 0; i < kLoadsPerWave; ++i) {
+    const int J = min(wave + kWaves * i, kTileInstr - 1);
+    raw[i] = (uint32_t)sidx[(J * 64 + lane) / kRowChunks];
+  }
+#pragma unroll
+  for (int i = 0; i < kLoadsPerWave; ++i) {
+    const int J = wave + kWaves * i;
+    if (J < kTileInstr) {
+      const int p = J * 64 + lane;
+      const int row = p / kRowChunks, pos = p - row * kRowChunks;
+      const bool ok = raw[i] <= lim && row < rows_left;
+      const uint32_t off = (ok ? raw[i] : 0u) * (uint32_t)kRowBytes + (uint32_t)((pos ^ swz8(row)) * 16);
+      __builtin_amdgcn_global_load_lds((const void*)(base + off),
+                                       (__attribute__((address_space(3))) void*)&tile_buf[J * 64], 16, 0, 0);
+    }
+  }
+  if (wave == 0) {
+    const bool ok = lane < kBN && lane < rows_left && (uint32_t)sidx[lane & (kBN - 1)] <= lim;
+    const uint64_t bal = __ballot(ok);
+    if (lane == 0) *vmask_slot = (uint32_t)bal;
+  }
+}
+
+// Index pipeline state of wave 0: the indices of block `blk` (lane < kBN), clamped to K.
+__device__ __forceinline__ int load_block_idx(const int32_t* ridx, int K, int blk, int lane) {
+  return ridx[min(blk * kBN + (lane & (kBN - 1)), K - 1)];
+}
+
+// Prologue: ring entries 0 and 1 hold blocks 0 and 1, `pending` holds block 2.
+__device__ __forceinline__ void idx_ring_init(int (*sidx)[kBN], const int32_t* ridx, int K, int nblk, int wave,
+                                              int lane, int& pending) {
+  if (wave == 0) {
+    const int i0 = load_block_idx(ridx, K, 0, lane);
+    const int i1 = load_block_idx(ridx, K, 1, lane);
+    if (lane < kBN) {
+      sidx[0][lane] = i0;
+      sidx[1][lane] = i1;
+    }
+    if (nblk > 2) pending = load_block_idx(ridx, K, 2, lane);
+  }
+}
+
+// Iteration blk (after issuing block blk+1 from ring entry (blk+1)&3): store block blk+2
+// into the ring and start loading block blk+3.  The barrier that ends the iteration makes
+// the entry visible and the waitcnt before it lands `pending`.
+__device__ __forceinline__ void idx_ring_advance(int (*sidx)[kBN], const int32_t* ridx, int K, int nblk, int blk,
+                                                 int wave, int lane, int& pending) {
+  if (wave == 0 && blk + 2 < nblk) {
+    if (lane < kBN) sidx[(blk + 2) & (kIdxRing - 1)][lane] = pending;
+    if (blk + 3 < nblk) pending = load_block_idx(ridx, K, blk + 3, lane);
+  }
+}
 
 __global__ void __launch_bounds__(kThreads, 1)
 sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv,
@@ -52,6 +134,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   __shared__ u32x4 qpe[kHeadsPerWG][(kDqk - kDv) / 8];  // [head][16 B chunk] of q[:, 512:576]
   __shared__ f32x4 xs[kWaves][4][64];                   // partial S exchange, [wave][r/4][lane]
   __shared__ uint32_t vmask[2];
+  __shared__ int sidx[kIdxRing][kBN];
   __shared__ int last_slot;
 
   const int tok = blockIdx.x;
@@ -64,6 +147,8 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
+  const int64_t lim64 = min(limit, (int64_t)s_kv - 1);  // largest usable key index
+  const uint32_t lim = lim64 < 0 ? 0u : (uint32_t)lim64;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
   const int64_t out_row = row_id * H + head;
 
@@ -107,36 +192,6 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
     }
   }
 
-  // ---- block loader: direct global->LDS DMA, 16 B per lane.  Instruction J fills tile
-  // positions [64J, 64J+64); position p = row*72 + (chunk ^ swz8(row)).  Wave w issues
-  // J = w, w+8, ... (waves 0-3: 5 instructions, waves 4-7: 4). ----
-  auto load_block = [&](int blk, int buf) {
-    int v[5], chunk[5];
-#pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int J = wave + kWaves * i;
-      const int p = min(J, kTileInstr - 1) * 64 + lane;
-      const int row = p / kRowChunks, pos = p - row * kRowChunks;
-      chunk[i] = pos ^ swz8(row);
-      const int slot = blk * kBN + row;
-      v[i] = ridx[min(slot, K - 1)];
-      if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;  // finite stand-in row, masked later
-    }
-#pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int J = wave + kWaves * i;
-      if (J < kTileInstr)
-        __builtin_amdgcn_global_load_lds((const void*)(kvb + (int64_t)v[i] * kDqk + chunk[i] * 8),
-                                         (__attribute__((address_space(3))) void*)&tile[buf][J * 64], 16, 0, 0);
-    }
-    if (wave == 0) {
-      const int slot = blk * kBN + lane;
-      const bool ok = lane < kBN && slot < K && slot_ok(ridx[min(slot, K - 1)], s_kv, limit);
-      const uint64_t bal = __ballot(ok);
-      if (lane == 0) vmask[buf] = (uint32_t)bal;
-    }
-  };
-
   // ---- LDS byte offsets ----
   // QK A operand: key row n, chunk (32h + 2c + hh) ^ swz8(n) for latent step c; with
   // c = 4k + c' the XOR only touches the low 3 bits, so offset = qk_off[c'] + 128 k.
@@ -168,37 +223,45 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   float m_ref = -INFINITY, m_true = -INFINITY, lsum = 0.f;
   bool clamped = false;
 
-  load_block(0, 0);
+  int pending = 0;
+  idx_ring_init(sidx, ridx, K, nblk, wave, lane, pending);
+  __syncthreads();
+  issue_block(kvb, tile[0], &vmask[0], sidx[0], 0, K, lim, wave, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int blk = 0; blk < nblk; ++blk) {
     const int buf = blk & 1;
-    const bool has_next = blk + 1 < nblk;
-    if (has_next) load_block(blk + 1, buf ^ 1);
+    if (blk + 1 < nblk)
+      issue_block(kvb, tile[buf ^ 1], &vmask[buf ^ 1], sidx[(blk + 1) & (kIdxRing - 1)], blk + 1, K, lim, wave, lane);
+    idx_ring_advance(sidx, ridx, K, nblk, blk, wave, lane, pending);
     const uint32_t tb = tile_base + buf * kTileBytes;
 
     // ---- partial S^T over this wave's half of the contraction ----
-    // operands fetched in batches of 6 ahead of their MFMAs (sched_barrier keeps each batch
-    // together so its LDS latency overlaps the previous batch's MFMAs)
+    // A operands (key rows) are fetched from LDS in batches ahead of their MFMAs; the
+    // sched_barrier keeps a batch together so its LDS latency overlaps the previous
+    // batch's MFMAs.  B operands are the Q registers (rope steps: LDS).
     f32x16 s = (f32x16){0};
 #pragma unroll
-    for (int cb = 0; cb < kQSteps + 2; cb += 6) {
-      u32x4 a[6], bq[6];
+    for (int cb = 0; cb < kQSteps + 2; cb += kQBatch) {
+      u32x4 a[kQBatch];
 #pragma unroll
-      for (int u = 0; u < 6; ++u) {
+      for (int u = 0; u < kQBatch; ++u) {
         const int c = cb + u;
-        if (c < kQSteps) {
-          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + qk_off[c & 3] + 128 * (c >> 2));
-          bq[u] = qr[c];
-        } else {
-          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + pe_off[c - kQSteps]);
-          bq[u] = qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
-        }
+        if (c < kQSteps) a[u] = *(const lds_u32x4*)(uintptr_t)(tb + qk_off[c & 3] + 128 * (c >> 2));
+        else if (c < kQSteps + 2) a[u] = *(const lds_u32x4*)(uintptr_t)(tb + pe_off[c - kQSteps]);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 6; ++u) s = mfma32x32x16(as_bf16x8(a[u]), as_bf16x8(bq[u]), s);
+      for (int u = 0; u < kQBatch; ++u) {
+        const int c = cb + u;
+        if (c < kQSteps) {
+          s = mfma32x32x16(as_bf16x8(a[u]), as_bf16x8(qr[c]), s);
+        } else if (c < kQSteps + 2) {
+          const u32x4 bq = qpe[grp * 32 + n][(4 * half + 2 * (c - kQSteps) + hh) ^ (n & 7)];
+          s = mfma32x32x16(as_bf16x8(a[u]), as_bf16x8(bq), s);
+        }
+      }
     }
     // ---- swap partial S with the other half of the pair ----
 #pragma unroll
@@ -261,13 +324,13 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
     {
       constexpr int kT = kDv / 64;
 #pragma unroll
-      for (int sb = 0; sb < 2 * kT; sb += 4) {
-        u32x4 av[4];
+      for (int sb = 0; sb < 2 * kT; sb += kVBatch) {
+        u32x4 av[kVBatch];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) av[u] = read_v((sb + u) / kT, (sb + u) % kT);
+        for (int u = 0; u < kVBatch; ++u) av[u] = read_v((sb + u) / kT, (sb + u) % kT);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kVBatch; ++u) {
           const int c = (sb + u) / kT, t = (sb + u) % kT;
           o[t] = mfma32x32x16(as_bf16x8(av[u]), as_bf16x8(c == 0 ? pb0 : pb1), o[t]);
         }
@@ -314,6 +377,7 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
   __shared__ f32x4 xs[kWaves][4][64];
   __shared__ float macc[2][kBN];
   __shared__ uint32_t vmask[2];
+  __shared__ int sidx[kIdxRing][kBN];
   __shared__ int last_slot;
 
   const int tok = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
@@ -324,6 +388,8 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
+  const int64_t lim64 = min(limit, (int64_t)s_kv - 1);  // largest usable key index
+  const uint32_t lim = lim64 < 0 ? 0u : (uint32_t)lim64;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
   const int64_t hrow = row_id * H + (head_ok ? head : 0);
   float* mrow = mass + row_id * K;
@@ -362,32 +428,6 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
       }
     }
   }
-  auto load_block = [&](int blk, int buf) {
-    int v[5], chunk[5];
-#pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int J = wave + kWaves * i;
-      const int p = min(J, kTileInstr - 1) * 64 + lane;
-      const int row = p / kRowChunks, pos = p - row * kRowChunks;
-      chunk[i] = pos ^ swz8(row);
-      const int slot = blk * kBN + row;
-      v[i] = ridx[min(slot, K - 1)];
-      if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;
-    }
-#pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int J = wave + kWaves * i;
-      if (J < kTileInstr)
-        __builtin_amdgcn_global_load_lds((const void*)(kvb + (int64_t)v[i] * kDqk + chunk[i] * 8),
-                                         (__attribute__((address_space(3))) void*)&tile[buf][J * 64], 16, 0, 0);
-    }
-    if (wave == 0) {
-      const int slot = blk * kBN + lane;
-      const bool ok = lane < kBN && slot < K && slot_ok(ridx[min(slot, K - 1)], s_kv, limit);
-      const uint64_t bal = __ballot(ok);
-      if (lane == 0) vmask[buf] = (uint32_t)bal;
-    }
-  };
   const uint32_t tile_base = (uint32_t)(uintptr_t)(&tile[0][0]);
   const int xsw = swz8(n);
   uint32_t qk_off[4];
@@ -397,12 +437,17 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
 #pragma unroll
   for (int c = 0; c < 2; ++c) pe_off[c] = n * kRowBytes + 16 * ((64 + 4 * half + 2 * c + hh) ^ xsw);
 
-  load_block(0, 0);
+  int pending = 0;
+  idx_ring_init(sidx, ridx, K, nblk, wave, lane, pending);
+  __syncthreads();
+  issue_block(kvb, tile[0], &vmask[0], sidx[0], 0, K, lim, wave, lane);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int blk = 0; blk < nblk; ++blk) {
     const int buf = blk & 1;
-    if (blk + 1 < nblk) load_block(blk + 1, buf ^ 1);
+    if (blk + 1 < nblk)
+      issue_block(kvb, tile[buf ^ 1], &vmask[buf ^ 1], sidx[(blk + 1) & (kIdxRing - 1)], blk + 1, K, lim, wave, lane);
+    idx_ring_advance(sidx, ridx, K, nblk, blk, wave, lane, pending);
     const uint32_t tb = tile_base + buf * kTileBytes;
     // operands fetched in batches of 6 ahead of their MFMAs (sched_barrier keeps each batch
     // together so its LDS latency overlaps the previous batch's MFMAs)
@@ -600,6 +645,7 @@ extern "C" int dsa_attn_mass(const void* q, const void* kv, const int32_t* indic
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DSA_BF16) {
     if (d_qk != kDqk) return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: bf16 path needs d_qk=576");
+    if (s_kv > kMaxGatherRows) return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: S_kv > %lld", (long long)kMaxGatherRows);
     const unsigned hgroups = ceil_div(n_heads, kHeadsPerWG);
     if (hgroups > 1) {  // partial sums from several head groups accumulate into a zeroed buffer
       if (hipMemsetAsync(mass, 0, (size_t)(batch * s_q * topk) * 4, st) != hipSuccess)
@@ -642,6 +688,8 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
     if (d_qk != kDqk || d_v != kDv)
       return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: bf16 path needs d_qk=576, d_v=512 (got %lld/%lld)",
                        (long long)d_qk, (long long)d_v);
+    if (s_kv > kMaxGatherRows)
+      return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: S_kv > %lld", (long long)kMaxGatherRows);
     dim3 grid((unsigned)s_q, ceil_div(n_heads, kHeadsPerWG), (unsigned)batch);
     sparse_mla_fwd_bf16_kernel<<<grid, kThreads, 0, st>>>(
         (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
