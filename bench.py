@@ -168,11 +168,12 @@ def measured_traffic(kernel, S, H, K):
 
 
 def copy_calibration(torch, device, nbytes=1 << 30):
-    """One plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    """One elementwise copy kernel of known size (reads and writes ``nbytes`` once each), for
+    scaling the FETCH_SIZE / WRITE_SIZE counters."""
     src = torch.empty(nbytes, dtype=torch.uint8, device=device).fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
-    dst.copy_(src)
+    torch.bitwise_not(src, out=dst)
     torch.cuda.synchronize()
     del src, dst
 

@@ -1,0 +1,221 @@
+"""Converter / host-plumbing tests with the fused ops mocked (CPU).
+
+Mirrors the reference's hardware-free converter tests
+(tests/unit_tests/converters/test_npu_li.py:36-72, test_npu_smla.py:35-68 and
+tests/unit_tests/models/test_dsa_indexer_loss.py:135-167): argument plumbing, dtypes,
+shapes, -1 preservation, +offset, loss deferral and scaling, the registry.
+"""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+from unittest.mock import patch
+
+import pytest
+import torch
+
+from torchtitan_npu_simulator_amd import converters as conv
+from torchtitan_npu_simulator_amd.converters import dsa as dsa_mod
+from torchtitan_npu_simulator_amd.converters import npu_smla as smla_mod
+from torchtitan_npu_simulator_amd.converters.dsa_indexer_loss import (
+    DSAIndexerLossAutoScaler,
+    DSAIndexerLossLoggingHelper,
+)
+
+
+# ---------------------------------------------------------------- registry
+def test_registry_configs_and_lookup():
+    for name in ("npu_dsa", "npu_smla"):
+        cfg = conv.get_model_converter_config(name)
+        assert cfg is not None and cfg.to_dict() == {"name": name}
+        assert conv.has_npu_converter([cfg], name)
+        assert not conv.has_npu_converter([cfg], "other")
+    assert conv.get_model_converter_config("missing") is None
+
+
+def test_converter_errors_are_wrapped():
+    class Boom(conv.ModelCustomConverter):
+        def convert(self, model):
+            raise ValueError("bad model")
+
+    @conv.register_model_converter("test_boom")
+    class BoomConfig(conv.ModelCustomConfig):
+        model_converter = Boom
+
+    cls = conv.registry().converter_class("test_boom")
+    with pytest.raises(RuntimeError, match="Failed to apply custom model config 'test_boom'"):
+        cls(cls.Config(), model_spec=SimpleNamespace(name="x")).convert(torch.nn.Module())
+
+
+# ---------------------------------------------------------------- npu_smla LiCompute
+class LiCompute(torch.nn.Module):  # stand-in with the reference's attributes
+    def __init__(self, ratio, index_topk):
+        super().__init__()
+        self.ratio = ratio
+        self.index_topk = index_topk
+
+
+def test_npu_li_compute_plumbing():
+    B, S, D, K, r = 2, 16, 8, 6, 4
+    calls = {}
+
+    def fake(q, k, w, *args, **kw):
+        calls.update(q=q, k=k, w=w, args=args, kw=kw)
+        idx = torch.full((B, S, 1, K), 10, dtype=torch.int32)
+        idx[0, 0, 0, 0] = -1
+        idx[..., 1] += kw["index_offset"]  # the HIP top-k adds the offset to valid entries
+        idx[0, 0, 0, 0] = -1
+        return idx, torch.randn(B, S, 1, K)
+
+    mod = smla_mod.NpuLiCompute(LiCompute(r, K))
+    with patch.object(smla_mod.npu, "npu_lightning_indexer", side_effect=fake):
+        ind, sc = mod(torch.randn(B, S, 4, D), torch.randn(B, S // r, D), torch.randn(B, S, 4), seqlen=S, offset=100)
+    assert calls["q"].dtype == torch.bfloat16 and calls["k"].dtype == torch.bfloat16
+    assert calls["w"].dtype == torch.bfloat16
+    assert calls["k"].ndim == 4
+    assert calls["args"][9] == r  # cmp_ratio
+    assert calls["args"][5] == K and calls["args"][6] == 3  # sparse_count, sparse_mode
+    assert ind.shape == (B, S, K) and sc.shape == (B, S, K)
+    assert ind[0, 0, 0].item() == -1
+    assert ind[0, 0, 1].item() == 110
+
+
+def test_npu_smla_converter_swaps_li_compute():
+    model = torch.nn.Sequential(torch.nn.Linear(2, 2), LiCompute(4, 8))
+    conv.registry().converter_class("npu_smla")(model_spec=SimpleNamespace(name="deepseek_v4")).convert(model)
+    assert isinstance(model[1], smla_mod.NpuLiCompute)
+    assert model[1].ratio == 4 and model[1].index_topk == 8
+
+
+# ---------------------------------------------------------------- npu_dsa
+class DSV32_SDPA(torch.nn.Module):  # stand-in of the reference class name
+    def __init__(self):
+        super().__init__()
+        self.config = SimpleNamespace(kv_lora_rank=512, qk_rope_head_dim=64)
+
+    def forward(self, *a, **k):
+        raise AssertionError("torch-native forward should have been replaced")
+
+
+class _Attn(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.inner_attention = DSV32_SDPA()
+
+
+class _Block(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.attention = _Attn()
+
+
+class _Model(torch.nn.Module):
+    def __init__(self, n):
+        super().__init__()
+        self.layers = torch.nn.ModuleDict({str(i): _Block() for i in range(n)})
+
+
+def test_npu_dsa_converter_installs_forward_and_loss():
+    model = _Model(3)
+    conv.registry().converter_class("npu_dsa")(model_spec=SimpleNamespace(name="deepseek_v32")).convert(model)
+    assert DSV32_SDPA.forward is dsa_mod.dsa_forward
+    for i, blk in model.layers.items():
+        inner = blk.attention.inner_attention
+        assert isinstance(inner.compute_dsa_indexer_loss, dsa_mod.SparseLightningIndexerKLLoss)
+        assert inner.layer_number == int(i) and inner.num_layers == 3
+
+
+def test_npu_dsa_converter_skips_other_models():
+    model = _Model(1)
+    conv.registry().converter_class("npu_dsa")(model_spec=SimpleNamespace(name="qwen3")).convert(model)
+    assert not hasattr(model.layers["0"].attention.inner_attention, "layer_number")
+
+
+def test_dsa_forward_plumbing_and_loss_deferral():
+    B, H, S, K, HI, DI = 1, 4, 8, 4, 2, 16
+    self_ = SimpleNamespace(config=SimpleNamespace(kv_lora_rank=512, qk_rope_head_dim=64), layer_number=0,
+                            num_layers=1, compute_dsa_indexer_loss=dsa_mod.SparseLightningIndexerKLLoss())
+    q = torch.randn(B, H, S, 576)
+    kv = torch.randn(B, 1, S, 576)
+    v = kv[..., :512]
+    qi, ki, w = torch.randn(B, S, HI, DI, requires_grad=True), torch.randn(B, S, 1, DI), torch.rand(B, S, HI)
+    seen = {}
+
+    def fake_li(q_, k_, w_, **kw):
+        seen["li"] = kw
+        return torch.zeros(B, S, 1, K, dtype=torch.int32), None
+
+    def fake_sfa(q_nope, k_nope, v_, **kw):
+        seen["sfa"] = dict(q_nope=q_nope, k_nope=k_nope, **kw)
+        return torch.zeros(B, S, H, 512), torch.zeros(B, S, H), torch.ones(B, S, H)
+
+    with patch.object(dsa_mod.npu, "npu_lightning_indexer", side_effect=fake_li), \
+            patch.object(dsa_mod.npu, "npu_sparse_flash_attention", side_effect=fake_sfa):
+        loss, out = dsa_mod.dsa_forward(self_, q, kv, v, None, 0.1, qi, ki, w, None, K)
+    assert seen["li"]["sparse_count"] == K and seen["li"]["sparse_mode"] == 3
+    s = seen["sfa"]
+    assert s["q_nope"].shape == (B, S, H, 512) and s["query_rope"].shape == (B, S, H, 64)
+    assert s["key_rope"].shape == (B, S, 1, 64) and s["sparse_indices"].dtype == torch.int32
+    assert s["attention_mode"] == 2 and s["sparse_mode"] == 3 and s["scale_value"] == 0.1
+    assert out.shape == (B, H, S, 512)
+    assert float(loss) == 0.0  # deferred to backward
+
+    # backward runs the fused KL op, scales the grads by the upstream grad, logs loss/(B*S)
+    def fake_kl(*a, **kw):
+        return torch.ones(B, S, HI, DI), torch.ones(B, S, 1, DI), torch.ones(B, S, HI), torch.tensor([8.0])
+
+    DSAIndexerLossLoggingHelper.tracker.clear()
+    with patch.object(dsa_mod.npu, "npu_sparse_lightning_indexer_grad_kl_loss", side_effect=fake_kl):
+        (loss * 3.0).backward()
+    # d(loss/(B*S))/d(LILossTrain) = 1/(B*S), times 3
+    torch.testing.assert_close(qi.grad, torch.full_like(qi, 3.0 / (B * S)))
+    assert DSAIndexerLossLoggingHelper.tracker["values"][0].item() == pytest.approx(8.0 / (B * S))
+
+
+def test_dsa_forward_rejects_multi_kv_heads():
+    self_ = SimpleNamespace(config=SimpleNamespace(kv_lora_rank=512, qk_rope_head_dim=64))
+    with pytest.raises(NotImplementedError):
+        dsa_mod.dsa_forward(self_, torch.zeros(1, 2, 4, 576), torch.zeros(1, 2, 4, 576), torch.zeros(1, 2, 4, 512))
+
+
+# ---------------------------------------------------------------- loss plumbing
+def test_auto_scaler_injects_loss_scale():
+    from torchtitan_npu_simulator_amd.converters import dsa_indexer_loss as m
+
+    DSAIndexerLossAutoScaler.set_loss_scale(torch.tensor(0.5))
+    assert m.LOSS_SCALE.item() == 0.5
+    out = torch.randn(3, requires_grad=True)
+    aux = torch.tensor(2.0, requires_grad=True)
+    y = DSAIndexerLossAutoScaler.apply(out, aux)
+    y.sum().backward()
+    assert aux.grad.item() == 0.5
+    torch.testing.assert_close(out.grad, torch.ones(3))
+    DSAIndexerLossAutoScaler.set_loss_scale(torch.tensor(1.0))
+
+
+def test_logging_helper_save_clean_and_track():
+    DSAIndexerLossLoggingHelper.tracker.clear()
+    DSAIndexerLossLoggingHelper.save_loss_to_tracker(torch.tensor(0.123), layer_number=0, num_layers=4)
+    assert DSAIndexerLossLoggingHelper.tracker["values"][0].item() == pytest.approx(0.123)
+    DSAIndexerLossLoggingHelper.save_loss_to_tracker(torch.tensor(0.2), layer_number=2, num_layers=4)
+    assert DSAIndexerLossLoggingHelper.track_dsa_indexer_metrics(2) == pytest.approx((0.123 + 0.2) / 2 / 2)
+    assert DSAIndexerLossLoggingHelper.tracker["values"].abs().sum().item() == 0.0
+    with pytest.raises(ValueError):
+        DSAIndexerLossLoggingHelper.save_loss_to_tracker(torch.tensor(1.0), layer_number=7, num_layers=4)
+
+
+def test_logging_helper_skips_none_layer_number():
+    DSAIndexerLossLoggingHelper.tracker.clear()
+    DSAIndexerLossLoggingHelper.save_loss_to_tracker(torch.tensor(0.1), layer_number=None, num_layers=4)
+    assert "values" not in DSAIndexerLossLoggingHelper.tracker
+
+
+def test_sparse_mode_offsets():
+    from torchtitan_npu_simulator_amd.torch_npu_ops import _resolve_q_offset
+
+    assert _resolve_q_offset(3, 128, 512, None) == 384  # bottom-right causal (one CP shard)
+    assert _resolve_q_offset(3, 128, 128, None) == 0
+    assert _resolve_q_offset(3, 128, 512, 7) == 7
+    assert _resolve_q_offset(0, 128, 512, None) >= 1 << 40  # no mask
+    with pytest.raises(ValueError):
+        _resolve_q_offset(1, 4, 4, None)
