@@ -37,6 +37,7 @@ __all__ = [
     "indexer_scores",
     "topk_select",
     "quantize_fp8_per_row",
+    "compressor_pool",
 ]
 
 _SCORE_BUDGET_BYTES = 1 << 30  # fp32 score rows materialised per indexer chunk
@@ -394,6 +395,39 @@ def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, 
         "dsa_indexer_kl_grad",
     )
     return dq_i, dk_i, dw, loss_rows
+
+
+# ---------------------------------------------------------------------------
+# block KV compressor (V4)
+# ---------------------------------------------------------------------------
+def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, norm_eps=1e-6, out_dtype=None):
+    """Softmax-gated pooling of ``ratio``-token blocks (dsa_compressor_fwd).
+
+    kv, score [B,S,coff*D] fp32 (the wkv / wgate projections; coff = 2 with overlap, which
+    defaults to ``ratio == 4`` as in the reference), ape [ratio, coff*D] fp32.  Returns
+    [B,S/ratio,D]: the pooled fp32 rows, or with ``norm_weight`` the RMSNorm of the
+    bf16-rounded pooled rows times the weight, in ``out_dtype`` (default bf16).
+    """
+    lib = load_library()
+    require_gpu_tensor(kv, "kv")
+    if overlap is None:
+        overlap = ratio == 4
+    B, S, CD = kv.shape
+    coff = 2 if overlap else 1
+    D = CD // coff
+    if out_dtype is None:
+        out_dtype = torch.bfloat16 if norm_weight is not None else torch.float32
+    kv = kv.float().contiguous()
+    score = score.float().contiguous()
+    ape = ape.float().contiguous()
+    nw = None if norm_weight is None else norm_weight.float().contiguous()
+    out = torch.empty(B, S // ratio, D, dtype=out_dtype, device=kv.device)
+    check(
+        lib.dsa_compressor_fwd(ptr(kv), ptr(score), ptr(ape), ptr(nw), ptr(out), _lib.dtype_code(out_dtype), B, S, D,
+                               int(ratio), int(bool(overlap)), float(norm_eps), stream_of(kv.device)),
+        "dsa_compressor_fwd",
+    )
+    return out
 
 
 def default_softmax_scale(d_qk: int) -> float:
