@@ -6,7 +6,8 @@ One step = one pass of the DeepSeek-V3.2 DSA hot path over one synthetic batch
 64 heads x 128 with fp8-e4m3 per-token-scaled keys and queries):
 
   fp8 quantise q_I, k_I -> lightning indexer + top-k -> sparse MLA forward ->
-  attention mass -> indexer KL loss gradients -> sparse MLA backward (dQ, dKV)
+  sparse MLA backward (dQ, dKV, and the head-summed attention mass the indexer loss
+  needs, from the probabilities the backward recomputes) -> indexer KL loss gradients
 
 Inputs are resident in HBM before the timed region.  Prints ONE JSON line.  The
 ``roofline`` object is for the dominant kernel (the gathered sparse MLA forward):
@@ -113,12 +114,11 @@ def dsa_step(inp, ops, timer):
         idx = idx[:, :, 0]
     with timer("attn_fwd"):
         out, smax, ssum = ops.sparse_mla_fwd(inp["q"], inp["kv"], idx, inp["scale"])
-    with timer("attn_mass"):
-        mass = ops.attn_mass(inp["q"], inp["kv"], idx, smax, ssum, inp["scale"])
+    with timer("attn_bwd"):
+        dq, dkv, mass = ops.sparse_mla_bwd(inp["q"], inp["kv"], idx, out, inp["dout"], smax, ssum, inp["scale"],
+                                           return_mass=True)
     with timer("indexer_kl_grad"):
         dq_i, dk_i, dw, loss_rows = ops.indexer_kl_grad_from_mass(inp["q_idx"], inp["k_idx"], inp["w"], idx, mass)
-    with timer("attn_bwd"):
-        dq, dkv = ops.sparse_mla_bwd(inp["q"], inp["kv"], idx, out, inp["dout"], smax, ssum, inp["scale"])
     return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss_rows)
 
 

@@ -101,6 +101,10 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, vo
  *   dq        [B, S, H, D_qk]  same dtype as q (written)
  *   dkv_accum [B, S_kv, D_qk]  fp32, ACCUMULATED into (caller zeroes it); latent alias:
  *             dkv[:, :D_v] = dK_nope + dV, dkv[:, D_v:] = dK_rope
+ *   mass      [B, S, K] fp32 or NULL: if given, also written with the head-summed attention
+ *             probability at each slot (what dsa_attn_mass computes), taken from the P this
+ *             backward recomputes anyway; bf16 path only (the A5 reference's
+ *             sparse_flash_mla_grad returns the same quantity, converters/kernels/npu_smla.py:540-568)
  *   workspace  device scratch of workspace_bytes (dsa_sparse_mla_bwd_workspace_size() gives the
  *              default; a smaller one processes query rows in more chunks); fp32 dtype needs none
  * The bf16 path needs D_qk = 576, D_v = 512, H <= 128.  dKV is reduced per key without
@@ -109,7 +113,7 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, vo
 int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
                                           int64_t d_qk, int64_t topk);
 int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out, const void* dout,
-                       const float* softmax_max, const float* softmax_sum, void* dq, float* dkv_accum,
+                       const float* softmax_max, const float* softmax_sum, void* dq, float* dkv_accum, float* mass,
                        void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q,
                        int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
                        int64_t q_offset, void* stream);

@@ -53,7 +53,9 @@ def test_library_exports_every_header_symbol(lib):
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.dsa_abi_version() == 1
+    from torchtitan_npu_simulator_amd import _lib
+
+    assert lib.dsa_abi_version() == _lib.ABI_VERSION
     assert isinstance(lib.dsa_last_error(), bytes)
 
 

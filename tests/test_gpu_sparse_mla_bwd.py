@@ -103,3 +103,24 @@ def test_attn_mass_parity(S, H, K, q_offset):
     # each head's softmax sums to one over the selected keys
     rows = torch.isfinite(lse).all(-1)
     assert torch.allclose(mass.sum(-1)[rows].double(), torch.full_like(mass.sum(-1)[rows].double(), H), rtol=1e-3)
+
+
+@pytest.mark.parametrize("S,H,K,q_offset", [(200, 128, 128, 0), (64, 16, 32, 16), (96, 72, 40, 0)])
+def test_bwd_fused_mass_matches_attn_mass(S, H, K, q_offset):
+    """The mass the backward returns (one or several head groups) equals dsa_attn_mass and the oracle."""
+    q, kv, dout, scale = attn_inputs(S, H, q_offset=q_offset, seed=11)
+    idx = rand_indices(S, K, q_offset=q_offset, seed=11, holes=0.1)
+    ops = _ops()
+    qd, kvd, idxd = q.to(DEV), kv.to(DEV), idx.to(DEV)
+    out, smax, ssum = ops.sparse_mla_fwd(qd, kvd, idxd, scale, q_offset=q_offset)
+    dq, dkv, mass = ops.sparse_mla_bwd(qd, kvd, idxd, out, dout.to(DEV), smax, ssum, scale, q_offset=q_offset,
+                                       return_mass=True)
+    dq2, dkv2 = ops.sparse_mla_bwd(qd, kvd, idxd, out, dout.to(DEV), smax, ssum, scale, q_offset=q_offset)
+    standalone = ops.attn_mass(qd, kvd, idxd, smax, ssum, scale, q_offset=q_offset)
+    torch.cuda.synchronize()
+    assert torch.equal(dq.cpu(), dq2.cpu())
+    lse = smax.cpu().double() + torch.log(ssum.cpu().double())
+    ref = O.attn_mass(q, kv, idx, lse, scale, q_offset=q_offset)
+    assert rel_err(mass.cpu(), ref) <= 1e-4
+    assert rel_err(mass.cpu(), standalone.cpu()) <= 1e-4
+    assert float(mass.cpu()[idx < 0].abs().sum()) == 0.0

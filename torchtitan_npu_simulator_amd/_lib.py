@@ -13,6 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
+ABI_VERSION = 2
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -33,7 +34,7 @@ _SIGNATURES = {
     ),
     "dsa_sparse_mla_bwd_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _i64], _i64),
     "dsa_sparse_mla_bwd": (
-        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _f32, _i64, _vp],
         _i32,
     ),
@@ -75,6 +76,8 @@ def load_library(path: Path | None = None):
             fn = getattr(lib, name)
             fn.argtypes = argtypes
             fn.restype = restype
+        if lib.dsa_abi_version() != ABI_VERSION:
+            raise DSAError(f"{p} has ABI {lib.dsa_abi_version()}, expected {ABI_VERSION}: rebuild it")
         _lib = lib
         return lib
 

@@ -27,14 +27,12 @@ int check_launch(const char* what);
 __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
-// round-to-nearest-even fp32 -> bf16 bits (inputs here are finite)
-__device__ __forceinline__ uint16_t f_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
+__device__ __forceinline__ uint16_t f_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f_to_bf16(lo) | ((uint32_t)f_to_bf16(hi) << 16);
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -44,6 +42,25 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
 }
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// LDS addressing through pointers (not integers): constant offsets added to an
+// address-space-3 pointer fold into the ds_read offset field, integer arithmetic does not.
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4_ptr_t;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4_ptr_t;
+__device__ __forceinline__ lds_char* lds_bytes(void* generic_lds_ptr) {
+  return (lds_char*)(uint32_t)(uintptr_t)generic_lds_ptr;
+}
+__device__ __forceinline__ u32x4 lds_read16(const lds_char* p) { return *(const lds_u32x4_ptr_t*)p; }
+// transposed 4 x 16-bit reads of two row groups, packed as the 8 bf16 of an MFMA operand
+__device__ __forceinline__ u32x4 lds_read_tr_pair(const lds_char* p1, const lds_char* p2) {
+  const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr_t*)p1);
+  const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr_t*)p2);
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 w1 = __builtin_bit_cast(u32x2, v1);
+  const u32x2 w2 = __builtin_bit_cast(u32x2, v2);
+  return (u32x4){w1[0], w1[1], w2[0], w2[1]};
 }
 
 // wave-level helpers (64-wide)
@@ -65,6 +82,24 @@ __device__ __forceinline__ float wave_sum(float v) {
 // (8-lane b128 reads of one column are conflict-free) and rows 4k..4k+3 to distinct even
 // values (a 4-row x 32-byte transposed read covers all banks once).
 __device__ __forceinline__ int swz8(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+// 16-byte-per-lane DMA from global memory straight into LDS (global_load_lds_dwordx4):
+// lane i reads gbase + voff and writes LDS byte lds_base + 16 i.  gbase and lds_base must
+// be wave-uniform.  Issued from inline assembly on purpose: the compiler then does not
+// treat every later LDS read as dependent on the DMA (it would otherwise wait for all DMAs
+// in flight before each ds_read), so the caller must wait for completion itself
+// (s_waitcnt vmcnt) before reading the destination.
+__device__ __forceinline__ void dma16_to_lds(const void* gbase, uint32_t voff, uint32_t lds_base) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gbase), "s"(m0v)
+               : "memory", "m0");
+}
+// 4-byte-per-lane variant: lane i writes LDS byte lds_base + 4 i.
+__device__ __forceinline__ void dma4_to_lds(const void* gbase, uint32_t voff, uint32_t lds_base) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(gbase), "s"(m0v)
+               : "memory", "m0");
+}
 
 inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
 

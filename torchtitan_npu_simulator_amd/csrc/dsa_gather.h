@@ -1,0 +1,129 @@
+// Gathered KV-row pipeline shared by the sparse-attention kernels (gfx950).
+//
+// A block is kBN = 32 selected latent-KV rows of 576 bf16 (1152 B).  Its LDS tile holds
+// the rows row-major with 16-byte chunk c of row r at chunk c ^ swz8(r), and is filled by
+// 36 wave-wide DMA instructions (global_load_lds, 16 B per lane): instruction J covers
+// tile positions [64J, 64J+64), position p = r*72 + (c ^ swz8(r)); wave w issues
+// J = w, w + W, ...  Unused slots (-1, past the causal limit, past K) load row 0 and are
+// masked by the block's validity bits.
+//
+// Tiles are triple-buffered: while block b computes, block b+1 has landed or is landing
+// and block b+2 is being issued, so a gather has two block times to arrive.  The slot
+// indices reach a 4-entry LDS ring by DMA as well (wave 0, one dword per lane, issued for
+// block b+3 just before block b+2's rows), so no index round trip precedes a gather and
+// no register waits on a load inside the loop.
+//
+// Waiting: vector-memory loads retire in issue order, so "block b+1 and the indices of
+// b+3 have landed" holds as soon as no more loads are outstanding than the rows of block
+// b+2 that this wave issued after them.  Stores issued after those rows would only add
+// to the count, so kernels issue their stores for block b-1 before block b+2's DMA.
+// With no block b+2 in flight the wait is for everything (vmcnt 0).  The DMAs are inline
+// assembly, so the compiler neither counts them nor waits on them; every wait is explicit.
+#pragma once
+#include "dsa_common.h"
+
+namespace dsa {
+
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4_t;
+
+struct GatherGeom {
+  static constexpr int kDqk = 576;
+  static constexpr int kRowChunks = kDqk / 8;           // 72
+  static constexpr int kRowBytes = kRowChunks * 16;     // 1152
+  static constexpr int kBN = 32;                        // rows per block
+  static constexpr int kTileChunks = kBN * kRowChunks;  // 2304 x 16 B
+  static constexpr int kTileBytes = kTileChunks * 16;   // 36864
+  static constexpr int kTileInstr = kTileChunks / 64;   // 36 wave-wide DMA instructions
+  static constexpr int kRing = 4;
+  static constexpr int64_t kMaxRows = (int64_t)UINT32_MAX / kRowBytes - 1;  // 32-bit byte offsets
+};
+
+// usable-key limit of a row: slot value v is used iff (uint32)v <= lim
+__device__ __forceinline__ uint32_t gather_limit(int64_t tok_limit, int s_kv) {
+  const int64_t l = tok_limit < (int64_t)s_kv - 1 ? tok_limit : (int64_t)s_kv - 1;
+  return l < 0 ? 0u : (uint32_t)l;
+}
+
+template <int kWaves>
+struct RowGather {
+  using G = GatherGeom;
+  static constexpr int kMaxPerWave = (G::kTileInstr + kWaves - 1) / kWaves;
+  static constexpr int kFullWaves = G::kTileInstr % kWaves == 0 ? kWaves : G::kTileInstr % kWaves;
+  static constexpr int kRingInts = 64;  // one dword per lane; lanes 32..63 repeat 0..31
+
+  // per-lane DMA geometry, computed once per workgroup: for the wave's i-th instruction
+  // (J = wave + kWaves i) the tile row this lane loads and the swizzled byte offset of its
+  // 16-byte chunk within the KV row
+  struct Lanes {
+    int row[kMaxPerWave];
+    uint32_t cbyte[kMaxPerWave];
+  };
+  static __device__ __forceinline__ Lanes lanes(int wave, int lane) {
+    Lanes L;
+#pragma unroll
+    for (int i = 0; i < kMaxPerWave; ++i) {
+      const int J = min(wave + kWaves * i, G::kTileInstr - 1);
+      const int p = J * 64 + lane;
+      const int row = p / G::kRowChunks, pos = p - row * G::kRowChunks;
+      L.row[i] = row;
+      L.cbyte[i] = (uint32_t)((pos ^ swz8(row)) * 16);
+    }
+    return L;
+  }
+
+  // issue block `blk`'s row DMA into `tile` from ring entry `sidx`; wave 0 also writes the
+  // block's validity bits.  `wave` must be wave-uniform (an SGPR value).
+  static __device__ __forceinline__ void issue(const uint16_t* kvb, u32x4* tile, uint32_t* vmask_slot,
+                                               const int* sidx, int blk, int K, uint32_t lim, int wave, int lane,
+                                               const Lanes& L) {
+    const int rows_left = K - blk * G::kBN;
+    const char* base = reinterpret_cast<const char*>(kvb);
+    uint32_t raw[kMaxPerWave];
+#pragma unroll
+    for (int i = 0; i < kMaxPerWave; ++i) raw[i] = (uint32_t)sidx[L.row[i]];
+#pragma unroll
+    for (int i = 0; i < kMaxPerWave; ++i) {
+      const int J = wave + kWaves * i;
+      if (J < G::kTileInstr) {
+        const bool ok = raw[i] <= lim && L.row[i] < rows_left;
+        const uint32_t off = (ok ? raw[i] : 0u) * (uint32_t)G::kRowBytes + L.cbyte[i];
+        dma16_to_lds(base, off, (uint32_t)(uintptr_t)&tile[J * 64]);
+      }
+    }
+    if (wave == 0) {
+      const bool ok = lane < G::kBN && lane < rows_left && (uint32_t)sidx[lane & (G::kBN - 1)] <= lim;
+      const uint64_t bal = __ballot(ok);
+      if (lane == 0) *vmask_slot = (uint32_t)bal;
+    }
+  }
+
+  // wave 0: DMA the slot indices of block `blk` (clamped to K) into ring entry `ring`
+  static __device__ __forceinline__ void issue_idx(const int32_t* ridx, int K, int blk, int* ring, int lane) {
+    const int j = min(blk * G::kBN + (lane & (G::kBN - 1)), K - 1);
+    dma4_to_lds(ridx, (uint32_t)j * 4u, (uint32_t)(uintptr_t)ring);
+  }
+
+  // prologue: indices of blocks 0..2 into ring entries 0..2 and landed, visible after the
+  // caller's barrier
+  static __device__ __forceinline__ void ring_init(int (*sidx)[kRingInts], const int32_t* ridx, int K, int nblk,
+                                                   int wave, int lane) {
+    if (wave == 0) {
+      for (int i = 0; i < 3 && i < nblk; ++i) issue_idx(ridx, K, i, sidx[i], lane);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+  }
+
+  // wait until block blk+1's rows (and the ring entry of blk+3) have landed; call at the
+  // end of iteration blk, after which the caller's barrier publishes them
+  static __device__ __forceinline__ void wait_next(bool rows2_in_flight, int wave) {
+    if (!rows2_in_flight) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (kFullWaves == kWaves || wave < kFullWaves) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kMaxPerWave) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kMaxPerWave - 1) : "memory");
+    }
+  }
+};
+
+}  // namespace dsa

@@ -20,6 +20,7 @@
 
 #include "dsa_common.h"
 #include "dsa_csr.h"
+#include "dsa_gather.h"
 
 namespace dsa {
 namespace {
@@ -74,16 +75,20 @@ __device__ int count_blocks(const int32_t* ridx, int K, int s_kv, int64_t limit,
 __global__ void __launch_bounds__(256, 1)
 bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
               const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, const float* __restrict__ smax,
-              const float* __restrict__ ssum, uint16_t* __restrict__ dq, uint16_t* __restrict__ gbuf, int S, int s_kv,
+              const float* __restrict__ ssum, uint16_t* __restrict__ dq, uint16_t* __restrict__ gbuf,
+              float* __restrict__ mbase, int64_t m_hg_stride, int64_t m_b_stride, int m_row_base, int S, int s_kv,
               int H, int K, float scale, int64_t q_offset, int row0) {
-  __shared__ u32x4 tile[2][kTileChunks];
-  __shared__ uint16_t gst[kBN][2 * kHG];  // staged G rows of this head group
-  __shared__ uint32_t vmask[2];
+  using Gather = RowGather<4>;
+  __shared__ u32x4 tile[3][kTileChunks];
+  __shared__ uint16_t gst[2][kBN][2 * kHG];  // staged G rows of this head group (by block parity)
+  __shared__ float pst[2][4][kBN];          // per-wave head sums of P (attention mass)
+  __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
+  __shared__ uint32_t vmask[3];
   __shared__ int sh_last;
 
   const int tok = row0 + blockIdx.x;  // row within the batch element
   const int hg = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
   const int head = hg * kHG + wave * 16 + col;
   const bool head_ok = head < H;
@@ -95,7 +100,12 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   // G rows of this chunk: [local row][slot][kGW]
   uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + blockIdx.x) * (int64_t)K * kGW;
 
+  // head-summed P of this head group for the row (mass; the host adds the head groups)
+  float* mrow = mbase ? mbase + hg * m_hg_stride + b * m_b_stride + (int64_t)(m_row_base + blockIdx.x) * K : nullptr;
+
   const int nblk = count_blocks(ridx, K, s_kv, limit, &sh_last);
+  if (mrow)  // slots past the last usable block carry no mass
+    for (int j = nblk * kBN + tid; j < K; j += 256) mrow[j] = 0.f;
   if (nblk == 0) {  // no usable key: dQ = 0 (G rows are never read)
     if (head_ok) {
       uint32_t* d32 = reinterpret_cast<uint32_t*>(dq + hrow * kDqk);
@@ -103,6 +113,7 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     }
     return;
   }
+  const uint32_t lim = gather_limit(limit, s_kv);
 
   // ---- per-head operands: Q (B layout of S^T = K Q^T), dO (B layout of dP^T = V dO^T) ----
   u32x4 qb[kDqk / 32], db[kDv / 32];
@@ -130,35 +141,8 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   }
   const float scale_log2 = scale * kLog2e;
 
-  auto load_block = [&](int blk, int buf) {
-    int v[9], chunk[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) {
-      const int J = wave * 9 + i;
-      const int p = J * 64 + lane;
-      const int row = p / kRowChunks, pos = p - row * kRowChunks;
-      chunk[i] = pos ^ swz8(row);
-      const int slot = blk * kBN + row;
-      v[i] = ridx[min(slot, K - 1)];
-      if (slot >= K || !slot_ok(v[i], s_kv, limit)) v[i] = 0;
-    }
-#pragma unroll
-    for (int i = 0; i < 9; ++i) {
-      const int J = wave * 9 + i;
-      __builtin_amdgcn_global_load_lds((const void*)(kvb + (int64_t)v[i] * kDqk + chunk[i] * 8),
-                                       (__attribute__((address_space(3))) void*)&tile[buf][J * 64], 16, 0, 0);
-    }
-    if (wave == 0) {
-      const int slot = blk * kBN + lane;
-      const bool ok = lane < kBN && slot < K && slot_ok(ridx[min(slot, K - 1)], s_kv, limit);
-      const uint64_t bal = __ballot(ok);
-      if (lane == 0) vmask[buf] = (uint32_t)bal;
-    }
-  };
-
   // LDS offsets.  A operand of S^T / dP^T: key row 16kt + col, chunk 4c + g (XOR swz8(row)).
   // With c = 2u + c0 the XOR touches only bits 0..2 of 4c + g -> ka_off[kt][c0] + 128 u.
-  const uint32_t tile_base = (uint32_t)(uintptr_t)(&tile[0][0]);
   uint32_t ka_off[2][2];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
@@ -180,15 +164,46 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
   for (int t = 0; t < kDqk / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  load_block(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
+  // G and mass of block `fb` staged in gst/pst[fb & 1] -> global (issued one iteration
+  // after staging, before the next row DMA, so the stores never hold up a tile wait)
+  auto flush = [&](int fb) {
+    const int sb = fb & 1;
+    if (mrow && tid < kBN && fb * kBN + tid < K)
+      mrow[fb * kBN + tid] = (pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid]);
+    for (int i = tid; i < kBN * 16; i += 256) {  // 32 slots x 256 B -> G[slot][128 hg ..]
+      const int slot = i >> 4, part = i & 15;
+      if (fb * kBN + slot >= K) continue;  // the row holds K slots only
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&gst[sb][slot][part * 8]);
+      *reinterpret_cast<u32x4*>(grow + (int64_t)(fb * kBN + slot) * kGW + 2 * kHG * hg + part * 8) = v;
+    }
+  };
+
+  // the per-head operands must have arrived before the first DMA: a later wait for them
+  // would also wait for every row DMA in flight
+#pragma unroll
+  for (int c = 0; c < kDqk / 32; ++c) asm volatile("" : "+v"(qb[c]));
+#pragma unroll
+  for (int c = 0; c < kDv / 32; ++c) asm volatile("" : "+v"(db[c]));
+  asm volatile("" : "+v"(delta), "+v"(lse2));
+  const typename Gather::Lanes gl = Gather::lanes(wave, lane);
+  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);
+  __syncthreads();
+  Gather::issue(kvb, tile[0], &vmask[0], sidx[0], 0, K, lim, wave, lane, gl);
+  if (nblk > 1) Gather::issue(kvb, tile[1], &vmask[1], sidx[1], 1, K, lim, wave, lane, gl);
+  Gather::wait_next(nblk > 1, wave);  // block 0 landed
   __syncthreads();
 
   for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk & 1;
-    const bool has_next = blk + 1 < nblk;
-    if (has_next) load_block(blk + 1, buf ^ 1);
-    const uint32_t tb = tile_base + buf * kTileBytes;
+    const int buf = blk % 3;
+    const bool in_flight2 = blk + 2 < nblk;
+    if (blk > 0) flush(blk - 1);
+    if (wave == 0 && blk + 3 < nblk)
+      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
+    if (in_flight2) {
+      const int nb = (blk + 2) % 3;
+      Gather::issue(kvb, tile[nb], &vmask[nb], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl);
+    }
+    const lds_char* tb = lds_bytes(&tile[buf][0]);
     const uint32_t vm = vmask[buf];
 
     // S^T and dP^T: operands read in batches of 6 ahead of their MFMAs (the sched_barrier
@@ -204,7 +219,7 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
         for (int u = 0; u < 6; ++u) {
           const int c = cb + u;
-          a[u] = *(const lds_u32x4*)(uintptr_t)(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
+          a[u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -217,13 +232,13 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     }
     // P and dS (lane: head col, keys 16kt + 4g + r)
     float pv[2][4], dsv[2][4];
+    const uint32_t vmg = vm >> (4 * g);  // bit r: key 4g + r, bit 16 + r: key 16 + 4g + r
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int key = 16 * kt + 4 * g + r;
-        const bool ok = (vm >> key) & 1u;
-        const float p = ok ? exp2f(sacc[kt][r] * scale_log2 - lse2) : 0.f;
+        const bool ok = (vmg >> (16 * kt + r)) & 1u;
+        const float p = ok ? __builtin_amdgcn_exp2f(sacc[kt][r] * scale_log2 - lse2) : 0.f;
         pv[kt][r] = p;
         dsv[kt][r] = p * (pacc[kt][r] - delta);
       }
@@ -239,8 +254,8 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int dt = db4 + u;
-        const uint32_t a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
-        a[u] = tr_pair(a1, a1 + 16 * kRowBytes);
+        const lds_char* a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
+        a[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -252,19 +267,33 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int slot = 16 * kt + 4 * g + r;
-        gst[slot][wave * 16 + col] = f_to_bf16(dsv[kt][r] * scale);
-        gst[slot][kHG + wave * 16 + col] = f_to_bf16(pv[kt][r]);
+        gst[blk & 1][slot][wave * 16 + col] = f_to_bf16(dsv[kt][r] * scale);
+        gst[blk & 1][slot][kHG + wave * 16 + col] = f_to_bf16(pv[kt][r]);
       }
-    __syncthreads();
-    for (int i = tid; i < kBN * 16; i += 256) {  // 32 slots x 256 B -> G[slot][128 hg ..]
-      const int slot = i >> 4, part = i & 15;
-      if (blk * kBN + slot >= K) continue;  // the row holds K slots only
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&gst[slot][part * 8]);
-      *reinterpret_cast<u32x4*>(grow + (int64_t)(blk * kBN + slot) * kGW + 2 * kHG * hg + part * 8) = v;
+    if (mrow) {
+      // sum P over this wave's 16 head lanes: three halving exchange steps (xor 8, 4, 2)
+      // leave lane col with value j = (col >> 1) & 7 (j = 4 kt + r), the xor-1 add
+      // completes it
+      const bool u8 = col & 8, u4 = col & 4, u2 = col & 2;
+      float h4[4], h2[2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = pv[0][j], hi = pv[1][j];  // values j and j + 4
+        h4[j] = (u8 ? hi : lo) + __shfl_xor(u8 ? lo : hi, 8, 64);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) h2[j] = (u4 ? h4[j + 2] : h4[j]) + __shfl_xor(u4 ? h4[j] : h4[j + 2], 4, 64);
+      const float h1 = (u2 ? h2[1] : h2[0]) + __shfl_xor(u2 ? h2[0] : h2[1], 2, 64);
+      const float tot = h1 + __shfl_xor(h1, 1, 64);
+      if ((col & 1) == 0) {
+        const int j = (col >> 1) & 7;
+        pst[blk & 1][wave][16 * (j >> 2) + 4 * g + (j & 3)] = tot;
+      }
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    Gather::wait_next(in_flight2, wave);  // block blk+1 (and ring entry blk+3) landed
     __syncthreads();
   }
+  flush(nblk - 1);
 
   // ---- dQ epilogue: lane (head col, g) holds d = 16 dt + 4 g + r ----
   if (!head_ok) return;
@@ -294,16 +323,18 @@ constexpr int kGTChunks = kCT * (kGW / 8);  // 4096 16-byte chunks (64 KB)
 constexpr int kXK = 64;                     // X rows staged per chunk while loading X
 constexpr int kXChunks = kXK * kRowChunks;  // 4608 chunks (73.7 KB)
 
+template <int kHGroups>
 __global__ void __launch_bounds__(kCThreads, 1)
 bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ dout,
                    const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf, uint16_t* __restrict__ cbuf,
                    int S, int s_kv, int H, int K, int64_t q_offset, int row0, int rows) {
-  __shared__ u32x4 lds[2 * kGTChunks];  // X staging at start, then two G tiles
+  constexpr int kKSteps = 4 * kHGroups;  // 32-row k steps of X (128 rows per head group)
+  __shared__ u32x4 lds[2 * kGTChunks];   // X staging at start, then two G tiles
   __shared__ int sh_last;
 
   const int lr = blockIdx.x;  // local row in chunk
   const int tok = row0 + lr, b = blockIdx.y;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
@@ -312,20 +343,14 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int nslots = min(K, nblk * kBN);
   const uint16_t* grow = gbuf + ((int64_t)b * rows + lr) * (int64_t)K * kGW;
   uint16_t* crow = cbuf + ((int64_t)b * rows + lr) * (int64_t)K * kDqk;
-  const int nheads_g = (H + kHG - 1) / kHG;
-  const int ksteps = 4 * nheads_g;  // 32-row k steps of X actually used (<= 8)
-  const uint32_t lds_base = (uint32_t)(uintptr_t)(&lds[0]);
+  const lds_char* lb = lds_bytes(&lds[0]);
 
   // ---- X^T slice into VGPRs: xa[t][ks] = X[32 ks + 8g .. +8][48w + 16t + col] ----
-  u32x4 xa[3][8];
-#pragma unroll
-  for (int t = 0; t < 3; ++t)
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) xa[t][ks] = (u32x4){0u, 0u, 0u, 0u};
+  // (rows of dO at the rope columns are zero, so every MFMA below runs unconditionally)
+  u32x4 xa[3][kKSteps];
   const int tr_row = 8 * g + (col >> 2);  // source row within a 32-row k step (+4 second read)
 #pragma unroll
-  for (int kc = 0; kc < 4; ++kc) {
-    if (kc / 2 >= nheads_g) continue;  // block-uniform
+  for (int kc = 0; kc < 2 * kHGroups; ++kc) {
     __syncthreads();
     const int hgk = kc >> 1, type = kc & 1;
     for (int i = tid; i < kXChunks; i += kCThreads) {
@@ -346,17 +371,23 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
         const int c0 = (48 * wave + 16 * t) / 8 + ((col & 3) >> 1);
-        const uint32_t a1 = lds_base + 16 * (r1 * kRowChunks + (c0 ^ swz8(r1))) + 8 * (col & 1);
-        const uint32_t a2 = lds_base + 16 * (r2 * kRowChunks + (c0 ^ swz8(r2))) + 8 * (col & 1);
-        xa[t][ks] = tr_pair(a1, a2);
+        const lds_char* a1 = lb + 16 * (r1 * kRowChunks + (c0 ^ swz8(r1))) + 8 * (col & 1);
+        const lds_char* a2 = lb + 16 * (r2 * kRowChunks + (c0 ^ swz8(r2))) + 8 * (col & 1);
+        xa[t][ks] = lds_read_tr_pair(a1, a2);
       }
     }
   }
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) asm volatile("" : "+v"(xa[t][ks]));  // landed before the DMAs
   __syncthreads();
 
   // ---- stream G tiles; C^T[16 cols x 16 slots] = X^T[16 cols x 256] . G^T[256 x 16 slots] ----
+  // per-lane DMA geometry: instruction J = wave + 12 i covers tile chunks [64J, 64J+64),
+  // chunk p = slot*32 + (c ^ swz8(slot))
   const int ntiles = (nslots + kCT - 1) / kCT;
-  auto load_g = [&](int tile, int buf) {  // 64 DMA instructions per tile, J = wave + 12 i
+  auto load_g = [&](int tl, int buf) {  // 64 DMA instructions per tile
 #pragma unroll
     for (int i = 0; i < 6; ++i) {
       const int J = wave + kCW * i;
@@ -364,38 +395,35 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
         const int p = J * 64 + lane;
         const int slot = p >> 5, pos = p & 31;
         const int c = pos ^ swz8(slot);
-        const int gs = min(tile * kCT + slot, K - 1);
-        __builtin_amdgcn_global_load_lds((const void*)(grow + (int64_t)gs * kGW + c * 8),
-                                         (__attribute__((address_space(3))) void*)&lds[buf * kGTChunks + J * 64], 16,
-                                         0, 0);
+        const int gs = min(tl * kCT + slot, K - 1);
+        dma16_to_lds(grow, (uint32_t)(gs * kGW + c * 8) * 2u,
+                     (uint32_t)(uintptr_t)&lds[buf * kGTChunks + J * 64]);
       }
     }
   };
   load_g(0, 0);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int buf = tile & 1;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // G tile landed for every wave; the other buffer is free
-    if (tile + 1 < ntiles) load_g(tile + 1, buf ^ 1);
-    const uint32_t gb = lds_base + buf * (kGTChunks * 16);
+  for (int tl = 0; tl < ntiles; ++tl) {
+    const int buf = tl & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of tile tl landed
+    __syncthreads();  // every wave's part landed; the other buffer is free
+    if (tl + 1 < ntiles) load_g(tl + 1, buf ^ 1);
+    const lds_char* gb = lb + buf * (kGTChunks * 16);
     for (int st = 0; st < kCT / 16; ++st) {
+      if (tl * kCT + 16 * st >= nslots) break;  // wave-uniform
       const int sl = 16 * st + col;  // B operand row (slot) of this lane
-      const int slot = tile * kCT + sl;
-      if (tile * kCT + 16 * st >= nslots) break;  // wave-uniform
+      const int slot = tl * kCT + sl;
+      const lds_char* grow_l = gb + 16 * (sl * 32);
+      const int sw = swz8(sl);
+      u32x4 bg[kKSteps];
+#pragma unroll
+      for (int ks = 0; ks < kKSteps; ++ks) bg[ks] = lds_read16(grow_l + 16 * ((4 * ks + g) ^ sw));
       f32x4 acc[3];
 #pragma unroll
       for (int t = 0; t < 3; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        if (ks >= ksteps) continue;  // block-uniform
-        const u32x4 bg = *(const lds_u32x4*)(uintptr_t)(gb + 16 * (sl * 32 + ((4 * ks + g) ^ swz8(sl))));
-        const bool dO_rows = (ks & 2) != 0;  // k = 128 hg + 64 type + i: type 1 when bit 6 of k set
+      for (int ks = 0; ks < kKSteps; ++ks)
 #pragma unroll
-        for (int t = 0; t < 3; ++t) {
-          if (dO_rows && 48 * wave + 16 * t >= kDv) continue;  // dO has no rope columns
-          acc[t] = mfma16x16x32(as_bf16x8(xa[t][ks]), as_bf16x8(bg), acc[t]);
-        }
-      }
+        for (int t = 0; t < 3; ++t) acc[t] = mfma16x16x32(as_bf16x8(xa[t][ks]), as_bf16x8(bg[ks]), acc[t]);
       if (slot < nslots) {  // lane (slot, g) holds columns 48w + 16t + 4g + r
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
@@ -470,12 +498,15 @@ bwd_exact_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, 
 
 struct BwdPlan {
   int64_t rows;  // query rows per chunk
-  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, total;
+  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, mass_bytes, total;
 };
 
+// Scratch per chunk: G and C (bf16), the CSR pair list and offsets, and the per-head-group
+// mass partials (fp32, summed into the caller's mass after each chunk).
 BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget) {
   BwdPlan p{};
-  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4);
+  const int64_t mass_groups = kHeadsMax / kHG;
+  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4 + 4 * mass_groups);
   int64_t rows = s_q;
   if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
   p.rows = rows;
@@ -483,9 +514,24 @@ BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t
   p.c_bytes = batch * rows * topk * kDqk * 2;
   p.pairs_bytes = rows * topk * 4;
   p.csr_bytes = (3 * (s_kv + 1)) * 4;
+  p.mass_bytes = mass_groups * batch * rows * topk * 4;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes);
+  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + al(p.mass_bytes);
   return p;
+}
+
+// mass[b, r0 + lr, :] = sum over head groups of the chunk's partials
+__global__ void __launch_bounds__(256)
+mass_combine_kernel(const float* __restrict__ part, float* __restrict__ mass, int groups, int64_t hg_stride,
+                    int64_t row_elems, int S, int r0, int rows, int K) {
+  const int64_t n = row_elems;  // batch * rows * K
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
+    float acc = part[i];
+    for (int hgi = 1; hgi < groups; ++hgi) acc += part[hgi * hg_stride + i];
+    const int64_t b = i / ((int64_t)rows * K);
+    const int64_t rem = i - b * (int64_t)rows * K;
+    mass[(b * S + r0) * (int64_t)K + rem] = acc;
+  }
 }
 
 constexpr int64_t kDefaultBudget = 16LL << 30;  // scratch for the G / C chunks
@@ -503,7 +549,8 @@ extern "C" int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q,
 
 extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out,
                                   const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
-                                  float* dkv_accum, void* workspace, int64_t workspace_bytes, int dtype, int64_t batch,
+                                  float* dkv_accum, float* mass, void* workspace, int64_t workspace_bytes, int dtype,
+                                  int64_t batch,
                                   int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
                                   int64_t topk, float scale, int64_t q_offset, void* stream) {
   using namespace dsa;
@@ -515,6 +562,8 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
     return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: sizes out of range");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DSA_F32) {
+    if (mass) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: the fp32 path has no mass output "
+                               "(use dsa_attn_mass)");
     if (topk * 4 > 64 * 1024) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: fp32 topk <= 16384");
     if (s_q > 2147483647LL || n_heads > 65535)
       return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: sizes out of range");
@@ -528,6 +577,8 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
   if (d_qk != kDqk || d_v != kDv)
     return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: bf16 path needs d_qk=576, d_v=512");
   if (n_heads > kHeadsMax) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: bf16 path needs H <= 128");
+  if (s_kv > GatherGeom::kMaxRows)
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: S_kv > %lld", (long long)GatherGeom::kMaxRows);
   if (!workspace) return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: workspace required");
   // choose the largest chunk whose scratch fits the given workspace
   BwdPlan plan = plan_bwd(batch, s_q, s_kv, topk, workspace_bytes);
@@ -541,18 +592,46 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
   uint16_t* cbuf = (uint16_t*)(ws + al(plan.g_bytes));
   int* pairs = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes));
   int* counts = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes));
+  float* mpart = (float*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes) + al(plan.csr_bytes));
   const unsigned hgroups = ceil_div(n_heads, kHG);
 
   for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
     const int rows = (int)std::min<int64_t>(plan.rows, s_q - r0);
     dim3 ga((unsigned)rows, hgroups, (unsigned)batch);
+    // mass: one head group writes the caller's rows directly; several write partials
+    float* mb = nullptr;
+    int64_t m_hg = 0, m_b = 0;
+    int m_row = 0;
+    if (mass && hgroups == 1) {
+      mb = mass;
+      m_b = s_q * topk;
+      m_row = (int)r0;
+    } else if (mass) {
+      mb = mpart;
+      m_hg = batch * rows * topk;
+      m_b = (int64_t)rows * topk;
+    }
     bwd_dq_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)out,
-                                      (const uint16_t*)dout, softmax_max, softmax_sum, (uint16_t*)dq, gbuf, (int)s_q,
-                                      (int)s_kv, (int)n_heads, (int)topk, scale, q_offset, (int)r0);
+                                      (const uint16_t*)dout, softmax_max, softmax_sum, (uint16_t*)dq, gbuf, mb, m_hg,
+                                      m_b, m_row, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale, q_offset,
+                                      (int)r0);
     if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
+    if (mass && hgroups > 1) {
+      const int64_t n = batch * rows * topk;
+      const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 65535);
+      mass_combine_kernel<<<blocks, 256, 0, st>>>(mpart, mass, (int)hgroups, m_hg, n, (int)s_q, (int)r0, rows,
+                                                  (int)topk);
+      if (int rc = check_launch("dsa_sparse_mla_bwd(mass)")) return rc;
+    }
     dim3 gb((unsigned)rows, (unsigned)batch);
-    bwd_contrib_kernel<<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf, (int)s_q,
-                                           (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0, rows);
+    if (hgroups == 1)
+      bwd_contrib_kernel<1><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf,
+                                                      (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0,
+                                                      rows);
+    else
+      bwd_contrib_kernel<2><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf,
+                                                      (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0,
+                                                      rows);
     if (int rc = check_launch("dsa_sparse_mla_bwd(contrib)")) return rc;
     for (int b = 0; b < (int)batch; ++b)
       if (int rc = csr_reduce(indices, cbuf, dkv_accum, pairs, counts, (int)s_q, (int)s_kv, (int)topk, q_offset,

@@ -194,8 +194,11 @@ def sparse_mla_fwd(q, kv, indices, scale, *, d_v=512, q_offset=0):
     return out, smax, ssum
 
 
-def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, workspace_bytes=None):
-    """(dq like q, dkv fp32 [B,S_kv,D_qk]) from dsa_sparse_mla_bwd.
+def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, workspace_bytes=None,
+                   return_mass=False):
+    """(dq like q, dkv fp32 [B,S_kv,D_qk]) from dsa_sparse_mla_bwd, plus the head-summed
+    attention mass [B,S,K] fp32 when ``return_mass`` (bf16 path; the same quantity as
+    ``attn_mass``, taken from the probabilities the backward recomputes anyway).
 
     ``workspace_bytes`` caps the scratch (fewer bytes -> more query-row chunks).
     """
@@ -208,17 +211,18 @@ def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, 
     indices = indices.reshape(B, S, K).to(torch.int32).contiguous()
     dq = torch.empty_like(q)
     dkv = torch.zeros(B, s_kv, D, dtype=torch.float32, device=q.device)
+    mass = torch.empty(B, S, K, dtype=torch.float32, device=q.device) if return_mass else None
     ws_bytes = int(lib.dsa_sparse_mla_bwd_workspace_size(B, S, s_kv, H, D, K))
     if workspace_bytes is not None:
         ws_bytes = int(workspace_bytes)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     check(
         lib.dsa_sparse_mla_bwd(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax), ptr(ssum), ptr(dq),
-                               ptr(dkv), ptr(ws), ws_bytes, _lib.dtype_code(q.dtype), B, S, s_kv, H, D, d_v, K,
-                               float(scale), int(q_offset), stream_of(q.device)),
+                               ptr(dkv), ptr(mass), ptr(ws), ws_bytes, _lib.dtype_code(q.dtype), B, S, s_kv, H, D, d_v,
+                               K, float(scale), int(q_offset), stream_of(q.device)),
         "dsa_sparse_mla_bwd",
     )
-    return dq, dkv
+    return (dq, dkv, mass) if return_mass else (dq, dkv)
 
 
 def attn_mass(q, kv, indices, smax, ssum, scale, *, q_offset=0):
