@@ -63,6 +63,26 @@ __device__ __forceinline__ u32x4 lds_read_tr_pair(const lds_char* p1, const lds_
   return (u32x4){w1[0], w1[1], w2[0], w2[1]};
 }
 
+// exchanges with the lane 16 / 32 apart without the LDS path (gfx950 v_permlane*_swap):
+// the swap returns (own, partner) in some order, so a commutative op of the pair is the
+// xor-reduction step
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // wave-level helpers (64-wide)
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
@@ -77,11 +97,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// LDS row swizzle for tiles whose rows are a multiple of 128 B apart: 16-byte chunk c of
-// row r lives at chunk c ^ swz8(r).  swz8 maps any 8 consecutive rows to distinct values
-// (8-lane b128 reads of one column are conflict-free) and rows 4k..4k+3 to distinct even
-// values (a 4-row x 32-byte transposed read covers all banks once).
+// LDS chunk swizzles.  gfx950's LDS has 64 banks of 4 bytes (256 B per clock): a b128
+// read is served 16 lanes per clock and a b64 read 32 lanes per clock, and each of those
+// lane groups must cover distinct banks.
+//
+// swz8: 16-byte chunk c of row r lives at chunk c ^ swz8(r); any 8 consecutive rows get
+// distinct values (rows whose stride is a multiple of 256 B, read 8 rows at a time).
 __device__ __forceinline__ int swz8(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// swz_kv: for tiles of 1152-byte latent-KV rows (72 chunks; a row starts on bank 0 or 32
+// by parity).  Over any 16 consecutive rows each parity class takes all 8 values (b128
+// reads of one chunk column by 16 rows), and over any 8 aligned rows each parity class
+// has distinct value pairs (swz_kv >> 1), which is what the transposed b64 reads of two
+// chunks x 4 rows per 16 lanes need.  Values are < 8, so XOR keeps a chunk inside its
+// aligned group of 8.
+__device__ __forceinline__ int swz_kv(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
+// swz16: for rows whose stride is a multiple of 256 B with >= 16 chunks: 16 consecutive
+// rows reading one chunk column hit 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int swz16(int r) { return r & 15; }
 
 // 16-byte-per-lane DMA from global memory straight into LDS (global_load_lds_dwordx4):
 // lane i reads gbase + voff and writes LDS byte lds_base + 16 i.  gbase and lds_base must

@@ -1,9 +1,9 @@
 // Gathered KV-row pipeline shared by the sparse-attention kernels (gfx950).
 //
 // A block is kBN = 32 selected latent-KV rows of 576 bf16 (1152 B).  Its LDS tile holds
-// the rows row-major with 16-byte chunk c of row r at chunk c ^ swz8(r), and is filled by
+// the rows row-major with 16-byte chunk c of row r at chunk c ^ swz_kv(r), and is filled by
 // 36 wave-wide DMA instructions (global_load_lds, 16 B per lane): instruction J covers
-// tile positions [64J, 64J+64), position p = r*72 + (c ^ swz8(r)); wave w issues
+// tile positions [64J, 64J+64), position p = r*72 + (c ^ swz_kv(r)); wave w issues
 // J = w, w + W, ...  Unused slots (-1, past the causal limit, past K) load row 0 and are
 // masked by the block's validity bits.
 //
@@ -66,7 +66,7 @@ struct RowGather {
       const int p = J * 64 + lane;
       const int row = p / G::kRowChunks, pos = p - row * G::kRowChunks;
       L.row[i] = row;
-      L.cbyte[i] = (uint32_t)((pos ^ swz8(row)) * 16);
+      L.cbyte[i] = (uint32_t)((pos ^ swz_kv(row)) * 16);
     }
     return L;
   }
@@ -95,6 +95,30 @@ struct RowGather {
       const uint64_t bal = __ballot(ok);
       if (lane == 0) *vmask_slot = (uint32_t)bal;
     }
+  }
+
+  // split form of issue(): prep() resolves the wave's row offsets (and wave 0's validity
+  // bits) for block `blk`; issue_one(i) then sends the wave's i-th instruction, so a
+  // kernel can spread the DMA over its compute instead of stalling on a burst
+  static __device__ __forceinline__ void prep(uint32_t* vmask_slot, const int* sidx, int blk, int K, uint32_t lim,
+                                              int wave, int lane, const Lanes& L, uint32_t (&off)[kMaxPerWave]) {
+    const int rows_left = K - blk * G::kBN;
+#pragma unroll
+    for (int i = 0; i < kMaxPerWave; ++i) {
+      const uint32_t raw = (uint32_t)sidx[L.row[i]];
+      const bool ok = raw <= lim && L.row[i] < rows_left;
+      off[i] = (ok ? raw : 0u) * (uint32_t)G::kRowBytes + L.cbyte[i];
+    }
+    if (wave == 0) {
+      const bool ok = lane < G::kBN && lane < rows_left && (uint32_t)sidx[lane & (G::kBN - 1)] <= lim;
+      const uint64_t bal = __ballot(ok);
+      if (lane == 0) *vmask_slot = (uint32_t)bal;
+    }
+  }
+  static __device__ __forceinline__ void issue_one(const uint16_t* kvb, u32x4* tile, int i, int wave,
+                                                   const uint32_t (&off)[kMaxPerWave]) {
+    const int J = wave + kWaves * i;
+    if (J < G::kTileInstr) dma16_to_lds(kvb, off[i], (uint32_t)(uintptr_t)&tile[J * 64]);
   }
 
   // wave 0: DMA the slot indices of block `blk` (clamped to K) into ring entry `ring`

@@ -133,15 +133,13 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
       for (int r = 0; r < 4; ++r)
         part += bf16_lo(db[c][r]) * bf16_lo(ov[r]) + bf16_hi(db[c][r]) * bf16_hi(ov[r]);
     }
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
-    delta = part;
+    delta = xor32_sum(xor16_sum(part));
     const float mx = head_ok ? smax[hrow] : 0.f, sm = head_ok ? ssum[hrow] : 0.f;
     lse2 = (sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0 (absent head / no key)
   }
   const float scale_log2 = scale * kLog2e;
 
-  // LDS offsets.  A operand of S^T / dP^T: key row 16kt + col, chunk 4c + g (XOR swz8(row)).
+  // LDS offsets.  A operand of S^T / dP^T: key row 16kt + col, chunk 4c + g (XOR swz_kv(row)).
   // With c = 2u + c0 the XOR touches only bits 0..2 of 4c + g -> ka_off[kt][c0] + 128 u.
   uint32_t ka_off[2][2];
 #pragma unroll
@@ -149,12 +147,12 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
     for (int c0 = 0; c0 < 2; ++c0) {
       const int row = 16 * kt + col;
-      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ swz8(row));
+      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ swz_kv(row));
     }
   // Transposed K reads for dQ^T += K^T dS^T: group g, source lane col supplies key row
   // 4g + col/4 (+16 for the second read), d columns 16dt + 4(col%4) -> chunk 2dt + (col%4)/2.
   const int tr_row = 4 * g + (col >> 2);
-  const int tr_x = swz8(tr_row);
+  const int tr_x = swz_kv(tr_row);
   const int tr_c0 = (col & 3) >> 1;
   uint32_t tr_off[4];  // dt = 4u + d0 -> chunk (8u + 2 d0 + tr_c0) ^ tr_x = 8u + ((2 d0 + tr_c0) ^ tr_x)
 #pragma unroll
@@ -208,25 +206,28 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 
     // S^T and dP^T: operands read in batches of 6 ahead of their MFMAs (the sched_barrier
     // keeps the batch together so its LDS latency overlaps the previous batch's MFMAs)
+    // four independent accumulation chains (S and dP for two key tiles)
     f32x4 sacc[2], pacc[2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      sacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      pacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < 2; ++kt) sacc[kt] = pacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int cb = 0; cb < kDqk / 32; cb += 6) {
-        u32x4 a[6];
+    for (int cb = 0; cb < kDqk / 32; cb += 3) {
+      u32x4 a[2][3];
 #pragma unroll
-        for (int u = 0; u < 6; ++u) {
+      for (int u = 0; u < 3; ++u)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
           const int c = cb + u;
-          a[u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
+          a[kt][u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
         }
-        __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < 6; ++u) {
-          const int c = cb + u;
-          sacc[kt] = mfma16x16x32(as_bf16x8(a[u]), as_bf16x8(qb[c]), sacc[kt]);
-          if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a[u]), as_bf16x8(db[c]), pacc[kt]);
+      for (int u = 0; u < 3; ++u) {
+        const int c = cb + u;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          sacc[kt] = mfma16x16x32(as_bf16x8(a[kt][u]), as_bf16x8(qb[c]), sacc[kt]);
+          if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a[kt][u]), as_bf16x8(db[c]), pacc[kt]);
         }
       }
     }
@@ -385,7 +386,7 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
 
   // ---- stream G tiles; C^T[16 cols x 16 slots] = X^T[16 cols x 256] . G^T[256 x 16 slots] ----
   // per-lane DMA geometry: instruction J = wave + 12 i covers tile chunks [64J, 64J+64),
-  // chunk p = slot*32 + (c ^ swz8(slot))
+  // chunk p = slot*32 + (c ^ swz16(slot))
   const int ntiles = (nslots + kCT - 1) / kCT;
   auto load_g = [&](int tl, int buf) {  // 64 DMA instructions per tile
 #pragma unroll
@@ -394,7 +395,7 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
       if (J < kGTChunks / 64) {
         const int p = J * 64 + lane;
         const int slot = p >> 5, pos = p & 31;
-        const int c = pos ^ swz8(slot);
+        const int c = pos ^ swz16(slot);
         const int gs = min(tl * kCT + slot, K - 1);
         dma16_to_lds(grow, (uint32_t)(gs * kGW + c * 8) * 2u,
                      (uint32_t)(uintptr_t)&lds[buf * kGTChunks + J * 64]);
@@ -413,7 +414,7 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
       const int sl = 16 * st + col;  // B operand row (slot) of this lane
       const int slot = tl * kCT + sl;
       const lds_char* grow_l = gb + 16 * (sl * 32);
-      const int sw = swz8(sl);
+      const int sw = swz16(sl);
       u32x4 bg[kKSteps];
 #pragma unroll
       for (int ks = 0; ks < kKSteps; ++ks) bg[ks] = lds_read16(grow_l + 16 * ((4 * ks + g) ^ sw));

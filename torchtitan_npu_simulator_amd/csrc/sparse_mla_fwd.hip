@@ -1,23 +1,24 @@
 // Gathered sparse MLA attention forward for gfx950.
 //
-// One workgroup = one query token x a group of 64 heads, 4 waves (one per SIMD, each with
-// the whole 512-register file).  The token's selected latent-KV rows (576 bf16 = 1152 B
-// each) are gathered in blocks of 32 by DMA (global_load_lds) into a swizzled,
-// triple-buffered LDS tile that the group's heads share.  The workgroups of one token's
-// head groups are numbered 8 apart, so they land on the same XCD and the second gather
-// of a row is an L2 hit.  Wave w owns heads 16w..16w+15 of its group over the whole
-// contraction, on v_mfma_f32_16x16x32_bf16:
-//   * QK: S^T[32 keys x 16 heads] (two 16-key tiles) over 18 k-steps of 32 columns; Q of
-//     the wave's heads stays in 72 VGPRs for the whole token, K rows are the A operand
-//     read from LDS in batches ahead of their MFMAs;
+// One workgroup = one query token x up to 128 heads, 4 waves (one per SIMD, each with the
+// whole 512-register file).  The token's selected latent-KV rows (576 bf16 = 1152 B each)
+// are gathered in blocks of 32 by DMA (global_load_lds) into a swizzled, triple-buffered
+// LDS tile shared by all heads, so each row crosses L2 once per token.  Wave w owns heads
+// 32w .. 32w+31 as two 16-head sub-groups over the whole contraction, on
+// v_mfma_f32_16x16x32_bf16, and every LDS operand it reads feeds both sub-groups:
+//   * QK: S^T[32 keys x 16 heads] per sub-group over 18 k-steps of 32 columns; latent Q
+//     of the wave's heads stays in 128 VGPRs for the whole token, rope Q in LDS; K rows
+//     are the A operand, read one batch ahead of their MFMAs;
 //   * softmax per head in the exp2 domain against a reference max fixed by the first
 //     valid block: no per-block O rescale (P may reach 2^64, well inside the fp32/bf16
 //     exponent range).  A row whose later logits outgrow that headroom is flagged with a
 //     negative softmax_sum and recomputed exactly by the fixup pass;
-//   * PV: O^T[512 dv x 16 heads] += V^T . P^T, 32 MFMAs of k = 32 keys, V read transposed
-//     by ds_read_b64_tr_b16 straight from the row-major K tile (k_nope == v); the key
-//     order inside the k dimension is the S^T tile order (4g+r, 16+4g+r) on both operands.
-// No cross-wave exchange: one barrier per block, for the tile hand-off.
+//   * PV: O^T[512 dv x 16 heads] += V^T . P^T per sub-group, V read transposed by
+//     ds_read_b64_tr_b16 straight from the row-major K tile (k_nope == v); the key order
+//     inside the k dimension is the S^T tile order (4g+r, 16+4g+r) on both operands.
+//     O (2 x 128 fp32 per lane) lives in the accumulation registers.
+// LDS traffic per token and block is 4 waves x (QK + PV) tile reads; one barrier per
+// block, for the tile hand-off.
 #include "dsa_common.h"
 #include "dsa_gather.h"
 
@@ -35,11 +36,11 @@ constexpr int kTileBytes = kTileChunks * 16;   // 36864
 constexpr float kHeadroom = 64.0f;             // log2 units of P above the reference max
 constexpr int kFwdWaves = 4;
 constexpr int kFwdThreads = kFwdWaves * 64;
-constexpr int kFwdHeads = 16 * kFwdWaves;      // heads per workgroup (one head group)
-constexpr int kXcds = 8;                       // workgroups are dealt round-robin to 8 XCDs
+constexpr int kFwdHeads = 32 * kFwdWaves;      // heads per workgroup
 constexpr int kKSteps = kDqk / 32;             // 18 MFMA k-steps of 32 columns
-constexpr int kQBatch = 6;                     // A-operand LDS reads issued ahead of their MFMAs
-constexpr int kVBatch = 8;                     // transposed V reads issued ahead of their MFMAs
+constexpr int kLatSteps = kDv / 32;            // 16 latent k-steps (Q in registers)
+constexpr int kQBatch = 2;                     // k-steps whose A operands are read a batch ahead
+constexpr int kVBatch = 2;                     // dv tiles whose V reads are issued a batch ahead
 // mass kernel (8 waves: 4 head groups x 2 contraction halves, 32x32x16 tiles)
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
@@ -53,16 +54,6 @@ __device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-__device__ __forceinline__ u32x4 tr_read_pair(uint32_t a1, uint32_t a2) {
-  const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)(a1));
-  const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)(a2));
-  u32x4 av;
-  av[0] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
-  av[1] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
-  av[2] = (uint32_t)(uint16_t)v2[0] | ((uint32_t)(uint16_t)v2[1] << 16);
-  av[3] = (uint32_t)(uint16_t)v2[2] | ((uint32_t)(uint16_t)v2[3] << 16);
-  return av;
-}
 
 // number of 32-slot blocks up to the last usable slot of a row (block-wide; needs sync)
 __device__ int fwd_count_blocks(const int32_t* ridx, int K, int s_kv, int64_t limit, int* sh_last) {
@@ -82,55 +73,68 @@ __global__ void __launch_bounds__(kFwdThreads, 1)
 sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv,
                            const int32_t* __restrict__ idx, uint16_t* __restrict__ out, float* __restrict__ smax,
                            float* __restrict__ ssum, int S, int s_kv, int H, int K, float scale_log2,
-                           int64_t q_offset, int hgroups) {
+                           int64_t q_offset) {
   using Gather = RowGather<kFwdWaves>;
   __shared__ u32x4 tile[3][kTileChunks];
+  __shared__ u32x4 qpe[kFwdHeads][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
   __shared__ uint32_t vmask[3];
   __shared__ int sh_last;
 
-  // linear id -> (token, head group): ids i and i + 8 (same XCD) share a token
-  const int lin = blockIdx.x;
-  const int span = kXcds * hgroups;
-  const int tok = (lin / span) * kXcds + lin % kXcds;
-  const int hgi = (lin / kXcds) % hgroups;
-  if (tok >= S) return;
-  const int b = blockIdx.z, tid = threadIdx.x;
+  const int tok = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, col = lane & 15, g = lane >> 4;
-  const int head = hgi * kFwdHeads + wave * 16 + col;
-  const bool head_ok = head < H;
+  const int head0 = blockIdx.y * kFwdHeads + wave * 32 + col;  // sub-group hg: head0 + 16 hg
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
-  const int64_t out_row = row_id * H + (head_ok ? head : 0);
+  bool hok[2];
+  int64_t orow[2];
+#pragma unroll
+  for (int hg = 0; hg < 2; ++hg) {
+    hok[hg] = head0 + 16 * hg < H;
+    orow[hg] = row_id * H + (hok[hg] ? head0 + 16 * hg : 0);
+  }
 
   const int nblk = fwd_count_blocks(ridx, K, s_kv, limit, &sh_last);
   if (nblk == 0) {
-    if (head_ok) {
-      uint32_t* o32 = reinterpret_cast<uint32_t*>(out + out_row * kDv);
+#pragma unroll
+    for (int hg = 0; hg < 2; ++hg) {
+      if (!hok[hg]) continue;
+      uint32_t* o32 = reinterpret_cast<uint32_t*>(out + orow[hg] * kDv);
       for (int i = g; i < kDv / 2; i += 4) o32[i] = 0u;
       if (g == 0) {
-        smax[out_row] = -INFINITY;
-        ssum[out_row] = 0.f;
+        smax[orow[hg]] = -INFINITY;
+        ssum[orow[hg]] = 0.f;
       }
     }
     return;
   }
   const uint32_t lim = gather_limit(limit, s_kv);
 
-  // ---- Q of head `col`: qb[c] = q[32c + 8g .. +8] (B operand of S^T = K Q^T) ----
-  u32x4 qb[kKSteps];
-  {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + out_row * kDqk);
+  // ---- Q: latent qb[hg][c] = q[32c + 8g .. +8] of head head0 + 16hg in VGPRs (B operand
+  // of S^T = K Q^T); rope columns into LDS ----
+  u32x4 qb[2][kLatSteps];
 #pragma unroll
-    for (int c = 0; c < kKSteps; ++c) qb[c] = head_ok ? qh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
+  for (int hg = 0; hg < 2; ++hg) {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + orow[hg] * kDqk);
 #pragma unroll
-    for (int c = 0; c < kKSteps; ++c) asm volatile("" : "+v"(qb[c]));  // landed before any DMA
+    for (int c = 0; c < kLatSteps; ++c) qb[hg][c] = hok[hg] ? qh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
+    // rope: chunks 64..71 of the row; lane g writes chunks 2g, 2g+1 of its head
+    const int hl = wave * 32 + 16 * hg + col;  // head within the workgroup
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int ch = 2 * g + j;
+      qpe[hl][ch ^ ((hl >> 1) & 7)] = hok[hg] ? qh[64 + ch] : (u32x4){0u, 0u, 0u, 0u};
+    }
   }
+#pragma unroll
+  for (int hg = 0; hg < 2; ++hg)
+#pragma unroll
+    for (int c = 0; c < kLatSteps; ++c) asm volatile("" : "+v"(qb[hg][c]));  // landed before any DMA
 
   // ---- LDS byte offsets ----
-  // A operand of S^T: key row 16kt + col, chunk (4c + g) ^ swz8(row); with c = 2u + c0 the
+  // A operand of S^T: key row 16kt + col, chunk (4c + g) ^ swz_kv(row); with c = 2u + c0 the
   // XOR only touches bits 0..2, so offset = ka_off[kt][c0] + 128 u.
   uint32_t ka_off[2][2];
 #pragma unroll
@@ -138,27 +142,39 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
 #pragma unroll
     for (int c0 = 0; c0 < 2; ++c0) {
       const int row = 16 * kt + col;
-      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ swz8(row));
+      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ swz_kv(row));
     }
+  // rope B operand of sub-group hg, step 16 + e: head row hl, chunk (4e + g) ^ ((hl >> 1) & 7)
+  const lds_char* qpe_b = lds_bytes(&qpe[0][0]);
+  uint32_t qpe_off[2][2];
+#pragma unroll
+  for (int hg = 0; hg < 2; ++hg) {
+    const int hl = wave * 32 + 16 * hg + col;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) qpe_off[hg][e] = hl * 128 + 16 * ((4 * e + g) ^ ((hl >> 1) & 7));
+  }
   // Transposed V reads for O^T += V^T P^T: group g, source lane col supplies key row
   // 4g + col/4 (+16 for the second read), dv columns 16dt + 4(col%4) -> chunk
   // 2dt + (col%4)/2; with dt = 4u + d0: tr_off[d0] + 128 u.
   const int tr_row = 4 * g + (col >> 2);
-  const int tr_x = swz8(tr_row);
+  const int tr_x = swz_kv(tr_row);
   const int tr_c0 = (col & 3) >> 1;
   uint32_t tr_off[4];
 #pragma unroll
   for (int d0 = 0; d0 < 4; ++d0) tr_off[d0] = tr_row * kRowBytes + 16 * ((2 * d0 + tr_c0) ^ tr_x) + 8 * (col & 1);
 
-  f32x4 o[kDv / 16];
+  f32x4 o[2][kDv / 16];
 #pragma unroll
-  for (int t = 0; t < kDv / 16; ++t) o[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_ref = -INFINITY, m_true = -INFINITY, lsum = 0.f;
-  bool clamped = false;
+  for (int hg = 0; hg < 2; ++hg)
+#pragma unroll
+    for (int t = 0; t < kDv / 16; ++t) o[hg][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m_ref[2] = {-INFINITY, -INFINITY}, m_true[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
+  bool clamped[2] = {false, false};
 
   const typename Gather::Lanes gl = Gather::lanes(wave, lane);
+  static_assert(kKSteps / kQBatch >= Gather::kMaxPerWave, "one row DMA per QK batch");
   Gather::ring_init(sidx, ridx, K, nblk, wave, lane);
-  __syncthreads();
+  __syncthreads();  // also publishes qpe
   Gather::issue(kvb, tile[0], &vmask[0], sidx[0], 0, K, lim, wave, lane, gl);
   if (nblk > 1) Gather::issue(kvb, tile[1], &vmask[1], sidx[1], 1, K, lim, wave, lane, gl);
   Gather::wait_next(nblk > 1, wave);  // block 0 landed
@@ -169,99 +185,130 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
     const bool in_flight2 = blk + 2 < nblk;
     if (wave == 0 && blk + 3 < nblk)
       Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
-    if (in_flight2) {
-      const int nb = (blk + 2) % 3;
-      Gather::issue(kvb, tile[nb], &vmask[nb], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl);
-    }
+    // block blk+2's rows: offsets resolved now, one DMA instruction per QK batch below
+    const int nbuf = (blk + 2) % 3;
+    uint32_t doff[Gather::kMaxPerWave];
+    if (in_flight2)
+      Gather::prep(&vmask[nbuf], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl, doff);
     const lds_char* tb = lds_bytes(&tile[buf][0]);
 
-    // ---- S^T (two 16-key tiles) over the full contraction; A operands fetched in batches
-    // ahead of their MFMAs (sched_barrier keeps a batch together so its LDS latency
-    // overlaps the previous batch's MFMAs) ----
-    f32x4 sacc[2];
+    // ---- S^T for both sub-groups; every A operand (2 key tiles) feeds both ----
+    f32x4 sacc[2][2];  // [hg][kt]
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      sacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int hg = 0; hg < 2; ++hg) sacc[hg][0] = sacc[hg][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    constexpr int kQB = kKSteps / kQBatch;
+    u32x4 a[2][2][kQBatch];  // [buffer][kt][u]
+    auto read_a = [&](u32x4 (&dst)[2][kQBatch], int cb) {
 #pragma unroll
-      for (int cb = 0; cb < kKSteps; cb += kQBatch) {
-        u32x4 a[kQBatch];
+      for (int u = 0; u < kQBatch; ++u)
 #pragma unroll
-        for (int u = 0; u < kQBatch; ++u) {
+        for (int kt = 0; kt < 2; ++kt) {
           const int c = cb + u;
-          a[u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
+          dst[kt][u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
         }
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    read_a(a[0], 0);
 #pragma unroll
-        for (int u = 0; u < kQBatch; ++u) sacc[kt] = mfma16x16x32(as_bf16x8(a[u]), as_bf16x8(qb[cb + u]), sacc[kt]);
+    for (int nb = 0; nb < kQB; ++nb) {
+      if (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
+      if (in_flight2 && nb < Gather::kMaxPerWave) Gather::issue_one(kvb, tile[nbuf], nb, wave, doff);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kQBatch; ++u) {
+        const int c = nb * kQBatch + u;
+#pragma unroll
+        for (int hg = 0; hg < 2; ++hg) {
+          // rope steps read their B operand from LDS (registers hold the latent part only)
+          const u32x4 bq = c < kLatSteps ? qb[hg][c] : lds_read16(qpe_b + qpe_off[hg][c - kLatSteps]);
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+            sacc[hg][kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(bq), sacc[hg][kt]);
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-
-    // ---- mask, scale, block max (lane holds keys 16kt + 4g + r of head col) ----
-    const uint32_t vmg = vmask[buf] >> (4 * g);  // bit r: key 4g + r, bit 16 + r: key 16 + 4g + r
-    float x[8];
-    float rmax = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float v = ((vmg >> (16 * kt + r)) & 1u) ? sacc[kt][r] * scale_log2 : -INFINITY;
-        x[4 * kt + r] = v;
-        rmax = fmaxf(rmax, v);
-      }
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 16, 64));
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
-    // (a block with no valid slot leaves every x at -inf and contributes exact zeros)
-    m_true = fmaxf(m_true, rmax);
-    if (m_ref == -INFINITY) m_ref = rmax;  // first block with a valid key fixes the reference
-    clamped |= rmax > m_ref + kHeadroom;
-    // while no key has been seen every x is -inf; subtracting 0 then keeps exp2 at 0
-    const float mr = m_ref == -INFINITY ? 0.f : m_ref;
-    float pp[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) pp[j] = __builtin_amdgcn_exp2f(fminf(x[j] - mr, kHeadroom));
-    lsum += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
-    // B operand P^T: k-slot 8g + t <-> key (t < 4 ? 4g + t : 16 + 4g + t - 4)
-    u32x4 bp;
-    bp[0] = pack_bf16x2(pp[0], pp[1]);
-    bp[1] = pack_bf16x2(pp[2], pp[3]);
-    bp[2] = pack_bf16x2(pp[4], pp[5]);
-    bp[3] = pack_bf16x2(pp[6], pp[7]);
-
-    // ---- O^T += V^T . P^T : 32 dv tiles of 16 ----
-#pragma unroll
-    for (int db = 0; db < kDv / 16; db += kVBatch) {
-      u32x4 av[kVBatch];
+    // the first V operands are requested before the softmax
+    constexpr int kVB = (kDv / 16) / kVBatch;
+    u32x4 av[2][kVBatch];
+    auto read_v = [&](u32x4 (&dst)[kVBatch], int db) {
 #pragma unroll
       for (int u = 0; u < kVBatch; ++u) {
         const int dt = db + u;
         const lds_char* a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
-        av[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
+        dst[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
       }
+    };
+    read_v(av[0], 0);
+
+    // ---- mask, scale, per-head block max and P (lane holds keys 16kt + 4g + r) ----
+    const uint32_t vmg = vmask[buf] >> (4 * g);  // bit r: key 4g + r, bit 16 + r: key 16 + 4g + r
+    u32x4 bp[2];
+#pragma unroll
+    for (int hg = 0; hg < 2; ++hg) {
+      float x[8];
+      float rmax = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = ((vmg >> (16 * kt + r)) & 1u) ? sacc[hg][kt][r] * scale_log2 : -INFINITY;
+          x[4 * kt + r] = v;
+          rmax = fmaxf(rmax, v);
+        }
+      rmax = xor32_max(xor16_max(rmax));
+      // (a block with no valid slot leaves every x at -inf and contributes exact zeros)
+      m_true[hg] = fmaxf(m_true[hg], rmax);
+      if (m_ref[hg] == -INFINITY) m_ref[hg] = rmax;  // first block with a valid key fixes the reference
+      clamped[hg] |= rmax > m_ref[hg] + kHeadroom;
+      // while no key has been seen every x is -inf; subtracting 0 then keeps exp2 at 0
+      const float mr = m_ref[hg] == -INFINITY ? 0.f : m_ref[hg];
+      float pp[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pp[j] = __builtin_amdgcn_exp2f(fminf(x[j] - mr, kHeadroom));
+      lsum[hg] += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
+      // B operand P^T: k-slot 8g + t <-> key (t < 4 ? 4g + t : 16 + 4g + t - 4)
+      bp[hg][0] = pack_bf16x2(pp[0], pp[1]);
+      bp[hg][1] = pack_bf16x2(pp[2], pp[3]);
+      bp[hg][2] = pack_bf16x2(pp[4], pp[5]);
+      bp[hg][3] = pack_bf16x2(pp[6], pp[7]);
+    }
+
+    // ---- O^T += V^T . P^T : 32 dv tiles of 16; each V operand feeds both sub-groups ----
+#pragma unroll
+    for (int nb = 0; nb < kVB; ++nb) {
+      if (nb + 1 < kVB) read_v(av[(nb + 1) & 1], (nb + 1) * kVBatch);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < kVBatch; ++u) o[db + u] = mfma16x16x32(as_bf16x8(av[u]), as_bf16x8(bp), o[db + u]);
+      for (int u = 0; u < kVBatch; ++u)
+#pragma unroll
+        for (int hg = 0; hg < 2; ++hg)
+          o[hg][nb * kVBatch + u] =
+              mfma16x16x32(as_bf16x8(av[nb & 1][u]), as_bf16x8(bp[hg]), o[hg][nb * kVBatch + u]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     Gather::wait_next(in_flight2, wave);  // block blk+1 (and ring entry blk+3) landed
     __syncthreads();
   }
 
-  // ---- epilogue: lane (head col, g) holds dv = 16 dt + 4 g + r ----
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  if (!head_ok) return;
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  uint2* orow = reinterpret_cast<uint2*>(out + out_row * kDv);
+  // ---- epilogue: lane (head, g) holds dv = 16 dt + 4 g + r ----
 #pragma unroll
-  for (int dt = 0; dt < kDv / 16; ++dt) {
-    uint2 w;
-    w.x = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-    w.y = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
-    orow[(16 * dt + 4 * g) / 4] = w;
-  }
-  if (g == 0) {
-    smax[out_row] = m_true * kLn2;
-    // a negative sum marks a row whose logits outgrew the headroom; the fixup pass redoes it
-    ssum[out_row] = clamped ? -1.f : lsum * exp2f(m_ref - m_true);
+  for (int hg = 0; hg < 2; ++hg) {
+    const float ls = xor32_sum(xor16_sum(lsum[hg]));
+    if (!hok[hg]) continue;
+    const float inv = ls > 0.f ? 1.f / ls : 0.f;
+    uint2* orp = reinterpret_cast<uint2*>(out + orow[hg] * kDv);
+#pragma unroll
+    for (int dt = 0; dt < kDv / 16; ++dt) {
+      uint2 w;
+      w.x = pack_bf16x2(o[hg][dt][0] * inv, o[hg][dt][1] * inv);
+      w.y = pack_bf16x2(o[hg][dt][2] * inv, o[hg][dt][3] * inv);
+      orp[(16 * dt + 4 * g) / 4] = w;
+    }
+    if (g == 0) {
+      smax[orow[hg]] = m_true[hg] * kLn2;
+      // a negative sum marks a row whose logits outgrew the headroom; the fixup pass redoes it
+      ssum[orow[hg]] = clamped[hg] ? -1.f : ls * exp2f(m_ref[hg] - m_true[hg]);
+    }
   }
 }
 
@@ -331,7 +378,7 @@ attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict
       }
     }
   }
-  const int xsw = swz8(n);
+  const int xsw = swz_kv(n);
   uint32_t qk_off[4];
 #pragma unroll
   for (int c4 = 0; c4 < 4; ++c4) qk_off[c4] = n * kRowBytes + 512 * half + 16 * ((2 * c4 + hh) ^ xsw);
@@ -609,13 +656,10 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
                        (long long)d_qk, (long long)d_v);
     if (s_kv > GatherGeom::kMaxRows)
       return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: S_kv > %lld", (long long)GatherGeom::kMaxRows);
-    const int hgroups = (int)ceil_div(n_heads, kFwdHeads);
-    const int64_t lin = ceil_div(s_q, kXcds) * (int64_t)kXcds * hgroups;  // tokens padded to a multiple of 8
-    if (lin > INT32_MAX) return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_fwd: too many rows");
-    dim3 grid((unsigned)lin, 1, (unsigned)batch);
+    dim3 grid((unsigned)s_q, ceil_div(n_heads, kFwdHeads), (unsigned)batch);
     sparse_mla_fwd_bf16_kernel<<<grid, kFwdThreads, 0, st>>>(
         (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
-        (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset, hgroups);
+        (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
     if (int rc = check_launch("dsa_sparse_mla_fwd(bf16)")) return rc;
     dim3 fgrid((unsigned)s_q, 1, (unsigned)batch);
     sparse_mla_fwd_exact_kernel<uint16_t><<<fgrid, 256, sc_bytes, st>>>(
