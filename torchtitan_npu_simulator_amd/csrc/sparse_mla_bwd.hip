@@ -197,40 +197,61 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     if (blk > 0) flush(blk - 1);
     if (wave == 0 && blk + 3 < nblk)
       Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
-    if (in_flight2) {
-      const int nb = (blk + 2) % 3;
-      Gather::issue(kvb, tile[nb], &vmask[nb], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl);
-    }
+    // block blk+2's rows: offsets resolved now, one DMA instruction per dQ batch below
+    const int nbuf = (blk + 2) % 3;
+    uint32_t doff[Gather::kMaxPerWave];
+    if (in_flight2)
+      Gather::prep(&vmask[nbuf], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl, doff);
     const lds_char* tb = lds_bytes(&tile[buf][0]);
     const uint32_t vm = vmask[buf];
 
-    // S^T and dP^T: operands read in batches of 6 ahead of their MFMAs (the sched_barrier
-    // keeps the batch together so its LDS latency overlaps the previous batch's MFMAs)
-    // four independent accumulation chains (S and dP for two key tiles)
+    // S^T and dP^T (four independent accumulation chains: S and dP for two key tiles);
+    // the A operands of batch n+1 are requested before the MFMAs of batch n issue
     f32x4 sacc[2], pacc[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) sacc[kt] = pacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    constexpr int kSB = 3;                   // k-steps per batch
+    constexpr int kSN = (kDqk / 32) / kSB;   // 6 batches
+    u32x4 a[2][2][kSB];
+    auto read_a = [&](u32x4 (&dst)[2][kSB], int cb) {
 #pragma unroll
-    for (int cb = 0; cb < kDqk / 32; cb += 3) {
-      u32x4 a[2][3];
-#pragma unroll
-      for (int u = 0; u < 3; ++u)
+      for (int u = 0; u < kSB; ++u)
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
           const int c = cb + u;
-          a[kt][u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
+          dst[kt][u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
         }
+    };
+    read_a(a[0], 0);
+#pragma unroll
+    for (int nb = 0; nb < kSN; ++nb) {
+      if (nb + 1 < kSN) read_a(a[(nb + 1) & 1], (nb + 1) * kSB);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 3; ++u) {
-        const int c = cb + u;
+      for (int u = 0; u < kSB; ++u) {
+        const int c = nb * kSB + u;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-          sacc[kt] = mfma16x16x32(as_bf16x8(a[kt][u]), as_bf16x8(qb[c]), sacc[kt]);
-          if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a[kt][u]), as_bf16x8(db[c]), pacc[kt]);
+          sacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(qb[c]), sacc[kt]);
+          if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(db[c]), pacc[kt]);
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // the first K^T operands of dQ are requested before the P / dS arithmetic
+    constexpr int kDB = 4;                   // dQ tiles per batch
+    constexpr int kDN = (kDqk / 16) / kDB;   // 9 batches
+    static_assert(kDN >= Gather::kMaxPerWave, "one row DMA per dQ batch");
+    u32x4 at[2][kDB];
+    auto read_kt = [&](u32x4 (&dst)[kDB], int db4) {
+#pragma unroll
+      for (int u = 0; u < kDB; ++u) {
+        const int dt = db4 + u;
+        const lds_char* a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
+        dst[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
+      }
+    };
+    read_kt(at[0], 0);
     // P and dS (lane: head col, keys 16kt + 4g + r)
     float pv[2][4], dsv[2][4];
     const uint32_t vmg = vm >> (4 * g);  // bit r: key 4g + r, bit 16 + r: key 16 + 4g + r
@@ -250,17 +271,14 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     bds[2] = pack_bf16x2(dsv[1][0], dsv[1][1]);
     bds[3] = pack_bf16x2(dsv[1][2], dsv[1][3]);
 #pragma unroll
-    for (int db4 = 0; db4 < kDqk / 16; db4 += 4) {
-      u32x4 a[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int dt = db4 + u;
-        const lds_char* a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
-        a[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
-      }
+    for (int nb = 0; nb < kDN; ++nb) {
+      if (nb + 1 < kDN) read_kt(at[(nb + 1) & 1], (nb + 1) * kDB);
+      if (in_flight2 && nb < Gather::kMaxPerWave) Gather::issue_one(kvb, tile[nbuf], nb, wave, doff);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) dqa[db4 + u] = mfma16x16x32(as_bf16x8(a[u]), as_bf16x8(bds), dqa[db4 + u]);
+      for (int u = 0; u < kDB; ++u)
+        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds), dqa[nb * kDB + u]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     // stage G = (dS * scale | P) for these 32 slots
 #pragma unroll
