@@ -3,6 +3,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 #include "dsa_mi355x.h"
 
 namespace dsa {
@@ -105,12 +108,13 @@ __device__ __forceinline__ float wave_sum(float v) {
 // distinct values (rows whose stride is a multiple of 256 B, read 8 rows at a time).
 __device__ __forceinline__ int swz8(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 // swz_kv: for tiles of 1152-byte latent-KV rows (72 chunks; a row starts on bank 0 or 32
-// by parity).  Over any 16 consecutive rows each parity class takes all 8 values (b128
-// reads of one chunk column by 16 rows), and over any 8 aligned rows each parity class
-// has distinct value pairs (swz_kv >> 1), which is what the transposed b64 reads of two
-// chunks x 4 rows per 16 lanes need.  Values are < 8, so XOR keeps a chunk inside its
-// aligned group of 8.
-__device__ __forceinline__ int swz_kv(int r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
+// by parity).  The XOR value is row bits 1, 2, 3 reversed (period 16), chosen (by
+// exhaustive check over the linear swizzles) so that all four read patterns of the
+// attention kernels are conflict-free: b128 reads of one chunk column by 16 aligned rows
+// (each parity class takes all 8 values), and transposed b64 reads of 4 rows x 4 chunks
+// (rows 4q and 4q+2 differ in bit 2) or 8 rows x 2 chunks per 32 lanes.  Values are < 8,
+// so XOR keeps a chunk inside its aligned group of 8.
+__device__ __forceinline__ int swz_kv(int r) { return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
 // swz16: for rows whose stride is a multiple of 256 B with >= 16 chunks: 16 consecutive
 // rows reading one chunk column hit 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int swz16(int r) { return r & 15; }
@@ -131,6 +135,18 @@ __device__ __forceinline__ void dma4_to_lds(const void* gbase, uint32_t voff, ui
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(gbase), "s"(m0v)
                : "memory", "m0");
+}
+
+// compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1, expanded by the
+// front end (a large "#pragma unroll" body may be left rolled by the optimizer, which turns
+// register arrays indexed by the loop variable into scratch memory)
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }

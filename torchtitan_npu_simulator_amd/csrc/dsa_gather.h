@@ -115,6 +115,58 @@ struct RowGather {
       if (lane == 0) *vmask_slot = (uint32_t)bal;
     }
   }
+  // register-light form for kernels that resolve each DMA instruction when they issue it
+  // and keep a block's validity bits in SGPRs: the row geometry packed as
+  // (row << 11) | chunk byte (16 bits, two instructions per VGPR)
+  static constexpr int kPackedRegs = (kMaxPerWave + 1) / 2;
+  struct PackedLanes {
+    uint32_t rc[kPackedRegs];
+  };
+  static __device__ __forceinline__ PackedLanes packed_lanes(int wave, int lane) {
+    const Lanes L = lanes(wave, lane);
+    PackedLanes P;
+#pragma unroll
+    for (int k = 0; k < kPackedRegs; ++k) {
+      const uint32_t lo = ((uint32_t)L.row[2 * k] << 11) | L.cbyte[2 * k];
+      const uint32_t hi = 2 * k + 1 < kMaxPerWave ? (((uint32_t)L.row[2 * k + 1] << 11) | L.cbyte[2 * k + 1]) : 0u;
+      P.rc[k] = lo | (hi << 16);
+    }
+    return P;
+  }
+  // the wave's i-th instruction straight from the ring: its slot value (read one batch
+  // ahead by the caller, an LDS load), then the DMA
+  typedef const __attribute__((address_space(3))) uint32_t lds_u32c;
+  // (the packed word passes through an empty asm so the unpacking is not hoisted out of
+  // the caller's loop, which would hold 2 kMaxPerWave unpacked values in registers)
+  static __device__ __forceinline__ uint32_t unpack(const PackedLanes& P, int i) {
+    uint32_t w = P.rc[i >> 1];
+    asm volatile("" : "+v"(w));
+    return (w >> (16 * (i & 1))) & 0xffffu;
+  }
+  static __device__ __forceinline__ uint32_t ring_slot(const int* ring, int i, const PackedLanes& P) {
+    const uint32_t e = unpack(P, i);
+    return *(lds_u32c*)(lds_bytes(const_cast<int*>(ring)) + ((e >> 11) << 2));
+  }
+  static __device__ __forceinline__ void issue_slot(const uint16_t* kvb, u32x4* tile, int i, int wave, uint32_t raw,
+                                                    const PackedLanes& P, uint32_t lim, int rows_left) {
+    static_assert(G::kRowBytes < (1 << 11) && G::kBN <= 32, "packed lane geometry");
+    const int J = wave + kWaves * i;
+    if constexpr (G::kTileInstr % kWaves != 0) {
+      if (J >= G::kTileInstr) return;
+    }
+    const uint32_t e = unpack(P, i);
+    const bool ok = raw <= lim && (int)(e >> 11) < rows_left;
+    // row * 1152 as a 24-bit multiply (rows < 2^22 by kMaxRows)
+    const uint32_t off = (ok ? __umul24(raw, (uint32_t)G::kRowBytes) : 0u) + (e & 0x7ffu);
+    dma16_to_lds(kvb, off, (uint32_t)(uintptr_t)&tile[J * 64]);
+  }
+  // validity bits of a block (bit j = slot j usable), computed by every wave, wave-uniform
+  static __device__ __forceinline__ uint32_t ring_valid(const int* ring, int lane, uint32_t lim, int rows_left) {
+    const uint32_t v = *(lds_u32c*)(lds_bytes(const_cast<int*>(ring)) + ((lane & (G::kBN - 1)) << 2));
+    const bool ok = lane < G::kBN && lane < rows_left && v <= lim;
+    return (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)__ballot(ok));
+  }
+
   static __device__ __forceinline__ void issue_one(const uint16_t* kvb, u32x4* tile, int i, int wave,
                                                    const uint32_t (&off)[kMaxPerWave]) {
     const int J = wave + kWaves * i;

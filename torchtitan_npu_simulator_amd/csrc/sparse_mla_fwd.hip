@@ -37,10 +37,8 @@ constexpr float kHeadroom = 64.0f;             // log2 units of P above the refe
 constexpr int kFwdWaves = 4;
 constexpr int kFwdThreads = kFwdWaves * 64;
 constexpr int kFwdHeads = 32 * kFwdWaves;      // heads per workgroup
-constexpr int kKSteps = kDqk / 32;             // 18 MFMA k-steps of 32 columns
-constexpr int kLatSteps = kDv / 32;            // 16 latent k-steps (Q in registers)
-constexpr int kQBatch = 2;                     // k-steps whose A operands are read a batch ahead
-constexpr int kVBatch = 2;                     // dv tiles whose V reads are issued a batch ahead
+constexpr int kKSteps = kDqk / 16;             // 36 MFMA k-steps of 16 columns (32x32x16)
+constexpr int kLatSteps = kDv / 16;            // 32 latent k-steps (Q in registers)
 // mass kernel (8 waves: 4 head groups x 2 contraction halves, 32x32x16 tiles)
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
@@ -75,240 +73,259 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
                            float* __restrict__ ssum, int S, int s_kv, int H, int K, float scale_log2,
                            int64_t q_offset) {
   using Gather = RowGather<kFwdWaves>;
+  constexpr int kPer = Gather::kMaxPerWave;
   __shared__ u32x4 tile[3][kTileChunks];
   __shared__ u32x4 qpe[kFwdHeads][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
-  __shared__ uint32_t vmask[3];
   __shared__ int sh_last;
 
   const int tok = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, col = lane & 15, g = lane >> 4;
-  const int head0 = blockIdx.y * kFwdHeads + wave * 32 + col;  // sub-group hg: head0 + 16 hg
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 31, h = lane >> 5;  // MFMA column (head / key row) and k half
+  const int hl = wave * 32 + n;           // head within the workgroup
+  const int head = blockIdx.y * kFwdHeads + hl;
+  const bool hok = head < H;
   const int64_t row_id = (int64_t)b * S + tok;
+  const int64_t orow = row_id * H + (hok ? head : 0);
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
-  bool hok[2];
-  int64_t orow[2];
-#pragma unroll
-  for (int hg = 0; hg < 2; ++hg) {
-    hok[hg] = head0 + 16 * hg < H;
-    orow[hg] = row_id * H + (hok[hg] ? head0 + 16 * hg : 0);
-  }
 
   const int nblk = fwd_count_blocks(ridx, K, s_kv, limit, &sh_last);
   if (nblk == 0) {
-#pragma unroll
-    for (int hg = 0; hg < 2; ++hg) {
-      if (!hok[hg]) continue;
-      uint32_t* o32 = reinterpret_cast<uint32_t*>(out + orow[hg] * kDv);
-      for (int i = g; i < kDv / 2; i += 4) o32[i] = 0u;
-      if (g == 0) {
-        smax[orow[hg]] = -INFINITY;
-        ssum[orow[hg]] = 0.f;
+    if (hok) {
+      uint32_t* o32 = reinterpret_cast<uint32_t*>(out + orow * kDv);
+      for (int i = h; i < kDv / 2; i += 2) o32[i] = 0u;
+      if (h == 0) {
+        smax[orow] = -INFINITY;
+        ssum[orow] = 0.f;
       }
     }
     return;
   }
   const uint32_t lim = gather_limit(limit, s_kv);
 
-  // ---- Q: latent qb[hg][c] = q[32c + 8g .. +8] of head head0 + 16hg in VGPRs (B operand
-  // of S^T = K Q^T); rope columns into LDS ----
-  u32x4 qb[2][kLatSteps];
+  // ---- Q: latent qb[s] = q[16s + 8h .. +8] of head `head` (B operand of S^T = K Q^T for
+  // k-step s) in VGPRs; the rope columns into LDS ----
+  u32x4 qb[kLatSteps];
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + orow * kDqk);
 #pragma unroll
-  for (int hg = 0; hg < 2; ++hg) {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + orow[hg] * kDqk);
+    for (int s = 0; s < kLatSteps; ++s) qb[s] = hok ? qh[2 * s + h] : (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int c = 0; c < kLatSteps; ++c) qb[hg][c] = hok[hg] ? qh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
-    // rope: chunks 64..71 of the row; lane g writes chunks 2g, 2g+1 of its head
-    const int hl = wave * 32 + 16 * hg + col;  // head within the workgroup
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int ch = 2 * g + j;
-      qpe[hl][ch ^ ((hl >> 1) & 7)] = hok[hg] ? qh[64 + ch] : (u32x4){0u, 0u, 0u, 0u};
+    for (int j = 0; j < 4; ++j) {  // rope chunks 64..71: lane h writes 4h .. 4h+3
+      const int ch = 4 * h + j;
+      qpe[hl][ch ^ ((hl >> 1) & 7)] = hok ? qh[64 + ch] : (u32x4){0u, 0u, 0u, 0u};
     }
   }
 #pragma unroll
-  for (int hg = 0; hg < 2; ++hg)
-#pragma unroll
-    for (int c = 0; c < kLatSteps; ++c) asm volatile("" : "+v"(qb[hg][c]));  // landed before any DMA
+  for (int s = 0; s < kLatSteps; ++s) asm volatile("" : "+v"(qb[s]));  // landed before any DMA
 
   // ---- LDS byte offsets ----
-  // A operand of S^T: key row 16kt + col, chunk (4c + g) ^ swz_kv(row); with c = 2u + c0 the
-  // XOR only touches bits 0..2, so offset = ka_off[kt][c0] + 128 u.
-  uint32_t ka_off[2][2];
+  // A operand of S^T, k-step s: key row n, chunk (2s + h) ^ swz_kv(n); with s = 4u + s0 the
+  // XOR only touches bits 0..2 of 8u + 2s0 + h, so offset = ka_off[s0] + 128 u.
+  uint32_t ka_off[4];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int c0 = 0; c0 < 2; ++c0) {
-      const int row = 16 * kt + col;
-      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ swz_kv(row));
-    }
-  // rope B operand of sub-group hg, step 16 + e: head row hl, chunk (4e + g) ^ ((hl >> 1) & 7)
+  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRowBytes + 16 * ((2 * s0 + h) ^ swz_kv(n));
+  // rope B operand, step 32 + e: head row hl, chunk (2e + h) ^ ((hl >> 1) & 7)
   const lds_char* qpe_b = lds_bytes(&qpe[0][0]);
-  uint32_t qpe_off[2][2];
+  // Transposed V reads for O^T[32 dv x 32 heads] += V^T . P^T, dv tile dt, key step kk:
+  // lane group G = lane / 16 covers dv 16 (G & 1) .. +15 and k half h = G >> 1; source lane
+  // c = lane % 16 supplies key row 16kk + 8x + 4h + c/4 (read x = 0, 1) and dv columns
+  // 32dt + 16 (G & 1) + 4 (c % 4) .. +3, so result lane gets 4 consecutive keys of one dv
+  // column.  k-slot 8h + t <-> key 16kk + 8 (t / 4) + 4h + t % 4 on both operands (the rows
+  // the S^T accumulator holds for this lane).  swz_kv of those rows does not depend on kk,
+  // and with dt = 2u + d0: offset = tr_off[x][d0] + 16 kk rows + 128 u.
+  uint32_t tr_off[2][2];
+  {
+    const int c = lane & 15, G = lane >> 4;
 #pragma unroll
-  for (int hg = 0; hg < 2; ++hg) {
-    const int hl = wave * 32 + 16 * hg + col;
+    for (int x = 0; x < 2; ++x) {
+      const int r = 8 * x + 4 * h + (c >> 2);
 #pragma unroll
-    for (int e = 0; e < 2; ++e) qpe_off[hg][e] = hl * 128 + 16 * ((4 * e + g) ^ ((hl >> 1) & 7));
+      for (int d0 = 0; d0 < 2; ++d0) {
+        const int ch = 4 * d0 + 2 * (G & 1) + ((c & 3) >> 1);
+        tr_off[x][d0] = r * kRowBytes + 16 * (ch ^ swz_kv(r)) + 8 * (c & 1);
+      }
+    }
   }
-  // Transposed V reads for O^T += V^T P^T: group g, source lane col supplies key row
-  // 4g + col/4 (+16 for the second read), dv columns 16dt + 4(col%4) -> chunk
-  // 2dt + (col%4)/2; with dt = 4u + d0: tr_off[d0] + 128 u.
-  const int tr_row = 4 * g + (col >> 2);
-  const int tr_x = swz_kv(tr_row);
-  const int tr_c0 = (col & 3) >> 1;
-  uint32_t tr_off[4];
-#pragma unroll
-  for (int d0 = 0; d0 < 4; ++d0) tr_off[d0] = tr_row * kRowBytes + 16 * ((2 * d0 + tr_c0) ^ tr_x) + 8 * (col & 1);
 
-  f32x4 o[2][kDv / 16];
+  f32x16 o[kDv / 32];  // O^T tile dt: lane holds dv 32dt + 8j + 4h + i (i = 0..3) of its head
 #pragma unroll
-  for (int hg = 0; hg < 2; ++hg)
-#pragma unroll
-    for (int t = 0; t < kDv / 16; ++t) o[hg][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_ref[2] = {-INFINITY, -INFINITY}, m_true[2] = {-INFINITY, -INFINITY}, lsum[2] = {0.f, 0.f};
-  bool clamped[2] = {false, false};
+  for (int t = 0; t < kDv / 32; ++t) o[t] = (f32x16){0.f};
+  float m_ref = -INFINITY, m_true = -INFINITY, lsum = 0.f;
+  bool clamped = false;
 
-  const typename Gather::Lanes gl = Gather::lanes(wave, lane);
-  static_assert(kKSteps / kQBatch >= Gather::kMaxPerWave, "one row DMA per QK batch");
-  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);
-  __syncthreads();  // also publishes qpe
-  Gather::issue(kvb, tile[0], &vmask[0], sidx[0], 0, K, lim, wave, lane, gl);
-  if (nblk > 1) Gather::issue(kvb, tile[1], &vmask[1], sidx[1], 1, K, lim, wave, lane, gl);
-  Gather::wait_next(nblk > 1, wave);  // block 0 landed
+  // ---- pipeline ----
+  // iteration blk: QK(blk) on tile blk % 3 while block blk+1's rows are DMA'd into tile
+  // (blk+1) % 3 (one instruction per QK batch), then softmax(blk) interleaved with PV(blk-1)
+  // on tile (blk-1) % 3, whose P (bp_prev) was made one iteration earlier.  The iteration
+  // ends with its DMAs landed (vmcnt 0) and one barrier, so a gather has about one block
+  // time to arrive.  Block validity bits travel in SGPRs.
+  const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
+  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);  // ring entries 0..2
+  __syncthreads();                                      // also publishes qpe
+  for (int i = tid; i < kTileChunks; i += kFwdThreads) tile[2][i] = (u32x4){0u, 0u, 0u, 0u};
+  uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) Gather::issue_slot(kvb, &tile[0][0], i, wave, Gather::ring_slot(sidx[0], i, gl), gl, lim, K);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk % 3;
-    const bool in_flight2 = blk + 2 < nblk;
-    if (wave == 0 && blk + 3 < nblk)
-      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
-    // block blk+2's rows: offsets resolved now, one DMA instruction per QK batch below
-    const int nbuf = (blk + 2) % 3;
-    uint32_t doff[Gather::kMaxPerWave];
-    if (in_flight2)
-      Gather::prep(&vmask[nbuf], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl, doff);
-    const lds_char* tb = lds_bytes(&tile[buf][0]);
+  constexpr int kQBatch = 4;                  // k-steps per QK batch
+  constexpr int kQB = kKSteps / kQBatch;      // 9 QK batches
+  static_assert(kQB >= kPer, "one row DMA per QK batch");
+  static_assert(kLatSteps % kQBatch == 0 && kKSteps - kLatSteps == kQBatch, "rope steps form the last QK batch");
+  constexpr int kVB = kDv / 32;               // 16 PV batches (one dv tile, two key steps)
+  u32x4 bp_prev[2] = {(u32x4){0u, 0u, 0u, 0u}, (u32x4){0u, 0u, 0u, 0u}};
 
-    // ---- S^T for both sub-groups; every A operand (2 key tiles) feeds both ----
-    f32x4 sacc[2][2];  // [hg][kt]
+  // S^T[32 keys x 32 heads] of block blk on v_mfma_f32_32x32x16_bf16 (one accumulator; the
+  // 32x32 shape issues at full rate without independent chains).  Block blk+1's rows go out
+  // meanwhile, one instruction per batch (ring entry `ring`, the slot value read a batch
+  // ahead); its validity bits are returned.  Past the last block the ring entry is stale and
+  // the rows land in a buffer nobody reads: every offset stays inside the KV tensor (a slot
+  // is used only if it is <= lim, else row 0 is read).
+  auto qk = [&](const lds_char* tb, u32x4* dst_tile, const int* ring, int rows_left, f32x16& sacc) {
+    const uint32_t vm_n = Gather::ring_valid(ring, lane, lim, rows_left);
+    uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
+    sacc = (f32x16){0.f};
+    u32x4 a[2][kQBatch];
+    u32x4 rope[kQBatch];
+    auto read_a = [&](u32x4 (&dst)[kQBatch], int sb) {
 #pragma unroll
-    for (int hg = 0; hg < 2; ++hg) sacc[hg][0] = sacc[hg][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    constexpr int kQB = kKSteps / kQBatch;
-    u32x4 a[2][2][kQBatch];  // [buffer][kt][u]
-    auto read_a = [&](u32x4 (&dst)[2][kQBatch], int cb) {
-#pragma unroll
-      for (int u = 0; u < kQBatch; ++u)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int c = cb + u;
-          dst[kt][u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
-        }
+      for (int u = 0; u < kQBatch; ++u) dst[u] = lds_read16(tb + ka_off[u] + 128 * (sb / kQBatch));
     };
     read_a(a[0], 0);
+    static_for<kQB>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      if constexpr (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
+      if constexpr ((nb + 1) * kQBatch == kLatSteps) {  // rope B operands one batch ahead
 #pragma unroll
-    for (int nb = 0; nb < kQB; ++nb) {
-      if (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
-      if (in_flight2 && nb < Gather::kMaxPerWave) Gather::issue_one(kvb, tile[nbuf], nb, wave, doff);
+        for (int e = 0; e < kQBatch; ++e) rope[e] = lds_read16(qpe_b + hl * 128 + 16 * ((2 * e + h) ^ ((hl >> 1) & 7)));
+      }
+      if constexpr (nb < kPer) {
+        const uint32_t raw = raw_next;
+        if constexpr (nb + 1 < kPer) raw_next = Gather::ring_slot(ring, nb + 1, gl);
+        Gather::issue_slot(kvb, dst_tile, nb, wave, raw, gl, lim, rows_left);
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kQBatch; ++u) {
-        const int c = nb * kQBatch + u;
+        constexpr int s0 = nb * kQBatch;
+        const u32x4 bq = s0 < kLatSteps ? qb[(s0 + u) % kLatSteps] : rope[u];
+        sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(bq), sacc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    return vm_n;
+  };
+
+  // softmax of block blk (sacc, validity bits vm) into bp_new, interleaved batch by batch
+  // with PV of block blk-1 (tile vb, P bp_prev; for blk = 0 a zeroed tile and P = 0).
+  // Lane holds keys 8j + 4h + i (value 4j + i) of head `head`; the lane 32 apart holds
+  // the other keys of the same head.
+  auto read_v = [&](const lds_char* vb, u32x4 (&dst)[2], int dt) {
 #pragma unroll
-        for (int hg = 0; hg < 2; ++hg) {
-          // rope steps read their B operand from LDS (registers hold the latent part only)
-          const u32x4 bq = c < kLatSteps ? qb[hg][c] : lds_read16(qpe_b + qpe_off[hg][c - kLatSteps]);
+    for (int kk = 0; kk < 2; ++kk) {
+      const lds_char* base = vb + kk * 16 * kRowBytes + 128 * (dt >> 1);
+      dst[kk] = lds_read_tr_pair(base + tr_off[0][dt & 1], base + tr_off[1][dt & 1]);
+    }
+  };
+  auto softmax_pv = [&](const lds_char* vb, const f32x16& sacc, uint32_t vm, u32x4 (&bp_new)[2]) {
+    u32x4 av[2][2];  // [buffer][kk]
+    read_v(vb, av[0], 0);
+    const uint32_t vmh = vm >> (4 * h);  // bit 8j + i: key 8j + 4h + i
+    float x[16], rmax;                     // masked logits, then P in place
+    static_for<kVB>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      if constexpr (nb + 1 < kVB) read_v(vb, av[(nb + 1) & 1], nb + 1);
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-            sacc[hg][kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(bq), sacc[hg][kt]);
+      for (int kk = 0; kk < 2; ++kk) o[nb] = mfma32x32x16(as_bf16x8(av[nb & 1][kk]), as_bf16x8(bp_prev[kk]), o[nb]);
+      // softmax work of this batch: masked logits and local max (0), cross-lane max and
+      // reference update (1), exp2 of a quarter of the values (2..5), pack and sum (5)
+      if constexpr (nb == 0) {
+        rmax = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = 8 * (v >> 2) + (v & 3);
+          x[v] = ((vmh >> key) & 1u) ? sacc[v] * scale_log2 : -INFINITY;
+          rmax = fmaxf(rmax, x[v]);
+        }
+      } else if constexpr (nb == 1) {
+        const float rm = xor32_max(rmax);
+        // (a block with no valid slot leaves every x at -inf and contributes exact zeros)
+        m_true = fmaxf(m_true, rm);
+        if (m_ref == -INFINITY) m_ref = rm;  // first block with a valid key fixes the reference
+        clamped |= rm > m_ref + kHeadroom;
+        // while no key has been seen every x is -inf; subtracting 0 then keeps exp2 at 0
+        rmax = m_ref == -INFINITY ? 0.f : m_ref;
+      } else if constexpr (nb >= 2 && nb < 6) {
+        constexpr int v0 = 4 * (nb - 2);
+#pragma unroll
+        for (int v = v0; v < v0 + 4; ++v) x[v] = __builtin_amdgcn_exp2f(fminf(x[v] - rmax, kHeadroom));
+        // B operand P^T of key step kk = j / 2: k-slot 8h + t <-> value 4 (2kk + t / 4) + t % 4
+        bp_new[v0 >> 3][(v0 & 4) >> 1] = pack_bf16x2(x[v0], x[v0 + 1]);
+        bp_new[v0 >> 3][((v0 & 4) >> 1) + 1] = pack_bf16x2(x[v0 + 2], x[v0 + 3]);
+        if constexpr (nb == 5) {
+          float s4[4];
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) s4[q4] = (x[4 * q4] + x[4 * q4 + 1]) + (x[4 * q4 + 2] + x[4 * q4 + 3]);
+          lsum += (s4[0] + s4[1]) + (s4[2] + s4[3]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    // the first V operands are requested before the softmax
-    constexpr int kVB = (kDv / 16) / kVBatch;
-    u32x4 av[2][kVBatch];
-    auto read_v = [&](u32x4 (&dst)[kVBatch], int db) {
-#pragma unroll
-      for (int u = 0; u < kVBatch; ++u) {
-        const int dt = db + u;
-        const lds_char* a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
-        dst[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
-      }
-    };
-    read_v(av[0], 0);
+    });
+  };
 
-    // ---- mask, scale, per-head block max and P (lane holds keys 16kt + 4g + r) ----
-    const uint32_t vmg = vmask[buf] >> (4 * g);  // bit r: key 4g + r, bit 16 + r: key 16 + 4g + r
-    u32x4 bp[2];
-#pragma unroll
-    for (int hg = 0; hg < 2; ++hg) {
-      float x[8];
-      float rmax = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float v = ((vmg >> (16 * kt + r)) & 1u) ? sacc[hg][kt][r] * scale_log2 : -INFINITY;
-          x[4 * kt + r] = v;
-          rmax = fmaxf(rmax, v);
-        }
-      rmax = xor32_max(xor16_max(rmax));
-      // (a block with no valid slot leaves every x at -inf and contributes exact zeros)
-      m_true[hg] = fmaxf(m_true[hg], rmax);
-      if (m_ref[hg] == -INFINITY) m_ref[hg] = rmax;  // first block with a valid key fixes the reference
-      clamped[hg] |= rmax > m_ref[hg] + kHeadroom;
-      // while no key has been seen every x is -inf; subtracting 0 then keeps exp2 at 0
-      const float mr = m_ref[hg] == -INFINITY ? 0.f : m_ref[hg];
-      float pp[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pp[j] = __builtin_amdgcn_exp2f(fminf(x[j] - mr, kHeadroom));
-      lsum[hg] += ((pp[0] + pp[1]) + (pp[2] + pp[3])) + ((pp[4] + pp[5]) + (pp[6] + pp[7]));
-      // B operand P^T: k-slot 8g + t <-> key (t < 4 ? 4g + t : 16 + 4g + t - 4)
-      bp[hg][0] = pack_bf16x2(pp[0], pp[1]);
-      bp[hg][1] = pack_bf16x2(pp[2], pp[3]);
-      bp[hg][2] = pack_bf16x2(pp[4], pp[5]);
-      bp[hg][3] = pack_bf16x2(pp[6], pp[7]);
-    }
-
-    // ---- O^T += V^T . P^T : 32 dv tiles of 16; each V operand feeds both sub-groups ----
-#pragma unroll
-    for (int nb = 0; nb < kVB; ++nb) {
-      if (nb + 1 < kVB) read_v(av[(nb + 1) & 1], (nb + 1) * kVBatch);
+  // PV of the last block
+  auto pv_only = [&](const lds_char* vb) {
+    u32x4 av[2][2];
+    read_v(vb, av[0], 0);
+    static_for<kVB>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      if constexpr (nb + 1 < kVB) read_v(vb, av[(nb + 1) & 1], nb + 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < kVBatch; ++u)
-#pragma unroll
-        for (int hg = 0; hg < 2; ++hg)
-          o[hg][nb * kVBatch + u] =
-              mfma16x16x32(as_bf16x8(av[nb & 1][u]), as_bf16x8(bp[hg]), o[hg][nb * kVBatch + u]);
+      for (int kk = 0; kk < 2; ++kk) o[nb] = mfma32x32x16(as_bf16x8(av[nb & 1][kk]), as_bf16x8(bp_prev[kk]), o[nb]);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    Gather::wait_next(in_flight2, wave);  // block blk+1 (and ring entry blk+3) landed
+    });
+  };
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (wave == 0 && blk + 3 < nblk)
+      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
+    f32x16 sacc;
+    // ring entry blk+1 landed during iteration blk-2 (or before the loop)
+    const uint32_t vm_next = qk(lds_bytes(&tile[blk % 3][0]), &tile[(blk + 1) % 3][0],
+                                sidx[(blk + 1) & (GatherGeom::kRing - 1)], K - (blk + 1) * kBN, sacc);
+    u32x4 bp_new[2];
+    softmax_pv(lds_bytes(&tile[(blk + 2) % 3][0]), sacc, vm_cur, bp_new);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
     __syncthreads();
+    vm_cur = vm_next;
+    bp_prev[0] = bp_new[0];
+    bp_prev[1] = bp_new[1];
   }
+  pv_only(lds_bytes(&tile[(nblk - 1) % 3][0]));
 
-  // ---- epilogue: lane (head, g) holds dv = 16 dt + 4 g + r ----
+  // ---- epilogue: lane holds dv = 32 dt + 8 j + 4 h + i of its head ----
+  const float ls = xor32_sum(lsum);
+  if (!hok) return;
+  const float inv = ls > 0.f ? 1.f / ls : 0.f;
+  uint2* orp = reinterpret_cast<uint2*>(out + orow * kDv);
 #pragma unroll
-  for (int hg = 0; hg < 2; ++hg) {
-    const float ls = xor32_sum(xor16_sum(lsum[hg]));
-    if (!hok[hg]) continue;
-    const float inv = ls > 0.f ? 1.f / ls : 0.f;
-    uint2* orp = reinterpret_cast<uint2*>(out + orow[hg] * kDv);
+  for (int dt = 0; dt < kDv / 32; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < kDv / 16; ++dt) {
+    for (int j = 0; j < 4; ++j) {
       uint2 w;
-      w.x = pack_bf16x2(o[hg][dt][0] * inv, o[hg][dt][1] * inv);
-      w.y = pack_bf16x2(o[hg][dt][2] * inv, o[hg][dt][3] * inv);
-      orp[(16 * dt + 4 * g) / 4] = w;
+      w.x = pack_bf16x2(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv);
+      w.y = pack_bf16x2(o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv);
+      orp[(32 * dt + 8 * j + 4 * h) / 4] = w;
     }
-    if (g == 0) {
-      smax[orow[hg]] = m_true[hg] * kLn2;
-      // a negative sum marks a row whose logits outgrew the headroom; the fixup pass redoes it
-      ssum[orow[hg]] = clamped[hg] ? -1.f : ls * exp2f(m_ref[hg] - m_true[hg]);
-    }
+  if (h == 0) {
+    smax[orow] = m_true * kLn2;
+    // a negative sum marks a row whose logits outgrew the headroom; the fixup pass redoes it
+    ssum[orow] = clamped ? -1.f : ls * exp2f(m_ref - m_true);
   }
 }
 
