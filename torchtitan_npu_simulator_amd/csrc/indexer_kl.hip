@@ -396,7 +396,7 @@ KlPlan plan_kl(int64_t batch, int64_t rows, int64_t s_k, int64_t topk) {
   p.rows = rows;
   p.ck_bytes = batch * rows * topk * kD * 2;
   p.pairs_bytes = rows * topk * 4;
-  p.csr_bytes = 3 * (s_k + 1) * 4;
+  p.csr_bytes = csr_ws_bytes(s_k, rows, topk);
   p.total = al(p.ck_bytes) + al(p.pairs_bytes) + al(p.csr_bytes);
   return p;
 }

@@ -532,7 +532,7 @@ BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t
   p.g_bytes = batch * rows * topk * kGW * 2;
   p.c_bytes = batch * rows * topk * kDqk * 2;
   p.pairs_bytes = rows * topk * 4;
-  p.csr_bytes = (3 * (s_kv + 1)) * 4;
+  p.csr_bytes = csr_ws_bytes(s_kv, rows, topk);
   p.mass_bytes = mass_groups * batch * rows * topk * 4;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
   p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + al(p.mass_bytes);
