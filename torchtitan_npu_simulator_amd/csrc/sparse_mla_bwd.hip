@@ -333,22 +333,31 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 // One workgroup per token, 12 waves; wave w owns the 48 output columns 48w .. 48w+47
 // (three 16-column MFMA tiles) and keeps its slice of X transposed in VGPRs for the whole
 // token (A operand of C^T = X^T G^T, 96 VGPRs).  G is streamed through a double-buffered
-// LDS tile of 128 slots x 256 (DMA), so G, X and C each cross HBM exactly once.
+// LDS tile of 64 slots x 256 (DMA), so G, X and C each cross HBM exactly once.  The C rows
+// of each 32-slot step are assembled in a double-buffered LDS stage (every wave adds its
+// 48 columns) and leave as whole 1152-byte rows, 16 bytes per lane: the MFMA output layout
+// alone would give 8-byte pieces scattered over 16 rows per store instruction.
 // --------------------------------------------------------------------------------------
 constexpr int kCW = 12;                     // waves
 constexpr int kCThreads = kCW * 64;
-constexpr int kCT = 128;                    // slots per G tile
-constexpr int kGTChunks = kCT * (kGW / 8);  // 4096 16-byte chunks (64 KB)
+constexpr int kCT = 64;                     // slots per G tile
+constexpr int kGTChunks = kCT * (kGW / 8);  // 2048 16-byte chunks (32 KB)
+constexpr int kCS = 32;                     // slots per step (C stage rows)
+constexpr int kStChunks = kCS * kRowChunks; // 2304 chunks (36 KB)
 constexpr int kXK = 64;                     // X rows staged per chunk while loading X
 constexpr int kXChunks = kXK * kRowChunks;  // 4608 chunks (73.7 KB)
+static_assert(2 * kGTChunks + 2 * kStChunks >= kXChunks, "X staging reuses the tile space");
+
+// C stage layout: row r (slot), 16-byte chunk c stored at c ^ ((r >> 1) & 7)
+__device__ __forceinline__ int stage_swz(int r) { return (r >> 1) & 7; }
 
 template <int kHGroups>
 __global__ void __launch_bounds__(kCThreads, 1)
 bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ dout,
                    const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf, uint16_t* __restrict__ cbuf,
                    int S, int s_kv, int H, int K, int64_t q_offset, int row0, int rows) {
-  constexpr int kKSteps = 4 * kHGroups;  // 32-row k steps of X (128 rows per head group)
-  __shared__ u32x4 lds[2 * kGTChunks];   // X staging at start, then two G tiles
+  constexpr int kKSteps = 4 * kHGroups;                // 32-row k steps of X (128 rows per head group)
+  __shared__ u32x4 lds[2 * kGTChunks + 2 * kStChunks];  // X staging at start; then G tiles + C stages
   __shared__ int sh_last;
 
   const int lr = blockIdx.x;  // local row in chunk
@@ -402,16 +411,23 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     for (int ks = 0; ks < kKSteps; ++ks) asm volatile("" : "+v"(xa[t][ks]));  // landed before the DMAs
   __syncthreads();
 
-  // ---- stream G tiles; C^T[16 cols x 16 slots] = X^T[16 cols x 256] . G^T[256 x 16 slots] ----
-  // per-lane DMA geometry: instruction J = wave + 12 i covers tile chunks [64J, 64J+64),
-  // chunk p = slot*32 + (c ^ swz16(slot))
+  // ---- stream G tiles; per 32-slot step C^T[16 cols x 16 slots] = X^T . G^T on six tiles ----
+  // G tile DMA: instruction J = wave + 12 i covers tile chunks [64J, 64J+64), chunk
+  // p = slot*32 + (c ^ swz16(slot))
+  lds_char* const gtile = lds_bytes(&lds[0]);
+  lds_char* const stage = lds_bytes(&lds[2 * kGTChunks]);
   const int ntiles = (nslots + kCT - 1) / kCT;
-  auto load_g = [&](int tl, int buf) {  // 64 DMA instructions per tile
+  // (lane and thread indices pass through empty asm inside the loops so their derived
+  // address arithmetic is recomputed there instead of being hoisted into registers that the
+  // X slice needs)
+  auto load_g = [&](int tl, int buf) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
+    for (int i = 0; i < (kGTChunks / 64 + kCW - 1) / kCW; ++i) {
       const int J = wave + kCW * i;
       if (J < kGTChunks / 64) {
-        const int p = J * 64 + lane;
+        const int p = J * 64 + ln;
         const int slot = p >> 5, pos = p & 31;
         const int c = pos ^ swz16(slot);
         const int gs = min(tl * kCT + slot, K - 1);
@@ -421,35 +437,71 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     }
   };
   load_g(0, 0);
+  int step = 0;
   for (int tl = 0; tl < ntiles; ++tl) {
     const int buf = tl & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of tile tl landed
-    __syncthreads();  // every wave's part landed; the other buffer is free
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of tile tl (and its stores) done
+    __syncthreads();  // every wave's part landed; the other G buffer is free
     if (tl + 1 < ntiles) load_g(tl + 1, buf ^ 1);
-    const lds_char* gb = lb + buf * (kGTChunks * 16);
-    for (int st = 0; st < kCT / 16; ++st) {
-      if (tl * kCT + 16 * st >= nslots) break;  // wave-uniform
-      const int sl = 16 * st + col;  // B operand row (slot) of this lane
-      const int slot = tl * kCT + sl;
-      const lds_char* grow_l = gb + 16 * (sl * 32);
-      const int sw = swz16(sl);
-      u32x4 bg[kKSteps];
+    const lds_char* gb = gtile + buf * (kGTChunks * 16);
+    for (int sh = 0; sh < kCT / kCS; ++sh, ++step) {
+      const int s0 = tl * kCT + kCS * sh;  // first slot of the step
+      if (s0 >= nslots) break;             // workgroup-uniform
+      f32x4 acc[2][3];
 #pragma unroll
-      for (int ks = 0; ks < kKSteps; ++ks) bg[ks] = lds_read16(grow_l + 16 * ((4 * ks + g) ^ sw));
-      f32x4 acc[3];
+      for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
-      for (int t = 0; t < 3; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 3; ++t) acc[h2][t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      const lds_char* gl[2];
+      int sw[2];
+      int cl = col;
+      asm volatile("" : "+v"(cl));
 #pragma unroll
-      for (int ks = 0; ks < kKSteps; ++ks)
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int sl = kCS * sh + 16 * h2 + cl;  // B operand row (slot) within the tile
+        gl[h2] = gb + 16 * (sl * 32);
+        sw[h2] = swz16(sl);
+      }
+      u32x4 bg[2][2];  // [buffer][h2]
 #pragma unroll
-        for (int t = 0; t < 3; ++t) acc[t] = mfma16x16x32(as_bf16x8(xa[t][ks]), as_bf16x8(bg[ks]), acc[t]);
-      if (slot < nslots) {  // lane (slot, g) holds columns 48w + 16t + 4g + r
+      for (int h2 = 0; h2 < 2; ++h2) bg[0][h2] = lds_read16(gl[h2] + 16 * (g ^ sw[h2]));
+#pragma unroll
+      for (int ks = 0; ks < kKSteps; ++ks) {
+        if (ks + 1 < kKSteps) {
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) bg[(ks + 1) & 1][h2] = lds_read16(gl[h2] + 16 * ((4 * (ks + 1) + g) ^ sw[h2]));
+        }
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+          for (int t = 0; t < 3; ++t)
+            acc[h2][t] = mfma16x16x32(as_bf16x8(xa[t][ks]), as_bf16x8(bg[ks & 1][h2]), acc[h2][t]);
+      }
+      // lane (slot 16 h2 + col, g) holds columns 48w + 16t + 4g + r: 8 bytes at chunk
+      // 6w + 2t + g/2, half g & 1 of the stage row
+      lds_char* stg = stage + (step & 1) * (kStChunks * 16);
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int r = 16 * h2 + col;
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
-          uint2 w2;
-          w2.x = pack_bf16x2(acc[t][0], acc[t][1]);
-          w2.y = pack_bf16x2(acc[t][2], acc[t][3]);
-          *reinterpret_cast<uint2*>(crow + (int64_t)slot * kDqk + 48 * wave + 16 * t + 4 * g) = w2;
+          typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 w2 = {pack_bf16x2(acc[h2][t][0], acc[h2][t][1]), pack_bf16x2(acc[h2][t][2], acc[h2][t][3])};
+          const int c = 6 * wave + 2 * t + (g >> 1);
+          *(__attribute__((address_space(3))) u32x2*)(stg + r * (kRowChunks * 16) + 16 * (c ^ stage_swz(r)) + 8 * (g & 1)) = w2;
+        }
+      }
+      __syncthreads();  // the step's C rows are complete in the stage
+      // whole rows out: thread chunk i -> row i / 72, chunk i % 72
+      int t_ = tid;
+      asm volatile("" : "+v"(t_));
+#pragma unroll
+      for (int m = 0; m < kStChunks / kCThreads; ++m) {
+        const int i = t_ + kCThreads * m;
+        const int r = i / kRowChunks, c = i - r * kRowChunks;
+        if (s0 + r < nslots) {
+          const u32x4 v = lds_read16(stg + r * (kRowChunks * 16) + 16 * (c ^ stage_swz(r)));
+          *reinterpret_cast<u32x4*>(crow + (int64_t)(s0 + r) * kDqk + 8 * c) = v;
         }
       }
     }
