@@ -55,6 +55,10 @@ __device__ __forceinline__ u32x4 tr_pair(uint32_t a1, uint32_t a2) {
   return av;
 }
 
+// piece swizzle of the transposed G stage (64-byte rows): conflict-free for the lanes'
+// 8-byte writes (16 rows x 2 pieces per 32 lanes) and for the flush's transposed reads
+__device__ __forceinline__ int gt_swz(int r) { return (r >> 1) & 7; }
+
 // number of 32-slot blocks up to the last usable slot of a row (block-wide; needs sync)
 __device__ int count_blocks(const int32_t* ridx, int K, int s_kv, int64_t limit, int* sh_last) {
   if (threadIdx.x == 0) *sh_last = -1;
@@ -80,7 +84,9 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
               int H, int K, float scale, int64_t q_offset, int row0) {
   using Gather = RowGather<4>;
   __shared__ u32x4 tile[3][kTileChunks];
-  __shared__ uint16_t gst[2][kBN][2 * kHG];  // staged G rows of this head group (by block parity)
+  // staged G of this head group, transposed: [block parity][dS heads 0..63 | P heads 0..63]
+  // [8-byte piece of 4 slots, at piece ^ gt_swz(row)]
+  __shared__ uint2 gst[2][2 * kHG][kBN / 4];
   __shared__ float pst[2][4][kBN];          // per-wave head sums of P (attention mass)
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
   __shared__ uint32_t vmask[3];
@@ -168,11 +174,25 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     const int sb = fb & 1;
     if (mrow && tid < kBN && fb * kBN + tid < K)
       mrow[fb * kBN + tid] = (pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid]);
-    for (int i = tid; i < kBN * 16; i += 256) {  // 32 slots x 256 B -> G[slot][128 hg ..]
-      const int slot = i >> 4, part = i & 15;
-      if (fb * kBN + slot >= K) continue;  // the row holds K slots only
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&gst[sb][slot][part * 8]);
-      *reinterpret_cast<u32x4*>(grow + (int64_t)(fb * kBN + slot) * kGW + 2 * kHG * hg + part * 8) = v;
+    // 32 slots x 128 staged rows -> G[slot][128 hg ..]: lane group (wave, G) takes head
+    // octet 4 wave + G of slots 16 u .. 16 u + 15; two transposed reads give lane c the
+    // octet's 8 values of slot 16 u + c (source lane c supplies row 8 octet + 4 x + c / 4,
+    // slots 16 u + 4 (c % 4) .. +3)
+    const int c16 = lane & 15, oct = 4 * wave + (lane >> 4);
+    const lds_char* gb = lds_bytes(&gst[sb][0][0]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const lds_char* a[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int row = 8 * oct + 4 * x + (c16 >> 2);
+        const int piece = 4 * u + (c16 & 3);
+        a[x] = gb + row * (kBN * 2) + 8 * (piece ^ gt_swz(row));
+      }
+      const u32x4 v = lds_read_tr_pair(a[0], a[1]);
+      const int slot = fb * kBN + 16 * u + c16;
+      if (slot < K)  // the row holds K slots only
+        *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 2 * kHG * hg + 8 * oct) = v;
     }
   };
 
@@ -280,15 +300,16 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
         dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds), dqa[nb * kDB + u]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // stage G = (dS * scale | P) for these 32 slots
+    // stage G = (dS * scale | P) for these 32 slots, transposed: the lane's 4 consecutive
+    // slots 16 kt + 4 g .. +3 of its head are one 8-byte piece
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int slot = 16 * kt + 4 * g + r;
-        gst[blk & 1][slot][wave * 16 + col] = f_to_bf16(dsv[kt][r] * scale);
-        gst[blk & 1][slot][kHG + wave * 16 + col] = f_to_bf16(pv[kt][r]);
-      }
+    for (int kt = 0; kt < 2; ++kt) {
+      const int hl = wave * 16 + col, piece = 4 * kt + g;
+      gst[blk & 1][hl][piece ^ gt_swz(hl)] =
+          make_uint2(pack_bf16x2(dsv[kt][0] * scale, dsv[kt][1] * scale), pack_bf16x2(dsv[kt][2] * scale, dsv[kt][3] * scale));
+      gst[blk & 1][kHG + hl][piece ^ gt_swz(kHG + hl)] =
+          make_uint2(pack_bf16x2(pv[kt][0], pv[kt][1]), pack_bf16x2(pv[kt][2], pv[kt][3]));
+    }
     if (mrow) {
       // sum P over this wave's 16 head lanes: three halving exchange steps (xor 8, 4, 2)
       // leave lane col with value j = (col >> 1) & 7 (j = 4 kt + r), the xor-1 add
