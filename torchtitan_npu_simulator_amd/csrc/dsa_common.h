@@ -86,6 +86,22 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// value of the lane whose index differs in bit 0..3 (mask 1, 2, 4, 8), through DPP moves
+// (VALU, no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1]; xor 4 = half-row mirror
+// (i -> 7 - i) then quad_perm [3,2,1,0]; xor 8 = rotate the 16-lane row by 8
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+template <int kMask>
+__device__ __forceinline__ float lane_xor(float x) {
+  static_assert(kMask == 1 || kMask == 2 || kMask == 4 || kMask == 8, "DPP lane exchange within 16-lane rows");
+  if constexpr (kMask == 1) return dpp_mov<0xB1>(x);
+  else if constexpr (kMask == 2) return dpp_mov<0x4E>(x);
+  else if constexpr (kMask == 4) return dpp_mov<0x1B>(dpp_mov<0x141>(x));
+  else return dpp_mov<0x128>(x);
+}
+
 // wave-level helpers (64-wide)
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
 

@@ -319,12 +319,12 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float lo = pv[0][j], hi = pv[1][j];  // values j and j + 4
-        h4[j] = (u8 ? hi : lo) + __shfl_xor(u8 ? lo : hi, 8, 64);
+        h4[j] = (u8 ? hi : lo) + lane_xor<8>(u8 ? lo : hi);
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) h2[j] = (u4 ? h4[j + 2] : h4[j]) + __shfl_xor(u4 ? h4[j] : h4[j + 2], 4, 64);
-      const float h1 = (u2 ? h2[1] : h2[0]) + __shfl_xor(u2 ? h2[0] : h2[1], 2, 64);
-      const float tot = h1 + __shfl_xor(h1, 1, 64);
+      for (int j = 0; j < 2; ++j) h2[j] = (u4 ? h4[j + 2] : h4[j]) + lane_xor<4>(u4 ? h4[j] : h4[j + 2]);
+      const float h1 = (u2 ? h2[1] : h2[0]) + lane_xor<2>(u2 ? h2[0] : h2[1]);
+      const float tot = h1 + lane_xor<1>(h1);
       if ((col & 1) == 0) {
         const int j = (col >> 1) & 7;
         pst[blk & 1][wave][16 * (j >> 2) + 4 * g + (j & 3)] = tot;
