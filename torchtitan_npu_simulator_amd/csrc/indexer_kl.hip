@@ -12,8 +12,9 @@
 //   phase 3  recompute S; E = g_j w_h [S > 0] staged in LDS as [slot][head] and
 //            [head][slot]; dw_h = sum_j g_j relu(S);
 //            dq^T[d x 16 heads] += k^T E^T (k read transposed with ds_read_tr16_b64);
-//            dk^T[32 d of wave w x slots] = q^T E over all 64 heads, written as bf16 and
-//            reduced per key by the shared CSR pass (no float atomics anywhere).
+//            dk^T[128 d x 16 slots of wave w] = q^T E over all 64 heads (q^T operands read
+//            transposed from q staged in LDS once per row), written as bf16 whole rows
+//            through a wave-private LDS stage and reduced per key by the shared CSR pass.
 // LDS key rows use the swz8 chunk swizzle (conflict-free b128 and transposed reads).
 // A generic fp32 kernel (any H, D) handles shapes outside the MFMA tile.
 #include <algorithm>
@@ -84,22 +85,6 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
 #pragma unroll
     for (int c = 0; c < kD / 32; ++c) qa[c] = qh[4 * c + g];
   }
-  // q^T for dk (A of 16x16x32 over heads): wave w covers d = 32w + 16 dt + col, k-step ks covers
-  // heads 32 ks + 8g .. +7
-  u32x4 qtr[2][2];
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int d = 32 * wave + 16 * dt + col;
-      uint32_t v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h0 = 32 * ks + 8 * g + 2 * i;
-        v[i] = (uint32_t)qi[(row_id * kH + h0) * kD + d] | ((uint32_t)qi[(row_id * kH + h0 + 1) * kD + d] << 16);
-      }
-      qtr[dt][ks] = (u32x4){v[0], v[1], v[2], v[3]};
-    }
   // C layout of S = q k^T tiles: lane (slot col, g) holds heads 16w + 4g + r
   float wr[4];
 #pragma unroll
@@ -148,8 +133,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       float part = 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r) part = fmaf(wr[r], fmaxf(sv[st][r], 0.f), part);
-      part += __shfl_xor(part, 16, 64);
-      part += __shfl_xor(part, 32, 64);
+      part = xor32_sum(xor16_sum(part));
       if (g == 0) ip[wave][16 * st + col] = part;
     }
     __syncthreads();
@@ -208,7 +192,30 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   // col supplies slot row 32 ks + 8g + col/4 (+4 second read), d columns 16dt + 4(col%4)
   const int tr_row = 8 * g + (col >> 2);
   if (gs != 0.f) {  // block-uniform
+    // q^T for dk (A of 16x16x32 over heads): tile dt covers d = 16 dt + col, k-step ks
+    // heads 32 ks + 8g .. +7; q [64 heads x 128 d] is staged row-major in kt[1] (swz8) and
+    // read transposed (source lane col supplies head row 32 ks + 8g + col/4 (+4 second
+    // read), d columns 16 dt + 4 (col % 4))
+    u32x4 qtr[kD / 16][2];
+    __syncthreads();  // phase 1 is done with kt
+    for (int i = tid; i < kH * kRowC; i += 256) {
+      const int h = i >> 4, c = i & 15;
+      kt[1][h * kRowC + (c ^ swz8(h))] = *reinterpret_cast<const u32x4*>(qi + (row_id * kH + h) * kD + 8 * c);
+    }
     __syncthreads();
+    {
+      const lds_char* qb = lds_bytes(&kt[1][0]);
+#pragma unroll
+      for (int dt = 0; dt < kD / 16; ++dt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int r1 = 32 * ks + tr_row, r2 = r1 + 4;
+          const int c0 = 2 * dt + ((col & 3) >> 1);
+          qtr[dt][ks] = lds_read_tr_pair(qb + 16 * (r1 * kRowC + (c0 ^ swz8(r1))) + 8 * (col & 1),
+                                         qb + 16 * (r2 * kRowC + (c0 ^ swz8(r2))) + 8 * (col & 1));
+        }
+    }
+    __syncthreads();  // kt[1] is a gather target again
     gather(0, 0);
     for (int blk = 0; blk < nblocks; ++blk) {
       const int buf = blk & 1;
@@ -254,25 +261,45 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
           dqa[dt] = mfma16x16x32(as_bf16x8(av), as_bf16x8(eb), dqa[dt]);
         }
       }
-      // dk^T[32 d of this wave x 64 slots] = q^T[d x 64 heads] . E[64 heads x slots]
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int sl = 16 * st + col;
-        const int slot = blk * kB + sl;
+      // dk^T[128 d x 16 slots of this wave] = q^T[d x 64 heads] . E[64 heads x slots 16w ..];
+      // the wave's rows of es / eh are read by this wave only, so once its MFMA operands are
+      // in registers they serve as its private stage: dk rows 0..7 in the es rows, 8..15 in
+      // the eh rows, 256 B each with 16-byte chunk c at c ^ (row & 15), stored as whole rows
+      {
+        const int sl = 16 * wave + col;
         u32x4 eo[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) eo[ks] = *reinterpret_cast<const u32x4*>(&es[sl][32 * ks + 8 * g]);
+        lds_char* stg[2] = {lds_bytes(&es[16 * wave][0]), lds_bytes(&eh[16 * wave][0])};
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // own es / eh reads done before reuse
+        // lane (slot col, g) holds d = 16 dt + 4g + r: 8 bytes at chunk 2 dt + g / 2, half g & 1;
+        // two halves of the d tiles keep the accumulators to 16 registers
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          f32x4 c4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int half = 0; half < 2; ++half) {
+          f32x4 c4[kD / 32];
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) c4 = mfma16x16x32(as_bf16x8(qtr[dt][ks]), as_bf16x8(eo[ks]), c4);
-          if (slot < K) {  // lane (slot, g) holds d = 32w + 16dt + 4g + r
-            uint2 wv;
-            wv.x = pack_bf16x2(c4[0], c4[1]);
-            wv.y = pack_bf16x2(c4[2], c4[3]);
-            *reinterpret_cast<uint2*>(ckrow + (int64_t)slot * kD + 32 * wave + 16 * dt + 4 * g) = wv;
+          for (int d4 = 0; d4 < kD / 32; ++d4) {
+            const int dt = 4 * half + d4;
+            c4[d4] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) c4[d4] = mfma16x16x32(as_bf16x8(qtr[dt][ks]), as_bf16x8(eo[ks]), c4[d4]);
           }
+#pragma unroll
+          for (int d4 = 0; d4 < kD / 32; ++d4) {
+            const int dt = 4 * half + d4;
+            const u32x2 wv = {pack_bf16x2(c4[d4][0], c4[d4][1]), pack_bf16x2(c4[d4][2], c4[d4][3])};
+            const int c = 2 * dt + (g >> 1);
+            *(__attribute__((address_space(3))) u32x2*)(stg[col >> 3] + (col & 7) * 256 + 16 * (c ^ col) + 8 * (g & 1)) = wv;
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const int row = 4 * m + (lane >> 4), c = lane & 15;
+          const u32x4 v = lds_read16(stg[row >> 3] + (row & 7) * 256 + 16 * (c ^ row));
+          const int slot = blk * kB + 16 * wave + row;
+          if (slot < K) *reinterpret_cast<u32x4*>(ckrow + (int64_t)slot * kD + 8 * c) = v;
         }
       }
     }
@@ -286,8 +313,10 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float v = dwp[r];
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, 64);
+    v += lane_xor<1>(v);
+    v += lane_xor<2>(v);
+    v += lane_xor<4>(v);
+    v += lane_xor<8>(v);
     dwp[r] = v;
   }
   if (col == 0)
