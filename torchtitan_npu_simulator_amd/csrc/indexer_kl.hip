@@ -66,6 +66,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   __shared__ uint16_t es[kB][kH + 8];       // E as [slot][head]
   __shared__ uint16_t eh[kH][kB + 8];       // E as [head][slot]
   __shared__ float red[4];
+  __shared__ int ring[4][kB];                 // slot indices of blocks b & 3
 
   const int lr = blockIdx.x, b = blockIdx.y;
   const int tok = row0 + lr;
@@ -89,8 +90,25 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   float wr[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) wr[r] = w[row_id * kH + 16 * wave + 4 * g + r];
+  // these operands must have arrived before the first DMA: a wait for them inside the loop
+  // would also wait for every row DMA in flight
+#pragma unroll
+  for (int c = 0; c < kD / 32; ++c) asm volatile("" : "+v"(qa[c]));
+#pragma unroll
+  for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(wr[r]));
 
-  auto gather = [&](int blk, int buf) {  // 64 rows x 256 B: 4 DMA instructions per wave
+  // Key-row gather, 64 rows x 256 B per block: 4 DMA instructions per wave, instruction
+  // J = 4 wave + i covering tile chunks [64J, 64J+64) (row p / 16, chunk (p % 16) ^ swz8(row)).
+  // The block's slot indices reach an LDS ring by DMA (wave 0, one dword per lane) two
+  // blocks ahead, and every DMA is inline assembly (the compiler neither waits for it before
+  // LDS reads nor counts it), so the only wait is the explicit one at the top of each block.
+  auto load_idx = [&](int blk) {  // wave 0: indices of block blk into ring entry blk & 3
+    if (wave == 0) {
+      const int j = min(blk * kB + lane, K - 1);
+      dma4_to_lds(ridx, (uint32_t)j * 4u, (uint32_t)(uintptr_t)&ring[blk & 3][0]);
+    }
+  };
+  auto gather = [&](int blk, int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int J = wave * 4 + i;
@@ -98,11 +116,18 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       const int row = p >> 4, pos = p & 15;
       const int chunk = pos ^ swz8(row);
       const int slot = blk * kB + row;
-      int v = ridx[min(slot, K - 1)];
-      if (slot >= K || !ok_slot(v, s_k, limit)) v = 0;
-      __builtin_amdgcn_global_load_lds((const void*)(kb + (int64_t)v * kD + chunk * 8),
-                                       (__attribute__((address_space(3))) void*)&kt[buf][J * 64], 16, 0, 0);
+      const int vi = ring[blk & 3][row];
+      const int r = (slot < K && ok_slot(vi, s_k, limit)) ? vi : 0;
+      dma16_to_lds(kb, (uint32_t)r * (kD * 2) + chunk * 16, (uint32_t)(uintptr_t)&kt[buf][J * 64]);
     }
+  };
+  // prologue of a pass: ring entries 0 and 1, then block 0's rows
+  auto start_pass = [&]() {
+    load_idx(0);
+    if (nblocks > 1) load_idx(1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    gather(0, 0);
   };
   const uint32_t kt_base = (uint32_t)(uintptr_t)(&kt[0][0]);
   auto s_tile = [&](uint32_t tb, int st) -> f32x4 {  // S tile (16 heads x 16 slots) of slot tile st
@@ -118,12 +143,13 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   };
 
   // ---------------- phase 1: index scores at the selected slots ----------------
-  gather(0, 0);
+  start_pass();
   for (int blk = 0; blk < nblocks; ++blk) {
     const int buf = blk & 1;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // tile[buf] landed for every wave; ip free
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // tile[buf] and ring entry blk+1 landed for every wave; ip free
     if (blk + 1 < nblocks) gather(blk + 1, buf ^ 1);
+    if (blk + 2 < nblocks) load_idx(blk + 2);
     const uint32_t tb = kt_base + buf * (kTileC * 16);
     f32x4 sv[4];
 #pragma unroll
@@ -145,28 +171,43 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   __syncthreads();
 
   // ---------------- phase 2: row statistics ----------------
+  // each thread keeps its slots' validity, target mass and score in registers (one batch
+  // of loads instead of a dependent load per pass)
+  constexpr int kPer = kMaxK / 256;
+  float mv[kPer], xv[kPer];
+  bool okv[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = tid + 256 * u;
+    okv[u] = j < K && ok_slot(ridx[min(j, K - 1)], s_k, limit);
+    mv[u] = j < K ? mrow[j] : 0.f;
+  }
   float lmax = -INFINITY, zsum = 0.f;
-  for (int j = tid; j < K; j += 256) {
-    if (ok_slot(ridx[j], s_k, limit)) {
-      lmax = fmaxf(lmax, iv[j]);
-      zsum += fmaxf(mrow[j], 0.f);
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = tid + 256 * u;
+    xv[u] = j < K ? iv[j] : 0.f;
+    if (okv[u]) {
+      lmax = fmaxf(lmax, xv[u]);
+      zsum += fmaxf(mv[u], 0.f);
     }
   }
   const float imax = block_reduce(lmax, red, true);
   const float Z = block_reduce(zsum, red, false);
   float esum = 0.f;
-  for (int j = tid; j < K; j += 256)
-    if (ok_slot(ridx[j], s_k, limit)) esum += expf(iv[j] - imax);
+#pragma unroll
+  for (int u = 0; u < kPer; ++u)
+    if (okv[u]) esum += expf(xv[u] - imax);
   const float E = block_reduce(esum, red, false);
   const bool valid_row = Z > eps;
   const float lse = imax + logf(E);
   const float zc = fmaxf(Z, eps);
   float lpart = 0.f, tpos = 0.f;
-  for (int j = tid; j < K; j += 256) {
-    const bool ok = ok_slot(ridx[j], s_k, limit);
-    const float t = ok ? fmaxf(mrow[j], 0.f) / zc : 0.f;
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const float t = okv[u] ? fmaxf(mv[u], 0.f) / zc : 0.f;
     if (t > 0.f) {
-      const float ls = valid_row ? (iv[j] - lse) : -logf((float)K);
+      const float ls = valid_row ? (xv[u] - lse) : -logf((float)K);
       lpart += t * (logf(fmaxf(t, eps)) - ls);
       tpos += t;
     }
@@ -175,11 +216,12 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const float T = block_reduce(tpos, red, false);
   if (tid == 0) loss_rows[row_id] = Z * lrow * loss_scale;
   const float gs = valid_row ? Z * loss_scale * grad_scale : 0.f;
-  for (int j = tid; j < K; j += 256) {
-    const bool ok = ok_slot(ridx[j], s_k, limit);
-    const float t = ok ? fmaxf(mrow[j], 0.f) / zc : 0.f;
-    const float sm = ok ? expf(iv[j] - lse) : 0.f;
-    iv[j] = gs * (sm * T - t);
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = tid + 256 * u;
+    const float t = okv[u] ? fmaxf(mv[u], 0.f) / zc : 0.f;
+    const float sm = okv[u] ? expf(xv[u] - lse) : 0.f;
+    if (j < K) iv[j] = gs * (sm * T - t);
   }
 
   // ---------------- phase 3: gradients ----------------
@@ -216,12 +258,13 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
         }
     }
     __syncthreads();  // kt[1] is a gather target again
-    gather(0, 0);
+    start_pass();
     for (int blk = 0; blk < nblocks; ++blk) {
       const int buf = blk & 1;
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();  // tile[buf] landed; es / eh free
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();  // tile[buf] and ring entry blk+1 landed; es / eh free
       if (blk + 1 < nblocks) gather(blk + 1, buf ^ 1);
+      if (blk + 2 < nblocks) load_idx(blk + 2);
       const uint32_t tb = kt_base + buf * (kTileC * 16);
       f32x4 sv[4];
 #pragma unroll
