@@ -89,7 +89,6 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   __shared__ uint2 gst[2][2 * kHG][kBN / 4];
   __shared__ float pst[2][4][kBN];          // per-wave head sums of P (attention mass)
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
-  __shared__ uint32_t vmask[3];
   __shared__ int sh_last;
 
   const int tok = row0 + blockIdx.x;  // row within the batch element
@@ -168,32 +167,33 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
   for (int t = 0; t < kDqk / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  // G and mass of block `fb` staged in gst/pst[fb & 1] -> global (issued one iteration
-  // after staging, before the next row DMA, so the stores never hold up a tile wait)
-  auto flush = [&](int fb) {
+  // G and mass of block `fb` staged in gst/pst[fb & 1] -> global, in three parts so they
+  // can be spread over the next block's dQ MFMAs (fb < 0: nothing is stored).
+  // G: lane group (wave, G) takes head octet 4 wave + G of slots 16 u .. 16 u + 15 (part
+  // u); two transposed reads give lane c the octet's 8 values of slot 16 u + c (source
+  // lane c supplies row 8 octet + 4 x + c / 4, slots 16 u + 4 (c % 4) .. +3).  Part 2:
+  // the head group's attention mass of the block's 32 slots.
+  auto flush_part = [&](int fb, int part) {
     const int sb = fb & 1;
-    if (mrow && tid < kBN && fb * kBN + tid < K)
-      mrow[fb * kBN + tid] = (pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid]);
-    // 32 slots x 128 staged rows -> G[slot][128 hg ..]: lane group (wave, G) takes head
-    // octet 4 wave + G of slots 16 u .. 16 u + 15; two transposed reads give lane c the
-    // octet's 8 values of slot 16 u + c (source lane c supplies row 8 octet + 4 x + c / 4,
-    // slots 16 u + 4 (c % 4) .. +3)
+    if (part == 2) {
+      if (mrow && fb >= 0 && tid < kBN && fb * kBN + tid < K)
+        mrow[fb * kBN + tid] = (pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid]);
+      return;
+    }
+    const int u = part;
     const int c16 = lane & 15, oct = 4 * wave + (lane >> 4);
     const lds_char* gb = lds_bytes(&gst[sb][0][0]);
+    const lds_char* a[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const lds_char* a[2];
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        const int row = 8 * oct + 4 * x + (c16 >> 2);
-        const int piece = 4 * u + (c16 & 3);
-        a[x] = gb + row * (kBN * 2) + 8 * (piece ^ gt_swz(row));
-      }
-      const u32x4 v = lds_read_tr_pair(a[0], a[1]);
-      const int slot = fb * kBN + 16 * u + c16;
-      if (slot < K)  // the row holds K slots only
-        *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 2 * kHG * hg + 8 * oct) = v;
+    for (int x = 0; x < 2; ++x) {
+      const int row = 8 * oct + 4 * x + (c16 >> 2);
+      const int piece = 4 * u + (c16 & 3);
+      a[x] = gb + row * (kBN * 2) + 8 * (piece ^ gt_swz(row));
     }
+    const u32x4 v = lds_read_tr_pair(a[0], a[1]);
+    const int slot = fb * kBN + 16 * u + c16;
+    if (fb >= 0 && slot < K)  // the row holds K slots only
+      *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 2 * kHG * hg + 8 * oct) = v;
   };
 
   // the per-head operands must have arrived before the first DMA: a later wait for them
@@ -203,35 +203,42 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
   for (int c = 0; c < kDv / 32; ++c) asm volatile("" : "+v"(db[c]));
   asm volatile("" : "+v"(delta), "+v"(lse2));
-  const typename Gather::Lanes gl = Gather::lanes(wave, lane);
-  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);
+
+  // ---- pipeline (as in the forward) ----
+  // iteration blk: S^T / dP^T of block blk on tile blk % 3 while block blk+1's rows are
+  // DMA'd into tile (blk+1) % 3 (one instruction per S/dP batch), then P / dS of blk
+  // interleaved batch by batch with dQ of blk-1 on tile (blk-1) % 3 (its dS^T operand
+  // bds_prev was made one iteration earlier), G / mass staging of blk and the stores of
+  // blk-1's.  The iteration ends with its DMAs landed (vmcnt 0) and one barrier.
+  constexpr int kPer = Gather::kMaxPerWave;
+  const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
+  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);  // ring entries 0..2
   __syncthreads();
-  Gather::issue(kvb, tile[0], &vmask[0], sidx[0], 0, K, lim, wave, lane, gl);
-  if (nblk > 1) Gather::issue(kvb, tile[1], &vmask[1], sidx[1], 1, K, lim, wave, lane, gl);
-  Gather::wait_next(nblk > 1, wave);  // block 0 landed
+  for (int i = tid; i < kTileChunks; i += 256) tile[2][i] = (u32x4){0u, 0u, 0u, 0u};  // dQ of "block -1"
+  uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    Gather::issue_slot(kvb, &tile[0][0], i, wave, Gather::ring_slot(sidx[0], i, gl), gl, lim, K);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk % 3;
-    const bool in_flight2 = blk + 2 < nblk;
-    if (blk > 0) flush(blk - 1);
-    if (wave == 0 && blk + 3 < nblk)
-      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
-    // block blk+2's rows: offsets resolved now, one DMA instruction per dQ batch below
-    const int nbuf = (blk + 2) % 3;
-    uint32_t doff[Gather::kMaxPerWave];
-    if (in_flight2)
-      Gather::prep(&vmask[nbuf], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl, doff);
-    const lds_char* tb = lds_bytes(&tile[buf][0]);
-    const uint32_t vm = vmask[buf];
+  constexpr int kSB = 2;                   // k-steps per S/dP batch
+  constexpr int kSN = (kDqk / 32) / kSB;   // 9 batches
+  static_assert(kSN >= kPer, "one row DMA per S/dP batch");
+  constexpr int kDB = 4;                   // dQ tiles per batch
+  constexpr int kDN = (kDqk / 16) / kDB;   // 9 batches
+  u32x4 bds_prev = (u32x4){0u, 0u, 0u, 0u};
 
-    // S^T and dP^T (four independent accumulation chains: S and dP for two key tiles);
-    // the A operands of batch n+1 are requested before the MFMAs of batch n issue
-    f32x4 sacc[2], pacc[2];
+  // S^T and dP^T of one block (four accumulation chains); block blk+1's DMA meanwhile
+  // (ring entry `ring`, slot value read a batch ahead); returns blk+1's validity bits.
+  // Past the last block the ring entry is stale and the rows land in a buffer nobody
+  // reads: every offset stays inside the KV tensor.
+  auto sdp = [&](const lds_char* tb, u32x4* dst_tile, const int* ring, int rows_left, f32x4 (&sacc)[2],
+                 f32x4 (&pacc)[2]) -> uint32_t {
+    const uint32_t vm_n = Gather::ring_valid(ring, lane, lim, rows_left);
+    uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) sacc[kt] = pacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    constexpr int kSB = 3;                   // k-steps per batch
-    constexpr int kSN = (kDqk / 32) / kSB;   // 6 batches
     u32x4 a[2][2][kSB];
     auto read_a = [&](u32x4 (&dst)[2][kSB], int cb) {
 #pragma unroll
@@ -243,97 +250,141 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
         }
     };
     read_a(a[0], 0);
-#pragma unroll
-    for (int nb = 0; nb < kSN; ++nb) {
-      if (nb + 1 < kSN) read_a(a[(nb + 1) & 1], (nb + 1) * kSB);
+    static_for<kSN>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      if constexpr (nb + 1 < kSN) read_a(a[(nb + 1) & 1], (nb + 1) * kSB);
+      if constexpr (nb < kPer) {
+        const uint32_t raw = raw_next;
+        if constexpr (nb + 1 < kPer) raw_next = Gather::ring_slot(ring, nb + 1, gl);
+        Gather::issue_slot(kvb, dst_tile, nb, wave, raw, gl, lim, rows_left);
+      }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kSB; ++u) {
-        const int c = nb * kSB + u;
+        constexpr int c0 = nb * kSB;
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-          sacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(qb[c]), sacc[kt]);
-          if (c < kDv / 32) pacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(db[c]), pacc[kt]);
+          sacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(qb[c0 + u]), sacc[kt]);
+          if (c0 + u < kDv / 32)
+            pacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(db[(c0 + u) % (kDv / 32)]), pacc[kt]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
+    });
+    return vm_n;
+  };
+
+  // Transposed K reads for dQ^T += K^T dS^T (tile vb)
+  auto read_kt = [&](const lds_char* vb, u32x4 (&dst)[kDB], int db4) {
+#pragma unroll
+    for (int u = 0; u < kDB; ++u) {
+      const int dt = db4 + u;
+      const lds_char* a1 = vb + tr_off[dt & 3] + 128 * (dt >> 2);
+      dst[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
     }
-    // the first K^T operands of dQ are requested before the P / dS arithmetic
-    constexpr int kDB = 4;                   // dQ tiles per batch
-    constexpr int kDN = (kDqk / 16) / kDB;   // 9 batches
-    static_assert(kDN >= Gather::kMaxPerWave, "one row DMA per dQ batch");
+  };
+
+  // P / dS of block blk (sacc, pacc, validity vm) -> bds_new, G and mass staged for blk;
+  // interleaved with dQ of block blk-1 (tile vb, bds_prev) and the stores of blk-1
+  auto pds_dq = [&](const lds_char* vb, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2], uint32_t vm, int blk,
+                    u32x4& bds_new) {
     u32x4 at[2][kDB];
-    auto read_kt = [&](u32x4 (&dst)[kDB], int db4) {
-#pragma unroll
-      for (int u = 0; u < kDB; ++u) {
-        const int dt = db4 + u;
-        const lds_char* a1 = tb + tr_off[dt & 3] + 128 * (dt >> 2);
-        dst[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
-      }
-    };
-    read_kt(at[0], 0);
-    // P and dS (lane: head col, keys 16kt + 4g + r)
-    float pv[2][4], dsv[2][4];
+    read_kt(vb, at[0], 0);
     const uint32_t vmg = vm >> (4 * g);  // bit r: key 4g + r, bit 16 + r: key 16 + 4g + r
+    float pv[2][4], dsv[2][4];
+    float h4[4], h2[2], h1 = 0.f;
+    const bool u8 = col & 8, u4 = col & 4, u2 = col & 2;
+    static_for<kDN>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      if constexpr (nb + 1 < kDN) read_kt(vb, at[(nb + 1) & 1], (nb + 1) * kDB);
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      for (int u = 0; u < kDB; ++u)
+        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds_prev), dqa[nb * kDB + u]);
+      if constexpr (nb == 0 || nb == 1) {  // P and dS of key tile kt (lane: head col, keys 16kt + 4g + r)
+        constexpr int kt = nb;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool ok = (vmg >> (16 * kt + r)) & 1u;
-        const float p = ok ? __builtin_amdgcn_exp2f(sacc[kt][r] * scale_log2 - lse2) : 0.f;
-        pv[kt][r] = p;
-        dsv[kt][r] = p * (pacc[kt][r] - delta);
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = (vmg >> (16 * kt + r)) & 1u;
+          const float p = ok ? __builtin_amdgcn_exp2f(sacc[kt][r] * scale_log2 - lse2) : 0.f;
+          pv[kt][r] = p;
+          dsv[kt][r] = p * (pacc[kt][r] - delta);
+        }
+      } else if constexpr (nb == 2) {
+        // dQ^T operand B = dS^T, k-slot 8g + t <-> key (t < 4 ? 4g + t : 16 + 4g + t - 4)
+        bds_new[0] = pack_bf16x2(dsv[0][0], dsv[0][1]);
+        bds_new[1] = pack_bf16x2(dsv[0][2], dsv[0][3]);
+        bds_new[2] = pack_bf16x2(dsv[1][0], dsv[1][1]);
+        bds_new[3] = pack_bf16x2(dsv[1][2], dsv[1][3]);
+        // stage G = (dS * scale | P) transposed: the lane's 4 consecutive slots
+        // 16 kt + 4 g .. +3 of its head are one 8-byte piece
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const int hl = wave * 16 + col, piece = 4 * kt + g;
+          gst[blk & 1][hl][piece ^ gt_swz(hl)] = make_uint2(pack_bf16x2(dsv[kt][0] * scale, dsv[kt][1] * scale),
+                                                            pack_bf16x2(dsv[kt][2] * scale, dsv[kt][3] * scale));
+          gst[blk & 1][kHG + hl][piece ^ gt_swz(kHG + hl)] =
+              make_uint2(pack_bf16x2(pv[kt][0], pv[kt][1]), pack_bf16x2(pv[kt][2], pv[kt][3]));
+        }
+      } else if constexpr (nb == 3) {
+        // attention mass: sum P over this wave's 16 head lanes in three halving exchange
+        // steps (xor 8, 4, 2) that leave lane col with value j = (col >> 1) & 7
+        // (j = 4 kt + r); the xor-1 add completes it
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = pv[0][j], hi = pv[1][j];  // values j and j + 4
+          h4[j] = (u8 ? hi : lo) + lane_xor<8>(u8 ? lo : hi);
+        }
+      } else if constexpr (nb == 4) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) h2[j] = (u4 ? h4[j + 2] : h4[j]) + lane_xor<4>(u4 ? h4[j] : h4[j + 2]);
+        h1 = (u2 ? h2[1] : h2[0]) + lane_xor<2>(u2 ? h2[0] : h2[1]);
+      } else if constexpr (nb == 5) {
+        const float tot = h1 + lane_xor<1>(h1);
+        if (mrow && (col & 1) == 0) {
+          const int j = (col >> 1) & 7;
+          pst[blk & 1][wave][16 * (j >> 2) + 4 * g + (j & 3)] = tot;
+        }
+      } else if constexpr (nb >= 6) {
+        flush_part(blk - 1, nb - 6);  // G (two parts) and mass of the previous block
       }
-    // dQ^T += K^T dS^T : B = dS^T, k-slot 8g + t <-> key (t < 4 ? 4g + t : 16 + 4g + t - 4)
-    u32x4 bds;
-    bds[0] = pack_bf16x2(dsv[0][0], dsv[0][1]);
-    bds[1] = pack_bf16x2(dsv[0][2], dsv[0][3]);
-    bds[2] = pack_bf16x2(dsv[1][0], dsv[1][1]);
-    bds[3] = pack_bf16x2(dsv[1][2], dsv[1][3]);
-#pragma unroll
-    for (int nb = 0; nb < kDN; ++nb) {
-      if (nb + 1 < kDN) read_kt(at[(nb + 1) & 1], (nb + 1) * kDB);
-      if (in_flight2 && nb < Gather::kMaxPerWave) Gather::issue_one(kvb, tile[nbuf], nb, wave, doff);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // dQ of the last block
+  auto dq_only = [&](const lds_char* vb) {
+    u32x4 at[2][kDB];
+    read_kt(vb, at[0], 0);
+    static_for<kDN>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      if constexpr (nb + 1 < kDN) read_kt(vb, at[(nb + 1) & 1], (nb + 1) * kDB);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kDB; ++u)
-        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds), dqa[nb * kDB + u]);
+        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds_prev), dqa[nb * kDB + u]);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    // stage G = (dS * scale | P) for these 32 slots, transposed: the lane's 4 consecutive
-    // slots 16 kt + 4 g .. +3 of its head are one 8-byte piece
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      const int hl = wave * 16 + col, piece = 4 * kt + g;
-      gst[blk & 1][hl][piece ^ gt_swz(hl)] =
-          make_uint2(pack_bf16x2(dsv[kt][0] * scale, dsv[kt][1] * scale), pack_bf16x2(dsv[kt][2] * scale, dsv[kt][3] * scale));
-      gst[blk & 1][kHG + hl][piece ^ gt_swz(kHG + hl)] =
-          make_uint2(pack_bf16x2(pv[kt][0], pv[kt][1]), pack_bf16x2(pv[kt][2], pv[kt][3]));
-    }
-    if (mrow) {
-      // sum P over this wave's 16 head lanes: three halving exchange steps (xor 8, 4, 2)
-      // leave lane col with value j = (col >> 1) & 7 (j = 4 kt + r), the xor-1 add
-      // completes it
-      const bool u8 = col & 8, u4 = col & 4, u2 = col & 2;
-      float h4[4], h2[2];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float lo = pv[0][j], hi = pv[1][j];  // values j and j + 4
-        h4[j] = (u8 ? hi : lo) + lane_xor<8>(u8 ? lo : hi);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) h2[j] = (u4 ? h4[j + 2] : h4[j]) + lane_xor<4>(u4 ? h4[j] : h4[j + 2]);
-      const float h1 = (u2 ? h2[1] : h2[0]) + lane_xor<2>(u2 ? h2[0] : h2[1]);
-      const float tot = h1 + lane_xor<1>(h1);
-      if ((col & 1) == 0) {
-        const int j = (col >> 1) & 7;
-        pst[blk & 1][wave][16 * (j >> 2) + 4 * g + (j & 3)] = tot;
-      }
-    }
-    Gather::wait_next(in_flight2, wave);  // block blk+1 (and ring entry blk+3) landed
+    });
+  };
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (wave == 0 && blk + 3 < nblk)
+      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
+    f32x4 sacc[2], pacc[2];
+    // ring entry blk+1 landed during iteration blk-2 (or before the loop)
+    const uint32_t vm_next = sdp(lds_bytes(&tile[blk % 3][0]), &tile[(blk + 1) % 3][0],
+                                 sidx[(blk + 1) & (GatherGeom::kRing - 1)], K - (blk + 1) * kBN, sacc, pacc);
+    u32x4 bds_new;
+    pds_dq(lds_bytes(&tile[(blk + 2) % 3][0]), sacc, pacc, vm_cur, blk, bds_new);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
     __syncthreads();
+    vm_cur = vm_next;
+    bds_prev = bds_new;
   }
-  flush(nblk - 1);
+  dq_only(lds_bytes(&tile[(nblk - 1) % 3][0]));
+  // the last block's G and mass were staged before the loop's final barrier
+  flush_part(nblk - 1, 0);
+  flush_part(nblk - 1, 1);
+  flush_part(nblk - 1, 2);
 
   // ---- dQ epilogue: lane (head col, g) holds d = 16 dt + 4 g + r ----
   if (!head_ok) return;
