@@ -86,6 +86,11 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// relu as one integer max on the bit pattern (negative floats, -0 included, have the sign
+// bit set and compare below 0): a float max would add a canonicalising max per operand in
+// IEEE mode.  +NaN passes through like torch.relu.
+__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
 // value of the lane whose index differs in bit 0..3 (mask 1, 2, 4, 8), through DPP moves
 // (VALU, no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1]; xor 4 = half-row mirror
 // (i -> 7 - i) then quad_perm [3,2,1,0]; xor 8 = rotate the 16-lane row by 8

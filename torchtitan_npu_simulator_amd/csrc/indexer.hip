@@ -3,15 +3,6 @@
 //   I[s, t] = -inf                                                       (t invalid)
 // (relu(c x) = c relu(x) for the positive per-token scales, so the quantise-then-
 // dequantise product of the reference folds into the head weights and one key scale.)
-//
-// Workgroup = 8 queries x 512 keys, 4 waves, 2 queries per wave.  A wave keeps its
-// queries' 64 heads as MFMA A operands in VGPRs and streams 16-key B tiles straight from
-// global memory (the whole key matrix is L2/MALL resident):
-//   bf16: 4 x v_mfma_f32_16x16x32_bf16 per (16-head tile, 16-key tile)
-//   fp8 : 1 x v_mfma_scale_f32_16x16x128_f8f6f4 (scales 0 = identity)
-// The 16x16 C tile (lane: key = l%16, heads 4(l/16)..+3) gets relu * w in registers,
-// is summed over the head tiles in-lane and over the 4 lane groups with two xor-shuffles.
-// Causal tiles past a query block's frontier are written as -inf without any MFMA.
 #include "dsa_common.h"
 
 namespace dsa {
@@ -19,47 +10,96 @@ namespace {
 
 constexpr int kD = 128;            // indexer head dim on the MFMA path
 constexpr int kThreads = 256;
-constexpr int kQPerWave = 2;
-constexpr int kQPerWG = 4 * kQPerWave;  // 8
-constexpr int kKeysPerWG = 512;
+
+// Workgroup = (4 waves x kQw queries) x 256 keys.  The 256 key rows are DMA'd once into a
+// swizzled LDS tile shared by the four waves (inline-asm global_load_lds, one wait), each
+// wave keeps its queries' heads as MFMA A operands in VGPRs (128 registers) and walks the
+// 16-key B tiles out of LDS:
+//   bf16: 4 x v_mfma_f32_16x16x32_bf16 per (16-head tile, 16-key tile)
+//   fp8 : 1 x v_mfma_scale_f32_16x16x128_f8f6f4 (scales 0 = identity)
+// The 16x16 C tile (lane: key = l%16, heads 4(l/16)..+3) gets relu * w in registers, is
+// summed over the head tiles in-lane and over the 4 lane groups with two lane swaps; the
+// workgroup's scores are staged in LDS and written as whole 1 KB rows.  Key ranges past
+// every query's causal frontier are written as -inf without any MFMA.
+template <bool kFp8, int kHeadTiles>
+struct IdxTile {
+  static constexpr int kQw = kFp8 ? (8 / kHeadTiles > 0 ? 8 / kHeadTiles : 1) : (4 / kHeadTiles > 0 ? 4 / kHeadTiles : 1);
+  static constexpr int kQ = 4 * kQw;                      // queries per workgroup
+  static constexpr int kKeys = 256;                       // keys per workgroup
+  static constexpr int kRowBytes = kD * (kFp8 ? 1 : 2);   // 128 or 256
+  static constexpr int kCpr = kRowBytes / 16;             // 16-byte chunks per key row
+  static constexpr int kTileBytes = kKeys * kRowBytes;
+  static constexpr int kDmaPerWave = kTileBytes / 1024 / 4;
+  static constexpr int kRegsPerTile = kFp8 ? 8 : 16;      // A/B dwords per lane per 16-row tile
+};
+// key-row chunk swizzle: fp8 rows (128 B) alternate bank halves, so the 8 rows of one
+// parity take distinct chunks; bf16 rows (256 B) all start on bank 0, 16 rows distinct
+template <bool kFp8>
+__device__ __forceinline__ int idx_swz(int r) { return kFp8 ? ((r >> 1) & 7) : (r & 15); }
 
 template <bool kFp8, int kHeadTiles>
-__global__ void __launch_bounds__(kThreads)
-indexer_mfma_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_scale, const uint8_t* __restrict__ k,
+__global__ void __launch_bounds__(kThreads, 2)
+indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_scale, const uint8_t* __restrict__ k,
                     const float* __restrict__ k_scale, const float* __restrict__ w, float* __restrict__ scores,
                     int S, int s_k, int64_t ld, int64_t q_offset, int cmp_ratio) {
+  using T = IdxTile<kFp8, kHeadTiles>;
   constexpr int H = kHeadTiles * 16;
-  constexpr int kElem = kFp8 ? 1 : 2;            // bytes per element
-  constexpr int kRegsPerTile = kFp8 ? 8 : 16;    // A/B dwords per lane per 16-row tile (all 128 columns)
+  constexpr int kQw = T::kQw;
+  __shared__ u32x4 ktile[T::kTileBytes / 16];
+  __shared__ float stage[T::kQ][T::kKeys];
+  __shared__ float ksc[T::kKeys];
   const int b = blockIdx.z;
-  const int q0 = blockIdx.x * kQPerWG;
-  const int t0 = blockIdx.y * kKeysPerWG;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int s0 = blockIdx.x * T::kQ;
+  const int t0 = blockIdx.y * T::kKeys;
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
+  const int t_end = min(s_k, t0 + T::kKeys);
 
-  // causal frontier of this workgroup's queries: key t is valid for query s iff t < nv(s)
+  // causal frontier: key t is valid for query s iff t < nvalid(s) (monotone in s)
   auto nvalid = [&](int s) -> int {
     const int64_t v = (s + q_offset + 1) / cmp_ratio;
     return (int)max((int64_t)0, min((int64_t)s_k, v));
   };
-  const int qa = q0 + wave * kQPerWave;
-  int nv[kQPerWave];
-#pragma unroll
-  for (int j = 0; j < kQPerWave; ++j) nv[j] = qa + j < S ? nvalid(qa + j) : 0;
-  const int t_end = min(s_k, t0 + kKeysPerWG);
+  const int nv_max = nvalid(min(s0 + T::kQ, S) - 1);  // last (largest) frontier of the workgroup
+  const int t_work = min(t_end, nv_max);               // keys below t_work need MFMA work
+  const int64_t q_row0 = (int64_t)b * S;
 
-  // A operands (queries) and folded head weights
-  uint32_t qa_reg[kQPerWave][kHeadTiles][kRegsPerTile];
-  float wv[kQPerWave][kHeadTiles][4];
+  if (t_work <= t0) {  // the whole key range lies past every query's frontier
+    for (int i = tid; i < T::kQ * T::kKeys; i += kThreads) {
+      const int qi = i / T::kKeys, kk = i - qi * T::kKeys;
+      if (s0 + qi < S && t0 + kk < t_end) scores[(q_row0 + s0 + qi) * ld + t0 + kk] = -INFINITY;
+    }
+    return;
+  }
+
+  // ---- key rows into LDS (row r, chunk c at c ^ idx_swz(r)); key scales ----
+  {
+    const uint8_t* kb = k + ((int64_t)b * s_k) * T::kRowBytes;
 #pragma unroll
-  for (int j = 0; j < kQPerWave; ++j) {
+    for (int i = 0; i < T::kDmaPerWave; ++i) {
+      const int J = wave + 4 * i;
+      const int p = J * 64 + lane;
+      const int row = p / T::kCpr, pos = p - row * T::kCpr;
+      const int key = min(t0 + row, s_k - 1);
+      dma16_to_lds(kb, (uint32_t)key * T::kRowBytes + 16 * (pos ^ idx_swz<kFp8>(row)),
+                   (uint32_t)(uintptr_t)&ktile[J * 64]);
+    }
+    ksc[tid] = k_scale ? k_scale[(int64_t)b * s_k + min(t0 + tid, s_k - 1)] : 1.f;
+  }
+
+  // ---- A operands (queries) and folded head weights, while the DMA is in flight ----
+  const int qa = s0 + wave * kQw;
+  uint32_t qa_reg[kQw][kHeadTiles][T::kRegsPerTile];
+  float wv[kQw][kHeadTiles][4];
+#pragma unroll
+  for (int j = 0; j < kQw; ++j) {
     const int s = min(qa + j, S - 1);
-    const int64_t qrow = ((int64_t)b * S + s) * H;
+    const int64_t qrow = (q_row0 + s) * H;
 #pragma unroll
     for (int ht = 0; ht < kHeadTiles; ++ht) {
       const int head = ht * 16 + col;
-      const uint8_t* src = q + (qrow + head) * kD * kElem;
-      if (kFp8) {  // lane holds k = 32g .. 32g+31
+      const uint8_t* src = q + (qrow + head) * kD * (kFp8 ? 1 : 2);
+      if constexpr (kFp8) {  // lane holds k = 32g .. 32g+31
         const u32x4* p = reinterpret_cast<const u32x4*>(src + 32 * g);
         const u32x4 x0 = p[0], x1 = p[1];
 #pragma unroll
@@ -83,74 +123,96 @@ indexer_mfma_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
       }
     }
   }
+  int nvq[kQw];
+#pragma unroll
+  for (int j = 0; j < kQw; ++j) nvq[j] = qa + j < S ? nvalid(qa + j) : 0;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA and operand loads done
+  __syncthreads();
 
-  for (int kt = t0; kt < t_end; kt += 16) {
-    const int key = kt + col;
-    const int keyc = min(key, s_k - 1);
-    const bool any_valid = (kt < nv[0]) || (kt < nv[kQPerWave - 1]);
-    float acc[kQPerWave];
+  // ---- 16-key tiles ----
+  const lds_char* kt_b = lds_bytes(&ktile[0]);
+  const int ntiles = (t_work - t0 + 15) >> 4;
+  for (int kt = 0; kt < ntiles; ++kt) {
+    const int row = 16 * kt + col;  // B operand row (key) of this lane
+    uint32_t kb[T::kRegsPerTile];
+    if constexpr (kFp8) {
 #pragma unroll
-    for (int j = 0; j < kQPerWave; ++j) acc[j] = 0.f;
-    if (any_valid) {  // wave-uniform
-      uint32_t kb[kRegsPerTile];
-      const uint8_t* ksrc = k + ((int64_t)b * s_k + keyc) * kD * kElem;
-      if (kFp8) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(ksrc + 32 * g);
-        const u32x4 x0 = p[0], x1 = p[1];
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const u32x4 x = lds_read16(kt_b + row * T::kRowBytes + 16 * ((2 * g + h2) ^ idx_swz<kFp8>(row)));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          kb[r] = x0[r];
-          kb[4 + r] = x1[r];
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const u32x4 x = *reinterpret_cast<const u32x4*>(ksrc + (32 * c + 8 * g) * 2);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) kb[4 * c + r] = x[r];
-        }
+        for (int r = 0; r < 4; ++r) kb[4 * h2 + r] = x[r];
       }
+    } else {
 #pragma unroll
-      for (int j = 0; j < kQPerWave; ++j) {
-        float part = 0.f;
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 x = lds_read16(kt_b + row * T::kRowBytes + 16 * ((4 * c + g) ^ idx_swz<kFp8>(row)));
 #pragma unroll
-        for (int ht = 0; ht < kHeadTiles; ++ht) {
-          f32x4 c4 = (f32x4){0.f, 0.f, 0.f, 0.f};
-          if (kFp8) {
-            i32x8 av, bv;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-              av[r] = (int)qa_reg[j][ht][r];
-              bv[r] = (int)kb[r];
-            }
-            c4 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c4, 0, 0, 0, 0, 0, 0);
-          } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              u32x4 av, bv;
-#pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                av[r] = qa_reg[j][ht][4 * c + r];
-                bv[r] = kb[4 * c + r];
-              }
-              c4 = mfma16x16x32(as_bf16x8(av), as_bf16x8(bv), c4);
-            }
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) part = fmaf(wv[j][ht][r], fmaxf(c4[r], 0.f), part);
-        }
-        part += __shfl_xor(part, 16, 64);
-        part += __shfl_xor(part, 32, 64);
-        acc[j] = part;
+        for (int r = 0; r < 4; ++r) kb[4 * c + r] = x[r];
       }
     }
-    if (g == 0 && key < t_end) {
-      const float ks = k_scale ? k_scale[(int64_t)b * s_k + keyc] : 1.f;
+    // software pipeline over the wave's queries: the MFMAs of query j+1 are issued before
+    // the relu * w reduction of query j reads its results
+    f32x4 cq[2][kHeadTiles];
+    auto mfma_q = [&](int j, f32x4 (&c)[kHeadTiles]) {
 #pragma unroll
-      for (int j = 0; j < kQPerWave; ++j) {
-        const int s = qa + j;
-        if (s < S) scores[((int64_t)b * S + s) * ld + key] = key < nv[j] ? acc[j] * ks : -INFINITY;
+      for (int ht = 0; ht < kHeadTiles; ++ht) {
+        c[ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        if constexpr (kFp8) {
+          i32x8 av, bv;
+#pragma unroll
+          for (int r = 0; r < 8; ++r) {
+            av[r] = (int)qa_reg[j][ht][r];
+            bv[r] = (int)kb[r];
+          }
+          c[ht] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c[ht], 0, 0, 0, 0, 0, 0);
+        } else {
+#pragma unroll
+          for (int c4i = 0; c4i < 4; ++c4i) {
+            u32x4 av, bv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              av[r] = qa_reg[j][ht][4 * c4i + r];
+              bv[r] = kb[4 * c4i + r];
+            }
+            c[ht] = mfma16x16x32(as_bf16x8(av), as_bf16x8(bv), c[ht]);
+          }
+        }
       }
+    };
+    mfma_q(0, cq[0]);
+#pragma unroll
+    for (int j = 0; j < kQw; ++j) {
+      if (j + 1 < kQw) mfma_q(j + 1, cq[(j + 1) & 1]);
+      float part = 0.f;
+#pragma unroll
+      for (int ht = 0; ht < kHeadTiles; ++ht)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part = fmaf(wv[j][ht][r], relu_bits(cq[j & 1][ht][r]), part);
+      part = xor32_sum(xor16_sum(part));
+      // lane group g stages query j (j mod 4)
+      if (g == (j & 3)) {
+        const int key = t0 + 16 * kt + col;
+        stage[wave * kQw + j][16 * kt + col] = key < nvq[j] ? part * ksc[16 * kt + col] : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+  // ---- scores out: whole rows; keys past t_work are -inf (beyond every frontier) ----
+  for (int i = tid; i < T::kQ * (T::kKeys / 4); i += kThreads) {
+    const int qi = i / (T::kKeys / 4), c4i = i - qi * (T::kKeys / 4);
+    const int s = s0 + qi, kk = 4 * c4i;
+    if (s >= S || t0 + kk >= t_end) continue;
+    float4 v;
+    v.x = t0 + kk + 0 < t_work ? stage[qi][kk + 0] : -INFINITY;
+    v.y = t0 + kk + 1 < t_work ? stage[qi][kk + 1] : -INFINITY;
+    v.z = t0 + kk + 2 < t_work ? stage[qi][kk + 2] : -INFINITY;
+    v.w = t0 + kk + 3 < t_work ? stage[qi][kk + 3] : -INFINITY;
+    float* dst = scores + (q_row0 + s) * ld + t0 + kk;
+    if (t0 + kk + 4 <= t_end && (((uintptr_t)dst) & 15) == 0) {
+      *reinterpret_cast<float4*>(dst) = v;
+    } else {
+      const float vv[4] = {v.x, v.y, v.z, v.w};
+      for (int e = 0; e < 4 && t0 + kk + e < t_end; ++e) dst[e] = vv[e];
     }
   }
 }
@@ -210,17 +272,20 @@ extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* 
   if (!q || !k || !w || !scores) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: null pointer");
   if (batch <= 0 || s_q <= 0 || s_k <= 0 || n_heads <= 0 || head_dim <= 0 || ld_scores < s_k || cmp_ratio <= 0)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: bad sizes");
-  if (s_q > 65535LL * 8 || batch > 65535 || s_k > 2147483647LL)
+  if (s_q > 2147483647LL || batch > 65535 || s_k > 2147483647LL)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: sizes out of range");
   hipStream_t st = (hipStream_t)stream;
   const bool mfma_shape = head_dim == kD && n_heads % 16 == 0 && n_heads <= 128 && dtype != DSA_F32;
   if (mfma_shape) {
-    dim3 grid(ceil_div(s_q, kQPerWG), ceil_div(s_k, kKeysPerWG), (unsigned)batch);
     const uint8_t* qp = (const uint8_t*)q;
     const uint8_t* kp = (const uint8_t*)k;
-#define DSA_IDX_LAUNCH(FP8, HT)                                                                              \
-  indexer_mfma_kernel<FP8, HT><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, (int)s_q, (int)s_k, \
-                                                          ld_scores, q_offset, (int)cmp_ratio)
+#define DSA_IDX_LAUNCH(FP8, HT)                                                                                   \
+  do {                                                                                                             \
+    using Tl = IdxTile<FP8, HT>;                                                                                   \
+    dim3 grid(ceil_div(s_q, Tl::kQ), ceil_div(s_k, Tl::kKeys), (unsigned)batch);                                    \
+    indexer_tile_kernel<FP8, HT><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, (int)s_q, (int)s_k, \
+                                                            ld_scores, q_offset, (int)cmp_ratio);                  \
+  } while (0)
     const int ht = (int)(n_heads / 16);
     if (dtype == DSA_FP8_E4M3) {
       switch (ht) {

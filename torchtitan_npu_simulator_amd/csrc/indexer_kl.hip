@@ -158,7 +158,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     for (int st = 0; st < 4; ++st) {
       float part = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) part = fmaf(wr[r], fmaxf(sv[st][r], 0.f), part);
+      for (int r = 0; r < 4; ++r) part = fmaf(wr[r], relu_bits(sv[st][r]), part);
       part = xor32_sum(xor16_sum(part));
       if (g == 0) ip[wave][16 * st + col] = part;
     }
@@ -277,7 +277,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float e = sv[st][r] > 0.f ? gj * wr[r] : 0.f;
-          dwp[r] += gj * fmaxf(sv[st][r], 0.f);
+          dwp[r] += gj * relu_bits(sv[st][r]);
           const uint16_t eb = f_to_bf16(e);
           es[sl][16 * wave + 4 * g + r] = eb;
           eh[16 * wave + 4 * g + r][sl] = eb;
