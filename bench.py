@@ -167,6 +167,32 @@ def measured_traffic(kernel, S, H, K):
     return k["fetch_bytes"] + k["write_bytes"]
 
 
+def time_indexer_kernel(inp, ops, torch, reps=10):
+    """Average duration (ms) of the lightning-indexer score kernel alone (dsa_indexer_fwd,
+    fp8 queries and keys, causal), timed with HIP events on the stream it runs on, outside
+    the timed steps.  The step's indexer phase also includes the top-k selection."""
+    q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
+    k8, ks = ops.quantize_fp8_per_row(inp["k_idx"])
+    S = q8.shape[1]
+    out = torch.empty(1, S, k8.shape[1], dtype=torch.float32, device=q8.device)
+
+    def run():
+        ops.indexer_scores(q8, k8, inp["w"], q_scale=qs, k_scale=ks, q_offset=0, out=out)
+
+    run()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del out
+    return ms
+
+
 def copy_calibration(torch, device, nbytes=1 << 30):
     """One elementwise copy kernel of known size (reads and writes ``nbytes`` once each), for
     scaling the FETCH_SIZE / WRITE_SIZE counters."""
@@ -299,6 +325,7 @@ def main():
     )
     roof_pair["frac"] = roof_pair["achieved"] / roof_pair["peak"]
     idx_ms = phases["indexer_topk"]
+    idx_kernel_ms = time_indexer_kernel(inp, ops, torch)
     line = dict(
         metric="sparse-attn fwd+bwd tokens/s @S=8K,top-k 2048; % HBM / MFMA roofline",
         value=S / (ms_per_step * 1e-3),
@@ -317,9 +344,12 @@ def main():
         roofline=roof,
         roofline_attention_fwd_bwd=roof_pair,
         phases_ms={k: round(v, 4) for k, v in phases.items()},
-        indexer_mfma=dict(flops=work["indexer_flops"], ms_with_topk=idx_ms,
-                          tflops_upper_bound=work["indexer_flops"] / (idx_ms * 1e-3) / 1e12,
-                          peak_tflops=FP8_PEAK_TFLOPS),
+        indexer_mfma=dict(kernel="indexer_tile_kernel<true, 4>", bound="mfma", flops=work["indexer_flops"],
+                          avg_launch_ms=idx_kernel_ms,
+                          achieved_tflops=work["indexer_flops"] / (idx_kernel_ms * 1e-3) / 1e12,
+                          peak_tflops=FP8_PEAK_TFLOPS,
+                          frac=work["indexer_flops"] / (idx_kernel_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS,
+                          ms_with_topk=idx_ms),
         attn_mfma=dict(fwd_tflops=work["attn_fwd_flops"] / (fwd_ms * 1e-3) / 1e12,
                        bwd_tflops=work["attn_bwd_flops"] / (bwd_ms * 1e-3) / 1e12, peak_tflops=BF16_PEAK_TFLOPS),
     )

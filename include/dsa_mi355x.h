@@ -24,6 +24,11 @@
  *                                 ops/aclnn/sparse_lightning_indexer_grad_kl_loss/binding.cpp:12-36)
  *   dsa_compressor_fwd           Compressor._forward_bsnd pooling + RMSNorm
  *                                (models/deepseek_v4/model.py:183-221; torch-only in the reference)
+ *   dsa_compressor_fwd_tnd       Compressor._forward_tnd (models/deepseek_v4/model.py:223-274)
+ *   dsa_*_varlen                 the A5 packed-varlen ("TND") ops taking cu_seqlens_q / cu_seqlens_k:
+ *                                lightning_indexer (converters/kernels/npu_smla.py:754-768),
+ *                                sparse_flash_mla{,_grad} (:457-479, :540-568),
+ *                                sparse_lightning_indexer_kl_loss_grad (:584-598)
  */
 #ifndef DSA_MI355X_H
 #define DSA_MI355X_H
@@ -107,8 +112,10 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, vo
  *             sparse_flash_mla_grad returns the same quantity, converters/kernels/npu_smla.py:540-568)
  *   workspace  device scratch of workspace_bytes (dsa_sparse_mla_bwd_workspace_size() gives the
  *              default; a smaller one processes query rows in more chunks); fp32 dtype needs none
- * The bf16 path needs D_qk = 576, D_v = 512, H <= 128.  dKV is reduced per key without
- * float atomics (bf16 per-(row, slot) contributions summed in fp32 through a key-major CSR).
+ * The bf16 path needs D_qk = 576, D_v = 512, H <= 128.  dKV is reduced per key through a
+ * key-major CSR of the bf16 per-(row, slot) contributions, summed in fp32; only a key whose
+ * list straddles two reduction segments adds its partial sums with fp32 atomics, so dKV
+ * is reproducible to fp32 rounding, not bit for bit.
  */
 int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
                                           int64_t d_qk, int64_t topk);
@@ -161,6 +168,72 @@ int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, co
 int dsa_compressor_fwd(const float* kv, const float* score, const float* ape, const float* norm_weight, void* out,
                        int out_dtype, int64_t batch, int64_t s, int64_t d, int64_t ratio, int overlap,
                        float norm_eps, void* stream);
+
+/*
+ * Block KV compressor over a packed varlen ("TND") batch (reference: Compressor._forward_tnd,
+ * models/deepseek_v4/model.py:223-274).  Block c pools the ratio tokens starting at
+ * block_starts[c] (device int64 [n_blocks], each in [0, n_tokens - ratio]; a start outside
+ * that range yields a zero row); with overlap its first ratio slots are the previous listed
+ * block's first D features when c > 0 and positions[block_starts[c]] >= ratio (device int32
+ * [n_tokens] request-local positions).
+ *   kv, score [n_tokens, coff*D] fp32; out [n_blocks, D] as in dsa_compressor_fwd.
+ */
+int dsa_compressor_fwd_tnd(const float* kv, const float* score, const float* ape, const float* norm_weight,
+                           void* out, int out_dtype, int64_t n_tokens, int64_t d, int64_t ratio, int overlap,
+                           const int64_t* block_starts, int64_t n_blocks, const int32_t* positions, float norm_eps,
+                           void* stream);
+
+/*
+ * Packed varlen ("TND") batches.  n_seq sequences are packed along the token axis:
+ * sequence i owns query tokens [cu_seqlens_q[i], cu_seqlens_q[i+1]) and key tokens
+ * [cu_seqlens_k[i], cu_seqlens_k[i+1]) of the packed tensors (the fixed-length layouts above
+ * with B = 1 and S = total tokens).  cu_seqlens_* are HOST int32 arrays of n_seq + 1
+ * non-decreasing entries starting at 0 (the launch schedule is decided on the host).
+ * Index tensors hold sequence-local key positions (0 = the sequence's first key), -1 for
+ * empty slots.  Within a sequence the causal rule is the fixed-length one aligned
+ * bottom-right: q_offset_i = max(0, len_k_i - len_q_i) for token keys.  Each call runs the
+ * fixed-length kernels once per non-empty sequence, in order, on `stream`, so the
+ * workspace of one call serves every sequence.  A sequence with queries and no keys is an
+ * error, except in the indexer, where its rows get no candidate (-1 padding).
+ */
+
+/* dsa_indexer_fwd + dsa_topk per sequence.  Keys may be compressed (cmp_ratio > 1):
+ * then sequence i has cmp_ratio * len_k_i + cmp_residual_k[i] original key tokens
+ * (cmp_residual_k: host int32 [n_seq] or NULL = 0) and, for sparse_mode 3,
+ * q_offset_i = max(0, that count - len_q_i); sparse_mode 0 applies no causal rule.
+ * scores_ws: device fp32 scratch of ws_bytes (>= 4 * the longest key sequence; a row chunk
+ * of a sequence is scored into it at a time).  indices [T_q, topk] int32, values
+ * [T_q, topk] fp32 or NULL. */
+int dsa_lightning_indexer_varlen(const void* q, const float* q_scale, const void* k, const float* k_scale,
+                                 const float* w, int32_t* indices, float* values, float* scores_ws, int64_t ws_bytes,
+                                 int dtype, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                 const int32_t* cmp_residual_k, int64_t n_seq, int64_t n_heads, int64_t head_dim,
+                                 int64_t topk, int64_t cmp_ratio, int64_t sparse_mode, int64_t index_offset,
+                                 void* stream);
+int dsa_sparse_mla_fwd_varlen(const void* q, const void* kv, const int32_t* indices, void* out, float* softmax_max,
+                              float* softmax_sum, int dtype, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kv,
+                              int64_t n_seq, int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
+                              void* stream);
+/* largest per-sequence dsa_sparse_mla_bwd_workspace_size() of the batch */
+int64_t dsa_sparse_mla_bwd_varlen_workspace_size(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kv,
+                                                 int64_t n_seq, int64_t n_heads, int64_t d_qk, int64_t topk);
+int dsa_sparse_mla_bwd_varlen(const void* q, const void* kv, const int32_t* indices, const void* out,
+                              const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
+                              float* dkv_accum, float* mass, void* workspace, int64_t workspace_bytes, int dtype,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_kv, int64_t n_seq,
+                              int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale, void* stream);
+int dsa_attn_mass_varlen(const void* q, const void* kv, const int32_t* indices, const float* softmax_max,
+                         const float* softmax_sum, float* mass, int dtype, const int32_t* cu_seqlens_q,
+                         const int32_t* cu_seqlens_kv, int64_t n_seq, int64_t n_heads, int64_t d_qk, int64_t topk,
+                         float scale, void* stream);
+/* largest per-sequence dsa_indexer_kl_grad_workspace_size() of the batch */
+int64_t dsa_indexer_kl_grad_varlen_workspace_size(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                                  int64_t n_seq, int64_t n_heads, int64_t head_dim, int64_t topk);
+int dsa_indexer_kl_grad_varlen(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
+                               const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
+                               void* workspace, int64_t workspace_bytes, const int32_t* cu_seqlens_q,
+                               const int32_t* cu_seqlens_k, int64_t n_seq, int64_t n_heads, int64_t head_dim,
+                               int64_t topk, float loss_scale, float eps, float grad_scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -34,8 +34,12 @@ follows (paths relative to the reference repository root):
                            + softmax-gated pooling + RMSNorm)
 * ``window_topk_idxs``     models/deepseek_v4/model.py:467-471
 * ``compress_topk_idxs``   models/deepseek_v4/model.py:483-488
+* ``compressor_pool_tnd``  models/deepseek_v4/model.py:223-274 (Compressor._forward_tnd:
+                           blocks gathered at block_starts, has_prev_block guard)
 * ``lengths_to_cu_seqlens``, ``tnd_compressed_block_starts``
                            models/deepseek_v4/tnd.py:32-38, :87-94
+* ``varlen_split``         per-sequence slices of a packed (TND) batch; the
+                           varlen reference result is the per-sequence one
 
 Which check pins each function (tests/test_oracle.py):
 
@@ -54,6 +58,9 @@ Which check pins each function (tests/test_oracle.py):
   ``loss / (B*S)`` scaling.
 * compressor_pool: uniform gates give the mean pool; first block gets no
   overlap contribution; r == 1 without overlap is the identity.
+* compressor_pool_tnd: one request whose length is a multiple of r equals
+  compressor_pool on it; several such requests equal compressor_pool per request
+  (the has_prev_block guard restarts the overlap at each request).
 * TND metadata: the known answers of the reference's
   tests/unit_tests/models/test_deepseek_v4_tnd.py:65-79.
 """
@@ -84,6 +91,8 @@ __all__ = [
     "compress_topk_idxs",
     "lengths_to_cu_seqlens",
     "tnd_compressed_block_starts",
+    "compressor_pool_tnd",
+    "varlen_split",
     "quantize_e4m3_per_row",
 ]
 
@@ -450,6 +459,52 @@ def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, no
     x = pooled.to(out_dtype or torch.float32).float()
     rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm_eps)
     return x * rms * norm_weight.float()
+
+
+def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions, *, overlap=None, norm_weight=None,
+                        norm_eps=1e-6, out_dtype=None):
+    """Compressor._forward_tnd pooling (models/deepseek_v4/model.py:223-265).
+
+    kv, score: [T,coff*D] fp32 projections of the packed tokens; block c pools tokens
+    block_starts[c] + [0, r).  With overlap, slots 0..r-1 take the PREVIOUS LISTED
+    block's features 0..D (:248-249) unless the block's position is < r (the
+    has_prev_block guard, :252-262) or it is the first block; those slots are kv=0,
+    score=-inf.  Returns [n_blocks,D] fp32 (RMSNorm'd like compressor_pool with
+    ``norm_weight``).
+    """
+    if overlap is None:
+        overlap = ratio == 4
+    T, CD = kv.shape
+    coff = 2 if overlap else 1
+    D = CD // coff
+    bs = block_starts.long()
+    rows = bs.unsqueeze(1) + torch.arange(ratio).unsqueeze(0)  # [n, r]
+    kvb = kv.float()[rows]  # [n, r, coff*D]
+    sc = score.float()[rows] + ape.float()
+    if overlap:
+        n = bs.numel()
+        kv2 = kvb.new_zeros(n, 2 * ratio, D)
+        sc2 = sc.new_full((n, 2 * ratio, D), float("-inf"))
+        kv2[:, ratio:] = kvb[..., D:]
+        sc2[:, ratio:] = sc[..., D:]
+        kv2[1:, :ratio] = kvb[:-1, :, :D]
+        sc2[1:, :ratio] = sc[:-1, :, :D]
+        has_prev = positions.reshape(-1)[bs].ge(ratio).view(-1, 1, 1)
+        kv2[:, :ratio] = torch.where(has_prev, kv2[:, :ratio], torch.zeros_like(kv2[:, :ratio]))
+        sc2[:, :ratio] = torch.where(has_prev, sc2[:, :ratio], torch.full_like(sc2[:, :ratio], float("-inf")))
+        kvb, sc = kv2, sc2
+    pooled = (kvb * sc.softmax(dim=1)).sum(dim=1)
+    if norm_weight is None:
+        return pooled
+    x = pooled.to(out_dtype or torch.float32).float()
+    rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm_eps)
+    return x * rms * norm_weight.float()
+
+
+def varlen_split(packed: torch.Tensor, cu_seqlens) -> list[torch.Tensor]:
+    """The per-sequence slices packed[cu[i]:cu[i+1]] of a TND tensor."""
+    cu = [int(v) for v in (cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens)]
+    return [packed[a:b] for a, b in zip(cu[:-1], cu[1:])]
 
 
 # ---------------------------------------------------------------------------

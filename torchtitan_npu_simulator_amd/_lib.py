@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -49,6 +49,36 @@ _SIGNATURES = {
         _i32,
     ),
     "dsa_compressor_fwd": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),
+    "dsa_compressor_fwd_tnd": (
+        [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _f32, _vp],
+        _i32,
+    ),
+    # packed varlen: cu_seqlens / cmp_residual_k are host int32 arrays (ctypes arrays or None)
+    "dsa_lightning_indexer_varlen": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _vp],
+        _i32,
+    ),
+    "dsa_sparse_mla_fwd_varlen": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f32, _vp],
+        _i32,
+    ),
+    "dsa_sparse_mla_bwd_varlen_workspace_size": ([_vp, _vp, _i64, _i64, _i64, _i64], _i64),
+    "dsa_sparse_mla_bwd_varlen": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+         _f32, _vp],
+        _i32,
+    ),
+    "dsa_attn_mass_varlen": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
+        _i32,
+    ),
+    "dsa_indexer_kl_grad_varlen_workspace_size": ([_vp, _vp, _i64, _i64, _i64, _i64], _i64),
+    "dsa_indexer_kl_grad_varlen": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _f32,
+         _vp],
+        _i32,
+    ),
 }
 
 _lib = None
@@ -90,6 +120,16 @@ def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load_library().dsa_last_error().decode(errors="replace")
         raise DSAError(f"{what} failed (status {rc}): {msg}")
+
+
+def host_i32(values) -> ctypes.Array | None:
+    """A host int32 array (ctypes) of ``values`` (a list or CPU/GPU tensor), or None."""
+    if values is None:
+        return None
+    if isinstance(values, torch.Tensor):
+        values = values.detach().to("cpu", torch.int64).tolist()
+    vals = [int(v) for v in values]
+    return (ctypes.c_int32 * len(vals))(*vals)
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -8,6 +8,11 @@
 //                   x = kv[b, c*r + i-r, D + f],   g = score[...] + ape[i-r, D + f]
 // then optionally RMSNorm over f of the bf16-rounded pooled row times norm_weight.
 //
+// Packed varlen ("TND") batches give each block's first token explicitly (block_starts,
+// whole r-token blocks inside one request): block c pools tokens block_starts[c] + i, and
+// with overlap its first r slots come from the previous listed block, block_starts[c-1],
+// when c > 0 and the block's position (positions[block_starts[c]]) is at least r.
+//
 // HBM-bound streaming: a row group of D/4 lanes owns one compressed block, each lane four
 // consecutive features (16-byte loads, coalesced along the row); a 256-lane workgroup
 // holds 256 / (D/4) row groups.  Each input row is read once per block that uses it (the
@@ -23,7 +28,8 @@ constexpr int kThreads = 256;
 __global__ void __launch_bounds__(kThreads)
 compressor_kernel(const float* __restrict__ kv, const float* __restrict__ score, const float* __restrict__ ape,
                   const float* __restrict__ norm_w, void* __restrict__ out, int out_bf16, int64_t n_blocks_total,
-                  int nb, int D, int r, int overlap, float eps) {
+                  int nb, int D, int r, int overlap, float eps, const int64_t* __restrict__ block_starts,
+                  const int32_t* __restrict__ positions, int64_t n_tokens) {
   extern __shared__ float red[];  // [row groups][lanes_per_group / 64 + 1]
   const int lanes = D / 4;        // lanes per row group
   const int groups = kThreads / lanes;
@@ -59,17 +65,33 @@ compressor_kernel(const float* __restrict__ kv, const float* __restrict__ score,
       m[u] = mn;
     }
   };
+  // first token of the block and of the block whose first half overlaps it
+  int64_t cur = 0, prev = 0;
+  bool has_prev = false, usable = active;
   if (active) {
-    const int64_t base = (b * (int64_t)nb * r) * row_elems;
-    if (overlap && c > 0) {
+    if (block_starts) {
+      cur = block_starts[c];
+      usable = cur >= 0 && cur <= n_tokens - r;  // out-of-range starts pool nothing
+      if (usable && overlap && c > 0 && positions[cur] >= r) {
+        prev = block_starts[c - 1];
+        has_prev = prev >= 0 && prev <= n_tokens - r;
+      }
+    } else {
+      cur = b * (int64_t)nb * r + (int64_t)c * r;
+      prev = cur - r;
+      has_prev = overlap && c > 0;
+    }
+  }
+  if (usable) {
+    if (has_prev) {
       for (int i = 0; i < r; ++i) {
-        const int64_t row = base + (int64_t)((c - 1) * r + i) * row_elems;
+        const int64_t row = (prev + i) * row_elems;
         consume(kv + row + f, score + row + f, ape + (int64_t)i * row_elems + f);
       }
     }
     const int off = overlap ? D : 0;
     for (int i = 0; i < r; ++i) {
-      const int64_t row = base + (int64_t)(c * r + i) * row_elems;
+      const int64_t row = (cur + i) * row_elems;
       consume(kv + row + off + f, score + row + off + f, ape + (int64_t)i * row_elems + off + f);
     }
   }
@@ -146,6 +168,35 @@ extern "C" int dsa_compressor_fwd(const float* kv, const float* score, const flo
   const size_t shm = (size_t)groups * ((lanes + 63) / 64 + 1) * sizeof(float);
   compressor_kernel<<<(unsigned)grid, kThreads, shm, (hipStream_t)stream>>>(
       kv, score, ape, norm_weight, out, out_dtype == DSA_BF16, total, (int)nb, (int)d, (int)ratio, overlap ? 1 : 0,
-      norm_eps);
+      norm_eps, nullptr, nullptr, batch * s);
   return check_launch("dsa_compressor_fwd");
+}
+
+extern "C" int dsa_compressor_fwd_tnd(const float* kv, const float* score, const float* ape,
+                                      const float* norm_weight, void* out, int out_dtype, int64_t n_tokens, int64_t d,
+                                      int64_t ratio, int overlap, const int64_t* block_starts, int64_t n_blocks,
+                                      const int32_t* positions, float norm_eps, void* stream) {
+  using namespace dsa;
+  if (!kv || !score || !ape || !out || (n_blocks > 0 && !block_starts))
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd_tnd: null pointer");
+  if (overlap && !positions)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd_tnd: overlap needs the token positions");
+  if (n_tokens <= 0 || d <= 0 || ratio <= 0 || n_blocks < 0)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd_tnd: bad sizes");
+  if (d < 4 || d > 4 * kThreads || (d & (d - 1)) != 0)
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_compressor_fwd_tnd: D=%lld (needs a power of two in [4, 1024])",
+                     (long long)d);
+  if (out_dtype != DSA_F32 && out_dtype != DSA_BF16)
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_compressor_fwd_tnd: out dtype %d", out_dtype);
+  if (n_blocks > INT32_MAX || ratio > 65536)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd_tnd: sizes out of range");
+  if (n_blocks == 0) return DSA_OK;
+  const int lanes = (int)(d / 4);
+  const int groups = kThreads / lanes;
+  const int64_t grid = (n_blocks + groups - 1) / groups;
+  const size_t shm = (size_t)groups * ((lanes + 63) / 64 + 1) * sizeof(float);
+  compressor_kernel<<<(unsigned)grid, kThreads, shm, (hipStream_t)stream>>>(
+      kv, score, ape, norm_weight, out, out_dtype == DSA_BF16, n_blocks, (int)n_blocks, (int)d, (int)ratio,
+      overlap ? 1 : 0, norm_eps, block_starts, positions, n_tokens);
+  return check_launch("dsa_compressor_fwd_tnd");
 }

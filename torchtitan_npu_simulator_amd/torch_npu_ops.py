@@ -11,10 +11,18 @@ reference's ``converters/kernels/dsa.py`` (paths relative to the reference repos
 Every op runs on the HIP library (``libdsa_mi355x.so``) on the tensors' GPU and raises
 if the library or a GPU is missing; nothing here computes on the CPU.
 
-Layout "BSND" throughout.  ``sparse_mode`` 3 is the causal rule aligned bottom-right
+Layouts "BSND" and "TND".  ``sparse_mode`` 3 is the causal rule aligned bottom-right
 (query row s may see key t <= s + (S_k - S_q)); 0 means no causal mask.  An explicit
 ``q_offset`` overrides it (one GPU's context-parallel share sees Q rows starting at
 ``q_offset`` against the KV prefix).
+
+"TND" packs sequences along the token axis (query [T,N,D], key [T_k,1,D], indices
+[T,1,K] holding sequence-local key positions).  Its sequence boundaries come either as
+``actual_seq_lengths_*`` in torch_npu's TND convention (cumulative END offsets, one per
+sequence, the last equal to T) or as ``cu_seqlens_*`` (``[0, ends...]``, the A5 ops'
+convention, converters/kernels/npu_smla.py:457-479, :754-768).  In "BSND",
+``actual_seq_lengths_*`` are per-batch valid lengths: rows past a batch's query length
+get no selection (-1) and keys past its key length are never candidates.
 """
 
 from __future__ import annotations
@@ -24,7 +32,7 @@ import math
 import torch
 
 from . import _lib
-from ._lib import check, load_library, ptr, require_gpu_tensor, stream_of
+from ._lib import check, host_i32, load_library, ptr, require_gpu_tensor, stream_of
 
 __all__ = [
     "npu_lightning_indexer",
@@ -38,6 +46,13 @@ __all__ = [
     "topk_select",
     "quantize_fp8_per_row",
     "compressor_pool",
+    "compressor_pool_tnd",
+    "lightning_indexer_varlen",
+    "sparse_mla_fwd_varlen",
+    "sparse_mla_bwd_varlen",
+    "attn_mass_varlen",
+    "indexer_kl_grad_from_mass_varlen",
+    "to_cu_seqlens",
 ]
 
 _SCORE_BUDGET_BYTES = 1 << 30  # fp32 score rows materialised per indexer chunk
@@ -52,6 +67,25 @@ def _resolve_q_offset(sparse_mode: int, s_q: int, s_k_tokens: int, q_offset: int
     if sparse_mode == 0:
         return _NO_MASK_OFFSET
     raise ValueError(f"sparse_mode={sparse_mode} is not supported (0 or 3)")
+
+
+def to_cu_seqlens(cu_seqlens=None, actual_seq_lengths=None, total=None) -> list[int]:
+    """Host ``[0, end_0, end_1, ...]`` from A5-style ``cu_seqlens`` or torch_npu-style TND
+    ``actual_seq_lengths`` (cumulative ends); checks the last end against ``total``."""
+    if cu_seqlens is not None:
+        cu = [int(v) for v in (cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens)]
+        if not cu or cu[0] != 0:
+            raise ValueError("cu_seqlens must start with 0")
+    elif actual_seq_lengths is not None:
+        ends = actual_seq_lengths.tolist() if isinstance(actual_seq_lengths, torch.Tensor) else actual_seq_lengths
+        cu = [0] + [int(v) for v in ends]
+    else:
+        raise ValueError("TND layout needs cu_seqlens or actual_seq_lengths")
+    if any(b < a for a, b in zip(cu[:-1], cu[1:])):
+        raise ValueError(f"sequence boundaries must be non-decreasing: {cu}")
+    if total is not None and cu[-1] != total:
+        raise ValueError(f"sequence boundaries end at {cu[-1]} but the packed tensor has {total} tokens")
+    return cu
 
 
 # ---------------------------------------------------------------------------
@@ -128,6 +162,9 @@ def npu_lightning_indexer(
     key_scale=None,
     q_offset=None,
     index_offset=0,
+    cu_seqlens_q=None,
+    cu_seqlens_k=None,
+    cmp_residual_k=None,
 ):
     """Fused lightning indexer + per-query top-k.
 
@@ -137,11 +174,27 @@ def npu_lightning_indexer(
     sparse_values fp32 [B,S,1,K] or None): the chosen key indices in ascending order with
     -1 padding (reference binding shape: lightning_indexer/binding.cpp:28).  Rows are
     processed in chunks so the fp32 score buffer stays under 1 GiB.
+
+    TND: query [T,H_I,D_I], key [T_k,1,D_I], weights [T,H_I], scales [T,H_I] / [T_k];
+    returns [T,1,K] with sequence-local indices (see ``lightning_indexer_varlen``).
     """
-    if layout_query != "BSND" or layout_key != "BSND":
-        raise NotImplementedError("only the BSND layout is supported")
-    if block_table is not None or actual_seq_lengths_query is not None or actual_seq_lengths_key is not None:
-        raise NotImplementedError("paged / varlen indexer inputs are not supported by this op (use dsa.varlen)")
+    if block_table is not None:
+        raise NotImplementedError("paged KV (block_table) is not supported")
+    if layout_query not in ("BSND", "TND") or layout_key != layout_query:
+        raise NotImplementedError(f"layouts {layout_query}/{layout_key} (BSND/BSND or TND/TND)")
+    if layout_query == "TND":
+        kt = key.reshape(key.shape[0], key.shape[-1])
+        cu_q = to_cu_seqlens(cu_seqlens_q, actual_seq_lengths_query, query.shape[0])
+        cu_k = to_cu_seqlens(cu_seqlens_k, actual_seq_lengths_key, kt.shape[0])
+        idx, vals = lightning_indexer_varlen(query, kt, weights, cu_q, cu_k, sparse_count, sparse_mode=sparse_mode,
+                                             cmp_ratio=cmp_ratio, cmp_residual_k=cmp_residual_k,
+                                             return_value=return_value, query_scale=query_scale, key_scale=key_scale,
+                                             index_offset=index_offset)
+        return idx.unsqueeze(1), (vals.unsqueeze(1) if return_value else None)
+    if actual_seq_lengths_query is not None or actual_seq_lengths_key is not None:
+        return _bsnd_lengths_indexer(query, key, weights, actual_seq_lengths_query, actual_seq_lengths_key,
+                                     sparse_count, sparse_mode, cmp_ratio, return_value, query_scale, key_scale,
+                                     index_offset)
     k3 = key.squeeze(2) if key.dim() == 4 else key
     B, S, H, D = query.shape
     s_k = k3.shape[1]
@@ -165,6 +218,89 @@ def npu_lightning_indexer(
             if return_value:
                 vals[b, r0:r1] = v_b[0]
     return idx.unsqueeze(2), (vals.unsqueeze(2) if return_value else None)
+
+
+def _bsnd_lengths_indexer(query, key, weights, len_q, len_k, sparse_count, sparse_mode, cmp_ratio, return_value,
+                          query_scale, key_scale, index_offset):
+    """BSND with per-batch valid lengths: batch b is one sequence of its first len_q[b]
+    queries and len_k[b] keys; its padded rows select nothing (-1)."""
+    k3 = key.squeeze(2) if key.dim() == 4 else key
+    B, S = query.shape[:2]
+    s_k = k3.shape[1]
+    lq = [S] * B if len_q is None else [int(v) for v in (len_q.tolist() if isinstance(len_q, torch.Tensor) else len_q)]
+    lk = [s_k] * B if len_k is None else [int(v) for v in (len_k.tolist() if isinstance(len_k, torch.Tensor) else len_k)]
+    if len(lq) != B or len(lk) != B or any(not 0 <= v <= S for v in lq) or any(not 0 <= v <= s_k for v in lk):
+        raise ValueError(f"actual sequence lengths {lq} / {lk} do not fit B={B}, S={S}, S_k={s_k}")
+    K = int(sparse_count)
+    idx = torch.full((B, S, K), -1, dtype=torch.int32, device=query.device)
+    vals = torch.full((B, S, K), float("-inf"), dtype=torch.float32, device=query.device) if return_value else None
+    for b in range(B):
+        if lq[b] == 0:
+            continue
+        qs = None if query_scale is None else query_scale[b, : lq[b]]
+        ks = None if key_scale is None else key_scale[b, : lk[b]]
+        i_b, v_b = lightning_indexer_varlen(query[b, : lq[b]], k3[b, : lk[b]], weights[b, : lq[b]], [0, lq[b]],
+                                            [0, lk[b]], K, sparse_mode=sparse_mode, cmp_ratio=cmp_ratio,
+                                            return_value=return_value, query_scale=qs, key_scale=ks,
+                                            index_offset=index_offset)
+        idx[b, : lq[b]] = i_b
+        if return_value:
+            vals[b, : lq[b]] = v_b
+    return idx.unsqueeze(2), (vals.unsqueeze(2) if return_value else None)
+
+
+def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sparse_count, *, sparse_mode=3,
+                             cmp_ratio=1, cmp_residual_k=None, return_value=False, query_scale=None, key_scale=None,
+                             index_offset=0):
+    """Indexer scores + top-k over a packed varlen batch (dsa_lightning_indexer_varlen).
+
+    query [T,H_I,D_I], key [T_k,D_I] (bf16, or fp8-e4m3fn with query_scale [T,H_I] and
+    key_scale [T_k]), weights [T,H_I].  Sequence i's queries see its own keys only;
+    indices are sequence-local (+ index_offset), -1 padded.  With compressed keys
+    (cmp_ratio > 1), ``cmp_residual_k[i]`` original tokens follow the last whole block.
+    Returns (indices int32 [T,K], values fp32 [T,K] or None).
+    """
+    lib = load_library()
+    for t, n in ((query, "query"), (key, "key"), (weights, "weights")):
+        require_gpu_tensor(t, n)
+    key = key.reshape(key.shape[0], key.shape[-1])
+    T, H, D = query.shape
+    T_k = key.shape[0]
+    if query.dtype != key.dtype:
+        raise ValueError("query and key must share a dtype")
+    cu_q = to_cu_seqlens(cu_seqlens_q, None, T)
+    cu_k = to_cu_seqlens(cu_seqlens_k, None, T_k)
+    if len(cu_q) != len(cu_k):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k describe different numbers of sequences")
+    n_seq = len(cu_q) - 1
+    res = None
+    if cmp_residual_k is not None:
+        res = [int(v) for v in (cmp_residual_k.tolist() if isinstance(cmp_residual_k, torch.Tensor)
+                                else cmp_residual_k)]
+        if len(res) != n_seq:
+            raise ValueError("cmp_residual_k needs one entry per sequence")
+    q = query.contiguous()
+    k = key.contiguous()
+    w = weights.float().contiguous()
+    qs = None if query_scale is None else query_scale.float().contiguous()
+    ks = None if key_scale is None else key_scale.float().contiguous()
+    K = int(sparse_count)
+    idx = torch.empty(T, K, dtype=torch.int32, device=q.device)
+    vals = torch.empty(T, K, dtype=torch.float32, device=q.device) if return_value else None
+    max_k = max(max(b - a for a, b in zip(cu_k[:-1], cu_k[1:])), 1)
+    max_q = max(max(b - a for a, b in zip(cu_q[:-1], cu_q[1:])), 1)
+    rows = max(1, min(max_q, _SCORE_BUDGET_BYTES // (4 * max_k)))
+    ws = torch.empty(rows * max_k, dtype=torch.float32, device=q.device)
+    if T == 0:
+        return idx, vals
+    check(
+        lib.dsa_lightning_indexer_varlen(ptr(q), ptr(qs), ptr(k), ptr(ks), ptr(w), ptr(idx), ptr(vals), ptr(ws),
+                                         ws.numel() * 4, _lib.dtype_code(q.dtype), host_i32(cu_q), host_i32(cu_k),
+                                         host_i32(res), n_seq, H, D, K, int(cmp_ratio), int(sparse_mode),
+                                         int(index_offset), stream_of(q.device)),
+        "dsa_lightning_indexer_varlen",
+    )
+    return idx, vals
 
 
 # ---------------------------------------------------------------------------
@@ -244,6 +380,90 @@ def attn_mass(q, kv, indices, smax, ssum, scale, *, q_offset=0):
     return mass
 
 
+def _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, T_kv):
+    cu_q = to_cu_seqlens(cu_seqlens_q, None, T)
+    cu_k = to_cu_seqlens(cu_seqlens_kv, None, T_kv)
+    if len(cu_q) != len(cu_k):
+        raise ValueError("cu_seqlens_q and cu_seqlens_kv describe different numbers of sequences")
+    return cu_q, cu_k, len(cu_q) - 1
+
+
+def sparse_mla_fwd_varlen(q, kv, indices, scale, cu_seqlens_q, cu_seqlens_kv, *, d_v=512):
+    """Packed varlen forward (dsa_sparse_mla_fwd_varlen): q [T,H,D_qk], kv [T_kv,D_qk],
+    indices [T,K] sequence-local; returns (out [T,H,d_v], softmax_max [T,H], softmax_sum [T,H])."""
+    lib = load_library()
+    require_gpu_tensor(q, "q")
+    T, H, D = q.shape
+    kv = kv.reshape(kv.shape[0], kv.shape[-1]).contiguous()
+    cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, kv.shape[0])
+    K = indices.shape[-1]
+    q = q.contiguous()
+    indices = indices.reshape(T, K).to(torch.int32).contiguous()
+    out = torch.empty(T, H, d_v, dtype=q.dtype, device=q.device)
+    smax = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    ssum = torch.empty(T, H, dtype=torch.float32, device=q.device)
+    if T:
+        check(
+            lib.dsa_sparse_mla_fwd_varlen(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(smax), ptr(ssum),
+                                          _lib.dtype_code(q.dtype), host_i32(cu_q), host_i32(cu_k), n_seq, H, D, d_v,
+                                          K, float(scale), stream_of(q.device)),
+            "dsa_sparse_mla_fwd_varlen",
+        )
+    return out, smax, ssum
+
+
+def sparse_mla_bwd_varlen(q, kv, indices, out, dout, smax, ssum, scale, cu_seqlens_q, cu_seqlens_kv, *,
+                          return_mass=False, workspace_bytes=None):
+    """Packed varlen backward (dsa_sparse_mla_bwd_varlen): (dq like q, dkv fp32 [T_kv,D_qk])
+    and, with ``return_mass``, the head-summed attention mass [T,K] fp32."""
+    lib = load_library()
+    T, H, D = q.shape
+    kv = kv.reshape(kv.shape[0], kv.shape[-1]).contiguous()
+    T_kv = kv.shape[0]
+    cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, T_kv)
+    K = indices.shape[-1]
+    d_v = out.shape[-1]
+    q, out, dout = (t.contiguous() for t in (q, out, dout))
+    indices = indices.reshape(T, K).to(torch.int32).contiguous()
+    dq = torch.empty_like(q)
+    dkv = torch.zeros(T_kv, D, dtype=torch.float32, device=q.device)
+    mass = torch.empty(T, K, dtype=torch.float32, device=q.device) if return_mass else None
+    hq, hk = host_i32(cu_q), host_i32(cu_k)
+    ws_bytes = int(lib.dsa_sparse_mla_bwd_varlen_workspace_size(hq, hk, n_seq, H, D, K))
+    if workspace_bytes is not None:
+        ws_bytes = int(workspace_bytes)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    if T:
+        check(
+            lib.dsa_sparse_mla_bwd_varlen(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax.contiguous()),
+                                          ptr(ssum.contiguous()), ptr(dq), ptr(dkv), ptr(mass), ptr(ws), ws_bytes,
+                                          _lib.dtype_code(q.dtype), hq, hk, n_seq, H, D, d_v, K, float(scale),
+                                          stream_of(q.device)),
+            "dsa_sparse_mla_bwd_varlen",
+        )
+    return (dq, dkv, mass) if return_mass else (dq, dkv)
+
+
+def attn_mass_varlen(q, kv, indices, smax, ssum, scale, cu_seqlens_q, cu_seqlens_kv):
+    """Head-summed softmax mass [T,K] of a packed varlen batch (dsa_attn_mass_varlen)."""
+    lib = load_library()
+    T, H, D = q.shape
+    kv = kv.reshape(kv.shape[0], kv.shape[-1]).contiguous()
+    cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, kv.shape[0])
+    K = indices.shape[-1]
+    q = q.contiguous()
+    indices = indices.reshape(T, K).to(torch.int32).contiguous()
+    mass = torch.empty(T, K, dtype=torch.float32, device=q.device)
+    if T:
+        check(
+            lib.dsa_attn_mass_varlen(ptr(q), ptr(kv), ptr(indices), ptr(smax.contiguous()), ptr(ssum.contiguous()),
+                                     ptr(mass), _lib.dtype_code(q.dtype), host_i32(cu_q), host_i32(cu_k), n_seq, H, D,
+                                     K, float(scale), stream_of(q.device)),
+            "dsa_attn_mass_varlen",
+        )
+    return mass
+
+
 def _packed_view(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor | None:
     """If ``a`` and ``b`` are the two halves of one contiguous last-dim split, return the whole."""
     if a.dtype != b.dtype or a.shape[:-1] != b.shape[:-1] or a.stride() != b.stride() or a.stride(-1) != 1:
@@ -285,6 +505,30 @@ class _SparseFlashAttention(torch.autograd.Function):
         return dq[..., :dnope], dkv[..., :dnope], dq[..., dnope:], dkv[..., dnope:], None, None, None
 
 
+class _SparseFlashAttentionTND(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q_nope, k_nope, q_pe, k_pe, indices, scale, cu_q, cu_k):
+        q = _cat_last(q_nope, q_pe)  # [T,H,576]
+        kv = _cat_last(k_nope, k_pe)  # [T_kv,1,576]
+        kv2 = kv.reshape(kv.shape[0], kv.shape[-1])
+        out, smax, ssum = sparse_mla_fwd_varlen(q, kv2, indices, scale, cu_q, cu_k, d_v=q_nope.shape[-1])
+        ctx.save_for_backward(q, kv2, indices, out, smax, ssum)
+        ctx.scale = scale
+        ctx.cu = (cu_q, cu_k)
+        ctx.split = (q_nope.shape[-1], q_pe.shape[-1])
+        ctx.kv_shape = kv.shape
+        ctx.mark_non_differentiable(smax, ssum)
+        return out, smax, ssum
+
+    @staticmethod
+    def backward(ctx, dout, _dmax, _dsum):
+        q, kv2, indices, out, smax, ssum = ctx.saved_tensors
+        dq, dkv = sparse_mla_bwd_varlen(q, kv2, indices, out, dout.contiguous(), smax, ssum, ctx.scale, *ctx.cu)
+        dnope, _ = ctx.split
+        dkv = dkv.to(kv2.dtype).reshape(ctx.kv_shape)
+        return dq[..., :dnope], dkv[..., :dnope], dq[..., dnope:], dkv[..., dnope:], None, None, None, None
+
+
 def npu_sparse_flash_attention(
     query,
     key,
@@ -301,6 +545,10 @@ def npu_sparse_flash_attention(
     attention_mode=2,
     return_softmax_lse=True,
     *,
+    actual_seq_lengths_query=None,
+    actual_seq_lengths_kv=None,
+    cu_seqlens_q=None,
+    cu_seqlens_kv=None,
     q_offset=None,
 ):
     """Gathered sparse MLA attention in absorb mode (attention_mode=2).
@@ -310,13 +558,28 @@ def npu_sparse_flash_attention(
     sparse_indices [B,S,1,K] int32 (-1 = empty).  Returns (out [B,S,H,512], softmax_max
     [B,S,H], softmax_sum [B,S,H]); differentiable in query/key/query_rope/key_rope, with
     the value gradient folded into the key gradient (dKV_latent = dK_nope + dV).
+
+    TND: query [T,H,512], key [T_kv,1,512], ropes [T,H,64] / [T_kv,1,64], sparse_indices
+    [T,1,K] sequence-local; sequences from ``actual_seq_lengths_*`` (cumulative ends) or
+    ``cu_seqlens_*``; causal within each sequence (sparse_mode 3).
     """
     if attention_mode != 2:
         raise NotImplementedError("only attention_mode=2 (MLA absorb) is supported")
-    if layout_query != "BSND" or layout_kv != "BSND" or block_table is not None or sparse_block_size != 1:
-        raise NotImplementedError("BSND, sparse_block_size=1, no block_table")
+    if block_table is not None or sparse_block_size != 1:
+        raise NotImplementedError("sparse_block_size=1 and no block_table")
+    if layout_query not in ("BSND", "TND") or layout_kv != layout_query:
+        raise NotImplementedError(f"layouts {layout_query}/{layout_kv} (BSND/BSND or TND/TND)")
     if query_rope is None or key_rope is None:
         raise ValueError("query_rope and key_rope are required in absorb mode")
+    if layout_query == "TND":
+        if sparse_mode != 3 or q_offset is not None:
+            raise NotImplementedError("TND runs the per-sequence causal rule (sparse_mode=3) only")
+        cu_q = to_cu_seqlens(cu_seqlens_q, actual_seq_lengths_query, query.shape[0])
+        cu_k = to_cu_seqlens(cu_seqlens_kv, actual_seq_lengths_kv, key.shape[0])
+        idx = sparse_indices.reshape(query.shape[0], -1)
+        return _SparseFlashAttentionTND.apply(query, key, query_rope, key_rope, idx, float(scale_value), cu_q, cu_k)
+    if actual_seq_lengths_query is not None or actual_seq_lengths_kv is not None:
+        raise NotImplementedError("BSND with actual_seq_lengths: pack the batch as TND instead")
     s_kv = key.shape[1]
     q_off = _resolve_q_offset(sparse_mode, query.shape[1], s_kv, q_offset)
     idx = sparse_indices.reshape(query.shape[0], query.shape[1], -1)
@@ -348,6 +611,8 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     loss_scale=1.0,
     eps=1e-8,
     grad_scale=1.0,
+    cu_seqlens_q=None,
+    cu_seqlens_k=None,
 ):
     """(d_query_index fp32, d_key_index fp32, d_weights fp32, loss fp32[1]) of the indexer KL loss.
 
@@ -355,9 +620,24 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     key_rope, softmax_max, softmax_sum) at the selected keys; ``loss`` is the token SUM
     (the caller divides by B*S, reference dsa.py:73).
     """
-    if actual_seq_qlen is not None or actual_seq_klen is not None or layout != "BSND":
-        raise NotImplementedError("BSND without actual_seq_* only")
-    lib = load_library()
+    if layout == "TND":
+        if sparse_mode != 3 or q_offset is not None:
+            raise NotImplementedError("TND runs the per-sequence causal rule (sparse_mode=3) only")
+        q = _cat_last(query, query_rope) if query_rope is not None else query.contiguous()
+        kv = _cat_last(key, key_rope) if key_rope is not None else key.contiguous()
+        kv2 = kv.reshape(kv.shape[0], kv.shape[-1])
+        cu_q = to_cu_seqlens(cu_seqlens_q, actual_seq_qlen, q.shape[0])
+        cu_k = to_cu_seqlens(cu_seqlens_k, actual_seq_klen, kv2.shape[0])
+        idx = sparse_indices.reshape(q.shape[0], -1).to(torch.int32).contiguous()
+        mass = attn_mass_varlen(q, kv2, idx, softmax_max, softmax_sum, scale_value, cu_q, cu_k)
+        dq_i, dk_i, dw, loss_rows = indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, idx, mass, cu_q,
+                                                                     cu_k, loss_scale=loss_scale, eps=eps,
+                                                                     grad_scale=grad_scale)
+        return dq_i, dk_i.reshape(key_index.shape), dw, loss_rows.sum().reshape(1)
+    if layout != "BSND":
+        raise NotImplementedError(f"layout {layout} (BSND or TND)")
+    if actual_seq_qlen is not None or actual_seq_klen is not None:
+        raise NotImplementedError("BSND with actual_seq_*: pack the batch as TND instead")
     q = _cat_last(query, query_rope) if query_rope is not None else query.contiguous()
     kv = _cat_last(key, key_rope) if key_rope is not None else key.contiguous()
     B, S, H, D = q.shape
@@ -401,6 +681,40 @@ def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, 
     return dq_i, dk_i, dw, loss_rows
 
 
+def indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, indices, mass, cu_seqlens_q, cu_seqlens_k, *,
+                                     loss_scale=1.0, eps=1e-8, grad_scale=1.0):
+    """Packed varlen indexer KL gradients (dsa_indexer_kl_grad_varlen): query_index
+    [T,H_I,D_I], key_index [T_k,D_I] (or [T_k,1,D_I]), weight [T,H_I], indices [T,K]
+    sequence-local, mass [T,K].  Returns (dq_idx [T,H_I,D_I], dk_idx [T_k,D_I], dw [T,H_I],
+    loss_rows [T]), all fp32."""
+    lib = load_library()
+    qi = query_index.to(torch.bfloat16).contiguous()
+    ki = key_index.reshape(key_index.shape[0], key_index.shape[-1]).to(torch.bfloat16).contiguous()
+    w = weight.float().contiguous()
+    T, HI, DI = qi.shape
+    T_k = ki.shape[0]
+    cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_k, T, T_k)
+    idx = indices.reshape(T, -1).to(torch.int32).contiguous()
+    K = idx.shape[-1]
+    mass = mass.float().contiguous()
+    dev = qi.device
+    dq_i = torch.empty(T, HI, DI, dtype=torch.float32, device=dev)
+    dk_i = torch.zeros(T_k, DI, dtype=torch.float32, device=dev)
+    dw = torch.empty(T, HI, dtype=torch.float32, device=dev)
+    loss_rows = torch.empty(T, dtype=torch.float32, device=dev)
+    hq, hk = host_i32(cu_q), host_i32(cu_k)
+    ws_bytes = int(lib.dsa_indexer_kl_grad_varlen_workspace_size(hq, hk, n_seq, HI, DI, K))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    if T:
+        check(
+            lib.dsa_indexer_kl_grad_varlen(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i),
+                                           ptr(dw), ptr(loss_rows), ptr(ws), ws_bytes, hq, hk, n_seq, HI, DI, K,
+                                           float(loss_scale), float(eps), float(grad_scale), stream_of(dev)),
+            "dsa_indexer_kl_grad_varlen",
+        )
+    return dq_i, dk_i, dw, loss_rows
+
+
 # ---------------------------------------------------------------------------
 # block KV compressor (V4)
 # ---------------------------------------------------------------------------
@@ -430,6 +744,46 @@ def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, no
         lib.dsa_compressor_fwd(ptr(kv), ptr(score), ptr(ape), ptr(nw), ptr(out), _lib.dtype_code(out_dtype), B, S, D,
                                int(ratio), int(bool(overlap)), float(norm_eps), stream_of(kv.device)),
         "dsa_compressor_fwd",
+    )
+    return out
+
+
+def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions=None, *, overlap=None, norm_weight=None,
+                        norm_eps=1e-6, out_dtype=None):
+    """Softmax-gated pooling over a packed varlen batch (dsa_compressor_fwd_tnd;
+    reference Compressor._forward_tnd, models/deepseek_v4/model.py:223-274).
+
+    kv, score [T,coff*D] fp32; block_starts [n_blocks] (tnd.compressed_block_starts); with
+    overlap, positions [T] (request-local) decide which blocks take the previous block's
+    first half.  Returns [n_blocks,D] like ``compressor_pool``.
+    """
+    lib = load_library()
+    require_gpu_tensor(kv, "kv")
+    if overlap is None:
+        overlap = ratio == 4
+    T, CD = kv.shape[-2], kv.shape[-1]
+    coff = 2 if overlap else 1
+    D = CD // coff
+    if out_dtype is None:
+        out_dtype = torch.bfloat16 if norm_weight is not None else torch.float32
+    kv = kv.reshape(T, CD).float().contiguous()
+    score = score.reshape(T, CD).float().contiguous()
+    ape = ape.float().contiguous()
+    nw = None if norm_weight is None else norm_weight.float().contiguous()
+    bs = block_starts.to(device=kv.device, dtype=torch.int64).contiguous()
+    pos = None
+    if overlap:
+        if positions is None:
+            raise ValueError("overlap pooling needs the token positions")
+        pos = positions.reshape(-1).to(device=kv.device, dtype=torch.int32).contiguous()
+        if pos.numel() != T:
+            raise ValueError(f"positions has {pos.numel()} entries for {T} tokens")
+    out = torch.empty(bs.numel(), D, dtype=out_dtype, device=kv.device)
+    check(
+        lib.dsa_compressor_fwd_tnd(ptr(kv), ptr(score), ptr(ape), ptr(nw), ptr(out), _lib.dtype_code(out_dtype), T, D,
+                                   int(ratio), int(bool(overlap)), ptr(bs), bs.numel(), ptr(pos), float(norm_eps),
+                                   stream_of(kv.device)),
+        "dsa_compressor_fwd_tnd",
     )
     return out
 
