@@ -11,31 +11,53 @@ namespace {
 constexpr int kD = 128;            // indexer head dim on the MFMA path
 constexpr int kThreads = 256;
 
-// Workgroup = (4 waves x kQw queries) x 256 keys.  The 256 key rows are DMA'd once into a
-// swizzled LDS tile shared by the four waves (inline-asm global_load_lds, one wait), each
-// wave keeps its queries' heads as MFMA A operands in VGPRs (128 registers) and walks the
-// 16-key B tiles out of LDS:
+// Workgroup = (4 waves x kQw queries) x a span of kSub key tiles.  Each wave keeps its
+// queries' heads as MFMA A operands in VGPRs for the whole span (one read of Q per span,
+// not per key tile), and the span's key tiles stream through two LDS buffers: tile i+1 is
+// DMA'd (inline-asm global_load_lds; the keys sit in L2) while tile i is computed.  Per
+// 16-key B tile read out of LDS:
 //   bf16: 4 x v_mfma_f32_16x16x32_bf16 per (16-head tile, 16-key tile)
 //   fp8 : 1 x v_mfma_scale_f32_16x16x128_f8f6f4 (scales 0 = identity)
 // The 16x16 C tile (lane: key = l%16, heads 4(l/16)..+3) gets relu * w in registers, is
-// summed over the head tiles in-lane and over the 4 lane groups with two lane swaps; the
-// workgroup's scores are staged in LDS and written as whole 1 KB rows.  Key ranges past
-// every query's causal frontier are written as -inf without any MFMA.
+// summed over the head tiles in-lane and over the 4 lane groups with two lane swaps; a
+// tile's scores are staged in LDS and written as whole rows.  Key ranges past every
+// query's causal frontier are written as -inf without any MFMA.
 template <bool kFp8, int kHeadTiles>
 struct IdxTile {
   static constexpr int kQw = kFp8 ? (8 / kHeadTiles > 0 ? 8 / kHeadTiles : 1) : (4 / kHeadTiles > 0 ? 4 / kHeadTiles : 1);
   static constexpr int kQ = 4 * kQw;                      // queries per workgroup
-  static constexpr int kKeys = 256;                       // keys per workgroup
   static constexpr int kRowBytes = kD * (kFp8 ? 1 : 2);   // 128 or 256
+  static constexpr int kKeys = 32768 / kRowBytes;         // keys per LDS tile (32 KB)
+  static constexpr int kSub = 4;                          // key tiles per workgroup
+  static constexpr int kSpan = kKeys * kSub;              // keys per workgroup
   static constexpr int kCpr = kRowBytes / 16;             // 16-byte chunks per key row
   static constexpr int kTileBytes = kKeys * kRowBytes;
   static constexpr int kDmaPerWave = kTileBytes / 1024 / 4;
   static constexpr int kRegsPerTile = kFp8 ? 8 : 16;      // A/B dwords per lane per 16-row tile
+  static constexpr int kStoreIters = (kQ * kKeys / 4 + kThreads - 1) / kThreads;  // float4 per thread
 };
 // key-row chunk swizzle: fp8 rows (128 B) alternate bank halves, so the 8 rows of one
 // parity take distinct chunks; bf16 rows (256 B) all start on bank 0, 16 rows distinct
 template <bool kFp8>
 __device__ __forceinline__ int idx_swz(int r) { return kFp8 ? ((r >> 1) & 7) : (r & 15); }
+
+// scores[rows s0.., keys t_lo..t_hi) = -inf (float4 stores where aligned)
+__device__ __forceinline__ void fill_neg_inf(float* __restrict__ scores, int64_t row0, int nrows, int64_t ld,
+                                             int t_lo, int t_hi, int tid) {
+  if (t_hi <= t_lo) return;
+  const int n4 = (t_hi - t_lo + 3) >> 2;
+  const float4 m4 = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  for (int i = tid; i < nrows * n4; i += kThreads) {
+    const int r = i / n4, c = i - r * n4;
+    const int t = t_lo + 4 * c;
+    float* dst = scores + (row0 + r) * ld + t;
+    if (t + 4 <= t_hi && (((uintptr_t)dst) & 15) == 0) {
+      *reinterpret_cast<float4*>(dst) = m4;
+    } else {
+      for (int e = 0; e < 4 && t + e < t_hi; ++e) dst[e] = -INFINITY;
+    }
+  }
+}
 
 template <bool kFp8, int kHeadTiles>
 __global__ void __launch_bounds__(kThreads, 2)
@@ -45,46 +67,54 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
   using T = IdxTile<kFp8, kHeadTiles>;
   constexpr int H = kHeadTiles * 16;
   constexpr int kQw = T::kQw;
-  __shared__ u32x4 ktile[T::kTileBytes / 16];
-  __shared__ float stage[T::kQ][T::kKeys];
-  __shared__ float ksc[T::kKeys];
+  constexpr int kK = T::kKeys;
+  __shared__ u32x4 ktile[2][T::kTileBytes / 16];
+  __shared__ float stage[T::kQ + 1][kK];  // + a spare row for duplicate lanes
+  __shared__ float ksc[2][kK];
+  __shared__ int nv_rows[T::kQ];
   const int b = blockIdx.z;
   const int s0 = blockIdx.x * T::kQ;
-  const int t0 = blockIdx.y * T::kKeys;
+  const int t0 = blockIdx.y * T::kSpan;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
-  const int t_end = min(s_k, t0 + T::kKeys);
+  const int t_end = min(s_k, t0 + T::kSpan);
+  const int nrows = min(T::kQ, S - s0);
 
   // causal frontier: key t is valid for query s iff t < nvalid(s) (monotone in s)
   auto nvalid = [&](int s) -> int {
     const int64_t v = (s + q_offset + 1) / cmp_ratio;
     return (int)max((int64_t)0, min((int64_t)s_k, v));
   };
-  const int nv_max = nvalid(min(s0 + T::kQ, S) - 1);  // last (largest) frontier of the workgroup
-  const int t_work = min(t_end, nv_max);               // keys below t_work need MFMA work
+  const int nv_max = nvalid(s0 + nrows - 1);  // last (largest) frontier of the workgroup
+  const int t_work = min(t_end, nv_max);      // keys below t_work need MFMA work
   const int64_t q_row0 = (int64_t)b * S;
 
-  if (t_work <= t0) {  // the whole key range lies past every query's frontier
-    for (int i = tid; i < T::kQ * T::kKeys; i += kThreads) {
-      const int qi = i / T::kKeys, kk = i - qi * T::kKeys;
-      if (s0 + qi < S && t0 + kk < t_end) scores[(q_row0 + s0 + qi) * ld + t0 + kk] = -INFINITY;
-    }
+  if (t_work <= t0) {  // the whole key span lies past every query's frontier
+    fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0, t_end, tid);
     return;
   }
+  const int nsub = (t_work - t0 + kK - 1) / kK;  // key tiles with work
 
-  // ---- key rows into LDS (row r, chunk c at c ^ idx_swz(r)); key scales ----
-  {
-    const uint8_t* kb = k + ((int64_t)b * s_k) * T::kRowBytes;
+  // ---- key tile DMA: rows (row r, chunk c at c ^ idx_swz(r)) and key scales ----
+  const uint8_t* kb_g = k + ((int64_t)b * s_k) * T::kRowBytes;
+  const float* ks_g = k_scale ? k_scale + (int64_t)b * s_k : nullptr;
+  auto issue_tile = [&](int sub, int buf) {
+    const int tb = t0 + sub * kK;
 #pragma unroll
     for (int i = 0; i < T::kDmaPerWave; ++i) {
       const int J = wave + 4 * i;
       const int p = J * 64 + lane;
       const int row = p / T::kCpr, pos = p - row * T::kCpr;
-      const int key = min(t0 + row, s_k - 1);
-      dma16_to_lds(kb, (uint32_t)key * T::kRowBytes + 16 * (pos ^ idx_swz<kFp8>(row)),
-                   (uint32_t)(uintptr_t)&ktile[J * 64]);
+      const int key = min(tb + row, s_k - 1);
+      dma16_to_lds(kb_g, (uint32_t)key * T::kRowBytes + 16 * (pos ^ idx_swz<kFp8>(row)),
+                   (uint32_t)(uintptr_t)&ktile[buf][J * 64]);
     }
-    ksc[tid] = k_scale ? k_scale[(int64_t)b * s_k + min(t0 + tid, s_k - 1)] : 1.f;
+    if (ks_g && 64 * wave < kK)
+      dma4_to_lds(ks_g, 4u * (uint32_t)min(tb + 64 * wave + lane, s_k - 1), (uint32_t)(uintptr_t)&ksc[buf][64 * wave]);
+  };
+  issue_tile(0, 0);
+  if (!ks_g) {
+    for (int i = tid; i < 2 * kK; i += kThreads) (&ksc[0][0])[i] = 1.f;
   }
 
   // ---- A operands (queries) and folded head weights, while the DMA is in flight ----
@@ -123,37 +153,52 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
       }
     }
   }
-  int nvq[kQw];
+  // the operands are forced ready here: a compiler-inserted wait for them inside the tile
+  // loop would also wait for the next tile's DMA
 #pragma unroll
-  for (int j = 0; j < kQw; ++j) nvq[j] = qa + j < S ? nvalid(qa + j) : 0;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's DMA and operand loads done
+  for (int j = 0; j < kQw; ++j)
+#pragma unroll
+    for (int ht = 0; ht < kHeadTiles; ++ht) {
+#pragma unroll
+      for (int r = 0; r < T::kRegsPerTile; ++r) asm volatile("" : "+v"(qa_reg[j][ht][r]));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(wv[j][ht][r]));
+    }
+  if (tid < T::kQ) nv_rows[tid] = s0 + tid < S ? nvalid(s0 + tid) : 0;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's tile-0 DMA landed
   __syncthreads();
 
-  // ---- 16-key tiles ----
-  const lds_char* kt_b = lds_bytes(&ktile[0]);
-  const int ntiles = (t_work - t0 + 15) >> 4;
-  for (int kt = 0; kt < ntiles; ++kt) {
-    const int row = 16 * kt + col;  // B operand row (key) of this lane
-    uint32_t kb[T::kRegsPerTile];
-    if constexpr (kFp8) {
+  for (int sub = 0; sub < nsub; ++sub) {
+    const int buf = sub & 1;
+    const int tb = t0 + sub * kK;
+    // the other buffer was last read before the previous iteration's barriers
+    if (sub + 1 < nsub) issue_tile(sub + 1, buf ^ 1);
+
+    // ---- 16-key tiles of this key tile, one software pipeline over (tile, query) items:
+    // the MFMAs of the next item (the next query, or query 0 of the next 16-key tile,
+    // whose B operand is read from LDS a tile ahead) are issued before the relu * w
+    // reduction of the current item reads its results ----
+    const lds_char* kt_b = lds_bytes(&ktile[buf][0]);
+    const int ntiles = (min(kK, t_work - tb) + 15) >> 4;
+    auto read_b = [&](int kt, uint32_t (&kb)[T::kRegsPerTile]) {
+      const int row = 16 * kt + col;  // B operand row (key) of this lane
+      if constexpr (kFp8) {
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const u32x4 x = lds_read16(kt_b + row * T::kRowBytes + 16 * ((2 * g + h2) ^ idx_swz<kFp8>(row)));
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const u32x4 x = lds_read16(kt_b + row * T::kRowBytes + 16 * ((2 * g + h2) ^ idx_swz<kFp8>(row)));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) kb[4 * h2 + r] = x[r];
+          for (int r = 0; r < 4; ++r) kb[4 * h2 + r] = x[r];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u32x4 x = lds_read16(kt_b + row * T::kRowBytes + 16 * ((4 * c + g) ^ idx_swz<kFp8>(row)));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) kb[4 * c + r] = x[r];
+        }
       }
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const u32x4 x = lds_read16(kt_b + row * T::kRowBytes + 16 * ((4 * c + g) ^ idx_swz<kFp8>(row)));
-#pragma unroll
-        for (int r = 0; r < 4; ++r) kb[4 * c + r] = x[r];
-      }
-    }
-    // software pipeline over the wave's queries: the MFMAs of query j+1 are issued before
-    // the relu * w reduction of query j reads its results
-    f32x4 cq[2][kHeadTiles];
-    auto mfma_q = [&](int j, f32x4 (&c)[kHeadTiles]) {
+    };
+    auto mfma_q = [&](int j, const uint32_t (&kb)[T::kRegsPerTile], f32x4 (&c)[kHeadTiles]) {
 #pragma unroll
       for (int ht = 0; ht < kHeadTiles; ++ht) {
         c[ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -179,42 +224,99 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
         }
       }
     };
-    mfma_q(0, cq[0]);
-#pragma unroll
-    for (int j = 0; j < kQw; ++j) {
-      if (j + 1 < kQw) mfma_q(j + 1, cq[(j + 1) & 1]);
-      float part = 0.f;
+    // relu * w partial sum of item (kt, j) over this lane's 16 C values
+    auto partial = [&](int j, const f32x4 (&c)[kHeadTiles]) -> float {
+      float p0 = 0.f, p1 = 0.f;
 #pragma unroll
       for (int ht = 0; ht < kHeadTiles; ++ht)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) part = fmaf(wv[j][ht][r], relu_bits(cq[j & 1][ht][r]), part);
-      part = xor32_sum(xor16_sum(part));
-      // lane group g stages query j (j mod 4)
-      if (g == (j & 3)) {
-        const int key = t0 + 16 * kt + col;
-        stage[wave * kQw + j][16 * kt + col] = key < nvq[j] ? part * ksc[16 * kt + col] : -INFINITY;
+        for (int r = 0; r < 4; r += 2) {
+          p0 = fmaf(wv[j][ht][r], relu_bits(c[ht][r]), p0);
+          p1 = fmaf(wv[j][ht][r + 1], relu_bits(c[ht][r + 1]), p1);
+        }
+      return p0 + p1;
+    };
+    // one 16-key tile: kQw items, each item's reduction behind the next item's MFMAs; raw
+    // head sums are staged (key scale and causal mask are applied when the rows are stored)
+    f32x4 cq[2][kHeadTiles];
+    auto tile = [&](int kt, const uint32_t (&kb_cur)[T::kRegsPerTile], uint32_t (&kb_nxt)[T::kRegsPerTile]) {
+      read_b(min(kt + 1, ntiles - 1), kb_nxt);  // (the last tile re-reads itself)
+      float pe = 0.f;
+#pragma unroll
+      for (int j = 0; j < kQw; ++j) {
+        // item (kt, j) is in cq[j & 1] (kQw is even, or 1 with the copy below)
+        if (j + 1 < kQw) mfma_q(j + 1, kb_cur, cq[(j + 1) & 1]);
+        else mfma_q(0, kb_nxt, cq[(j + 1) & 1]);
+        const float pj = partial(j, cq[j & 1]);
+        if constexpr (kQw == 1) {
+          const float v = xor32_sum(xor16_sum(pj));
+          if (g == 0) stage[wave][16 * kt + col] = v;
+        } else if ((j & 1) == 0) {
+          pe = pj;
+        } else {
+          // queries j-1 and j together: a 32-lane swap leaves query j-1's sums over lane
+          // groups {g, g^2} in lanes 0-31 and query j's in lanes 32-63; a 16-lane swap
+          // completes both (lane groups 0,1 hold query j-1, groups 2,3 query j)
+          const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(pe), __float_as_uint(pj), false, false);
+          const float h = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+          const float v = xor16_sum(h);
+          // lane groups 1 and 3 hold copies: they write the spare row (no branch, so the
+          // tile stays one scheduling region)
+          stage[(g & 1) ? T::kQ : wave * kQw + j - 1 + (g >> 1)][16 * kt + col] = v;
+        }
+      }
+      if constexpr (kQw == 1) {  // one query: the next tile's item went to cq[1]
+#pragma unroll
+        for (int ht = 0; ht < kHeadTiles; ++ht) cq[0][ht] = cq[1][ht];
+      }
+    };
+    uint32_t kb_a[T::kRegsPerTile], kb_b[T::kRegsPerTile];
+    read_b(0, kb_a);
+    mfma_q(0, kb_a, cq[0]);
+    for (int kt = 0; kt < ntiles; kt += 2) {  // two tiles per trip: the B registers alternate
+      tile(kt, kb_a, kb_b);
+      if (kt + 1 < ntiles) tile(kt + 1, kb_b, kb_a);
+    }
+    __syncthreads();  // the tile's scores are staged
+
+    // ---- scores out: whole rows; keys past t_work are -inf (beyond every frontier) ----
+    float4 v[T::kStoreIters];
+#pragma unroll
+    for (int it = 0; it < T::kStoreIters; ++it) {
+      const int i = tid + kThreads * it;
+      const int qi = min(i / (kK / 4), T::kQ - 1), kk = 4 * (i % (kK / 4));
+      // key t of row qi is valid iff t < nv_rows[qi] (<= t_work: staged keys past it are
+      // never read)
+      const int lim = nv_rows[qi] - tb - kk;
+      const float4 x = *reinterpret_cast<const float4*>(&stage[qi][kk]);
+      const float4 sc = *reinterpret_cast<const float4*>(&ksc[buf][kk]);
+      v[it].x = 0 < lim ? x.x * sc.x : -INFINITY;
+      v[it].y = 1 < lim ? x.y * sc.y : -INFINITY;
+      v[it].z = 2 < lim ? x.z * sc.z : -INFINITY;
+      v[it].w = 3 < lim ? x.w * sc.w : -INFINITY;
+    }
+    // next tile landed (this wave's DMA; the stores issued one iteration ago are long
+    // done), and every wave has read the stage
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < T::kStoreIters; ++it) {
+      const int i = tid + kThreads * it;
+      if (i >= T::kQ * (kK / 4)) break;
+      const int qi = i / (kK / 4), kk = 4 * (i % (kK / 4));
+      const int t = tb + kk;
+      if (qi >= nrows || t >= t_end) continue;
+      float* dst = scores + (q_row0 + s0 + qi) * ld + t;
+      if (t + 4 <= t_end && (((uintptr_t)dst) & 15) == 0) {
+        *reinterpret_cast<float4*>(dst) = v[it];
+      } else {
+        const float vv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+        for (int e = 0; e < 4 && t + e < t_end; ++e) dst[e] = vv[e];
       }
     }
   }
-  __syncthreads();
-  // ---- scores out: whole rows; keys past t_work are -inf (beyond every frontier) ----
-  for (int i = tid; i < T::kQ * (T::kKeys / 4); i += kThreads) {
-    const int qi = i / (T::kKeys / 4), c4i = i - qi * (T::kKeys / 4);
-    const int s = s0 + qi, kk = 4 * c4i;
-    if (s >= S || t0 + kk >= t_end) continue;
-    float4 v;
-    v.x = t0 + kk + 0 < t_work ? stage[qi][kk + 0] : -INFINITY;
-    v.y = t0 + kk + 1 < t_work ? stage[qi][kk + 1] : -INFINITY;
-    v.z = t0 + kk + 2 < t_work ? stage[qi][kk + 2] : -INFINITY;
-    v.w = t0 + kk + 3 < t_work ? stage[qi][kk + 3] : -INFINITY;
-    float* dst = scores + (q_row0 + s) * ld + t0 + kk;
-    if (t0 + kk + 4 <= t_end && (((uintptr_t)dst) & 15) == 0) {
-      *reinterpret_cast<float4*>(dst) = v;
-    } else {
-      const float vv[4] = {v.x, v.y, v.z, v.w};
-      for (int e = 0; e < 4 && t0 + kk + e < t_end; ++e) dst[e] = vv[e];
-    }
-  }
+  // key tiles of the span past every frontier
+  fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0 + nsub * kK, t_end, tid);
 }
 
 // Generic path (any H, D; fp32 arithmetic): one thread per (query, key).
@@ -282,7 +384,7 @@ extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* 
 #define DSA_IDX_LAUNCH(FP8, HT)                                                                                   \
   do {                                                                                                             \
     using Tl = IdxTile<FP8, HT>;                                                                                   \
-    dim3 grid(ceil_div(s_q, Tl::kQ), ceil_div(s_k, Tl::kKeys), (unsigned)batch);                                    \
+    dim3 grid(ceil_div(s_q, Tl::kQ), ceil_div(s_k, Tl::kSpan), (unsigned)batch);                                          \
     indexer_tile_kernel<FP8, HT><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, (int)s_q, (int)s_k, \
                                                             ld_scores, q_offset, (int)cmp_ratio);                  \
   } while (0)
