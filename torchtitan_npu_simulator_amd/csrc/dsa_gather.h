@@ -38,6 +38,43 @@ struct GatherGeom {
   static constexpr int64_t kMaxRows = (int64_t)UINT32_MAX / kRowBytes - 1;  // 32-bit byte offsets
 };
 
+// slot value v of a row whose causal limit is `limit` is a usable key
+__device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
+  return v >= 0 && v < s_kv && (int64_t)v <= limit;
+}
+
+// Number of 32-slot blocks up to the last usable slot of a row, in two parts so a kernel
+// can request the row's indices together with its other prologue loads and test them
+// later (one memory round trip): load_row_indices() issues each thread's first kIdxU
+// index loads with no wait between them; count_row_blocks() tests them (a loop reads
+// slots past kIdxU * blockDim.x) and reduces over the workgroup (needs sync).
+constexpr int kIdxU = 8;
+__device__ __forceinline__ void load_row_indices(const int32_t* ridx, int K, int (&v)[kIdxU]) {
+#pragma unroll
+  for (int u = 0; u < kIdxU; ++u) {
+    const int j = (int)threadIdx.x + u * (int)blockDim.x;
+    v[u] = j < K ? ridx[j] : -1;
+  }
+}
+__device__ __forceinline__ int count_row_blocks(const int32_t* ridx, int K, int s_kv, int64_t limit,
+                                                const int (&v)[kIdxU], int* sh_last) {
+  if (threadIdx.x == 0) *sh_last = -1;
+  int last = -1;
+#pragma unroll
+  for (int u = 0; u < kIdxU; ++u) {
+    const int j = (int)threadIdx.x + u * (int)blockDim.x;
+    if (j < K && slot_ok(v[u], s_kv, limit)) last = j;
+  }
+  for (int j = (int)threadIdx.x + kIdxU * (int)blockDim.x; j < K; j += blockDim.x)
+    if (slot_ok(ridx[j], s_kv, limit)) last = j;
+  __syncthreads();  // sh_last initialised
+  if (last >= 0) atomicMax(sh_last, last);
+  __syncthreads();
+  const int n = (*sh_last + GatherGeom::kBN) / GatherGeom::kBN;
+  __syncthreads();
+  return n;
+}
+
 // usable-key limit of a row: slot value v is used iff (uint32)v <= lim
 __device__ __forceinline__ uint32_t gather_limit(int64_t tok_limit, int s_kv) {
   const int64_t l = tok_limit < (int64_t)s_kv - 1 ? tok_limit : (int64_t)s_kv - 1;

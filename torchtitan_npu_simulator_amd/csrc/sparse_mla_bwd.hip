@@ -40,10 +40,6 @@ constexpr int kHeadsMax = 128;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-__device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
-  return v >= 0 && v < s_kv && (int64_t)v <= limit;
-}
-
 __device__ __forceinline__ u32x4 tr_pair(uint32_t a1, uint32_t a2) {
   const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a1));
   const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a2));
@@ -58,20 +54,6 @@ __device__ __forceinline__ u32x4 tr_pair(uint32_t a1, uint32_t a2) {
 // piece swizzle of the transposed G stage (64-byte rows): conflict-free for the lanes'
 // 8-byte writes (16 rows x 2 pieces per 32 lanes) and for the flush's transposed reads
 __device__ __forceinline__ int gt_swz(int r) { return (r >> 1) & 7; }
-
-// number of 32-slot blocks up to the last usable slot of a row (block-wide; needs sync)
-__device__ int count_blocks(const int32_t* ridx, int K, int s_kv, int64_t limit, int* sh_last) {
-  if (threadIdx.x == 0) *sh_last = -1;
-  __syncthreads();
-  int last = -1;
-  for (int j = threadIdx.x; j < K; j += blockDim.x)
-    if (slot_ok(ridx[j], s_kv, limit)) last = j;
-  if (last >= 0) atomicMax(sh_last, last);
-  __syncthreads();
-  const int n = (*sh_last + kBN) / kBN;
-  __syncthreads();
-  return n;
-}
 
 // --------------------------------------------------------------------------------------
 // (alpha) dQ and G
@@ -108,10 +90,39 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   // head-summed P of this head group for the row (mass; the host adds the head groups)
   float* mrow = mbase ? mbase + hg * m_hg_stride + b * m_b_stride + (int64_t)(m_row_base + blockIdx.x) * K : nullptr;
 
-  const int nblk = count_blocks(ridx, K, s_kv, limit, &sh_last);
+  // ---- prologue: the row's slot indices (block count), the index ring entries of blocks
+  // 0..2 (wave 0, DMA), the per-head operands Q (B layout of S^T = K Q^T), dO (B layout
+  // of dP^T = V dO^T), O and the row statistics are all requested before any is waited
+  // for: the block count needs only the first loads, the operands land meanwhile ----
+  int vidx[kIdxU];
+  load_row_indices(ridx, K, vidx);
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);  // clamped to slot K-1
+  }
+  // (unconditional loads, hrow points at head 0 for absent heads: a load under a branch
+  // would make the compiler wait for every load before the block count; absent heads are
+  // zeroed after it)
+  u32x4 qb[kDqk / 32], db[kDv / 32], ov[kDv / 32];
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
+    const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
+    const u32x4* oh = reinterpret_cast<const u32x4*>(out + hrow * kDv);
+#pragma unroll
+    for (int c = 0; c < kDqk / 32; ++c) qb[c] = qh[4 * c + g];
+#pragma unroll
+    for (int c = 0; c < kDv / 32; ++c) {
+      db[c] = dh[4 * c + g];
+      ov[c] = oh[4 * c + g];
+    }
+  }
+  const float mx = smax[hrow], sm = ssum[hrow];
+
+  const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (mrow)  // slots past the last usable block carry no mass
     for (int j = nblk * kBN + tid; j < K; j += 256) mrow[j] = 0.f;
   if (nblk == 0) {  // no usable key: dQ = 0 (G rows are never read)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring DMA has landed before the LDS is released
     if (head_ok) {
       uint32_t* d32 = reinterpret_cast<uint32_t*>(dq + hrow * kDqk);
       for (int i = g; i < kDqk / 2; i += 4) d32[i] = 0u;
@@ -120,27 +131,22 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   }
   const uint32_t lim = gather_limit(limit, s_kv);
 
-  // ---- per-head operands: Q (B layout of S^T = K Q^T), dO (B layout of dP^T = V dO^T) ----
-  u32x4 qb[kDqk / 32], db[kDv / 32];
+  if (!head_ok) {
+#pragma unroll
+    for (int c = 0; c < kDqk / 32; ++c) qb[c] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int c = 0; c < kDv / 32; ++c) db[c] = ov[c] = (u32x4){0u, 0u, 0u, 0u};
+  }
   float delta, lse2;
   {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
-    const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
-    const u32x4* oh = reinterpret_cast<const u32x4*>(out + hrow * kDv);
     float part = 0.f;
 #pragma unroll
-    for (int c = 0; c < kDqk / 32; ++c) qb[c] = head_ok ? qh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int c = 0; c < kDv / 32; ++c) {
-      db[c] = head_ok ? dh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
-      const u32x4 ov = head_ok ? oh[4 * c + g] : (u32x4){0u, 0u, 0u, 0u};
+    for (int c = 0; c < kDv / 32; ++c)
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        part += bf16_lo(db[c][r]) * bf16_lo(ov[r]) + bf16_hi(db[c][r]) * bf16_hi(ov[r]);
-    }
+        part += bf16_lo(db[c][r]) * bf16_lo(ov[c][r]) + bf16_hi(db[c][r]) * bf16_hi(ov[c][r]);
     delta = xor32_sum(xor16_sum(part));
-    const float mx = head_ok ? smax[hrow] : 0.f, sm = head_ok ? ssum[hrow] : 0.f;
-    lse2 = (sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0 (absent head / no key)
+    lse2 = (head_ok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0 (absent head / no key)
   }
   const float scale_log2 = scale * kLog2e;
 
@@ -212,7 +218,7 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   // blk-1's.  The iteration ends with its DMAs landed (vmcnt 0) and one barrier.
   constexpr int kPer = Gather::kMaxPerWave;
   const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
-  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);  // ring entries 0..2
+  if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
   __syncthreads();
   for (int i = tid; i < kTileChunks; i += 256) tile[2][i] = (u32x4){0u, 0u, 0u, 0u};  // dQ of "block -1"
   uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
@@ -438,7 +444,9 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int col = lane & 15, g = lane >> 4;
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
-  const int nblk = count_blocks(ridx, K, s_kv, tok + q_offset, &sh_last);
+  int vidx[kIdxU];
+  load_row_indices(ridx, K, vidx);
+  const int nblk = count_row_blocks(ridx, K, s_kv, tok + q_offset, vidx, &sh_last);
   if (nblk == 0) return;
   const int nslots = min(K, nblk * kBN);
   const uint16_t* grow = gbuf + ((int64_t)b * rows + lr) * (int64_t)K * kGW;
@@ -677,7 +685,7 @@ mass_combine_kernel(const float* __restrict__ part, float* __restrict__ mass, in
   }
 }
 
-constexpr int64_t kDefaultBudget = 16LL << 30;  // scratch for the G / C chunks
+constexpr int64_t kDefaultBudget = 32LL << 30;  // scratch for the G / C chunks (C3 in one chunk)
 
 }  // namespace
 }  // namespace dsa

@@ -45,27 +45,9 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kHeadsPerWG = 128;
 constexpr int kHalfSteps = 16;                 // latent MFMA steps per contraction half
 
-__device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
-  return v >= 0 && v < s_kv && (int64_t)v <= limit;
-}
-
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-
-// number of 32-slot blocks up to the last usable slot of a row (block-wide; needs sync)
-__device__ int fwd_count_blocks(const int32_t* ridx, int K, int s_kv, int64_t limit, int* sh_last) {
-  if (threadIdx.x == 0) *sh_last = -1;
-  __syncthreads();
-  int last = -1;
-  for (int j = threadIdx.x; j < K; j += blockDim.x)
-    if (slot_ok(ridx[j], s_kv, limit)) last = j;
-  if (last >= 0) atomicMax(sh_last, last);
-  __syncthreads();
-  const int n = (*sh_last + kBN) / kBN;
-  __syncthreads();
-  return n;
-}
 
 __global__ void __launch_bounds__(kFwdThreads, 1)
 sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv,
@@ -91,7 +73,24 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   const int64_t limit = tok + q_offset;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
 
-  const int nblk = fwd_count_blocks(ridx, K, s_kv, limit, &sh_last);
+  // the row's slot indices (block count) and the row's Q are requested together; the
+  // block count waits only for the indices
+  int vidx[kIdxU];
+  load_row_indices(ridx, K, vidx);
+  // ---- Q: latent qb[s] = q[16s + 8h .. +8] of head `head` (B operand of S^T = K Q^T for
+  // k-step s) in VGPRs; the rope columns go to LDS below ----
+  // (unconditional loads, orow points at head 0 for absent heads: a load under a branch
+  // would make the compiler wait for every load before the block count; absent heads are
+  // zeroed after it)
+  u32x4 qb[kLatSteps], qr[4];
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + orow * kDqk);
+#pragma unroll
+    for (int s = 0; s < kLatSteps; ++s) qb[s] = qh[2 * s + h];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qr[j] = qh[64 + 4 * h + j];  // rope chunks 64 + 4h ..
+  }
+  const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (nblk == 0) {
     if (hok) {
       uint32_t* o32 = reinterpret_cast<uint32_t*>(out + orow * kDv);
@@ -105,18 +104,16 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   }
   const uint32_t lim = gather_limit(limit, s_kv);
 
-  // ---- Q: latent qb[s] = q[16s + 8h .. +8] of head `head` (B operand of S^T = K Q^T for
-  // k-step s) in VGPRs; the rope columns into LDS ----
-  u32x4 qb[kLatSteps];
-  {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + orow * kDqk);
+  if (!hok) {
 #pragma unroll
-    for (int s = 0; s < kLatSteps; ++s) qb[s] = hok ? qh[2 * s + h] : (u32x4){0u, 0u, 0u, 0u};
+    for (int s = 0; s < kLatSteps; ++s) qb[s] = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {  // rope chunks 64..71: lane h writes 4h .. 4h+3
-      const int ch = 4 * h + j;
-      qpe[hl][ch ^ ((hl >> 1) & 7)] = hok ? qh[64 + ch] : (u32x4){0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < 4; ++j) qr[j] = (u32x4){0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // rope chunks 64..71: lane h writes 4h .. 4h+3
+    const int ch = 4 * h + j;
+    qpe[hl][ch ^ ((hl >> 1) & 7)] = qr[j];
   }
 #pragma unroll
   for (int s = 0; s < kLatSteps; ++s) asm volatile("" : "+v"(qb[s]));  // landed before any DMA
