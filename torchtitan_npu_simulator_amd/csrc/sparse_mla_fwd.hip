@@ -205,13 +205,26 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
         if constexpr (nb + 1 < kPer) raw_next = Gather::ring_slot(ring, nb + 1, gl);
         Gather::issue_slot(kvb, dst_tile, nb, wave, raw, gl, lim, rows_left);
       }
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kQBatch; ++u) {
         constexpr int s0 = nb * kQBatch;
         const u32x4 bq = s0 < kLatSteps ? qb[(s0 + u) % kLatSteps] : rope[u];
         sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(bq), sacc);
       }
+      // the batch's LDS reads, address arithmetic and DMA are spread between its MFMAs:
+      // with one accumulation chain the wave issues in order, so work placed after the
+      // MFMAs would only overlap the last one
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
+      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);  // VALU / SALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x006, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // the row DMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_barrier(0);
     });
     return vm_n;
