@@ -32,6 +32,11 @@ follows (paths relative to the reference repository root):
                            B*S at :73 and :182-183)
 * ``compressor_pool``      models/deepseek_v4/model.py:174-221 (overlap_transform
                            + softmax-gated pooling + RMSNorm)
+* ``sparse_attn_sink``     models/deepseek_v4/model.py:573-623 (SparseAttention.forward:
+                           window + compressed indices over cat(kv, kv_compress),
+                           index mask, per-head sink logit appended to the softmax,
+                           output = probs @ kv); ``v4_attn_indices`` builds its
+                           index tensor (:581-592)
 * ``window_topk_idxs``     models/deepseek_v4/model.py:467-471
 * ``compress_topk_idxs``   models/deepseek_v4/model.py:483-488
 * ``compressor_pool_tnd``  models/deepseek_v4/model.py:223-274 (Compressor._forward_tnd:
@@ -58,6 +63,9 @@ Which check pins each function (tests/test_oracle.py):
   ``loss / (B*S)`` scaling.
 * compressor_pool: uniform gates give the mean pool; first block gets no
   overlap contribution; r == 1 without overlap is the identity.
+* sparse_attn_sink: a sink of -inf reduces it to sparse_mla_fwd with v = the
+  whole row; brute-force loops over (s, h) on tiny inputs; fp64 gradcheck of
+  the gradients to q, kv and the sink.
 * compressor_pool_tnd: one request whose length is a multiple of r equals
   compressor_pool on it; several such requests equal compressor_pool per request
   (the has_prev_block guard restarts the overlap at each request).
@@ -87,6 +95,8 @@ __all__ = [
     "indexer_kl_loss_grad",
     "indexer_kl_from_mass",
     "compressor_pool",
+    "sparse_attn_sink",
+    "v4_attn_indices",
     "window_topk_idxs",
     "compress_topk_idxs",
     "lengths_to_cu_seqlens",
@@ -499,6 +509,47 @@ def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions, *, overl
     x = pooled.to(out_dtype or torch.float32).float()
     rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm_eps)
     return x * rms * norm_weight.float()
+
+
+def v4_attn_indices(bsz, seqlen, window_size, ratio, kv_len, cmp_idxs=None):
+    """Index tensor of SparseAttention.forward (models/deepseek_v4/model.py:581-592): the
+    sliding-window indices into kv_states, then (ratio > 1) the compressed ones into
+    kv_compress offset by kv_len (``cmp_idxs``, already offset, or every causal block)."""
+    idx = window_topk_idxs(window_size, bsz, seqlen)
+    if ratio > 1:
+        if cmp_idxs is None:
+            cmp_idxs = compress_topk_idxs(ratio, bsz, seqlen, kv_len)
+        idx = torch.cat([idx, cmp_idxs.to(idx.dtype)], dim=-1)
+    return idx.int()
+
+
+def sparse_attn_sink(q, kv, sink, idx, scale, *, dtype=torch.float64):
+    """SparseAttention.forward math (models/deepseek_v4/model.py:600-623).
+
+    q [B,S,H,D], kv [B,T,D] (cat of kv_states and kv_compress; k = v = the row), sink
+    [H], idx [B,S,K] into kv (-1 = masked).  logits = scale q.k over the indexed keys
+    (the reference's index mask adds bf16 min elsewhere, i.e. excludes them), the sink
+    logit is appended, a softmax over [keys, sink] gives probs, and out = probs[:-1] @ kv.
+    Returns (out [B,S,H,D], lse [B,S,H]) with lse = logsumexp over keys and sink.
+    Differentiable in q, kv and sink (autograd in ``dtype``).
+    """
+    B, S, H, D = q.shape
+    T = kv.shape[1]
+    qd, kvd, sd = q.to(dtype), kv.to(dtype), sink.to(dtype)
+    ii = idx.long()
+    valid = (ii >= 0) & (ii < T)
+    iic = ii.clamp(0, T - 1)
+    outs, lses = [], []
+    for b in range(B):
+        kk = kvd[b][iic[b]]  # [S,K,D]
+        logits = torch.einsum("shd,skd->shk", qd[b], kk) * scale
+        logits = logits.masked_fill(~valid[b].unsqueeze(1), float("-inf"))
+        comb = torch.cat([logits, sd.view(1, H, 1).expand(S, H, 1)], dim=-1)
+        lse = torch.logsumexp(comb, dim=-1)
+        p = torch.exp(comb - lse.unsqueeze(-1))[..., :-1]
+        outs.append(torch.einsum("shk,skd->shd", p, kk))
+        lses.append(lse)
+    return torch.stack(outs), torch.stack(lses)
 
 
 def varlen_split(packed: torch.Tensor, cu_seqlens) -> list[torch.Tensor]:

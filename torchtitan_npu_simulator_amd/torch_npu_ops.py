@@ -53,6 +53,8 @@ __all__ = [
     "attn_mass_varlen",
     "indexer_kl_grad_from_mass_varlen",
     "to_cu_seqlens",
+    "npu_sparse_attn_shared_kv",
+    "v4_attention_indices",
 ]
 
 _SCORE_BUDGET_BYTES = 1 << 30  # fp32 score rows materialised per indexer chunk
@@ -585,6 +587,135 @@ def npu_sparse_flash_attention(
     idx = sparse_indices.reshape(query.shape[0], query.shape[1], -1)
     out, smax, ssum = _SparseFlashAttention.apply(query, key, query_rope, key_rope, idx, float(scale_value), q_off)
     return out, smax, ssum
+
+
+# ---------------------------------------------------------------------------
+# DeepSeek-V4 shared-KV sparse attention: sliding window + compressed KV + sink
+# ---------------------------------------------------------------------------
+def v4_attention_indices(B, S, device, *, win_left=127, win_right=0, cmp_ratio=1, n_cmp=0, cmp_indices=None):
+    """int32 [B,S,W(+K)] slot indices over cat(ori_kv, cmp_kv), -1 = empty.
+
+    Window slots: ori tokens t in [s - win_left, s + win_right] (reference
+    GetWindowTopkIdxs, models/deepseek_v4/model.py:467-471, is the win_right = 0 case).
+    Compressed slots (cmp_ratio > 1, ``n_cmp`` compressed rows): ``cmp_indices`` as given
+    (offset by S, as LiCompute returns them), or every causal block t < (s+1)//r
+    offset by S (GetCompressTopkIdxs, :483-488; the ratio-128 layers).
+    """
+    W = win_left + win_right + 1
+    s_pos = torch.arange(S, device=device).view(S, 1)
+    w = s_pos - win_left + torch.arange(W, device=device).view(1, W)
+    w = torch.where((w >= 0) & (w < S), w, torch.full_like(w, -1))
+    idx = w.unsqueeze(0).expand(B, S, W)
+    if cmp_ratio > 1 and n_cmp > 0:
+        if cmp_indices is None:
+            t = torch.arange(n_cmp, device=device).view(1, n_cmp)
+            c = torch.where(t < (s_pos + 1) // cmp_ratio, t + S, torch.full_like(t, -1))
+            cmp_indices = c.unsqueeze(0).expand(B, S, n_cmp)
+        idx = torch.cat([idx, cmp_indices.to(device=device, dtype=idx.dtype)], dim=-1)
+    return idx.to(torch.int32).contiguous()
+
+
+def _pad_rows(x: torch.Tensor, width: int) -> torch.Tensor:
+    if x.shape[-1] == width:
+        return x.contiguous()
+    pad = x.new_zeros(*x.shape[:-1], width - x.shape[-1])
+    return torch.cat([x, pad], dim=-1).contiguous()
+
+
+def _sink_fold(smax, ssum, sinks):
+    """Fold a per-head sink logit into the row statistics: returns (m2, s2, factor) with
+    m2 = max(smax, sink), s2 = ssum e^(smax-m2) + e^(sink-m2) and factor = the share of
+    the probability mass on the keys (the output scale)."""
+    sk = sinks.float().view(*([1] * (smax.dim() - 1)), -1)
+    m2 = torch.maximum(smax, sk)
+    a = torch.where(ssum > 0, ssum * torch.exp(smax - m2), torch.zeros_like(ssum))
+    s2 = a + torch.exp(sk - m2)
+    return m2, s2, a / s2
+
+
+class _SparseAttnSharedKV(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, query, ori_kv, cmp_kv, sinks, idx, scale):
+        B, S, H, D = query.shape
+        kv = ori_kv if cmp_kv is None else torch.cat([ori_kv, cmp_kv], dim=1)
+        bf16 = query.dtype == torch.bfloat16
+        if bf16 and D > 512:
+            raise NotImplementedError(f"bf16 shared-KV attention needs head_dim <= 512 (got {D})")
+        # bf16: rows padded to the kernel's 576 = 512 value columns + 64 (zero) columns; k = v
+        # = the whole row.  fp32: the exact kernel takes any width.
+        dqk, dv = (576, 512) if bf16 else (D, D)
+        q_ext = _pad_rows(query, dqk)
+        kv_ext = _pad_rows(kv, dqk)
+        out, smax, ssum = sparse_mla_fwd(q_ext, kv_ext, idx, scale, d_v=dv, q_offset=_NO_MASK_OFFSET)
+        m2, s2, factor = _sink_fold(smax, ssum, sinks)
+        out = (out.float() * factor.unsqueeze(-1)).to(query.dtype)
+        ctx.save_for_backward(q_ext, kv_ext, idx, out, m2, s2, sinks)
+        ctx.scale = scale
+        ctx.meta = (D, dv, ori_kv.shape[1], cmp_kv is not None)
+        return out[..., :D] if dv != D else out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q_ext, kv_ext, idx, out, m2, s2, sinks = ctx.saved_tensors
+        D, dv, s_ori, has_cmp = ctx.meta
+        dout = _pad_rows(dout.to(out.dtype), dv) if dv != D else dout.contiguous().to(out.dtype)
+        # P_j = exp(x_j - lse) with lse = m2 + log s2 already includes the sink, and the
+        # kernel's delta = rowsum(dO * O) uses the sink-scaled O: dQ and dKV are exact
+        dq, dkv = sparse_mla_bwd(q_ext, kv_ext, idx, out, dout, m2, s2, ctx.scale, q_offset=_NO_MASK_OFFSET)
+        # the sink has no value: d sink = -sum over rows of p_sink * delta
+        delta = (dout.float() * out.float()).sum(-1)
+        p_sink = torch.exp(sinks.float().view(1, 1, -1) - m2) / s2
+        dsink = -(p_sink * delta).sum(dim=(0, 1))
+        dq = dq[..., :D]
+        dkv = dkv[..., :D].to(kv_ext.dtype)
+        d_ori = dkv[:, :s_ori]
+        d_cmp = dkv[:, s_ori:] if has_cmp else None
+        return dq, d_ori, d_cmp, dsink.to(sinks.dtype), None, None
+
+
+def npu_sparse_attn_shared_kv(
+    query,
+    ori_kv,
+    cmp_kv,
+    cmp_sparse_indices,
+    sinks,
+    softmax_scale,
+    cmp_ratio,
+    ori_mask_mode=4,
+    cmp_mask_mode=3,
+    ori_win_left=127,
+    ori_win_right=0,
+):
+    """DeepSeek-V4 shared-KV sparse attention (reference npu_sparse_attn_shared_kv,
+    converters/kernels/npu_smla.py:351-400; math of SparseAttention.forward,
+    models/deepseek_v4/model.py:573-623).
+
+    query [B,S,H,D], ori_kv [B,S,D] (window keys), cmp_kv [B,S/r,D] or None (compressed
+    keys), cmp_sparse_indices [B,S,K] int (top-k compressed rows offset by S, -1 empty;
+    ratio 4) or None (every causal block), sinks [H] fp32.  Keys and values are the same
+    rows (k = v).  Each query sees the ori tokens of its band [s - ori_win_left,
+    s + ori_win_right] and the selected compressed rows; the softmax also includes the
+    head's sink logit, which carries no value.  Returns [B,S,H,D], differentiable in
+    query, ori_kv, cmp_kv and sinks.  bf16 rows need D <= 512 (MFMA path); fp32 rows any D.
+    """
+    if ori_mask_mode != 4 or cmp_mask_mode != 3:
+        raise NotImplementedError("mask modes: band window (4) over ori_kv, causal (3) over cmp_kv")
+    for t, n in ((query, "query"), (ori_kv, "ori_kv")):
+        require_gpu_tensor(t, n)
+    B, S, H, D = query.shape
+    if ori_kv.dim() == 4:
+        ori_kv = ori_kv.squeeze(2)
+    if cmp_kv is not None and cmp_kv.dim() == 4:
+        cmp_kv = cmp_kv.squeeze(2)
+    if cmp_sparse_indices is not None and cmp_sparse_indices.dim() == 4:
+        cmp_sparse_indices = cmp_sparse_indices.squeeze(2)
+    n_cmp = 0 if cmp_kv is None else cmp_kv.shape[1]
+    cmp_idx = cmp_sparse_indices if cmp_ratio == 4 else None
+    idx = v4_attention_indices(B, S, query.device, win_left=int(ori_win_left), win_right=int(ori_win_right),
+                               cmp_ratio=int(cmp_ratio), n_cmp=n_cmp, cmp_indices=cmp_idx)
+    return _SparseAttnSharedKV.apply(query.contiguous(), ori_kv.contiguous(),
+                                     None if cmp_kv is None else cmp_kv.contiguous(), sinks.float(), idx,
+                                     float(softmax_scale))
 
 
 def npu_sparse_lightning_indexer_grad_kl_loss(
