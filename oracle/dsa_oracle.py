@@ -37,6 +37,10 @@ follows (paths relative to the reference repository root):
                            index mask, per-head sink logit appended to the softmax,
                            output = probs @ kv); ``v4_attn_indices`` builds its
                            index tensor (:581-592)
+* ``v4_selected_attn_dist``  models/deepseek_v4/model.py:421-456 (LiLoss target: the
+                           combined softmax at the selected compressed rows, averaged
+                           over heads); the V4 loss is then ``indexer_kl_from_mass``
+                           with loss_scale = softmax_scale, eps 1e-10 (:385, :412-417)
 * ``window_topk_idxs``     models/deepseek_v4/model.py:467-471
 * ``compress_topk_idxs``   models/deepseek_v4/model.py:483-488
 * ``compressor_pool_tnd``  models/deepseek_v4/model.py:223-274 (Compressor._forward_tnd:
@@ -66,6 +70,9 @@ Which check pins each function (tests/test_oracle.py):
 * sparse_attn_sink: a sink of -inf reduces it to sparse_mla_fwd with v = the
   whole row; brute-force loops over (s, h) on tiny inputs; fp64 gradcheck of
   the gradients to q, kv and the sink.
+* v4_selected_attn_dist: equals the compressed-slot columns of sparse_attn_sink's
+  probabilities summed over heads / H (recomputed from its lse); rows sum to at
+  most 1.
 * compressor_pool_tnd: one request whose length is a multiple of r equals
   compressor_pool on it; several such requests equal compressor_pool per request
   (the has_prev_block guard restarts the overlap at each request).
@@ -97,6 +104,7 @@ __all__ = [
     "compressor_pool",
     "sparse_attn_sink",
     "v4_attn_indices",
+    "v4_selected_attn_dist",
     "window_topk_idxs",
     "compress_topk_idxs",
     "lengths_to_cu_seqlens",
@@ -550,6 +558,33 @@ def sparse_attn_sink(q, kv, sink, idx, scale, *, dtype=torch.float64):
         outs.append(torch.einsum("shk,skd->shd", p, kk))
         lses.append(lse)
     return torch.stack(outs), torch.stack(lses)
+
+
+def v4_selected_attn_dist(q, kv, kv_compress, sink, cmp_idx, scale, window_size, *, dtype=torch.float64):
+    """LiLoss._current_selected_attn_dist (models/deepseek_v4/model.py:421-456): the
+    probability of the combined softmax (window keys, compressed keys, sink) at each
+    selected compressed row, averaged over heads; 0 for -1 slots.  cmp_idx [B,S,K] are
+    local compressed indices (offset removed)."""
+    B, S, H, _ = q.shape
+    kv_len = kv.shape[1]
+    kv_all = torch.cat([kv, kv_compress], dim=1)
+    cmp_off = torch.where(cmp_idx < 0, cmp_idx, cmp_idx + kv_len)
+    idx = torch.cat([window_topk_idxs(window_size, B, S), cmp_off.to(torch.long)], dim=-1)
+    T = kv_all.shape[1]
+    ii = idx.long()
+    valid = (ii >= 0) & (ii < T)
+    iic = ii.clamp(0, T - 1)
+    W = idx.shape[-1] - cmp_idx.shape[-1]
+    rows = []
+    for b in range(B):
+        kk = kv_all[b].to(dtype)[iic[b]]
+        logits = torch.einsum("shd,skd->shk", q[b].to(dtype), kk) * scale
+        logits = logits.masked_fill(~valid[b].unsqueeze(1), float("-inf"))
+        comb = torch.cat([logits, sink.to(dtype).view(1, H, 1).expand(S, H, 1)], dim=-1)
+        p = torch.softmax(comb, dim=-1)[..., :-1]
+        rows.append(p[..., W:].sum(dim=1) / H)
+    dist = torch.stack(rows)
+    return dist.masked_fill(cmp_idx < 0, 0.0)
 
 
 def varlen_split(packed: torch.Tensor, cu_seqlens) -> list[torch.Tensor]:

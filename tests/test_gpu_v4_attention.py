@@ -79,3 +79,34 @@ def test_v4_sink_dominates_empty_rows():
     out.backward(dout.to(DEV))
     assert out.abs().max().item() < 1e-6
     assert torch.isfinite(sink.grad).all()
+
+
+def test_v4_li_loss_gradients():
+    """NpuLiLoss (loss deferred to backward) against the oracle's LiLoss: target = the
+    combined-softmax probability at the selected compressed rows averaged over heads,
+    loss = DSAIndexerLoss(eps 1e-10, loss_scale = softmax_scale), mean over tokens."""
+    from types import SimpleNamespace
+
+    from torchtitan_npu_simulator_amd.converters import npu_smla as smla_mod
+
+    S, H, D, r, K, HI, DI, window = 256, 16, 512, 4, 32, 64, 128, 128
+    q, ori, cmp, sink, idx_off, _ = _case(S, H, D, r, K, torch.bfloat16, seed=41)
+    g = torch.Generator().manual_seed(42)
+    qi = torch.randn(1, S, HI, DI, generator=g).bfloat16()
+    ki = torch.randn(1, S // r, DI, generator=g).bfloat16()
+    w = torch.rand(1, S, HI, generator=g) * HI ** -0.5 * DI ** -0.5
+    scale = D ** -0.5
+    parent = SimpleNamespace(softmax_scale=scale, window_size=window, layer_id=None, n_layers=0)
+    mod = smla_mod.NpuLiLoss(torch.nn.Module())
+    mod.__dict__.update(parent.__dict__)
+    leaves = [t.to(DEV).requires_grad_(True) for t in (qi, ki, w)]
+    loss = mod(q.to(DEV), ori.to(DEV), cmp.to(DEV), sink.to(DEV), *leaves, idx_off.to(DEV), None, None, S)
+    assert float(loss) == 0.0  # deferred to backward
+    loss.backward()
+    local = torch.where(idx_off < 0, idx_off, idx_off - S)
+    dist = O.v4_selected_attn_dist(q, ori, cmp, sink, local, scale, window)
+    rdq, rdk, rdw, _ = O.indexer_kl_from_mass(qi, ki, w, local, dist, q_offset=1 << 40, loss_scale=scale, eps=1e-10)
+    n = S  # B * S tokens
+    assert rel_err(leaves[0].grad, rdq / n) <= 2e-2, rel_err(leaves[0].grad, rdq / n)
+    assert rel_err(leaves[1].grad, rdk / n) <= 2e-2
+    assert rel_err(leaves[2].grad, rdw / n) <= 2e-2

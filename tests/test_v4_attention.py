@@ -122,3 +122,44 @@ def test_npu_smla_converter_swaps_sparse_attention():
     model = torch.nn.Sequential(torch.nn.Linear(2, 2), SparseAttention())
     conv.registry().converter_class("npu_smla")(model_spec=SimpleNamespace(name="deepseek_v4")).convert(model)
     assert isinstance(model[1], smla_mod.NpuSparseAttention) and model[1].window_size == 128
+
+
+def test_selected_attn_dist_is_sink_attention_mass():
+    """The LiLoss target equals the compressed-slot probabilities of sparse_attn_sink,
+    summed over heads / H (recomputed from its lse), and rows sum to at most one."""
+    B, S, H, D, r, W = 1, 20, 3, 6, 4, 5
+    q, kv_all, sink = _inputs(B, S, H, D, S + S // r, seed=7)
+    kv, kvc = kv_all[:, :S], kv_all[:, S:]
+    g = torch.Generator().manual_seed(8)
+    K = 3
+    cmp = torch.full((B, S, K), -1, dtype=torch.int32)
+    for s in range(S):
+        nv = (s + 1) // r
+        c = min(K, nv)
+        if c:
+            cmp[0, s, :c] = torch.randperm(nv, generator=g)[:c].int()
+    dist = O.v4_selected_attn_dist(q, kv, kvc, sink, cmp, 0.4, W)
+    idx = O.v4_attn_indices(B, S, W, r, S, cmp_idxs=torch.where(cmp < 0, cmp, cmp + S))
+    _, lse = O.sparse_attn_sink(q, kv_all, sink, idx, 0.4)
+    for s in range(S):
+        for k in range(K):
+            j = int(cmp[0, s, k])
+            if j < 0:
+                assert dist[0, s, k] == 0
+                continue
+            p = torch.exp(0.4 * (q[0, s] @ kv_all[0, S + j]) - lse[0, s]).sum() / H
+            assert abs(float(dist[0, s, k] - p)) < 1e-12
+    assert float(dist.sum(-1).max()) <= 1.0 + 1e-12
+
+
+def test_npu_smla_converter_swaps_li_loss():
+    from torchtitan_npu_simulator_amd import converters as conv
+
+    class LiLoss(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.softmax_scale, self.window_size, self.layer_id, self.n_layers = 0.1, 128, 0, 2
+
+    model = torch.nn.Sequential(LiLoss())
+    conv.registry().converter_class("npu_smla")(model_spec=SimpleNamespace(name="deepseek_v4")).convert(model)
+    assert isinstance(model[0], smla_mod.NpuLiLoss) and model[0].softmax_scale == 0.1

@@ -55,6 +55,7 @@ __all__ = [
     "to_cu_seqlens",
     "npu_sparse_attn_shared_kv",
     "v4_attention_indices",
+    "v4_indexer_kl_grad",
 ]
 
 _SCORE_BUDGET_BYTES = 1 << 30  # fp32 score rows materialised per indexer chunk
@@ -716,6 +717,40 @@ def npu_sparse_attn_shared_kv(
     return _SparseAttnSharedKV.apply(query.contiguous(), ori_kv.contiguous(),
                                      None if cmp_kv is None else cmp_kv.contiguous(), sinks.float(), idx,
                                      float(softmax_scale))
+
+
+def v4_indexer_kl_grad(q, kv, kv_compress, attn_sink, q_indexer, k_indexer, weights, compress_topk_idxs, offset,
+                       softmax_scale, window_size=128, *, eps=1e-10, grad_scale=1.0):
+    """DeepSeek-V4 indexer KL loss and its gradients (reference LiLoss, models/deepseek_v4/
+    model.py:366-456, the loss of DSAIndexerLoss with eps 1e-10 and loss_scale =
+    softmax_scale).  The target is the main attention's probability at each selected
+    compressed row (combined softmax over the window keys, the compressed keys and the
+    head's sink), averaged over heads: dsa_attn_mass over the same gathered slots as
+    npu_sparse_attn_shared_kv with the sink folded into the row statistics.  The student
+    scores and the gradients come from dsa_indexer_kl_grad.
+
+    q [B,S,H,D], kv [B,S,D], kv_compress [B,S_c,D], attn_sink [H], q_indexer [B,S,H_I,D_I],
+    k_indexer [B,S_c,D_I], weights [B,S,H_I], compress_topk_idxs [B,S,K] (offset by
+    ``offset``, -1 empty).  Returns (dq_indexer fp32, dk_indexer fp32 [B,S_c,D_I],
+    dweights fp32, loss_rows fp32 [B,S]); gradients are scaled by ``grad_scale``.
+    """
+    B, S, H, D = q.shape
+    cmp = compress_topk_idxs.to(torch.int32)
+    local = torch.where(cmp < 0, cmp, cmp - int(offset)).contiguous()
+    n_cmp = kv_compress.shape[1]
+    idx = v4_attention_indices(B, S, q.device, win_left=window_size - 1, cmp_ratio=2, n_cmp=n_cmp,
+                               cmp_indices=torch.where(local < 0, local, local + kv.shape[1]))
+    W = window_size
+    bf16 = q.dtype == torch.bfloat16
+    dqk, dv = (576, 512) if bf16 else (D, D)
+    q_ext = _pad_rows(q.detach(), dqk)
+    kv_ext = _pad_rows(torch.cat([kv.detach(), kv_compress.detach()], dim=1), dqk)
+    _, smax, ssum = sparse_mla_fwd(q_ext, kv_ext, idx, softmax_scale, d_v=dv, q_offset=_NO_MASK_OFFSET)
+    m2, s2, _ = _sink_fold(smax, ssum, attn_sink.detach())
+    mass = attn_mass(q_ext, kv_ext, idx, m2, s2, softmax_scale, q_offset=_NO_MASK_OFFSET)
+    dist = (mass[..., W:] / H).contiguous()
+    return indexer_kl_grad_from_mass(q_indexer, k_indexer, weights, local, dist, q_offset=_NO_MASK_OFFSET,
+                                     loss_scale=softmax_scale, eps=eps, grad_scale=grad_scale)
 
 
 def npu_sparse_lightning_indexer_grad_kl_loss(
