@@ -73,10 +73,14 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   const int64_t limit = tok + q_offset;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
 
-  // the row's slot indices (block count) and the row's Q are requested together; the
-  // block count waits only for the indices
+  // the row's slot indices (block count), the index ring entries of blocks 0..2 (wave 0,
+  // DMA) and the row's Q are requested together; the block count waits only for the indices
   int vidx[kIdxU];
   load_row_indices(ridx, K, vidx);
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);  // clamped to slot K-1
+  }
   // ---- Q: latent qb[s] = q[16s + 8h .. +8] of head `head` (B operand of S^T = K Q^T for
   // k-step s) in VGPRs; the rope columns go to LDS below ----
   // (unconditional loads, orow points at head 0 for absent heads: a load under a branch
@@ -92,6 +96,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   }
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (nblk == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring DMA has landed before the LDS is released
     if (hok) {
       uint32_t* o32 = reinterpret_cast<uint32_t*>(out + orow * kDv);
       for (int i = h; i < kDv / 2; i += 2) o32[i] = 0u;
@@ -160,8 +165,8 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   // ends with its DMAs landed (vmcnt 0) and one barrier, so a gather has about one block
   // time to arrive.  Block validity bits travel in SGPRs.
   const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
-  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);  // ring entries 0..2
-  __syncthreads();                                      // also publishes qpe
+  if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
+  __syncthreads();                                                  // publishes them and qpe
   for (int i = tid; i < kTileChunks; i += kFwdThreads) tile[2][i] = (u32x4){0u, 0u, 0u, 0u};
   uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
 #pragma unroll
