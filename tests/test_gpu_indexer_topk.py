@@ -66,6 +66,58 @@ def test_topk_all_equal_and_short_rows():
     assert torch.all(idx.cpu()[0, 0, 1:] == -1) and idx.cpu()[0, 0, 0] == 0
 
 
+def _topk_check(scores, k, **kw):
+    idx, vals = _ops().topk_select(scores.to(DEV), k, return_values=True, **kw)
+    ref = _oracle_topk(scores, k, kw.get("q_offset", 0), kw.get("cmp_ratio", 1), kw.get("index_offset", 0))
+    assert torch.equal(idx.cpu(), ref)
+    src = torch.where(ref >= 0, ref - kw.get("index_offset", 0), 0).long()
+    ref_vals = torch.where(ref >= 0, torch.gather(scores, -1, src), torch.tensor(float("-inf")))
+    assert torch.equal(vals.cpu().view(torch.int32), ref_vals.view(torch.int32))  # bit for bit, -0.0 kept
+
+
+@pytest.mark.parametrize("n", [8191, 8192, 8193, 16383, 16384, 16385, 24577, 40003])
+def test_topk_segment_boundaries(n):
+    # rows of one register-resident segment (<= 8192 / 16384 scores) and rows re-read in
+    # segments, with lengths that are not multiples of 4 (scalar tail chunk)
+    S, k = 6, 2048
+    g = torch.Generator().manual_seed(n)
+    scores = torch.randn(1, S, n, generator=g)
+    _topk_check(scores, k, q_offset=n - S)
+
+
+def test_topk_unaligned_row_stride():
+    # a column slice: rows start at 4-byte but not 16-byte aligned offsets (scalar loads)
+    S, n, k = 40, 3001, 300
+    g = torch.Generator().manual_seed(11)
+    wide = torch.randn(1, S, n + 2, generator=g)  # row stride 3003 floats
+    scores = wide[:, :, :n]
+    idx, _ = _ops().topk_select(wide.to(DEV)[:, :, :n], k, q_offset=n - S)
+    assert torch.equal(idx.cpu(), _oracle_topk(scores.contiguous(), k, q_offset=n - S))
+
+
+def test_topk_clustered_keys_need_every_pass():
+    # scores 1 + m * 2^-23 with m < 2^22 (one exponent, 22 significant key bits) and runs of
+    # equal values: the threshold needs all refinement passes and then the tie rule
+    S, n, k = 24, 6000, 1000
+    g = torch.Generator().manual_seed(12)
+    m = torch.randint(0, 1 << 22, (1, S, n), generator=g)
+    m[:, :, ::5] = m[:, :, :1]  # many copies of each row's first value
+    scores = 1.0 + m.double() * 2.0 ** -23
+    _topk_check(scores.float(), k, q_offset=n - S)
+
+
+def test_topk_outliers_and_infinities():
+    S, n, k = 16, 9000, 2048
+    g = torch.Generator().manual_seed(13)
+    scores = torch.full((1, S, n), 0.5)
+    scores[:, :, torch.randint(0, n, (50,), generator=g)] = torch.randn(50, generator=g) * 1e30
+    scores[:, 3:, 7::97] = float("inf")
+    scores[:, 5:, 9::89] = float("-inf")
+    scores[:, 8:, 11::83] = float("nan")
+    scores[:, 10:, 13::71] = -0.0
+    _topk_check(scores, k, q_offset=n - S)
+
+
 def test_topk_index_offset():
     S, n, k = 32, 32, 8
     scores = torch.randn(1, S, n, generator=torch.Generator().manual_seed(4))

@@ -1,142 +1,322 @@
-// Per-row top-k select by 8-bit radix select (4 passes, MSB first) on orderable uint32
-// keys, followed by a stable compaction that emits the chosen indices in ascending order.
+// Per-row top-k select: radix select on orderable uint32 keys with range-adaptive 11-bit
+// digits, followed by a stable compaction that emits the chosen indices in ascending order.
 //
 // Contract (bit-exact): row (b, s) considers t < n_valid = min(s_k, (s + q_offset + 1) /
 // cmp_ratio) whose score is not NaN; it keeps the first k of a stable descending order by
-// (score, lower index) with -0.0 == +0.0.  Ties at the threshold are broken by lower index
-// because the compaction walks indices in order and admits equal keys until the quota is
-// met.  One 256-thread workgroup per row; rows up to 16384 candidates are cached in LDS,
-// longer rows are re-read from global (L2) on each pass.
+// (score, lower index) with -0.0 == +0.0.
+//
+// One 256-thread workgroup per row.  A row is read in segments of 1024·kR scores: thread t
+// holds float4 chunks j = 0..kR-1 at positions 4(t + 256 j), so a segment is one coalesced
+// sweep and index order is (segment, j, thread, element).  Rows of one segment stay in
+// registers for every pass; longer rows are re-read per pass (from L2 / MALL).
+//   pass 0   count of candidates, min and max key
+//   pass 1.. histogram of the next 11 bits of (key - min) below the current bin; the bin
+//            holding the k-th largest key becomes the new prefix.  Digits start at the
+//            highest set bit of (max - min), so clustered scores (all of one exponent)
+//            spread over the bins from the first pass on.  Stops when the bin's keys are
+//            exactly the remaining quota or the bin is a single key value.
+//   compact  key > T is taken; key == T is taken for the first need_eq such keys in index
+//            order.  Output position = (#taken-above before it) + min(#equal before it,
+//            need_eq), from wave ballots and per-(wave, chunk) totals.
 #include "dsa_common.h"
 
 namespace dsa {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kCacheMax = 16384;  // candidates cached in LDS (64 KiB)
+constexpr int kWaves = kThreads / 64;
+constexpr int kDigitBits = 11;
+constexpr int kBins = 1 << kDigitBits;
+constexpr int kBinsPerThread = kBins / kThreads;
 
 __device__ __forceinline__ uint32_t order_key(float x) {
-  if (x != x) return 0u;  // NaN: excluded (key 0 is below every real value's key)
+  if (x != x) return 0u;  // NaN (and masked positions): not a candidate; key 0 is below every real key
   const uint32_t u = __float_as_uint(x + 0.0f);  // -0.0 -> +0.0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// inclusive scan over 256 threads (Hillis-Steele in LDS); returns inclusive value
-__device__ __forceinline__ uint32_t block_scan_incl(uint32_t v, uint32_t* buf) {
-  const int t = threadIdx.x;
-  buf[t] = v;
-  __syncthreads();
-  for (int off = 1; off < kThreads; off <<= 1) {
-    const uint32_t add = t >= off ? buf[t - off] : 0u;
-    __syncthreads();
-    buf[t] += add;
-    __syncthreads();
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = min(v, (uint32_t)__shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)__shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_scan_incl_u(uint32_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t u = __shfl_up(v, o, 64);
+    if (lane >= o) v += u;
   }
-  const uint32_t r = buf[t];
-  __syncthreads();
-  return r;
+  return v;
+}
+// number of set bits of `mask` in lanes below this one
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
-template <bool kCached>
+template <int kR, bool kSingle, bool kVec>
 __global__ void __launch_bounds__(kThreads)
 topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int S,
             int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio, int64_t index_offset) {
-  extern __shared__ uint32_t cache[];
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t scan_buf[kThreads];
-  __shared__ uint32_t sh_prefix, sh_mask, sh_remaining;
+  constexpr int kSeg = kThreads * 4 * kR;
+  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t red[3][kWaves];
+  __shared__ uint32_t tot[2][kR][kWaves];  // per-(chunk, wave) counts of key > T and key == T
+  __shared__ uint32_t sh_bin[3];
 
   const int s = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
   const int64_t row = (int64_t)b * S + s;
   const float* src = scores + row * ld;
-  int64_t nv64 = (s + q_offset + 1) / cmp_ratio;
+  const int64_t nv64 = (s + q_offset + 1) / cmp_ratio;
   const int nv = (int)max((int64_t)0, min((int64_t)s_k, nv64));
+  const int nseg = kSingle ? 1 : (nv + kSeg - 1) / kSeg;
+  const int s_k4 = s_k & ~3;  // scores [0, s_k4) are covered by whole float4 loads
 
-  auto key_at = [&](int i) -> uint32_t { return kCached ? cache[i] : order_key(src[i]); };
-
-  // candidates
-  uint32_t cnt = 0;
-  for (int i = t; i < nv; i += kThreads) {
-    const uint32_t key = order_key(src[i]);
-    if (kCached) cache[i] = key;
-    cnt += key != 0u;
-  }
-  const uint32_t total = block_scan_incl(cnt, scan_buf);  // value at t is partial; take last
-  if (t == kThreads - 1) sh_remaining = total;
-  __syncthreads();
-  const uint32_t n_cand = sh_remaining;
-  __syncthreads();
-
-  uint32_t thresh = 0u;  // keys > thresh are taken outright
-  uint32_t need_eq = 0u; // keys == thresh taken, lowest indices first
-  if (n_cand > (uint32_t)k) {
-    if (t == 0) {
-      sh_prefix = 0u;
-      sh_mask = 0u;
-      sh_remaining = (uint32_t)k;
-    }
-    __syncthreads();
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      hist[t] = 0u;
-      __syncthreads();
-      const uint32_t prefix = sh_prefix, mask = sh_mask;
-      for (int i = t; i < nv; i += kThreads) {
-        const uint32_t key = key_at(i);
-        if (key != 0u && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+  float x[kR][4];
+  // positions past the row's valid prefix become NaN (not candidates)
+  auto load_seg = [&](int sg) {
+    if (kVec) {
+#pragma unroll
+      for (int j = 0; j < kR; ++j) {
+        const int base = sg * kSeg + 4 * (t + kThreads * j);
+        const int at = min(base, s_k4 - 4);  // in bounds; used only when at == base
+        const float4 v = *reinterpret_cast<const float4*>(src + at);
+        x[j][0] = v.x;
+        x[j][1] = v.y;
+        x[j][2] = v.z;
+        x[j][3] = v.w;
       }
-      __syncthreads();
-      // suffix sums: suf[d] = sum_{e >= d} hist[e]; thread t handles bin d = 255 - t
-      const uint32_t incl = block_scan_incl(hist[255 - t], scan_buf);  // sum over bins >= 255-t
-      const uint32_t excl = incl - hist[255 - t];                      // bins > 255-t
-      const uint32_t rem = sh_remaining;
-      __syncthreads();
-      if (excl < rem && incl >= rem) {  // exactly one bin satisfies this
-        const uint32_t d = 255u - (uint32_t)t;
-        sh_prefix = prefix | (d << shift);
-        sh_mask = mask | (255u << shift);
-        sh_remaining = rem - excl;
+#pragma unroll
+      for (int j = 0; j < kR; ++j) {
+        const int base = sg * kSeg + 4 * (t + kThreads * j);
+        if (base >= s_k4 && base < nv) {  // the partial last chunk of a row whose length is not a multiple of 4
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[j][e] = base + e < nv ? src[base + e] : 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (base + e >= nv) x[j][e] = __builtin_nanf("");
       }
-      __syncthreads();
+    } else {
+#pragma unroll
+      for (int j = 0; j < kR; ++j) {
+        const int base = sg * kSeg + 4 * (t + kThreads * j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[j][e] = src[min(base + e, nv - 1)];
+      }
+#pragma unroll
+      for (int j = 0; j < kR; ++j) {
+        const int base = sg * kSeg + 4 * (t + kThreads * j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (base + e >= nv) x[j][e] = __builtin_nanf("");
+      }
     }
-    thresh = sh_prefix;
-    need_eq = sh_remaining;
-  }
+  };
 
-  // stable compaction over contiguous per-thread segments, ascending index order
-  const int seg = (nv + kThreads - 1) / kThreads;
-  const int i0 = min(nv, t * seg), i1 = min(nv, i0 + seg);
-  uint32_t c_gt = 0, c_eq = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = key_at(i);
-    c_gt += key > thresh;
-    c_eq += (key == thresh) && key != 0u;
-  }
-  const uint32_t eq_before = block_scan_incl(c_eq, scan_buf) - c_eq;
-  const uint32_t eq_take = need_eq > eq_before ? min(c_eq, need_eq - eq_before) : 0u;
-  const uint32_t mine = c_gt + eq_take;
-  const uint32_t pos0 = block_scan_incl(mine, scan_buf) - mine;
   int32_t* oi = out_idx + row * k;
   float* ov = out_val ? out_val + row * k : nullptr;
-  uint32_t pos = pos0, eq_seen = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = key_at(i);
-    bool take = key > thresh;
-    if (!take && key == thresh && key != 0u) {
-      take = eq_seen < eq_take;
-      ++eq_seen;
+  if (nv == 0) {
+    for (int j = t; j < k; j += kThreads) {
+      oi[j] = -1;
+      if (ov) ov[j] = -INFINITY;
     }
-    if (take) {
-      oi[pos] = (int32_t)(i + index_offset);
-      if (ov) ov[pos] = src[i];
-      ++pos;
+    return;
+  }
+
+  // ---- pass 0: candidates, min and max key ----
+  uint32_t cnt = 0, kmin = 0xffffffffu, kmax = 0u;
+  for (int sg = 0; sg < nseg; ++sg) {
+    load_seg(sg);
+#pragma unroll
+    for (int j = 0; j < kR; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t key = order_key(x[j][e]);
+        if (key) {
+          ++cnt;
+          kmin = min(kmin, key);
+          kmax = max(kmax, key);
+        }
+      }
+  }
+  cnt = wave_sum_u(cnt);
+  kmin = wave_min_u(kmin);
+  kmax = wave_max_u(kmax);
+  if (lane == 0) {
+    red[0][wave] = cnt;
+    red[1][wave] = kmin;
+    red[2][wave] = kmax;
+  }
+  __syncthreads();
+  uint32_t n_cand = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    n_cand += red[0][w];
+    kmin = min(kmin, red[1][w]);
+    kmax = max(kmax, red[2][w]);
+  }
+
+  // ---- threshold: take key > T, and key == T for the first need_eq in index order ----
+  uint32_t T = 0u, need_eq = 0u;  // n_cand <= k: every candidate (key > 0)
+  if (n_cand > (uint32_t)k) {
+    const uint32_t range = kmax - kmin;
+    int sh = range ? 32 - __clz(range) : 0;  // the current bin is rel in [lo, lo + 2^sh)
+    uint32_t lo = 0u, rem = (uint32_t)k;
+    bool whole_bin = false;
+    while (sh > 0) {
+      const int nsh = max(sh - kDigitBits, 0);
+      const int nb = 1 << (sh - nsh);
+      for (int i = t; i < nb; i += kThreads) hist[i] = 0u;
+      __syncthreads();
+      for (int sg = 0; sg < nseg; ++sg) {
+        if (!kSingle) load_seg(sg);
+#pragma unroll
+        for (int j = 0; j < kR; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t key = order_key(x[j][e]);
+            const uint64_t d = (uint64_t)(key - kmin) - lo;  // wraps far above the bin when rel < lo
+            if (key && d < (1ull << sh)) atomicAdd(&hist[(uint32_t)(d >> nsh)], 1u);
+          }
+      }
+      __syncthreads();
+      // thread t sums bins [nb - 8(t+1), nb - 8t) (from the top); exclusive scan in thread
+      // order = keys in bins above its range
+      const int hi = nb - kBinsPerThread * t;
+      uint32_t c[kBinsPerThread], my = 0;
+#pragma unroll
+      for (int i = 0; i < kBinsPerThread; ++i) {
+        const int bin = hi - 1 - i;
+        c[i] = bin >= 0 ? hist[bin] : 0u;
+        my += c[i];
+      }
+      const uint32_t incl = wave_scan_incl_u(my, lane);
+      if (lane == 63) red[0][wave] = incl;
+      __syncthreads();
+      uint32_t above = incl - my;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w)
+        if (w < wave) above += red[0][w];
+      if (above < rem && rem <= above + my) {  // exactly one thread
+#pragma unroll
+        for (int i = 0; i < kBinsPerThread; ++i) {
+          if (above < rem && rem <= above + c[i]) {
+            sh_bin[0] = (uint32_t)(hi - 1 - i);
+            sh_bin[1] = above;
+            sh_bin[2] = c[i];
+          }
+          above += c[i];
+        }
+      }
+      __syncthreads();
+      const uint32_t bin = sh_bin[0], n_above = sh_bin[1], n_bin = sh_bin[2];
+      lo += bin << nsh;
+      rem -= n_above;
+      sh = nsh;
+      if (n_bin == rem) {
+        whole_bin = true;
+        break;
+      }
+      __syncthreads();  // sh_bin and red are rewritten by the next pass
     }
+    if (whole_bin) {
+      T = kmin + lo - 1u;  // lo >= 1 here: lo == 0 would take every candidate (n_cand == k)
+      need_eq = 0u;
+    } else {
+      T = kmin + lo;
+      need_eq = rem;
+    }
+  }
+
+  // ---- compaction in index order ----
+  uint32_t gt_base = 0, eq_base = 0;
+  for (int sg = 0; sg < nseg; ++sg) {
+    if (!kSingle) load_seg(sg);
+    uint32_t pg[kR], pe[kR], mg[kR], me[kR];  // lanes-below counts and this lane's flag bits
+#pragma unroll
+    for (int j = 0; j < kR; ++j) {
+      uint32_t below_g = 0, below_e = 0, wg = 0, we = 0, fg = 0, fe = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t key = order_key(x[j][e]);
+        const bool g = key > T;
+        const bool q = key == T && key != 0u;
+        const uint64_t bg = __ballot(g), bq = __ballot(q);
+        below_g += lanes_below(bg);
+        below_e += lanes_below(bq);
+        wg += (uint32_t)__popcll(bg);
+        we += (uint32_t)__popcll(bq);
+        fg |= (uint32_t)g << e;
+        fe |= (uint32_t)q << e;
+      }
+      pg[j] = below_g;
+      pe[j] = below_e;
+      mg[j] = fg;
+      me[j] = fe;
+      if (lane == 0) {
+        tot[0][j][wave] = wg;
+        tot[1][j][wave] = we;
+      }
+    }
+    __syncthreads();
+    uint32_t run_g = gt_base, run_e = eq_base;  // counts before chunk j of this segment
+#pragma unroll
+    for (int j = 0; j < kR; ++j) {
+      uint32_t bg = run_g + pg[j], be = run_e + pe[j];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        if (w < wave) {
+          bg += tot[0][j][w];
+          be += tot[1][j][w];
+        }
+        run_g += tot[0][j][w];
+        run_e += tot[1][j][w];
+      }
+      const int base = sg * kSeg + 4 * (t + kThreads * j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool g = (mg[j] >> e) & 1u, q = (me[j] >> e) & 1u;
+        const bool take = g || (q && be < need_eq);
+        const uint32_t pos = bg + min(be, need_eq);
+        if (take && pos < (uint32_t)k) {  // (always < k: the threshold admits exactly min(n_cand, k))
+          oi[pos] = (int32_t)(base + e + index_offset);
+          if (ov) ov[pos] = x[j][e];
+        }
+        bg += g;
+        be += q;
+      }
+    }
+    gt_base = run_g;
+    eq_base = run_e;
+    if (!kSingle) __syncthreads();  // tot is rewritten by the next segment
   }
   const uint32_t taken = min(n_cand, (uint32_t)k);
   for (int j = (int)taken + t; j < k; j += kThreads) {
     oi[j] = -1;
     if (ov) ov[j] = -INFINITY;
   }
+}
+
+template <int kR, bool kSingle>
+void launch_topk(bool vec, dim3 grid, hipStream_t st, const float* scores, int32_t* indices, float* values, int S,
+                 int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio, int64_t index_offset) {
+  if (vec)
+    topk_kernel<kR, kSingle, true><<<grid, kThreads, 0, st>>>(scores, indices, values, S, s_k, ld, k, q_offset,
+                                                              cmp_ratio, index_offset);
+  else
+    topk_kernel<kR, kSingle, false><<<grid, kThreads, 0, st>>>(scores, indices, values, S, s_k, ld, k, q_offset,
+                                                               cmp_ratio, index_offset);
 }
 
 }  // namespace
@@ -151,17 +331,18 @@ extern "C" int dsa_topk(const float* scores, int32_t* indices, float* values, in
     return set_error(DSA_ERR_INVALID_ARG, "dsa_topk: bad sizes (B=%lld S=%lld S_k=%lld ld=%lld k=%lld r=%lld)",
                      (long long)batch, (long long)s_q, (long long)s_k, (long long)ld_scores, (long long)k,
                      (long long)cmp_ratio);
-  if (s_q > 2147483647LL || batch > 65535 || s_k > 2147483647LL)
+  if (s_q > 2147483647LL || batch > 65535 || s_k > 2147483647LL - 16384)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_topk: sizes out of range");
   hipStream_t st = (hipStream_t)stream;
   dim3 grid((unsigned)s_q, (unsigned)batch);
-  if (s_k <= kCacheMax) {
-    topk_kernel<true><<<grid, kThreads, (size_t)s_k * 4, st>>>(scores, indices, values, (int)s_q, (int)s_k,
-                                                               ld_scores, (int)k, q_offset, (int)cmp_ratio,
-                                                               index_offset);
-  } else {
-    topk_kernel<false><<<grid, kThreads, 0, st>>>(scores, indices, values, (int)s_q, (int)s_k, ld_scores, (int)k,
-                                                  q_offset, (int)cmp_ratio, index_offset);
-  }
+  // float4 loads need 16-byte aligned rows and at least one whole float4 per row
+  const bool vec = s_k >= 4 && (ld_scores % 4) == 0 && ((uintptr_t)scores % 16) == 0;
+  const int S = (int)s_q, n = (int)s_k, kk = (int)k, r = (int)cmp_ratio;
+  if (s_k <= 8192)
+    launch_topk<8, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
+  else if (s_k <= 16384)
+    launch_topk<16, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
+  else
+    launch_topk<16, false>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
   return check_launch("dsa_topk");
 }
