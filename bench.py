@@ -35,7 +35,13 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--seq", type=int, default=8192)
+    p.add_argument("--workload", choices=("c3", "c4", "c5", "c5-long"), default="c3",
+                   help="c3 (default, the headline): dense-KV step at S=8192; c4: compressed-KV step "
+                        "(block compressor r=4, indexer and attention over S/4 compressed rows, S=32768); "
+                        "c5: 8 packed sequences of U[1024,32768] tokens through the varlen entry points; "
+                        "c5-long: one 131072-token sequence")
+    p.add_argument("--seq", type=int, default=None, help="query tokens (default: 8192, or 32768 for c4, "
+                                                          "131072 for c5-long)")
     p.add_argument("--heads", type=int, default=128)
     p.add_argument("--topk", type=int, default=2048)
     p.add_argument("--seed", type=int, default=0)
@@ -46,9 +52,14 @@ def parse_args():
     return p.parse_args()
 
 
-def make_inputs(S, H, topk, seed, device):
+def make_inputs(S, H, topk, seed, device, on_device=False):
+    """Seeded synthetic inputs of one dense-KV step.  ``on_device`` draws them with a
+    generator on the GPU (the long-sequence workloads; the host generator would spend
+    minutes on tens of GB of normals)."""
     import torch
 
+    if on_device:
+        return _device_inputs(S, H, topk, seed, device, [S], [S])
     g = torch.Generator().manual_seed(seed)
     d_qk, d_v, h_i, d_i = 576, 512, 64, 128
     # fixed draw order: q, kv, q_idx, k_idx, w, dout
@@ -69,6 +80,64 @@ def make_inputs(S, H, topk, seed, device):
         scale=d_qk ** -0.5,
         topk=topk,
     )
+
+
+def _device_inputs(T, H, topk, seed, device, lens_q, lens_k, kv_rows=None):
+    """Packed inputs drawn on the device: q [1,T,H,576], kv [1,kv_rows,576], q_idx
+    [1,T,64,128], k_idx [1,kv_rows,128], w [1,T,64], dout [1,T,H,512] (same draw order as
+    the host variant)."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    d_qk, d_v, h_i, d_i = 576, 512, 64, 128
+    kv_rows = T if kv_rows is None else kv_rows
+    bf = dict(device=device, dtype=torch.bfloat16, generator=g)
+    q = torch.randn(1, T, H, d_qk, **bf)
+    kv = torch.randn(1, kv_rows, d_qk, **bf)
+    q_idx = torch.randn(1, T, h_i, d_i, **bf)
+    k_idx = torch.randn(1, kv_rows, d_i, **bf)
+    w = torch.rand(1, T, h_i, device=device, generator=g) * h_i ** -0.5 * d_i ** -0.5
+    dout = torch.randn(1, T, H, d_v, **bf)
+    return dict(q=q, kv=kv, q_idx=q_idx, k_idx=k_idx, w=w, dout=dout, scale=d_qk ** -0.5, topk=topk,
+                lens_q=list(lens_q), lens_k=list(lens_k))
+
+
+def compressor_inputs(S, D, ratio, seed, device):
+    """Inputs of one block-compressor call (reference Compressor._forward_bsnd): the wkv and
+    wgate projections [1,S,coff*D] fp32 (gate logits ~N(0,1)), ape ~N(0,0.02) [ratio,coff*D],
+    RMSNorm weight [D]; coff = 2 (overlapping blocks) when ratio == 4."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    coff = 2 if ratio == 4 else 1
+    f = dict(device=device, dtype=torch.float32, generator=g)
+    kv = torch.randn(1, S, coff * D, **f)
+    score = torch.randn(1, S, coff * D, **f)
+    ape = torch.randn(ratio, coff * D, **f) * 0.02
+    norm_w = 1.0 + 0.1 * torch.randn(D, **f)
+    return dict(kv=kv, score=score, ape=ape, norm_w=norm_w, ratio=ratio, D=D, coff=coff, S=S)
+
+
+def compressor_bytes(c):
+    """Algorithmic bytes of one compressor call: both fp32 projections read once, ape, and the
+    bf16 output rows."""
+    S, D, r, coff = c["S"], c["D"], c["ratio"], c["coff"]
+    return 2 * S * coff * D * 4 + r * coff * D * 4 + (S // r) * D * 2
+
+
+def time_ms(torch, fn, reps=10):
+    """Average duration (ms) of ``fn`` over ``reps`` back-to-back calls, HIP events on the
+    current stream (the one every op here launches on), after one untimed call."""
+    fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 class PhaseTimer:
@@ -122,15 +191,71 @@ def dsa_step(inp, ops, timer):
     return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss_rows)
 
 
-def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128):
+def c4_step(inp, comp, comp_i, ops, timer):
+    """One compressed-KV layer (config C4): block compressor (r=4, overlapping blocks,
+    RMSNorm epilogue) for the 512-column KV and the 128-column indexer keys -> fp8
+    indexer + top-k over the S/4 compressed rows (valid: t < (s+1)//4) -> gathered
+    attention forward + backward over the selected compressed rows -> indexer KL
+    gradients.  Compressed rows have 512 columns (k = v = the row, as in
+    SparseAttention); the 576-column kernels see them with 64 zero columns."""
+    import torch.nn.functional as F
+
+    with timer("compressor"):
+        ckv = ops.compressor_pool(comp["kv"], comp["score"], comp["ape"], 4, norm_weight=comp["norm_w"])
+        cki = ops.compressor_pool(comp_i["kv"], comp_i["score"], comp_i["ape"], 4, norm_weight=comp_i["norm_w"])
+    with timer("quantize"):
+        q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
+        k8, ks = ops.quantize_fp8_per_row(cki)
+    with timer("indexer_topk"):
+        idx, _ = ops.npu_lightning_indexer(q8, k8, inp["w"], sparse_count=inp["topk"], sparse_mode=3, cmp_ratio=4,
+                                           query_scale=qs, key_scale=ks)
+        idx = idx[:, :, 0]
+    nm = ops._NO_MASK_OFFSET  # validity is already in the indices (-1 past (s+1)//4)
+    with timer("attn_fwd"):
+        kv = F.pad(ckv, (0, 64))
+        out, smax, ssum = ops.sparse_mla_fwd(inp["q"], kv, idx, inp["scale"], q_offset=nm)
+    with timer("attn_bwd"):
+        dq, dkv, mass = ops.sparse_mla_bwd(inp["q"], kv, idx, out, inp["dout"], smax, ssum, inp["scale"],
+                                           q_offset=nm, return_mass=True)
+    with timer("indexer_kl_grad"):
+        dq_i, dk_i, dw, loss_rows = ops.indexer_kl_grad_from_mass(inp["q_idx"], cki, inp["w"], idx, mass,
+                                                                  q_offset=nm)
+    return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss_rows)
+
+
+def c5_step(inp, ops, timer):
+    """One layer over a packed varlen batch (config C5 ii) through the ``_varlen`` entry
+    points: each sequence attends causally to its own tokens only."""
+    cu = [0]
+    for n in inp["lens_q"]:
+        cu.append(cu[-1] + n)
+    q, kv, qi, ki, w, do = (inp[k][0] for k in ("q", "kv", "q_idx", "k_idx", "w", "dout"))
+    with timer("quantize"):
+        q8, qs = ops.quantize_fp8_per_row(qi)
+        k8, ks = ops.quantize_fp8_per_row(ki)
+    with timer("indexer_topk"):
+        idx, _ = ops.lightning_indexer_varlen(q8, k8, w, cu, cu, inp["topk"], query_scale=qs, key_scale=ks)
+    with timer("attn_fwd"):
+        out, smax, ssum = ops.sparse_mla_fwd_varlen(q, kv, idx, inp["scale"], cu, cu)
+    with timer("attn_bwd"):
+        dq, dkv, mass = ops.sparse_mla_bwd_varlen(q, kv, idx, out, do, smax, ssum, inp["scale"], cu, cu,
+                                                  return_mass=True)
+    with timer("indexer_kl_grad"):
+        dq_i, dk_i, dw, loss_rows = ops.indexer_kl_grad_from_mass_varlen(qi, ki, w, idx, mass, cu, cu)
+    return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss_rows)
+
+
+def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128, causal_pairs=None):
     """Algorithmic bytes and FLOPs of the DSA path per step.
 
     sum_keff = number of valid (row, slot) pairs; every head of a row shares its gathered
     KV rows, so each row's keys are counted once; dKV is counted as an fp32 scatter-add
-    payload (4 bytes per element per pair).
+    payload (4 bytes per element per pair).  ``causal_pairs`` = the (query, key) pairs the
+    indexer scores (default: one causal sequence of S tokens).
     """
     sum_keff = int((idx >= 0).sum().item())
-    causal_pairs = S * (S + 1) // 2
+    if causal_pairs is None:
+        causal_pairs = S * (S + 1) // 2
     K = topk
     fwd_bytes = 2 * H * d_qk * S + 2 * d_qk * sum_keff + 4 * K * S + 2 * H * d_v * S + 4 * H * S
     bwd_bytes = (2 * H * d_qk * S * 2 + 2 * H * d_v * S * 2 + 4 * H * S + 4 * K * S + 2 * d_qk * sum_keff
@@ -176,19 +301,8 @@ def time_indexer_kernel(inp, ops, torch, reps=10):
     S = q8.shape[1]
     out = torch.empty(1, S, k8.shape[1], dtype=torch.float32, device=q8.device)
 
-    def run():
-        ops.indexer_scores(q8, k8, inp["w"], q_scale=qs, k_scale=ks, q_offset=0, out=out)
-
-    run()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
+    ms = time_ms(torch, lambda: ops.indexer_scores(q8, k8, inp["w"], q_scale=qs, k_scale=ks, q_offset=0, out=out),
+                 reps)
     del out
     return ms
 
@@ -265,6 +379,39 @@ def cpu_baseline(inp_gpu, S, H, topk, seconds):
     )
 
 
+def kernel_rooflines(inp, ops, torch, dev, S, K, seed, with_topk):
+    """Per-kernel roofline entries measured outside the timed steps: the block compressor at
+    config C4's shape (32768 tokens, r = 4 with overlapping blocks, D = 512 and the indexer's
+    D_I = 128; HBM-bound) and, for a dense-KV workload, the top-k selection over the full
+    causal score matrix (HBM-bound: scores read once, indices written)."""
+    out = {}
+    comp = [compressor_inputs(32768, d, 4, seed + 1 + i, dev) for i, d in enumerate((512, 128))]
+
+    def run_comp():
+        for c in comp:
+            ops.compressor_pool(c["kv"], c["score"], c["ape"], 4, norm_weight=c["norm_w"])
+
+    ms = time_ms(torch, run_comp)
+    nbytes = sum(compressor_bytes(c) for c in comp)
+    out["compressor"] = dict(kernel="compressor_kernel (D=512 and D=128 launches)", bound="hbm",
+                             shape="C4: 32768 tokens, r=4, overlap, RMSNorm epilogue, bf16 out",
+                             algorithmic_bytes=nbytes, avg_launch_ms=ms,
+                             achieved=nbytes / (ms * 1e-3) / 1e9, peak=HBM_PEAK_GBPS, unit="GB/s",
+                             frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS)
+    del comp
+    if with_topk:
+        q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
+        k8, ks = ops.quantize_fp8_per_row(inp["k_idx"])
+        scores = ops.indexer_scores(q8, k8, inp["w"], q_scale=qs, k_scale=ks, q_offset=0)
+        ms = time_ms(torch, lambda: ops.topk_select(scores, K, q_offset=0))
+        nbytes = 4 * (S * (S + 1) // 2) + 4 * K * S
+        out["topk"] = dict(kernel="dsa_topk", bound="hbm", algorithmic_bytes=nbytes, avg_launch_ms=ms,
+                           achieved=nbytes / (ms * 1e-3) / 1e9, peak=HBM_PEAK_GBPS, unit="GB/s",
+                           frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS)
+        del scores
+    return out
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -277,13 +424,41 @@ def main():
     from torchtitan_npu_simulator_amd import torch_npu_ops as ops
 
     dev = torch.device("cuda:0")
-    S, H, K = args.seq, args.heads, args.topk
+    wl = args.workload
+    H, K = args.heads, args.topk
+    S = args.seq or {"c3": 8192, "c4": 32768, "c5": 0, "c5-long": 131072}[wl]
     if args.copy_calibration:
         copy_calibration(torch, dev)
-    inp = make_inputs(S, H, K, args.seed, dev)
+    pairs = None
+    if wl == "c3":
+        inp = make_inputs(S, H, K, args.seed, dev)
+        step = lambda t: dsa_step(inp, ops, t)  # noqa: E731
+        cfg = dict(workload="C3: DeepSeek-V3.2 DSA layer fwd+bwd", batch=1, seq_len=S)
+    elif wl == "c5-long":
+        inp = make_inputs(S, H, K, args.seed, dev, on_device=True)
+        step = lambda t: dsa_step(inp, ops, t)  # noqa: E731
+        cfg = dict(workload="C5(i): one long sequence, DSA layer fwd+bwd, indexer chunked by query rows",
+                   batch=1, seq_len=S)
+    elif wl == "c4":
+        inp = _device_inputs(S, H, K, args.seed, dev, [S], [S // 4], kv_rows=0)
+        comp = compressor_inputs(S, 512, 4, args.seed + 1, dev)
+        comp_i = compressor_inputs(S, 128, 4, args.seed + 2, dev)
+        step = lambda t: c4_step(inp, comp, comp_i, ops, t)  # noqa: E731
+        pairs = sum((s + 1) // 4 for s in range(S))
+        cfg = dict(workload="C4: compressed KV (r=4, overlap) compressor + indexer + attention fwd+bwd",
+                   batch=1, seq_len=S, compressed_rows=S // 4, cmp_ratio=4)
+    else:  # c5: packed varlen batch
+        g = torch.Generator().manual_seed(args.seed)
+        lens = torch.randint(1024, 32769, (8,), generator=g).tolist()
+        S = sum(lens)
+        inp = _device_inputs(S, H, K, args.seed, dev, lens, lens)
+        step = lambda t: c5_step(inp, ops, t)  # noqa: E731
+        pairs = sum(n * (n + 1) // 2 for n in lens)
+        cfg = dict(workload="C5(ii): 8 packed sequences (TND), varlen entry points, fwd+bwd", tokens=S,
+                   seq_lens=lens)
     timer = PhaseTimer(torch)
     for _ in range(args.warmup):
-        res = dsa_step(inp, ops, timer)
+        res = step(timer)
     torch.cuda.synchronize()
     timer.enabled = True
     t0 = torch.cuda.Event(enable_timing=True)
@@ -291,12 +466,13 @@ def main():
     torch.cuda.synchronize()
     t0.record()
     for _ in range(args.steps):
-        res = dsa_step(inp, ops, timer)
+        res = step(timer)
     t1.record()
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / args.steps
     phases = timer.averages_ms()
-    work = algorithmic_work(S, H, K, res["idx"])
+    work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs)
+    del res
 
     # Dominant kernel: the gathered sparse MLA forward (sparse_mla_fwd_bf16_kernel; its
     # row-fixup pass is launched in the same call and is timed with it).  Its algorithmic
@@ -311,7 +487,7 @@ def main():
         unit="GB/s",
         algorithmic_bytes=work["attn_fwd_bytes"],
         avg_launch_ms=fwd_ms,
-        traffic=measured_traffic("sparse_mla_fwd_bf16_kernel", S, H, K),
+        traffic=measured_traffic("sparse_mla_fwd_bf16_kernel", S, H, K) if wl == "c3" else None,
     )
     roof["frac"] = roof["achieved"] / roof["peak"]
     attn_bytes = work["attn_fwd_bytes"] + work["attn_bwd_bytes"]
@@ -324,10 +500,13 @@ def main():
         algorithmic_bytes=attn_bytes,
     )
     roof_pair["frac"] = roof_pair["achieved"] / roof_pair["peak"]
-    idx_ms = phases["indexer_topk"]
-    idx_kernel_ms = time_indexer_kernel(inp, ops, torch)
+    cfg.update(heads=H, d_qk=576, d_v=512, topk=K, index_heads=64, index_dim=128, sum_k_eff=work["sum_keff"],
+               indexer_pairs=pairs if pairs is not None else S * (S + 1) // 2)
+    metric = "sparse-attn fwd+bwd tokens/s @S=8K,top-k 2048; % HBM / MFMA roofline"
+    if wl != "c3":
+        metric = f"sparse-attn fwd+bwd tokens/s, workload {wl}; % HBM / MFMA roofline"
     line = dict(
-        metric="sparse-attn fwd+bwd tokens/s @S=8K,top-k 2048; % HBM / MFMA roofline",
+        metric=metric,
         value=S / (ms_per_step * 1e-3),
         unit="tokens/s",
         n_gpus=1,
@@ -339,21 +518,27 @@ def main():
         vs_baseline=None,
         dtype="bf16 (attention), fp8-e4m3 (indexer)",
         data="synthetic, seeded N(0,1) inputs",
-        config=dict(workload="C3: DeepSeek-V3.2 DSA layer fwd+bwd", batch=1, seq_len=S, heads=H, d_qk=576, d_v=512,
-                    topk=K, index_heads=64, index_dim=128, sum_k_eff=work["sum_keff"]),
+        config=cfg,
         roofline=roof,
         roofline_attention_fwd_bwd=roof_pair,
         phases_ms={k: round(v, 4) for k, v in phases.items()},
-        indexer_mfma=dict(kernel="indexer_tile_kernel<true, 4>", bound="mfma", flops=work["indexer_flops"],
-                          avg_launch_ms=idx_kernel_ms,
-                          achieved_tflops=work["indexer_flops"] / (idx_kernel_ms * 1e-3) / 1e12,
-                          peak_tflops=FP8_PEAK_TFLOPS,
-                          frac=work["indexer_flops"] / (idx_kernel_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS,
-                          ms_with_topk=idx_ms),
         attn_mfma=dict(fwd_tflops=work["attn_fwd_flops"] / (fwd_ms * 1e-3) / 1e12,
                        bwd_tflops=work["attn_bwd_flops"] / (bwd_ms * 1e-3) / 1e12, peak_tflops=BF16_PEAK_TFLOPS),
     )
-    if not args.no_cpu_baseline:
+    idx_ms = phases["indexer_topk"]
+    line["indexer_topk"] = dict(flops=work["indexer_flops"], ms_with_topk=idx_ms,
+                                tflops_with_topk=work["indexer_flops"] / (idx_ms * 1e-3) / 1e12)
+    if wl == "c3":
+        idx_kernel_ms = time_indexer_kernel(inp, ops, torch)
+        line["indexer_mfma"] = dict(kernel="indexer_tile_kernel<true, 4>", bound="mfma", flops=work["indexer_flops"],
+                                    avg_launch_ms=idx_kernel_ms,
+                                    achieved_tflops=work["indexer_flops"] / (idx_kernel_ms * 1e-3) / 1e12,
+                                    peak_tflops=FP8_PEAK_TFLOPS,
+                                    frac=work["indexer_flops"] / (idx_kernel_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS,
+                                    ms_with_topk=idx_ms)
+    if wl in ("c3", "c4"):
+        line["kernels"] = kernel_rooflines(inp, ops, torch, dev, S, K, args.seed, with_topk=wl == "c3")
+    if wl == "c3" and not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(inp, S, H, K, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
