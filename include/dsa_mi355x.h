@@ -22,6 +22,9 @@
  *   dsa_indexer_kl_grad          torch_npu.npu_sparse_lightning_indexer_grad_kl_loss
  *                                (converters/kernels/dsa.py:159-177;
  *                                 ops/aclnn/sparse_lightning_indexer_grad_kl_loss/binding.cpp:12-36)
+ *   dsa_quantize_fp8_rows        the fp8-e4m3 per-row quantisation this build adds in front of
+ *                                npu_lightning_indexer (the reference indexes in bf16 and marks fp8
+ *                                as a QAT step: models/deepseek_v4/model.py:646, :822)
  *   dsa_compressor_fwd           Compressor._forward_bsnd pooling + RMSNorm
  *                                (models/deepseek_v4/model.py:183-221; torch-only in the reference)
  *   dsa_compressor_fwd_tnd       Compressor._forward_tnd (models/deepseek_v4/model.py:223-274)
@@ -168,6 +171,16 @@ int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, co
 int dsa_compressor_fwd(const float* kv, const float* score, const float* ape, const float* norm_weight, void* out,
                        int out_dtype, int64_t batch, int64_t s, int64_t d, int64_t ratio, int overlap,
                        float norm_eps, void* stream);
+
+/*
+ * Per-row fp8-e4m3fn quantisation of indexer operands (q_I rows [.., H_I, D_I], k_I rows).
+ *   x [rows, d] bf16 or fp32 (in_dtype), q [rows, d] e4m3fn bytes, scale [rows] fp32:
+ *   scale = max(amax|x_row| / 448, 1e-12), q = e4m3fn(x / scale) rounded to nearest even,
+ *   magnitudes that round above 448 -> NaN; byte-identical to torch's float8_e4m3fn cast of
+ *   the same quotient.  d <= 2048 (DSA_ERR_UNSUPPORTED beyond).
+ */
+int dsa_quantize_fp8_rows(const void* x, int in_dtype, uint8_t* q, float* scale, int64_t rows, int64_t d,
+                          void* stream);
 
 /*
  * Block KV compressor over a packed varlen ("TND") batch (reference: Compressor._forward_tnd,

@@ -153,15 +153,18 @@ def indexer_scores(q_idx, k_idx, weights, *, q_offset=0, cmp_ratio=1, dtype=torc
 def quantize_e4m3_per_row(x: torch.Tensor):
     """OCP fp8-e4m3fn quantisation with one fp32 scale per row (last dim).
 
-    scale = amax(|row|) / 448 (448 = largest finite e4m3fn), q = round(x / scale).
-    Returns (q as torch.float8_e4m3fn, scale fp32 with the row shape).  The
-    oracle's fp8 indexer computes on ``q.float() * scale`` (quantise, then
-    dequantise), which is what the fp8 MFMA path must reproduce up to fp32
-    summation order.
+    scale = max(amax(|row|) / 448, 1e-12) (448 = largest finite e4m3fn; both the
+    division and x / scale are correctly rounded fp32 divisions), q = x / scale rounded
+    to the nearest e4m3fn value (ties to even).  Returns (q as torch.float8_e4m3fn, scale
+    fp32 with the row shape).  The reference indexes in bf16 (fp8 is a QAT note there,
+    models/deepseek_v4/model.py:646, :822), so this quantiser is the build's definition;
+    the oracle's fp8 indexer computes on ``q.float() * scale`` (quantise, then
+    dequantise), which is what the fp8 MFMA path must reproduce up to fp32 summation
+    order.
     """
     xf = x.float()
-    amax = xf.abs().amax(dim=-1).clamp_min(1e-12)
-    scale = amax / 448.0
+    amax = xf.abs().amax(dim=-1).numpy()
+    scale = torch.from_numpy(np.maximum(amax / np.float32(448.0), np.float32(1e-12)).astype(np.float32))
     q = (xf / scale.unsqueeze(-1)).to(torch.float8_e4m3fn)
     return q, scale
 

@@ -75,6 +75,28 @@ def test_fp8_quantise_dequantise_bound():
     assert torch.allclose(qx.float().abs().amax(-1), torch.full((6,), 448.0))
 
 
+def test_fp8_quantise_definition():
+    # scale: correctly rounded amax / 448 clamped at 1e-12 (numpy float32 arithmetic);
+    # rows whose amax is 448 have scale 1, so midpoints between adjacent e4m3fn values
+    # land on exact ties and must go to the even code
+    codes = torch.arange(0, 0x7F, dtype=torch.uint8)
+    vals = codes.view(torch.float8_e4m3fn).float().double()
+    mids = ((vals[:-1] + vals[1:]) / 2).float()
+    x = torch.cat([torch.tensor([448.0]), mids]).unsqueeze(0)
+    q, sc = O.quantize_e4m3_per_row(x)
+    assert sc.item() == 1.0
+    got = q.view(torch.uint8)[0, 1:].long()
+    lo = codes[:-1].long()
+    assert torch.equal(got, torch.where(lo % 2 == 0, lo, lo + 1))  # ties to the even code
+    g = _g(4)
+    y = torch.randn(5, 64, generator=g) * 7
+    q, sc = O.quantize_e4m3_per_row(y)
+    ref = np.maximum(np.abs(y.numpy()).max(-1) / np.float32(448), np.float32(1e-12))
+    assert np.array_equal(sc.numpy().view(np.uint32), ref.astype(np.float32).view(np.uint32))
+    zero = O.quantize_e4m3_per_row(torch.zeros(1, 8))
+    assert zero[1].item() == np.float32(1e-12) and not zero[0].float().any()
+
+
 # ---------------------------------------------------------------------------
 # a4 top-k
 # ---------------------------------------------------------------------------

@@ -95,10 +95,23 @@ def to_cu_seqlens(cu_seqlens=None, actual_seq_lengths=None, total=None) -> list[
 # lightning indexer + top-k
 # ---------------------------------------------------------------------------
 def quantize_fp8_per_row(x: torch.Tensor):
-    """OCP fp8-e4m3fn with one fp32 scale (amax/448) per row of the last dim."""
-    xf = x.float()
-    scale = (xf.abs().amax(dim=-1) / 448.0).clamp_min(1e-12)
-    return (xf / scale.unsqueeze(-1)).to(torch.float8_e4m3fn), scale
+    """OCP fp8-e4m3fn with one fp32 scale per row of the last dim (dsa_quantize_fp8_rows):
+    scale = max(amax|row| / 448, 1e-12), q = e4m3fn(x / scale) (correctly rounded fp32
+    divisions, round-to-nearest-even cast).  Returns (q like x in
+    torch.float8_e4m3fn, scale fp32 x.shape[:-1])."""
+    lib = load_library()
+    require_gpu_tensor(x, "x")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    x = x.contiguous()
+    d = x.shape[-1]
+    rows = x.numel() // d if d else 0
+    q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
+    scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    if rows:
+        check(lib.dsa_quantize_fp8_rows(ptr(x), _lib.dtype_code(x.dtype), ptr(q), ptr(scale), rows, d,
+                                        stream_of(x.device)), "dsa_quantize_fp8_rows")
+    return q, scale
 
 
 def indexer_scores(q_idx, k_idx, weights, *, q_scale=None, k_scale=None, q_offset=0, cmp_ratio=1, out=None):
