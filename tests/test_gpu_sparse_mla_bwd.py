@@ -55,6 +55,33 @@ def test_bwd_bf16_parity(S, H, K, q_offset, seed, shuffle, holes):
     assert rel_err(dq, adq) <= BF16_TOL and rel_err(dkv, adkv) <= BF16_TOL
 
 
+@pytest.mark.parametrize("K", [96, 99])
+def test_bwd_long_kv_spans_several_counting_ranges(K):
+    """A KV prefix of 40000 rows: the key-major CSR behind dKV counts keys in 16384-key
+    ranges, so the slots (boundary keys 16383/16384, 32767/32768 in every row) fall in
+    three ranges; K = 99 takes the scalar index loads."""
+    S, H = 24, 16
+    s_kv = 40000
+    q_offset = s_kv - S
+    q, kv, dout, scale = attn_inputs(S, H, q_offset=q_offset, seed=21)
+    g = torch.Generator().manual_seed(21)
+    edge = torch.tensor([0, 16383, 16384, 32767, 32768, s_kv - S])
+    idx = torch.empty(1, S, K, dtype=torch.int32)
+    for s in range(S):
+        pick = torch.randperm(s + q_offset + 1, generator=g)[: 2 * K]
+        pick = pick[~torch.isin(pick, edge)][: K - len(edge)]
+        row = torch.cat([edge, pick])
+        idx[0, s] = row[torch.randperm(K, generator=g)].int()
+    out, smax, ssum, dq, dkv = _gpu_fwd_bwd(q, kv, idx, dout, scale, q_offset)
+    _, ref_lse = O.sparse_mla_fwd(q, kv, idx, scale, q_offset=q_offset)
+    rdq, rdkv, _ = O.sparse_mla_bwd_closed_form(q, kv, idx, out, ref_lse, dout, scale, q_offset=q_offset)
+    assert rel_err(dq, rdq) <= BF16_TOL, rel_err(dq, rdq)
+    assert rel_err(dkv, rdkv) <= BF16_TOL, rel_err(dkv, rdkv)
+    touched = torch.zeros(s_kv, dtype=torch.bool)
+    touched[idx.flatten().long()] = True
+    assert float(dkv[0, ~touched].abs().sum()) == 0.0
+
+
 def test_bwd_bf16_chunked_workspace_matches_single_pass():
     """A workspace that only fits a few query rows gives the same gradients (row chunking)."""
     S, H, K = 128, 32, 64

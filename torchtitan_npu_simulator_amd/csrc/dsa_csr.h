@@ -1,9 +1,13 @@
 // Key-major CSR of (query row, slot) pairs and the contribution reduction shared by the
 // attention backward (dKV, 576 wide) and the indexer KL gradient (dK_index, 128 wide).
 //
-// The pairs of a query-row chunk are counted per key with LDS-privatised histograms
-// (keys <= 16384; plain global atomics beyond), scanned into row_ptr, and placed by a
-// second pass that reserves one contiguous range per (workgroup, key).  The reduction
+// The pairs of a query-row chunk are counted per key with LDS-privatised histograms (one
+// workgroup per block of query rows and 16384-key range, the ranges of one row block
+// adjacent in launch order so they share its index rows in L2), scanned into row_ptr, and
+// placed by a second pass that reserves one contiguous range per (workgroup, key).  The
+// row block grows with the key count (about four pairs per key and workgroup), so the
+// global atomics of the histogram flush and the range reservation stay well below one
+// per pair also for long KV prefixes.  The reduction
 // then gives every key a single owner that sums its pairs' bf16 contribution rows in
 // fp32 and adds the result to the caller's accumulator with plain loads/stores, so no
 // float atomics are issued.  Order within a key's list varies run to run, so fp32 sums
@@ -14,67 +18,100 @@
 namespace dsa {
 namespace {
 
-constexpr int kCsrRows = 16;     // query rows per counting workgroup
+constexpr int kCsrRowsMin = 16;   // query rows per counting workgroup: at least
+constexpr int kCsrRowsMax = 512;  // and at most
+constexpr int kCsrRowBatch = 8;   // index rows loaded together
 constexpr int kLdsKeys = 16384;  // keys privatised in LDS
 
 __device__ __forceinline__ bool csr_slot_ok(int v, int s_kv, int64_t limit) {
   return v >= 0 && v < s_kv && (int64_t)v <= limit;
 }
 
-template <bool kFill>
-__global__ void __launch_bounds__(256)
-csr_count_kernel(const int32_t* __restrict__ idx, int* __restrict__ counts, int* __restrict__ cursor,
-                 int* __restrict__ pairs, int S, int s_kv, int K, int64_t q_offset, int row0, int rows, int b) {
-  extern __shared__ int hist[];
-  const bool priv = s_kv <= kLdsKeys;
-  const int r0 = blockIdx.x * kCsrRows;
-  const int r1 = min(rows, r0 + kCsrRows);
-  if (priv) {
-    for (int j = threadIdx.x; j < s_kv; j += 256) hist[j] = 0;
-    __syncthreads();
-  }
-  for (int lr = r0; lr < r1; ++lr) {
-    const int tok = row0 + lr;
-    const int32_t* ridx = idx + ((int64_t)b * S + tok) * K;
-    const int64_t limit = tok + q_offset;
-    for (int j = threadIdx.x; j < K; j += 256) {
-      const int v = ridx[j];
-      if (!csr_slot_ok(v, s_kv, limit)) continue;
-      if (!kFill) {
-        if (priv) atomicAdd(&hist[v], 1);
-        else atomicAdd(&counts[v], 1);
-      } else if (!priv) {
-        const int pos = atomicAdd(&cursor[v], 1);
-        pairs[pos] = lr * K + j;
-      } else {
-        atomicAdd(&hist[v], 1);
+// Calls f(key - key0, pair) for every valid slot of query rows [r0, r1) whose key lies in
+// [key0, key0 + nkeys); the index rows of kCsrRowBatch rows are loaded before any is used.
+template <bool kVec, typename F>
+__device__ __forceinline__ void csr_for_pairs(const int32_t* __restrict__ idx, int S, int s_kv, int K, int64_t q_offset,
+                                              int row0, int r0, int r1, int b, int key0, int nkeys, F&& f) {
+  constexpr int kPer = kVec ? 2 : 8;  // loads per row and chunk (int4 or int)
+  constexpr int kW = kVec ? 4 : 1;
+  const int t = threadIdx.x;
+  for (int lr0 = r0; lr0 < r1; lr0 += kCsrRowBatch) {
+    for (int j0 = 0; j0 < K; j0 += 256 * kPer * kW) {
+      int v[kCsrRowBatch][kPer][kW];
+#pragma unroll
+      for (int a = 0; a < kCsrRowBatch; ++a) {
+        const int lr = min(lr0 + a, r1 - 1);
+        const int32_t* ridx = idx + ((int64_t)b * S + row0 + lr) * K;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int j = j0 + kW * (t + 256 * u);
+          if constexpr (kVec) {
+            const int4 w = *reinterpret_cast<const int4*>(ridx + min(j, K - 4));
+            v[a][u][0] = w.x, v[a][u][1] = w.y, v[a][u][2] = w.z, v[a][u][3] = w.w;
+          } else {
+            v[a][u][0] = ridx[min(j, K - 1)];
+          }
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < kCsrRowBatch; ++a) {
+        const int lr = lr0 + a;
+        if (lr >= r1) break;
+        const int64_t limit = (int64_t)(row0 + lr) + q_offset;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u)
+#pragma unroll
+          for (int e = 0; e < kW; ++e) {
+            const int j = j0 + kW * (t + 256 * u) + e;
+            const int key = v[a][u][e];
+            if (j < K && csr_slot_ok(key, s_kv, limit) && (unsigned)(key - key0) < (unsigned)nkeys)
+              f(key - key0, lr * K + j);
+          }
       }
     }
   }
-  if (!priv) return;
+}
+
+template <bool kFill, bool kVec>
+__global__ void __launch_bounds__(256)
+csr_count_kernel(const int32_t* __restrict__ idx, int* __restrict__ counts, int* __restrict__ cursor,
+                 int* __restrict__ pairs, int S, int s_kv, int K, int64_t q_offset, int row0, int rows, int b,
+                 int n_ranges, int rows_per_wg) {
+  extern __shared__ int hist[];
+  const int rb = blockIdx.x / n_ranges, kr = blockIdx.x - rb * n_ranges;
+  const int key0 = kr * kLdsKeys, nkeys = min(kLdsKeys, s_kv - key0);
+  const int r0 = rb * rows_per_wg;
+  const int r1 = min(rows, r0 + rows_per_wg);
+  for (int j = threadIdx.x; j < nkeys; j += 256) hist[j] = 0;
+  __syncthreads();
+  csr_for_pairs<kVec>(idx, S, s_kv, K, q_offset, row0, r0, r1, b, key0, nkeys,
+                      [&](int u, int) { atomicAdd(&hist[u], 1); });
   __syncthreads();
   if (!kFill) {
-    for (int j = threadIdx.x; j < s_kv; j += 256)
-      if (hist[j]) atomicAdd(&counts[j], hist[j]);
+    for (int j = threadIdx.x; j < nkeys; j += 256)
+      if (hist[j]) atomicAdd(&counts[key0 + j], hist[j]);
     return;
   }
   // fill: reserve this workgroup's range per key, then place pairs
-  for (int j = threadIdx.x; j < s_kv; j += 256) {
+  for (int j = threadIdx.x; j < nkeys; j += 256) {
     const int c = hist[j];
-    hist[j] = c ? atomicAdd(&cursor[j], c) : 0;
+    hist[j] = c ? atomicAdd(&cursor[key0 + j], c) : 0;
   }
   __syncthreads();
-  for (int lr = r0; lr < r1; ++lr) {
-    const int tok = row0 + lr;
-    const int32_t* ridx = idx + ((int64_t)b * S + tok) * K;
-    const int64_t limit = tok + q_offset;
-    for (int j = threadIdx.x; j < K; j += 256) {
-      const int v = ridx[j];
-      if (!csr_slot_ok(v, s_kv, limit)) continue;
-      const int pos = atomicAdd(&hist[v], 1);
-      pairs[pos] = lr * K + j;
-    }
-  }
+  csr_for_pairs<kVec>(idx, S, s_kv, K, q_offset, row0, r0, r1, b, key0, nkeys,
+                      [&](int u, int pair) { pairs[atomicAdd(&hist[u], 1)] = pair; });
+}
+
+template <bool kFill>
+void launch_csr_count(bool vec, unsigned grid, size_t lds, hipStream_t st, const int32_t* idx, int* counts,
+                      int* cursor, int* pairs, int S, int s_kv, int K, int64_t q_offset, int row0, int rows, int b,
+                      int n_ranges, int rows_per_wg) {
+  if (vec)
+    csr_count_kernel<kFill, true><<<grid, 256, lds, st>>>(idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
+                                                          rows, b, n_ranges, rows_per_wg);
+  else
+    csr_count_kernel<kFill, false><<<grid, 256, lds, st>>>(idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
+                                                           rows, b, n_ranges, rows_per_wg);
 }
 
 __global__ void zero_i32_kernel(int* __restrict__ p, int n) {
@@ -82,34 +119,34 @@ __global__ void zero_i32_kernel(int* __restrict__ p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// exclusive scan of counts -> row_ptr (s_kv + 1 entries) and cursor = row_ptr; one workgroup
+// exclusive scan of counts -> row_ptr (s_kv + 1 entries) and cursor = row_ptr; one
+// workgroup: thread t sums its contiguous segment of ceil(s_kv / 1024) counts, the 1024
+// segment sums are scanned (wave scans + one pass over the 16 wave totals), and each
+// thread writes its segment's prefixes
 __global__ void __launch_bounds__(1024) csr_scan_kernel(const int* __restrict__ counts, int* __restrict__ row_ptr,
                                                         int* __restrict__ cursor, int s_kv) {
-  __shared__ int buf[1024];
-  __shared__ int carry;
-  if (threadIdx.x == 0) carry = 0;
-  __syncthreads();
-  for (int base = 0; base < s_kv; base += 1024) {
-    const int j = base + threadIdx.x;
-    const int v = j < s_kv ? counts[j] : 0;
-    buf[threadIdx.x] = v;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int add = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
-      __syncthreads();
-      buf[threadIdx.x] += add;
-      __syncthreads();
-    }
-    const int excl = carry + buf[threadIdx.x] - v;
-    if (j < s_kv) {
-      row_ptr[j] = excl;
-      cursor[j] = excl;
-    }
-    __syncthreads();
-    if (threadIdx.x == 1023) carry += buf[1023];
-    __syncthreads();
+  __shared__ int wsum[16];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int seg = (s_kv + 1023) / 1024;
+  const int j0 = min(s_kv, t * seg), j1 = min(s_kv, j0 + seg);
+  int sum = 0;
+  for (int j = j0; j < j1; ++j) sum += counts[j];
+  int incl = sum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += u;
   }
-  if (threadIdx.x == 0) row_ptr[s_kv] = carry;
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  int run = incl - sum;
+  for (int w = 0; w < wave; ++w) run += wsum[w];
+  for (int j = j0; j < j1; ++j) {
+    row_ptr[j] = run;
+    cursor[j] = run;
+    run += counts[j];
+  }
+  if (t == 1023) row_ptr[s_kv] = run;  // the last thread's segment ends at s_kv (or is empty)
 }
 
 // acc[key] += sum over the key's pairs of bf16 contribution rows of kChunks 16-byte chunks.
@@ -248,18 +285,26 @@ inline int64_t csr_ws_bytes(int64_t s_kv, int64_t rows, int64_t K) {
 // csr_ws holds csr_ws_bytes(s_kv, rows, K) bytes.
 inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, int* pairs, int* csr_ws, int S,
                       int s_kv, int K, int64_t q_offset, int row0, int rows, int b, int row_chunks, hipStream_t st) {
+  if (s_kv <= 0 || rows <= 0) return DSA_OK;  // no pairs: the accumulator keeps its contents
   int* counts = csr_ws;
   int* row_ptr = counts + (s_kv + 1);
   int* cursor = row_ptr + (s_kv + 1);
   int* seg_key = cursor + (s_kv + 1);
-  const size_t hist_bytes = s_kv <= kLdsKeys ? (size_t)s_kv * 4 : 0;
+  const int n_ranges = (int)ceil_div(s_kv, kLdsKeys);
+  const size_t hist_bytes = (size_t)(s_kv < kLdsKeys ? s_kv : kLdsKeys) * 4;
+  // about four pairs per key of a range per workgroup
+  const int64_t want = 4 * (int64_t)s_kv / (K > 0 ? K : 1);
+  const int rows_per_wg = (int)(want < kCsrRowsMin ? kCsrRowsMin : want > kCsrRowsMax ? kCsrRowsMax : want);
   zero_i32_kernel<<<ceil_div(s_kv + 1, 256), 256, 0, st>>>(counts, s_kv + 1);
-  const unsigned cgrid = ceil_div(rows, kCsrRows);
-  csr_count_kernel<false><<<cgrid, 256, hist_bytes, st>>>(idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
-                                                          rows, b);
+  const int64_t cgrid = ceil_div(rows, rows_per_wg) * (int64_t)n_ranges;
+  if (cgrid > 2147483647LL) return set_error(DSA_ERR_INVALID_ARG, "csr_reduce: too many rows x keys");
+  const int64_t row_base = (int64_t)b * S + row0;  // int4 loads need 16-byte aligned index rows
+  const bool vec = K % 4 == 0 && ((uintptr_t)(idx + row_base * K) % 16) == 0;
+  launch_csr_count<false>(vec, (unsigned)cgrid, hist_bytes, st, idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
+                          rows, b, n_ranges, rows_per_wg);
   csr_scan_kernel<<<1, 1024, 0, st>>>(counts, row_ptr, cursor, s_kv);
-  csr_count_kernel<true><<<cgrid, 256, hist_bytes, st>>>(idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0, rows,
-                                                         b);
+  launch_csr_count<true>(vec, (unsigned)cgrid, hist_bytes, st, idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
+                         rows, b, n_ranges, rows_per_wg);
   csr_seg_key_kernel<<<ceil_div(s_kv, 256), 256, 0, st>>>(row_ptr, seg_key, s_kv);
   const unsigned rgrid = ceil_div(ceil_div((int64_t)rows * K, kSegPairs), 4);
   if (row_chunks == 72)
