@@ -5,10 +5,12 @@
 // the backward reduces dKV through a key-major pass instead:
 //
 //   (alpha) bwd_dq_kernel, workgroup = (token, 64-head group), 4 waves x 16 heads:
-//           recompute S^T = K Q^T and dP^T = V dO^T on v_mfma_f32_16x16x32_bf16 over the
-//           gathered KV tile, P = exp2(S*scale*log2e - lse2), dS = P (dP - delta);
-//           dQ^T += K^T dS^T (K read transposed with ds_read_tr16_b64) in AGPRs; and
-//           G[token][slot][128 hg + (0..63 | 64..127)] = (dS * scale | P) in bf16.
+//           recompute [S ; dP] = [Q ; dO] K^T for the wave's 16 heads as ONE 32-row
+//           v_mfma_f32_32x32x16_bf16 chain over the gathered KV tile (rows 0..15 the
+//           heads' Q, rows 16..31 their dO; v = k_nope, so the first 512 columns serve both),
+//           P = exp2(S*scale*log2e - lse2), dS = P (dP - delta); G[token][slot][128 hg +
+//           (0..63 | 64..127)] = (dS * scale | P) in bf16 staged in LDS; dQ^T += K^T dS^T
+//           (K read transposed with ds_read_tr16_b64, dS^T from the G stage) in AGPRs.
 //   (beta)  bwd_contrib_kernel, workgroup = token, 12 waves (X slice in VGPRs, G streamed):
 //           C[token][slot][0..576) = G[slot][0..256) . [Q_token ; dO_token]  (bf16 out),
 //           the dKV contribution of one (token, slot) pair summed over all 128 heads.
@@ -51,9 +53,12 @@ __device__ __forceinline__ u32x4 tr_pair(uint32_t a1, uint32_t a2) {
   return av;
 }
 
-// piece swizzle of the transposed G stage (64-byte rows): conflict-free for the lanes'
-// 8-byte writes (16 rows x 2 pieces per 32 lanes) and for the flush's transposed reads
-__device__ __forceinline__ int gt_swz(int r) { return (r >> 1) & 7; }
+// 8-byte piece swizzle of the slot-major G stage (256-byte rows, piece p of slot r at
+// p ^ gs_swz(r)): injective over the 32 slots, so the 32 lanes writing one piece column
+// hit 32 distinct bank pairs; bits 2..3 follow r & 3, so a transposed read of 4 slots x
+// 4 pieces (4-aligned) covers 16 distinct pieces; a 16-lane read of a whole row is a
+// permutation of the row.
+__device__ __forceinline__ int gs_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3) | (((r >> 4) & 1) << 4); }
 
 // --------------------------------------------------------------------------------------
 // (alpha) dQ and G
@@ -61,15 +66,16 @@ __device__ __forceinline__ int gt_swz(int r) { return (r >> 1) & 7; }
 __global__ void __launch_bounds__(256, 1)
 bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
               const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, const float* __restrict__ smax,
-              const float* __restrict__ ssum, uint16_t* __restrict__ dq, uint16_t* __restrict__ gbuf,
-              float* __restrict__ mbase, int64_t m_hg_stride, int64_t m_b_stride, int m_row_base, int S, int s_kv,
-              int H, int K, float scale, int64_t q_offset, int row0) {
+              const float* __restrict__ ssum, const float* __restrict__ dbuf, uint16_t* __restrict__ dq,
+              uint16_t* __restrict__ gbuf, float* __restrict__ mbase, int64_t m_hg_stride, int64_t m_b_stride,
+              int m_row_base, int S, int s_kv, int H, int K, float scale, int64_t q_offset, int row0) {
   using Gather = RowGather<4>;
   __shared__ u32x4 tile[3][kTileChunks];
-  // staged G of this head group, transposed: [block parity][dS heads 0..63 | P heads 0..63]
-  // [8-byte piece of 4 slots, at piece ^ gt_swz(row)]
-  __shared__ uint2 gst[2][2 * kHG][kBN / 4];
+  // staged G of this head group, slot-major: [block parity][slot][8-byte piece of 4 entries
+  // (dS heads 0..63 | P heads 0..63), at piece ^ gs_swz(slot)]
+  __shared__ __attribute__((aligned(16))) uint2 gst[2][kBN][2 * kHG / 4];
   __shared__ float pst[2][4][kBN];          // per-wave head sums of P (attention mass)
+  __shared__ float2 hstat[4][16];           // per wave and head: (delta, lse2)
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
   __shared__ int sh_last;
 
@@ -100,23 +106,32 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
 #pragma unroll
     for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);  // clamped to slot K-1
   }
-  // (unconditional loads, hrow points at head 0 for absent heads: a load under a branch
+  // A operand of [S ; dP] = [Q ; dO] K^T (32x32x16, k-step s = columns 16s .. 16s+15):
+  // lane (row an, k half ah) holds columns 16s + 8ah .. +8 of row an: Q of head
+  // 16 wave + an for an < 16, dO of head 16 wave + an - 16 otherwise (dO has no rope
+  // columns: zero for s >= 32).  delta = rowsum(dO o O) comes from the pre-pass.
+  // (unconditional loads, arow points at head 0 for absent heads: a load under a branch
   // would make the compiler wait for every load before the block count; absent heads are
   // zeroed after it)
-  u32x4 qb[kDqk / 32], db[kDv / 32], ov[kDv / 32];
+  const int an = lane & 31, ah = lane >> 5;
+  const bool a_is_q = an < 16;
+  const int a_head = hg * kHG + wave * 16 + (an & 15);
+  const bool a_ok = a_head < H;
+  const int64_t arow = row_id * H + (a_ok ? a_head : 0);
+  constexpr int kAS = kDqk / 16;  // 36 k-steps
+  constexpr int kAL = kDv / 16;   // 32 of them cover the latent columns
+  u32x4 aq[kAS];
   {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
-    const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
-    const u32x4* oh = reinterpret_cast<const u32x4*>(out + hrow * kDv);
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + arow * kDqk);
+    const u32x4* dh = reinterpret_cast<const u32x4*>(dout + arow * kDv);
+    const u32x4* src = a_is_q ? qh : dh;
 #pragma unroll
-    for (int c = 0; c < kDqk / 32; ++c) qb[c] = qh[4 * c + g];
+    for (int st = 0; st < kAL; ++st) aq[st] = src[2 * st + ah];
 #pragma unroll
-    for (int c = 0; c < kDv / 32; ++c) {
-      db[c] = dh[4 * c + g];
-      ov[c] = oh[4 * c + g];
-    }
+    for (int st = kAL; st < kAS; ++st) aq[st] = qh[2 * st + ah];
   }
-  const float mx = smax[hrow], sm = ssum[hrow];
+  const float mx = smax[arow], sm = ssum[arow];
+  const float dlt = dbuf[((int64_t)b * gridDim.x + blockIdx.x) * H + (a_ok ? a_head : 0)];
 
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (mrow)  // slots past the last usable block carry no mass
@@ -131,35 +146,35 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   }
   const uint32_t lim = gather_limit(limit, s_kv);
 
-  if (!head_ok) {
+  if (!a_ok) {
 #pragma unroll
-    for (int c = 0; c < kDqk / 32; ++c) qb[c] = (u32x4){0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int c = 0; c < kDv / 32; ++c) db[c] = ov[c] = (u32x4){0u, 0u, 0u, 0u};
+    for (int st = 0; st < kAS; ++st) aq[st] = (u32x4){0u, 0u, 0u, 0u};
   }
-  float delta, lse2;
+  if (!a_is_q) {
+#pragma unroll
+    for (int st = kAL; st < kAS; ++st) aq[st] = (u32x4){0u, 0u, 0u, 0u};
+  }
+  // delta and lse2 of head 16 wave + an (rows an < 16) go through LDS to the lanes that
+  // hold the head's S / dP values: lane (key an, ah) holds rows 8j + 4ah + i (j < 2: S,
+  // j >= 2: dP of the same head), i.e. heads hw(v) = 8 (v >> 2) + 4 ah + (v & 3), v < 8
+  float dl[8], l2[8];
   {
-    float part = 0.f;
+    const float lse2 = (a_ok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0
+    if (a_is_q && ah == 0) hstat[wave][an] = make_float2(a_ok ? dlt : 0.f, lse2);
 #pragma unroll
-    for (int c = 0; c < kDv / 32; ++c)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        part += bf16_lo(db[c][r]) * bf16_lo(ov[c][r]) + bf16_hi(db[c][r]) * bf16_hi(ov[c][r]);
-    delta = xor32_sum(xor16_sum(part));
-    lse2 = (head_ok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0 (absent head / no key)
+    for (int v = 0; v < 8; ++v) {
+      const float2 st2 = hstat[wave][8 * (v >> 2) + 4 * ah + (v & 3)];  // written by this wave
+      dl[v] = st2.x;
+      l2[v] = st2.y;
+    }
   }
   const float scale_log2 = scale * kLog2e;
 
-  // LDS offsets.  A operand of S^T / dP^T: key row 16kt + col, chunk 4c + g (XOR swz_kv(row)).
-  // With c = 2u + c0 the XOR touches only bits 0..2 of 4c + g -> ka_off[kt][c0] + 128 u.
-  uint32_t ka_off[2][2];
+  // LDS offsets.  B operand of [S ; dP] (key an, k half ah), k-step s: chunk (2s + ah) ^
+  // swz_kv(an); with s = 4u + s0 the XOR touches only bits 0..2 -> kb_off[s0] + 128 u.
+  uint32_t kb_off[4];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int c0 = 0; c0 < 2; ++c0) {
-      const int row = 16 * kt + col;
-      ka_off[kt][c0] = row * kRowBytes + 16 * ((4 * c0 + g) ^ swz_kv(row));
-    }
+  for (int s0 = 0; s0 < 4; ++s0) kb_off[s0] = an * kRowBytes + 16 * ((2 * s0 + ah) ^ swz_kv(an));
   // Transposed K reads for dQ^T += K^T dS^T: group g, source lane col supplies key row
   // 4g + col/4 (+16 for the second read), d columns 16dt + 4(col%4) -> chunk 2dt + (col%4)/2.
   const int tr_row = 4 * g + (col >> 2);
@@ -174,11 +189,9 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   for (int t = 0; t < kDqk / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // G and mass of block `fb` staged in gst/pst[fb & 1] -> global, in three parts so they
-  // can be spread over the next block's dQ MFMAs (fb < 0: nothing is stored).
-  // G: lane group (wave, G) takes head octet 4 wave + G of slots 16 u .. 16 u + 15 (part
-  // u); two transposed reads give lane c the octet's 8 values of slot 16 u + c (source
-  // lane c supplies row 8 octet + 4 x + c / 4, slots 16 u + 4 (c % 4) .. +3).  Part 2:
-  // the head group's attention mass of the block's 32 slots.
+  // can be spread over the next block's dQ MFMAs (fb < 0: nothing is stored).  G part u:
+  // slots 16u .. 16u+15, 16 lanes per slot row (16 bytes each, whole 256-byte rows).
+  // Part 2: the head group's attention mass of the block's 32 slots.
   auto flush_part = [&](int fb, int part) {
     const int sb = fb & 1;
     if (part == 2) {
@@ -186,36 +199,29 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
         mrow[fb * kBN + tid] = (pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid]);
       return;
     }
-    const int u = part;
-    const int c16 = lane & 15, oct = 4 * wave + (lane >> 4);
-    const lds_char* gb = lds_bytes(&gst[sb][0][0]);
-    const lds_char* a[2];
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      const int row = 8 * oct + 4 * x + (c16 >> 2);
-      const int piece = 4 * u + (c16 & 3);
-      a[x] = gb + row * (kBN * 2) + 8 * (piece ^ gt_swz(row));
-    }
-    const u32x4 v = lds_read_tr_pair(a[0], a[1]);
-    const int slot = fb * kBN + 16 * u + c16;
+    const int i = tid + 256 * part, row = i >> 4, k = i & 15;
+    const int p0 = (2 * k) ^ gs_swz(row);  // the pair (2k, 2k+1) stays one aligned 16-byte pair
+    u32x4 v = *reinterpret_cast<const u32x4*>(&gst[sb][row][p0 & ~1]);
+    if (p0 & 1) v = (u32x4){v[2], v[3], v[0], v[1]};
+    const int slot = fb * kBN + row;
     if (fb >= 0 && slot < K)  // the row holds K slots only
-      *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 2 * kHG * hg + 8 * oct) = v;
+      *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 2 * kHG * hg + 8 * k) = v;
   };
 
   // the per-head operands must have arrived before the first DMA: a later wait for them
   // would also wait for every row DMA in flight
 #pragma unroll
-  for (int c = 0; c < kDqk / 32; ++c) asm volatile("" : "+v"(qb[c]));
+  for (int st = 0; st < kAS; ++st) asm volatile("" : "+v"(aq[st]));
 #pragma unroll
-  for (int c = 0; c < kDv / 32; ++c) asm volatile("" : "+v"(db[c]));
-  asm volatile("" : "+v"(delta), "+v"(lse2));
+  for (int v = 0; v < 8; ++v) asm volatile("" : "+v"(dl[v]), "+v"(l2[v]));
 
   // ---- pipeline (as in the forward) ----
-  // iteration blk: S^T / dP^T of block blk on tile blk % 3 while block blk+1's rows are
+  // iteration blk: [S ; dP] of block blk on tile blk % 3 while block blk+1's rows are
   // DMA'd into tile (blk+1) % 3 (one instruction per S/dP batch), then P / dS of blk
-  // interleaved batch by batch with dQ of blk-1 on tile (blk-1) % 3 (its dS^T operand
-  // bds_prev was made one iteration earlier), G / mass staging of blk and the stores of
-  // blk-1's.  The iteration ends with its DMAs landed (vmcnt 0) and one barrier.
+  // interleaved batch by batch with dQ of blk-1 on tile (blk-1) % 3 (its dS^T operand read
+  // back from blk-1's G stage, which this wave wrote), G / mass staging of blk and the
+  // stores of blk-1's.  The iteration ends with its DMAs landed (vmcnt 0) and one barrier.
+  // Tile (blk-1) % 3 for blk = 0 is zeroed (dS^T = 0 there, and 0 * garbage could be NaN).
   constexpr int kPer = Gather::kMaxPerWave;
   const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
   if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
@@ -228,53 +234,48 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  constexpr int kSB = 2;                   // k-steps per S/dP batch
-  constexpr int kSN = (kDqk / 32) / kSB;   // 9 batches
+  constexpr int kSB = 4;                   // k-steps per S/dP batch
+  constexpr int kSN = kAS / kSB;           // 9 batches
   static_assert(kSN >= kPer, "one row DMA per S/dP batch");
   constexpr int kDB = 4;                   // dQ tiles per batch
   constexpr int kDN = (kDqk / 16) / kDB;   // 9 batches
-  u32x4 bds_prev = (u32x4){0u, 0u, 0u, 0u};
 
-  // S^T and dP^T of one block (four accumulation chains); block blk+1's DMA meanwhile
-  // (ring entry `ring`, slot value read a batch ahead); returns blk+1's validity bits.
-  // Past the last block the ring entry is stale and the rows land in a buffer nobody
+  // [S ; dP] of one block (one 32x32x16 accumulation chain, full rate); block blk+1's DMA
+  // meanwhile (ring entry `ring`, slot value read a batch ahead); returns blk+1's validity
+  // bits.  Past the last block the ring entry is stale and the rows land in a buffer nobody
   // reads: every offset stays inside the KV tensor.
-  auto sdp = [&](const lds_char* tb, u32x4* dst_tile, const int* ring, int rows_left, f32x4 (&sacc)[2],
-                 f32x4 (&pacc)[2]) -> uint32_t {
+  auto sdp = [&](const lds_char* tb, u32x4* dst_tile, const int* ring, int rows_left, f32x16& acc) -> uint32_t {
     const uint32_t vm_n = Gather::ring_valid(ring, lane, lim, rows_left);
     uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
+    acc = (f32x16){0.f};
+    u32x4 kb[2][kSB];
+    auto read_b = [&](u32x4 (&dst)[kSB], int sb) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) sacc[kt] = pacc[kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    u32x4 a[2][2][kSB];
-    auto read_a = [&](u32x4 (&dst)[2][kSB], int cb) {
-#pragma unroll
-      for (int u = 0; u < kSB; ++u)
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int c = cb + u;
-          dst[kt][u] = lds_read16(tb + ka_off[kt][c & 1] + 128 * (c >> 1));
-        }
+      for (int u = 0; u < kSB; ++u) dst[u] = lds_read16(tb + kb_off[u] + 128 * (sb / kSB));
     };
-    read_a(a[0], 0);
+    read_b(kb[0], 0);
     static_for<kSN>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
-      if constexpr (nb + 1 < kSN) read_a(a[(nb + 1) & 1], (nb + 1) * kSB);
+      if constexpr (nb + 1 < kSN) read_b(kb[(nb + 1) & 1], (nb + 1) * kSB);
       if constexpr (nb < kPer) {
         const uint32_t raw = raw_next;
         if constexpr (nb + 1 < kPer) raw_next = Gather::ring_slot(ring, nb + 1, gl);
         Gather::issue_slot(kvb, dst_tile, nb, wave, raw, gl, lim, rows_left);
       }
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < kSB; ++u) {
-        constexpr int c0 = nb * kSB;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          sacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(qb[c0 + u]), sacc[kt]);
-          if (c0 + u < kDv / 32)
-            pacc[kt] = mfma16x16x32(as_bf16x8(a[nb & 1][kt][u]), as_bf16x8(db[(c0 + u) % (kDv / 32)]), pacc[kt]);
-        }
-      }
+      for (int u = 0; u < kSB; ++u) acc = mfma32x32x16(as_bf16x8(aq[nb * kSB + u]), as_bf16x8(kb[nb & 1][u]), acc);
+      // one accumulation chain issues in order: spread the batch's LDS reads, address
+      // arithmetic and DMA between its MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
+      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);  // VALU / SALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x006, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // the row DMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_barrier(0);
     });
     return vm_n;
@@ -290,66 +291,61 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
     }
   };
 
-  // P / dS of block blk (sacc, pacc, validity vm) -> bds_new, G and mass staged for blk;
-  // interleaved with dQ of block blk-1 (tile vb, bds_prev) and the stores of blk-1
-  auto pds_dq = [&](const lds_char* vb, const f32x4 (&sacc)[2], const f32x4 (&pacc)[2], uint32_t vm, int blk,
-                    u32x4& bds_new) {
+  // dQ^T operand B = dS^T * scale of block fb from its G stage (the wave's own entries):
+  // lane (head col, g) takes slots 4g .. 4g+3 and 16 + 4g .. +3 (the k-slot order of the
+  // transposed K reads) by two transposed reads; source lane c supplies slot row
+  // 4g + c/4 (+16) and entries 16 wave + 4 (c % 4) .. +3
+  auto read_bds = [&](int fb) -> u32x4 {
+    const lds_char* gb = lds_bytes(&gst[fb & 1][0][0]);
+    const int q = 4 * wave + (col & 3);
+    const int r0 = 4 * g + (col >> 2), r1 = r0 + 16;
+    return lds_read_tr_pair(gb + r0 * (2 * kHG * 2) + 8 * (q ^ gs_swz(r0)),
+                            gb + r1 * (2 * kHG * 2) + 8 * (q ^ gs_swz(r1)));
+  };
+
+  // P / dS of block blk (acc, validity vm): G and mass staged for blk; interleaved with
+  // dQ of block blk-1 (tile vb, dS^T from blk-1's G stage; nothing for blk = 0) and the
+  // stores of blk-1
+  auto pds_dq = [&](const lds_char* vb, const f32x16& acc, uint32_t vm, int blk, const u32x4& bds,
+                    u32x4& bds_next) {
     u32x4 at[2][kDB];
     read_kt(vb, at[0], 0);
-    const uint32_t vmg = vm >> (4 * g);  // bit r: key 4g + r, bit 16 + r: key 16 + 4g + r
-    float pv[2][4], dsv[2][4];
-    float h4[4], h2[2], h1 = 0.f;
-    const bool u8 = col & 8, u4 = col & 4, u2 = col & 2;
+    const bool ok = (vm >> an) & 1u;
+    const int sb = blk & 1;
+    float pv[8], dsv[8];
+    // G stage: lane (slot an, ah) writes its 8 heads' values as two 8-byte pieces: heads
+    // 16 wave + 4 ah + (0..3) and 16 wave + 8 + 4 ah + (0..3); P entries follow the 64 dS
+    auto stage = [&](const float (&val)[8], int piece0, float mul) {
+      const int pa = piece0 + 4 * wave + ah, pb = pa + 2;
+      gst[sb][an][pa ^ gs_swz(an)] = make_uint2(pack_bf16x2(val[0] * mul, val[1] * mul),
+                                                pack_bf16x2(val[2] * mul, val[3] * mul));
+      gst[sb][an][pb ^ gs_swz(an)] = make_uint2(pack_bf16x2(val[4] * mul, val[5] * mul),
+                                                pack_bf16x2(val[6] * mul, val[7] * mul));
+    };
     static_for<kDN>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
       if constexpr (nb + 1 < kDN) read_kt(vb, at[(nb + 1) & 1], (nb + 1) * kDB);
 #pragma unroll
       for (int u = 0; u < kDB; ++u)
-        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds_prev), dqa[nb * kDB + u]);
-      if constexpr (nb == 0 || nb == 1) {  // P and dS of key tile kt (lane: head col, keys 16kt + 4g + r)
-        constexpr int kt = nb;
+        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds), dqa[nb * kDB + u]);
+      if constexpr (nb == 0) {  // P and dS: value v < 8 is S of head hw(v) at key an, v + 8 its dP
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool ok = (vmg >> (16 * kt + r)) & 1u;
-          const float p = ok ? __builtin_amdgcn_exp2f(sacc[kt][r] * scale_log2 - lse2) : 0.f;
-          pv[kt][r] = p;
-          dsv[kt][r] = p * (pacc[kt][r] - delta);
+        for (int v = 0; v < 8; ++v) {
+          const float p = ok ? __builtin_amdgcn_exp2f(acc[v] * scale_log2 - l2[v]) : 0.f;
+          pv[v] = p;
+          dsv[v] = p * (acc[v + 8] - dl[v]);
         }
+      } else if constexpr (nb == 1) {
+        stage(dsv, 0, scale);
       } else if constexpr (nb == 2) {
-        // dQ^T operand B = dS^T, k-slot 8g + t <-> key (t < 4 ? 4g + t : 16 + 4g + t - 4)
-        bds_new[0] = pack_bf16x2(dsv[0][0], dsv[0][1]);
-        bds_new[1] = pack_bf16x2(dsv[0][2], dsv[0][3]);
-        bds_new[2] = pack_bf16x2(dsv[1][0], dsv[1][1]);
-        bds_new[3] = pack_bf16x2(dsv[1][2], dsv[1][3]);
-        // stage G = (dS * scale | P) transposed: the lane's 4 consecutive slots
-        // 16 kt + 4 g .. +3 of its head are one 8-byte piece
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int hl = wave * 16 + col, piece = 4 * kt + g;
-          gst[blk & 1][hl][piece ^ gt_swz(hl)] = make_uint2(pack_bf16x2(dsv[kt][0] * scale, dsv[kt][1] * scale),
-                                                            pack_bf16x2(dsv[kt][2] * scale, dsv[kt][3] * scale));
-          gst[blk & 1][kHG + hl][piece ^ gt_swz(kHG + hl)] =
-              make_uint2(pack_bf16x2(pv[kt][0], pv[kt][1]), pack_bf16x2(pv[kt][2], pv[kt][3]));
-        }
-      } else if constexpr (nb == 3) {
-        // attention mass: sum P over this wave's 16 head lanes in three halving exchange
-        // steps (xor 8, 4, 2) that leave lane col with value j = (col >> 1) & 7
-        // (j = 4 kt + r); the xor-1 add completes it
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float lo = pv[0][j], hi = pv[1][j];  // values j and j + 4
-          h4[j] = (u8 ? hi : lo) + lane_xor<8>(u8 ? lo : hi);
-        }
+        stage(pv, kHG / 4, 1.f);
       } else if constexpr (nb == 4) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) h2[j] = (u4 ? h4[j + 2] : h4[j]) + lane_xor<4>(u4 ? h4[j] : h4[j + 2]);
-        h1 = (u2 ? h2[1] : h2[0]) + lane_xor<2>(u2 ? h2[0] : h2[1]);
-      } else if constexpr (nb == 5) {
-        const float tot = h1 + lane_xor<1>(h1);
-        if (mrow && (col & 1) == 0) {
-          const int j = (col >> 1) & 7;
-          pst[blk & 1][wave][16 * (j >> 2) + 4 * g + (j & 3)] = tot;
-        }
+        bds_next = read_bds(blk);  // written above by this wave; used by the next block's dQ
+      } else if constexpr (nb == 3) {
+        // attention mass: the lane's 8 heads, then the 8 of the lane 32 apart
+        const float part = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+        const float tot = xor32_sum(part);
+        if (mrow && ah == 0) pst[sb][wave][an] = tot;
       } else if constexpr (nb >= 6) {
         flush_part(blk - 1, nb - 6);  // G (two parts) and mass of the previous block
       }
@@ -358,7 +354,7 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   };
 
   // dQ of the last block
-  auto dq_only = [&](const lds_char* vb) {
+  auto dq_only = [&](const lds_char* vb, const u32x4& bds) {
     u32x4 at[2][kDB];
     read_kt(vb, at[0], 0);
     static_for<kDN>([&](auto nbc) {
@@ -367,39 +363,40 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < kDB; ++u)
-        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds_prev), dqa[nb * kDB + u]);
+        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds), dqa[nb * kDB + u]);
       __builtin_amdgcn_sched_barrier(0);
     });
   };
 
+  u32x4 bds_cur = (u32x4){0u, 0u, 0u, 0u};  // dS^T of block -1
   for (int blk = 0; blk < nblk; ++blk) {
     if (wave == 0 && blk + 3 < nblk)
       Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
-    f32x4 sacc[2], pacc[2];
+    f32x16 acc;
     // ring entry blk+1 landed during iteration blk-2 (or before the loop)
     const uint32_t vm_next = sdp(lds_bytes(&tile[blk % 3][0]), &tile[(blk + 1) % 3][0],
-                                 sidx[(blk + 1) & (GatherGeom::kRing - 1)], K - (blk + 1) * kBN, sacc, pacc);
-    u32x4 bds_new;
-    pds_dq(lds_bytes(&tile[(blk + 2) % 3][0]), sacc, pacc, vm_cur, blk, bds_new);
+                                 sidx[(blk + 1) & (GatherGeom::kRing - 1)], K - (blk + 1) * kBN, acc);
+    u32x4 bds_next;
+    pds_dq(lds_bytes(&tile[(blk + 2) % 3][0]), acc, vm_cur, blk, bds_cur, bds_next);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
     __syncthreads();
     vm_cur = vm_next;
-    bds_prev = bds_new;
+    bds_cur = bds_next;
   }
-  dq_only(lds_bytes(&tile[(nblk - 1) % 3][0]));
+  dq_only(lds_bytes(&tile[(nblk - 1) % 3][0]), bds_cur);
   // the last block's G and mass were staged before the loop's final barrier
   flush_part(nblk - 1, 0);
   flush_part(nblk - 1, 1);
   flush_part(nblk - 1, 2);
 
-  // ---- dQ epilogue: lane (head col, g) holds d = 16 dt + 4 g + r ----
+  // ---- dQ epilogue: lane (head col, g) holds d = 16 dt + 4 g + r (dS^T was pre-scaled) ----
   if (!head_ok) return;
   uint2* drow = reinterpret_cast<uint2*>(dq + hrow * kDqk);
 #pragma unroll
   for (int dt = 0; dt < kDqk / 16; ++dt) {
     uint2 w;
-    w.x = pack_bf16x2(dqa[dt][0] * scale, dqa[dt][1] * scale);
-    w.y = pack_bf16x2(dqa[dt][2] * scale, dqa[dt][3] * scale);
+    w.x = pack_bf16x2(dqa[dt][0], dqa[dt][1]);
+    w.y = pack_bf16x2(dqa[dt][2], dqa[dt][3]);
     drow[(16 * dt + 4 * g) / 4] = w;
   }
 }
@@ -647,9 +644,39 @@ bwd_exact_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, 
   }
 }
 
+// delta[b][lr][h] = sum_d dO[row, h, d] * O[row, h, d] (fp32) for the chunk's rows: one
+// 16-lane group per (row, head), 32 columns per lane (four 16-byte loads of each tensor)
+__global__ void __launch_bounds__(256)
+bwd_delta_kernel(const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, float* __restrict__ delta,
+                 int S, int H, int row0, int rows) {
+  const int64_t grp = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (b, lr, h) flattened
+  const int l = threadIdx.x & 15;
+  const int64_t n = (int64_t)gridDim.y * rows * H;  // gridDim.y = batch
+  const int64_t g = grp < n ? grp : n - 1;
+  const int64_t b = g / ((int64_t)rows * H), rem = g - b * rows * H;
+  const int64_t hr = (b * S + row0 + rem / H) * H + rem % H;
+  const u32x4* o4 = reinterpret_cast<const u32x4*>(out + hr * kDv);
+  const u32x4* d4 = reinterpret_cast<const u32x4*>(dout + hr * kDv);
+  u32x4 ov[4], dv[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    ov[c] = o4[l + 16 * c];
+    dv[c] = d4[l + 16 * c];
+  }
+  float part = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      part += bf16_lo(dv[c][r]) * bf16_lo(ov[c][r]) + bf16_hi(dv[c][r]) * bf16_hi(ov[c][r]);
+#pragma unroll
+  for (int m = 8; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
+  if (l == 0 && grp < n) delta[g] = part;
+}
+
 struct BwdPlan {
   int64_t rows;  // query rows per chunk
-  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, mass_bytes, total;
+  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, mass_bytes, delta_bytes, total;
 };
 
 // Scratch per chunk: G and C (bf16), the CSR pair list and offsets, and the per-head-group
@@ -657,7 +684,7 @@ struct BwdPlan {
 BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget) {
   BwdPlan p{};
   const int64_t mass_groups = kHeadsMax / kHG;
-  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4 + 4 * mass_groups);
+  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4 + 4 * mass_groups) + batch * kHeadsMax * 4;
   int64_t rows = s_q;
   if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
   p.rows = rows;
@@ -666,8 +693,10 @@ BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t
   p.pairs_bytes = rows * topk * 4;
   p.csr_bytes = csr_ws_bytes(s_kv, rows, topk);
   p.mass_bytes = mass_groups * batch * rows * topk * 4;
+  p.delta_bytes = batch * rows * kHeadsMax * 4;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + al(p.mass_bytes);
+  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + al(p.mass_bytes) +
+            al(p.delta_bytes);
   return p;
 }
 
@@ -744,6 +773,7 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
   int* pairs = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes));
   int* counts = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes));
   float* mpart = (float*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes) + al(plan.csr_bytes));
+  float* dbuf = (float*)((char*)mpart + al(plan.mass_bytes));
   const unsigned hgroups = ceil_div(n_heads, kHG);
 
   for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
@@ -762,9 +792,15 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
       m_hg = batch * rows * topk;
       m_b = (int64_t)rows * topk;
     }
+    {
+      const int64_t groups = batch * rows * n_heads;
+      bwd_delta_kernel<<<dim3((unsigned)((groups * 16 + 255) / 256), (unsigned)batch), 256, 0, st>>>(
+          (const uint16_t*)out, (const uint16_t*)dout, dbuf, (int)s_q, (int)n_heads, (int)r0, rows);
+      if (int rc = check_launch("dsa_sparse_mla_bwd(delta)")) return rc;
+    }
     bwd_dq_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)out,
-                                      (const uint16_t*)dout, softmax_max, softmax_sum, (uint16_t*)dq, gbuf, mb, m_hg,
-                                      m_b, m_row, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale, q_offset,
+                                      (const uint16_t*)dout, softmax_max, softmax_sum, dbuf, (uint16_t*)dq, gbuf, mb,
+                                      m_hg, m_b, m_row, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale, q_offset,
                                       (int)r0);
     if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
     if (mass && hgroups > 1) {
