@@ -120,33 +120,59 @@ __global__ void zero_i32_kernel(int* __restrict__ p, int n) {
 }
 
 // exclusive scan of counts -> row_ptr (s_kv + 1 entries) and cursor = row_ptr; one
-// workgroup: thread t sums its contiguous segment of ceil(s_kv / 1024) counts, the 1024
-// segment sums are scanned (wave scans + one pass over the 16 wave totals), and each
-// thread writes its segment's prefixes
+// workgroup over tiles of 1024 x 32 counts: thread t loads its 32 consecutive counts of
+// the tile at once (int4 loads), the 1024 segment sums are scanned (wave scans + the 16
+// wave totals), and each thread writes its segment's prefixes; a carry crosses tiles.
+constexpr int kScanPer = 32;
 __global__ void __launch_bounds__(1024) csr_scan_kernel(const int* __restrict__ counts, int* __restrict__ row_ptr,
                                                         int* __restrict__ cursor, int s_kv) {
   __shared__ int wsum[16];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int seg = (s_kv + 1023) / 1024;
-  const int j0 = min(s_kv, t * seg), j1 = min(s_kv, j0 + seg);
-  int sum = 0;
-  for (int j = j0; j < j1; ++j) sum += counts[j];
-  int incl = sum;
+  const bool vec = ((uintptr_t)counts % 16) == 0;
+  int carry = 0;
+  for (int base = 0; base < s_kv; base += 1024 * kScanPer) {
+    const int j0 = base + kScanPer * t;
+    int v[kScanPer];
+    if (vec && j0 + kScanPer <= s_kv) {
 #pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(incl, o, 64);
-    if (lane >= o) incl += u;
+      for (int u = 0; u < kScanPer / 4; ++u) {
+        const int4 w = *reinterpret_cast<const int4*>(counts + j0 + 4 * u);
+        v[4 * u] = w.x, v[4 * u + 1] = w.y, v[4 * u + 2] = w.z, v[4 * u + 3] = w.w;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kScanPer; ++u) v[u] = j0 + u < s_kv ? counts[j0 + u] : 0;
+    }
+    int sum = 0;
+#pragma unroll
+    for (int u = 0; u < kScanPer; ++u) sum += v[u];
+    int incl = sum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int run = carry + incl - sum;
+    int tile_total = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) {
+      if (w < wave) run += wsum[w];
+      tile_total += wsum[w];
+    }
+#pragma unroll
+    for (int u = 0; u < kScanPer; ++u) {
+      if (j0 + u < s_kv) {
+        row_ptr[j0 + u] = run;
+        cursor[j0 + u] = run;
+      }
+      run += v[u];
+    }
+    carry += tile_total;
+    __syncthreads();  // wsum is rewritten by the next tile
   }
-  if (lane == 63) wsum[wave] = incl;
-  __syncthreads();
-  int run = incl - sum;
-  for (int w = 0; w < wave; ++w) run += wsum[w];
-  for (int j = j0; j < j1; ++j) {
-    row_ptr[j] = run;
-    cursor[j] = run;
-    run += counts[j];
-  }
-  if (t == 1023) row_ptr[s_kv] = run;  // the last thread's segment ends at s_kv (or is empty)
+  if (t == 0) row_ptr[s_kv] = carry;
 }
 
 // acc[key] += sum over the key's pairs of bf16 contribution rows of kChunks 16-byte chunks.

@@ -4,19 +4,19 @@
 // whole 512-register file).  The token's selected latent-KV rows (576 bf16 = 1152 B each)
 // are gathered in blocks of 32 by DMA (global_load_lds) into a swizzled, triple-buffered
 // LDS tile shared by all heads, so each row crosses L2 once per token.  Wave w owns heads
-// 32w .. 32w+31 as two 16-head sub-groups over the whole contraction, on
-// v_mfma_f32_16x16x32_bf16, and every LDS operand it reads feeds both sub-groups:
-//   * QK: S^T[32 keys x 16 heads] per sub-group over 18 k-steps of 32 columns; latent Q
-//     of the wave's heads stays in 128 VGPRs for the whole token, rope Q in LDS; K rows
-//     are the A operand, read one batch ahead of their MFMAs;
+// 32w .. 32w+31 on v_mfma_f32_32x32x16_bf16 (one accumulation chain issues at full rate):
+//   * QK: S^T[32 keys x 32 heads] over 36 k-steps of 16 columns; latent Q of the wave's
+//     heads stays in 128 VGPRs for the whole token, rope Q in LDS; K rows are the A
+//     operand, read one batch ahead of their MFMAs;
 //   * softmax per head in the exp2 domain against a reference max fixed by the first
 //     valid block: no per-block O rescale (P may reach 2^64, well inside the fp32/bf16
 //     exponent range).  A row whose later logits outgrow that headroom is flagged with a
 //     negative softmax_sum and recomputed exactly by the fixup pass;
-//   * PV: O^T[512 dv x 16 heads] += V^T . P^T per sub-group, V read transposed by
+//   * PV: O^T[512 dv x 32 heads] += V^T . P^T in 16 dv tiles, V read transposed by
 //     ds_read_b64_tr_b16 straight from the row-major K tile (k_nope == v); the key order
-//     inside the k dimension is the S^T tile order (4g+r, 16+4g+r) on both operands.
-//     O (2 x 128 fp32 per lane) lives in the accumulation registers.
+//     inside the k dimension is the S^T accumulator order on both operands, so P is packed
+//     from the softmax registers directly.  O (256 fp32 per lane) lives in the
+//     accumulation registers.
 // LDS traffic per token and block is 4 waves x (QK + PV) tile reads; one barrier per
 // block, for the tile hand-off.
 #include "dsa_common.h"
