@@ -35,11 +35,12 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", choices=("c3", "c4", "c5", "c5-long"), default="c3",
+    p.add_argument("--workload", choices=("c3", "c4", "c5", "c5-long", "v4"), default="c3",
                    help="c3 (default, the headline): dense-KV step at S=8192; c4: compressed-KV step "
                         "(block compressor r=4, indexer and attention over S/4 compressed rows, S=32768); "
                         "c5: 8 packed sequences of U[1024,32768] tokens through the varlen entry points; "
-                        "c5-long: one 131072-token sequence")
+                        "c5-long: one 131072-token sequence; v4: DeepSeek-V4 shared-KV attention (128-token "
+                        "window + top-1024 of the S/4 compressed rows + per-head sink, 128 heads x 512) fwd+bwd")
     p.add_argument("--seq", type=int, default=None, help="query tokens (default: 8192, or 32768 for c4, "
                                                           "131072 for c5-long)")
     p.add_argument("--heads", type=int, default=128)
@@ -245,7 +246,50 @@ def c5_step(inp, ops, timer):
     return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss_rows)
 
 
-def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128, causal_pairs=None):
+def v4_inputs(S, H, topk, seed, device, ratio=4):
+    """DeepSeek-V4 attention layer inputs drawn on the device: query [1,S,H,512], window
+    rows ori_kv [1,S,512], compressed rows cmp_kv [1,S/r,512], indexer q_I [1,S,64,128],
+    compressed indexer keys [1,S/r,128], w [1,S,64], sinks [H] ~ N(0,1), dout."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    bf = dict(device=device, dtype=torch.bfloat16, generator=g)
+    n_c = S // ratio
+    return dict(q=torch.randn(1, S, H, 512, **bf), ori=torch.randn(1, S, 512, **bf),
+                cmp=torch.randn(1, n_c, 512, **bf), q_idx=torch.randn(1, S, 64, 128, **bf),
+                k_idx=torch.randn(1, n_c, 128, **bf),
+                w=torch.rand(1, S, 64, device=device, generator=g) * 64 ** -0.5 * 128 ** -0.5,
+                sinks=torch.randn(H, device=device, generator=g), dout=torch.randn(1, S, H, 512, **bf),
+                scale=512 ** -0.5, topk=topk, ratio=ratio, window=128)
+
+
+def v4_step(inp, ops, timer):
+    """One DeepSeek-V4 attention layer (SparseAttention with the NPU op's layout): fp8
+    indexer + top-k over the compressed rows (valid t < (s+1)//4), then the shared-KV
+    attention over the 128-token window and the selected compressed rows with the per-head
+    sink, forward and backward (gradients to query, both KV sets and the sinks)."""
+    import torch
+
+    S = inp["q"].shape[1]
+    with timer("quantize"):
+        q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
+        k8, ks = ops.quantize_fp8_per_row(inp["k_idx"])
+    with timer("indexer_topk"):
+        idx, _ = ops.npu_lightning_indexer(q8, k8, inp["w"], sparse_count=inp["topk"], sparse_mode=3,
+                                           cmp_ratio=inp["ratio"], query_scale=qs, key_scale=ks)
+        idx = idx[:, :, 0]
+        idx = torch.where(idx >= 0, idx + S, idx)  # rows of cat(ori_kv, cmp_kv)
+    leaves = [inp[k].detach().requires_grad_(True) for k in ("q", "ori", "cmp", "sinks")]
+    with timer("attn_fwd"):
+        out = ops.npu_sparse_attn_shared_kv(leaves[0], leaves[1], leaves[2], idx, leaves[3], inp["scale"],
+                                            inp["ratio"], ori_win_left=inp["window"] - 1)
+    with timer("attn_bwd"):
+        out.backward(inp["dout"])
+    return dict(idx=idx, out=out, dq=leaves[0].grad, d_ori=leaves[1].grad, d_cmp=leaves[2].grad,
+                dsink=leaves[3].grad)
+
+
+def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128, causal_pairs=None, sum_keff=None):
     """Algorithmic bytes and FLOPs of the DSA path per step.
 
     sum_keff = number of valid (row, slot) pairs; every head of a row shares its gathered
@@ -253,7 +297,8 @@ def algorithmic_work(S, H, topk, idx, d_qk=576, d_v=512, h_i=64, d_i=128, causal
     payload (4 bytes per element per pair).  ``causal_pairs`` = the (query, key) pairs the
     indexer scores (default: one causal sequence of S tokens).
     """
-    sum_keff = int((idx >= 0).sum().item())
+    if sum_keff is None:
+        sum_keff = int((idx >= 0).sum().item())
     if causal_pairs is None:
         causal_pairs = S * (S + 1) // 2
     K = topk
@@ -426,7 +471,7 @@ def main():
     dev = torch.device("cuda:0")
     wl = args.workload
     H, K = args.heads, args.topk
-    S = args.seq or {"c3": 8192, "c4": 32768, "c5": 0, "c5-long": 131072}[wl]
+    S = args.seq or {"c3": 8192, "c4": 32768, "c5": 0, "c5-long": 131072, "v4": 8192}[wl]
     if args.copy_calibration:
         copy_calibration(torch, dev)
     pairs = None
@@ -447,6 +492,13 @@ def main():
         pairs = sum((s + 1) // 4 for s in range(S))
         cfg = dict(workload="C4: compressed KV (r=4, overlap) compressor + indexer + attention fwd+bwd",
                    batch=1, seq_len=S, compressed_rows=S // 4, cmp_ratio=4)
+    elif wl == "v4":
+        inp = v4_inputs(S, H, K if args.topk != 2048 else 1024, args.seed, dev)
+        step = lambda t: v4_step(inp, ops, t)  # noqa: E731
+        pairs = sum((s + 1) // 4 for s in range(S))
+        K = inp["topk"]
+        cfg = dict(workload="DeepSeek-V4 shared-KV attention fwd+bwd (window 128 + compressed r=4 top-k + sink)",
+                   batch=1, seq_len=S, window=128, cmp_ratio=4, compressed_rows=S // 4)
     else:  # c5: packed varlen batch
         g = torch.Generator().manual_seed(args.seed)
         lens = torch.randint(1024, 32769, (8,), generator=g).tolist()
@@ -471,7 +523,14 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / args.steps
     phases = timer.averages_ms()
-    work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs)
+    if wl == "v4":
+        # slots per row: the window (min(128, s + 1) rows) plus the valid compressed picks;
+        # rows are 512 wide, padded to the 576-column kernels' layout
+        win = sum(min(128, s + 1) for s in range(S))
+        work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs)
+        work = algorithmic_work(S, H, K + 128, None, causal_pairs=pairs, sum_keff=work["sum_keff"] + win)
+    else:
+        work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs)
     del res
 
     # Dominant kernel: the gathered sparse MLA forward (sparse_mla_fwd_bf16_kernel; its

@@ -25,6 +25,11 @@
  *   dsa_quantize_fp8_rows        the fp8-e4m3 per-row quantisation this build adds in front of
  *                                npu_lightning_indexer (the reference indexes in bf16 and marks fp8
  *                                as a QAT step: models/deepseek_v4/model.py:646, :822)
+ *   dsa_attn_sink_fold +
+ *   dsa_attn_sink_grad           the per-head sink of SparseAttention.forward (models/deepseek_v4/
+ *                                model.py:573-623) inside npu_sparse_attn_shared_kv{,_grad}
+ *                                (converters/kernels/npu_smla.py:351-400;
+ *                                 ops/aclnn/sparse_attn_sharedkv/binding.cpp:30-88)
  *   dsa_compressor_fwd           Compressor._forward_bsnd pooling + RMSNorm
  *                                (models/deepseek_v4/model.py:183-221; torch-only in the reference)
  *   dsa_compressor_fwd_tnd       Compressor._forward_tnd (models/deepseek_v4/model.py:223-274)
@@ -181,6 +186,21 @@ int dsa_compressor_fwd(const float* kv, const float* score, const float* ape, co
  */
 int dsa_quantize_fp8_rows(const void* x, int in_dtype, uint8_t* q, float* scale, int64_t rows, int64_t d,
                           void* stream);
+
+/*
+ * Attention sink (DeepSeek-V4): a per-head logit with no value in every row's softmax.
+ * dsa_attn_sink_fold, after dsa_sparse_mla_fwd over the row's keys: with m, l the row's
+ * softmax_max / softmax_sum, m2 = max(m, sink[h]), a = l e^(m - m2), s2 = a + e^(sink - m2);
+ * out[row, h, :] *= a / s2 in place and (softmax_max, softmax_sum) <- (m2, s2), which is
+ * what dsa_sparse_mla_bwd then needs.  dsa_attn_sink_grad adds to dsink[h] (fp32, caller
+ * zeroes it) - sum over rows of e^(sink - m2) / s2 * sum_d dout * out.
+ *   out / dout [rows, n_heads, d_v] in dtype (bf16 or fp32), statistics [rows, n_heads].
+ */
+int dsa_attn_sink_fold(void* out, float* softmax_max, float* softmax_sum, const float* sinks, int dtype,
+                       int64_t rows, int64_t n_heads, int64_t d_v, void* stream);
+int dsa_attn_sink_grad(const void* out, const void* dout, const float* softmax_max, const float* softmax_sum,
+                       const float* sinks, float* dsink, int dtype, int64_t rows, int64_t n_heads, int64_t d_v,
+                       void* stream);
 
 /*
  * Block KV compressor over a packed varlen ("TND") batch (reference: Compressor._forward_tnd,

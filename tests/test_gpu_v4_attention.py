@@ -110,3 +110,34 @@ def test_v4_li_loss_gradients():
     assert rel_err(leaves[0].grad, rdq / n) <= 2e-2, rel_err(leaves[0].grad, rdq / n)
     assert rel_err(leaves[1].grad, rdk / n) <= 2e-2
     assert rel_err(leaves[2].grad, rdw / n) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,dv", [(torch.bfloat16, 512), (torch.float32, 512), (torch.bfloat16, 100)])
+def test_sink_fold_and_grad_kernels(dtype, dv):
+    """dsa_attn_sink_fold / dsa_attn_sink_grad against the same formulas in fp64: rows with
+    no key (max -inf, sum 0), sinks above and below the row max."""
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    g = torch.Generator().manual_seed(31)
+    B, S, H = 2, 37, 24
+    out = torch.randn(B, S, H, dv, generator=g).to(dtype)
+    dout = torch.randn(B, S, H, dv, generator=g).to(dtype)
+    smax = torch.randn(B, S, H, generator=g) * 3
+    ssum = torch.rand(B, S, H, generator=g) * 5 + 1
+    smax[0, 0] = float("-inf")
+    ssum[0, 0] = 0.0
+    sinks = torch.randn(H, generator=g) * 4
+    o, m2, s2 = ops.attn_sink_fold_(out.to(DEV), smax.to(DEV), ssum.to(DEV), sinks.to(DEV))
+    sk = sinks.double().view(1, 1, -1)
+    rm2 = torch.maximum(smax.double(), sk)
+    a = torch.where(ssum > 0, ssum.double() * torch.exp(smax.double() - rm2), torch.zeros_like(rm2))
+    rs2 = a + torch.exp(sk - rm2)
+    ro = out.double() * (a / rs2).unsqueeze(-1)
+    assert torch.allclose(m2.cpu().double(), rm2, rtol=1e-6)
+    assert torch.allclose(s2.cpu().double(), rs2, rtol=1e-5)
+    tol = 8e-3 if dtype == torch.bfloat16 else 1e-5
+    assert rel_err(o.cpu(), ro) <= tol
+    dsink = ops.attn_sink_grad(o, dout.to(DEV), m2, s2, sinks.to(DEV)).cpu()
+    delta = (dout.double() * o.cpu().double()).sum(-1)
+    ref = -(torch.exp(sk - rm2) / rs2 * delta).sum(dim=(0, 1))
+    assert rel_err(dsink, ref) <= 1e-5

@@ -647,6 +647,33 @@ def _sink_fold(smax, ssum, sinks):
     return m2, s2, a / s2
 
 
+def attn_sink_fold_(out, smax, ssum, sinks):
+    """In place (dsa_attn_sink_fold): out [.., H, d_v] *= a / s2 and (smax, ssum) <- (m2, s2)
+    with m2 = max(smax, sink), a = ssum e^(smax - m2), s2 = a + e^(sink - m2)."""
+    lib = load_library()
+    H, dv = out.shape[-2], out.shape[-1]
+    rows = out.numel() // (H * dv) if out.numel() else 0
+    if rows:
+        check(lib.dsa_attn_sink_fold(ptr(out), ptr(smax), ptr(ssum), ptr(sinks.float().contiguous()),
+                                     _lib.dtype_code(out.dtype), rows, H, dv, stream_of(out.device)),
+              "dsa_attn_sink_fold")
+    return out, smax, ssum
+
+
+def attn_sink_grad(out, dout, m2, s2, sinks):
+    """d sink [H] fp32 = - sum over rows of e^(sink - m2) / s2 * rowsum(dout * out)
+    (dsa_attn_sink_grad)."""
+    lib = load_library()
+    H, dv = out.shape[-2], out.shape[-1]
+    rows = out.numel() // (H * dv) if out.numel() else 0
+    dsink = torch.zeros(H, dtype=torch.float32, device=out.device)
+    if rows:
+        check(lib.dsa_attn_sink_grad(ptr(out), ptr(dout), ptr(m2), ptr(s2), ptr(sinks.float().contiguous()),
+                                     ptr(dsink), _lib.dtype_code(out.dtype), rows, H, dv, stream_of(out.device)),
+              "dsa_attn_sink_grad")
+    return dsink
+
+
 class _SparseAttnSharedKV(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query, ori_kv, cmp_kv, sinks, idx, scale):
@@ -661,8 +688,7 @@ class _SparseAttnSharedKV(torch.autograd.Function):
         q_ext = _pad_rows(query, dqk)
         kv_ext = _pad_rows(kv, dqk)
         out, smax, ssum = sparse_mla_fwd(q_ext, kv_ext, idx, scale, d_v=dv, q_offset=_NO_MASK_OFFSET)
-        m2, s2, factor = _sink_fold(smax, ssum, sinks)
-        out = (out.float() * factor.unsqueeze(-1)).to(query.dtype)
+        out, m2, s2 = attn_sink_fold_(out, smax, ssum, sinks)
         ctx.save_for_backward(q_ext, kv_ext, idx, out, m2, s2, sinks)
         ctx.scale = scale
         ctx.meta = (D, dv, ori_kv.shape[1], cmp_kv is not None)
@@ -676,10 +702,8 @@ class _SparseAttnSharedKV(torch.autograd.Function):
         # P_j = exp(x_j - lse) with lse = m2 + log s2 already includes the sink, and the
         # kernel's delta = rowsum(dO * O) uses the sink-scaled O: dQ and dKV are exact
         dq, dkv = sparse_mla_bwd(q_ext, kv_ext, idx, out, dout, m2, s2, ctx.scale, q_offset=_NO_MASK_OFFSET)
-        # the sink has no value: d sink = -sum over rows of p_sink * delta
-        delta = (dout.float() * out.float()).sum(-1)
-        p_sink = torch.exp(sinks.float().view(1, 1, -1) - m2) / s2
-        dsink = -(p_sink * delta).sum(dim=(0, 1))
+        # the sink has no value: d sink = -sum over rows of p_sink * rowsum(dO o O)
+        dsink = attn_sink_grad(out, dout, m2, s2, sinks)
         dq = dq[..., :D]
         dkv = dkv[..., :D].to(kv_ext.dtype)
         d_ori = dkv[:, :s_ori]
