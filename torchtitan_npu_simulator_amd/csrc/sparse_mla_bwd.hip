@@ -4,13 +4,15 @@
 // per clock), far too slow for the dKV scatter-add (576 fp32 per (token, key) pair), so
 // the backward reduces dKV through a key-major pass instead:
 //
-//   (alpha) bwd_dq_kernel, workgroup = (token, 64-head group), 4 waves x 16 heads:
-//           recompute [S ; dP] = [Q ; dO] K^T for the wave's 16 heads as ONE 32-row
-//           v_mfma_f32_32x32x16_bf16 chain over the gathered KV tile (rows 0..15 the
-//           heads' Q, rows 16..31 their dO; v = k_nope, so the first 512 columns serve both),
-//           P = exp2(S*scale*log2e - lse2), dS = P (dP - delta); G[token][slot][128 hg +
-//           (0..63 | 64..127)] = (dS * scale | P) in bf16 staged in LDS; dQ^T += K^T dS^T
-//           (K read transposed with ds_read_tr16_b64, dS^T from the G stage) in AGPRs.
+//   (delta) bwd_delta_kernel: delta = rowsum(dO o O) per (token, head), one streaming pass.
+//   (alpha) bwd_sdp_kernel, workgroup = token x 128 heads, 4 waves x 32 heads (the
+//           forward's gather pipeline): S^T = K Q^T and dP^T = V dO^T as two
+//           v_mfma_f32_32x32x16_bf16 chains sharing every K operand read, P = exp2(S*scale*
+//           log2e - lse2), dS = P (dP - delta); G[token][slot][128 hg + (0..63 | 64..127)] =
+//           (dS * scale | P) in bf16 and the head-summed P (attention mass) per slot.
+//           bwd_dqk_kernel, workgroup = token x 128 heads, 8 waves: dQ^T += K^T dS^T with
+//           each wave owning d tiles for two 32-head groups (K read transposed, dS^T from
+//           the G rows staged in LDS).
 //   (beta)  bwd_contrib_kernel, workgroup = token, 12 waves (X slice in VGPRs, G streamed):
 //           C[token][slot][0..576) = G[slot][0..256) . [Q_token ; dO_token]  (bf16 out),
 //           the dKV contribution of one (token, slot) pair summed over all 128 heads.
@@ -35,198 +37,146 @@ constexpr int kBN = 32;
 constexpr int kTileChunks = kBN * kRowChunks;
 constexpr int kTileBytes = kTileChunks * 16;
 constexpr int kTileInstr = kTileChunks / 64;  // 36
-constexpr int kHG = 64;                       // heads per alpha workgroup
+constexpr int kHG = 64;                       // heads per G head group (one 128-entry half of a G row)
 constexpr int kGW = 256;                      // G row width: (dS | P) x 128 heads
 constexpr int kHeadsMax = 128;
 
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-__device__ __forceinline__ u32x4 tr_pair(uint32_t a1, uint32_t a2) {
-  const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a1));
-  const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(a2));
-  u32x4 av;
-  av[0] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
-  av[1] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
-  av[2] = (uint32_t)(uint16_t)v2[0] | ((uint32_t)(uint16_t)v2[1] << 16);
-  av[3] = (uint32_t)(uint16_t)v2[2] | ((uint32_t)(uint16_t)v2[3] << 16);
-  return av;
-}
 
-// 8-byte piece swizzle of the slot-major G stage (256-byte rows, piece p of slot r at
-// p ^ gs_swz(r)): injective over the 32 slots, so the 32 lanes writing one piece column
-// hit 32 distinct bank pairs; bits 2..3 follow r & 3, so a transposed read of 4 slots x
-// 4 pieces (4-aligned) covers 16 distinct pieces; a 16-lane read of a whole row is a
-// permutation of the row.
-__device__ __forceinline__ int gs_swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3) | (((r >> 4) & 1) << 4); }
 
 // --------------------------------------------------------------------------------------
-// (alpha) dQ and G
+// (alpha-1) bwd_sdp_kernel: G and the attention mass of a token, all heads in one workgroup
+//
+// The forward kernel's gather pipeline and layout, 4 waves x 32 heads: per 32-key block
+// S^T = K Q^T and dP^T = V dO^T as two v_mfma_f32_32x32x16_bf16 chains that share every K
+// operand read (v = k_nope: the first 32 k-steps serve both; latent Q and dO of the wave's
+// heads stay in VGPRs, rope Q in LDS).  Lane (head n, h) then holds keys 8j + 4h + i of its
+// head: P = exp2(S*scale*log2e - lse2), dS = P (dP - delta); G = (dS * scale | P) is staged
+// transposed in LDS (8-byte pieces of 4 slots, four per type and lane) and leaves as whole
+// 512-byte slot rows; the mass sums P over the 128 heads (butterfly over a wave's 32 head
+// lanes, then the 4 waves).  No dQ here: with no dQ accumulators the wave holds 32 heads,
+// so each K element read from LDS serves twice the heads of the one-kernel backward.
 // --------------------------------------------------------------------------------------
+// piece swizzle of the 256-entry transposed stage (64-byte rows): (r & 3, swz) injective
+// over 32 consecutive rows (the write of one piece by a wave's 32 head lanes), and 4
+// aligned rows x 4 pieces distinct (the flush's transposed reads)
+__device__ __forceinline__ int g2_swz(int r) { return (r >> 2) & 7; }
+
 __global__ void __launch_bounds__(256, 1)
-bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
-              const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, const float* __restrict__ smax,
-              const float* __restrict__ ssum, const float* __restrict__ dbuf, uint16_t* __restrict__ dq,
-              uint16_t* __restrict__ gbuf, float* __restrict__ mbase, int64_t m_hg_stride, int64_t m_b_stride,
-              int m_row_base, int S, int s_kv, int H, int K, float scale, int64_t q_offset, int row0) {
+bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
+               const uint16_t* __restrict__ dout, const float* __restrict__ smax, const float* __restrict__ ssum,
+               const float* __restrict__ dbuf, uint16_t* __restrict__ gbuf, float* __restrict__ mass, int S, int s_kv,
+               int H, int K, float scale, int64_t q_offset, int row0) {
   using Gather = RowGather<4>;
-  __shared__ u32x4 tile[3][kTileChunks];
-  // staged G of this head group, slot-major: [block parity][slot][8-byte piece of 4 entries
-  // (dS heads 0..63 | P heads 0..63), at piece ^ gs_swz(slot)]
-  __shared__ __attribute__((aligned(16))) uint2 gst[2][kBN][2 * kHG / 4];
-  __shared__ float pst[2][4][kBN];          // per-wave head sums of P (attention mass)
-  __shared__ float2 hstat[4][16];           // per wave and head: (delta, lse2)
+  constexpr int kPer = Gather::kMaxPerWave;
+  constexpr int kLat = kDv / 16;   // 32 latent k-steps
+  constexpr int kSteps = kDqk / 16;  // 36
+  __shared__ u32x4 tile[2][kTileChunks];
+  __shared__ u32x4 qpe[kHeadsMax][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
+  __shared__ uint2 gst[2][kGW][kBN / 4];  // [parity][G entry][piece of 4 slots ^ g2_swz(entry)]
+  __shared__ float pst[2][4][kBN];
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
   __shared__ int sh_last;
 
-  const int tok = row0 + blockIdx.x;  // row within the batch element
-  const int hg = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int col = lane & 15, g = lane >> 4;
-  const int head = hg * kHG + wave * 16 + col;
-  const bool head_ok = head < H;
+  const int lr = blockIdx.x, tok = row0 + lr, b = blockIdx.z, tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 31, h = lane >> 5;
+  const int hl = wave * 32 + n;  // head (the workgroup holds all heads)
+  const bool hok = hl < H;
   const int64_t row_id = (int64_t)b * S + tok;
+  const int64_t hrow = row_id * H + (hok ? hl : 0);
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
-  const int64_t hrow = row_id * H + (head_ok ? head : 0);
-  // G rows of this chunk: [local row][slot][kGW]
-  uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + blockIdx.x) * (int64_t)K * kGW;
+  uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)K * kGW;
+  float* mrow = mass ? mass + row_id * K : nullptr;
 
-  // head-summed P of this head group for the row (mass; the host adds the head groups)
-  float* mrow = mbase ? mbase + hg * m_hg_stride + b * m_b_stride + (int64_t)(m_row_base + blockIdx.x) * K : nullptr;
-
-  // ---- prologue: the row's slot indices (block count), the index ring entries of blocks
-  // 0..2 (wave 0, DMA), the per-head operands Q (B layout of S^T = K Q^T), dO (B layout
-  // of dP^T = V dO^T), O and the row statistics are all requested before any is waited
-  // for: the block count needs only the first loads, the operands land meanwhile ----
   int vidx[kIdxU];
   load_row_indices(ridx, K, vidx);
   if (wave == 0) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);  // clamped to slot K-1
+    for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);
   }
-  // A operand of [S ; dP] = [Q ; dO] K^T (32x32x16, k-step s = columns 16s .. 16s+15):
-  // lane (row an, k half ah) holds columns 16s + 8ah .. +8 of row an: Q of head
-  // 16 wave + an for an < 16, dO of head 16 wave + an - 16 otherwise (dO has no rope
-  // columns: zero for s >= 32).  delta = rowsum(dO o O) comes from the pre-pass.
-  // (unconditional loads, arow points at head 0 for absent heads: a load under a branch
-  // would make the compiler wait for every load before the block count; absent heads are
-  // zeroed after it)
-  const int an = lane & 31, ah = lane >> 5;
-  const bool a_is_q = an < 16;
-  const int a_head = hg * kHG + wave * 16 + (an & 15);
-  const bool a_ok = a_head < H;
-  const int64_t arow = row_id * H + (a_ok ? a_head : 0);
-  constexpr int kAS = kDqk / 16;  // 36 k-steps
-  constexpr int kAL = kDv / 16;   // 32 of them cover the latent columns
-  u32x4 aq[kAS];
+  // latent Q and dO of head hl: k-step s holds columns 16s + 8h .. +8 (B operands)
+  u32x4 qb[kLat], db[kLat], qr[4];
   {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + arow * kDqk);
-    const u32x4* dh = reinterpret_cast<const u32x4*>(dout + arow * kDv);
-    const u32x4* src = a_is_q ? qh : dh;
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
+    const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
 #pragma unroll
-    for (int st = 0; st < kAL; ++st) aq[st] = src[2 * st + ah];
+    for (int st = 0; st < kLat; ++st) qb[st] = qh[2 * st + h];
 #pragma unroll
-    for (int st = kAL; st < kAS; ++st) aq[st] = qh[2 * st + ah];
+    for (int st = 0; st < kLat; ++st) db[st] = dh[2 * st + h];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qr[j] = qh[64 + 4 * h + j];
   }
-  const float mx = smax[arow], sm = ssum[arow];
-  const float dlt = dbuf[((int64_t)b * gridDim.x + blockIdx.x) * H + (a_ok ? a_head : 0)];
-
+  const float mx = smax[hrow], sm = ssum[hrow];
+  const float dlt = dbuf[((int64_t)b * gridDim.x + lr) * H + (hok ? hl : 0)];
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (mrow)  // slots past the last usable block carry no mass
     for (int j = nblk * kBN + tid; j < K; j += 256) mrow[j] = 0.f;
-  if (nblk == 0) {  // no usable key: dQ = 0 (G rows are never read)
+  if (nblk == 0) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring DMA has landed before the LDS is released
-    if (head_ok) {
-      uint32_t* d32 = reinterpret_cast<uint32_t*>(dq + hrow * kDqk);
-      for (int i = g; i < kDqk / 2; i += 4) d32[i] = 0u;
-    }
     return;
   }
   const uint32_t lim = gather_limit(limit, s_kv);
-
-  if (!a_ok) {
+  if (!hok) {
 #pragma unroll
-    for (int st = 0; st < kAS; ++st) aq[st] = (u32x4){0u, 0u, 0u, 0u};
-  }
-  if (!a_is_q) {
+    for (int st = 0; st < kLat; ++st) qb[st] = db[st] = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int st = kAL; st < kAS; ++st) aq[st] = (u32x4){0u, 0u, 0u, 0u};
+    for (int j = 0; j < 4; ++j) qr[j] = (u32x4){0u, 0u, 0u, 0u};
   }
-  // delta and lse2 of head 16 wave + an (rows an < 16) go through LDS to the lanes that
-  // hold the head's S / dP values: lane (key an, ah) holds rows 8j + 4ah + i (j < 2: S,
-  // j >= 2: dP of the same head), i.e. heads hw(v) = 8 (v >> 2) + 4 ah + (v & 3), v < 8
-  float dl[8], l2[8];
-  {
-    const float lse2 = (a_ok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0
-    if (a_is_q && ah == 0) hstat[wave][an] = make_float2(a_ok ? dlt : 0.f, lse2);
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const float2 st2 = hstat[wave][8 * (v >> 2) + 4 * ah + (v & 3)];  // written by this wave
-      dl[v] = st2.x;
-      l2[v] = st2.y;
-    }
+  for (int j = 0; j < 4; ++j) {
+    const int ch = 4 * h + j;
+    qpe[hl][ch ^ ((hl >> 1) & 7)] = qr[j];
   }
+  const float lse2 = (hok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0
+  const float delta = hok ? dlt : 0.f;
   const float scale_log2 = scale * kLog2e;
-
-  // LDS offsets.  B operand of [S ; dP] (key an, k half ah), k-step s: chunk (2s + ah) ^
-  // swz_kv(an); with s = 4u + s0 the XOR touches only bits 0..2 -> kb_off[s0] + 128 u.
-  uint32_t kb_off[4];
 #pragma unroll
-  for (int s0 = 0; s0 < 4; ++s0) kb_off[s0] = an * kRowBytes + 16 * ((2 * s0 + ah) ^ swz_kv(an));
-  // Transposed K reads for dQ^T += K^T dS^T: group g, source lane col supplies key row
-  // 4g + col/4 (+16 for the second read), d columns 16dt + 4(col%4) -> chunk 2dt + (col%4)/2.
-  const int tr_row = 4 * g + (col >> 2);
-  const int tr_x = swz_kv(tr_row);
-  const int tr_c0 = (col & 3) >> 1;
-  uint32_t tr_off[4];  // dt = 4u + d0 -> chunk (8u + 2 d0 + tr_c0) ^ tr_x = 8u + ((2 d0 + tr_c0) ^ tr_x)
-#pragma unroll
-  for (int d0 = 0; d0 < 4; ++d0) tr_off[d0] = tr_row * kRowBytes + 16 * ((2 * d0 + tr_c0) ^ tr_x) + 8 * (col & 1);
+  for (int st = 0; st < kLat; ++st) asm volatile("" : "+v"(qb[st]), "+v"(db[st]));  // landed before any DMA
 
-  f32x4 dqa[kDqk / 16];
+  uint32_t ka_off[4];  // A operand (K row n, chunk (2s + h) ^ swz_kv(n)), s = 4u + s0 -> + 128 u
 #pragma unroll
-  for (int t = 0; t < kDqk / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRowBytes + 16 * ((2 * s0 + h) ^ swz_kv(n));
+  const lds_char* qpe_b = lds_bytes(&qpe[0][0]);
+  // G entries of head hl: dS at 128 (hl / 64) + hl % 64, P 64 entries later
+  const int e_ds = 128 * (hl >> 6) + (hl & 63), e_p = e_ds + 64;
 
-  // G and mass of block `fb` staged in gst/pst[fb & 1] -> global, in three parts so they
-  // can be spread over the next block's dQ MFMAs (fb < 0: nothing is stored).  G part u:
-  // slots 16u .. 16u+15, 16 lanes per slot row (16 bytes each, whole 256-byte rows).
-  // Part 2: the head group's attention mass of the block's 32 slots.
+  // G rows and mass of block fb from stage fb & 1 -> global, in three parts.  G part u:
+  // slots 16u .. 16u+15; lane group (wave, G) takes entry octets oct and oct + 16
+  // (oct = 4 wave + G); two transposed reads give lane c the octet's 8 values of slot
+  // 16u + c (source lane c supplies entry row 8 oct + 4x + c/4, slots 16u + 4(c % 4) ..+3).
   auto flush_part = [&](int fb, int part) {
     const int sb = fb & 1;
     if (part == 2) {
-      if (mrow && fb >= 0 && tid < kBN && fb * kBN + tid < K)
+      if (mrow && tid < kBN && fb * kBN + tid < K)
         mrow[fb * kBN + tid] = (pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid]);
       return;
     }
-    const int i = tid + 256 * part, row = i >> 4, k = i & 15;
-    const int p0 = (2 * k) ^ gs_swz(row);  // the pair (2k, 2k+1) stays one aligned 16-byte pair
-    u32x4 v = *reinterpret_cast<const u32x4*>(&gst[sb][row][p0 & ~1]);
-    if (p0 & 1) v = (u32x4){v[2], v[3], v[0], v[1]};
-    const int slot = fb * kBN + row;
-    if (fb >= 0 && slot < K)  // the row holds K slots only
-      *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 2 * kHG * hg + 8 * k) = v;
+    const int c16 = lane & 15;
+    const lds_char* gb = lds_bytes(&gst[sb][0][0]);
+    const int slot = fb * kBN + 16 * part + c16;
+#pragma unroll
+    for (int o2 = 0; o2 < 2; ++o2) {
+      const int oct = 4 * wave + (lane >> 4) + 16 * o2;
+      const lds_char* a[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int row = 8 * oct + 4 * x + (c16 >> 2);
+        const int piece = 4 * part + (c16 & 3);
+        a[x] = gb + row * (kBN * 2) + 8 * (piece ^ g2_swz(row));
+      }
+      const u32x4 v = lds_read_tr_pair(a[0], a[1]);
+      if (slot < K) *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 8 * oct) = v;
+    }
   };
 
-  // the per-head operands must have arrived before the first DMA: a later wait for them
-  // would also wait for every row DMA in flight
-#pragma unroll
-  for (int st = 0; st < kAS; ++st) asm volatile("" : "+v"(aq[st]));
-#pragma unroll
-  for (int v = 0; v < 8; ++v) asm volatile("" : "+v"(dl[v]), "+v"(l2[v]));
-
-  // ---- pipeline (as in the forward) ----
-  // iteration blk: [S ; dP] of block blk on tile blk % 3 while block blk+1's rows are
-  // DMA'd into tile (blk+1) % 3 (one instruction per S/dP batch), then P / dS of blk
-  // interleaved batch by batch with dQ of blk-1 on tile (blk-1) % 3 (its dS^T operand read
-  // back from blk-1's G stage, which this wave wrote), G / mass staging of blk and the
-  // stores of blk-1's.  The iteration ends with its DMAs landed (vmcnt 0) and one barrier.
-  // Tile (blk-1) % 3 for blk = 0 is zeroed (dS^T = 0 there, and 0 * garbage could be NaN).
-  constexpr int kPer = Gather::kMaxPerWave;
   const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
   if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
-  __syncthreads();
-  for (int i = tid; i < kTileChunks; i += 256) tile[2][i] = (u32x4){0u, 0u, 0u, 0u};  // dQ of "block -1"
+  __syncthreads();                                                  // publishes them and qpe
   uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
 #pragma unroll
   for (int i = 0; i < kPer; ++i)
@@ -234,170 +184,342 @@ bwd_dq_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, c
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  constexpr int kSB = 4;                   // k-steps per S/dP batch
-  constexpr int kSN = kAS / kSB;           // 9 batches
-  static_assert(kSN >= kPer, "one row DMA per S/dP batch");
-  constexpr int kDB = 4;                   // dQ tiles per batch
-  constexpr int kDN = (kDqk / 16) / kDB;   // 9 batches
+  constexpr int kQBatch = 4;
+  constexpr int kQB = kSteps / kQBatch;  // 9 batches
+  static_assert(kQB >= kPer, "one row DMA per batch");
 
-  // [S ; dP] of one block (one 32x32x16 accumulation chain, full rate); block blk+1's DMA
-  // meanwhile (ring entry `ring`, slot value read a batch ahead); returns blk+1's validity
-  // bits.  Past the last block the ring entry is stale and the rows land in a buffer nobody
-  // reads: every offset stays inside the KV tensor.
-  auto sdp = [&](const lds_char* tb, u32x4* dst_tile, const int* ring, int rows_left, f32x16& acc) -> uint32_t {
-    const uint32_t vm_n = Gather::ring_valid(ring, lane, lim, rows_left);
-    uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
-    acc = (f32x16){0.f};
-    u32x4 kb[2][kSB];
-    auto read_b = [&](u32x4 (&dst)[kSB], int sb) {
+  // P / dS / G staging / mass of block pb (its S^T, dP^T in sp, pp; validity vm), in pieces
+  // so they can be spread over the next block's MFMA batches:
+  //   0: P and dS (16 values),  1: stage dS,  2: stage P,  3: mass butterfly + partial
+  float pv[16], dv[16];
+  auto pds_piece = [&](int piece, const f32x16& sp, const f32x16& pp, uint32_t vm, int pb) {
+    const uint32_t vmh = vm >> (4 * h);  // bit 8j + i: key 8j + 4h + i
+    const int sb = pb & 1;
+    if (piece == 0) {
 #pragma unroll
-      for (int u = 0; u < kSB; ++u) dst[u] = lds_read16(tb + kb_off[u] + 128 * (sb / kSB));
+      for (int v = 0; v < 16; ++v) {
+        const bool ok = (vmh >> (8 * (v >> 2) + (v & 3))) & 1u;
+        const float p = ok ? __builtin_amdgcn_exp2f(sp[v] * scale_log2 - lse2) : 0.f;
+        pv[v] = p;
+        dv[v] = p * (pp[v] - delta) * scale;
+      }
+    } else if (piece == 1 || piece == 2) {
+      const float* src = piece == 1 ? dv : pv;
+      const int e = piece == 1 ? e_ds : e_p;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int pc = 2 * j + h;  // slots 8j + 4h .. +3
+        gst[sb][e][pc ^ g2_swz(e)] = make_uint2(pack_bf16x2(src[4 * j], src[4 * j + 1]),
+                                                pack_bf16x2(src[4 * j + 2], src[4 * j + 3]));
+      }
+    } else {
+      // mass: butterfly over the 32 head lanes (lane bits 4..1 halve the 16 values, bit 0
+      // completes the sum); lane l ends with value (l >> 1) & 15.  Step bit 4 exchanges
+      // rows of 16 lanes with one permlane16 swap; bits 3..0 use DPP.  The halves are
+      // chosen by bit masks (a select between two array elements would become an indexed
+      // read).
+      const bool odd = (lane >> 4) & 1;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {  // even rows keep value j, odd rows j + 8
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(pv[j]), __float_as_uint(pv[j + 8]), false, false);
+        const float even_sum = pv[j] + __uint_as_float(r[1]), odd_sum = pv[j + 8] + __uint_as_float(r[0]);
+        pv[j] = odd ? odd_sum : even_sum;
+      }
+      auto bstep = [&](auto mc, int nh) {
+        constexpr int m = decltype(mc)::value;
+        const uint32_t up = ((lane & m) != 0) ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int j = 0; j < nh; ++j) {
+          const uint32_t a = __float_as_uint(pv[j]), b = __float_as_uint(pv[j + nh]);
+          const float send = __uint_as_float((a & up) | (b & ~up));
+          const float keep = __uint_as_float((b & up) | (a & ~up));
+          pv[j] = keep + lane_xor<m>(send);
+        }
+      };
+      bstep(std::integral_constant<int, 8>{}, 4);
+      bstep(std::integral_constant<int, 4>{}, 2);
+      bstep(std::integral_constant<int, 2>{}, 1);
+      const float tot = pv[0] + lane_xor<1>(pv[0]);
+      if ((lane & 1) == 0) {
+        const int r = (lane >> 1) & 15;
+        pst[sb][wave][8 * (r >> 2) + 4 * h + (r & 3)] = tot;
+      }
+    }
+  };
+
+  // iteration blk: S^T / dP^T of block blk on tile blk & 1 while block blk+1's rows are
+  // DMA'd into the other tile, with P / dS / G / mass of block blk-1 and the G and mass
+  // stores of block blk-2 spread over its MFMA batches; the iteration ends with its DMAs
+  // landed and one barrier (which also publishes blk-1's stage for its flush).
+  f32x16 sprev = (f32x16){0.f}, pprev = (f32x16){0.f};
+  uint32_t vm_prev = 0u;
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (wave == 0 && blk + 3 < nblk)
+      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
+    const lds_char* tb = lds_bytes(&tile[blk & 1][0]);
+    u32x4* dst_tile = &tile[(blk + 1) & 1][0];
+    const int* ring = sidx[(blk + 1) & (GatherGeom::kRing - 1)];
+    const int rows_left = K - (blk + 1) * kBN;
+    const uint32_t vm_next = Gather::ring_valid(ring, lane, lim, rows_left);
+    uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
+    f32x16 sacc = (f32x16){0.f}, pacc = (f32x16){0.f};
+    u32x4 a[2][kQBatch], rope[kQBatch];
+    auto read_a = [&](u32x4 (&dst)[kQBatch], int sb) {
+#pragma unroll
+      for (int u = 0; u < kQBatch; ++u) dst[u] = lds_read16(tb + ka_off[u] + 128 * (sb / kQBatch));
     };
-    read_b(kb[0], 0);
-    static_for<kSN>([&](auto nbc) {
+    read_a(a[0], 0);
+    static_for<kQB>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
-      if constexpr (nb + 1 < kSN) read_b(kb[(nb + 1) & 1], (nb + 1) * kSB);
+      if constexpr (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
+      if constexpr ((nb + 1) * kQBatch == kLat) {
+#pragma unroll
+        for (int e = 0; e < kQBatch; ++e) rope[e] = lds_read16(qpe_b + hl * 128 + 16 * ((2 * e + h) ^ ((hl >> 1) & 7)));
+      }
       if constexpr (nb < kPer) {
         const uint32_t raw = raw_next;
         if constexpr (nb + 1 < kPer) raw_next = Gather::ring_slot(ring, nb + 1, gl);
         Gather::issue_slot(kvb, dst_tile, nb, wave, raw, gl, lim, rows_left);
       }
 #pragma unroll
-      for (int u = 0; u < kSB; ++u) acc = mfma32x32x16(as_bf16x8(aq[nb * kSB + u]), as_bf16x8(kb[nb & 1][u]), acc);
-      // one accumulation chain issues in order: spread the batch's LDS reads, address
-      // arithmetic and DMA between its MFMAs
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
-      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);  // VALU / SALU
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x006, 6, 0);
-      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // the row DMA
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    });
-    return vm_n;
-  };
-
-  // Transposed K reads for dQ^T += K^T dS^T (tile vb)
-  auto read_kt = [&](const lds_char* vb, u32x4 (&dst)[kDB], int db4) {
-#pragma unroll
-    for (int u = 0; u < kDB; ++u) {
-      const int dt = db4 + u;
-      const lds_char* a1 = vb + tr_off[dt & 3] + 128 * (dt >> 2);
-      dst[u] = lds_read_tr_pair(a1, a1 + 16 * kRowBytes);
-    }
-  };
-
-  // dQ^T operand B = dS^T * scale of block fb from its G stage (the wave's own entries):
-  // lane (head col, g) takes slots 4g .. 4g+3 and 16 + 4g .. +3 (the k-slot order of the
-  // transposed K reads) by two transposed reads; source lane c supplies slot row
-  // 4g + c/4 (+16) and entries 16 wave + 4 (c % 4) .. +3
-  auto read_bds = [&](int fb) -> u32x4 {
-    const lds_char* gb = lds_bytes(&gst[fb & 1][0][0]);
-    const int q = 4 * wave + (col & 3);
-    const int r0 = 4 * g + (col >> 2), r1 = r0 + 16;
-    return lds_read_tr_pair(gb + r0 * (2 * kHG * 2) + 8 * (q ^ gs_swz(r0)),
-                            gb + r1 * (2 * kHG * 2) + 8 * (q ^ gs_swz(r1)));
-  };
-
-  // P / dS of block blk (acc, validity vm): G and mass staged for blk; interleaved with
-  // dQ of block blk-1 (tile vb, dS^T from blk-1's G stage; nothing for blk = 0) and the
-  // stores of blk-1
-  auto pds_dq = [&](const lds_char* vb, const f32x16& acc, uint32_t vm, int blk, const u32x4& bds,
-                    u32x4& bds_next) {
-    u32x4 at[2][kDB];
-    read_kt(vb, at[0], 0);
-    const bool ok = (vm >> an) & 1u;
-    const int sb = blk & 1;
-    float pv[8], dsv[8];
-    // G stage: lane (slot an, ah) writes its 8 heads' values as two 8-byte pieces: heads
-    // 16 wave + 4 ah + (0..3) and 16 wave + 8 + 4 ah + (0..3); P entries follow the 64 dS
-    auto stage = [&](const float (&val)[8], int piece0, float mul) {
-      const int pa = piece0 + 4 * wave + ah, pb = pa + 2;
-      gst[sb][an][pa ^ gs_swz(an)] = make_uint2(pack_bf16x2(val[0] * mul, val[1] * mul),
-                                                pack_bf16x2(val[2] * mul, val[3] * mul));
-      gst[sb][an][pb ^ gs_swz(an)] = make_uint2(pack_bf16x2(val[4] * mul, val[5] * mul),
-                                                pack_bf16x2(val[6] * mul, val[7] * mul));
-    };
-    static_for<kDN>([&](auto nbc) {
-      constexpr int nb = decltype(nbc)::value;
-      if constexpr (nb + 1 < kDN) read_kt(vb, at[(nb + 1) & 1], (nb + 1) * kDB);
-#pragma unroll
-      for (int u = 0; u < kDB; ++u)
-        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds), dqa[nb * kDB + u]);
-      if constexpr (nb == 0) {  // P and dS: value v < 8 is S of head hw(v) at key an, v + 8 its dP
-#pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          const float p = ok ? __builtin_amdgcn_exp2f(acc[v] * scale_log2 - l2[v]) : 0.f;
-          pv[v] = p;
-          dsv[v] = p * (acc[v + 8] - dl[v]);
+      for (int u = 0; u < kQBatch; ++u) {
+        constexpr int s0 = nb * kQBatch;
+        if constexpr (s0 < kLat) {
+          sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(qb[s0 + u]), sacc);
+          pacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(db[s0 + u]), pacc);
+        } else {
+          sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(rope[u]), sacc);
         }
-      } else if constexpr (nb == 1) {
-        stage(dsv, 0, scale);
-      } else if constexpr (nb == 2) {
-        stage(pv, kHG / 4, 1.f);
-      } else if constexpr (nb == 4) {
-        bds_next = read_bds(blk);  // written above by this wave; used by the next block's dQ
-      } else if constexpr (nb == 3) {
-        // attention mass: the lane's 8 heads, then the 8 of the lane 32 apart
-        const float part = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-        const float tot = xor32_sum(part);
-        if (mrow && ah == 0) pst[sb][wave][an] = tot;
-      } else if constexpr (nb >= 6) {
-        flush_part(blk - 1, nb - 6);  // G (two parts) and mass of the previous block
       }
+      if constexpr (nb < 4) {
+        if (blk > 0) pds_piece(nb, sprev, pprev, vm_prev, blk - 1);
+      } else if constexpr (nb >= 5 && nb < 8) {
+        if (blk > 1) flush_part(blk - 2, nb - 5);
+      }
+      // one wave per SIMD issues in order: put the batch's VALU, LDS and memory work in the
+      // gaps between its MFMAs, not after them
+      static_for<(nb * kQBatch < kLat ? 2 * kQBatch : kQBatch)>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+        __builtin_amdgcn_sched_group_barrier(0x006, 6, 0);  // VALU / SALU
+        __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM (row DMA, G stores)
+      });
       __builtin_amdgcn_sched_barrier(0);
     });
-  };
-
-  // dQ of the last block
-  auto dq_only = [&](const lds_char* vb, const u32x4& bds) {
-    u32x4 at[2][kDB];
-    read_kt(vb, at[0], 0);
-    static_for<kDN>([&](auto nbc) {
-      constexpr int nb = decltype(nbc)::value;
-      if constexpr (nb + 1 < kDN) read_kt(vb, at[(nb + 1) & 1], (nb + 1) * kDB);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < kDB; ++u)
-        dqa[nb * kDB + u] = mfma16x16x32(as_bf16x8(at[nb & 1][u]), as_bf16x8(bds), dqa[nb * kDB + u]);
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  };
-
-  u32x4 bds_cur = (u32x4){0u, 0u, 0u, 0u};  // dS^T of block -1
-  for (int blk = 0; blk < nblk; ++blk) {
-    if (wave == 0 && blk + 3 < nblk)
-      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
-    f32x16 acc;
-    // ring entry blk+1 landed during iteration blk-2 (or before the loop)
-    const uint32_t vm_next = sdp(lds_bytes(&tile[blk % 3][0]), &tile[(blk + 1) % 3][0],
-                                 sidx[(blk + 1) & (GatherGeom::kRing - 1)], K - (blk + 1) * kBN, acc);
-    u32x4 bds_next;
-    pds_dq(lds_bytes(&tile[(blk + 2) % 3][0]), acc, vm_cur, blk, bds_cur, bds_next);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
     __syncthreads();
+    sprev = sacc;
+    pprev = pacc;
+    vm_prev = vm_cur;
     vm_cur = vm_next;
-    bds_cur = bds_next;
   }
-  dq_only(lds_bytes(&tile[(nblk - 1) % 3][0]), bds_cur);
-  // the last block's G and mass were staged before the loop's final barrier
+  // the last block's P / dS / G / mass, the stores of the one before, then its own stores
+#pragma unroll
+  for (int piece = 0; piece < 4; ++piece) pds_piece(piece, sprev, pprev, vm_prev, nblk - 1);
+  if (nblk > 1) {
+    flush_part(nblk - 2, 0);
+    flush_part(nblk - 2, 1);
+    flush_part(nblk - 2, 2);
+  }
+  __syncthreads();
   flush_part(nblk - 1, 0);
   flush_part(nblk - 1, 1);
   flush_part(nblk - 1, 2);
+}
 
-  // ---- dQ epilogue: lane (head col, g) holds d = 16 dt + 4 g + r (dS^T was pre-scaled) ----
-  if (!head_ok) return;
-  uint2* drow = reinterpret_cast<uint2*>(dq + hrow * kDqk);
+// --------------------------------------------------------------------------------------
+// (alpha-2) bwd_dqk_kernel: dQ = (dS * scale) K for a token, all heads in one workgroup
+//
+// The forward's P.V structure with P := the staged dS of bwd_sdp_kernel and V := the whole
+// 576-column K row: dQ^T[32 d x 32 heads] += K^T dS^T on v_mfma_f32_32x32x16_bf16.  Eight
+// waves (two per SIMD): wave w owns the d tiles w % 4, w % 4 + 4, .. (of 18) for the two
+// 32-head groups of half w / 4, so each K^T operand read from LDS feeds 4 MFMAs (2 head
+// groups x 2 key steps) and the tile is read twice per workgroup instead of once per head
+// group; dQ^T (up to 5 x 2 x 16 fp32 per lane) stays in the accumulation registers.  The dS columns of each slot's G row (two 128-byte pieces) are
+// DMA'd into a [slot][128 heads] tile (16-byte chunk c of slot r at c ^ 4 (r & 3)) and read
+// back transposed with the forward's V^T lane pattern, so both operands share the k order.
+// Keys that are not valid contribute 0.
+// --------------------------------------------------------------------------------------
+__device__ __forceinline__ int ds_swz(int r) { return 4 * (r & 3); }
+
+__global__ void __launch_bounds__(512, 1)
+bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf,
+               uint16_t* __restrict__ dq, int S, int s_kv, int H, int K, int64_t q_offset, int row0) {
+  using Gather = RowGather<8>;
+  constexpr int kPer = Gather::kMaxPerWave;  // 5 row instructions per wave and block
+  constexpr int kDT = kDqk / 32;             // 18 d tiles
+  constexpr int kOwn = (kDT + 3) / 4;        // d tiles per wave (5; tile owners 2, 3 own 4)
+  __shared__ u32x4 tile[2][kTileChunks];
+  __shared__ u32x4 dsl[2][kBN * 16];  // dS tile: [slot][16 chunks of 8 heads ^ ds_swz(slot)]
+  __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
+  __shared__ int sh_last;
+
+  const int lr = blockIdx.x, tok = row0 + lr, b = blockIdx.z, tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wt = wave & 3, hh2 = wave >> 2;  // d-tile owner, head half (groups 2 hh2, 2 hh2 + 1)
+  const int n = lane & 31, h = lane >> 5;
+  const int64_t row_id = (int64_t)b * S + tok;
+  const int32_t* ridx = idx + row_id * K;
+  const int64_t limit = tok + q_offset;
+  const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
+  const uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)K * kGW;
+
+  int vidx[kIdxU];
+  load_row_indices(ridx, K, vidx);
+  if (wave == 0) {
 #pragma unroll
-  for (int dt = 0; dt < kDqk / 16; ++dt) {
-    uint2 w;
-    w.x = pack_bf16x2(dqa[dt][0], dqa[dt][1]);
-    w.y = pack_bf16x2(dqa[dt][2], dqa[dt][3]);
-    drow[(16 * dt + 4 * g) / 4] = w;
+    for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);
+  }
+  const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
+  if (nblk == 0) {  // no usable key: dQ = 0
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (int i = tid; i < H * (kDqk / 2); i += 512)
+      reinterpret_cast<uint32_t*>(dq + row_id * H * kDqk)[i] = 0u;
+    return;
+  }
+  const uint32_t lim = gather_limit(limit, s_kv);
+
+  // K^T reads (A operand), as the forward's V^T reads: lane group G = lane / 16 covers d
+  // 16 (G & 1) .. +15 and k half h = G >> 1; source lane c supplies key row 16kk + 8x + 4h
+  // + c/4 and d columns 32dt + 16 (G & 1) + 4 (c % 4) .. +3; dt = 2u + d0 -> + 128 u.
+  // dS^T reads (B operand) of head group g4: the same rows of the dS tile, heads 32 g4 +
+  // 16 (G & 1) + 4 (c % 4) .. +3 (chunk 4 g4 + 2 (G & 1) + (c % 4) / 2); kk -> + 16 rows.
+  uint32_t tr_off[2][2], ds_off[2][2];
+  {
+    const int c = lane & 15, G = lane >> 4;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int r = 8 * x + 4 * h + (c >> 2);
+#pragma unroll
+      for (int d0 = 0; d0 < 2; ++d0) {
+        const int ch = 4 * d0 + 2 * (G & 1) + ((c & 3) >> 1);
+        tr_off[x][d0] = r * kRowBytes + 16 * (ch ^ swz_kv(r)) + 8 * (c & 1);
+      }
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const int dch = 4 * (2 * hh2 + gg) + 2 * (G & 1) + ((c & 3) >> 1);
+        ds_off[gg][x] = r * 256 + 16 * (dch ^ ds_swz(r)) + 8 * (c & 1);
+      }
+    }
+  }
+  // dS tile DMA of block blk: instruction J (wave J) covers slots 4J .. 4J+3, lane ->
+  // slot 4J + lane/16, stored chunk lane % 16 = source chunk (lane % 16) ^ ds_swz(slot);
+  // source chunk c < 8: dS entries 8c .. (head group 0), else 128 + 8 (c - 8) (group 1)
+  auto issue_ds = [&](int blk, int buf) {
+    {
+      const int J = wave;
+      const int r = 4 * J + (lane >> 4);
+      const int c = (lane & 15) ^ ds_swz(r);
+      const int eo = c < 8 ? 8 * c : 128 + 8 * (c - 8);
+      const int slot = min(blk * kBN + r, K - 1);
+      dma16_to_lds(grow, (uint32_t)(slot * kGW + eo) * 2u, (uint32_t)(uintptr_t)&dsl[buf][J * 64]);
+    }
+  };
+
+  f32x16 dqa[kOwn][2];
+#pragma unroll
+  for (int t = 0; t < kOwn; ++t)
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) dqa[t][gg] = (f32x16){0.f};
+
+  const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
+  if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
+  __syncthreads();
+  uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i)
+    Gather::issue_slot(kvb, &tile[0][0], i, wave, Gather::ring_slot(sidx[0], i, gl), gl, lim, K);
+  issue_ds(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    if (wave == 0 && blk + 3 < nblk)
+      Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
+    const int buf = blk & 1;
+    const lds_char* vb = lds_bytes(&tile[buf][0]);
+    const lds_char* db = lds_bytes(&dsl[buf][0]);
+    u32x4* dst_tile = &tile[buf ^ 1][0];
+    const int* ring = sidx[(blk + 1) & (GatherGeom::kRing - 1)];
+    const int rows_left = K - (blk + 1) * kBN;
+    const uint32_t vm_next = Gather::ring_valid(ring, lane, lim, rows_left);
+    if (blk + 1 < nblk) issue_ds(blk + 1, buf ^ 1);
+    auto read_kt = [&](u32x4 (&dst)[2], int dt) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const lds_char* base = vb + kk * 16 * kRowBytes + 128 * (dt >> 1);
+        dst[kk] = lds_read_tr_pair(base + tr_off[0][dt & 1], base + tr_off[1][dt & 1]);
+      }
+    };
+    u32x4 av[2][2];
+    read_kt(av[0], wt);
+    // dS^T operands of the wave's two head groups (masked to the block's valid keys)
+    const uint32_t vmh = vm_cur >> (4 * h);
+    u32x4 bs[2][2];
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        u32x4 v = lds_read_tr_pair(db + ds_off[gg][0] + kk * 16 * 256, db + ds_off[gg][1] + kk * 16 * 256);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {  // dword q4: keys 16kk + 8 (q4 / 2) + 4h + 2 (q4 % 2) + {0, 1}
+          const int k0 = 16 * kk + 8 * (q4 >> 1) + 2 * (q4 & 1);
+          const uint32_t lo = ((vmh >> k0) & 1u) ? 0x0000ffffu : 0u;
+          const uint32_t hi = ((vmh >> (k0 + 1)) & 1u) ? 0xffff0000u : 0u;
+          v[q4] &= lo | hi;
+        }
+        bs[gg][kk] = v;
+      }
+    uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
+    auto issue_rows = [&](auto tc) {  // one row instruction per tile
+      constexpr int nb = decltype(tc)::value;
+      if constexpr (nb < kPer) {
+        const uint32_t raw = raw_next;
+        if constexpr (nb + 1 < kPer) raw_next = Gather::ring_slot(ring, nb + 1, gl);
+        Gather::issue_slot(kvb, dst_tile, nb, wave, raw, gl, lim, rows_left);
+      }
+    };
+    static_for<kOwn>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      const int dt = wt + 4 * t;  // wave-uniform
+      if (dt < kDT) {
+        if (t + 1 < kOwn && dt + 4 < kDT) read_kt(av[(t + 1) & 1], dt + 4);
+        issue_rows(tc);  // block blk+1's rows
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+            dqa[t][gg] = mfma32x32x16(as_bf16x8(av[t & 1][kk]), as_bf16x8(bs[gg][kk]), dqa[t][gg]);
+      } else {  // (waves with four tiles) the remaining row instructions
+        issue_rows(tc);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 (rows, dS) and ring entry blk+3 landed
+    __syncthreads();
+    vm_cur = vm_next;
+  }
+
+  // ---- epilogue: tile t, group gg: lane holds d = 32 dt + 8 j + 4 h + i of head
+  // 32 (2 hh2 + gg) + n (dS was pre-scaled) ----
+#pragma unroll
+  for (int t = 0; t < kOwn; ++t) {
+    const int dt = wt + 4 * t;
+    if (dt >= kDT) break;
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const int hd = 32 * (2 * hh2 + gg) + n;
+      if (hd >= H) continue;
+      uint2* drow = reinterpret_cast<uint2*>(dq + (row_id * H + hd) * kDqk);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint2 w;
+        w.x = pack_bf16x2(dqa[t][gg][4 * j], dqa[t][gg][4 * j + 1]);
+        w.y = pack_bf16x2(dqa[t][gg][4 * j + 2], dqa[t][gg][4 * j + 3]);
+        drow[(32 * dt + 8 * j + 4 * h) / 4] = w;
+      }
+    }
   }
 }
 
@@ -648,10 +770,9 @@ bwd_exact_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, 
 // 16-lane group per (row, head), 32 columns per lane (four 16-byte loads of each tensor)
 __global__ void __launch_bounds__(256)
 bwd_delta_kernel(const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, float* __restrict__ delta,
-                 int S, int H, int row0, int rows) {
-  const int64_t grp = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (b, lr, h) flattened
+                 int64_t n, int S, int H, int row0, int rows) {
+  const int64_t grp = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (b, lr, h) flattened, n of them
   const int l = threadIdx.x & 15;
-  const int64_t n = (int64_t)gridDim.y * rows * H;  // gridDim.y = batch
   const int64_t g = grp < n ? grp : n - 1;
   const int64_t b = g / ((int64_t)rows * H), rem = g - b * rows * H;
   const int64_t hr = (b * S + row0 + rem / H) * H + rem % H;
@@ -676,15 +797,14 @@ bwd_delta_kernel(const uint16_t* __restrict__ out, const uint16_t* __restrict__ 
 
 struct BwdPlan {
   int64_t rows;  // query rows per chunk
-  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, mass_bytes, delta_bytes, total;
+  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, delta_bytes, total;
 };
 
-// Scratch per chunk: G and C (bf16), the CSR pair list and offsets, and the per-head-group
-// mass partials (fp32, summed into the caller's mass after each chunk).
+// Scratch per chunk: G and C (bf16), the CSR pair list and offsets, and delta (fp32 per
+// row and head).
 BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget) {
   BwdPlan p{};
-  const int64_t mass_groups = kHeadsMax / kHG;
-  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4 + 4 * mass_groups) + batch * kHeadsMax * 4;
+  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4) + batch * kHeadsMax * 4;
   int64_t rows = s_q;
   if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
   p.rows = rows;
@@ -692,26 +812,10 @@ BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t
   p.c_bytes = batch * rows * topk * kDqk * 2;
   p.pairs_bytes = rows * topk * 4;
   p.csr_bytes = csr_ws_bytes(s_kv, rows, topk);
-  p.mass_bytes = mass_groups * batch * rows * topk * 4;
   p.delta_bytes = batch * rows * kHeadsMax * 4;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + al(p.mass_bytes) +
-            al(p.delta_bytes);
+  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + al(p.delta_bytes);
   return p;
-}
-
-// mass[b, r0 + lr, :] = sum over head groups of the chunk's partials
-__global__ void __launch_bounds__(256)
-mass_combine_kernel(const float* __restrict__ part, float* __restrict__ mass, int groups, int64_t hg_stride,
-                    int64_t row_elems, int S, int r0, int rows, int K) {
-  const int64_t n = row_elems;  // batch * rows * K
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) {
-    float acc = part[i];
-    for (int hgi = 1; hgi < groups; ++hgi) acc += part[hgi * hg_stride + i];
-    const int64_t b = i / ((int64_t)rows * K);
-    const int64_t rem = i - b * (int64_t)rows * K;
-    mass[(b * S + r0) * (int64_t)K + rem] = acc;
-  }
 }
 
 constexpr int64_t kDefaultBudget = 32LL << 30;  // scratch for the G / C chunks (C3 in one chunk)
@@ -772,44 +876,25 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
   uint16_t* cbuf = (uint16_t*)(ws + al(plan.g_bytes));
   int* pairs = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes));
   int* counts = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes));
-  float* mpart = (float*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes) + al(plan.csr_bytes));
-  float* dbuf = (float*)((char*)mpart + al(plan.mass_bytes));
+  float* dbuf = (float*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes) + al(plan.csr_bytes));
   const unsigned hgroups = ceil_div(n_heads, kHG);
 
   for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
     const int rows = (int)std::min<int64_t>(plan.rows, s_q - r0);
-    dim3 ga((unsigned)rows, hgroups, (unsigned)batch);
-    // mass: one head group writes the caller's rows directly; several write partials
-    float* mb = nullptr;
-    int64_t m_hg = 0, m_b = 0;
-    int m_row = 0;
-    if (mass && hgroups == 1) {
-      mb = mass;
-      m_b = s_q * topk;
-      m_row = (int)r0;
-    } else if (mass) {
-      mb = mpart;
-      m_hg = batch * rows * topk;
-      m_b = (int64_t)rows * topk;
-    }
     {
       const int64_t groups = batch * rows * n_heads;
-      bwd_delta_kernel<<<dim3((unsigned)((groups * 16 + 255) / 256), (unsigned)batch), 256, 0, st>>>(
-          (const uint16_t*)out, (const uint16_t*)dout, dbuf, (int)s_q, (int)n_heads, (int)r0, rows);
+      bwd_delta_kernel<<<(unsigned)((groups * 16 + 255) / 256), 256, 0, st>>>(
+          (const uint16_t*)out, (const uint16_t*)dout, dbuf, groups, (int)s_q, (int)n_heads, (int)r0, rows);
       if (int rc = check_launch("dsa_sparse_mla_bwd(delta)")) return rc;
     }
-    bwd_dq_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)out,
-                                      (const uint16_t*)dout, softmax_max, softmax_sum, dbuf, (uint16_t*)dq, gbuf, mb,
-                                      m_hg, m_b, m_row, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale, q_offset,
-                                      (int)r0);
+    dim3 ga((unsigned)rows, 1, (unsigned)batch);
+    bwd_sdp_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout,
+                                       softmax_max, softmax_sum, dbuf, gbuf, mass, (int)s_q, (int)s_kv,
+                                       (int)n_heads, (int)topk, scale, q_offset, (int)r0);
+    if (int rc = check_launch("dsa_sparse_mla_bwd(sdp)")) return rc;
+    bwd_dqk_kernel<<<ga, 512, 0, st>>>((const uint16_t*)kv, indices, gbuf, (uint16_t*)dq, (int)s_q, (int)s_kv,
+                                       (int)n_heads, (int)topk, q_offset, (int)r0);
     if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
-    if (mass && hgroups > 1) {
-      const int64_t n = batch * rows * topk;
-      const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 65535);
-      mass_combine_kernel<<<blocks, 256, 0, st>>>(mpart, mass, (int)hgroups, m_hg, n, (int)s_q, (int)r0, rows,
-                                                  (int)topk);
-      if (int rc = check_launch("dsa_sparse_mla_bwd(mass)")) return rc;
-    }
     dim3 gb((unsigned)rows, (unsigned)batch);
     if (hgroups == 1)
       bwd_contrib_kernel<1><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf,
