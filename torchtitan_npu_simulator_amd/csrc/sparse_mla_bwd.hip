@@ -40,6 +40,9 @@ constexpr int kTileInstr = kTileChunks / 64;  // 36
 constexpr int kHG = 64;                       // heads per G head group (one 128-entry half of a G row)
 constexpr int kGW = 256;                      // G row width: (dS | P) x 128 heads
 constexpr int kHeadsMax = 128;
+// G rows hold the slots of whole 32-key blocks (K rounded up), so every block's G stores
+// are unconditional
+__host__ __device__ __forceinline__ int64_t g_slots(int64_t K) { return (K + kBN - 1) / kBN * kBN; }
 
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -90,7 +93,7 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
-  uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)K * kGW;
+  uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)g_slots(K) * kGW;
   float* mrow = mass ? mass + row_id * K : nullptr;
 
   int vidx[kIdxU];
@@ -170,7 +173,7 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
         a[x] = gb + row * (kBN * 2) + 8 * (piece ^ g2_swz(row));
       }
       const u32x4 v = lds_read_tr_pair(a[0], a[1]);
-      if (slot < K) *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 8 * oct) = v;
+      *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 8 * oct) = v;  // (rows padded to whole blocks)
     }
   };
 
@@ -293,8 +296,6 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
       }
       if constexpr (nb < 4) {
         if (blk > 0) pds_piece(nb, sprev, pprev, vm_prev, blk - 1);
-      } else if constexpr (nb >= 5 && nb < 8) {
-        if (blk > 1) flush_part(blk - 2, nb - 5);
       }
       // one wave per SIMD issues in order: put the batch's VALU, LDS and memory work in the
       // gaps between its MFMAs, not after them
@@ -307,7 +308,17 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
+    // block blk-2's G and mass stores go out after the block's last row DMA; at least four
+    // store instructions follow that DMA (two per G part, unconditional), so vmcnt(4) waits
+    // for every DMA (they retire in order) but not for the stores
+    if (blk > 1) {
+      flush_part(blk - 2, 0);
+      flush_part(blk - 2, 1);
+      flush_part(blk - 2, 2);
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __syncthreads();
     sprev = sacc;
     pprev = pacc;
@@ -363,7 +374,7 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
   const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
-  const uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)K * kGW;
+  const uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)g_slots(K) * kGW;
 
   int vidx[kIdxU];
   load_row_indices(ridx, K, vidx);
@@ -568,7 +579,7 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int nblk = count_row_blocks(ridx, K, s_kv, tok + q_offset, vidx, &sh_last);
   if (nblk == 0) return;
   const int nslots = min(K, nblk * kBN);
-  const uint16_t* grow = gbuf + ((int64_t)b * rows + lr) * (int64_t)K * kGW;
+  const uint16_t* grow = gbuf + ((int64_t)b * rows + lr) * (int64_t)g_slots(K) * kGW;
   uint16_t* crow = cbuf + ((int64_t)b * rows + lr) * (int64_t)K * kDqk;
   const lds_char* lb = lds_bytes(&lds[0]);
 
@@ -804,11 +815,12 @@ struct BwdPlan {
 // row and head).
 BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget) {
   BwdPlan p{};
-  const int64_t per_row = batch * topk * (int64_t)(kGW * 2 + kDqk * 2 + 4) + batch * kHeadsMax * 4;
+  const int64_t per_row = batch * g_slots(topk) * kGW * 2 + batch * topk * (int64_t)(kDqk * 2 + 4) +
+                          batch * kHeadsMax * 4;
   int64_t rows = s_q;
   if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
   p.rows = rows;
-  p.g_bytes = batch * rows * topk * kGW * 2;
+  p.g_bytes = batch * rows * g_slots(topk) * kGW * 2;
   p.c_bytes = batch * rows * topk * kDqk * 2;
   p.pairs_bytes = rows * topk * 4;
   p.csr_bytes = csr_ws_bytes(s_kv, rows, topk);
