@@ -338,9 +338,10 @@ def measured_traffic(kernel, S, H, K):
 
 
 def time_indexer_kernel(inp, ops, torch, reps=10):
-    """Average duration (ms) of the lightning-indexer score kernel alone (dsa_indexer_fwd,
-    fp8 queries and keys, causal), timed with HIP events on the stream it runs on, outside
-    the timed steps.  The step's indexer phase also includes the top-k selection."""
+    """Average duration (ms) of the lightning-indexer scores alone (dsa_indexer_fwd_ws, fp8
+    queries and keys, causal: the linear-split pre-pass plus the score kernel), timed with HIP
+    events on the stream they run on, outside the timed steps.  The step's indexer phase also
+    includes the top-k selection."""
     q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
     k8, ks = ops.quantize_fp8_per_row(inp["k_idx"])
     S = q8.shape[1]
@@ -589,7 +590,7 @@ def main():
                                 tflops_with_topk=work["indexer_flops"] / (idx_ms * 1e-3) / 1e12)
     if wl == "c3":
         idx_kernel_ms = time_indexer_kernel(inp, ops, torch)
-        line["indexer_mfma"] = dict(kernel="indexer_tile_kernel<true, 4>", bound="mfma", flops=work["indexer_flops"],
+        line["indexer_mfma"] = dict(kernel="indexer_lin_pieces_kernel<64> + indexer_tile_kernel<true, 4, true>", bound="mfma", flops=work["indexer_flops"],
                                     avg_launch_ms=idx_kernel_ms,
                                     achieved_tflops=work["indexer_flops"] / (idx_kernel_ms * 1e-3) / 1e12,
                                     peak_tflops=FP8_PEAK_TFLOPS,

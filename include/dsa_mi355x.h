@@ -79,6 +79,24 @@ int dsa_indexer_fwd(const void* q, const float* q_scale, const void* k, const fl
                     int64_t head_dim, int64_t ld_scores, int64_t q_offset, int64_t cmp_ratio, void* stream);
 
 /*
+ * dsa_indexer_fwd with a caller workspace (same reference interface: npu_lightning_indexer,
+ * converters/kernels/dsa.py:217-226).  For fp8-e4m3 operands with H_I = 64 and D_I = 128 the
+ * workspace holds, per query row, four fp8 pieces of u = sum_h (w q_scale / 2)[h] q[h, :] and
+ * their power-of-two scales, written by a pre-pass; the score kernel then takes
+ *   sum_h c_h relu(x_h) = sum_h (c_h / 2) |x_h| + u . k
+ * with u . k on the MFMA (half the VALU work of the relu form; the same scores to about
+ * 1e-6 of the row's magnitude).  Other shapes ignore the workspace and run dsa_indexer_fwd.
+ *   workspace        device scratch of at least dsa_indexer_fwd_workspace_size() bytes
+ *                    (NULL: dsa_indexer_fwd's kernels)
+ * dsa_indexer_fwd_workspace_size returns 0 where the split does not apply.
+ */
+int64_t dsa_indexer_fwd_workspace_size(int64_t batch, int64_t s_q, int64_t n_heads, int64_t head_dim, int dtype);
+int dsa_indexer_fwd_ws(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
+                       float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                       int64_t head_dim, int64_t ld_scores, int64_t q_offset, int64_t cmp_ratio, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/*
  * Per-row top-k of fp32 scores (reference: DSV32_SDPA.forward topk,
  * models/deepseek_v32/model.py:389-395; LiCompute, models/deepseek_v4/model.py:653-655).
  * Row (b, s) considers candidates t < min(s_k, (s + q_offset + 1) / cmp_ratio) whose score is
@@ -235,7 +253,9 @@ int dsa_compressor_fwd_tnd(const float* kv, const float* score, const float* ape
  * (cmp_residual_k: host int32 [n_seq] or NULL = 0) and, for sparse_mode 3,
  * q_offset_i = max(0, that count - len_q_i); sparse_mode 0 applies no causal rule.
  * scores_ws: device fp32 scratch of ws_bytes (>= 4 * the longest key sequence; a row chunk
- * of a sequence is scored into it at a time).  indices [T_q, topk] int32, values
+ * of a sequence is scored into it at a time; for fp8 with H_I = 64 each chunk row also takes
+ * dsa_indexer_fwd_workspace_size(1, 1, H_I, D_I, dtype) bytes of linear-split pieces, placed
+ * after the chunk's scores at a 256-byte boundary, so add that per row plus 256).  indices [T_q, topk] int32, values
  * [T_q, topk] fp32 or NULL. */
 int dsa_lightning_indexer_varlen(const void* q, const float* q_scale, const void* k, const float* k_scale,
                                  const float* w, int32_t* indices, float* values, float* scores_ws, int64_t ws_bytes,

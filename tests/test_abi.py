@@ -70,3 +70,15 @@ def test_ops_refuse_cpu_tensors(lib):
         ops.sparse_mla_fwd(q, kv, idx, 0.1)
     with pytest.raises(DSAError):
         ops.indexer_scores(torch.zeros(1, 4, 2, 8), torch.zeros(1, 4, 8), torch.zeros(1, 4, 2))
+
+
+def test_indexer_workspace_size(lib):
+    """The linear-split workspace (four fp8 pieces of 128 bytes and their fp32 scales per
+    query row) is sized for fp8 with H_I=64, D_I=128 only; other shapes need none."""
+    from torchtitan_npu_simulator_amd import _lib
+
+    fp8, bf16 = _lib.dtype_code(torch.float8_e4m3fn), _lib.dtype_code(torch.bfloat16)
+    assert lib.dsa_indexer_fwd_workspace_size(2, 8192, 64, 128, fp8) == 2 * 8192 * (4 * 128 + 4 * 4)
+    assert lib.dsa_indexer_fwd_workspace_size(1, 8192, 64, 128, bf16) == 0
+    assert lib.dsa_indexer_fwd_workspace_size(1, 8192, 32, 128, fp8) == 0
+    assert lib.dsa_indexer_fwd_workspace_size(1, 0, 64, 128, fp8) == 0

@@ -162,6 +162,34 @@ def test_indexer_fp8_quantise_dequantise_parity():
     assert float((err / mag).max()) <= 5e-5
 
 
+@pytest.mark.parametrize("S,s_k,q_offset,cmp_ratio,signed_w,split", [
+    (256, 256, 0, 1, False, True), (256, 256, 0, 1, False, False), (203, 1400, 1197, 1, True, True),
+    (96, 600, 2300, 4, True, True), (1, 64, 63, 1, False, True), (1030, 1030, 0, 1, True, True)])
+def test_indexer_fp8_linear_split_parity(S, s_k, q_offset, cmp_ratio, signed_w, split):
+    """fp8 H_I=64 scores through the linear split sum_h c|x|/2 + u.k (u as four fp8 pieces from
+    the pre-pass) and through the relu form, against the fp64 oracle of the dequantised
+    operands: 5e-5 of the row magnitude; mixed-sign head weights make the |x| and u.k halves
+    cancel, ragged S leaves a partial query pair, q_offset / cmp_ratio move the frontier."""
+    H, D = 64, 128
+    g = torch.Generator().manual_seed(S * 7 + s_k)
+    n_k = s_k
+    q = torch.randn(1, S, H, D, generator=g)
+    k = torch.randn(1, n_k, D, generator=g) * 3.0
+    w = (torch.randn(1, S, H, generator=g) if signed_w else torch.rand(1, S, H, generator=g)) * H ** -0.5 * D ** -0.5
+    q8, qs = O.quantize_e4m3_per_row(q)
+    k8, ks = O.quantize_e4m3_per_row(k)
+    got = _ops().indexer_scores(q8.to(DEV), k8.to(DEV), w.to(DEV), q_scale=qs.to(DEV), k_scale=ks.to(DEV),
+                                q_offset=q_offset, cmp_ratio=cmp_ratio, linear_split=split).cpu()
+    qd = q8.double() * qs.double().unsqueeze(-1)
+    kd = k8.double() * ks.double().unsqueeze(-1)
+    ref = O.indexer_scores(qd, kd, w.double(), q_offset=q_offset, cmp_ratio=cmp_ratio, dtype=torch.float64)
+    fin = torch.isfinite(ref)
+    assert torch.equal(fin, torch.isfinite(got))
+    err = (got.double() - ref).abs().masked_fill(~fin, 0).amax(-1)
+    mag = ref.abs().masked_fill(~fin, 0).amax(-1).clamp_min(1e-6)
+    assert float((err / mag).max()) <= 5e-5
+
+
 def test_lightning_indexer_op_end_to_end():
     """npu_lightning_indexer == oracle top-k applied to the GPU's own fp32 scores (bit-exact)."""
     S, H, D, K = 300, 64, 128, 64

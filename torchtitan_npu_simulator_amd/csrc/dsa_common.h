@@ -86,6 +86,25 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// fp32 -> OCP e4m3fn byte, round to nearest even
+__device__ __forceinline__ uint32_t e4m3fn_rne(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sgn = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return sgn | 0x7fu;  // inf, NaN
+  uint32_t enc;
+  if (a < 0x3c800000u) {
+    // below 2^-6: multiples of 2^-9 (the scaling is exact); 8 encodes 2^-6 itself
+    enc = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
+  } else {
+    const uint32_t mant = a & 0x7fffffu;
+    enc = (((a >> 23) - 120u) << 3) | (mant >> 20);  // exponent rebiased 127 -> 7, 3 mantissa bits
+    const uint32_t rest = mant & 0xfffffu;
+    enc += (rest > 0x80000u) || (rest == 0x80000u && (enc & 1u));  // carries into the exponent
+  }
+  return sgn | (enc > 0x7eu ? 0x7fu : enc);
+}
+
 // relu as one integer max on the bit pattern (negative floats, -0 included, have the sign
 // bit set and compare below 0): a float max would add a canonicalising max per operand in
 // IEEE mode.  +NaN passes through like torch.relu.

@@ -22,6 +22,17 @@ constexpr int kThreads = 256;
 // summed over the head tiles in-lane and over the 4 lane groups with two lane swaps; a
 // tile's scores are staged in LDS and written as whole rows.  Key ranges past every
 // query's causal frontier are written as -inf without any MFMA.
+//
+// Linear split (kLin, fp8 with two queries per wave): relu(x) = (x + |x|) / 2, so
+//   sum_h c_h relu(x_h) = sum_h (c_h/2) |x_h| + u . k,   u = sum_h (c_h/2) q_h   (x_h = q_h . k)
+// The |x| sum is one fma per C value (abs source modifier) instead of a max and an fma, which
+// halves the VALU work that bounds this kernel.  u . k runs on the MFMA: u comes from a
+// per-query pre-pass as kLinPieces fp8 pieces with power-of-two scales (u = sum_p 2^-e_p P_p
+// to about 2^-18 of max|u|), held as the rows of one more A tile per query pair (rows 0-3:
+// the pair's first query, rows 8-11: the second, the rest zero), so each 16-key tile costs
+// 9 MFMAs per two queries instead of 8.
+constexpr int kLinPieces = 4;
+constexpr int64_t kLinRowBytes = kLinPieces * kD + kLinPieces * 4;  // pieces + their scales
 template <bool kFp8, int kHeadTiles>
 struct IdxTile {
   static constexpr int kQw = kFp8 ? (8 / kHeadTiles > 0 ? 8 / kHeadTiles : 1) : (4 / kHeadTiles > 0 ? 4 / kHeadTiles : 1);
@@ -59,12 +70,101 @@ __device__ __forceinline__ void fill_neg_inf(float* __restrict__ scores, int64_t
   }
 }
 
-template <bool kFp8, int kHeadTiles>
+// four e4m3fn bytes -> fp32 by the packed hardware conversion (OCP e4m3 on gfx950, the
+// format the f8f6f4 MFMA reads)
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t v, float (&f)[4]) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)v, false), hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)v, true);
+  f[0] = lo[0];
+  f[1] = lo[1];
+  f[2] = hi[0];
+  f[3] = hi[1];
+}
+
+// Pre-pass of the linear split, one wave per query row r:
+//   u[r, :] = sum_h 0.5 * (w[r,h] * q_scale[r,h]) * q[r,h,:]
+// lane l reads 16-byte pieces of heads 8i + l/8 (i < H/8), dims 16(l%8)..+15, and the eight
+// lanes of one dim range are summed by lane exchanges.  Then kLinPieces greedy pieces:
+// 2^e_p makes max|res_p| fit e4m3 (<= 448), P_p = e4m3(2^e_p res_p) by the hardware
+// conversion, res_{p+1} = res_p - 2^-e_p P_p with P_p read back by the same hardware (so the
+// residual is exact for whatever rounding the conversion applies); lane group p (= l/8)
+// stores piece p.
+// pieces [rows][kLinPieces][kD] bytes, then scales [rows][kLinPieces] fp32 (= 2^-e_p).
+template <int H>
+__global__ void __launch_bounds__(kThreads)
+indexer_lin_pieces_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_scale,
+                          const float* __restrict__ w, uint8_t* __restrict__ pieces, float* __restrict__ pscale,
+                          int64_t nrows) {
+  const int64_t r = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (r >= nrows) return;  // whole waves
+  const int lane = threadIdx.x & 63, grp = lane >> 3, d0 = 16 * (lane & 7);
+  static_assert(H % 8 == 0, "eight heads per wave step");
+  constexpr int kSteps = H / 8;
+  float c[kSteps];
+  u32x4 x[kSteps];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {  // every load of the row issued at once
+    const int64_t hr = r * H + 8 * i + grp;
+    c[i] = w[hr] * (q_scale ? q_scale[hr] : 1.f);
+    x[i] = *reinterpret_cast<const u32x4*>(q + hr * kD + d0);
+  }
+  float u[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) u[e] = 0.f;
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) {
+    const float ci = 0.5f * c[i];
+#pragma unroll
+    for (int d4 = 0; d4 < 4; ++d4) {
+      float f[4];
+      fp8x4_to_f32(x[i][d4], f);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) u[4 * d4 + e] = fmaf(ci, f[e], u[4 * d4 + e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    u[e] += __shfl_xor(u[e], 8);
+    u[e] += __shfl_xor(u[e], 16);
+    u[e] += __shfl_xor(u[e], 32);
+  }
+  for (int p = 0; p < kLinPieces; ++p) {
+    float m = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(u[e]));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, __shfl_xor(m, 4));
+    int ex = 0;
+    if (m > 0.f && m <= 3.4028235e38f) {
+      int E;
+      const float f = frexpf(m, &E);  // m = f 2^E, f in [0.5, 1); 448 = 0.875 * 2^9
+      ex = min((f <= 0.875f ? 9 : 8) - E, 126);
+    }
+    const float up = ldexpf(1.f, ex), down = ldexpf(1.f, -ex);  // exact powers of two
+    u32x4 pk;
+#pragma unroll
+    for (int d4 = 0; d4 < 4; ++d4) {
+      int v = __builtin_amdgcn_cvt_pk_fp8_f32(u[4 * d4] * up, u[4 * d4 + 1] * up, 0, false);
+      v = __builtin_amdgcn_cvt_pk_fp8_f32(u[4 * d4 + 2] * up, u[4 * d4 + 3] * up, v, true);
+      pk[d4] = (uint32_t)v;
+      float f[4];
+      fp8x4_to_f32(pk[d4], f);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) u[4 * d4 + e] -= f[e] * down;
+    }
+    if (grp == p) *reinterpret_cast<u32x4*>(pieces + (r * kLinPieces + p) * kD + d0) = pk;
+    if (lane == 0) pscale[r * kLinPieces + p] = down;
+  }
+}
+
+template <bool kFp8, int kHeadTiles, bool kLin>
 __global__ void __launch_bounds__(kThreads, 2)
 indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_scale, const uint8_t* __restrict__ k,
                     const float* __restrict__ k_scale, const float* __restrict__ w, float* __restrict__ scores,
-                    int S, int s_k, int64_t ld, int64_t q_offset, int cmp_ratio) {
+                    int S, int s_k, int64_t ld, int64_t q_offset, int cmp_ratio,
+                    const uint8_t* __restrict__ lin_pieces, const float* __restrict__ lin_scale) {
   using T = IdxTile<kFp8, kHeadTiles>;
+  static_assert(!kLin || (kFp8 && T::kQw == 2), "the linear split pairs two fp8 queries per wave");
   constexpr int H = kHeadTiles * 16;
   constexpr int kQw = T::kQw;
   constexpr int kK = T::kKeys;
@@ -149,9 +249,35 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
       for (int r = 0; r < 4; ++r) {
         const int hr = ht * 16 + 4 * g + r;  // C row (head) held by this lane
         const float sc = q_scale ? q_scale[qrow + hr] : 1.f;
-        wv[j][ht][r] = w[qrow + hr] * sc;
+        wv[j][ht][r] = w[qrow + hr] * sc * (kLin ? 0.5f : 1.f);
       }
     }
+  }
+  // linear-split A tile (lane: row col, k = 32g..32g+31): rows 0-3 pieces of query qa,
+  // rows 8-11 of query qa + 1; C rows 4g..4g+3 get the pieces' scales (g = 0: qa, g = 2:
+  // qa + 1, odd g: zero rows)
+  uint32_t la_reg[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  float ls[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (kLin) {
+    if ((col & 4) == 0) {
+      const int s = min(qa + (col >> 3), S - 1);
+      const u32x4* p = reinterpret_cast<const u32x4*>(lin_pieces + ((q_row0 + s) * kLinPieces + (col & 3)) * kD + 32 * g);
+      const u32x4 x0 = p[0], x1 = p[1];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        la_reg[r] = x0[r];
+        la_reg[4 + r] = x1[r];
+      }
+    }
+    if ((g & 1) == 0) {
+      const int s = min(qa + (g >> 1), S - 1);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ls[r] = lin_scale[(q_row0 + s) * kLinPieces + r];
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r) asm volatile("" : "+v"(la_reg[r]));
+#pragma unroll
+    for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(ls[r]));
   }
   // the operands are forced ready here: a compiler-inserted wait for them inside the tile
   // loop would also wait for the next tile's DMA
@@ -224,29 +350,50 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
         }
       }
     };
-    // relu * w partial sum of item (kt, j) over this lane's 16 C values
+    auto mfma_lin = [&](const uint32_t (&kb)[T::kRegsPerTile], f32x4& c) {
+      if constexpr (kLin) {
+        i32x8 av, bv;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          av[r] = (int)la_reg[r];
+          bv[r] = (int)kb[r];
+        }
+        c = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, (f32x4){0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 0, 0, 0);
+      }
+    };
+    // relu * w partial sum of item (kt, j) over this lane's 16 C values (kLin: |x| * w / 2)
     auto partial = [&](int j, const f32x4 (&c)[kHeadTiles]) -> float {
       float p0 = 0.f, p1 = 0.f;
 #pragma unroll
       for (int ht = 0; ht < kHeadTiles; ++ht)
 #pragma unroll
         for (int r = 0; r < 4; r += 2) {
-          p0 = fmaf(wv[j][ht][r], relu_bits(c[ht][r]), p0);
-          p1 = fmaf(wv[j][ht][r + 1], relu_bits(c[ht][r + 1]), p1);
+          if constexpr (kLin) {
+            p0 = fmaf(wv[j][ht][r], fabsf(c[ht][r]), p0);
+            p1 = fmaf(wv[j][ht][r + 1], fabsf(c[ht][r + 1]), p1);
+          } else {
+            p0 = fmaf(wv[j][ht][r], relu_bits(c[ht][r]), p0);
+            p1 = fmaf(wv[j][ht][r + 1], relu_bits(c[ht][r + 1]), p1);
+          }
         }
       return p0 + p1;
     };
     // one 16-key tile: kQw items, each item's reduction behind the next item's MFMAs; raw
     // head sums are staged (key scale and causal mask are applied when the rows are stored)
     f32x4 cq[2][kHeadTiles];
-    auto tile = [&](int kt, const uint32_t (&kb_cur)[T::kRegsPerTile], uint32_t (&kb_nxt)[T::kRegsPerTile]) {
+    auto tile = [&](int kt, const uint32_t (&kb_cur)[T::kRegsPerTile], uint32_t (&kb_nxt)[T::kRegsPerTile],
+                    const f32x4& cl_cur, f32x4& cl_nxt) {
       read_b(min(kt + 1, ntiles - 1), kb_nxt);  // (the last tile re-reads itself)
       float pe = 0.f;
 #pragma unroll
       for (int j = 0; j < kQw; ++j) {
         // item (kt, j) is in cq[j & 1] (kQw is even, or 1 with the copy below)
-        if (j + 1 < kQw) mfma_q(j + 1, kb_cur, cq[(j + 1) & 1]);
-        else mfma_q(0, kb_nxt, cq[(j + 1) & 1]);
+        if (j + 1 < kQw) {
+          mfma_q(j + 1, kb_cur, cq[(j + 1) & 1]);
+        } else {
+          mfma_q(0, kb_nxt, cq[(j + 1) & 1]);
+          mfma_lin(kb_nxt, cl_nxt);
+        }
         const float pj = partial(j, cq[j & 1]);
         if constexpr (kQw == 1) {
           const float v = xor32_sum(xor16_sum(pj));
@@ -258,7 +405,9 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
           // groups {g, g^2} in lanes 0-31 and query j's in lanes 32-63; a 16-lane swap
           // completes both (lane groups 0,1 hold query j-1, groups 2,3 query j)
           const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(pe), __float_as_uint(pj), false, false);
-          const float h = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+          float h = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+          if constexpr (kLin)  // u . k of this lane group's query (zero in odd groups)
+            h += cl_cur[0] * ls[0] + cl_cur[1] * ls[1] + cl_cur[2] * ls[2] + cl_cur[3] * ls[3];
           const float v = xor16_sum(h);
           // lane groups 1 and 3 hold copies: they write the spare row (no branch, so the
           // tile stays one scheduling region)
@@ -271,11 +420,13 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
       }
     };
     uint32_t kb_a[T::kRegsPerTile], kb_b[T::kRegsPerTile];
+    f32x4 cl_a = (f32x4){0.f, 0.f, 0.f, 0.f}, cl_b = cl_a;
     read_b(0, kb_a);
     mfma_q(0, kb_a, cq[0]);
+    mfma_lin(kb_a, cl_a);
     for (int kt = 0; kt < ntiles; kt += 2) {  // two tiles per trip: the B registers alternate
-      tile(kt, kb_a, kb_b);
-      if (kt + 1 < ntiles) tile(kt + 1, kb_b, kb_a);
+      tile(kt, kb_a, kb_b, cl_a, cl_b);
+      if (kt + 1 < ntiles) tile(kt + 1, kb_b, kb_a, cl_b, cl_a);
     }
     __syncthreads();  // the tile's scores are staged
 
@@ -363,14 +514,15 @@ indexer_generic_kernel(const T* __restrict__ q, const float* __restrict__ q_scal
   scores[qrow * ld + t] = out;
 }
 
-}  // namespace
-}  // namespace dsa
+// the linear split applies to the fp8 H_I = 64, D_I = 128 tile kernel (two queries per wave)
+bool lin_split_shape(int dtype, int64_t n_heads, int64_t head_dim) {
+  return dtype == DSA_FP8_E4M3 && n_heads == 64 && head_dim == kD;
+}
 
-extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* k, const float* k_scale,
-                               const float* w, float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k,
-                               int64_t n_heads, int64_t head_dim, int64_t ld_scores, int64_t q_offset,
-                               int64_t cmp_ratio, void* stream) {
-  using namespace dsa;
+int indexer_fwd(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
+                float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                int64_t head_dim, int64_t ld_scores, int64_t q_offset, int64_t cmp_ratio, void* workspace,
+                int64_t workspace_bytes, void* stream) {
   if (!q || !k || !w || !scores) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: null pointer");
   if (batch <= 0 || s_q <= 0 || s_k <= 0 || n_heads <= 0 || head_dim <= 0 || ld_scores < s_k || cmp_ratio <= 0)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: bad sizes");
@@ -378,6 +530,23 @@ extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* 
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: sizes out of range");
   hipStream_t st = (hipStream_t)stream;
   const bool mfma_shape = head_dim == kD && n_heads % 16 == 0 && n_heads <= 128 && dtype != DSA_F32;
+  if (workspace && lin_split_shape(dtype, n_heads, head_dim)) {
+    const int64_t rows = batch * s_q;
+    if (workspace_bytes < rows * kLinRowBytes)
+      return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd_ws: workspace of %lld bytes, %lld needed",
+                       (long long)workspace_bytes, (long long)(rows * kLinRowBytes));
+    uint8_t* pieces = (uint8_t*)workspace;
+    float* pscale = (float*)(pieces + rows * kLinPieces * kD);
+    const uint8_t* qp = (const uint8_t*)q;
+    indexer_lin_pieces_kernel<64><<<(unsigned)ceil_div(rows, kThreads / 64), kThreads, 0, st>>>(qp, q_scale, w,
+                                                                                               pieces, pscale, rows);
+    using Tl = IdxTile<true, 4>;
+    dim3 grid(ceil_div(s_q, Tl::kQ), ceil_div(s_k, Tl::kSpan), (unsigned)batch);
+    indexer_tile_kernel<true, 4, true><<<grid, kThreads, 0, st>>>(qp, q_scale, (const uint8_t*)k, k_scale, w, scores,
+                                                                  (int)s_q, (int)s_k, ld_scores, q_offset,
+                                                                  (int)cmp_ratio, pieces, pscale);
+    return check_launch("dsa_indexer_fwd_ws(mfma, linear split)");
+  }
   if (mfma_shape) {
     const uint8_t* qp = (const uint8_t*)q;
     const uint8_t* kp = (const uint8_t*)k;
@@ -385,8 +554,9 @@ extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* 
   do {                                                                                                             \
     using Tl = IdxTile<FP8, HT>;                                                                                   \
     dim3 grid(ceil_div(s_q, Tl::kQ), ceil_div(s_k, Tl::kSpan), (unsigned)batch);                                          \
-    indexer_tile_kernel<FP8, HT><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, (int)s_q, (int)s_k, \
-                                                            ld_scores, q_offset, (int)cmp_ratio);                  \
+    indexer_tile_kernel<FP8, HT, false><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, (int)s_q,      \
+                                                                   (int)s_k, ld_scores, q_offset, (int)cmp_ratio,   \
+                                                                   nullptr, nullptr);                              \
   } while (0)
     const int ht = (int)(n_heads / 16);
     if (dtype == DSA_FP8_E4M3) {
@@ -433,4 +603,29 @@ extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* 
       return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_fwd: dtype %d", dtype);
   }
   return check_launch("dsa_indexer_fwd(generic)");
+}
+
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* k, const float* k_scale,
+                               const float* w, float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k,
+                               int64_t n_heads, int64_t head_dim, int64_t ld_scores, int64_t q_offset,
+                               int64_t cmp_ratio, void* stream) {
+  return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim, ld_scores,
+                          q_offset, cmp_ratio, nullptr, 0, stream);
+}
+
+extern "C" int64_t dsa_indexer_fwd_workspace_size(int64_t batch, int64_t s_q, int64_t n_heads, int64_t head_dim,
+                                                  int dtype) {
+  if (batch <= 0 || s_q <= 0 || !dsa::lin_split_shape(dtype, n_heads, head_dim)) return 0;
+  return batch * s_q * dsa::kLinRowBytes;
+}
+
+extern "C" int dsa_indexer_fwd_ws(const void* q, const float* q_scale, const void* k, const float* k_scale,
+                                  const float* w, float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k,
+                                  int64_t n_heads, int64_t head_dim, int64_t ld_scores, int64_t q_offset,
+                                  int64_t cmp_ratio, void* workspace, int64_t workspace_bytes, void* stream) {
+  return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim, ld_scores,
+                          q_offset, cmp_ratio, workspace, workspace_bytes, stream);
 }

@@ -80,8 +80,11 @@ extern "C" int dsa_lightning_indexer_varlen(const void* q, const float* q_scale,
     const int64_t res = cmp_residual_k ? cmp_residual_k[i] : 0;
     if (res < 0) return set_error(DSA_ERR_INVALID_ARG, "%s: cmp_residual_k[%lld] < 0", what, (long long)i);
     const int64_t q_off = sparse_mode == 3 ? std::max<int64_t>(0, cmp_ratio * lk + res - lq) : (int64_t)1 << 40;
-    const int64_t row_bytes = 4 * std::max<int64_t>(lk, 1);
-    const int64_t rows = std::min<int64_t>(lq, ws_bytes / row_bytes);
+    // per chunk row: its fp32 scores, plus (fp8, H_I = 64) the linear-split pieces placed after
+    // the chunk's scores at a 256-byte boundary
+    const int64_t lin_bytes = dsa_indexer_fwd_workspace_size(1, 1, n_heads, head_dim, dtype);
+    const int64_t row_bytes = 4 * std::max<int64_t>(lk, 1) + lin_bytes;
+    const int64_t rows = std::min<int64_t>(lq, std::max<int64_t>(0, ws_bytes - (lin_bytes ? 256 : 0)) / row_bytes);
     if (rows <= 0)
       return set_error(DSA_ERR_INVALID_ARG, "%s: score scratch of %lld bytes holds no row of sequence %lld", what,
                        (long long)ws_bytes, (long long)i);
@@ -89,10 +92,11 @@ extern "C" int dsa_lightning_indexer_varlen(const void* q, const float* q_scale,
       const int64_t nr = std::min(rows, lq - r0);
       const int64_t row = q0 + r0;
       if (lk > 0) {
-        if (int rc = dsa_indexer_fwd(at(q, row * n_heads * head_dim * es), at(q_scale, row * n_heads * 4),
-                                     at(k, k0 * head_dim * es), at(k_scale, k0 * 4), at(w, row * n_heads * 4),
-                                     scores_ws, dtype, 1, nr, lk, n_heads, head_dim, lk, q_off + r0, cmp_ratio,
-                                     stream))
+        void* lin_ws = lin_bytes ? (void*)((char*)scores_ws + (rows * 4 * lk + 255) / 256 * 256) : nullptr;
+        if (int rc = dsa_indexer_fwd_ws(at(q, row * n_heads * head_dim * es), at(q_scale, row * n_heads * 4),
+                                        at(k, k0 * head_dim * es), at(k_scale, k0 * 4), at(w, row * n_heads * 4),
+                                        scores_ws, dtype, 1, nr, lk, n_heads, head_dim, lk, q_off + r0, cmp_ratio,
+                                        lin_ws, nr * lin_bytes, stream))
           return rc;
       }
       // with no keys the selection sees no candidate and pads the rows with -1

@@ -114,8 +114,13 @@ def quantize_fp8_per_row(x: torch.Tensor):
     return q, scale
 
 
-def indexer_scores(q_idx, k_idx, weights, *, q_scale=None, k_scale=None, q_offset=0, cmp_ratio=1, out=None):
-    """fp32 index scores [B,S,S_k] (-inf where invalid) from dsa_indexer_fwd."""
+def indexer_scores(q_idx, k_idx, weights, *, q_scale=None, k_scale=None, q_offset=0, cmp_ratio=1, out=None,
+                   linear_split=True):
+    """fp32 index scores [B,S,S_k] (-inf where invalid) from dsa_indexer_fwd_ws.
+
+    ``linear_split`` gives the fp8 H_I=64 kernel its pre-pass workspace (relu(x) = (x + |x|)/2
+    with the linear part on the MFMA); False runs the relu-form kernels of dsa_indexer_fwd.
+    """
     lib = load_library()
     for t, n in ((q_idx, "query"), (k_idx, "key"), (weights, "weights")):
         require_gpu_tensor(t, n)
@@ -132,11 +137,14 @@ def indexer_scores(q_idx, k_idx, weights, *, q_scale=None, k_scale=None, q_offse
     ks = None if k_scale is None else k_scale.float().contiguous()
     if out is None:
         out = torch.empty(B, S, s_k, dtype=torch.float32, device=q_idx.device)
+    dt = _lib.dtype_code(q_idx.dtype)
+    ws_bytes = int(lib.dsa_indexer_fwd_workspace_size(B, S, H, D, dt)) if linear_split else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q_idx.device) if ws_bytes else None
     check(
-        lib.dsa_indexer_fwd(ptr(q_idx), ptr(qs), ptr(k_idx), ptr(ks), ptr(w), ptr(out), _lib.dtype_code(q_idx.dtype),
-                            B, S, s_k, H, D, out.stride(1), int(q_offset), int(cmp_ratio),
-                            stream_of(q_idx.device)),
-        "dsa_indexer_fwd",
+        lib.dsa_indexer_fwd_ws(ptr(q_idx), ptr(qs), ptr(k_idx), ptr(ks), ptr(w), ptr(out), dt, B, S, s_k, H, D,
+                               out.stride(1), int(q_offset), int(cmp_ratio), ptr(ws), ws_bytes,
+                               stream_of(q_idx.device)),
+        "dsa_indexer_fwd_ws",
     )
     return out
 
@@ -306,7 +314,10 @@ def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sp
     max_k = max(max(b - a for a, b in zip(cu_k[:-1], cu_k[1:])), 1)
     max_q = max(max(b - a for a, b in zip(cu_q[:-1], cu_q[1:])), 1)
     rows = max(1, min(max_q, _SCORE_BUDGET_BYTES // (4 * max_k)))
-    ws = torch.empty(rows * max_k, dtype=torch.float32, device=q.device)
+    # + the linear-split pieces of the chunk's rows (fp8, H_I=64), after a 256-byte boundary
+    lin = int(lib.dsa_indexer_fwd_workspace_size(1, 1, H, D, _lib.dtype_code(q.dtype)))
+    ws = torch.empty(rows * max_k + (rows * lin + 256) // 4 if lin else rows * max_k, dtype=torch.float32,
+                     device=q.device)
     if T == 0:
         return idx, vals
     check(
