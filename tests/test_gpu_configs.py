@@ -1,0 +1,560 @@
+"""Parity at the full sizes of the benchmark configurations (C2-C5) on the GPU.
+
+Each configuration runs through the HIP path at its real shape, and its results are held
+to the CPU oracle on sampled query rows (every row's result depends only on that row's
+inputs, its selected keys and the KV prefix) and on sampled keys (a key's gradient
+depends only on the rows that selected it), plus size-independent identities over the
+whole output:
+
+* top-k: on every row min(K, #valid) indices, ascending, causal, -1 padded; on the
+  sampled rows bit-exact against ``topk_select_numpy`` on the GPU's own fp32 scores;
+* indexer scores (fp8): against fp64 of the dequantised operands, per (row, key) within
+  1e-5 of  sum_h |w_h q_scale_h| (|q_h| . |k|) k_scale  (the absolute-value sum that bounds
+  the rounding of fp32 dot products, so rows whose signed head weights or products cancel
+  are held to the same bound);
+* attention (bf16): out, LSE, dQ and the head-summed mass on the sampled rows, and dKV on
+  the sampled keys, at 2e-2 relative (the contract tolerance);
+* indexer KL: dq_I, dw and the loss on the sampled rows, dk_I on the sampled keys, at 1e-2
+  (its E term is rounded to bf16) / 1e-4 for the loss;
+* identities over the full output: sum kv.dKV = sum q.dQ + sum O.dO (the latent alias
+  k_nope == v makes dK_nope + dV one term; oracle-pinned in tests/test_oracle.py), and,
+  since the indexer score is degree-1 homogeneous in each of q_I, k_I and w,
+  sum k_I.dk_I = sum q_I.dq_I = sum w.dw.
+
+Inputs are drawn on the device from seeded generators in the fixed order q, kv, q_I, k_I,
+w, dO.  Each configuration is a test class whose fixture runs the GPU pipeline once and
+frees it afterwards.
+"""
+
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+from tests.dsa_cases import rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+BF16_TOL = 2e-2
+KL_TOL = 1e-2
+IDX_TOL = 1e-5
+IDENT_TOL = 1e-3
+H, HI, DI, DQK, DV = 128, 64, 128, 576, 512
+BIG = 1 << 40  # q_offset that makes every listed key causal (validity is in the indices)
+
+
+def _ops():
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    return ops
+
+
+def _log(msg):
+    print(f"[configs] {msg}", flush=True)
+
+
+def _draw(S, s_kv, seed, *, signed_w=False, d_kv=DQK):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    bf = dict(device=DEV, dtype=torch.bfloat16, generator=g)
+    q = torch.randn(1, S, H, DQK, **bf)
+    kv = torch.randn(1, s_kv, d_kv, **bf) if s_kv else None
+    qi = torch.randn(1, S, HI, DI, **bf)
+    ki = torch.randn(1, s_kv, DI, **bf) if s_kv else None
+    w = torch.rand(1, S, HI, device=DEV, generator=g) if not signed_w else torch.randn(1, S, HI, device=DEV,
+                                                                                      generator=g)
+    w = w * HI ** -0.5 * DI ** -0.5
+    dout = torch.randn(1, S, H, DV, **bf)
+    return q, kv, qi, ki, w, dout
+
+
+def _blocks(spans, S):
+    return [(max(0, a), min(S, b)) for a, b in spans if min(S, b) > max(0, a)]
+
+
+# ---------------------------------------------------------------------------
+# shared checks
+# ---------------------------------------------------------------------------
+def check_index_structure(idx, K, q_off, cmp_ratio, s_k):
+    """Every row: min(K, #valid) indices, strictly ascending, causal, then -1 padding."""
+    S = idx.shape[1]
+    s = torch.arange(S, device=idx.device, dtype=torch.int64)
+    n_valid = torch.clamp(torch.minimum((s + q_off + 1) // cmp_ratio, torch.full_like(s, s_k)), min=0)
+    valid = idx[0] >= 0
+    assert torch.equal(valid.sum(-1), torch.clamp(n_valid, max=K)), "valid count per row"
+    assert not bool((valid[:, 1:] & ~valid[:, :-1]).any()), "-1 padding only after the valid prefix"
+    step = idx[0, :, 1:].long() - idx[0, :, :-1].long()
+    assert bool(((step > 0) | ~valid[:, 1:]).all()), "ascending indices"
+    assert bool(((idx[0].long() < n_valid.unsqueeze(1)) | ~valid).all()), "causal indices"
+
+
+def check_topk_rows(ops, q8, qs, k8, ks, w, idx, blocks, K, q_off, cmp_ratio):
+    """GPU selection == the oracle's stable descending selection on the GPU's own scores."""
+    s_k = k8.shape[1]
+    for r0, r1 in blocks:
+        sc = ops.indexer_scores(q8[:, r0:r1], k8, w[:, r0:r1], q_scale=qs[:, r0:r1], k_scale=ks,
+                                q_offset=q_off + r0, cmp_ratio=cmp_ratio).cpu()[0]
+        nv = np.array([O.valid_key_count(s, q_off + r0, cmp_ratio, s_k) for s in range(r1 - r0)])
+        ref = O.topk_select_numpy(sc.numpy(), K, nv)
+        got = idx[0, r0:r1].cpu().numpy()
+        bad = np.nonzero((got != ref).any(-1))[0]
+        assert bad.size == 0, f"top-k differs on rows {[r0 + int(b) for b in bad[:8]]}"
+
+
+def indexer_score_error(ops, q8, qs, k8, ks, w, blocks, q_off, cmp_ratio, linear_split=True):
+    """max over sampled (row, key) of |gpu - fp64| / sum_h |w q_scale| (|q| . |k|) k_scale,
+    the rounding bound of the fp32 sums; also logs the same error over the smaller
+    sum_h |w q_scale| |q . k| k_scale."""
+    kd = (k8[0].float().double() * ks[0].double().unsqueeze(-1)).cpu()  # [S_k, D]
+    kd_abs = kd.abs()
+    worst, worst_row, worst_x = 0.0, None, 0.0
+    for r0, r1 in blocks:
+        got = ops.indexer_scores(q8[:, r0:r1], k8, w[:, r0:r1], q_scale=qs[:, r0:r1], k_scale=ks,
+                                 q_offset=q_off + r0, cmp_ratio=cmp_ratio, linear_split=linear_split).cpu()[0]
+        qd = (q8[0, r0:r1].float().double() * qs[0, r0:r1].double().unsqueeze(-1)).cpu()
+        wb = w[0, r0:r1].double().cpu()
+        ref = O.indexer_scores(qd.unsqueeze(0), kd.unsqueeze(0), wb.unsqueeze(0), q_offset=q_off + r0,
+                               cmp_ratio=cmp_ratio, dtype=torch.float64)[0]
+        fin = torch.isfinite(ref)
+        assert torch.equal(fin, torch.isfinite(got)), "indexer mask"
+        for i in range(r1 - r0):
+            diff = (got[i].double() - ref[i]).abs().masked_fill(~fin[i], 0.0)
+            bound = (wb[i].abs().unsqueeze(1) * (qd[i].abs() @ kd_abs.T)).sum(0).clamp_min(1e-30)
+            m = float((diff / bound).max()) if diff.numel() else 0.0
+            if m > worst:
+                worst, worst_row = m, r0 + i
+            x_bound = (wb[i].abs().unsqueeze(1) * (qd[i] @ kd.T).abs()).sum(0).clamp_min(1e-30)
+            worst_x = max(worst_x, float((diff / x_bound).max()) if diff.numel() else 0.0)
+    _log(f"indexer error / sum|c||q.k|: {worst_x:.3g}")
+    return worst, worst_row
+
+
+def check_attention_rows(res, q, kv, dout, scale, blocks, q_off, sub=32):
+    """out / LSE / dQ / mass on the sampled rows against the oracle (full KV prefix)."""
+    kv_c = kv.cpu()
+    errs = dict(out=0.0, lse=0.0, dq=0.0, mass=0.0)
+    for a, b in blocks:
+        for r0 in range(a, b, sub):
+            r1 = min(b, r0 + sub)
+            qb, db = q[:, r0:r1].cpu(), dout[:, r0:r1].cpu()
+            ib = res["idx"][:, r0:r1].cpu()
+            ob = res["out"][:, r0:r1].cpu()
+            lse = (res["smax"][:, r0:r1] + torch.log(res["ssum"][:, r0:r1])).cpu().double()
+            ref_out, ref_lse = O.sparse_mla_fwd(qb, kv_c, ib, scale, q_offset=q_off + r0, chunk=8)
+            fin = torch.isfinite(ref_lse)
+            assert torch.equal(fin, torch.isfinite(lse)), f"rows {r0}-{r1}: rows without keys"
+            errs["out"] = max(errs["out"], rel_err(ob, ref_out))
+            if bool(fin.any()):
+                errs["lse"] = max(errs["lse"], float((lse[fin] - ref_lse[fin]).abs().max()))
+            rdq, _, rmass = O.sparse_mla_bwd_closed_form(qb, kv_c, ib, ob, ref_lse, db, scale, q_offset=q_off + r0)
+            errs["dq"] = max(errs["dq"], rel_err(res["dq"][:, r0:r1].cpu(), rdq))
+            errs["mass"] = max(errs["mass"], rel_err(res["mass"][:, r0:r1].cpu(), rmass))
+    _log(f"attention rows: {errs}")
+    assert errs["out"] <= BF16_TOL and errs["dq"] <= BF16_TOL and errs["mass"] <= BF16_TOL, errs
+    assert errs["lse"] <= BF16_TOL, errs
+
+
+def _rows_selecting(idx, key):
+    return (idx[0] == key).any(-1).nonzero().flatten()
+
+
+def selected_keys(idx, picks):
+    """Keys the GPU selected: idx[0, row, slot] for (row, slot) in ``picks``; slot -1 is the
+    row's last valid slot (its largest key)."""
+    keys = []
+    for row, slot in picks:
+        r = idx[0, row]
+        n = int((r >= 0).sum())
+        assert n > 0, f"row {row} selected nothing"
+        keys.append(int(r[n - 1 if slot < 0 else min(slot, n - 1)]))
+    return sorted(set(keys))
+
+
+def check_dkv_keys(res, q, kv, dout, scale, keys, chunk=256):
+    """dKV[j] = sum over the (row, head) pairs whose row selected j (oracle closed form
+    with the GPU's LSE; K = 1 slot holding j)."""
+    worst = 0.0
+    for j in keys:
+        rows = _rows_selecting(res["idx"], j)
+        assert rows.numel() > 0, f"key {j} was never selected"
+        ref = torch.zeros(DQK, dtype=torch.float64)
+        kv_j = kv[:, j : j + 1].cpu()
+        for c0 in range(0, rows.numel(), chunk):
+            r = rows[c0 : c0 + chunk]
+            qb = q[0, r].unsqueeze(0).cpu()
+            ob = res["out"][0, r].unsqueeze(0).cpu()
+            db = dout[0, r].unsqueeze(0).cpu()
+            lse = (res["smax"][0, r] + torch.log(res["ssum"][0, r])).unsqueeze(0).cpu().double()
+            one = torch.zeros(1, r.numel(), 1, dtype=torch.int32)
+            _, rdkv, _ = O.sparse_mla_bwd_closed_form(qb, kv_j, one, ob, lse, db, scale, q_offset=BIG)
+            ref += rdkv[0, 0]
+        e = rel_err(res["dkv"][0, j].cpu(), ref)
+        worst = max(worst, e)
+        assert e <= BF16_TOL, f"dKV of key {j} ({rows.numel()} rows): rel err {e:.3g}"
+    _log(f"dKV sampled keys {list(keys)}: worst rel err {worst:.3g}")
+
+
+def check_kl_rows(res, qi, ki, w, blocks, q_off, eps=1e-8):
+    errs = dict(dq_i=0.0, dw=0.0, loss=0.0)
+    ki_c = ki.cpu()
+    for r0, r1 in blocks:
+        rdq, _, rdw, rloss = O.indexer_kl_from_mass(qi[:, r0:r1].cpu(), ki_c, w[:, r0:r1].cpu(),
+                                                    res["idx"][:, r0:r1].cpu(), res["mass"][:, r0:r1].cpu(),
+                                                    q_offset=q_off + r0, eps=eps)
+        errs["dq_i"] = max(errs["dq_i"], rel_err(res["dq_i"][:, r0:r1].cpu(), rdq))
+        errs["dw"] = max(errs["dw"], rel_err(res["dw"][:, r0:r1].cpu(), rdw))
+        got = float(res["loss_rows"][:, r0:r1].double().sum())
+        errs["loss"] = max(errs["loss"], abs(got - float(rloss)) / max(abs(float(rloss)), 1e-30))
+    _log(f"indexer KL rows: {errs}")
+    assert errs["dq_i"] <= KL_TOL and errs["dw"] <= KL_TOL and errs["loss"] <= 1e-4, errs
+
+
+def check_dk_i_keys(res, qi, ki, w, keys, chunk=128, eps=1e-8):
+    """dk_I[t] from the oracle's autograd over exactly the rows that selected t (fp32)."""
+    ki_c = ki.cpu()
+    worst = 0.0
+    for t in keys:
+        rows = _rows_selecting(res["idx"], t)
+        ref = torch.zeros(DI, dtype=torch.float64)
+        for c0 in range(0, rows.numel(), chunk):
+            r = rows[c0 : c0 + chunk]
+            _, rdk, _, _ = O.indexer_kl_from_mass(qi[0, r].unsqueeze(0).cpu(), ki_c, w[0, r].unsqueeze(0).cpu(),
+                                                  res["idx"][0, r].unsqueeze(0).cpu(),
+                                                  res["mass"][0, r].unsqueeze(0).cpu(), q_offset=BIG, eps=eps,
+                                                  dtype=torch.float32)
+            ref += rdk[0, t].double()
+        e = rel_err(res["dk_i"][0, t].cpu(), ref)
+        worst = max(worst, e)
+        assert e <= KL_TOL, f"dk_I of key {t} ({rows.numel()} rows): rel err {e:.3g}"
+    _log(f"dk_I sampled keys {list(keys)}: worst rel err {worst:.3g}")
+
+
+def _dot_rows(a, b, chunk=512):
+    """Per-row fp64 sums of a * b over every dim but the row axis (dim 1), [S]."""
+    out = []
+    for r0 in range(0, a.shape[1], chunk):
+        x = a[:, r0 : r0 + chunk].double() * b[:, r0 : r0 + chunk].double()
+        out.append(x.reshape(x.shape[1], -1).sum(-1))
+    return torch.cat(out)
+
+
+def check_identities(res, q, kv, dout, qi, ki, w):
+    """sum kv.dKV = sum q.dQ + sum O.dO and sum k_I.dk_I = sum q_I.dq_I = sum w.dw,
+    each held to 1e-3 of the sum of the per-row magnitudes."""
+    qdq = _dot_rows(q, res["dq"])
+    odo = _dot_rows(res["out"], dout)
+    lhs = float(_dot_rows(kv, res["dkv"]).sum())
+    rhs = float(qdq.sum() + odo.sum())
+    mag = float(qdq.abs().sum() + odo.abs().sum())
+    _log(f"dKV identity: sum kv.dKV={lhs:.6g}  sum q.dQ + sum O.dO={rhs:.6g}  (scale {mag:.6g})")
+    assert abs(lhs - rhs) <= IDENT_TOL * mag
+    qi_dq = _dot_rows(qi, res["dq_i"])
+    w_dw = _dot_rows(w.unsqueeze(-1), res["dw"].unsqueeze(-1))
+    k_dk = float(_dot_rows(ki, res["dk_i"]).sum())
+    mag_i = float(qi_dq.abs().sum())
+    _log(f"dk_I identity: sum k.dk={k_dk:.6g} sum q.dq={float(qi_dq.sum()):.6g} sum w.dw={float(w_dw.sum()):.6g} "
+         f"(scale {mag_i:.6g})")
+    assert abs(k_dk - float(qi_dq.sum())) <= IDENT_TOL * mag_i
+    assert abs(float(w_dw.sum()) - float(qi_dq.sum())) <= IDENT_TOL * mag_i
+
+
+def run_dense_step(q, kv, qi, ki, w, dout, K, scale, *, backward=True, cmp_ratio=1, attn_q_offset=0):
+    """The benchmarked layer: fp8 quantise -> indexer + top-k -> attention fwd (-> bwd with
+    mass -> indexer KL grads)."""
+    ops = _ops()
+    q8, qs = ops.quantize_fp8_per_row(qi)
+    k8, ks = ops.quantize_fp8_per_row(ki)
+    idx, _ = ops.npu_lightning_indexer(q8, k8, w, sparse_count=K, sparse_mode=3, cmp_ratio=cmp_ratio,
+                                       query_scale=qs, key_scale=ks)
+    idx = idx[:, :, 0].contiguous()
+    out, smax, ssum = ops.sparse_mla_fwd(q, kv, idx, scale, q_offset=attn_q_offset)
+    res = dict(q8=q8, qs=qs, k8=k8, ks=ks, idx=idx, out=out, smax=smax, ssum=ssum)
+    if backward:
+        dq, dkv, mass = ops.sparse_mla_bwd(q, kv, idx, out, dout, smax, ssum, scale, q_offset=attn_q_offset,
+                                           return_mass=True)
+        dq_i, dk_i, dw, loss_rows = ops.indexer_kl_grad_from_mass(qi, ki, w, idx, mass, q_offset=attn_q_offset)
+        res.update(dq=dq, dkv=dkv, mass=mass, dq_i=dq_i, dk_i=dk_i, dw=dw, loss_rows=loss_rows)
+    torch.cuda.synchronize()
+    return res
+
+
+def _free(run):
+    run["res"].clear()
+    run.clear()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+# ---------------------------------------------------------------------------
+# C2: S=4096 forward
+# ---------------------------------------------------------------------------
+class TestC2Forward:
+    S, K, SEED = 4096, 2048, 2
+
+    @pytest.fixture(scope="class")
+    def run(self):
+        _log(f"C2: S={self.S} H={H} K={self.K} forward")
+        q, kv, qi, ki, w, dout = _draw(self.S, self.S, self.SEED)
+        res = run_dense_step(q, kv, qi, ki, w, dout, self.K, DQK ** -0.5, backward=False)
+        run = dict(q=q, kv=kv, qi=qi, ki=ki, w=w, dout=dout, res=res)
+        yield run
+        _free(run)
+
+    def blocks(self):
+        return _blocks([(0, 32), (2032, 2064), (4064, 4096)], self.S)
+
+    def test_indices(self, run):
+        r = run["res"]
+        check_index_structure(r["idx"], self.K, 0, 1, self.S)
+        check_topk_rows(_ops(), r["q8"], r["qs"], r["k8"], r["ks"], run["w"], r["idx"], self.blocks(), self.K, 0, 1)
+
+    def test_indexer_scores(self, run):
+        r = run["res"]
+        err, row = indexer_score_error(_ops(), r["q8"], r["qs"], r["k8"], r["ks"], run["w"],
+                                       _blocks([(0, 8), (2040, 2048), (4088, 4096)], self.S), 0, 1)
+        _log(f"C2 indexer: worst {err:.3g} (row {row})")
+        assert err <= IDX_TOL
+
+    def test_attention_forward(self, run):
+        r = run["res"]
+        kv_c = run["kv"].cpu()
+        worst_out = worst_lse = 0.0
+        for a, b in self.blocks():
+            for r0 in range(a, b, 16):
+                r1 = min(b, r0 + 16)
+                ref_out, ref_lse = O.sparse_mla_fwd(run["q"][:, r0:r1].cpu(), kv_c, r["idx"][:, r0:r1].cpu(),
+                                                    DQK ** -0.5, q_offset=r0, chunk=8)
+                lse = (r["smax"][:, r0:r1] + torch.log(r["ssum"][:, r0:r1])).cpu().double()
+                worst_out = max(worst_out, rel_err(r["out"][:, r0:r1].cpu(), ref_out))
+                worst_lse = max(worst_lse, float((lse - ref_lse).abs().max()))
+        _log(f"C2 attention: out {worst_out:.3g}, lse {worst_lse:.3g}")
+        assert worst_out <= BF16_TOL and worst_lse <= BF16_TOL
+
+
+# ---------------------------------------------------------------------------
+# C3: S=8192 forward + backward (the benchmarked step)
+# ---------------------------------------------------------------------------
+class TestC3Step:
+    S, K, SEED = 8192, 2048, 3
+
+    @pytest.fixture(scope="class")
+    def run(self):
+        _log(f"C3: S={self.S} H={H} K={self.K} forward + backward")
+        q, kv, qi, ki, w, dout = _draw(self.S, self.S, self.SEED)
+        res = run_dense_step(q, kv, qi, ki, w, dout, self.K, DQK ** -0.5)
+        run = dict(q=q, kv=kv, qi=qi, ki=ki, w=w, dout=dout, res=res)
+        yield run
+        _free(run)
+
+    def blocks(self):
+        return _blocks([(0, 64), (2016, 2080), (8128, 8192)], self.S)
+
+    def test_indices(self, run):
+        r = run["res"]
+        check_index_structure(r["idx"], self.K, 0, 1, self.S)
+        check_topk_rows(_ops(), r["q8"], r["qs"], r["k8"], r["ks"], run["w"], r["idx"], self.blocks(), self.K, 0, 1)
+
+    def test_attention_rows(self, run):
+        check_attention_rows(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, self.blocks(), 0)
+
+    def test_dkv_sampled_keys(self, run):
+        # key 5: every row < 2048 selects it (popular key); the last row's largest key: few rows
+        keys = [5, 2047] + selected_keys(run["res"]["idx"], [(4096, 1000), (8000, -1), (8191, -1)])
+        check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, keys)
+
+    def test_indexer_kl_rows_and_keys(self, run):
+        check_kl_rows(run["res"], run["qi"], run["ki"], run["w"], self.blocks(), 0)
+        keys = selected_keys(run["res"]["idx"], [(3100, -1), (6100, -1), (8191, -1)])
+        check_dk_i_keys(run["res"], run["qi"], run["ki"], run["w"], keys)
+
+    def test_full_size_identities(self, run):
+        check_identities(run["res"], run["q"], run["kv"], run["dout"], run["qi"], run["ki"], run["w"])
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_c3_fp8_indexer_mixed_sign_weights(split):
+    """fp8 indexer at the C3 shape with N(0,1) head weights (signed: the relu terms cancel)
+    against fp64 of the dequantised operands, per (row, key) within 2e-5 of
+    sum_h |w_h q_scale_h| |q_h . k| k_scale, on early rows (few keys, most cancellation)
+    and rows across the sequence."""
+    ops = _ops()
+    S = 8192
+    _, _, qi, ki, w, _ = _draw(S, S, 31, signed_w=True)
+    q8, qs = ops.quantize_fp8_per_row(qi)
+    k8, ks = ops.quantize_fp8_per_row(ki)
+    blocks = _blocks([(0, 16), (1000, 1016), (4090, 4106), (8176, 8192)], S)
+    err, row = indexer_score_error(ops, q8, qs, k8, ks, w, blocks, 0, 1, linear_split=split)
+    _log(f"C3 fp8 indexer, signed weights, linear_split={split}: worst {err:.3g} (row {row})")
+    assert err <= IDX_TOL
+
+
+# ---------------------------------------------------------------------------
+# C4: S=32768, r=4 compressed KV
+# ---------------------------------------------------------------------------
+class TestC4CompressedStep:
+    S, R, K, SEED = 32768, 4, 2048, 4
+
+    @pytest.fixture(scope="class")
+    def run(self):
+        ops = _ops()
+        S, r = self.S, self.R
+        _log(f"C4: S={S} r={r} compressor + indexer + attention over {S // r} compressed rows")
+        g = torch.Generator(device=DEV).manual_seed(self.SEED)
+        f = dict(device=DEV, dtype=torch.float32, generator=g)
+        comp = []
+        for d in (DV, DI):
+            kv_p = torch.randn(1, S, 2 * d, **f)
+            sc_p = torch.randn(1, S, 2 * d, **f)
+            ape = torch.randn(r, 2 * d, **f) * 0.02
+            nw = 1.0 + 0.1 * torch.randn(d, **f)
+            comp.append((kv_p, sc_p, ape, nw))
+        pooled = [ops.compressor_pool(c[0], c[1], c[2], r) for c in comp]
+        normed = [ops.compressor_pool(c[0], c[1], c[2], r, norm_weight=c[3]) for c in comp]
+        q, _, qi, _, w, dout = _draw(S, 0, self.SEED + 100)
+        ckv, cki = normed
+        kv = torch.nn.functional.pad(ckv, (0, DQK - DV))  # 512 value columns + 64 zero columns
+        res = run_dense_step(q, kv, qi, cki, w, dout, self.K, DQK ** -0.5, cmp_ratio=r, attn_q_offset=BIG)
+        run = dict(comp=comp, pooled=pooled, normed=normed, q=q, kv=kv, qi=qi, ki=cki, w=w, dout=dout, res=res)
+        yield run
+        _free(run)
+
+    def blocks(self):
+        # rows 0-2 have no compressed key yet; the frontier reaches K = 2048 blocks at row 8191
+        return _blocks([(0, 32), (8176, 8208), (32736, 32768)], self.S)
+
+    def test_compressor_full_size(self, run):
+        for (kv_p, sc_p, ape, nw), pooled, normed in zip(run["comp"], run["pooled"], run["normed"]):
+            ref = O.compressor_pool(kv_p.cpu(), sc_p.cpu(), ape.cpu(), self.R)
+            e = rel_err(pooled.cpu(), ref)
+            assert e <= 1e-5, e
+            ref_n = O.compressor_pool(kv_p.cpu(), sc_p.cpu(), ape.cpu(), self.R, norm_weight=nw.cpu(),
+                                      out_dtype=torch.bfloat16)
+            e_n = rel_err(normed.float().cpu(), ref_n)
+            assert e_n <= BF16_TOL, e_n
+            _log(f"C4 compressor D={ref.shape[-1]}: pooled {e:.3g}, RMSNorm bf16 {e_n:.3g}")
+
+    def test_indices(self, run):
+        r = run["res"]
+        check_index_structure(r["idx"], self.K, 0, self.R, self.S // self.R)
+        check_topk_rows(_ops(), r["q8"], r["qs"], r["k8"], r["ks"], run["w"], r["idx"], self.blocks(), self.K, 0,
+                        self.R)
+        err, row = indexer_score_error(_ops(), r["q8"], r["qs"], r["k8"], r["ks"], run["w"],
+                                       _blocks([(4, 12), (32760, 32768)], self.S), 0, self.R)
+        _log(f"C4 indexer over compressed keys: worst {err:.3g} (row {row})")
+        assert err <= IDX_TOL
+
+    def test_attention_rows(self, run):
+        check_attention_rows(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, self.blocks(), BIG)
+
+    def test_dkv_and_dk_i_sampled_keys(self, run):
+        idx = run["res"]["idx"]
+        check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5,
+                       [0, 2047] + selected_keys(idx, [(24100, -1), (32767, -1)]))
+        check_dk_i_keys(run["res"], run["qi"], run["ki"], run["w"], selected_keys(idx, [(24100, -1), (32767, -1)]))
+
+    def test_indexer_kl_rows(self, run):
+        check_kl_rows(run["res"], run["qi"], run["ki"], run["w"], self.blocks(), BIG)
+
+    def test_full_size_identities(self, run):
+        check_identities(run["res"], run["q"], run["kv"], run["dout"], run["qi"], run["ki"], run["w"])
+
+
+# ---------------------------------------------------------------------------
+# C5 (i): one 131072-token sequence (one GPU's context-parallel shard)
+# ---------------------------------------------------------------------------
+class TestC5LongSequence:
+    S, K, SEED = 131072, 2048, 5
+
+    @pytest.fixture(scope="class")
+    def run(self):
+        _log(f"C5(i): S={self.S} H={H} K={self.K} forward + backward, indexer chunked by query rows")
+        q, kv, qi, ki, w, dout = _draw(self.S, self.S, self.SEED)
+        res = run_dense_step(q, kv, qi, ki, w, dout, self.K, DQK ** -0.5)
+        run = dict(q=q, kv=kv, qi=qi, ki=ki, w=w, dout=dout, res=res)
+        yield run
+        _free(run)
+
+    def blocks(self):
+        # the last 32 rows of the shard, and rows straddling an indexer chunk boundary
+        return _blocks([(2040, 2056), (65528, 65544), (131040, 131072)], self.S)
+
+    def test_indices(self, run):
+        r = run["res"]
+        check_index_structure(r["idx"], self.K, 0, 1, self.S)
+        check_topk_rows(_ops(), r["q8"], r["qs"], r["k8"], r["ks"], run["w"], r["idx"], self.blocks(), self.K, 0, 1)
+        err, row = indexer_score_error(_ops(), r["q8"], r["qs"], r["k8"], r["ks"], run["w"],
+                                       _blocks([(131064, 131072)], self.S), 0, 1)
+        _log(f"C5(i) indexer: worst {err:.3g} (row {row})")
+        assert err <= IDX_TOL
+
+    def test_attention_rows(self, run):
+        check_attention_rows(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, self.blocks(), 0)
+
+    def test_dkv_and_dk_i_sampled_keys(self, run):
+        idx = run["res"]["idx"]
+        check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5,
+                       [1000] + selected_keys(idx, [(120100, -1), (131071, -1)]))
+        check_dk_i_keys(run["res"], run["qi"], run["ki"], run["w"], selected_keys(idx, [(125100, -1), (131071, -1)]))
+
+    def test_indexer_kl_rows(self, run):
+        check_kl_rows(run["res"], run["qi"], run["ki"], run["w"], self.blocks(), 0)
+
+    def test_full_size_identities(self, run):
+        check_identities(run["res"], run["q"], run["kv"], run["dout"], run["qi"], run["ki"], run["w"])
+
+
+# ---------------------------------------------------------------------------
+# C5 (ii): 8 packed sequences, lengths U[1024, 32768], through the varlen entry points
+# ---------------------------------------------------------------------------
+class TestC5PackedVarlen:
+    SEED, K = 0, 2048
+
+    @pytest.fixture(scope="class")
+    def run(self):
+        ops = _ops()
+        lens = torch.randint(1024, 32769, (8,), generator=torch.Generator().manual_seed(self.SEED)).tolist()
+        cu = [0]
+        for n in lens:
+            cu.append(cu[-1] + n)
+        T = cu[-1]
+        _log(f"C5(ii): {len(lens)} packed sequences {lens} ({T} tokens)")
+        q, kv, qi, ki, w, dout = _draw(T, T, self.SEED + 50)
+        q8, qs = ops.quantize_fp8_per_row(qi[0])
+        k8, ks = ops.quantize_fp8_per_row(ki[0])
+        idx, _ = ops.lightning_indexer_varlen(q8, k8, w[0], cu, cu, self.K, query_scale=qs, key_scale=ks)
+        scale = DQK ** -0.5
+        out, smax, ssum = ops.sparse_mla_fwd_varlen(q[0], kv[0], idx, scale, cu, cu)
+        dq, dkv, mass = ops.sparse_mla_bwd_varlen(q[0], kv[0], idx, out, dout[0], smax, ssum, scale, cu, cu,
+                                                  return_mass=True)
+        dq_i, dk_i, dw, loss_rows = ops.indexer_kl_grad_from_mass_varlen(qi[0], ki[0], w[0], idx, mass, cu, cu)
+        torch.cuda.synchronize()
+        res = dict(q8=q8.unsqueeze(0), qs=qs.unsqueeze(0), k8=k8.unsqueeze(0), ks=ks.unsqueeze(0),
+                   idx=idx.unsqueeze(0), out=out.unsqueeze(0), smax=smax.unsqueeze(0), ssum=ssum.unsqueeze(0),
+                   dq=dq.unsqueeze(0), dkv=dkv.unsqueeze(0), mass=mass.unsqueeze(0), dq_i=dq_i.unsqueeze(0),
+                   dk_i=dk_i.unsqueeze(0), dw=dw.unsqueeze(0), loss_rows=loss_rows.unsqueeze(0))
+        run = dict(lens=lens, cu=cu, q=q, kv=kv, qi=qi, ki=ki, w=w, dout=dout, res=res)
+        yield run
+        _free(run)
+
+    @pytest.mark.parametrize("i", range(8))
+    def test_sequence(self, run, i):
+        """Sequence i of the pack, seen through the fixed-length checks: its rows, its keys
+        (rows and keys a..b of the packed tensors; indices are sequence-local)."""
+        ops = _ops()
+        a, b = run["cu"][i], run["cu"][i + 1]
+        n = b - a
+        sr = {k: v[:, a:b] for k, v in run["res"].items()}
+        q, kv, dout = run["q"][:, a:b], run["kv"][:, a:b], run["dout"][:, a:b]
+        qi, ki, w = run["qi"][:, a:b], run["ki"][:, a:b], run["w"][:, a:b]
+        check_index_structure(sr["idx"], self.K, 0, 1, n)
+        blocks = _blocks([(0, 8), (n - 8, n)], n)
+        check_topk_rows(ops, sr["q8"], sr["qs"], sr["k8"], sr["ks"], w, sr["idx"], blocks, self.K, 0, 1)
+        check_attention_rows(sr, q, kv, dout, DQK ** -0.5, blocks, 0)
+        check_kl_rows(sr, qi, ki, w, blocks, 0)
+        check_dkv_keys(sr, q, kv, dout, DQK ** -0.5, selected_keys(sr["idx"], [(n - 1, -1), (max(0, n - 600), -1)]))
+        if i < 2:
+            check_dk_i_keys(sr, qi, ki, w, selected_keys(sr["idx"], [(n - 1, -1), (max(0, n - 300), -1)]))
+        _log(f"C5(ii) sequence {i} ({n} tokens) matches")
+
+    def test_full_size_identities(self, run):
+        check_identities(run["res"], run["q"], run["kv"], run["dout"], run["qi"], run["ki"], run["w"])
