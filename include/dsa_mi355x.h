@@ -97,6 +97,24 @@ int dsa_indexer_fwd_ws(const void* q, const float* q_scale, const void* k, const
                        int64_t workspace_bytes, void* stream);
 
 /*
+ * dsa_indexer_fwd_ws without a workspace and without any allocation.  No counterpart in the
+ * reference: this entry point is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The linear-split
+ * pieces live in a static 32 MiB device array of the library (one per GPU, held until the
+ * process ends), enough for dsa_indexer_fwd_noalloc_max_rows() = 63550 query rows
+ * (batch * s_q) per call; more rows are rejected with DSA_ERR_INVALID_ARG (split them over
+ * several calls).  Same arguments, results and kernels as dsa_indexer_fwd_ws; shapes the
+ * split does not apply to run dsa_indexer_fwd's kernels.  Every call on a GPU uses that GPU's
+ * one array, so calls that overlap on one GPU (concurrent streams or threads) race; calls on
+ * one stream are ordered and safe.  Nothing in the array needs clearing between calls.
+ */
+int64_t dsa_indexer_fwd_noalloc_max_rows(void);
+int dsa_indexer_fwd_noalloc(const void* q, const float* q_scale, const void* k, const float* k_scale,
+                            const float* w, float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k,
+                            int64_t n_heads, int64_t head_dim, int64_t ld_scores, int64_t q_offset,
+                            int64_t cmp_ratio, void* stream);
+
+/*
  * Per-row top-k of fp32 scores (reference: DSV32_SDPA.forward topk,
  * models/deepseek_v32/model.py:389-395; LiCompute, models/deepseek_v4/model.py:653-655).
  * Row (b, s) considers candidates t < min(s_k, (s + q_offset + 1) / cmp_ratio) whose score is

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -30,6 +30,9 @@ _SIGNATURES = {
     "dsa_indexer_fwd_workspace_size": ([_i64, _i64, _i64, _i64, _i32], _i64),
     "dsa_indexer_fwd_ws": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
                             _i64, _vp], _i32),
+    "dsa_indexer_fwd_noalloc_max_rows": ([], _i64),
+    "dsa_indexer_fwd_noalloc": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                 _vp], _i32),
     "dsa_quantize_fp8_rows": ([_vp, _i32, _vp, _vp, _i64, _i64, _vp], _i32),
     "dsa_attn_sink_fold": ([_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp], _i32),
     "dsa_attn_sink_grad": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp], _i32),

@@ -3,6 +3,8 @@
 //   I[s, t] = -inf                                                       (t invalid)
 // (relu(c x) = c relu(x) for the positive per-token scales, so the quantise-then-
 // dequantise product of the reference folds into the head weights and one key scale.)
+#include <mutex>
+
 #include "dsa_common.h"
 
 namespace dsa {
@@ -628,4 +630,67 @@ extern "C" int dsa_indexer_fwd_ws(const void* q, const float* q_scale, const voi
                                   int64_t cmp_ratio, void* workspace, int64_t workspace_bytes, void* stream) {
   return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim, ld_scores,
                           q_offset, cmp_ratio, workspace, workspace_bytes, stream);
+}
+
+// ----- the entry point that allocates nothing -----
+// Scratch of dsa_indexer_fwd_noalloc: the linear-split pieces of up to kNoAllocRows query rows,
+// in device memory that the code object carries (each GPU the library runs on holds its own
+// copy until the process ends).  Host code never passes `scratch` itself to a kernel: its
+// host-side name is not a device address.  The device address comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+static constexpr int64_t kNoAllocScratchBytes = 32ll << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace dsa {
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to (looked up on first use).
+int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(DSA_ERR_LAUNCH, "dsa_indexer_fwd_noalloc: cannot tell the stream's device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return set_error(DSA_ERR_LAUNCH, "dsa_indexer_fwd_noalloc: hipGetDevice");
+    if (cur != dev && hipSetDevice(dev) != hipSuccess)
+      return set_error(DSA_ERR_LAUNCH, "dsa_indexer_fwd_noalloc: hipSetDevice(%d)", dev);
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !p)
+      return set_error(DSA_ERR_LAUNCH, "dsa_indexer_fwd_noalloc: hipGetSymbolAddress(scratch): %s",
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DSA_OK;
+}
+}  // namespace
+}  // namespace dsa
+
+extern "C" int64_t dsa_indexer_fwd_noalloc_max_rows(void) { return kNoAllocScratchBytes / dsa::kLinRowBytes; }
+
+extern "C" int dsa_indexer_fwd_noalloc(const void* q, const float* q_scale, const void* k, const float* k_scale,
+                                       const float* w, float* scores, int dtype, int64_t batch, int64_t s_q,
+                                       int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t ld_scores,
+                                       int64_t q_offset, int64_t cmp_ratio, void* stream) {
+  if (!dsa::lin_split_shape(dtype, n_heads, head_dim))  // no scratch on these shapes
+    return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim,
+                            ld_scores, q_offset, cmp_ratio, nullptr, 0, stream);
+  if (batch <= 0 || s_q <= 0) return dsa::set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd_noalloc: bad sizes");
+  const int64_t max_rows = dsa_indexer_fwd_noalloc_max_rows();
+  if (batch > max_rows || s_q > max_rows / batch)
+    return dsa::set_error(DSA_ERR_INVALID_ARG,
+                          "dsa_indexer_fwd_noalloc: %lld query rows exceed the static scratch (%lld rows of %lld "
+                          "bytes); split the rows over several calls or use dsa_indexer_fwd_ws",
+                          (long long)(batch * s_q), (long long)max_rows, (long long)dsa::kLinRowBytes);
+  void* ws = nullptr;
+  const int rc = dsa::noalloc_scratch((hipStream_t)stream, &ws);
+  if (rc != DSA_OK) return rc;
+  return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim, ld_scores,
+                          q_offset, cmp_ratio, ws, batch * s_q * dsa::kLinRowBytes, stream);
 }
