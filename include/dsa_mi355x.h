@@ -84,8 +84,13 @@ int dsa_indexer_fwd(const void* q, const float* q_scale, const void* k, const fl
  * workspace holds, per query row, four fp8 pieces of u = sum_h (w q_scale / 2)[h] q[h, :] and
  * their power-of-two scales, written by a pre-pass; the score kernel then takes
  *   sum_h c_h relu(x_h) = sum_h (c_h / 2) |x_h| + u . k
- * with u . k on the MFMA (half the VALU work of the relu form; the same scores to about
- * 1e-6 of the row's magnitude).  Other shapes ignore the workspace and run dsa_indexer_fwd.
+ * with u . k on the MFMA (half the VALU work of the relu form).  Other shapes ignore the
+ * workspace and run dsa_indexer_fwd.
+ * Precision (both forms, fp8): each score is within 1e-5 * k_scale * sum_h |w_h q_scale_h| (|q_h| . |k|)
+ * of the exact value on the dequantised operands (the fp32 rounding bound of the dot products
+ * and the head sum; measured <= 1.8e-6 of it at S = 4096 .. 131072 with signed head weights).
+ * Relative to max_t |score| a row whose head weights cancel can show larger deviations
+ * (about 9e-5 measured on early causal rows with N(0,1) weights).
  *   workspace        device scratch of at least dsa_indexer_fwd_workspace_size() bytes
  *                    (NULL: dsa_indexer_fwd's kernels)
  * dsa_indexer_fwd_workspace_size returns 0 where the split does not apply.

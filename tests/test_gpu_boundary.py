@@ -1,0 +1,148 @@
+"""The binding-level DeepSeek-V4 ops and the torch.library custom ops on the GPU.
+
+* npu_sparse_attn_sharedkv (out, softmax_lse) and npu_sparse_attn_sharedkv_grad (d_query,
+  d_ori_kv, d_cmp_kv, d_sinks) against the oracle's ``sparse_attn_sink`` and its fp64
+  autograd (bf16 2e-2; the LSE includes the sink), for ratio 4 with a given top-k and ratio
+  128 (every causal compressed block);
+* every dsa_mi355x custom op through ``torch.library.opcheck`` (schema, fake tensors,
+  autograd registration) on small inputs;
+* the absorb-mode attention custom op compiled with ``torch.compile(fullgraph=True)``
+  (aot_eager) gives the eager results, forward and gradients.
+"""
+
+import pytest
+import torch
+
+from oracle import dsa_oracle as O
+from tests.dsa_cases import attn_inputs, rand_indices, rel_err
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _v4_case(S, H, ratio, K, seed, D=512):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, S, H, D, generator=g).bfloat16()
+    ori = torch.randn(1, S, D, generator=g).bfloat16()
+    n_cmp = S // ratio
+    cmp = torch.randn(1, n_cmp, D, generator=g).bfloat16()
+    sink = torch.randn(H, generator=g)
+    idx = None
+    if ratio == 4:
+        idx = torch.full((1, S, K), -1, dtype=torch.int32)
+        for s in range(S):
+            nv = min(n_cmp, (s + 1) // ratio)
+            c = min(K, nv)
+            if c:
+                idx[0, s, :c] = torch.sort(torch.randperm(nv, generator=g)[:c]).values.int() + S
+    dout = torch.randn(1, S, H, D, generator=g).bfloat16()
+    return q, ori, cmp, sink, idx, dout
+
+
+@pytest.mark.parametrize("S,H,ratio,K", [(256, 16, 4, 32), (384, 32, 128, 0)])
+def test_sharedkv_binding_forward_and_grad(S, H, ratio, K):
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    q, ori, cmp, sink, idx, dout = _v4_case(S, H, ratio, K, seed=S + ratio)
+    scale = 512 ** -0.5
+    qd, od, cd, sd = q.to(DEV), ori.to(DEV).unsqueeze(2), cmp.to(DEV).unsqueeze(2), sink.to(DEV)
+    cidx = None if idx is None else idx.to(DEV).unsqueeze(2)
+    meta = ops.npu_sparse_attn_sharedkv_metadata(None, None, None, None, None, H, 1, 512, 1, S, S, 0, K, ratio, 4, 3,
+                                                 127, 0, "BSND", "BSND", True, True, device=DEV)
+    out, lse = ops.npu_sparse_attn_sharedkv(qd, od, cd, None, cidx, sinks=sd, metadata=meta, softmax_scale=scale,
+                                            cmp_ratio=ratio)
+    assert out.shape == q.shape and out.dtype == q.dtype and lse.shape == (1, S, H, 1) and lse.dtype == torch.float32
+    dq, d_ori, d_cmp, d_sink = ops.npu_sparse_attn_sharedkv_grad(qd, od, cd, dout.to(DEV), out, lse, None, cidx,
+                                                                 sinks=sd, scale_value=scale, cmp_ratio=ratio)
+    torch.cuda.synchronize()
+    assert d_ori.shape == od.shape and d_cmp.shape == cd.shape and d_sink.shape == sd.shape
+    assert dq.dtype == q.dtype and d_ori.dtype == ori.dtype and d_sink.dtype == sink.dtype
+    full_idx = O.v4_attn_indices(1, S, 128, ratio, S, cmp_idxs=idx)
+    oq = q.double().requires_grad_(True)
+    okv = torch.cat([ori, cmp], dim=1).double().requires_grad_(True)
+    osk = sink.double().requires_grad_(True)
+    ref, ref_lse = O.sparse_attn_sink(oq, okv, osk, full_idx, scale)
+    ref.backward(dout.double())
+    assert rel_err(out, ref.detach()) <= 2e-2
+    assert float((lse[..., 0].double().cpu() - ref_lse.detach()).abs().max()) <= 2e-2
+    assert rel_err(dq, oq.grad) <= 2e-2
+    assert rel_err(torch.cat([d_ori[:, :, 0], d_cmp[:, :, 0]], dim=1), okv.grad) <= 2e-2
+    assert rel_err(d_sink, osk.grad) <= 2e-2
+
+
+def _opcheck(op, args, kwargs=None):
+    torch.library.opcheck(op, args, kwargs or {},
+                          test_utils=("test_schema", "test_autograd_registration", "test_faketensor"))
+
+
+def test_custom_ops_opcheck():
+    from torchtitan_npu_simulator_amd import library  # noqa: F401
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    lib = torch.ops.dsa_mi355x
+    S, H, K = 64, 16, 24
+    q, kv, dout, scale = attn_inputs(S, H, seed=3)
+    idx = rand_indices(S, K, seed=3).to(DEV).unsqueeze(2)
+    qd, kvd = q.to(DEV), kv.to(DEV)
+    qn = qd[..., :512].contiguous().requires_grad_(True)
+    qp = qd[..., 512:].contiguous().requires_grad_(True)
+    kn = kvd[:, :, None, :512].contiguous().requires_grad_(True)
+    kp = kvd[:, :, None, 512:].contiguous().requires_grad_(True)
+    _opcheck(lib.npu_sparse_flash_attention, (qn, kn, kn, idx, qp, kp, scale, 3))
+    out, smax, ssum = lib.npu_sparse_flash_attention(qn, kn, kn, idx, qp, kp, scale, 3)
+    _opcheck(lib.npu_sparse_flash_attention_grad,
+             (qn.detach(), kn.detach(), qp.detach(), kp.detach(), idx, out.detach(), dout.to(DEV), smax, ssum, scale,
+              3))
+    g = torch.Generator().manual_seed(4)
+    qi = torch.randn(1, S, 64, 128, generator=g).bfloat16().to(DEV)
+    ki = torch.randn(1, S, 1, 128, generator=g).bfloat16().to(DEV)
+    w = (torch.rand(1, S, 64, generator=g) * 0.01).to(DEV)
+    _opcheck(lib.npu_lightning_indexer, (qi, ki, w), dict(sparse_count=K, return_value=True))
+    # fp8 operands: opcheck's schema mode cannot handle float8 tensors, so the fake
+    # implementation is compared with the real op directly
+    q8, qs = ops.quantize_fp8_per_row(qi)
+    k8, ks = ops.quantize_fp8_per_row(ki)
+    i8, v8 = lib.npu_lightning_indexer(q8, k8, w, sparse_count=K, return_value=True, query_scale=qs, key_scale=ks)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        fi, fv = lib.npu_lightning_indexer(q8, k8, w, sparse_count=K, return_value=True, query_scale=qs, key_scale=ks)
+    assert (fi.shape, fi.dtype, fv.shape, fv.dtype) == (i8.shape, i8.dtype, v8.shape, v8.dtype)
+    _opcheck(lib.npu_sparse_lightning_indexer_grad_kl_loss,
+             (qn.detach(), kn.detach(), qi, ki, w, idx, smax, ssum),
+             dict(query_rope=qp.detach(), key_rope=kp.detach(), scale_value=scale))
+    qv, ori, cmp, sink, cidx, _ = _v4_case(64, 16, 4, 8, seed=5)
+    args = (qv.to(DEV).requires_grad_(True), ori.to(DEV).unsqueeze(2).requires_grad_(True),
+            cmp.to(DEV).unsqueeze(2).requires_grad_(True), cidx.to(DEV).unsqueeze(2), sink.to(DEV).requires_grad_(True),
+            None, 512 ** -0.5, 4)
+    _opcheck(lib.npu_sparse_attn_sharedkv, args)
+
+
+def test_compiled_attention_matches_eager():
+    from torchtitan_npu_simulator_amd import library  # noqa: F401
+
+    S, H, K = 96, 16, 32
+    q, kv, dout, scale = attn_inputs(S, H, seed=7)
+    idx = rand_indices(S, K, seed=7).to(DEV).unsqueeze(2)
+    dout = dout.to(DEV)
+
+    def step(qn, qp, kn, kp):
+        out, _, _ = torch.ops.dsa_mi355x.npu_sparse_flash_attention(qn, kn, kn, idx, qp, kp, scale, 3)
+        return out
+
+    def leaves():
+        qd, kvd = q.to(DEV), kv.to(DEV)
+        return [qd[..., :512].contiguous().requires_grad_(True), qd[..., 512:].contiguous().requires_grad_(True),
+                kvd[:, :, None, :512].contiguous().requires_grad_(True),
+                kvd[:, :, None, 512:].contiguous().requires_grad_(True)]
+
+    eager_in = leaves()
+    eager = step(*eager_in)
+    eager.backward(dout)
+    comp_in = leaves()
+    compiled = torch.compile(step, backend="aot_eager", fullgraph=True)(*comp_in)
+    compiled.backward(dout)
+    torch.cuda.synchronize()
+    assert torch.equal(compiled, eager)
+    for a, b in zip(comp_in, eager_in):
+        assert rel_err(a.grad, b.grad) <= 1e-6

@@ -203,3 +203,8 @@ def test_lightning_indexer_op_end_to_end():
     scores = ops.indexer_scores(q.to(DEV), k.to(DEV), w.to(DEV)).cpu()
     assert idx.shape == (1, S, 1, K)
     assert torch.equal(idx[:, :, 0].cpu(), _oracle_topk(scores, K))
+    # sparse_values in the query's dtype, as the binding allocates them (binding.cpp:29)
+    assert vals.shape == (1, S, 1, K) and vals.dtype == torch.bfloat16
+    sel = idx[:, :, 0].cpu()
+    ref_vals = torch.gather(scores, -1, sel.clamp_min(0).long()).masked_fill(sel < 0, float("-inf"))
+    assert torch.equal(vals[:, :, 0].cpu(), ref_vals.to(torch.bfloat16))

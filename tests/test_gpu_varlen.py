@@ -81,7 +81,8 @@ def test_indexer_varlen_equals_per_sequence(fp8):
                                                  query_scale=None if qs is None else qs[a:b].unsqueeze(0),
                                                  key_scale=None if ks is None else ks[a:b].unsqueeze(0))
         assert torch.equal(idx[a:b].cpu(), ref_i[0, :, 0].cpu()), f"sequence {i}"
-        assert torch.equal(vals[a:b].cpu(), ref_v[0, :, 0].cpu()), f"sequence {i}"
+        # the op returns sparse_values in the query's dtype (bf16 for fp8 queries)
+        assert torch.equal(vals[a:b].to(ref_v.dtype).cpu(), ref_v[0, :, 0].cpu()), f"sequence {i}"
         # the oracle's selection on the same fp32 scores
         sc = ops.indexer_scores(qi[a:b].unsqueeze(0), ki[a:b].unsqueeze(0), w[a:b].unsqueeze(0),
                                 q_scale=None if qs is None else qs[a:b].unsqueeze(0),
@@ -230,6 +231,9 @@ def test_indexer_kl_tnd_equals_per_sequence():
     qd, kvd, idd = q.to(DEV), kv.to(DEV), idx.to(DEV)
     cu = _cu(lens)
     _, smax, ssum = ops.sparse_mla_fwd_varlen(qd, kvd, idd, scale, cu, cu)
+    # fp32 index operands (bf16 values): the op then returns fp32 gradients, compared below
+    # bit for bit across the two layouts
+    qi, ki = qi.float(), ki.float()
     dq_i, dk_i, dw, loss = ops.npu_sparse_lightning_indexer_grad_kl_loss(
         qd[..., :512], kvd[:, None, :512], qi, ki, w, idd.unsqueeze(1), smax, ssum, scale,
         query_rope=qd[..., 512:], key_rope=kvd[:, None, 512:], layout="TND", actual_seq_qlen=cu[1:],

@@ -532,6 +532,12 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: sizes out of range");
   hipStream_t st = (hipStream_t)stream;
   const bool mfma_shape = head_dim == kD && n_heads % 16 == 0 && n_heads <= 128 && dtype != DSA_F32;
+  // the tile kernels address key rows of one batch with 32-bit byte offsets
+  const int64_t key_row_bytes = head_dim * (dtype == DSA_FP8_E4M3 ? 1 : 2);
+  if (mfma_shape && s_k > (int64_t)(0xffffffffu / key_row_bytes))
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_fwd: %lld keys exceed the tile kernels' 32-bit key offsets "
+                     "(at most %lld keys of %lld bytes)", (long long)s_k,
+                     (long long)(0xffffffffu / key_row_bytes), (long long)key_row_bytes);
   if (workspace && lin_split_shape(dtype, n_heads, head_dim)) {
     const int64_t rows = batch * s_q;
     if (workspace_bytes < rows * kLinRowBytes)

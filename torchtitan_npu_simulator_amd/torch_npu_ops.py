@@ -28,6 +28,7 @@ get no selection (-1) and keys past its key length are never candidates.
 from __future__ import annotations
 
 import math
+import warnings
 
 import torch
 
@@ -54,6 +55,10 @@ __all__ = [
     "indexer_kl_grad_from_mass_varlen",
     "to_cu_seqlens",
     "npu_sparse_attn_shared_kv",
+    "npu_sparse_attn_sharedkv_metadata",
+    "npu_sparse_attn_sharedkv",
+    "npu_sparse_attn_sharedkv_grad",
+    "SparseAttnSharedKV",
     "v4_attention_indices",
     "v4_indexer_kl_grad",
 ]
@@ -166,6 +171,12 @@ def topk_select(scores, k, *, q_offset=0, cmp_ratio=1, index_offset=0, return_va
     return idx, vals
 
 
+def _values_dtype(query: torch.Tensor) -> torch.dtype:
+    """dtype of sparse_values: the query's, as the binding allocates them (lightning_indexer/
+    binding.cpp:29); bf16 for this build's fp8 queries."""
+    return torch.bfloat16 if query.dtype == torch.float8_e4m3fn else query.dtype
+
+
 def npu_lightning_indexer(
     query,
     key,
@@ -195,9 +206,10 @@ def npu_lightning_indexer(
     query [B,S,H_I,D_I], key [B,S_k,1,D_I] (or [B,S_k,D_I]), weights [B,S,H_I]; bf16, or
     fp8-e4m3fn with ``query_scale`` [B,S,H_I] / ``key_scale`` [B,S_k] (this build's
     extension for the fp8 indexer).  Returns (sparse_indices int32 [B,S,1,K],
-    sparse_values fp32 [B,S,1,K] or None): the chosen key indices in ascending order with
-    -1 padding (reference binding shape: lightning_indexer/binding.cpp:28).  Rows are
-    processed in chunks so the fp32 score buffer stays under 1 GiB.
+    sparse_values [B,S,1,K] in the query's dtype (bf16 for fp8 queries; -inf in padded
+    slots) or None): the chosen key indices in ascending order with -1 padding (reference
+    binding shapes and dtypes: lightning_indexer/binding.cpp:27-29).  Rows are processed in
+    chunks so the fp32 score buffer stays under 1 GiB.
 
     TND: query [T,H_I,D_I], key [T_k,1,D_I], weights [T,H_I], scales [T,H_I] / [T_k];
     returns [T,1,K] with sequence-local indices (see ``lightning_indexer_varlen``).
@@ -214,11 +226,12 @@ def npu_lightning_indexer(
                                              cmp_ratio=cmp_ratio, cmp_residual_k=cmp_residual_k,
                                              return_value=return_value, query_scale=query_scale, key_scale=key_scale,
                                              index_offset=index_offset)
-        return idx.unsqueeze(1), (vals.unsqueeze(1) if return_value else None)
+        return idx.unsqueeze(1), (vals.to(_values_dtype(query)).unsqueeze(1) if return_value else None)
     if actual_seq_lengths_query is not None or actual_seq_lengths_key is not None:
-        return _bsnd_lengths_indexer(query, key, weights, actual_seq_lengths_query, actual_seq_lengths_key,
-                                     sparse_count, sparse_mode, cmp_ratio, return_value, query_scale, key_scale,
-                                     index_offset)
+        idx, vals = _bsnd_lengths_indexer(query, key, weights, actual_seq_lengths_query, actual_seq_lengths_key,
+                                          sparse_count, sparse_mode, cmp_ratio, return_value, query_scale, key_scale,
+                                          index_offset)
+        return idx, (vals.to(_values_dtype(query)) if return_value else None)
     k3 = key.squeeze(2) if key.dim() == 4 else key
     B, S, H, D = query.shape
     s_k = k3.shape[1]
@@ -241,7 +254,7 @@ def npu_lightning_indexer(
             idx[b, r0:r1] = i_b[0]
             if return_value:
                 vals[b, r0:r1] = v_b[0]
-    return idx.unsqueeze(2), (vals.unsqueeze(2) if return_value else None)
+    return idx.unsqueeze(2), (vals.to(_values_dtype(query)).unsqueeze(2) if return_value else None)
 
 
 def _bsnd_lengths_indexer(query, key, weights, len_q, len_k, sparse_count, sparse_mode, cmp_ratio, return_value,
@@ -685,41 +698,286 @@ def attn_sink_grad(out, dout, m2, s2, sinks):
     return dsink
 
 
-class _SparseAttnSharedKV(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, query, ori_kv, cmp_kv, sinks, idx, scale):
-        B, S, H, D = query.shape
-        kv = ori_kv if cmp_kv is None else torch.cat([ori_kv, cmp_kv], dim=1)
-        bf16 = query.dtype == torch.bfloat16
-        if bf16 and D > 512:
-            raise NotImplementedError(f"bf16 shared-KV attention needs head_dim <= 512 (got {D})")
-        # bf16: rows padded to the kernel's 576 = 512 value columns + 64 (zero) columns; k = v
-        # = the whole row.  fp32: the exact kernel takes any width.
-        dqk, dv = (576, 512) if bf16 else (D, D)
-        q_ext = _pad_rows(query, dqk)
-        kv_ext = _pad_rows(kv, dqk)
-        out, smax, ssum = sparse_mla_fwd(q_ext, kv_ext, idx, scale, d_v=dv, q_offset=_NO_MASK_OFFSET)
-        out, m2, s2 = attn_sink_fold_(out, smax, ssum, sinks)
-        ctx.save_for_backward(q_ext, kv_ext, idx, out, m2, s2, sinks)
-        ctx.scale = scale
-        ctx.meta = (D, dv, ori_kv.shape[1], cmp_kv is not None)
-        return out[..., :D] if dv != D else out
+_SHAREDKV_MAGIC = 0x44534B56  # "DSKV": first word of the metadata record
+_LAYOUT_CODES = {"BSND": 1, "TND": 2, "SBH": 3, "BSH": 4}
+
+
+def npu_sparse_attn_sharedkv_metadata(
+    cu_seqlens_q=None,
+    seqused_ori_kv=None,
+    seqused_cmp_kv=None,
+    seqused_q=None,
+    seqused_kv=None,
+    num_heads_q=1,
+    num_heads_kv=1,
+    head_dim=512,
+    batch_size=1,
+    max_seqlen_q=0,
+    max_seqlen_kv=0,
+    ori_topk=0,
+    cmp_topk=0,
+    cmp_ratio=1,
+    ori_mask_mode=4,
+    cmp_mask_mode=3,
+    ori_win_left=127,
+    ori_win_right=0,
+    layout_q="SBH",
+    layout_kv="SBH",
+    has_ori_kv=True,
+    has_cmp_kv=False,
+    *,
+    device=None,
+):
+    """Launch metadata of the shared-KV attention (reference binding
+    ``npu_sparse_attn_sharedkv_metadata``, ops/aclnn/sparse_attn_sharedkv/binding.cpp:12-28):
+    an int32 [1024] device tensor, as the binding returns.
+
+    Here the gathered-attention kernels schedule themselves from the shapes, so the record
+    only carries the problem description (magic, version, heads, head_dim, batch, sequence
+    lengths, top-k, ratio, mask modes, window, layout codes, which KV sets exist) for
+    ``npu_sparse_attn_sharedkv`` to check against its own arguments; the host copy of the
+    record rides on the tensor, so the check reads no device memory.
+    """
+    if num_heads_kv != 1:
+        raise NotImplementedError(f"num_heads_kv={num_heads_kv}: the shared KV has one head")
+    if ori_mask_mode != 4 or cmp_mask_mode != 3:
+        raise NotImplementedError("mask modes: band window (4) over ori_kv, causal (3) over cmp_kv")
+    for name, t in (("seqused_ori_kv", seqused_ori_kv), ("seqused_cmp_kv", seqused_cmp_kv),
+                    ("seqused_q", seqused_q), ("seqused_kv", seqused_kv)):
+        if t is not None and t.numel():
+            raise NotImplementedError(f"{name} (per-batch used lengths) is not supported")
+    if device is None:
+        device = cu_seqlens_q.device if cu_seqlens_q is not None else torch.device("cuda", torch.cuda.current_device())
+    rec = [_SHAREDKV_MAGIC, 1, int(num_heads_q), int(num_heads_kv), int(head_dim), int(batch_size),
+           int(max_seqlen_q), int(max_seqlen_kv), int(ori_topk), int(cmp_topk), int(cmp_ratio), int(ori_mask_mode),
+           int(cmp_mask_mode), int(ori_win_left), int(ori_win_right), _LAYOUT_CODES.get(str(layout_q), 0),
+           _LAYOUT_CODES.get(str(layout_kv), 0), int(bool(has_ori_kv)), int(bool(has_cmp_kv))]
+    meta = torch.zeros(1024, dtype=torch.int32)
+    meta[: len(rec)] = torch.tensor(rec, dtype=torch.int32)
+    meta = meta.to(device)
+    meta._dsa_record = tuple(rec)
+    return meta
+
+
+def _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, ori_win_right):
+    rec = getattr(metadata, "_dsa_record", None) if metadata is not None else None
+    if rec is None:
+        return
+    B, S, H, D = query.shape
+    want = dict(num_heads_q=(2, H), head_dim=(4, D), batch_size=(5, B), cmp_ratio=(10, cmp_ratio),
+                ori_win_left=(13, ori_win_left), ori_win_right=(14, ori_win_right), has_cmp_kv=(18, int(cmp_kv is not None)))
+    for name, (i, v) in want.items():
+        if rec[i] != int(v):
+            raise ValueError(f"metadata was built for {name}={rec[i]}, the call has {v}")
+
+
+def _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, cmp_ratio, ori_win_left, ori_win_right):
+    """Kernel operands of the shared-KV attention: query and cat(ori_kv, cmp_kv) rows as the
+    gathered-attention kernels take them (bf16: 576-column rows, the value columns first and
+    zeros after; fp32: as given) and the [B,S,W(+K)] slot indices over the concatenated rows."""
+    B, S, H, D = query.shape
+    ori = ori_kv.reshape(ori_kv.shape[0], ori_kv.shape[1], ori_kv.shape[-1])
+    cmp = None if cmp_kv is None else cmp_kv.reshape(cmp_kv.shape[0], cmp_kv.shape[1], cmp_kv.shape[-1])
+    if cmp_sparse_indices is not None and cmp_sparse_indices.dim() == 4:
+        cmp_sparse_indices = cmp_sparse_indices.squeeze(2)
+    n_cmp = 0 if cmp is None else cmp.shape[1]
+    idx = v4_attention_indices(B, S, query.device, win_left=int(ori_win_left), win_right=int(ori_win_right),
+                               cmp_ratio=int(cmp_ratio), n_cmp=n_cmp,
+                               cmp_indices=cmp_sparse_indices if cmp_ratio == 4 else None)
+    kv = ori if cmp is None else torch.cat([ori, cmp], dim=1)
+    bf16 = query.dtype == torch.bfloat16
+    if bf16 and D > 512:
+        raise NotImplementedError(f"bf16 shared-KV attention needs head_dim <= 512 (got {D})")
+    # bf16: rows padded to the kernel's 576 = 512 value columns + 64 (zero) columns; k = v
+    # = the whole row.  fp32: the exact kernel takes any width.
+    dqk, dv = (576, 512) if bf16 else (D, D)
+    return dict(q=_pad_rows(query, dqk), kv=_pad_rows(kv, dqk), idx=idx, D=D, dv=dv, s_ori=ori.shape[1],
+                has_cmp=cmp is not None)
+
+
+def _sharedkv_forward(prep, sinks, scale):
+    """(out [B,S,H,dv] with the sink folded in, m2, s2): the row statistics include the sink."""
+    out, smax, ssum = sparse_mla_fwd(prep["q"], prep["kv"], prep["idx"], scale, d_v=prep["dv"],
+                                     q_offset=_NO_MASK_OFFSET)
+    if sinks is not None:
+        out, smax, ssum = attn_sink_fold_(out, smax, ssum, sinks)
+    return out, smax, ssum
+
+
+def _sharedkv_backward(prep, out, dout, m2, s2, sinks, scale):
+    """(dq [B,S,H,D], d_ori [B,S_ori,D], d_cmp [B,S_c,D] or None, d_sink [H] or None), fp32 dKV."""
+    D, dv = prep["D"], prep["dv"]
+    dout = _pad_rows(dout.to(out.dtype), dv) if dv != D else dout.contiguous().to(out.dtype)
+    # P_j = exp(x_j - lse) with lse = m2 + log s2 includes the sink, and the kernel's
+    # delta = rowsum(dO * O) uses the sink-scaled O: dQ and dKV are exact
+    dq, dkv = sparse_mla_bwd(prep["q"], prep["kv"], prep["idx"], out, dout, m2, s2, scale, q_offset=_NO_MASK_OFFSET)
+    # the sink has no value: d sink = -sum over rows of p_sink * rowsum(dO o O)
+    dsink = attn_sink_grad(out, dout, m2, s2, sinks) if sinks is not None else None
+    dkv = dkv[..., :D]
+    s_ori = prep["s_ori"]
+    return dq[..., :D], dkv[:, :s_ori], (dkv[:, s_ori:] if prep["has_cmp"] else None), dsink
+
+
+def _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, block_tables, seq_tensors, ori_mask_mode,
+                         cmp_mask_mode):
+    if layout_q != "BSND" or layout_kv != "BSND":
+        raise NotImplementedError(f"layouts {layout_q}/{layout_kv}: BSND only (the reference's shared-KV wrapper "
+                                  "passes BSND and no cu_seqlens)")
+    if ori_sparse_indices is not None:
+        raise NotImplementedError("ori_sparse_indices: the window over ori_kv is the band of ori_mask_mode 4")
+    if any(t is not None for t in block_tables):
+        raise NotImplementedError("paged KV (block tables) is not supported")
+    if any(t is not None and t.numel() for t in seq_tensors):
+        raise NotImplementedError("cu_seqlens / seqused arguments need layout TND, which is not supported here")
+    if ori_mask_mode != 4 or cmp_mask_mode != 3:
+        raise NotImplementedError("mask modes: band window (4) over ori_kv, causal (3) over cmp_kv")
+
+
+def npu_sparse_attn_sharedkv(
+    query,
+    ori_kv=None,
+    cmp_kv=None,
+    ori_sparse_indices=None,
+    cmp_sparse_indices=None,
+    ori_block_table=None,
+    cmp_block_table=None,
+    cu_seqlens_q=None,
+    cu_seqlens_ori_kv=None,
+    cu_seqlens_cmp_kv=None,
+    seqused_q=None,
+    seqused_kv=None,
+    sinks=None,
+    metadata=None,
+    softmax_scale=1.0,
+    cmp_ratio=1,
+    ori_mask_mode=4,
+    cmp_mask_mode=3,
+    ori_kv_stride=0,
+    cmp_kv_stride=0,
+    ori_win_left=127,
+    ori_win_right=0,
+    layout_q="BSND",
+    layout_kv="BSND",
+    return_softmax_lse=True,
+):
+    """Shared-KV sparse attention forward (reference binding ``npu_sparse_attn_sharedkv``,
+    ops/aclnn/sparse_attn_sharedkv/binding.cpp:30-60; math of SparseAttention.forward,
+    models/deepseek_v4/model.py:573-623).
+
+    query [B,S,N,D]; ori_kv [B,S,1,D] (window keys, also the values); cmp_kv [B,S_c,1,D] or
+    None; cmp_sparse_indices [B,S,1,K] int32, the selected compressed rows offset by S as
+    LiCompute returns them (-1 empty; ratio 4 only, every causal block t < (s+1)//r
+    otherwise); sinks [N] fp32 (a per-head logit with no value) or None.  Each query sees
+    the ori tokens of its band [s - ori_win_left, s + ori_win_right] and its compressed rows.
+    Returns (attn_out like query, softmax_lse fp32 [B,S,N,1] = the natural-log logsumexp of
+    every logit of the row including the sink, or None without ``return_softmax_lse``).
+    Not differentiable by itself: ``npu_sparse_attn_sharedkv_grad`` is its backward.
+    """
+    _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, (ori_block_table, cmp_block_table),
+                         (cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, seqused_q, seqused_kv), ori_mask_mode,
+                         cmp_mask_mode)
+    if ori_kv is None:
+        raise NotImplementedError("ori_kv is required (the window keys)")
+    require_gpu_tensor(query, "query")
+    _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, ori_win_right)
+    prep = _sharedkv_prepare(query.contiguous(), ori_kv.contiguous(), cmp_kv, cmp_sparse_indices, int(cmp_ratio),
+                             ori_win_left, ori_win_right)
+    sk = None if sinks is None else sinks.float().contiguous()
+    out, m2, s2 = _sharedkv_forward(prep, sk, float(softmax_scale))
+    D = prep["D"]
+    out = out[..., :D].contiguous() if prep["dv"] != D else out
+    lse = (m2 + torch.log(s2)).unsqueeze(-1) if return_softmax_lse else None
+    return out, lse
+
+
+def npu_sparse_attn_sharedkv_grad(
+    query,
+    ori_kv,
+    cmp_kv=None,
+    d_out=None,
+    out=None,
+    lse=None,
+    ori_sparse_indices=None,
+    cmp_sparse_indices=None,
+    cu_seqlens_q=None,
+    cu_seqlens_ori_kv=None,
+    cu_seqlens_cmp_kv=None,
+    sinks=None,
+    scale_value=1.0,
+    cmp_ratio=1,
+    ori_mask_mode=4,
+    cmp_mask_mode=3,
+    ori_win_left=127,
+    ori_win_right=0,
+    layout="BSND",
+):
+    """Backward of ``npu_sparse_attn_sharedkv`` (reference binding
+    ``npu_sparse_attn_sharedkv_grad``, ops/aclnn/sparse_attn_sharedkv/binding.cpp:62-88): from
+    the forward's output and softmax_lse, returns (d_query like query, d_ori_kv like ori_kv,
+    d_cmp_kv like cmp_kv or None, d_sinks like sinks), allocated in the inputs' dtypes as the
+    binding does."""
+    _check_sharedkv_args(layout, layout, ori_sparse_indices, (), (cu_seqlens_q, cu_seqlens_ori_kv,
+                                                                 cu_seqlens_cmp_kv), ori_mask_mode, cmp_mask_mode)
+    if d_out is None or out is None or lse is None or sinks is None:
+        raise ValueError("d_out, out, lse and sinks are required")
+    prep = _sharedkv_prepare(query.contiguous(), ori_kv.contiguous(), cmp_kv, cmp_sparse_indices, int(cmp_ratio),
+                             ori_win_left, ori_win_right)
+    D, dv = prep["D"], prep["dv"]
+    o = _pad_rows(out.to(prep["q"].dtype), dv) if dv != D else out.contiguous().to(prep["q"].dtype)
+    m2 = lse.reshape(lse.shape[:3]).float().contiguous()
+    s2 = torch.ones_like(m2)
+    dq, d_ori, d_cmp, dsink = _sharedkv_backward(prep, o, d_out, m2, s2, sinks.float().contiguous(),
+                                                 float(scale_value))
+    d_ori = d_ori.reshape(ori_kv.shape).to(ori_kv.dtype)
+    d_cmp = None if d_cmp is None or cmp_ratio <= 1 else d_cmp.reshape(cmp_kv.shape).to(cmp_kv.dtype)
+    return dq.to(query.dtype), d_ori, d_cmp, dsink.reshape(sinks.shape).to(sinks.dtype)
+
+
+class SparseAttnSharedKV(torch.autograd.Function):
+    """The reference's autograd wrapper of the shared-KV op (converters/kernels/npu_smla.py:192-348),
+    same arguments and order: metadata, forward with the LSE saved, and the binding-level
+    gradient in backward (query, ori_kv, cmp_kv and sinks)."""
 
     @staticmethod
-    def backward(ctx, dout):
-        q_ext, kv_ext, idx, out, m2, s2, sinks = ctx.saved_tensors
-        D, dv, s_ori, has_cmp = ctx.meta
-        dout = _pad_rows(dout.to(out.dtype), dv) if dv != D else dout.contiguous().to(out.dtype)
-        # P_j = exp(x_j - lse) with lse = m2 + log s2 already includes the sink, and the
-        # kernel's delta = rowsum(dO * O) uses the sink-scaled O: dQ and dKV are exact
-        dq, dkv = sparse_mla_bwd(q_ext, kv_ext, idx, out, dout, m2, s2, ctx.scale, q_offset=_NO_MASK_OFFSET)
-        # the sink has no value: d sink = -sum over rows of p_sink * rowsum(dO o O)
-        dsink = attn_sink_grad(out, dout, m2, s2, sinks)
-        dq = dq[..., :D]
-        dkv = dkv[..., :D].to(kv_ext.dtype)
-        d_ori = dkv[:, :s_ori]
-        d_cmp = dkv[:, s_ori:] if has_cmp else None
-        return dq, d_ori, d_cmp, dsink.to(sinks.dtype), None, None
+    def forward(ctx, query, ori_kv, cmp_kv, cu_seq_lens_q, cu_seq_lens_ori_kv, cu_seq_lens_cmp_kv, ori_sparse_indices,
+                cmp_sparse_indices, sinks, softmax_scale, cmp_ratio, ori_mask_mode, cmp_mask_mode, ori_win_left,
+                ori_win_right, num_heads_q, num_heads_kv, head_dim, batch_size, max_seq_len_q, max_seq_len_kv, topk,
+                layout_q, layout_kv):
+        _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, (),
+                             (cu_seq_lens_q, cu_seq_lens_ori_kv, cu_seq_lens_cmp_kv), ori_mask_mode, cmp_mask_mode)
+        metadata = npu_sparse_attn_sharedkv_metadata(
+            cu_seq_lens_q, None, None, None, None, num_heads_q, num_heads_kv, head_dim, batch_size, max_seq_len_q,
+            max_seq_len_kv, 0, topk, cmp_ratio, ori_mask_mode, cmp_mask_mode, ori_win_left, ori_win_right, layout_q,
+            layout_kv, ori_kv is not None, cmp_kv is not None, device=query.device)
+        _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, ori_win_right)
+        # the kernels' operands are kept for backward (the bf16 path pads query rows to 576)
+        prep = _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, int(cmp_ratio), ori_win_left,
+                                 ori_win_right)
+        sk = None if sinks is None else sinks.float().contiguous()
+        out, m2, s2 = _sharedkv_forward(prep, sk, float(softmax_scale))
+        ctx.prep = prep
+        ctx.save_for_backward(out, m2, s2, sk)
+        ctx.softmax_scale = float(softmax_scale)
+        ctx.in_dtypes = (ori_kv.dtype, None if cmp_kv is None else cmp_kv.dtype, None if sinks is None else sinks.dtype)
+        ctx.shapes = (ori_kv.shape, None if cmp_kv is None else cmp_kv.shape, None if sinks is None else sinks.shape)
+        ctx.cmp_ratio = int(cmp_ratio)
+        D = prep["D"]
+        return out[..., :D] if prep["dv"] != D else out
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        out, m2, s2, sk = ctx.saved_tensors
+        dq, d_ori, d_cmp, dsink = _sharedkv_backward(ctx.prep, out, grad_output, m2, s2, sk, ctx.softmax_scale)
+        ori_dt, cmp_dt, sink_dt = ctx.in_dtypes
+        ori_shape, cmp_shape, sink_shape = ctx.shapes
+        d_ori = d_ori.reshape(ori_shape).to(ori_dt)
+        if d_cmp is not None and ctx.cmp_ratio > 1:
+            d_cmp = d_cmp.reshape(cmp_shape).to(cmp_dt)
+        else:
+            d_cmp = None
+        ctx.prep = None
+        dsink = None if dsink is None else dsink.reshape(sink_shape).to(sink_dt)
+        return (dq, d_ori, d_cmp, *([None] * 5), dsink, *([None] * 15))
 
 
 def npu_sparse_attn_shared_kv(
@@ -736,7 +994,7 @@ def npu_sparse_attn_shared_kv(
     ori_win_right=0,
 ):
     """DeepSeek-V4 shared-KV sparse attention (reference npu_sparse_attn_shared_kv,
-    converters/kernels/npu_smla.py:351-400; math of SparseAttention.forward,
+    converters/kernels/npu_smla.py:351-402; math of SparseAttention.forward,
     models/deepseek_v4/model.py:573-623).
 
     query [B,S,H,D], ori_kv [B,S,D] (window keys), cmp_kv [B,S/r,D] or None (compressed
@@ -744,27 +1002,30 @@ def npu_sparse_attn_shared_kv(
     ratio 4) or None (every causal block), sinks [H] fp32.  Keys and values are the same
     rows (k = v).  Each query sees the ori tokens of its band [s - ori_win_left,
     s + ori_win_right] and the selected compressed rows; the softmax also includes the
-    head's sink logit, which carries no value.  Returns [B,S,H,D], differentiable in
-    query, ori_kv, cmp_kv and sinks.  bf16 rows need D <= 512 (MFMA path); fp32 rows any D.
+    head's sink logit, which carries no value.  Returns [B,S,H,D] (contiguous),
+    differentiable in query, ori_kv, cmp_kv and sinks through ``SparseAttnSharedKV``.
+    bf16 rows need D <= 512 (MFMA path); fp32 rows any D.
     """
-    if ori_mask_mode != 4 or cmp_mask_mode != 3:
-        raise NotImplementedError("mask modes: band window (4) over ori_kv, causal (3) over cmp_kv")
-    for t, n in ((query, "query"), (ori_kv, "ori_kv")):
-        require_gpu_tensor(t, n)
-    B, S, H, D = query.shape
-    if ori_kv.dim() == 4:
-        ori_kv = ori_kv.squeeze(2)
-    if cmp_kv is not None and cmp_kv.dim() == 4:
-        cmp_kv = cmp_kv.squeeze(2)
-    if cmp_sparse_indices is not None and cmp_sparse_indices.dim() == 4:
-        cmp_sparse_indices = cmp_sparse_indices.squeeze(2)
-    n_cmp = 0 if cmp_kv is None else cmp_kv.shape[1]
-    cmp_idx = cmp_sparse_indices if cmp_ratio == 4 else None
-    idx = v4_attention_indices(B, S, query.device, win_left=int(ori_win_left), win_right=int(ori_win_right),
-                               cmp_ratio=int(cmp_ratio), n_cmp=n_cmp, cmp_indices=cmp_idx)
-    return _SparseAttnSharedKV.apply(query.contiguous(), ori_kv.contiguous(),
-                                     None if cmp_kv is None else cmp_kv.contiguous(), sinks.float(), idx,
-                                     float(softmax_scale))
+    batch_size, max_seq_len_q, num_heads_q, head_dim = query.size()
+    max_seq_len_kv = ori_kv.size(1)
+    topk = 0 if cmp_ratio != 4 else cmp_sparse_indices.size(-1)
+    layout_q = layout_kv = "BSND"
+    query = query.contiguous()
+    ori_kv = (ori_kv if ori_kv.dim() == 4 else ori_kv.unsqueeze(2)).contiguous()  # [B,S,1,D]
+    if cmp_kv is not None:
+        cmp_kv = (cmp_kv if cmp_kv.dim() == 4 else cmp_kv.unsqueeze(2)).contiguous()
+    if cmp_ratio == 4:
+        cmp_sparse_indices = cmp_sparse_indices.to(torch.int32)
+        if cmp_sparse_indices.dim() == 3:
+            cmp_sparse_indices = cmp_sparse_indices.unsqueeze(2)
+        cmp_sparse_indices = cmp_sparse_indices.contiguous()
+    else:
+        cmp_sparse_indices = None
+    out = SparseAttnSharedKV.apply(query, ori_kv, cmp_kv, None, None, None, None, cmp_sparse_indices, sinks,
+                                   float(softmax_scale), int(cmp_ratio), ori_mask_mode, cmp_mask_mode, ori_win_left,
+                                   ori_win_right, num_heads_q, 1, head_dim, batch_size, max_seq_len_q,
+                                   max_seq_len_kv, topk, layout_q, layout_kv)
+    return out.contiguous()
 
 
 def v4_indexer_kl_grad(q, kv, kv_compress, attn_sink, q_indexer, k_indexer, weights, compress_topk_idxs, offset,
@@ -821,6 +1082,7 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     pre_tokens=65536,
     next_tokens=65536,
     deterministic=False,
+    cmp_ratio=1,
     q_offset=None,
     loss_scale=1.0,
     eps=1e-8,
@@ -828,15 +1090,27 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     cu_seqlens_q=None,
     cu_seqlens_k=None,
 ):
-    """(d_query_index fp32, d_key_index fp32, d_weights fp32, loss fp32[1]) of the indexer KL loss.
+    """(d_query_index, d_key_index, d_weights, loss fp32[1]) of the indexer KL loss, the
+    gradients in the dtypes of query_index / key_index / weight as the binding allocates them
+    (sparse_lightning_indexer_grad_kl_loss/binding.cpp:26-29).
 
     The main-attention target mass is recomputed from (query || query_rope, key ||
     key_rope, softmax_max, softmax_sum) at the selected keys; ``loss`` is the token SUM
-    (the caller divides by B*S, reference dsa.py:73).
+    (the caller divides by B*S, reference dsa.py:73).  ``cmp_ratio`` > 1: key / key_index
+    are compressed rows (binding.cpp:17) and sparse_indices come from the indexer's
+    compressed rule t < (s+1)//r, so the -1 slots carry the validity and no causal test is
+    applied on top.  ``deterministic``: d_key_index sums each key's contributions in
+    fp32 in an order that can change from run to run (a key-major list built with atomics,
+    and fp32 atomic adds for keys whose list straddles two reduction segments), so results
+    are reproducible to fp32 rounding, not bit for bit; ``deterministic=True`` warns once that
+    this build does not offer the bitwise mode.
     """
+    if deterministic:
+        _warn_nondeterministic()
+    out_dtypes = (query_index.dtype, key_index.dtype, weight.dtype)
     if layout == "TND":
-        if sparse_mode != 3 or q_offset is not None:
-            raise NotImplementedError("TND runs the per-sequence causal rule (sparse_mode=3) only")
+        if sparse_mode != 3 or q_offset is not None or int(cmp_ratio) != 1:
+            raise NotImplementedError("TND runs the per-sequence causal rule (sparse_mode=3, cmp_ratio=1) only")
         q = _cat_last(query, query_rope) if query_rope is not None else query.contiguous()
         kv = _cat_last(key, key_rope) if key_rope is not None else key.contiguous()
         kv2 = kv.reshape(kv.shape[0], kv.shape[-1])
@@ -847,7 +1121,8 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
         dq_i, dk_i, dw, loss_rows = indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, idx, mass, cu_q,
                                                                      cu_k, loss_scale=loss_scale, eps=eps,
                                                                      grad_scale=grad_scale)
-        return dq_i, dk_i.reshape(key_index.shape), dw, loss_rows.sum().reshape(1)
+        return (dq_i.to(out_dtypes[0]), dk_i.reshape(key_index.shape).to(out_dtypes[1]), dw.to(out_dtypes[2]),
+                loss_rows.sum().reshape(1))
     if layout != "BSND":
         raise NotImplementedError(f"layout {layout} (BSND or TND)")
     if actual_seq_qlen is not None or actual_seq_klen is not None:
@@ -857,13 +1132,28 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     B, S, H, D = q.shape
     kv3 = kv.reshape(B, kv.shape[1], D)
     s_kv = kv3.shape[1]
-    q_off = _resolve_q_offset(sparse_mode, S, s_kv, q_offset)
+    if int(cmp_ratio) > 1:
+        q_off = _NO_MASK_OFFSET if q_offset is None else int(q_offset)
+    else:
+        q_off = _resolve_q_offset(sparse_mode, S, s_kv, q_offset)
     idx = sparse_indices.reshape(B, S, -1).to(torch.int32).contiguous()
-    K = idx.shape[-1]
     mass = attn_mass(q, kv3, idx, softmax_max, softmax_sum, scale_value, q_offset=q_off)
     dq_i, dk_i, dw, loss_rows = indexer_kl_grad_from_mass(query_index, key_index, weight, idx, mass, q_offset=q_off,
                                                           loss_scale=loss_scale, eps=eps, grad_scale=grad_scale)
-    return dq_i, dk_i.reshape(key_index.shape), dw, loss_rows.sum().reshape(1)
+    return (dq_i.to(out_dtypes[0]), dk_i.reshape(key_index.shape).to(out_dtypes[1]), dw.to(out_dtypes[2]),
+            loss_rows.sum().reshape(1))
+
+
+_warned_nondeterministic = False
+
+
+def _warn_nondeterministic():
+    global _warned_nondeterministic
+    if not _warned_nondeterministic:
+        _warned_nondeterministic = True
+        warnings.warn("npu_sparse_lightning_indexer_grad_kl_loss(deterministic=True): d_key_index is reproducible "
+                      "to fp32 rounding only (per-key sums in a run-dependent order); there is no bitwise mode",
+                      stacklevel=3)
 
 
 def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, q_offset=0, loss_scale=1.0, eps=1e-8,
