@@ -445,6 +445,27 @@ def kernel_rooflines(inp, ops, torch, dev, S, K, seed, with_topk):
                              achieved=nbytes / (ms * 1e-3) / 1e9, peak=HBM_PEAK_GBPS, unit="GB/s",
                              frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS)
     del comp
+    # the indexer input producer at the C3 indexer shape: RoPE (V3.2 layout) + Hadamard +
+    # fp8 of q_I [1,S,64,128] and k_I [1,S,128]; per 128-feature row 256 B read, 256 B bf16
+    # + 128 B fp8 + 4 B scale written
+    g = torch.Generator(device=dev).manual_seed(seed + 3)
+    qi = torch.randn(1, S, 64, 128, device=dev, dtype=torch.bfloat16, generator=g)
+    ki = torch.randn(1, S, 128, device=dev, dtype=torch.bfloat16, generator=g)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, 64, 2, dtype=torch.float64) / 64))
+    ang = torch.outer(torch.arange(S, dtype=torch.float64), inv)
+    fc = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(dev)
+
+    def run_prep():
+        ops.indexer_prep(qi, fc)
+        ops.indexer_prep(ki, fc)
+
+    ms = time_ms(torch, run_prep)
+    nbytes = S * 65 * (256 + 256 + 128 + 4)
+    out["indexer_prep"] = dict(kernel="indexer_prep_kernel (q_I and k_I launches)", bound="hbm",
+                               shape=f"S={S}: q_I [1,S,64,128] + k_I [1,S,128] bf16, RoPE + Hadamard + fp8",
+                               algorithmic_bytes=nbytes, avg_launch_ms=ms, achieved=nbytes / (ms * 1e-3) / 1e9,
+                               peak=HBM_PEAK_GBPS, unit="GB/s", frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS)
+    del qi, ki
     if with_topk:
         q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
         k8, ks = ops.quantize_fp8_per_row(inp["k_idx"])

@@ -33,6 +33,9 @@
  *   dsa_compressor_fwd           Compressor._forward_bsnd pooling + RMSNorm
  *                                (models/deepseek_v4/model.py:183-221; torch-only in the reference)
  *   dsa_compressor_fwd_tnd       Compressor._forward_tnd (models/deepseek_v4/model.py:223-274)
+ *   dsa_indexer_prep             the indexer's RoPE + rotate_activation (+ this build's fp8 quantisation)
+ *                                (models/deepseek_v32/model.py:196-221, :264-282;
+ *                                 models/deepseek_v4/model.py:343-357; torch-only in the reference)
  *   dsa_*_varlen                 the A5 packed-varlen ("TND") ops taking cu_seqlens_q / cu_seqlens_k:
  *                                lightning_indexer (converters/kernels/npu_smla.py:754-768),
  *                                sparse_flash_mla{,_grad} (:457-479, :540-568),
@@ -213,10 +216,37 @@ int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, co
  *   kv, score [B, S, coff*D] fp32 (coff = 2 with overlap, else 1); ape [ratio, coff*D] fp32
  *   out [B, S/ratio, D]: fp32 pooled values, or, with norm_weight != NULL,
  *   RMSNorm(bf16(pooled)) * norm_weight written as bf16 (out_dtype selects f32/bf16 output).
+ * RoPE epilogue (model.py:218-220), with rope_cs != NULL: the last rope_dim features of the
+ * stored row (bf16-rounded first when out is bf16) are rotated in interleaved pairs
+ * (2i, 2i+1) by cs[pos][i] = (cos, sin), rope_cs fp32 [n_pos, rope_dim/2, 2] (torch's
+ * view_as_real of freqs_cis), pos = the block's first token position: positions[b*S + c*ratio]
+ * (int32 [B*S]) or c*ratio when positions is NULL; rows at positions outside the table are
+ * not rotated.  rope_dim a multiple of 4, <= D.
  */
 int dsa_compressor_fwd(const float* kv, const float* score, const float* ape, const float* norm_weight, void* out,
                        int out_dtype, int64_t batch, int64_t s, int64_t d, int64_t ratio, int overlap,
-                       float norm_eps, void* stream);
+                       float norm_eps, const float* rope_cs, int64_t n_pos, int64_t rope_dim,
+                       const int32_t* positions, void* stream);
+
+/*
+ * Indexer input producer (reference: Indexer.forward, models/deepseek_v32/model.py:264-282 with
+ * rotate_activation :196-221; models/deepseek_v4/model.py:343-357): per row of D = 128 bf16
+ * features (x [rows, heads, 128], one row per query head or key),
+ *   1. RoPE of features [rope_start, rope_start + rope_dim) in fp32, rounded to bf16: pairs
+ *      (rope_start + 2i, +1) when interleaved (V4), (rope_start + i, rope_start + i + rope_dim/2)
+ *      otherwise (V3.2's blocked layout), rotated by cs[pos][i]; rope_cs fp32
+ *      [n_pos, rope_dim/2, 2]; pos = positions[row] (int32 [rows]) or
+ *      pos_offset + row % seq_len; rows at positions outside the table are not rotated;
+ *      rope_dim = 0 skips the step;
+ *   2. with hadamard != 0: y = bf16(bf16(H x) * 128^-0.5), H the Sylvester Hadamard matrix;
+ *   3. y written as bf16 [rows, heads, 128] (y != NULL) and/or its fp8-e4m3fn per-row
+ *      quantisation q8 [rows, heads, 128] with scale [rows, heads] fp32 (the rule of
+ *      dsa_quantize_fp8_rows).
+ */
+int dsa_indexer_prep(const void* x, void* y, uint8_t* q8, float* scale, int64_t rows, int64_t heads, int64_t d,
+                     int64_t seq_len, const float* rope_cs, int64_t n_pos, const int32_t* positions,
+                     int64_t pos_offset, int64_t rope_dim, int64_t rope_start, int interleaved, int hadamard,
+                     void* stream);
 
 /*
  * Per-row fp8-e4m3fn quantisation of indexer operands (q_I rows [.., H_I, D_I], k_I rows).
@@ -250,12 +280,13 @@ int dsa_attn_sink_grad(const void* out, const void* dout, const float* softmax_m
  * that range yields a zero row); with overlap its first ratio slots are the previous listed
  * block's first D features when c > 0 and positions[block_starts[c]] >= ratio (device int32
  * [n_tokens] request-local positions).
- *   kv, score [n_tokens, coff*D] fp32; out [n_blocks, D] as in dsa_compressor_fwd.
+ *   kv, score [n_tokens, coff*D] fp32; out [n_blocks, D] as in dsa_compressor_fwd; the RoPE
+ *   epilogue rotates block c at positions[block_starts[c]] (model.py:266-273).
  */
 int dsa_compressor_fwd_tnd(const float* kv, const float* score, const float* ape, const float* norm_weight,
                            void* out, int out_dtype, int64_t n_tokens, int64_t d, int64_t ratio, int overlap,
                            const int64_t* block_starts, int64_t n_blocks, const int32_t* positions, float norm_eps,
-                           void* stream);
+                           const float* rope_cs, int64_t n_pos, int64_t rope_dim, void* stream);
 
 /*
  * Packed varlen ("TND") batches.  n_seq sequences are packed along the token axis:

@@ -49,6 +49,24 @@ follows (paths relative to the reference repository root):
                            models/deepseek_v4/tnd.py:32-38, :87-94
 * ``varlen_split``         per-sequence slices of a packed (TND) batch; the
                            varlen reference result is the per-sequence one
+* ``rope_rotate``          apply_rotary_emb: models/deepseek_v32/model.py:173-193
+                           (the indexer's non-interleaved layout viewed as interleaved
+                           pairs and back), models/deepseek_v4/model.py:45-87
+                           (interleaved); the complex product is torchtitan's
+                           apply_rotary_emb_single_complex (an absent third-party
+                           module: x as fp32 complex pairs times freqs_cis[pos], cast
+                           back to x's dtype), restated here in fp64
+* ``hadamard_rotate``      rotate_activation / hadamard_transform_ref,
+                           models/deepseek_v32/model.py:196-221 and
+                           models/deepseek_v4/model.py:90-111: F.linear with
+                           scipy.linalg.hadamard(D) in the input dtype, then times
+                           D^-0.5 in that dtype
+* ``indexer_prep``         Indexer.forward's q / k producer:
+                           models/deepseek_v32/model.py:264-282 (rope on the first
+                           64 features, non-interleaved, then rotate) and
+                           models/deepseek_v4/model.py:343-357 (rope on the last 64,
+                           interleaved, then rotate), followed by this build's fp8
+                           per-row quantisation (``quantize_e4m3_per_row``)
 
 Which check pins each function (tests/test_oracle.py):
 
@@ -78,6 +96,14 @@ Which check pins each function (tests/test_oracle.py):
   (the has_prev_block guard restarts the overlap at each request).
 * TND metadata: the known answers of the reference's
   tests/unit_tests/models/test_deepseek_v4_tnd.py:65-79.
+* rope_rotate: explicit per-pair loops (pair i = features (i, i + d/2) blocked,
+  (2i, 2i + 1) interleaved); position 0 is the identity; rotating by the table and
+  then by its conjugate restores the input; pair norms are preserved.
+* hadamard_rotate: in fp64 it is orthogonal and symmetric, so applying it twice
+  restores the input; the matrix is scipy.linalg.hadamard (entries +-1, H H = D I);
+  a one-hot input gives the corresponding column times D^-0.5.
+* indexer_prep: the composition of the two loops above with the reference's bf16
+  rounding points, and quantize_e4m3_per_row of its output.
 """
 
 from __future__ import annotations
@@ -112,6 +138,9 @@ __all__ = [
     "compressor_pool_tnd",
     "varlen_split",
     "quantize_e4m3_per_row",
+    "rope_rotate",
+    "hadamard_rotate",
+    "indexer_prep",
 ]
 
 
@@ -446,7 +475,8 @@ def indexer_kl_from_mass(q_idx, k_idx, weights, idx, mass, *, q_offset=0, loss_s
 # ---------------------------------------------------------------------------
 # a1: block KV compressor (V4)
 # ---------------------------------------------------------------------------
-def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, norm_eps=1e-6, out_dtype=None):
+def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, norm_eps=1e-6, out_dtype=None,
+                    freqs_cis=None, rope_dim=64, positions=None):
     """Softmax-gated pooling of token blocks (models/deepseek_v4/model.py:183-218).
 
     kv, score: [B,S,coff*D] fp32 (the wkv/wgate projections), ape [r,coff*D].
@@ -454,7 +484,9 @@ def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, no
     block's features D..2D and slots 0..r-1 the previous block's features 0..D;
     the first block's overlap slots are kv=0, score=-inf (overlap_transform,
     :174-181).  Returns the pooled [B,S/r,D] fp32, or, with ``norm_weight``,
-    RMSNorm(pooled.to(out_dtype)) (:218) in float32.
+    RMSNorm(pooled.to(out_dtype)) (:218) in float32.  With ``freqs_cis`` the last
+    ``rope_dim`` features of the (out_dtype-rounded) row are rotated at the block's first
+    position, positions[:, ::r] or c*r (:198-220), in fp64.
     """
     if overlap is None:
         overlap = ratio == 4
@@ -475,15 +507,22 @@ def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, no
         sc2[:, 1:, :ratio] = sc[:, :-1, :, :D]
         kvb, sc = kv2, sc2
     pooled = (kvb * sc.softmax(dim=2)).sum(dim=2)
-    if norm_weight is None:
+    if norm_weight is not None:
+        x = pooled.to(out_dtype or torch.float32).float()
+        rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm_eps)
+        pooled = x * rms * norm_weight.float()
+    if freqs_cis is None:
         return pooled
-    x = pooled.to(out_dtype or torch.float32).float()
-    rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm_eps)
-    return x * rms * norm_weight.float()
+    nb = pooled.shape[1]
+    cpos = positions[:, ::ratio] if positions is not None else torch.arange(nb).unsqueeze(0).expand(B, nb) * ratio
+    x = pooled.to(out_dtype or torch.float32)
+    rot = torch.stack([rope_rotate(x[b], freqs_cis, cpos[b], rope_dim=rope_dim, rope_start=D - rope_dim,
+                                   interleaved=True, out_dtype=torch.float64) for b in range(B)])
+    return rot
 
 
 def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions, *, overlap=None, norm_weight=None,
-                        norm_eps=1e-6, out_dtype=None):
+                        norm_eps=1e-6, out_dtype=None, freqs_cis=None, rope_dim=64):
     """Compressor._forward_tnd pooling (models/deepseek_v4/model.py:223-265).
 
     kv, score: [T,coff*D] fp32 projections of the packed tokens; block c pools tokens
@@ -515,11 +554,16 @@ def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions, *, overl
         sc2[:, :ratio] = torch.where(has_prev, sc2[:, :ratio], torch.full_like(sc2[:, :ratio], float("-inf")))
         kvb, sc = kv2, sc2
     pooled = (kvb * sc.softmax(dim=1)).sum(dim=1)
-    if norm_weight is None:
+    if norm_weight is not None:
+        x = pooled.to(out_dtype or torch.float32).float()
+        rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm_eps)
+        pooled = x * rms * norm_weight.float()
+    if freqs_cis is None:
         return pooled
-    x = pooled.to(out_dtype or torch.float32).float()
-    rms = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + norm_eps)
-    return x * rms * norm_weight.float()
+    # RoPE at each block's own position (:266-273)
+    x = pooled.to(out_dtype or torch.float32)
+    return rope_rotate(x, freqs_cis, positions.reshape(-1)[bs], rope_dim=rope_dim, rope_start=D - rope_dim,
+                       interleaved=True, out_dtype=torch.float64)
 
 
 def v4_attn_indices(bsz, seqlen, window_size, ratio, kv_len, cmp_idxs=None):
@@ -648,3 +692,71 @@ def seeded_inputs(S, H, *, B=1, d_qk=576, d_v=512, h_idx=64, d_idx=128, topk=204
     w = torch.rand(B, S, h_idx, generator=g) * (h_idx ** -0.5) * (d_idx ** -0.5)
     dout = torch.randn(B, S, H, d_v, generator=g)
     return dict(q=q.to(dtype), kv=kv.to(dtype), q_idx=q_idx.to(dtype), k_idx=k_idx.to(dtype), w=w, dout=dout.to(dtype))
+
+
+# ---------------------------------------------------------------------------
+# the indexer input producer: RoPE, Hadamard rotation, fp8
+# ---------------------------------------------------------------------------
+def rope_rotate(x, freqs_cis, positions, *, rope_dim=64, rope_start=0, interleaved=True, out_dtype=None):
+    """apply_rotary_emb on features [rope_start, rope_start + rope_dim) of x [N, ..., D]
+    (models/deepseek_v32/model.py:173-193; models/deepseek_v4/model.py:45-87).
+
+    Token n (the leading axis) is rotated by freqs_cis[positions[n]] (complex [n_pos,
+    rope_dim/2]).  Interleaved: complex pair i is features (2i, 2i+1).  Not interleaved (the
+    V3.2 indexer): the features are viewed as interleaved pairs first,
+    ``x.view(..., 2, -1).transpose(-1, -2)``, so pair i is (i, i + rope_dim/2), and the
+    result is put back with ``cat([y[..., 0::2], y[..., 1::2]])``.  The complex product
+    (torchtitan's apply_rotary_emb_single_complex) is computed exactly in fp64 and cast to
+    ``out_dtype`` (default: x's dtype), the reference's single rounding.
+    """
+    out_dtype = out_dtype or x.dtype
+    fc = freqs_cis if freqs_cis.is_complex() else torch.view_as_complex(freqs_cis.float().contiguous())
+    rot = fc.to(torch.complex128)[positions.long()]  # [N, rope_dim/2]
+    xr = x[..., rope_start: rope_start + rope_dim].to(torch.float64)
+    s = xr.shape
+    if not interleaved:
+        xr = xr.reshape(*s[:-1], 2, -1).transpose(-1, -2).reshape(*s)
+    c = torch.view_as_complex(xr.reshape(*s[:-1], -1, 2).contiguous())
+    shape = [rot.shape[0]] + [1] * (c.dim() - 2) + [rot.shape[1]]
+    y = torch.view_as_real(c * rot.reshape(shape)).reshape(*s)
+    if not interleaved:
+        y = torch.cat([y[..., 0::2], y[..., 1::2]], dim=-1)
+    out = x.to(torch.float64).clone()
+    out[..., rope_start: rope_start + rope_dim] = y
+    return out.to(out_dtype)
+
+
+def hadamard_rotate(x, *, out_dtype=None):
+    """rotate_activation (models/deepseek_v32/model.py:196-221; models/deepseek_v4/model.py:
+    90-111): ``F.linear(x, H) * D^-0.5`` with H = scipy.linalg.hadamard(D) in x's dtype.
+    The product is exact in fp64 and rounded to ``out_dtype`` (default x's dtype); the
+    scaling then runs in fp32 on the rounded values and is rounded again, as a bf16 tensor
+    times a Python float is in torch.  With out_dtype float64 nothing is rounded.
+    """
+    from scipy.linalg import hadamard
+
+    out_dtype = out_dtype or x.dtype
+    D = x.shape[-1]
+    H = torch.tensor(hadamard(D), dtype=torch.float64)
+    y = x.to(torch.float64) @ H.T
+    if out_dtype == torch.float64:
+        return y * D ** -0.5
+    y = y.to(out_dtype)
+    return (y.float() * np.float32(D ** -0.5)).to(out_dtype)
+
+
+def indexer_prep(x, freqs_cis, positions, *, rope_dim=64, rope_start=0, interleaved=False, hadamard=True,
+                 out_dtype=torch.bfloat16):
+    """The indexer's q / k producer: RoPE (skipped when freqs_cis is None) then
+    rotate_activation, with the reference's rounding points in ``out_dtype``; returns
+    (y, q8, scale) with (q8, scale) = quantize_e4m3_per_row(y).  x [N, ..., D] with token
+    positions [N].  V3.2: rope_start 0, not interleaved (models/deepseek_v32/model.py:
+    264-282); V4: rope_start D - 64, interleaved (models/deepseek_v4/model.py:343-357)."""
+    y = x
+    if freqs_cis is not None:
+        y = rope_rotate(y, freqs_cis, positions, rope_dim=rope_dim, rope_start=rope_start, interleaved=interleaved,
+                        out_dtype=out_dtype)
+    if hadamard:
+        y = hadamard_rotate(y.to(out_dtype) if out_dtype != torch.float64 else y, out_dtype=out_dtype)
+    q8, sc = quantize_e4m3_per_row(y.float())
+    return y, q8, sc

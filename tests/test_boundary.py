@@ -164,3 +164,17 @@ def test_custom_ops_fake_shapes_and_autograd_on_meta():
     o.sum().backward()
     assert Q.grad.shape == Q.shape and ori.grad.shape == ori.shape and cmp.grad.shape == cmp.shape
     assert sk.grad.shape == sk.shape
+
+
+def test_host_tensors_are_refused_before_any_launch():
+    """A host tensor handed to a kernel argument raises (the kernel would read a CPU address)."""
+    from torchtitan_npu_simulator_amd import DSAError
+    from torchtitan_npu_simulator_amd import _lib
+
+    assert _lib.ptr(None) is None
+    with pytest.raises(DSAError, match="passed to a GPU kernel"):
+        _lib.ptr(torch.zeros(4))
+    with pytest.raises(DSAError):
+        ops._rope_args(torch.polar(torch.ones(4, 32), torch.zeros(4, 32)), 64, torch.device("cpu"))[0].data_ptr() \
+            and _lib.ptr(ops._rope_args(torch.polar(torch.ones(4, 32), torch.zeros(4, 32)), 64,
+                                        torch.device("cpu"))[0])

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -57,11 +57,14 @@ _SIGNATURES = {
          _f32, _f32, _vp],
         _i32,
     ),
-    "dsa_compressor_fwd": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _f32, _vp], _i32),
+    "dsa_compressor_fwd": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _i64, _vp,
+                            _vp], _i32),
     "dsa_compressor_fwd_tnd": (
-        [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _f32, _vp],
+        [_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i32, _vp, _i64, _vp, _f32, _vp, _i64, _i64, _vp],
         _i32,
     ),
+    "dsa_indexer_prep": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _vp],
+                         _i32),
     # packed varlen: cu_seqlens / cmp_residual_k are host int32 arrays (ctypes arrays or None)
     "dsa_lightning_indexer_varlen": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -142,7 +145,13 @@ def host_i32(values) -> ctypes.Array | None:
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
+    """Device address of ``t`` for a kernel argument; a host tensor here would make the
+    kernel dereference a CPU address, so it is refused."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise DSAError(f"a {tuple(t.shape)} {t.dtype} tensor on {t.device} was passed to a GPU kernel")
+    return t.data_ptr()
 
 
 def stream_of(device: torch.device) -> int:

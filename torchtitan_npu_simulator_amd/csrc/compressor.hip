@@ -6,7 +6,13 @@
 //                   x = kv[b, (c-1)*r + i, f],     g = score[...] + ape[i, f]   (absent for c = 0)
 //                                       i >= r -> current block's features D..2D
 //                   x = kv[b, c*r + i-r, D + f],   g = score[...] + ape[i-r, D + f]
-// then optionally RMSNorm over f of the bf16-rounded pooled row times norm_weight.
+// then optionally RMSNorm over f of the bf16-rounded pooled row times norm_weight, and
+// optionally RoPE on the last rope_dim features (interleaved pairs (2i, 2i+1), angle i at
+// the block's position, in fp32 on the row as stored: bf16-rounded when the output is
+// bf16), as Compressor._forward_bsnd / _forward_tnd apply it after the norm.  The block's
+// position is that of its first token: c * ratio, or positions[first token] when token
+// positions are given (rows whose position falls outside the cos/sin table keep their
+// features).
 //
 // Packed varlen ("TND") batches give each block's first token explicitly (block_starts,
 // whole r-token blocks inside one request): block c pools tokens block_starts[c] + i, and
@@ -29,7 +35,8 @@ __global__ void __launch_bounds__(kThreads)
 compressor_kernel(const float* __restrict__ kv, const float* __restrict__ score, const float* __restrict__ ape,
                   const float* __restrict__ norm_w, void* __restrict__ out, int out_bf16, int64_t n_blocks_total,
                   int nb, int D, int r, int overlap, float eps, const int64_t* __restrict__ block_starts,
-                  const int32_t* __restrict__ positions, int64_t n_tokens) {
+                  const int32_t* __restrict__ positions, int64_t n_tokens, const float* __restrict__ rope_cs,
+                  int64_t n_pos, int rope_dim) {
   extern __shared__ float red[];  // [row groups][lanes_per_group / 64 + 1]
   const int lanes = D / 4;        // lanes per row group
   const int groups = kThreads / lanes;
@@ -127,6 +134,21 @@ compressor_kernel(const float* __restrict__ kv, const float* __restrict__ score,
     pooled[2] *= inv * w4.z;
     pooled[3] *= inv * w4.w;
   }
+  if (rope_cs && usable && f >= D - rope_dim) {
+    // RoPE of the stored row: this lane's features are the pairs (f, f+1), (f+2, f+3)
+    const int64_t pos = positions ? (int64_t)positions[cur] : (int64_t)c * r;
+    if (pos >= 0 && pos < n_pos) {
+      if (out_bf16)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pooled[u] = bf16_to_f(f_to_bf16(pooled[u]));
+      const float4 cs4 = *reinterpret_cast<const float4*>(rope_cs + pos * rope_dim + (f - (D - rope_dim)));
+      const float a0 = pooled[0], b0 = pooled[1], a1 = pooled[2], b1 = pooled[3];
+      pooled[0] = a0 * cs4.x - b0 * cs4.y;
+      pooled[1] = a0 * cs4.y + b0 * cs4.x;
+      pooled[2] = a1 * cs4.z - b1 * cs4.w;
+      pooled[3] = a1 * cs4.w + b1 * cs4.z;
+    }
+  }
   if (!active) return;
   const int64_t o = blk * (int64_t)D + f;
   if (out_bf16) {
@@ -143,11 +165,25 @@ compressor_kernel(const float* __restrict__ kv, const float* __restrict__ score,
 }  // namespace
 }  // namespace dsa
 
+namespace dsa {
+namespace {
+int check_rope(const char* what, const float* rope_cs, int64_t n_pos, int64_t rope_dim, int64_t d) {
+  if (!rope_cs) return DSA_OK;
+  if (rope_dim <= 0 || rope_dim % 4 != 0 || rope_dim > d || n_pos <= 0)
+    return set_error(DSA_ERR_INVALID_ARG, "%s: rope_dim=%lld with %lld positions (needs a multiple of 4 <= D)", what,
+                     (long long)rope_dim, (long long)n_pos);
+  return DSA_OK;
+}
+}  // namespace
+}  // namespace dsa
+
 extern "C" int dsa_compressor_fwd(const float* kv, const float* score, const float* ape, const float* norm_weight,
                                   void* out, int out_dtype, int64_t batch, int64_t s, int64_t d, int64_t ratio,
-                                  int overlap, float norm_eps, void* stream) {
+                                  int overlap, float norm_eps, const float* rope_cs, int64_t n_pos, int64_t rope_dim,
+                                  const int32_t* positions, void* stream) {
   using namespace dsa;
   if (!kv || !score || !ape || !out) return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd: null pointer");
+  if (int rc = check_rope("dsa_compressor_fwd", rope_cs, n_pos, rope_dim, d)) return rc;
   if (batch <= 0 || s <= 0 || d <= 0 || ratio <= 0)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd: bad sizes");
   if (s % ratio != 0)
@@ -168,17 +204,21 @@ extern "C" int dsa_compressor_fwd(const float* kv, const float* score, const flo
   const size_t shm = (size_t)groups * ((lanes + 63) / 64 + 1) * sizeof(float);
   compressor_kernel<<<(unsigned)grid, kThreads, shm, (hipStream_t)stream>>>(
       kv, score, ape, norm_weight, out, out_dtype == DSA_BF16, total, (int)nb, (int)d, (int)ratio, overlap ? 1 : 0,
-      norm_eps, nullptr, nullptr, batch * s);
+      norm_eps, nullptr, positions, batch * s, rope_cs, n_pos, (int)rope_dim);
   return check_launch("dsa_compressor_fwd");
 }
 
 extern "C" int dsa_compressor_fwd_tnd(const float* kv, const float* score, const float* ape,
                                       const float* norm_weight, void* out, int out_dtype, int64_t n_tokens, int64_t d,
                                       int64_t ratio, int overlap, const int64_t* block_starts, int64_t n_blocks,
-                                      const int32_t* positions, float norm_eps, void* stream) {
+                                      const int32_t* positions, float norm_eps, const float* rope_cs, int64_t n_pos,
+                                      int64_t rope_dim, void* stream) {
   using namespace dsa;
   if (!kv || !score || !ape || !out || (n_blocks > 0 && !block_starts))
     return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd_tnd: null pointer");
+  if (int rc = check_rope("dsa_compressor_fwd_tnd", rope_cs, n_pos, rope_dim, d)) return rc;
+  if (rope_cs && !positions)
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd_tnd: RoPE needs the token positions");
   if (overlap && !positions)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd_tnd: overlap needs the token positions");
   if (n_tokens <= 0 || d <= 0 || ratio <= 0 || n_blocks < 0)
@@ -197,6 +237,6 @@ extern "C" int dsa_compressor_fwd_tnd(const float* kv, const float* score, const
   const size_t shm = (size_t)groups * ((lanes + 63) / 64 + 1) * sizeof(float);
   compressor_kernel<<<(unsigned)grid, kThreads, shm, (hipStream_t)stream>>>(
       kv, score, ape, norm_weight, out, out_dtype == DSA_BF16, n_blocks, (int)n_blocks, (int)d, (int)ratio,
-      overlap ? 1 : 0, norm_eps, block_starts, positions, n_tokens);
+      overlap ? 1 : 0, norm_eps, block_starts, positions, n_tokens, rope_cs, n_pos, (int)rope_dim);
   return check_launch("dsa_compressor_fwd_tnd");
 }

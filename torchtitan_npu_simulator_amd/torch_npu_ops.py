@@ -48,6 +48,8 @@ __all__ = [
     "quantize_fp8_per_row",
     "compressor_pool",
     "compressor_pool_tnd",
+    "indexer_prep",
+    "rope_cos_sin",
     "lightning_indexer_varlen",
     "sparse_mla_fwd_varlen",
     "sparse_mla_bwd_varlen",
@@ -1222,13 +1224,78 @@ def indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, indices, ma
 # ---------------------------------------------------------------------------
 # block KV compressor (V4)
 # ---------------------------------------------------------------------------
-def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, norm_eps=1e-6, out_dtype=None):
+def rope_cos_sin(freqs_cis: torch.Tensor) -> torch.Tensor:
+    """The fp32 [n_pos, rope_dim/2, 2] (cos, sin) table the kernels take, from a complex
+    ``freqs_cis`` [n_pos, rope_dim/2] (torch.view_as_real), or an already-real table."""
+    t = torch.view_as_real(freqs_cis) if freqs_cis.is_complex() else freqs_cis
+    return t.float().contiguous()
+
+
+def _rope_args(freqs_cis, rope_dim, device):
+    if freqs_cis is None:
+        return None, 0, 0
+    cs = rope_cos_sin(freqs_cis).to(device)
+    if cs.shape[-2] * 2 != rope_dim:
+        raise ValueError(f"freqs_cis covers {cs.shape[-2] * 2} rope features, rope_dim is {rope_dim}")
+    return cs, cs.shape[0], rope_dim
+
+
+def indexer_prep(x, freqs_cis=None, *, positions=None, pos_offset=0, rope_dim=64, rope_start=0, interleaved=False,
+                 hadamard=True, fp8=True, return_bf16=True, layout="BSND"):
+    """Indexer input producer (dsa_indexer_prep): RoPE, the Hadamard ``rotate_activation`` and
+    the fp8-e4m3 per-row quantisation of query / key rows in one HIP pass.
+
+    x bf16: "BSND" [B,S,H,128] (queries) or [B,S,128] (keys); "TND" [T,H,128] or [T,128].
+    The RoPE position of token row r is ``positions`` (int [B,S] or [T]) or
+    ``pos_offset + s`` (BSND) / ``pos_offset + t`` (TND);
+    ``freqs_cis`` [n_pos, rope_dim/2] complex (or its real view) is the reference's rope
+    cache, None skips the RoPE.  V3.2 (models/deepseek_v32/model.py:264-282): rope_start 0,
+    interleaved False; V4 (models/deepseek_v4/model.py:343-357): rope_start 64, interleaved
+    True.  Returns (y bf16 like x or None, q8 float8_e4m3fn like x or None, scale fp32
+    x.shape[:-1] or None).
+    """
+    lib = load_library()
+    require_gpu_tensor(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("indexer_prep takes bf16 rows (the model dtype)")
+    if x.shape[-1] != 128:
+        raise ValueError(f"indexer_prep takes 128-feature rows (got {x.shape[-1]})")
+    x = x.contiguous()
+    if layout == "BSND" and x.dim() in (3, 4):
+        B, S = x.shape[:2]
+        rows, H, seq_len = B * S, (x.shape[2] if x.dim() == 4 else 1), S
+    elif layout == "TND" and x.dim() in (2, 3):
+        rows, H = x.shape[0], (x.shape[1] if x.dim() == 3 else 1)
+        seq_len = max(rows, 1)
+    else:
+        raise ValueError(f"indexer_prep: shape {tuple(x.shape)} does not fit layout {layout}")
+    cs, n_pos, rd = _rope_args(freqs_cis, rope_dim, x.device)
+    pos = None
+    if positions is not None and rd:
+        pos = positions.reshape(-1).to(device=x.device, dtype=torch.int32).contiguous()
+        if pos.numel() != rows:
+            raise ValueError(f"positions has {pos.numel()} entries for {rows} rows")
+    y = torch.empty_like(x) if return_bf16 else None
+    q8 = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device) if fp8 else None
+    sc = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device) if fp8 else None
+    if rows:
+        check(lib.dsa_indexer_prep(ptr(x), ptr(y), ptr(q8), ptr(sc), rows, H, 128, seq_len, ptr(cs), n_pos, ptr(pos),
+                                   int(pos_offset), rd, int(rope_start), int(bool(interleaved)), int(bool(hadamard)),
+                                   stream_of(x.device)), "dsa_indexer_prep")
+    return y, q8, sc
+
+
+def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, norm_eps=1e-6, out_dtype=None,
+                    freqs_cis=None, rope_dim=64, positions=None):
     """Softmax-gated pooling of ``ratio``-token blocks (dsa_compressor_fwd).
 
     kv, score [B,S,coff*D] fp32 (the wkv / wgate projections; coff = 2 with overlap, which
     defaults to ``ratio == 4`` as in the reference), ape [ratio, coff*D] fp32.  Returns
     [B,S/ratio,D]: the pooled fp32 rows, or with ``norm_weight`` the RMSNorm of the
-    bf16-rounded pooled rows times the weight, in ``out_dtype`` (default bf16).
+    bf16-rounded pooled rows times the weight, in ``out_dtype`` (default bf16).  With
+    ``freqs_cis`` the last ``rope_dim`` features are rotated (interleaved pairs) at each
+    block's first-token position, ``positions`` [B,S] or c*ratio
+    (Compressor._forward_bsnd, models/deepseek_v4/model.py:218-220).
     """
     lib = load_library()
     require_gpu_tensor(kv, "kv")
@@ -1244,22 +1311,31 @@ def compressor_pool(kv, score, ape, ratio, *, overlap=None, norm_weight=None, no
     ape = ape.float().contiguous()
     nw = None if norm_weight is None else norm_weight.float().contiguous()
     out = torch.empty(B, S // ratio, D, dtype=out_dtype, device=kv.device)
+    cs, n_pos, rd = _rope_args(freqs_cis, rope_dim, kv.device)
+    pos = None
+    if cs is not None and positions is not None:
+        pos = positions.reshape(-1).to(device=kv.device, dtype=torch.int32).contiguous()
+        if pos.numel() != B * S:
+            raise ValueError(f"positions has {pos.numel()} entries for {B * S} tokens")
     check(
         lib.dsa_compressor_fwd(ptr(kv), ptr(score), ptr(ape), ptr(nw), ptr(out), _lib.dtype_code(out_dtype), B, S, D,
-                               int(ratio), int(bool(overlap)), float(norm_eps), stream_of(kv.device)),
+                               int(ratio), int(bool(overlap)), float(norm_eps), ptr(cs), n_pos, rd, ptr(pos),
+                               stream_of(kv.device)),
         "dsa_compressor_fwd",
     )
     return out
 
 
 def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions=None, *, overlap=None, norm_weight=None,
-                        norm_eps=1e-6, out_dtype=None):
+                        norm_eps=1e-6, out_dtype=None, freqs_cis=None, rope_dim=64):
     """Softmax-gated pooling over a packed varlen batch (dsa_compressor_fwd_tnd;
     reference Compressor._forward_tnd, models/deepseek_v4/model.py:223-274).
 
     kv, score [T,coff*D] fp32; block_starts [n_blocks] (tnd.compressed_block_starts); with
     overlap, positions [T] (request-local) decide which blocks take the previous block's
-    first half.  Returns [n_blocks,D] like ``compressor_pool``.
+    first half.  Returns [n_blocks,D] like ``compressor_pool``; with ``freqs_cis`` the last
+    ``rope_dim`` features of block c are rotated at positions[block_starts[c]]
+    (models/deepseek_v4/model.py:266-273).
     """
     lib = load_library()
     require_gpu_tensor(kv, "kv")
@@ -1276,9 +1352,10 @@ def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions=None, *, 
     nw = None if norm_weight is None else norm_weight.float().contiguous()
     bs = block_starts.to(device=kv.device, dtype=torch.int64).contiguous()
     pos = None
-    if overlap:
+    cs, n_pos, rd = _rope_args(freqs_cis, rope_dim, kv.device)
+    if overlap or cs is not None:
         if positions is None:
-            raise ValueError("overlap pooling needs the token positions")
+            raise ValueError("overlap pooling and the RoPE epilogue need the token positions")
         pos = positions.reshape(-1).to(device=kv.device, dtype=torch.int32).contiguous()
         if pos.numel() != T:
             raise ValueError(f"positions has {pos.numel()} entries for {T} tokens")
@@ -1286,7 +1363,7 @@ def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions=None, *, 
     check(
         lib.dsa_compressor_fwd_tnd(ptr(kv), ptr(score), ptr(ape), ptr(nw), ptr(out), _lib.dtype_code(out_dtype), T, D,
                                    int(ratio), int(bool(overlap)), ptr(bs), bs.numel(), ptr(pos), float(norm_eps),
-                                   stream_of(kv.device)),
+                                   ptr(cs), n_pos, rd, stream_of(kv.device)),
         "dsa_compressor_fwd_tnd",
     )
     return out
