@@ -33,6 +33,7 @@
  *   dsa_compressor_fwd           Compressor._forward_bsnd pooling + RMSNorm
  *                                (models/deepseek_v4/model.py:183-221; torch-only in the reference)
  *   dsa_compressor_fwd_tnd       Compressor._forward_tnd (models/deepseek_v4/model.py:223-274)
+ *   dsa_tnd_metadata             build_smla_attention_masks (models/deepseek_v4/tnd.py:97-164) on the device
  *   dsa_indexer_prep             the indexer's RoPE + rotate_activation (+ this build's fp8 quantisation)
  *                                (models/deepseek_v32/model.py:196-221, :264-282;
  *                                 models/deepseek_v4/model.py:343-357; torch-only in the reference)
@@ -198,7 +199,9 @@ int dsa_attn_mass(const void* q, const void* kv, const int32_t* indices, const f
  *   q_idx [B,S,H_I,D_I] bf16, k_idx [B,S_k,D_I] bf16, w [B,S,H_I] fp32, mass [B,S,K] fp32
  *   dq_idx [B,S,H_I,D_I] fp32 (written), dk_idx_accum [B,S_k,D_I] fp32 (ACCUMULATED),
  *   dw [B,S,H_I] fp32 (written), loss_rows [B,S] fp32 (written; the op's loss is their sum)
- * grad_scale multiplies every gradient (the upstream gradient of the summed loss).
+ * grad_scale multiplies every gradient (the upstream gradient of the summed loss), times
+ * *grad_scale_dev when that device fp32 scalar is given (so a caller holding the upstream
+ * gradient on the device needs no host round trip; NULL = 1).
  * H_I = 64, D_I = 128 run on MFMA with a workspace of
  * dsa_indexer_kl_grad_workspace_size() bytes; other shapes use an exact fp32 kernel.
  */
@@ -208,7 +211,7 @@ int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, co
                         const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
                         void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q, int64_t s_k,
                         int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset, float loss_scale,
-                        float eps, float grad_scale, void* stream);
+                        float eps, float grad_scale, const float* grad_scale_dev, void* stream);
 
 /*
  * Block KV compressor (reference: Compressor._forward_bsnd + overlap_transform,
@@ -289,6 +292,23 @@ int dsa_compressor_fwd_tnd(const float* kv, const float* score, const float* ape
                            const float* rope_cs, int64_t n_pos, int64_t rope_dim, void* stream);
 
 /*
+ * Packed varlen ("TND") metadata built on the device (reference: build_smla_attention_masks,
+ * models/deepseek_v4/tnd.py:97-164, which reads its lengths back to the host with .item()).
+ * positions [n] int32 or int64 (pos_dtype_bytes 4 / 8), packed tokens in row-major order, -1
+ * for padding after the last valid token.  A request starts at every position 0 and at the
+ * first token; a ratio-r block starts at token t when positions[t] % r == 0 and the valid
+ * token t + r - 1 has position positions[t] + r - 1.  ratios: device int32 [n_ratios]
+ * (<= 4, each > 0).  Outputs, all device int32 (R = number of requests, known only on the
+ * device):
+ *   counts [4 + 2 n_ratios]: valid tokens, R, max request length, 1 if a valid token follows
+ *          padding (invalid input), then per ratio (blocks, max compressed length);
+ *   cu_q [n + 1] (entries 0..R), block_starts [n_ratios, n] (entries 0..blocks-1),
+ *   cu_cmp [n_ratios, n + 1] (entries 0..R), residual [n_ratios, n] (entries 0..R-1).
+ */
+int dsa_tnd_metadata(const void* positions, int pos_dtype_bytes, int64_t n, const int* ratios, int64_t n_ratios,
+                     int* counts, int* cu_q, int* block_starts, int* cu_cmp, int* residual, void* stream);
+
+/*
  * Packed varlen ("TND") batches.  n_seq sequences are packed along the token axis:
  * sequence i owns query tokens [cu_seqlens_q[i], cu_seqlens_q[i+1]) and key tokens
  * [cu_seqlens_k[i], cu_seqlens_k[i+1]) of the packed tensors (the fixed-length layouts above
@@ -340,7 +360,8 @@ int dsa_indexer_kl_grad_varlen(const void* q_idx, const void* k_idx, const float
                                const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
                                void* workspace, int64_t workspace_bytes, const int32_t* cu_seqlens_q,
                                const int32_t* cu_seqlens_k, int64_t n_seq, int64_t n_heads, int64_t head_dim,
-                               int64_t topk, float loss_scale, float eps, float grad_scale, void* stream);
+                               int64_t topk, float loss_scale, float eps, float grad_scale,
+                               const float* grad_scale_dev, void* stream);
 
 #ifdef __cplusplus
 }

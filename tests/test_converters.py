@@ -160,15 +160,19 @@ def test_dsa_forward_plumbing_and_loss_deferral():
     assert out.shape == (B, H, S, 512)
     assert float(loss) == 0.0  # deferred to backward
 
-    # backward runs the fused KL op, scales the grads by the upstream grad, logs loss/(B*S)
+    # backward runs the fused KL op with the upstream grad as its grad_scale (a tensor, so the
+    # op scales on the device without a host round trip) and logs loss/(B*S)
     def fake_kl(*a, **kw):
-        return torch.ones(B, S, HI, DI), torch.ones(B, S, 1, DI), torch.ones(B, S, HI), torch.tensor([8.0])
+        g = kw["grad_scale"]
+        seen["grad_scale"] = g
+        return torch.ones(B, S, HI, DI) * g, torch.ones(B, S, 1, DI) * g, torch.ones(B, S, HI) * g, torch.tensor([8.0])
 
     DSAIndexerLossLoggingHelper.tracker.clear()
     with patch.object(dsa_mod.npu, "npu_sparse_lightning_indexer_grad_kl_loss", side_effect=fake_kl):
         (loss * 3.0).backward()
     # d(loss/(B*S))/d(LILossTrain) = 1/(B*S), times 3
     torch.testing.assert_close(qi.grad, torch.full_like(qi, 3.0 / (B * S)))
+    assert isinstance(seen["grad_scale"], torch.Tensor)
     assert DSAIndexerLossLoggingHelper.tracker["values"][0].item() == pytest.approx(8.0 / (B * S))
 
 

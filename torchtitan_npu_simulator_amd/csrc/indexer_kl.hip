@@ -59,7 +59,8 @@ __global__ void __launch_bounds__(256, 2)
 indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restrict__ ki, const float* __restrict__ w,
                        const int32_t* __restrict__ idx, const float* __restrict__ mass, float* __restrict__ dq,
                        float* __restrict__ dw, float* __restrict__ loss_rows, uint16_t* __restrict__ ck, int S,
-                       int s_k, int K, int64_t q_offset, float loss_scale, float eps, float grad_scale, int row0) {
+                       int s_k, int K, int64_t q_offset, float loss_scale, float eps, float grad_scale,
+                       const float* __restrict__ grad_scale_dev, int row0) {
   __shared__ u32x4 kt[2][kTileC];           // gathered key rows [64][16 chunks], swizzled
   __shared__ float iv[kMaxK];               // I_j, then g_j
   __shared__ float ip[4][kB];               // per-wave partial I of one block
@@ -90,12 +91,15 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   float wr[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) wr[r] = w[row_id * kH + 16 * wave + 4 * g + r];
+  // the upstream gradient may live on the device (no host round trip for the caller)
+  float gsc = grad_scale_dev ? grad_scale * grad_scale_dev[0] : grad_scale;
   // these operands must have arrived before the first DMA: a wait for them inside the loop
   // would also wait for every row DMA in flight
 #pragma unroll
   for (int c = 0; c < kD / 32; ++c) asm volatile("" : "+v"(qa[c]));
 #pragma unroll
   for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(wr[r]));
+  asm volatile("" : "+v"(gsc));
 
   // Key-row gather, 64 rows x 256 B per block: 4 DMA instructions per wave, instruction
   // J = 4 wave + i covering tile chunks [64J, 64J+64) (row p / 16, chunk (p % 16) ^ swz8(row)).
@@ -215,7 +219,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const float lrow = block_reduce(lpart, red, false);
   const float T = block_reduce(tpos, red, false);
   if (tid == 0) loss_rows[row_id] = Z * lrow * loss_scale;
-  const float gs = valid_row ? Z * loss_scale * grad_scale : 0.f;
+  const float gs = valid_row ? Z * loss_scale * gsc : 0.f;
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
     const int j = tid + 256 * u;
@@ -379,7 +383,8 @@ indexer_kl_generic_kernel(const uint16_t* __restrict__ qi, const uint16_t* __res
                           const float* __restrict__ w, const int32_t* __restrict__ idx,
                           const float* __restrict__ mass, float* __restrict__ dq, float* __restrict__ dk,
                           float* __restrict__ dw, float* __restrict__ loss_rows, int S, int s_k, int H, int D, int K,
-                          int64_t q_offset, float loss_scale, float eps, float grad_scale) {
+                          int64_t q_offset, float loss_scale, float eps, float grad_scale,
+                          const float* __restrict__ grad_scale_dev) {
   extern __shared__ float sh[];  // iv[K]
   __shared__ float red[4];
   const int tok = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
@@ -427,7 +432,7 @@ indexer_kl_generic_kernel(const uint16_t* __restrict__ qi, const uint16_t* __res
   const float lrow = block_reduce(lpart, red, false);
   const float T = block_reduce(tpos, red, false);
   if (tid == 0) loss_rows[row_id] = Z * lrow * loss_scale;
-  const float gs = valid_row ? Z * loss_scale * grad_scale : 0.f;
+  const float gs = valid_row ? Z * loss_scale * (grad_scale_dev ? grad_scale * grad_scale_dev[0] : grad_scale) : 0.f;
   __syncthreads();
   for (int j = tid; j < K; j += 256) {
     const bool ok = ok_slot(ridx[j], s_k, limit);
@@ -492,7 +497,8 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
                                    const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
                                    void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q, int64_t s_k,
                                    int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset,
-                                   float loss_scale, float eps, float grad_scale, void* stream) {
+                                   float loss_scale, float eps, float grad_scale, const float* grad_scale_dev,
+                                   void* stream) {
   using namespace dsa;
   if (!q_idx || !k_idx || !w || !indices || !mass || !dq_idx || !dk_idx_accum || !dw || !loss_rows)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: null pointer");
@@ -506,7 +512,8 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
     dim3 grid((unsigned)s_q, (unsigned)batch);
     indexer_kl_generic_kernel<<<grid, 256, topk * 4, st>>>(
         (const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass, dq_idx, dk_idx_accum, dw, loss_rows,
-        (int)s_q, (int)s_k, (int)n_heads, (int)head_dim, (int)topk, q_offset, loss_scale, eps, grad_scale);
+        (int)s_q, (int)s_k, (int)n_heads, (int)head_dim, (int)topk, q_offset, loss_scale, eps, grad_scale,
+        grad_scale_dev);
     return check_launch("dsa_indexer_kl_grad(generic)");
   }
   if (!workspace) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: workspace required");
@@ -527,7 +534,7 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
     dim3 grid((unsigned)rows_c, (unsigned)batch);
     indexer_kl_mfma_kernel<<<grid, 256, 0, st>>>((const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass,
                                                  dq_idx, dw, loss_rows, ck, (int)s_q, (int)s_k, (int)topk, q_offset,
-                                                 loss_scale, eps, grad_scale, (int)r0);
+                                                 loss_scale, eps, grad_scale, grad_scale_dev, (int)r0);
     if (int rc = check_launch("dsa_indexer_kl_grad(mfma)")) return rc;
     for (int b = 0; b < (int)batch; ++b)
       if (int rc = csr_reduce(indices, ck, dk_idx_accum, pairs, csr, (int)s_q, (int)s_k, (int)topk, q_offset, (int)r0,

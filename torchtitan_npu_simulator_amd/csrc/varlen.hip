@@ -209,7 +209,7 @@ extern "C" int dsa_indexer_kl_grad_varlen(const void* q_idx, const void* k_idx, 
                                           int64_t workspace_bytes, const int32_t* cu_seqlens_q,
                                           const int32_t* cu_seqlens_k, int64_t n_seq, int64_t n_heads,
                                           int64_t head_dim, int64_t topk, float loss_scale, float eps,
-                                          float grad_scale, void* stream) {
+                                          float grad_scale, const float* grad_scale_dev, void* stream) {
   using namespace dsa;
   const char* what = "dsa_indexer_kl_grad_varlen";
   if (int rc = check_seqs(cu_seqlens_q, cu_seqlens_k, n_seq, what)) return rc;
@@ -224,7 +224,8 @@ extern "C" int dsa_indexer_kl_grad_varlen(const void* q_idx, const void* k_idx, 
                                      at(indices, q0 * topk * 4), at(mass, q0 * topk * 4), at(dq_idx, q0 * hd * 4),
                                      at(dk_idx_accum, k0 * head_dim * 4), at(dw, q0 * n_heads * 4),
                                      at(loss_rows, q0 * 4), workspace, workspace_bytes, 1, lq, lk, n_heads, head_dim,
-                                     topk, token_offset(lq, lk), loss_scale, eps, grad_scale, stream))
+                                     topk, token_offset(lq, lk), loss_scale, eps, grad_scale, grad_scale_dev,
+                                     stream))
       return rc;
   }
   return DSA_OK;

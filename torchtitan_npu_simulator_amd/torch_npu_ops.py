@@ -1158,9 +1158,19 @@ def _warn_nondeterministic():
                       stacklevel=3)
 
 
+def _grad_scale_args(grad_scale, device):
+    """(host float, device fp32 scalar or None): a tensor upstream gradient stays on the device."""
+    if isinstance(grad_scale, torch.Tensor):
+        if grad_scale.numel() != 1:
+            raise ValueError("grad_scale must be a scalar")
+        return 1.0, grad_scale.detach().reshape(1).to(device=device, dtype=torch.float32)
+    return float(grad_scale), None
+
+
 def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, q_offset=0, loss_scale=1.0, eps=1e-8,
                               grad_scale=1.0):
-    """(dq_idx fp32, dk_idx fp32 [B,S_k,D_I], dw fp32, loss_rows fp32 [B,S]) given the target mass."""
+    """(dq_idx fp32, dk_idx fp32 [B,S_k,D_I], dw fp32, loss_rows fp32 [B,S]) given the target mass;
+    ``grad_scale`` (a float or a device scalar tensor) multiplies the gradients."""
     lib = load_library()
     ki = key_index.squeeze(2) if key_index.dim() == 4 else key_index
     qi = query_index.to(torch.bfloat16).contiguous()
@@ -1178,10 +1188,11 @@ def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, 
     loss_rows = torch.empty(B, S, dtype=torch.float32, device=dev)
     ws_bytes = int(lib.dsa_indexer_kl_grad_workspace_size(B, S, s_k, HI, DI, K))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    gsf, gsd = _grad_scale_args(grad_scale, dev)
     check(
         lib.dsa_indexer_kl_grad(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i), ptr(dw),
                                 ptr(loss_rows), ptr(ws), ws_bytes, B, S, s_k, HI, DI, K, int(q_offset),
-                                float(loss_scale), float(eps), float(grad_scale), stream_of(dev)),
+                                float(loss_scale), float(eps), gsf, ptr(gsd), stream_of(dev)),
         "dsa_indexer_kl_grad",
     )
     return dq_i, dk_i, dw, loss_rows
@@ -1211,11 +1222,12 @@ def indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, indices, ma
     hq, hk = host_i32(cu_q), host_i32(cu_k)
     ws_bytes = int(lib.dsa_indexer_kl_grad_varlen_workspace_size(hq, hk, n_seq, HI, DI, K))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    gsf, gsd = _grad_scale_args(grad_scale, dev)
     if T:
         check(
             lib.dsa_indexer_kl_grad_varlen(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i),
                                            ptr(dw), ptr(loss_rows), ptr(ws), ws_bytes, hq, hk, n_seq, HI, DI, K,
-                                           float(loss_scale), float(eps), float(grad_scale), stream_of(dev)),
+                                           float(loss_scale), float(eps), gsf, ptr(gsd), stream_of(dev)),
             "dsa_indexer_kl_grad_varlen",
         )
     return dq_i, dk_i, dw, loss_rows
