@@ -466,6 +466,28 @@ def kernel_rooflines(inp, ops, torch, dev, S, K, seed, with_topk):
                                algorithmic_bytes=nbytes, avg_launch_ms=ms, achieved=nbytes / (ms * 1e-3) / 1e9,
                                peak=HBM_PEAK_GBPS, unit="GB/s", frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS)
     del qi, ki
+    # the MLA absorb kernels at the C3 attention shape (128 heads): q_nope [1,S,H,128] . w_uk ->
+    # the 576-wide query with q_pe appended, and the [1,S,H,512] output . w_uv_t -> [1,S,H,128]
+    H = 128
+    qn = torch.randn(1, S, H, 128, device=dev, dtype=torch.bfloat16, generator=g)
+    qp = torch.randn(1, S, H, 64, device=dev, dtype=torch.bfloat16, generator=g)
+    wuk = torch.randn(H, 128, 512, device=dev, dtype=torch.bfloat16, generator=g)
+    ao = torch.randn(1, S, H, 512, device=dev, dtype=torch.bfloat16, generator=g)
+    wuv = torch.randn(H, 512, 128, device=dev, dtype=torch.bfloat16, generator=g)
+    wuk_t, wuv_tt = wuk.transpose(1, 2).contiguous(), wuv.transpose(1, 2).contiguous()
+
+    def run_absorb():
+        ops.mla_absorb(qn, wuk_t, append=qp)
+        ops.mla_absorb(ao, wuv_tt)
+
+    ms = time_ms(torch, run_absorb)
+    nbytes = S * H * 2 * ((128 + 64 + 576) + (512 + 128)) + 2 * H * 128 * 512 * 2
+    out["mla_absorb"] = dict(kernel="mla_absorb_kernel<128,512> + <512,128>", bound="hbm",
+                             shape=f"S={S}, H={H}: q absorb (128 -> 512, q_pe appended) + output absorb (512 -> 128)",
+                             algorithmic_bytes=nbytes, avg_launch_ms=ms, achieved=nbytes / (ms * 1e-3) / 1e9,
+                             peak=HBM_PEAK_GBPS, unit="GB/s", frac=nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+                             flops=4 * S * H * 128 * 512)
+    del qn, qp, wuk, ao, wuv, wuk_t, wuv_tt
     if with_topk:
         q8, qs = ops.quantize_fp8_per_row(inp["q_idx"])
         k8, ks = ops.quantize_fp8_per_row(inp["k_idx"])

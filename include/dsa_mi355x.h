@@ -33,6 +33,7 @@
  *   dsa_compressor_fwd           Compressor._forward_bsnd pooling + RMSNorm
  *                                (models/deepseek_v4/model.py:183-221; torch-only in the reference)
  *   dsa_compressor_fwd_tnd       Compressor._forward_tnd (models/deepseek_v4/model.py:223-274)
+ *   dsa_mla_absorb               the MLA absorb einsums (models/deepseek_v32/model.py:520-535, :574-575)
  *   dsa_tnd_metadata             build_smla_attention_masks (models/deepseek_v4/tnd.py:97-164) on the device
  *   dsa_indexer_prep             the indexer's RoPE + rotate_activation (+ this build's fp8 quantisation)
  *                                (models/deepseek_v32/model.py:196-221, :264-282;
@@ -290,6 +291,21 @@ int dsa_compressor_fwd_tnd(const float* kv, const float* score, const float* ape
                            void* out, int out_dtype, int64_t n_tokens, int64_t d, int64_t ratio, int overlap,
                            const int64_t* block_starts, int64_t n_blocks, const int32_t* positions, float norm_eps,
                            const float* rope_cs, int64_t n_pos, int64_t rope_dim, void* stream);
+
+/*
+ * MLA weight absorption (reference: models/deepseek_v32/model.py:520-535, the einsum
+ * q_nope . w_uk before the attention, and :574-575, the output . w_uv_t after it):
+ *   c[t, h, 0:n] = sum_k a[t, h, k] * wt[h, :, k]   (bf16 in, fp32 accumulation, bf16 out)
+ *   c[t, h, n:n + append_width] = append[t, h, 0:append_width]   (append != NULL)
+ *   a [tokens, heads, lda], wt [heads, n, k] (the weight transposed: row = output column),
+ *   c [tokens, heads, ldc], append [tokens, heads, ld_append]; (k, n) = (128, 512) or (512, 128).
+ * Forward of the query absorb: a = q_nope, wt = w_uk^T, append = q_pe, c = q [.., 576];
+ * of the output absorb: a = attention output, wt = w_uv; their input gradients are the
+ * other shape with the weight's transpose.
+ */
+int dsa_mla_absorb(const void* a, int64_t lda, const void* wt, void* c, int64_t ldc, const void* append,
+                   int64_t ld_append, int64_t append_width, int64_t tokens, int64_t heads, int64_t k, int64_t n,
+                   void* stream);
 
 /*
  * Packed varlen ("TND") metadata built on the device (reference: build_smla_attention_masks,

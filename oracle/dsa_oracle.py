@@ -61,6 +61,10 @@ follows (paths relative to the reference repository root):
                            models/deepseek_v4/model.py:90-111: F.linear with
                            scipy.linalg.hadamard(D) in the input dtype, then times
                            D^-0.5 in that dtype
+* ``mla_absorb_q``, ``mla_absorb_out``
+                           the absorbed-MLA einsums, models/deepseek_v32/model.py:
+                           520-535 (q_nope . w_uk, then cat with q_pe) and :574-575
+                           (output . w_uv_t), in fp64
 * ``indexer_prep``         Indexer.forward's q / k producer:
                            models/deepseek_v32/model.py:264-282 (rope on the first
                            64 features, non-interleaved, then rotate) and
@@ -104,6 +108,10 @@ Which check pins each function (tests/test_oracle.py):
   a one-hot input gives the corresponding column times D^-0.5.
 * indexer_prep: the composition of the two loops above with the reference's bf16
   rounding points, and quantize_e4m3_per_row of its output.
+* mla_absorb_q / mla_absorb_out: per-head torch.matmul loops and the non-absorbed
+  attention: with kv = [kv_latent, k_pe], the absorbed scores q_abs . kv equal the
+  explicit q_nope . (kv_latent w_uk^T) + q_pe . k_pe, and the absorbed output
+  (P kv_latent) w_uv equals P (kv_latent w_uv) (tests/test_oracle_prep.py).
 """
 
 from __future__ import annotations
@@ -141,6 +149,8 @@ __all__ = [
     "rope_rotate",
     "hadamard_rotate",
     "indexer_prep",
+    "mla_absorb_q",
+    "mla_absorb_out",
 ]
 
 
@@ -760,3 +770,19 @@ def indexer_prep(x, freqs_cis, positions, *, rope_dim=64, rope_start=0, interlea
         y = hadamard_rotate(y.to(out_dtype) if out_dtype != torch.float64 else y, out_dtype=out_dtype)
     q8, sc = quantize_e4m3_per_row(y.float())
     return y, q8, sc
+
+
+# ---------------------------------------------------------------------------
+# the MLA absorb einsums
+# ---------------------------------------------------------------------------
+def mla_absorb_q(q_nope, q_pe, w_uk, *, dtype=torch.float64):
+    """PreAttention's absorbed query (models/deepseek_v32/model.py:520-535):
+    ``cat([einsum("bshq,hqr->bshr", q_nope, w_uk), q_pe], -1)`` computed in ``dtype``."""
+    q_abs = torch.einsum("bshq,hqr->bshr", q_nope.to(dtype), w_uk.to(dtype))
+    return torch.cat([q_abs, q_pe.to(dtype)], dim=-1)
+
+
+def mla_absorb_out(out, w_uv_t, *, dtype=torch.float64):
+    """PostAttention's absorbed output projection (models/deepseek_v32/model.py:574-575),
+    ``einsum("bhsr,hrv->bhsv", output, w_uv_t)``, on the BSND output [B,S,H,512]."""
+    return torch.einsum("bshr,hrv->bshv", out.to(dtype), w_uv_t.to(dtype))

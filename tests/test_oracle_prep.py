@@ -122,3 +122,28 @@ def test_compressor_rope_epilogue_rotates_block_positions():
                                   freqs_cis=fc)
     ref_t = _rope_loop(base_t.bfloat16(), fc, positions[bs], 64, D - 64, True)
     torch.testing.assert_close(got_t, ref_t, rtol=1e-6, atol=1e-6)
+
+
+def test_mla_absorb_oracle_against_loops_and_non_absorbed_attention():
+    g = torch.Generator().manual_seed(9)
+    B, S, H, R = 1, 6, 3, 32
+    q_nope = torch.randn(B, S, H, 16, generator=g, dtype=torch.float64)
+    q_pe = torch.randn(B, S, H, 8, generator=g, dtype=torch.float64)
+    w_uk = torch.randn(H, 16, R, generator=g, dtype=torch.float64)
+    q = O.mla_absorb_q(q_nope, q_pe, w_uk)
+    for h in range(H):
+        torch.testing.assert_close(q[0, :, h, :R], q_nope[0, :, h] @ w_uk[h])
+    torch.testing.assert_close(q[..., R:], q_pe)
+    # absorbed scores == explicit keys k_nope = kv_latent w_uk^T (plus the rope part)
+    kv = torch.randn(B, S, R, generator=g, dtype=torch.float64)
+    k_pe = torch.randn(B, S, 8, generator=g, dtype=torch.float64)
+    scores = torch.einsum("bshd,btd->bhst", q, torch.cat([kv, k_pe], -1))
+    k_nope = torch.einsum("btr,hqr->bhtq", kv, w_uk)
+    explicit = torch.einsum("bshq,bhtq->bhst", q_nope, k_nope) + torch.einsum("bshp,btp->bhst", q_pe, k_pe)
+    torch.testing.assert_close(scores, explicit)
+    # absorbed output (P kv) w_uv == P (kv w_uv)
+    P = torch.softmax(scores, dim=-1)
+    w_uv_t = torch.randn(H, R, 10, generator=g, dtype=torch.float64)
+    o_lat = torch.einsum("bhst,btr->bshr", P, kv)
+    v = torch.einsum("btr,hrv->bhtv", kv, w_uv_t)
+    torch.testing.assert_close(O.mla_absorb_out(o_lat, w_uv_t), torch.einsum("bhst,bhtv->bshv", P, v))

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -65,6 +65,7 @@ _SIGNATURES = {
     ),
     "dsa_indexer_prep": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _vp],
                          _i32),
+    "dsa_mla_absorb": ([_vp, _i64, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _i32),
     "dsa_tnd_metadata": ([_vp, _i32, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp], _i32),
     # packed varlen: cu_seqlens / cmp_residual_k are host int32 arrays (ctypes arrays or None)
     "dsa_lightning_indexer_varlen": (

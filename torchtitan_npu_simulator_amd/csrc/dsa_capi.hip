@@ -29,4 +29,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* dsa_last_error(void) { return dsa::g_last_error.c_str(); }
 
-extern "C" int dsa_abi_version(void) { return 10; }
+extern "C" int dsa_abi_version(void) { return 11; }

@@ -50,6 +50,9 @@ __all__ = [
     "compressor_pool_tnd",
     "indexer_prep",
     "rope_cos_sin",
+    "mla_absorb",
+    "mla_absorb_q",
+    "mla_absorb_out",
     "lightning_indexer_varlen",
     "sparse_mla_fwd_varlen",
     "sparse_mla_bwd_varlen",
@@ -1379,6 +1382,112 @@ def compressor_pool_tnd(kv, score, ape, ratio, block_starts, positions=None, *, 
         "dsa_compressor_fwd_tnd",
     )
     return out
+
+
+# ---------------------------------------------------------------------------
+# MLA weight absorption around the absorbed attention
+# ---------------------------------------------------------------------------
+def _rows_view(x):
+    """``x`` [..., H, D] with a unit last stride and its (token, head) rows at a fixed stride
+    ``ld`` (token stride H * ld), as the absorb kernel addresses them; copies otherwise.
+    Returns (x, ld)."""
+    H, D = x.shape[-2], x.shape[-1]
+    ld = x.stride(-2)
+    ok = x.stride(-1) == 1 and ld >= D and ld % 8 == 0 and x.data_ptr() % 16 == 0
+    expected = H * ld
+    for i in range(x.dim() - 3, -1, -1):
+        if x.shape[i] != 1 and x.stride(i) != expected:
+            ok = False
+        expected *= x.shape[i]
+    if not ok:
+        x = x.contiguous()
+        ld = D
+    return x, ld
+
+
+def mla_absorb(a, wt, *, append=None):
+    """c[t, h, :N] = a[t, h, :K] . wt[h]^T, c[t, h, N:] = append[t, h] (dsa_mla_absorb).
+
+    a [..., H, K] bf16 (rows may be a strided view, e.g. the first 512 columns of a 576-wide
+    gradient), wt [H, N, K] bf16, append [..., H, E] or None; (K, N) = (128, 512) or
+    (512, 128).  Returns c [..., H, N + E] bf16, contiguous."""
+    lib = load_library()
+    require_gpu_tensor(a, "a")
+    a, lda = _rows_view(a.to(torch.bfloat16))
+    H, K = a.shape[-2], a.shape[-1]
+    N = wt.shape[1]
+    if wt.shape != (H, N, K):
+        raise ValueError(f"weight {tuple(wt.shape)} does not fit rows [.., {H}, {K}]")
+    lead = a.shape[:-2]
+    tokens = math.prod(lead)
+    wt = wt.to(torch.bfloat16).contiguous()
+    E, lde = 0, 0
+    if append is not None:
+        append, lde = _rows_view(append.to(torch.bfloat16))
+        E = append.shape[-1]
+    out = torch.empty(*lead, H, N + E, dtype=torch.bfloat16, device=a.device)
+    check(lib.dsa_mla_absorb(ptr(a), lda, ptr(wt), ptr(out), N + E, ptr(append), lde, E, tokens, H, K, N,
+                             stream_of(a.device)), "dsa_mla_absorb")
+    return out
+
+
+class _AbsorbQ(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q_nope, q_pe, w_uk):
+        wt = w_uk.transpose(1, 2).contiguous()  # [H, 512, 128]
+        q = mla_absorb(q_nope, wt, append=q_pe)
+        ctx.save_for_backward(q_nope, w_uk)
+        ctx.rope = q_pe.shape[-1]
+        return q
+
+    @staticmethod
+    def backward(ctx, dq):
+        q_nope, w_uk = ctx.saved_tensors
+        R = w_uk.shape[-1]
+        dq = dq.to(torch.bfloat16)
+        d_nope = mla_absorb(dq[..., :R], w_uk.to(torch.bfloat16).contiguous())  # [.., H, 128]
+        # d w_uk[h] = sum_t q_nope[t, h]^T dq[t, h, :R]: a plain batched GEMM (hipBLASLt)
+        H = q_nope.shape[-2]
+        qn = q_nope.reshape(-1, H, q_nope.shape[-1]).permute(1, 2, 0).contiguous().float()
+        dqa = dq[..., :R].reshape(-1, H, R).transpose(0, 1).contiguous().float()
+        d_w = torch.bmm(qn, dqa).to(w_uk.dtype)
+        return d_nope.to(q_nope.dtype), dq[..., R:].to(q_nope.dtype), d_w
+
+
+class _AbsorbOut(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, out, w_uv_t):
+        wt = w_uv_t.transpose(1, 2).contiguous()  # [H, 128, 512]
+        y = mla_absorb(out, wt)
+        ctx.save_for_backward(out, w_uv_t)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        out, w_uv_t = ctx.saved_tensors
+        dy = dy.to(torch.bfloat16)
+        d_out = mla_absorb(dy, w_uv_t.to(torch.bfloat16).contiguous())  # [.., H, 512]
+        H = out.shape[-2]
+        o = out.reshape(-1, H, out.shape[-1]).permute(1, 2, 0).contiguous().float()
+        g = dy.reshape(-1, H, dy.shape[-1]).transpose(0, 1).contiguous().float()
+        d_w = torch.bmm(o, g).to(w_uv_t.dtype)
+        return d_out.to(out.dtype), d_w
+
+
+def mla_absorb_q(q_nope, q_pe, w_uk):
+    """The absorbed query of MLA (reference PreAttention, models/deepseek_v32/model.py:520-535):
+    ``cat([einsum("bshq,hqr->bshr", q_nope, w_uk), q_pe], -1)`` in one kernel.
+    q_nope [B,S,H,128], q_pe [B,S,H,64], w_uk [H,128,512] bf16 -> q [B,S,H,576];
+    differentiable in all three (the weight gradient is a batched GEMM)."""
+    return _AbsorbQ.apply(q_nope, q_pe, w_uk)
+
+
+def mla_absorb_out(out, w_uv_t):
+    """The output projection of absorbed MLA (reference PostAttention,
+    models/deepseek_v32/model.py:574-575): ``einsum("bshr,hrv->bshv", out, w_uv_t)`` on the
+    BSND attention output [B,S,H,512] with w_uv_t [H,512,128] -> [B,S,H,128] (contiguous,
+    so .view(B, S, H*128) feeds wo); differentiable in both."""
+    return _AbsorbOut.apply(out, w_uv_t)
 
 
 def default_softmax_scale(d_qk: int) -> float:
