@@ -15,8 +15,10 @@
 // The bf16 rounding points are the reference's: RoPE output cast to the model dtype, the
 // bf16 linear, then the bf16 scale multiply.
 //
-// HBM-bound: one wave per row, lane l holds features 2l, 2l+1 (4-byte loads and stores
-// coalesced along the row); the butterfly's cross-lane stages are lane exchanges.
+// HBM-bound: a 16-lane group per row (four rows per wave), lane l holding features
+// 8l .. 8l+7 (16-byte loads and stores coalesced along the row).  Every cross-lane step --
+// the butterfly's strides 8 .. 64, the V3.2 rope partner four lanes away and the amax --
+// is a DPP lane exchange inside the 16-lane row.
 #include "dsa_common.h"
 
 namespace dsa {
@@ -27,55 +29,59 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f(f_to_bf16(x)); }
 
-template <int kMask>
-__device__ __forceinline__ float lane_swap(float x) {
-  return __shfl_xor(x, kMask, 64);
-}
-
 __global__ void __launch_bounds__(kThreads)
 indexer_prep_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, uint8_t* __restrict__ q8,
                     float* __restrict__ scale, int64_t vecs, int heads, int64_t seq_len, const float* __restrict__ cs,
                     int64_t n_pos, const int32_t* __restrict__ positions, int64_t pos_offset, int rope_dim,
                     int rope_start, int interleaved, int hadamard) {
-  const int64_t v = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
-  if (v >= vecs) return;  // whole waves: v is wave-uniform
-  const uint32_t w = reinterpret_cast<const uint32_t*>(x + v * kD)[lane];
-  float e0 = bf16_lo(w), e1 = bf16_hi(w);
-  const int f0 = 2 * lane;  // features f0, f0 + 1
+  const int64_t v_raw = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 4;
+  const int l = threadIdx.x & 15;
+  const bool active = v_raw < vecs;
+  const int64_t v = active ? v_raw : vecs - 1;  // idle groups of the last wave redo the last row
+  const int f0 = 8 * l;
+  float e[8];
+  {
+    const u32x4 w = reinterpret_cast<const u32x4*>(x + v * kD)[l];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e[2 * i] = bf16_lo(w[i]);
+      e[2 * i + 1] = bf16_hi(w[i]);
+    }
+  }
 
   // ---- 1. RoPE (fp32, rounded to bf16) ----
   if (rope_dim > 0) {
     const int64_t row = v / heads;
     const int64_t pos = positions ? (int64_t)positions[row] : pos_offset + row % seq_len;
     const bool pos_ok = pos >= 0 && pos < n_pos;  // rows outside the table keep their features
-    const int half = rope_dim / 2;
-    const int lf = f0 - rope_start;  // local feature index of e0
-    const bool in_rope = lf >= 0 && lf < rope_dim;
+    const float* cp = cs + (pos_ok ? pos : 0) * rope_dim;
+    const int lf = f0 - rope_start;  // local feature of e[0]
+    const bool in_rope = pos_ok && lf >= 0 && lf < rope_dim;
     if (interleaved) {
-      // pair (lf, lf + 1) lives in this lane: angle lf / 2
-      if (in_rope && pos_ok) {
-        const float2 c = reinterpret_cast<const float2*>(cs + pos * rope_dim)[lf / 2];
-        const float a = e0, b = e1;
-        e0 = round_bf16(a * c.x - b * c.y);
-        e1 = round_bf16(a * c.y + b * c.x);
+      // pairs (lf + 2i, lf + 2i + 1) inside the lane, angles lf/2 + i
+      if (in_rope) {
+        const float4 c01 = *reinterpret_cast<const float4*>(cp + lf);
+        const float4 c23 = *reinterpret_cast<const float4*>(cp + lf + 4);
+        const float cc[4] = {c01.x, c01.z, c23.x, c23.z}, ss[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = e[2 * i], b = e[2 * i + 1];
+          e[2 * i] = round_bf16(a * cc[i] - b * ss[i]);
+          e[2 * i + 1] = round_bf16(a * ss[i] + b * cc[i]);
+        }
       }
     } else {
-      // pair (i, i + half): the partner features sit half / 2 lanes away
-      const int dl = half / 2;
-      const bool lower = in_rope && lf < half;
-      const int partner = in_rope ? (lower ? lane + dl : lane - dl) : lane;
-      const float p0 = __shfl(e0, partner, 64), p1 = __shfl(e1, partner, 64);
-      if (in_rope && pos_ok) {
-        const int i0 = lower ? lf : lf - half;  // angle of e0 (e1: i0 + 1)
-        const float2* cp = reinterpret_cast<const float2*>(cs + pos * rope_dim);
-        const float2 c0 = cp[i0], c1 = cp[i0 + 1];
-        if (lower) {  // real parts: a c - b s with b = partner
-          e0 = round_bf16(e0 * c0.x - p0 * c0.y);
-          e1 = round_bf16(e1 * c1.x - p1 * c1.y);
-        } else {  // imaginary parts: a s + b c with a = partner
-          e0 = round_bf16(p0 * c0.y + e0 * c0.x);
-          e1 = round_bf16(p1 * c1.y + e1 * c1.x);
+      // pairs (i, i + 32) of a 64-feature block: the partner lane is four lanes away
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p[i] = lane_xor<4>(e[i]);
+      if (in_rope) {
+        const bool lower = lf < 32;
+        const int a0 = lower ? lf : lf - 32;  // angle of e[0]
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float2 c = reinterpret_cast<const float2*>(cp)[a0 + i];
+          e[i] = lower ? round_bf16(e[i] * c.x - p[i] * c.y) : round_bf16(p[i] * c.y + e[i] * c.x);
         }
       }
     }
@@ -83,37 +89,61 @@ indexer_prep_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y, ui
 
   // ---- 2. Hadamard: y = bf16(bf16(H x) * D^-0.5) ----
   if (hadamard) {
-    // stage h = 1 inside the lane, then h = 2 .. 64 across lanes (feature bit k <-> lane bit k-1)
-    float s0 = e0 + e1, s1 = e0 - e1;
-    e0 = s0;
-    e1 = s1;
-    static_for<6>([&](auto k) {
-      constexpr int m = 1 << decltype(k)::value;  // lane mask of feature stride 2m
-      const float o0 = lane_swap<m>(e0), o1 = lane_swap<m>(e1);
-      const bool upper = lane & m;
-      e0 = upper ? o0 - e0 : e0 + o0;
-      e1 = upper ? o1 - e1 : e1 + o1;
+    // feature strides 1, 2, 4 inside the lane
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (!(i & h)) {
+          const float a = e[i], b = e[i + h];
+          e[i] = a + b;
+          e[i + h] = a - b;
+        }
+    // strides 8 .. 64 across the lanes of the row: lane bit k <-> feature stride 8 * 2^k
+    static_for<4>([&](auto k) {
+      constexpr int m = 1 << decltype(k)::value;
+      const bool upper = l & m;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float o = lane_xor<m>(e[i]);
+        e[i] = upper ? o - e[i] : e[i] + o;
+      }
     });
     const float sc = 0.08838834764831845f;  // 128^-0.5 rounded to fp32
-    e0 = round_bf16(round_bf16(e0) * sc);
-    e1 = round_bf16(round_bf16(e1) * sc);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = round_bf16(round_bf16(e[i]) * sc);
   }
-  if (y) reinterpret_cast<uint32_t*>(y + v * kD)[lane] = pack_bf16x2(e0, e1);
+  if (y && active) {
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(e[2 * i], e[2 * i + 1]);
+    reinterpret_cast<u32x4*>(y + v * kD)[l] = w;
+  }
 
   // ---- 3. fp8-e4m3 with a per-row scale ----
   if (q8) {
-    float amax = fmaxf(fabsf(e0), fabsf(e1));
-    if (e0 != e0 || e1 != e1) amax = __int_as_float(0x7fc00000);
+    float amax = 0.f;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const float o = __shfl_xor(amax, m, 64);
-      amax = (o > amax || o != o) ? o : amax;
+    for (int i = 0; i < 8; ++i) {
+      const float a = fabsf(e[i]);
+      amax = (a > amax || a != a) ? a : amax;  // a NaN makes the row's amax NaN
     }
+    static_for<4>([&](auto k) {
+      constexpr int m = 1 << decltype(k)::value;
+      const float o = lane_xor<m>(amax);
+      amax = (o > amax || o != o) ? o : amax;
+    });
     float s = amax / 448.0f;
     s = s < 1e-12f ? 1e-12f : s;  // (keeps NaN)
-    const uint32_t b0 = e4m3fn_rne(e0 / s), b1 = e4m3fn_rne(e1 / s);
-    reinterpret_cast<uint16_t*>(q8 + v * kD)[lane] = (uint16_t)(b0 | (b1 << 8));
-    if (lane == 0 && scale) scale[v] = s;
+    if (active) {
+      uint32_t b[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) b[i] = e4m3fn_rne(e[i] / s);
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      const u32x2 w = {b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24)};
+      reinterpret_cast<u32x2*>(q8 + v * kD)[l] = w;
+      if (l == 0 && scale) scale[v] = s;
+    }
   }
 }
 
@@ -131,15 +161,16 @@ extern "C" int dsa_indexer_prep(const void* x, void* y, uint8_t* q8, float* scal
   if (rows < 0 || heads <= 0 || seq_len <= 0) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_prep: bad sizes");
   if (d != kD) return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_prep: D=%lld (the producer takes D = 128)",
                                 (long long)d);
-  if (rope_dim < 0 || rope_dim % 4 != 0 || rope_start < 0 || rope_start % 2 != 0 || rope_start + rope_dim > kD)
-    return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_prep: rope features [%lld, %lld) (need rope_dim a multiple "
-                     "of 4 inside [0, 128) starting at an even feature)", (long long)rope_start,
+  if (rope_dim < 0 || rope_start < 0 || rope_start + rope_dim > kD ||
+      (rope_dim > 0 && (interleaved ? (rope_dim % 8 || rope_start % 8) : (rope_dim != 64 || rope_start % 64))))
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_prep: rope features [%lld, %lld) (interleaved: multiples of "
+                     "8; blocked: 64 features starting at 0 or 64)", (long long)rope_start,
                      (long long)(rope_start + rope_dim));
   if (rope_dim > 0 && (!rope_cs || n_pos <= 0))
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_prep: RoPE needs the cos/sin table");
   const int64_t vecs = rows * heads;
   if (vecs == 0) return DSA_OK;
-  const int64_t grid = (vecs * 64 + kThreads - 1) / kThreads;
+  const int64_t grid = (vecs * 16 + kThreads - 1) / kThreads;
   if (grid > INT32_MAX) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_prep: too many rows");
   indexer_prep_kernel<<<(unsigned)grid, kThreads, 0, (hipStream_t)stream>>>(
       (const uint16_t*)x, (uint16_t*)y, q8, scale, vecs, (int)heads, seq_len, rope_cs, n_pos, positions, pos_offset,
