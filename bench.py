@@ -10,10 +10,13 @@ One step = one pass of the DeepSeek-V3.2 DSA hot path over one synthetic batch
   needs, from the probabilities the backward recomputes) -> indexer KL loss gradients
 
 Inputs are resident in HBM before the timed region.  Prints ONE JSON line.  The
-``roofline`` object is for the dominant kernel (the gathered sparse MLA forward):
-its algorithmic bytes per step (Q + gathered KV rows + indices + O + LSE) over its
-average duration, measured with HIP events on the stream the kernel runs on.  ``cpu_baseline`` times the CPU oracle
-(fp32, all host threads) on a bounded sample of the same workload.
+library's kernel timing (HIP events around every kernel launch, on the stream the kernel
+runs on) is on over the timed region: ``kernels_in_step`` lists every kernel with its
+average launch duration, algorithmic bytes (or FLOPs) per launch and fraction of peak,
+slowest first, and ``roofline`` is the dominant one (the most time per step).
+``roofline_attention_fwd_bwd`` is the attention forward + backward as a whole.
+``cpu_baseline`` times the CPU oracle (fp32, all host threads) on a bounded sample of the
+same workload.
 """
 
 from __future__ import annotations
@@ -337,6 +340,83 @@ def measured_traffic(kernel, S, H, K):
     return k["fetch_bytes"] + k["write_bytes"]
 
 
+def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128):
+    """Algorithmic work of one launch-set per step of every kernel in the DSA step, keyed by
+    the name the library's kernel timing reports (dsa_kernel_timing).
+
+    S query rows, H heads, K top-k slots, P = valid (row, slot) pairs, ``pairs`` = causal
+    (query, key) pairs the indexer scores, s_kv attention keys, s_ki indexer keys (default
+    s_kv).  Bytes are the data each kernel must move once (no cache hits assumed, gathered
+    rows counted per pair); FLOPs count the MFMA products.  Returns name -> (bound, bytes,
+    flops).
+    """
+    s_ki = s_kv if s_ki is None else s_ki
+    dq, dv, gw = 576, 512, 256  # latent + rope width, latent width, G row (dS | P) x 128 heads
+    return {
+        "quantize_fp8_kernel": ("hbm", (S * h_i + s_ki) * (2 * d_i + d_i + 4), 0),
+        "indexer_lin_pieces_kernel<64>": ("hbm", S * (h_i * d_i + 4 * h_i + 4 * h_i + 4 * d_i + 16), 0),
+        "indexer_tile_kernel<fp8, 4, split>": ("mfma", 0, 2 * h_i * d_i * pairs),
+        "topk_kernel": ("hbm", 4 * pairs + 4 * K * S, 0),
+        "sparse_mla_fwd_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * K * S + 2 * H * dv * S + 4 * H * S,
+                                       2 * H * (dq + dv) * P),
+        "sparse_mla_fwd_exact_kernel<fixup>": ("hbm", 4 * H * S, 0),
+        "bwd_delta_kernel": ("hbm", 2 * (2 * H * dv * S) + 4 * H * S, 0),
+        # Q, dO, gathered rows, indices, G written, mass, (max, sum, delta)
+        "bwd_sdp_kernel": ("hbm", 2 * H * dq * S + 2 * H * dv * S + 2 * dq * P + 4 * K * S + 2 * gw * P + 4 * K * S
+                           + 12 * H * S, 2 * H * (dq + dv) * P),
+        # gathered rows, indices, dS half of G, dQ written
+        "bwd_dqk_kernel": ("hbm", 2 * dq * P + 4 * K * S + 2 * (gw // 2) * P + 2 * H * dq * S, 2 * H * dq * P),
+        # G, X = [Q; dO], indices, C written
+        "bwd_contrib_kernel<2>": ("hbm", 2 * gw * P + 2 * H * (dq + dv) * S + 4 * K * S + 2 * dq * P,
+                                  2 * P * (gw * dv + (gw // 2) * (dq - dv))),
+        "zero_i32_kernel": ("hbm", 4 * (s_kv + 1) + 4 * (s_ki + 1), 0),
+        "csr_count_kernel<count>": ("hbm", 8 * K * S, 0),
+        "csr_count_kernel<fill>": ("hbm", 8 * K * S + 8 * P, 0),
+        "csr_scan_kernel": ("hbm", 12 * (s_kv + s_ki), 0),
+        "csr_seg_key_kernel": ("hbm", 8 * (s_kv + s_ki), 0),
+        # C rows read, pair list, fp32 dKV written
+        "dkv_reduce_kernel<72>": ("hbm", 2 * dq * P + 4 * P + 4 * dq * s_kv, 0),
+        # q_I, gathered k_I rows, mass, weights, dq_I (fp32), dk_I contributions, dw, loss
+        "indexer_kl_mfma_kernel": ("hbm", S * (2 * h_i * d_i + 4 * K + 4 * h_i + 4 * h_i * d_i + 4 * h_i + 4)
+                                   + P * (2 * d_i + 2 * d_i), 2 * P * h_i * d_i * 3),
+        "dkv_reduce_kernel<16>": ("hbm", 2 * d_i * P + 4 * P + 4 * d_i * s_ki, 0),
+        "compressor_kernel": ("hbm", 0, 0),  # per-call bytes depend on the block geometry; see kernels
+    }
+
+
+def kernel_table(ktimes, work, steps, traffic_of=None):
+    """Per-kernel roofline rows, slowest first: average launch duration and launches per step
+    from the kernel timing, the algorithmic bytes (or FLOPs for MFMA-bound kernels) per launch,
+    achieved rate and fraction of peak, MFMA fraction of the bf16 peak where the kernel runs
+    MFMAs, and the counter bytes per launch when a PMC summary has the kernel."""
+    rows = []
+    for name, (total_ms, launches) in ktimes.items():
+        per_step = launches / steps
+        avg = total_ms / launches
+        row = dict(kernel=name, avg_launch_ms=avg, launches_per_step=per_step, ms_per_step=total_ms / steps)
+        if name in work:
+            bound, nbytes, flops = work[name]
+            b1, f1 = nbytes / per_step, flops / per_step
+            if bound == "mfma":
+                ach = f1 / (avg * 1e-3) / 1e12
+                row.update(bound="mfma", algorithmic_flops=f1, achieved=ach, peak=FP8_PEAK_TFLOPS, unit="TFLOP/s",
+                           frac=ach / FP8_PEAK_TFLOPS)
+            elif nbytes:
+                ach = b1 / (avg * 1e-3) / 1e9
+                row.update(bound="hbm", algorithmic_bytes=b1, achieved=ach, peak=HBM_PEAK_GBPS, unit="GB/s",
+                           frac=ach / HBM_PEAK_GBPS)
+                if flops:
+                    row["mfma_frac_bf16"] = f1 / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS
+        if traffic_of is not None:
+            t = traffic_of(name)
+            if t is not None:
+                row["traffic"] = t
+                row["traffic_gbps"] = t / (avg * 1e-3) / 1e9
+        rows.append(row)
+    rows.sort(key=lambda r: -r["ms_per_step"])
+    return rows
+
+
 def time_indexer_kernel(inp, ops, torch, reps=10):
     """Average duration (ms) of the lightning-indexer scores alone (dsa_indexer_fwd_ws, fp8
     queries and keys, causal: the linear-split pre-pass plus the score kernel), timed with HIP
@@ -510,6 +590,7 @@ def main():
     import torch
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from torchtitan_npu_simulator_amd import _lib
     from torchtitan_npu_simulator_amd import torch_npu_ops as ops
 
     dev = torch.device("cuda:0")
@@ -560,12 +641,16 @@ def main():
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t0.record()
-    for _ in range(args.steps):
-        res = step(timer)
-    t1.record()
-    torch.cuda.synchronize()
+    # HIP events around every library kernel launch inside the timed region, on the stream
+    # each kernel runs on (the library's own timing; a few microseconds per step)
+    with _lib.kernel_timing() as ktimer:
+        t0.record()
+        for _ in range(args.steps):
+            res = step(timer)
+        t1.record()
+        torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / args.steps
+    ktimes = ktimer.summary()
     phases = timer.averages_ms()
     if wl == "v4":
         # slots per row: the window (min(128, s + 1) rows) plus the valid compressed picks;
@@ -577,22 +662,32 @@ def main():
         work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs)
     del res
 
-    # Dominant kernel: the gathered sparse MLA forward (sparse_mla_fwd_bf16_kernel; its
-    # row-fixup pass is launched in the same call and is timed with it).  Its algorithmic
-    # bytes are Q + gathered KV rows + indices + O + LSE for one step.
     fwd_ms = phases["attn_fwd"]
     bwd_ms = phases["attn_bwd"]
-    roof = dict(
-        bound="hbm",
-        kernel="sparse_mla_fwd_bf16_kernel",
-        achieved=work["attn_fwd_bytes"] / (fwd_ms * 1e-3) / 1e9,
-        peak=HBM_PEAK_GBPS,
-        unit="GB/s",
-        algorithmic_bytes=work["attn_fwd_bytes"],
-        avg_launch_ms=fwd_ms,
-        traffic=measured_traffic("sparse_mla_fwd_bf16_kernel", S, H, K) if wl == "c3" else None,
-    )
-    roof["frac"] = roof["achieved"] / roof["peak"]
+    if wl == "v4":
+        kwork = {}
+    else:
+        s_kv = S // 4 if wl == "c4" else S
+        kwork = step_kernel_work(S, H, K, work["sum_keff"], pairs if pairs is not None else S * (S + 1) // 2, s_kv)
+    traffic_of = (lambda name: measured_traffic(name, S, H, K)) if wl == "c3" else None
+    ktable = kernel_table(ktimes, kwork, args.steps, traffic_of)
+    # Dominant kernel: the kernel with the most time per step that has an algorithmic
+    # roofline (every kernel of the step has one except the compressor's per-call geometry)
+    dom = next((r for r in ktable if "frac" in r), None)
+    if dom is not None:
+        roof = dict(bound=dom["bound"], kernel=dom["kernel"], achieved=dom["achieved"], peak=dom["peak"],
+                    unit=dom["unit"], frac=dom["frac"], traffic=dom.get("traffic"),
+                    avg_launch_ms=dom["avg_launch_ms"], launches_per_step=dom["launches_per_step"],
+                    share_of_step=dom["ms_per_step"] / ms_per_step)
+        if dom["bound"] == "hbm":
+            roof["algorithmic_bytes"] = dom["algorithmic_bytes"]
+        else:
+            roof["algorithmic_flops"] = dom["algorithmic_flops"]
+    else:  # (v4: the attention forward as a whole)
+        roof = dict(bound="hbm", kernel="dsa_sparse_mla_fwd", achieved=work["attn_fwd_bytes"] / (fwd_ms * 1e-3) / 1e9,
+                    peak=HBM_PEAK_GBPS, unit="GB/s", algorithmic_bytes=work["attn_fwd_bytes"], avg_launch_ms=fwd_ms,
+                    traffic=None)
+        roof["frac"] = roof["achieved"] / roof["peak"]
     attn_bytes = work["attn_fwd_bytes"] + work["attn_bwd_bytes"]
     roof_pair = dict(
         bound="hbm",
@@ -624,6 +719,7 @@ def main():
         config=cfg,
         roofline=roof,
         roofline_attention_fwd_bwd=roof_pair,
+        kernels_in_step=[{k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()} for r in ktable],
         phases_ms={k: round(v, 4) for k, v in phases.items()},
         attn_mfma=dict(fwd_tflops=work["attn_fwd_flops"] / (fwd_ms * 1e-3) / 1e12,
                        bwd_tflops=work["attn_bwd_flops"] / (bwd_ms * 1e-3) / 1e12, peak_tflops=BF16_PEAK_TFLOPS),

@@ -67,6 +67,20 @@ const char* dsa_last_error(void);
 int dsa_abi_version(void);
 
 /*
+ * Per-kernel timing (no counterpart in the reference; for benchmarks and profiling).
+ * dsa_kernel_timing(1) drops earlier records and makes every later kernel launch of this
+ * library record a HIP event before and after itself on its stream; dsa_kernel_timing(0)
+ * stops recording.  dsa_kernel_timing_count() waits for the recorded events, sums the
+ * elapsed times per kernel name and returns the number of distinct kernels (or < 0 with
+ * dsa_last_error); dsa_kernel_timing_get(i, ...) returns entry i: its name (truncated to
+ * name_cap - 1 bytes), the summed milliseconds and the number of launches.  While
+ * enabled, each launch creates two events and takes a lock; leave it off in production.
+ */
+int dsa_kernel_timing(int enable);
+int dsa_kernel_timing_count(void);
+int dsa_kernel_timing_get(int i, char* name, int64_t name_cap, double* total_ms, int64_t* launches);
+
+/*
  * Lightning-indexer scores (reference: bf16_index, models/deepseek_v32/model.py:224-236;
  * LiCompute, models/deepseek_v4/model.py:647-652).
  *   scores[b, s, t] = k_scale[b,t] * sum_h w[b,s,h] * q_scale[b,s,h] * relu(q[b,s,h,:] . k[b,t,:])
@@ -117,6 +131,8 @@ int dsa_indexer_fwd_ws(const void* q, const float* q_scale, const void* k, const
  * split does not apply to run dsa_indexer_fwd's kernels.  Every call on a GPU uses that GPU's
  * one array, so calls that overlap on one GPU (concurrent streams or threads) race; calls on
  * one stream are ordered and safe.  Nothing in the array needs clearing between calls.
+ * (While dsa_kernel_timing is enabled, every launch also creates two HIP events; it is off
+ * by default.)
  */
 int64_t dsa_indexer_fwd_noalloc_max_rows(void);
 int dsa_indexer_fwd_noalloc(const void* q, const float* q_scale, const void* k, const float* k_scale,

@@ -146,3 +146,27 @@ def test_compiled_attention_matches_eager():
     assert torch.equal(compiled, eager)
     for a, b in zip(comp_in, eager_in):
         assert rel_err(a.grad, b.grad) <= 1e-6
+
+
+def test_kernel_timing_records_each_launch():
+    """dsa_kernel_timing: event pairs around the library's launches while enabled, summed per
+    kernel name; nothing recorded once it is off."""
+    from torchtitan_npu_simulator_amd import _lib
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    x = torch.randn(300, 128, device=DEV).bfloat16()
+    with _lib.kernel_timing() as kt:
+        for _ in range(3):
+            ops.quantize_fp8_per_row(x)
+        torch.cuda.synchronize()
+    summary = kt.summary()
+    assert list(summary) == ["quantize_fp8_kernel"]
+    total_ms, launches = summary["quantize_fp8_kernel"]
+    assert launches == 3 and total_ms > 0.0
+    ops.quantize_fp8_per_row(x)  # timing is off: the last window's summary is unchanged
+    torch.cuda.synchronize()
+    lib = _lib.load_library()
+    assert lib.dsa_kernel_timing_count() == 1
+    with _lib.kernel_timing() as kt2:  # a new window starts empty
+        pass
+    assert kt2.summary() == {}

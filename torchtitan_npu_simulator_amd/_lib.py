@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -26,6 +26,10 @@ _vp = ctypes.c_void_p
 _SIGNATURES = {
     "dsa_last_error": ([], ctypes.c_char_p),
     "dsa_abi_version": ([], _i32),
+    "dsa_kernel_timing": ([_i32], _i32),
+    "dsa_kernel_timing_count": ([], _i32),
+    "dsa_kernel_timing_get": ([_i32, ctypes.c_char_p, _i64, ctypes.POINTER(ctypes.c_double),
+                               ctypes.POINTER(ctypes.c_int64)], _i32),
     "dsa_indexer_fwd": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _i32),
     "dsa_indexer_fwd_workspace_size": ([_i64, _i64, _i64, _i64, _i32], _i64),
     "dsa_indexer_fwd_ws": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
@@ -134,6 +138,37 @@ def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load_library().dsa_last_error().decode(errors="replace")
         raise DSAError(f"{what} failed (status {rc}): {msg}")
+
+
+class kernel_timing:
+    """Context manager: HIP events around every kernel this library launches inside the
+    block (dsa_kernel_timing).  ``summary()`` afterwards returns {kernel name: (total ms,
+    launches)}, in the order the kernels first ran."""
+
+    def __enter__(self):
+        check(load_library().dsa_kernel_timing(1), "dsa_kernel_timing")
+        self._summary = None
+        return self
+
+    def __exit__(self, *exc):
+        check(load_library().dsa_kernel_timing(0), "dsa_kernel_timing")
+        return False
+
+    def summary(self) -> dict[str, tuple[float, int]]:
+        if self._summary is None:
+            lib = load_library()
+            n = lib.dsa_kernel_timing_count()
+            if n < 0:
+                check(-n, "dsa_kernel_timing_count")
+            out = {}
+            buf = ctypes.create_string_buffer(256)
+            ms, cnt = ctypes.c_double(), ctypes.c_int64()
+            for i in range(n):
+                check(lib.dsa_kernel_timing_get(i, buf, 256, ctypes.byref(ms), ctypes.byref(cnt)),
+                      "dsa_kernel_timing_get")
+                out[buf.value.decode()] = (ms.value, cnt.value)
+            self._summary = out
+        return self._summary
 
 
 def host_i32(values) -> ctypes.Array | None:

@@ -46,8 +46,16 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build the DSA HIP extension)")
 
 
+# per-source additions: the backward's score kernel keeps Q and dO in AGPRs as MFMA operands
+# and its accumulators in VGPRs (read by the softmax every block)
+EXTRA_FLAGS = {
+    "sparse_mla_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o",
+           str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

@@ -202,6 +202,7 @@ extern "C" int dsa_compressor_fwd(const float* kv, const float* score, const flo
   const int64_t grid = (total + groups - 1) / groups;
   if (grid > INT32_MAX) return set_error(DSA_ERR_INVALID_ARG, "dsa_compressor_fwd: too many blocks");
   const size_t shm = (size_t)groups * ((lanes + 63) / 64 + 1) * sizeof(float);
+  const TimedLaunch tl("compressor_kernel", (hipStream_t)stream);
   compressor_kernel<<<(unsigned)grid, kThreads, shm, (hipStream_t)stream>>>(
       kv, score, ape, norm_weight, out, out_dtype == DSA_BF16, total, (int)nb, (int)d, (int)ratio, overlap ? 1 : 0,
       norm_eps, nullptr, positions, batch * s, rope_cs, n_pos, (int)rope_dim);
@@ -235,6 +236,7 @@ extern "C" int dsa_compressor_fwd_tnd(const float* kv, const float* score, const
   const int groups = kThreads / lanes;
   const int64_t grid = (n_blocks + groups - 1) / groups;
   const size_t shm = (size_t)groups * ((lanes + 63) / 64 + 1) * sizeof(float);
+  const TimedLaunch tl("compressor_kernel", (hipStream_t)stream);
   compressor_kernel<<<(unsigned)grid, kThreads, shm, (hipStream_t)stream>>>(
       kv, score, ape, norm_weight, out, out_dtype == DSA_BF16, n_blocks, (int)n_blocks, (int)d, (int)ratio,
       overlap ? 1 : 0, norm_eps, block_starts, positions, n_tokens, rope_cs, n_pos, (int)rope_dim);

@@ -26,6 +26,27 @@ constexpr float kLn2 = 0.6931471805599453f;
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// ----- optional per-kernel timing (host) -----
+// While dsa_kernel_timing(1) is in force, a TimedLaunch scope around a kernel launch
+// records a HIP event before and after it on the launch stream; dsa_kernel_timing_get
+// sums the elapsed times per kernel name.  Off (no event calls) by default.
+bool kernel_timing_on();
+void kernel_timing_begin(hipStream_t st, hipEvent_t* ev);
+void kernel_timing_end(const char* name, hipStream_t st, hipEvent_t* ev);
+struct TimedLaunch {
+  const char* name;
+  hipStream_t st;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  TimedLaunch(const char* n, hipStream_t s) : name(n), st(s) {
+    if (kernel_timing_on()) kernel_timing_begin(st, ev);
+  }
+  ~TimedLaunch() {
+    if (ev[0]) kernel_timing_end(name, st, ev);
+  }
+  TimedLaunch(const TimedLaunch&) = delete;
+  TimedLaunch& operator=(const TimedLaunch&) = delete;
+};
+
 // ----- bf16 helpers -----
 __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }

@@ -106,6 +106,7 @@ template <bool kFill>
 void launch_csr_count(bool vec, unsigned grid, size_t lds, hipStream_t st, const int32_t* idx, int* counts,
                       int* cursor, int* pairs, int S, int s_kv, int K, int64_t q_offset, int row0, int rows, int b,
                       int n_ranges, int rows_per_wg) {
+  const TimedLaunch tl(kFill ? "csr_count_kernel<fill>" : "csr_count_kernel<count>", st);
   if (vec)
     csr_count_kernel<kFill, true><<<grid, 256, lds, st>>>(idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
                                                           rows, b, n_ranges, rows_per_wg);
@@ -321,18 +322,28 @@ inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, 
   // about four pairs per key of a range per workgroup
   const int64_t want = 4 * (int64_t)s_kv / (K > 0 ? K : 1);
   const int rows_per_wg = (int)(want < kCsrRowsMin ? kCsrRowsMin : want > kCsrRowsMax ? kCsrRowsMax : want);
-  zero_i32_kernel<<<ceil_div(s_kv + 1, 256), 256, 0, st>>>(counts, s_kv + 1);
+  {
+    const TimedLaunch tl("zero_i32_kernel", st);
+    zero_i32_kernel<<<ceil_div(s_kv + 1, 256), 256, 0, st>>>(counts, s_kv + 1);
+  }
   const int64_t cgrid = ceil_div(rows, rows_per_wg) * (int64_t)n_ranges;
   if (cgrid > 2147483647LL) return set_error(DSA_ERR_INVALID_ARG, "csr_reduce: too many rows x keys");
   const int64_t row_base = (int64_t)b * S + row0;  // int4 loads need 16-byte aligned index rows
   const bool vec = K % 4 == 0 && ((uintptr_t)(idx + row_base * K) % 16) == 0;
   launch_csr_count<false>(vec, (unsigned)cgrid, hist_bytes, st, idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
                           rows, b, n_ranges, rows_per_wg);
-  csr_scan_kernel<<<1, 1024, 0, st>>>(counts, row_ptr, cursor, s_kv);
+  {
+    const TimedLaunch tl("csr_scan_kernel", st);
+    csr_scan_kernel<<<1, 1024, 0, st>>>(counts, row_ptr, cursor, s_kv);
+  }
   launch_csr_count<true>(vec, (unsigned)cgrid, hist_bytes, st, idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
                          rows, b, n_ranges, rows_per_wg);
-  csr_seg_key_kernel<<<ceil_div(s_kv, 256), 256, 0, st>>>(row_ptr, seg_key, s_kv);
+  {
+    const TimedLaunch tl("csr_seg_key_kernel", st);
+    csr_seg_key_kernel<<<ceil_div(s_kv, 256), 256, 0, st>>>(row_ptr, seg_key, s_kv);
+  }
   const unsigned rgrid = ceil_div(ceil_div((int64_t)rows * K, kSegPairs), 4);
+  const TimedLaunch tl(row_chunks == 72 ? "dkv_reduce_kernel<72>" : "dkv_reduce_kernel<16>", st);
   if (row_chunks == 72)
     dkv_reduce_kernel<72><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, s_kv, rows, K, b);
   else if (row_chunks == 16)

@@ -546,10 +546,14 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
     uint8_t* pieces = (uint8_t*)workspace;
     float* pscale = (float*)(pieces + rows * kLinPieces * kD);
     const uint8_t* qp = (const uint8_t*)q;
-    indexer_lin_pieces_kernel<64><<<(unsigned)ceil_div(rows, kThreads / 64), kThreads, 0, st>>>(qp, q_scale, w,
-                                                                                               pieces, pscale, rows);
+    {
+      const TimedLaunch tl("indexer_lin_pieces_kernel<64>", st);
+      indexer_lin_pieces_kernel<64><<<(unsigned)ceil_div(rows, kThreads / 64), kThreads, 0, st>>>(qp, q_scale, w,
+                                                                                                 pieces, pscale, rows);
+    }
     using Tl = IdxTile<true, 4>;
     dim3 grid(ceil_div(s_q, Tl::kQ), ceil_div(s_k, Tl::kSpan), (unsigned)batch);
+    const TimedLaunch tl("indexer_tile_kernel<fp8, 4, split>", st);
     indexer_tile_kernel<true, 4, true><<<grid, kThreads, 0, st>>>(qp, q_scale, (const uint8_t*)k, k_scale, w, scores,
                                                                   (int)s_q, (int)s_k, ld_scores, q_offset,
                                                                   (int)cmp_ratio, pieces, pscale);
@@ -562,6 +566,7 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
   do {                                                                                                             \
     using Tl = IdxTile<FP8, HT>;                                                                                   \
     dim3 grid(ceil_div(s_q, Tl::kQ), ceil_div(s_k, Tl::kSpan), (unsigned)batch);                                          \
+    const TimedLaunch tl("indexer_tile_kernel", st);                                                               \
     indexer_tile_kernel<FP8, HT, false><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, (int)s_q,      \
                                                                    (int)s_k, ld_scores, q_offset, (int)cmp_ratio,   \
                                                                    nullptr, nullptr);                              \

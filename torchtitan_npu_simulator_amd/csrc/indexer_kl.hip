@@ -510,6 +510,7 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
   if (!(n_heads == kH && head_dim == kD)) {
     if (s_q > 2147483647LL) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: sizes out of range");
     dim3 grid((unsigned)s_q, (unsigned)batch);
+    const TimedLaunch tl("indexer_kl_generic_kernel", st);
     indexer_kl_generic_kernel<<<grid, 256, topk * 4, st>>>(
         (const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass, dq_idx, dk_idx_accum, dw, loss_rows,
         (int)s_q, (int)s_k, (int)n_heads, (int)head_dim, (int)topk, q_offset, loss_scale, eps, grad_scale,
@@ -532,9 +533,12 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
   for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
     const int rows_c = (int)std::min<int64_t>(plan.rows, s_q - r0);
     dim3 grid((unsigned)rows_c, (unsigned)batch);
-    indexer_kl_mfma_kernel<<<grid, 256, 0, st>>>((const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass,
-                                                 dq_idx, dw, loss_rows, ck, (int)s_q, (int)s_k, (int)topk, q_offset,
-                                                 loss_scale, eps, grad_scale, grad_scale_dev, (int)r0);
+    {
+      const TimedLaunch tl("indexer_kl_mfma_kernel", st);
+      indexer_kl_mfma_kernel<<<grid, 256, 0, st>>>((const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass,
+                                                   dq_idx, dw, loss_rows, ck, (int)s_q, (int)s_k, (int)topk, q_offset,
+                                                   loss_scale, eps, grad_scale, grad_scale_dev, (int)r0);
+    }
     if (int rc = check_launch("dsa_indexer_kl_grad(mfma)")) return rc;
     for (int b = 0; b < (int)batch; ++b)
       if (int rc = csr_reduce(indices, ck, dk_idx_accum, pairs, csr, (int)s_q, (int)s_k, (int)topk, q_offset, (int)r0,

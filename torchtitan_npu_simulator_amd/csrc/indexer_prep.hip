@@ -172,6 +172,7 @@ extern "C" int dsa_indexer_prep(const void* x, void* y, uint8_t* q8, float* scal
   if (vecs == 0) return DSA_OK;
   const int64_t grid = (vecs * 16 + kThreads - 1) / kThreads;
   if (grid > INT32_MAX) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_prep: too many rows");
+  const TimedLaunch tl("indexer_prep_kernel", (hipStream_t)stream);
   indexer_prep_kernel<<<(unsigned)grid, kThreads, 0, (hipStream_t)stream>>>(
       (const uint16_t*)x, (uint16_t*)y, q8, scale, vecs, (int)heads, seq_len, rope_cs, n_pos, positions, pos_offset,
       (int)rope_dim, (int)rope_start, interleaved ? 1 : 0, hadamard ? 1 : 0);

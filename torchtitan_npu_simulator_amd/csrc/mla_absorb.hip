@@ -234,6 +234,7 @@ extern "C" int dsa_mla_absorb(const void* a, int64_t lda, const void* wt, void* 
   const uint16_t* ap = (const uint16_t*)a;
   const uint16_t* wp = (const uint16_t*)wt;
   const uint16_t* ep = (const uint16_t*)append;
+  const TimedLaunch tl(q_shape ? "mla_absorb_q_kernel" : "mla_absorb_o_kernel", st);
   if (q_shape)
     mla_absorb_q_kernel<<<grid, kThreads, 0, st>>>(ap, lda, wp, (uint16_t*)c, ldc, ep, ld_append, (int)append_width,
                                                    tokens, (int)heads);

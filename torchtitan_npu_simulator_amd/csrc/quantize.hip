@@ -95,6 +95,7 @@ template <typename T>
 void launch_quantize(bool vec, const void* x, uint8_t* q, float* scale, int64_t rows, int D, int lg, hipStream_t st) {
   const int64_t threads = rows << lg;
   const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
+  const TimedLaunch tl("quantize_fp8_kernel", st);
   if (vec)
     quantize_fp8_kernel<T, true><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), q, scale, rows, D, lg);
   else

@@ -139,7 +139,9 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   const float delta = hok ? dlt : 0.f;
   const float scale_log2 = scale * kLog2e;
 #pragma unroll
-  for (int st = 0; st < kLat; ++st) asm volatile("" : "+v"(qb[st]), "+v"(db[st]));  // landed before any DMA
+  // landed before any DMA; held in AGPRs, which the MFMAs read directly as B operands, so
+  // the VGPRs stay free for the softmax and for prefetching the K operands from LDS
+  for (int st = 0; st < kLat; ++st) asm volatile("" : "+a"(qb[st]), "+a"(db[st]));
 
   uint32_t ka_off[4];  // A operand (K row n, chunk (2s + h) ^ swz_kv(n)), s = 4u + s0 -> + 128 u
 #pragma unroll
@@ -199,12 +201,21 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
     const uint32_t vmh = vm >> (4 * h);  // bit 8j + i: key 8j + 4h + i
     const int sb = pb & 1;
     if (piece == 0) {
+      if (vm == 0xffffffffu) {  // (wave-uniform) every key of the block is valid: no masking
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const bool ok = (vmh >> (8 * (v >> 2) + (v & 3))) & 1u;
-        const float p = ok ? __builtin_amdgcn_exp2f(sp[v] * scale_log2 - lse2) : 0.f;
-        pv[v] = p;
-        dv[v] = p * (pp[v] - delta) * scale;
+        for (int v = 0; v < 16; ++v) {
+          const float p = __builtin_amdgcn_exp2f(sp[v] * scale_log2 - lse2);
+          pv[v] = p;
+          dv[v] = p * (pp[v] - delta) * scale;
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const bool ok = (vmh >> (8 * (v >> 2) + (v & 3))) & 1u;
+          const float p = ok ? __builtin_amdgcn_exp2f(sp[v] * scale_log2 - lse2) : 0.f;
+          pv[v] = p;
+          dv[v] = p * (pp[v] - delta) * scale;
+        }
       }
     } else if (piece == 1 || piece == 2) {
       const float* src = piece == 1 ? dv : pv;
@@ -254,9 +265,11 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   // DMA'd into the other tile, with P / dS / G / mass of block blk-1 and the G and mass
   // stores of block blk-2 spread over its MFMA batches; the iteration ends with its DMAs
   // landed and one barrier (which also publishes blk-1's stage for its flush).
-  f32x16 sprev = (f32x16){0.f}, pprev = (f32x16){0.f};
+  // (the loop below is unrolled by two so that block blk's accumulators and block blk-1's
+  // alternate between two register sets instead of being copied every block)
+  f32x16 s_a = (f32x16){0.f}, p_a = (f32x16){0.f}, s_b = (f32x16){0.f}, p_b = (f32x16){0.f};
   uint32_t vm_prev = 0u;
-  for (int blk = 0; blk < nblk; ++blk) {
+  auto block_iter = [&](int blk, f32x16& sacc, f32x16& pacc, const f32x16& sprev, const f32x16& pprev) {
     if (wave == 0 && blk + 3 < nblk)
       Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
     const lds_char* tb = lds_bytes(&tile[blk & 1][0]);
@@ -265,7 +278,8 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
     const int rows_left = K - (blk + 1) * kBN;
     const uint32_t vm_next = Gather::ring_valid(ring, lane, lim, rows_left);
     uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
-    f32x16 sacc = (f32x16){0.f}, pacc = (f32x16){0.f};
+    sacc = (f32x16){0.f};
+    pacc = (f32x16){0.f};
     u32x4 a[2][kQBatch], rope[kQBatch];
     auto read_a = [&](u32x4 (&dst)[kQBatch], int sb) {
 #pragma unroll
@@ -320,14 +334,20 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     __syncthreads();
-    sprev = sacc;
-    pprev = pacc;
     vm_prev = vm_cur;
     vm_cur = vm_next;
+  };
+  int blk = 0;
+  for (; blk + 1 < nblk; blk += 2) {
+    block_iter(blk, s_a, p_a, s_b, p_b);
+    block_iter(blk + 1, s_b, p_b, s_a, p_a);
   }
+  if (blk < nblk) block_iter(blk, s_a, p_a, s_b, p_b);
   // the last block's P / dS / G / mass, the stores of the one before, then its own stores
+  const bool last_a = nblk & 1;
+  const f32x16 s_last = last_a ? s_a : s_b, p_last = last_a ? p_a : p_b;
 #pragma unroll
-  for (int piece = 0; piece < 4; ++piece) pds_piece(piece, sprev, pprev, vm_prev, nblk - 1);
+  for (int piece = 0; piece < 4; ++piece) pds_piece(piece, s_last, p_last, vm_prev, nblk - 1);
   if (nblk > 1) {
     flush_part(nblk - 2, 0);
     flush_part(nblk - 2, 1);
@@ -864,9 +884,12 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
     if (s_q > 2147483647LL || n_heads > 65535)
       return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: sizes out of range");
     dim3 grid((unsigned)s_q, (unsigned)n_heads, (unsigned)batch);
-    bwd_exact_f32_kernel<<<grid, 256, topk * 4, st>>>(
-        (const float*)q, (const float*)kv, indices, (const float*)out, (const float*)dout, softmax_max, softmax_sum,
-        (float*)dq, dkv_accum, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset);
+    {
+      const TimedLaunch tl("bwd_exact_f32_kernel", st);
+      bwd_exact_f32_kernel<<<grid, 256, topk * 4, st>>>(
+          (const float*)q, (const float*)kv, indices, (const float*)out, (const float*)dout, softmax_max, softmax_sum,
+          (float*)dq, dkv_accum, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset);
+    }
     return check_launch("dsa_sparse_mla_bwd(f32)");
   }
   if (dtype != DSA_BF16) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: dtype %d", dtype);
@@ -895,27 +918,37 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
     const int rows = (int)std::min<int64_t>(plan.rows, s_q - r0);
     {
       const int64_t groups = batch * rows * n_heads;
+      const TimedLaunch tl("bwd_delta_kernel", st);
       bwd_delta_kernel<<<(unsigned)((groups * 16 + 255) / 256), 256, 0, st>>>(
           (const uint16_t*)out, (const uint16_t*)dout, dbuf, groups, (int)s_q, (int)n_heads, (int)r0, rows);
       if (int rc = check_launch("dsa_sparse_mla_bwd(delta)")) return rc;
     }
     dim3 ga((unsigned)rows, 1, (unsigned)batch);
-    bwd_sdp_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout,
-                                       softmax_max, softmax_sum, dbuf, gbuf, mass, (int)s_q, (int)s_kv,
-                                       (int)n_heads, (int)topk, scale, q_offset, (int)r0);
+    {
+      const TimedLaunch tl("bwd_sdp_kernel", st);
+      bwd_sdp_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout,
+                                         softmax_max, softmax_sum, dbuf, gbuf, mass, (int)s_q, (int)s_kv,
+                                         (int)n_heads, (int)topk, scale, q_offset, (int)r0);
+    }
     if (int rc = check_launch("dsa_sparse_mla_bwd(sdp)")) return rc;
-    bwd_dqk_kernel<<<ga, 512, 0, st>>>((const uint16_t*)kv, indices, gbuf, (uint16_t*)dq, (int)s_q, (int)s_kv,
-                                       (int)n_heads, (int)topk, q_offset, (int)r0);
+    {
+      const TimedLaunch tl("bwd_dqk_kernel", st);
+      bwd_dqk_kernel<<<ga, 512, 0, st>>>((const uint16_t*)kv, indices, gbuf, (uint16_t*)dq, (int)s_q, (int)s_kv,
+                                         (int)n_heads, (int)topk, q_offset, (int)r0);
+    }
     if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
     dim3 gb((unsigned)rows, (unsigned)batch);
-    if (hgroups == 1)
-      bwd_contrib_kernel<1><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf,
-                                                      (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0,
-                                                      rows);
-    else
-      bwd_contrib_kernel<2><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf,
-                                                      (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0,
-                                                      rows);
+    {
+      const TimedLaunch tl(hgroups == 1 ? "bwd_contrib_kernel<1>" : "bwd_contrib_kernel<2>", st);
+      if (hgroups == 1)
+        bwd_contrib_kernel<1><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf,
+                                                        cbuf, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset,
+                                                        (int)r0, rows);
+      else
+        bwd_contrib_kernel<2><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf,
+                                                        cbuf, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset,
+                                                        (int)r0, rows);
+    }
     if (int rc = check_launch("dsa_sparse_mla_bwd(contrib)")) return rc;
     for (int b = 0; b < (int)batch; ++b)
       if (int rc = csr_reduce(indices, cbuf, dkv_accum, pairs, counts, (int)s_q, (int)s_kv, (int)topk, q_offset,

@@ -689,11 +689,15 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
     if (s_kv > GatherGeom::kMaxRows)
       return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: S_kv > %lld", (long long)GatherGeom::kMaxRows);
     dim3 grid((unsigned)s_q, ceil_div(n_heads, kFwdHeads), (unsigned)batch);
-    sparse_mla_fwd_bf16_kernel<<<grid, kFwdThreads, 0, st>>>(
-        (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
-        (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
+    {
+      const TimedLaunch tl("sparse_mla_fwd_bf16_kernel", st);
+      sparse_mla_fwd_bf16_kernel<<<grid, kFwdThreads, 0, st>>>(
+          (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
+          (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
+    }
     if (int rc = check_launch("dsa_sparse_mla_fwd(bf16)")) return rc;
     dim3 fgrid((unsigned)s_q, 1, (unsigned)batch);
+    const TimedLaunch tl("sparse_mla_fwd_exact_kernel<fixup>", st);
     sparse_mla_fwd_exact_kernel<uint16_t><<<fgrid, 256, sc_bytes, st>>>(
         (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
         (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset, 1);
@@ -701,6 +705,7 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
   }
   if (dtype == DSA_F32) {
     dim3 grid((unsigned)s_q, (unsigned)n_heads, (unsigned)batch);
+    const TimedLaunch tl("sparse_mla_fwd_exact_kernel<float>", st);
     sparse_mla_fwd_exact_kernel<float><<<grid, 256, sc_bytes, st>>>(
         (const float*)q, (const float*)kv, indices, (float*)out, softmax_max, softmax_sum, (int)s_q, (int)s_kv,
         (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset, 0);

@@ -311,6 +311,7 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
 template <int kR, bool kSingle>
 void launch_topk(bool vec, dim3 grid, hipStream_t st, const float* scores, int32_t* indices, float* values, int S,
                  int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio, int64_t index_offset) {
+  const TimedLaunch tl("topk_kernel", st);
   if (vec)
     topk_kernel<kR, kSingle, true><<<grid, kThreads, 0, st>>>(scores, indices, values, S, s_k, ld, k, q_offset,
                                                               cmp_ratio, index_offset);
