@@ -10,8 +10,9 @@
  *
  * Reference interfaces each entry point replaces (paths relative to the
  * torchtitan-npu reference repository):
- *   dsa_indexer_fwd + dsa_topk   torch_npu.npu_lightning_indexer
- *                                (converters/kernels/dsa.py:217-226;
+ *   dsa_lightning_indexer        torch_npu.npu_lightning_indexer (scores + top-k in one call;
+ *   (= dsa_indexer_fwd +          the two halves are also exported on their own)
+ *      dsa_topk)                 (converters/kernels/dsa.py:217-226;
  *                                 ops/aclnn/lightning_indexer/binding.cpp:12-36)
  *   dsa_sparse_mla_fwd           torch_npu.npu_sparse_flash_attention, attention_mode=2
  *                                (converters/kernels/dsa.py:238-253;
@@ -153,6 +154,26 @@ int dsa_indexer_fwd_noalloc(const void* q, const float* q_scale, const void* k, 
 int dsa_topk(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
              int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset,
              void* stream);
+
+/*
+ * The fused lightning indexer (reference: npu_lightning_indexer, ops/aclnn/lightning_indexer/
+ * binding.cpp:14-31, as called by converters/kernels/dsa.py:217-226): the scores of
+ * dsa_indexer_fwd_ws followed by dsa_topk, with the fp32 score rows kept in `workspace`
+ * instead of a caller-visible buffer.  Same arguments and results as those two calls
+ * (indices [B, S, k] int32 ascending with -1 padding, values [B, S, k] fp32 or NULL), with
+ * ld_scores = s_k.  The score kernels leave the key spans past every query's causal
+ * frontier unwritten and the top-k reads only each row's valid prefix, so the masked part
+ * of the score matrix costs no memory traffic.
+ * workspace: 256-byte aligned; dsa_lightning_indexer_workspace_size(.., max_rows) bytes
+ * process max_rows query rows per pass (every row of every batch at once when max_rows >= S;
+ * smaller workspaces run batch by batch in row chunks).  Calls on one stream may share it.
+ */
+int64_t dsa_lightning_indexer_workspace_size(int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                                             int64_t head_dim, int dtype, int64_t max_rows);
+int dsa_lightning_indexer(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
+                          int32_t* indices, float* values, int dtype, int64_t batch, int64_t s_q, int64_t s_k,
+                          int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset, int64_t cmp_ratio,
+                          int64_t index_offset, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Gathered sparse MLA attention forward (reference: npu_sparse_flash_attention with

@@ -75,24 +75,19 @@ def test_sharedkv_rejects_what_it_does_not_support():
         ops.npu_sparse_attn_sharedkv(q, kv, ori_mask_mode=3)
 
 
-def _fake_indexer_calls():
-    def fake_scores(q, k, w, **kw):
-        return torch.randn(q.shape[0], q.shape[1], k.shape[1])
+def _fake_indexer_call():
+    def fake_indexer(q, k, w, kk, return_value=False, **kw):
+        B, S = q.shape[:2]
+        return torch.zeros(B, S, kk, dtype=torch.int32), (torch.randn(B, S, kk) if return_value else None)
 
-    def fake_topk(sc, k, **kw):
-        B, S = sc.shape[:2]
-        return torch.zeros(B, S, k, dtype=torch.int32), torch.randn(B, S, k)
-
-    return patch.object(ops, "indexer_scores", side_effect=fake_scores), \
-        patch.object(ops, "topk_select", side_effect=fake_topk)
+    return patch.object(ops, "lightning_indexer", side_effect=fake_indexer)
 
 
 @pytest.mark.parametrize("qdt,vdt", [(torch.bfloat16, torch.bfloat16), (torch.float8_e4m3fn, torch.bfloat16),
                                      (torch.float32, torch.float32)])
 def test_indexer_values_in_query_dtype(qdt, vdt):
     B, S, H, D, K = 1, 12, 4, 8, 5
-    p1, p2 = _fake_indexer_calls()
-    with p1, p2:
+    with _fake_indexer_call():
         idx, vals = ops.npu_lightning_indexer(torch.zeros(B, S, H, D).to(qdt), torch.zeros(B, S, 1, D).to(qdt),
                                               torch.zeros(B, S, H), sparse_count=K, return_value=True)
     assert idx.shape == (B, S, 1, K) and idx.dtype == torch.int32

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -41,6 +41,9 @@ _SIGNATURES = {
     "dsa_attn_sink_fold": ([_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp], _i32),
     "dsa_attn_sink_grad": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp], _i32),
     "dsa_topk": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _i32),
+    "dsa_lightning_indexer_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _i32, _i64], _i64),
+    "dsa_lightning_indexer": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                               _i64, _vp, _i64, _vp], _i32),
     "dsa_sparse_mla_fwd": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _vp],
         _i32,

@@ -26,6 +26,15 @@ constexpr float kLn2 = 0.6931471805599453f;
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// ----- lightning-indexer scores shared by the entry points (host) -----
+// dsa_indexer_fwd_ws's work; fill_masked = false leaves the key spans that lie past every
+// query's causal frontier of a tile unwritten (for consumers that read only each row's
+// valid prefix t < (s + q_offset + 1) / cmp_ratio, such as dsa_topk).
+int indexer_fwd(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
+                float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                int64_t head_dim, int64_t ld_scores, int64_t q_offset, int64_t cmp_ratio, void* workspace,
+                int64_t workspace_bytes, void* stream, bool fill_masked);
+
 // ----- optional per-kernel timing (host) -----
 // While dsa_kernel_timing(1) is in force, a TimedLaunch scope around a kernel launch
 // records a HIP event before and after it on the launch stream; dsa_kernel_timing_get

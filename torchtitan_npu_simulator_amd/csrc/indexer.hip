@@ -23,7 +23,8 @@ constexpr int kThreads = 256;
 // The 16x16 C tile (lane: key = l%16, heads 4(l/16)..+3) gets relu * w in registers, is
 // summed over the head tiles in-lane and over the 4 lane groups with two lane swaps; a
 // tile's scores are staged in LDS and written as whole rows.  Key ranges past every
-// query's causal frontier are written as -inf without any MFMA.
+// query's causal frontier are written as -inf without any MFMA, or left unwritten for
+// consumers that read only each row's valid prefix (the fused indexer + top-k).
 //
 // Linear split (kLin, fp8 with two queries per wave): relu(x) = (x + |x|) / 2, so
 //   sum_h c_h relu(x_h) = sum_h (c_h/2) |x_h| + u . k,   u = sum_h (c_h/2) q_h   (x_h = q_h . k)
@@ -164,7 +165,7 @@ __global__ void __launch_bounds__(kThreads, 2)
 indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_scale, const uint8_t* __restrict__ k,
                     const float* __restrict__ k_scale, const float* __restrict__ w, float* __restrict__ scores,
                     int S, int s_k, int64_t ld, int64_t q_offset, int cmp_ratio,
-                    const uint8_t* __restrict__ lin_pieces, const float* __restrict__ lin_scale) {
+                    const uint8_t* __restrict__ lin_pieces, const float* __restrict__ lin_scale, int fill_masked) {
   using T = IdxTile<kFp8, kHeadTiles>;
   static_assert(!kLin || (kFp8 && T::kQw == 2), "the linear split pairs two fp8 queries per wave");
   constexpr int H = kHeadTiles * 16;
@@ -192,7 +193,7 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
   const int64_t q_row0 = (int64_t)b * S;
 
   if (t_work <= t0) {  // the whole key span lies past every query's frontier
-    fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0, t_end, tid);
+    if (fill_masked) fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0, t_end, tid);
     return;
   }
   const int nsub = (t_work - t0 + kK - 1) / kK;  // key tiles with work
@@ -469,7 +470,7 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
     }
   }
   // key tiles of the span past every frontier
-  fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0 + nsub * kK, t_end, tid);
+  if (fill_masked) fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0 + nsub * kK, t_end, tid);
 }
 
 // Generic path (any H, D; fp32 arithmetic): one thread per (query, key).
@@ -521,10 +522,13 @@ bool lin_split_shape(int dtype, int64_t n_heads, int64_t head_dim) {
   return dtype == DSA_FP8_E4M3 && n_heads == 64 && head_dim == kD;
 }
 
+}  // namespace
+
 int indexer_fwd(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
                 float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
                 int64_t head_dim, int64_t ld_scores, int64_t q_offset, int64_t cmp_ratio, void* workspace,
-                int64_t workspace_bytes, void* stream) {
+                int64_t workspace_bytes, void* stream, bool fill_masked) {
+  const int fm = fill_masked ? 1 : 0;
   if (!q || !k || !w || !scores) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: null pointer");
   if (batch <= 0 || s_q <= 0 || s_k <= 0 || n_heads <= 0 || head_dim <= 0 || ld_scores < s_k || cmp_ratio <= 0)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd: bad sizes");
@@ -556,7 +560,7 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
     const TimedLaunch tl("indexer_tile_kernel<fp8, 4, split>", st);
     indexer_tile_kernel<true, 4, true><<<grid, kThreads, 0, st>>>(qp, q_scale, (const uint8_t*)k, k_scale, w, scores,
                                                                   (int)s_q, (int)s_k, ld_scores, q_offset,
-                                                                  (int)cmp_ratio, pieces, pscale);
+                                                                  (int)cmp_ratio, pieces, pscale, fm);
     return check_launch("dsa_indexer_fwd_ws(mfma, linear split)");
   }
   if (mfma_shape) {
@@ -569,7 +573,7 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
     const TimedLaunch tl("indexer_tile_kernel", st);                                                               \
     indexer_tile_kernel<FP8, HT, false><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, (int)s_q,      \
                                                                    (int)s_k, ld_scores, q_offset, (int)cmp_ratio,   \
-                                                                   nullptr, nullptr);                              \
+                                                                   nullptr, nullptr, fm);                          \
   } while (0)
     const int ht = (int)(n_heads / 16);
     if (dtype == DSA_FP8_E4M3) {
@@ -618,7 +622,6 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
   return check_launch("dsa_indexer_fwd(generic)");
 }
 
-}  // namespace
 }  // namespace dsa
 
 extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* k, const float* k_scale,
@@ -626,7 +629,7 @@ extern "C" int dsa_indexer_fwd(const void* q, const float* q_scale, const void* 
                                int64_t n_heads, int64_t head_dim, int64_t ld_scores, int64_t q_offset,
                                int64_t cmp_ratio, void* stream) {
   return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim, ld_scores,
-                          q_offset, cmp_ratio, nullptr, 0, stream);
+                          q_offset, cmp_ratio, nullptr, 0, stream, true);
 }
 
 extern "C" int64_t dsa_indexer_fwd_workspace_size(int64_t batch, int64_t s_q, int64_t n_heads, int64_t head_dim,
@@ -640,7 +643,7 @@ extern "C" int dsa_indexer_fwd_ws(const void* q, const float* q_scale, const voi
                                   int64_t n_heads, int64_t head_dim, int64_t ld_scores, int64_t q_offset,
                                   int64_t cmp_ratio, void* workspace, int64_t workspace_bytes, void* stream) {
   return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim, ld_scores,
-                          q_offset, cmp_ratio, workspace, workspace_bytes, stream);
+                          q_offset, cmp_ratio, workspace, workspace_bytes, stream, true);
 }
 
 // ----- the entry point that allocates nothing -----
@@ -691,7 +694,7 @@ extern "C" int dsa_indexer_fwd_noalloc(const void* q, const float* q_scale, cons
                                        int64_t q_offset, int64_t cmp_ratio, void* stream) {
   if (!dsa::lin_split_shape(dtype, n_heads, head_dim))  // no scratch on these shapes
     return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim,
-                            ld_scores, q_offset, cmp_ratio, nullptr, 0, stream);
+                            ld_scores, q_offset, cmp_ratio, nullptr, 0, stream, true);
   if (batch <= 0 || s_q <= 0) return dsa::set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_fwd_noalloc: bad sizes");
   const int64_t max_rows = dsa_indexer_fwd_noalloc_max_rows();
   if (batch > max_rows || s_q > max_rows / batch)
@@ -703,5 +706,5 @@ extern "C" int dsa_indexer_fwd_noalloc(const void* q, const float* q_scale, cons
   const int rc = dsa::noalloc_scratch((hipStream_t)stream, &ws);
   if (rc != DSA_OK) return rc;
   return dsa::indexer_fwd(q, q_scale, k, k_scale, w, scores, dtype, batch, s_q, s_k, n_heads, head_dim, ld_scores,
-                          q_offset, cmp_ratio, ws, batch * s_q * dsa::kLinRowBytes, stream);
+                          q_offset, cmp_ratio, ws, batch * s_q * dsa::kLinRowBytes, stream, true);
 }

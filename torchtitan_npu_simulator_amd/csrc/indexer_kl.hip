@@ -3,9 +3,10 @@
 //
 // Per query row s (one workgroup, 4 waves, wave w owns index heads 16w..16w+15), over
 // blocks of 64 selected slots whose key rows are DMA'd into a double-buffered LDS tile:
-//   phase 1  I_j = sum_h w_h relu(q_h . k_{idx_j}): S = q k^T on v_mfma_f32_16x16x32_bf16,
-//            relu * w summed in-lane and across lane groups; the four per-wave partials
-//            are written to LDS and added by one thread per slot (no LDS atomics)
+//   phase 1  I_j = sum_h w_h relu(q_h . k_{idx_j}): S = q k^T on v_mfma_f32_16x16x32_bf16 with
+//            the waves splitting the slots and each holding q of all 64 heads, so I_j is
+//            summed in-lane and across the lane groups of one wave; key rows go straight to
+//            VGPRs three slot groups ahead (no LDS, no barrier)
 //   phase 2  row statistics: softmax of I over usable slots, target t = mass / Z, the
 //            row loss Z * sum_{t>0} t (log max(t, eps) - log_softmax(I)) * loss_scale and
 //            g_j = dloss/dI_j = Z * loss_scale * grad_scale * (softmax_j * T - t_j)
@@ -63,7 +64,6 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
                        const float* __restrict__ grad_scale_dev, int row0) {
   __shared__ u32x4 kt[2][kTileC];           // gathered key rows [64][16 chunks], swizzled
   __shared__ float iv[kMaxK];               // I_j, then g_j
-  __shared__ float ip[4][kB];               // per-wave partial I of one block
   __shared__ uint16_t es[kB][kH + 8];       // E as [slot][head]
   __shared__ uint16_t eh[kH][kB + 8];       // E as [head][slot]
   __shared__ float red[4];
@@ -80,26 +80,8 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const int head_a = 16 * wave + col;  // A-operand row (head) of this lane
   const int nblocks = (K + kB - 1) / kB;
 
-  // A = q [16 heads x 32 d] per step c: lane (head col, g) holds q[head][32c + 8g .. +8]
-  u32x4 qa[kD / 32];
-  {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(qi + (row_id * kH + head_a) * kD);
-#pragma unroll
-    for (int c = 0; c < kD / 32; ++c) qa[c] = qh[4 * c + g];
-  }
-  // C layout of S = q k^T tiles: lane (slot col, g) holds heads 16w + 4g + r
-  float wr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) wr[r] = w[row_id * kH + 16 * wave + 4 * g + r];
   // the upstream gradient may live on the device (no host round trip for the caller)
-  float gsc = grad_scale_dev ? grad_scale * grad_scale_dev[0] : grad_scale;
-  // these operands must have arrived before the first DMA: a wait for them inside the loop
-  // would also wait for every row DMA in flight
-#pragma unroll
-  for (int c = 0; c < kD / 32; ++c) asm volatile("" : "+v"(qa[c]));
-#pragma unroll
-  for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(wr[r]));
-  asm volatile("" : "+v"(gsc));
+  const float gsc = grad_scale_dev ? grad_scale * grad_scale_dev[0] : grad_scale;
 
   // Key-row gather, 64 rows x 256 B per block: 4 DMA instructions per wave, instruction
   // J = 4 wave + i covering tile chunks [64J, 64J+64) (row p / 16, chunk (p % 16) ^ swz8(row)).
@@ -134,42 +116,66 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     gather(0, 0);
   };
   const uint32_t kt_base = (uint32_t)(uintptr_t)(&kt[0][0]);
-  auto s_tile = [&](uint32_t tb, int st) -> f32x4 {  // S tile (16 heads x 16 slots) of slot tile st
-    f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const int row = 16 * st + col;
-    u32x4 bk[kD / 32];
-#pragma unroll
-    for (int c = 0; c < kD / 32; ++c)
-      bk[c] = *(const lds_u32x4*)(uintptr_t)(tb + 16 * (row * kRowC + ((4 * c + g) ^ swz8(row))));
-#pragma unroll
-    for (int c = 0; c < kD / 32; ++c) acc = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk[c]), acc);
-    return acc;
-  };
 
   // ---------------- phase 1: index scores at the selected slots ----------------
-  start_pass();
-  for (int blk = 0; blk < nblocks; ++blk) {
-    const int buf = blk & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // tile[buf] and ring entry blk+1 landed for every wave; ip free
-    if (blk + 1 < nblocks) gather(blk + 1, buf ^ 1);
-    if (blk + 2 < nblocks) load_idx(blk + 2);
-    const uint32_t tb = kt_base + buf * (kTileC * 16);
-    f32x4 sv[4];
+  // Waves split the slots (wave w: slots 64 blk + 16 w + col) and hold q of all 64 heads as
+  // A operands, so each I_j is complete inside one wave: no LDS, no barrier.  Slot
+  // indices and the 256-byte key rows go straight to VGPRs by ordinary loads, three groups
+  // ahead (lane (slot col, g) holds d chunks 32 c + 8 g .. +8 of its slot's key, the B
+  // operand of S = q k^T).
+  {
+    u32x4 qall[4][kD / 32];  // q[16 ht + col][32 c + 8 g ..] (A operands, all heads)
+    float wall[4][4];        // w[16 ht + 4 g + r] (C rows of this lane)
 #pragma unroll
-    for (int st = 0; st < 4; ++st) sv[st] = s_tile(tb, st);
+    for (int ht = 0; ht < 4; ++ht) {
+      const u32x4* qh = reinterpret_cast<const u32x4*>(qi + (row_id * kH + 16 * ht + col) * kD);
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
+      for (int c = 0; c < kD / 32; ++c) qall[ht][c] = qh[4 * c + g];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wall[ht][r] = w[row_id * kH + 16 * ht + 4 * g + r];
+    }
+    const int nsb = (K + 15) / 16;  // 16-slot groups
+    auto slot_of = [&](int i) { return 16 * i + col; };  // group i = 4 blk + wave
+    auto load_idx1 = [&](int i) -> int {
+      const int sl = slot_of(i);
+      return (i < nsb && sl < K) ? ridx[sl] : -1;
+    };
+    auto load_rows = [&](int v, u32x4 (&dst)[kD / 32]) {
+      const int r = ok_slot(v, s_k, limit) ? v : 0;
+      const u32x4* kr = reinterpret_cast<const u32x4*>(kb + (int64_t)r * kD);
+#pragma unroll
+      for (int c = 0; c < kD / 32; ++c) dst[c] = kr[4 * c + g];
+    };
+    // this wave's groups are i = wave, wave + 4, ...; key rows kDepth groups ahead, slot
+    // indices one group further
+    constexpr int kDepth = 3;
+    u32x4 kq[kDepth][kD / 32];
+    int vnext = load_idx1(wave + 4 * kDepth);
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) load_rows(load_idx1(wave + 4 * d), kq[d]);
+    for (int i = wave; i < nsb; i += 4) {
+      const int vn2 = load_idx1(i + 4 * (kDepth + 1));
+      u32x4 knew[kD / 32];
+      load_rows(vnext, knew);
       float part = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) part = fmaf(wr[r], relu_bits(sv[st][r]), part);
+      for (int ht = 0; ht < 4; ++ht) {
+        f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < kD / 32; ++c) acc = mfma16x16x32(as_bf16x8(qall[ht][c]), as_bf16x8(kq[0][c]), acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) part = fmaf(wall[ht][r], relu_bits(acc[r]), part);
+      }
       part = xor32_sum(xor16_sum(part));
-      if (g == 0) ip[wave][16 * st + col] = part;
-    }
-    __syncthreads();
-    if (tid < kB) {
-      const int slot = blk * kB + tid;
-      if (slot < K) iv[slot] = (ip[0][tid] + ip[1][tid]) + (ip[2][tid] + ip[3][tid]);
+      const int sl = slot_of(i);
+      if (g == 0 && sl < K) iv[sl] = part;
+#pragma unroll
+      for (int d = 0; d + 1 < kDepth; ++d)
+#pragma unroll
+        for (int c = 0; c < kD / 32; ++c) kq[d][c] = kq[d + 1][c];
+#pragma unroll
+      for (int c = 0; c < kD / 32; ++c) kq[kDepth - 1][c] = knew[c];
+      vnext = vn2;
     }
   }
   __syncthreads();
@@ -229,6 +235,34 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   }
 
   // ---------------- phase 3: gradients ----------------
+  // A = q [16 heads x 32 d] per step c: lane (head col, g) holds q[16 w + col][32c + 8g .. +8];
+  // C layout of S = q k^T tiles: lane (slot col, g) holds heads 16w + 4g + r
+  u32x4 qa[kD / 32];
+  float wr[4];
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(qi + (row_id * kH + head_a) * kD);
+#pragma unroll
+    for (int c = 0; c < kD / 32; ++c) qa[c] = qh[4 * c + g];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wr[r] = w[row_id * kH + 16 * wave + 4 * g + r];
+  }
+  // these operands must have arrived before the first DMA: a wait for them inside the loop
+  // would also wait for every row DMA in flight
+#pragma unroll
+  for (int c = 0; c < kD / 32; ++c) asm volatile("" : "+v"(qa[c]));
+#pragma unroll
+  for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(wr[r]));
+  auto s_tile = [&](uint32_t tb, int st) -> f32x4 {  // S tile (16 heads x 16 slots) of slot tile st
+    f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int row = 16 * st + col;
+    u32x4 bk[kD / 32];
+#pragma unroll
+    for (int c = 0; c < kD / 32; ++c)
+      bk[c] = *(const lds_u32x4*)(uintptr_t)(tb + 16 * (row * kRowC + ((4 * c + g) ^ swz8(row))));
+#pragma unroll
+    for (int c = 0; c < kD / 32; ++c) acc = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk[c]), acc);
+    return acc;
+  };
   f32x4 dqa[kD / 16];
 #pragma unroll
   for (int t = 0; t < kD / 16; ++t) dqa[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -273,19 +307,30 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       f32x4 sv[4];
 #pragma unroll
       for (int st = 0; st < 4; ++st) sv[st] = s_tile(tb, st);
+      // E = g_j w_h [S > 0] in bf16: es[slot][head] takes the lane's four heads as one 8-byte
+      // store; for eh[head][slot] the lanes of adjacent slots (col, col ^ 1) swap two values
+      // so that each writes two whole dwords (slot pair, one head each)
+      const bool odd = col & 1;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int sl = 16 * st + col;
         const int slot = blk * kB + sl;
         const float gj = slot < K ? iv[slot] : 0.f;
+        float e[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float e = sv[st][r] > 0.f ? gj * wr[r] : 0.f;
+          e[r] = sv[st][r] > 0.f ? gj * wr[r] : 0.f;
           dwp[r] += gj * relu_bits(sv[st][r]);
-          const uint16_t eb = f_to_bf16(e);
-          es[sl][16 * wave + 4 * g + r] = eb;
-          eh[16 * wave + 4 * g + r][sl] = eb;
         }
+        const uint32_t p01 = pack_bf16x2(e[0], e[1]), p23 = pack_bf16x2(e[2], e[3]);
+        *reinterpret_cast<uint2*>(&es[sl][16 * wave + 4 * g]) = make_uint2(p01, p23);
+        const uint32_t recv = __float_as_uint(lane_xor<1>(__uint_as_float(odd ? p01 : p23)));
+        // even lane: heads 4g, 4g+1 of slots (sl, sl+1); odd lane: heads 4g+2, 4g+3 of (sl-1, sl)
+        const uint32_t da = odd ? ((recv & 0xffffu) | (p23 << 16)) : ((p01 & 0xffffu) | (recv << 16));
+        const uint32_t db = odd ? ((recv >> 16) | (p23 & 0xffff0000u)) : ((p01 >> 16) | (recv & 0xffff0000u));
+        const int ha = 16 * wave + 4 * g + (odd ? 2 : 0);
+        *reinterpret_cast<uint32_t*>(&eh[ha][sl & ~1]) = da;
+        *reinterpret_cast<uint32_t*>(&eh[ha + 1][sl & ~1]) = db;
       }
       __syncthreads();
       // dq^T[16 d x 16 heads] += k^T[16 d x 32 slots] E^T[32 slots x 16 heads], two k-steps
@@ -298,13 +343,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
           const int c0 = 2 * dt + ((col & 3) >> 1);
           const uint32_t a1 = tb + 16 * (r1 * kRowC + (c0 ^ swz8(r1))) + 8 * (col & 1);
           const uint32_t a2 = tb + 16 * (r2 * kRowC + (c0 ^ swz8(r2))) + 8 * (col & 1);
-          const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a1);
-          const i16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)a2);
-          u32x4 av;
-          av[0] = (uint32_t)(uint16_t)v1[0] | ((uint32_t)(uint16_t)v1[1] << 16);
-          av[1] = (uint32_t)(uint16_t)v1[2] | ((uint32_t)(uint16_t)v1[3] << 16);
-          av[2] = (uint32_t)(uint16_t)v2[0] | ((uint32_t)(uint16_t)v2[1] << 16);
-          av[3] = (uint32_t)(uint16_t)v2[2] | ((uint32_t)(uint16_t)v2[3] << 16);
+          const u32x4 av = lds_read_tr_pair((const lds_char*)(uintptr_t)a1, (const lds_char*)(uintptr_t)a2);
           dqa[dt] = mfma16x16x32(as_bf16x8(av), as_bf16x8(eb), dqa[dt]);
         }
       }

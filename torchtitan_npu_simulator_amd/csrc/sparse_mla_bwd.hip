@@ -308,8 +308,10 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
           sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(rope[u]), sacc);
         }
       }
-      if constexpr (nb < 4) {
-        if (blk > 0) pds_piece(nb, sprev, pprev, vm_prev, blk - 1);
+      // the four pieces go to every other batch so that their VALU work spreads over the
+      // block's MFMAs
+      if constexpr (nb % 2 == 0 && nb / 2 < 4) {
+        if (blk > 0) pds_piece(nb / 2, sprev, pprev, vm_prev, blk - 1);
       }
       // one wave per SIMD issues in order: put the batch's VALU, LDS and memory work in the
       // gaps between its MFMAs, not after them

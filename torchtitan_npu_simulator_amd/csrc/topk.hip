@@ -3,7 +3,7 @@
 //
 // Contract (bit-exact): row (b, s) considers t < n_valid = min(s_k, (s + q_offset + 1) /
 // cmp_ratio) whose score is not NaN; it keeps the first k of a stable descending order by
-// (score, lower index) with -0.0 == +0.0.
+// (score, lower index) with -0.0 == +0.0.  Only the valid prefix of a row is read.
 //
 // One 256-thread workgroup per row.  A row is read in segments of 1024·kR scores: thread t
 // holds float4 chunks j = 0..kR-1 at positions 4(t + 256 j), so a segment is one coalesced
@@ -90,7 +90,8 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
       for (int j = 0; j < kR; ++j) {
         const int base = sg * kSeg + 4 * (t + kThreads * j);
         const int at = min(base, s_k4 - 4);  // in bounds; used only when at == base
-        const float4 v = *reinterpret_cast<const float4*>(src + at);
+        // only the row's valid prefix is read: scores at or past nv may be unwritten
+        const float4 v = base < nv ? *reinterpret_cast<const float4*>(src + at) : make_float4(0.f, 0.f, 0.f, 0.f);
         x[j][0] = v.x;
         x[j][1] = v.y;
         x[j][2] = v.z;

@@ -93,10 +93,11 @@ extern "C" int dsa_lightning_indexer_varlen(const void* q, const float* q_scale,
       const int64_t row = q0 + r0;
       if (lk > 0) {
         void* lin_ws = lin_bytes ? (void*)((char*)scores_ws + (rows * 4 * lk + 255) / 256 * 256) : nullptr;
-        if (int rc = dsa_indexer_fwd_ws(at(q, row * n_heads * head_dim * es), at(q_scale, row * n_heads * 4),
-                                        at(k, k0 * head_dim * es), at(k_scale, k0 * 4), at(w, row * n_heads * 4),
-                                        scores_ws, dtype, 1, nr, lk, n_heads, head_dim, lk, q_off + r0, cmp_ratio,
-                                        lin_ws, nr * lin_bytes, stream))
+        // (spans past every frontier stay unwritten: the top-k reads only valid prefixes)
+        if (int rc = indexer_fwd(at(q, row * n_heads * head_dim * es), at(q_scale, row * n_heads * 4),
+                                 at(k, k0 * head_dim * es), at(k_scale, k0 * 4), at(w, row * n_heads * 4), scores_ws,
+                                 dtype, 1, nr, lk, n_heads, head_dim, lk, q_off + r0, cmp_ratio, lin_ws,
+                                 nr * lin_bytes, stream, false))
           return rc;
       }
       // with no keys the selection sees no candidate and pads the rows with -1

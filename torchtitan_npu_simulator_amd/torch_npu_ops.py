@@ -241,25 +241,45 @@ def npu_lightning_indexer(
     B, S, H, D = query.shape
     s_k = k3.shape[1]
     q_off = _resolve_q_offset(sparse_mode, S, s_k * cmp_ratio, q_offset)
-    K = int(sparse_count)
-    idx = torch.empty(B, S, K, dtype=torch.int32, device=query.device)
-    vals = torch.empty(B, S, K, dtype=torch.float32, device=query.device) if return_value else None
-    rows = max(1, min(S, _SCORE_BUDGET_BYTES // max(1, 4 * s_k * B)))
-    buf = torch.empty(B, rows, s_k, dtype=torch.float32, device=query.device)
-    for r0 in range(0, S, rows):
-        r1 = min(S, r0 + rows)
-        sc = buf[:, : r1 - r0]
-        for b in range(B):
-            qs = None if query_scale is None else query_scale[b : b + 1, r0:r1]
-            ks = None if key_scale is None else key_scale[b : b + 1]
-            indexer_scores(query[b : b + 1, r0:r1], k3[b : b + 1], weights[b : b + 1, r0:r1], q_scale=qs,
-                           k_scale=ks, q_offset=q_off + r0, cmp_ratio=cmp_ratio, out=sc[b : b + 1])
-            i_b, v_b = topk_select(sc[b : b + 1], K, q_offset=q_off + r0, cmp_ratio=cmp_ratio,
-                                   index_offset=index_offset, return_values=return_value)
-            idx[b, r0:r1] = i_b[0]
-            if return_value:
-                vals[b, r0:r1] = v_b[0]
+    idx, vals = lightning_indexer(query, k3, weights, int(sparse_count), query_scale=query_scale,
+                                  key_scale=key_scale, q_offset=q_off, cmp_ratio=cmp_ratio, index_offset=index_offset,
+                                  return_value=return_value)
     return idx.unsqueeze(2), (vals.to(_values_dtype(query)).unsqueeze(2) if return_value else None)
+
+
+def lightning_indexer(query, key, weights, k, *, query_scale=None, key_scale=None, q_offset=0, cmp_ratio=1,
+                      index_offset=0, return_value=False):
+    """Index scores + per-row top-k in one library call (dsa_lightning_indexer).
+
+    query [B,S,H_I,D_I], key [B,S_k,D_I] (bf16, or fp8-e4m3fn with query_scale [B,S,H_I] and
+    key_scale [B,S_k]), weights [B,S,H_I].  Returns (indices int32 [B,S,k], values fp32
+    [B,S,k] or None).  The fp32 score rows live in a workspace of at most 1 GiB: every row of
+    every batch at once when they fit, else batch by batch in row chunks."""
+    lib = load_library()
+    for t, n in ((query, "query"), (key, "key"), (weights, "weights")):
+        require_gpu_tensor(t, n)
+    if query.dtype != key.dtype:
+        raise ValueError("query and key must share a dtype")
+    B, S, H, D = query.shape
+    s_k = key.shape[1]
+    q = query.contiguous()
+    kk = key.contiguous()
+    w = weights.float().contiguous()
+    qs = None if query_scale is None else query_scale.float().contiguous()
+    ks = None if key_scale is None else key_scale.float().contiguous()
+    dt = _lib.dtype_code(q.dtype)
+    idx = torch.empty(B, S, k, dtype=torch.int32, device=q.device)
+    vals = torch.empty(B, S, k, dtype=torch.float32, device=q.device) if return_value else None
+    max_rows = S if B * S * s_k * 4 <= _SCORE_BUDGET_BYTES else max(1, _SCORE_BUDGET_BYTES // (4 * s_k))
+    ws_bytes = int(lib.dsa_lightning_indexer_workspace_size(B, S, s_k, H, D, dt, max_rows))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    check(
+        lib.dsa_lightning_indexer(ptr(q), ptr(qs), ptr(kk), ptr(ks), ptr(w), ptr(idx), ptr(vals), dt, B, S, s_k, H, D,
+                                  int(k), int(q_offset), int(cmp_ratio), int(index_offset), ptr(ws), ws_bytes,
+                                  stream_of(q.device)),
+        "dsa_lightning_indexer",
+    )
+    return idx, vals
 
 
 def _bsnd_lengths_indexer(query, key, weights, len_q, len_k, sparse_count, sparse_mode, cmp_ratio, return_value,
