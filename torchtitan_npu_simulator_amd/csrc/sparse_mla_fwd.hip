@@ -541,6 +541,11 @@ sparse_mla_fwd_exact_kernel(const T* __restrict__ q, const T* __restrict__ kv, c
   const T* kvb = kv + (int64_t)b * s_kv * dqk;
   const int64_t limit = tok + q_offset;
   const int h0 = fixup ? 0 : (int)blockIdx.y, h1 = fixup ? H : h0 + 1;
+  if (fixup) {  // one parallel test of the row's flags: almost every row has none
+    bool any = false;
+    for (int hh = tid; hh < H; hh += 256) any |= ssum[row_id * H + hh] < 0.f;
+    if (!__syncthreads_or(any)) return;
+  }
   for (int head = h0; head < h1; ++head) {
     const int64_t hr = row_id * H + head;
     if (fixup && !(ssum[hr] < 0.f)) continue;  // block-uniform
