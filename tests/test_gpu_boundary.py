@@ -170,3 +170,15 @@ def test_kernel_timing_records_each_launch():
     with _lib.kernel_timing() as kt2:  # a new window starts empty
         pass
     assert kt2.summary() == {}
+
+
+def test_device_cu_seqlens_read_back_once_per_version():
+    """A device cu_seqlens tensor shared by the ops of a step is read back once; an in-place
+    change (new version) is seen."""
+    from torchtitan_npu_simulator_amd import _lib
+
+    cu = torch.tensor([0, 100, 250], dtype=torch.int32, device=DEV)
+    first = _lib.host_ints(cu)
+    assert first == [0, 100, 250] and _lib.host_ints(cu) is first  # cached
+    cu[2] = 260
+    assert _lib.host_ints(cu) == [0, 100, 260]

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import weakref
 from pathlib import Path
 
 import torch
@@ -174,13 +175,32 @@ class kernel_timing:
         return self._summary
 
 
+# host copies of device integer tensors (cu_seqlens and the like), keyed by the tensor and
+# valid while its version counter is unchanged: the ops of one step that share a device
+# cu_seqlens tensor read it back once, not once per op
+_host_cache: "weakref.WeakKeyDictionary[torch.Tensor, tuple[int, list[int]]]" = weakref.WeakKeyDictionary()
+
+
+def host_ints(values) -> list[int]:
+    """``values`` (a list, a CPU tensor or a GPU tensor) as a host list of ints; a GPU
+    tensor is read back once per version of that tensor."""
+    if isinstance(values, torch.Tensor):
+        if values.is_cuda:
+            hit = _host_cache.get(values)
+            if hit is not None and hit[0] == values._version:
+                return hit[1]
+            lst = [int(v) for v in values.detach().to("cpu", torch.int64).tolist()]
+            _host_cache[values] = (values._version, lst)
+            return lst
+        return [int(v) for v in values.tolist()]
+    return [int(v) for v in values]
+
+
 def host_i32(values) -> ctypes.Array | None:
     """A host int32 array (ctypes) of ``values`` (a list or CPU/GPU tensor), or None."""
     if values is None:
         return None
-    if isinstance(values, torch.Tensor):
-        values = values.detach().to("cpu", torch.int64).tolist()
-    vals = [int(v) for v in values]
+    vals = host_ints(values)
     return (ctypes.c_int32 * len(vals))(*vals)
 
 

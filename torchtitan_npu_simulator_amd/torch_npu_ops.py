@@ -86,12 +86,11 @@ def to_cu_seqlens(cu_seqlens=None, actual_seq_lengths=None, total=None) -> list[
     """Host ``[0, end_0, end_1, ...]`` from A5-style ``cu_seqlens`` or torch_npu-style TND
     ``actual_seq_lengths`` (cumulative ends); checks the last end against ``total``."""
     if cu_seqlens is not None:
-        cu = [int(v) for v in (cu_seqlens.tolist() if isinstance(cu_seqlens, torch.Tensor) else cu_seqlens)]
+        cu = list(_lib.host_ints(cu_seqlens))
         if not cu or cu[0] != 0:
             raise ValueError("cu_seqlens must start with 0")
     elif actual_seq_lengths is not None:
-        ends = actual_seq_lengths.tolist() if isinstance(actual_seq_lengths, torch.Tensor) else actual_seq_lengths
-        cu = [0] + [int(v) for v in ends]
+        cu = [0] + list(_lib.host_ints(actual_seq_lengths))
     else:
         raise ValueError("TND layout needs cu_seqlens or actual_seq_lengths")
     if any(b < a for a, b in zip(cu[:-1], cu[1:])):
