@@ -340,38 +340,41 @@ def measured_traffic(kernel, S, H, K):
     return k["fetch_bytes"] + k["write_bytes"]
 
 
-def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128):
+def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=576, k_attn=None):
     """Algorithmic work of one launch-set per step of every kernel in the DSA step, keyed by
     the name the library's kernel timing reports (dsa_kernel_timing).
 
-    S query rows, H heads, K top-k slots, P = valid (row, slot) pairs, ``pairs`` = causal
-    (query, key) pairs the indexer scores, s_kv attention keys, s_ki indexer keys (default
-    s_kv).  Bytes are the data each kernel must move once (no cache hits assumed, gathered
-    rows counted per pair); FLOPs count the MFMA products.  Returns name -> (bound, bytes,
-    flops).
+    S query rows, H heads, K top-k slots, P = valid (row, slot) pairs of the attention,
+    ``pairs`` = causal (query, key) pairs the indexer scores, s_kv attention keys, s_ki
+    indexer keys (default s_kv), d_qk the attention row width (576: latent + rope; 512: the
+    rope-less DeepSeek-V4 rows, whose kernels report a ``<512>`` name), k_attn the attention
+    slots per row (default K; V4: the 128-token window + K).  Bytes are the data each kernel
+    must move once (no cache hits assumed, gathered rows counted per pair); FLOPs count the
+    MFMA products.  Returns name -> (bound, bytes, flops).
     """
     s_ki = s_kv if s_ki is None else s_ki
-    dq, dv, gw = 576, 512, 256  # latent + rope width, latent width, G row (dS | P) x 128 heads
-    return {
+    Ka = K if k_attn is None else k_attn
+    dq, dv, gw = d_qk, 512, 256  # row width, latent width, G row (dS | P) x 128 heads
+    w = {
         "quantize_fp8_kernel": ("hbm", (S * h_i + s_ki) * (2 * d_i + d_i + 4), 0),
         "indexer_lin_pieces_kernel<64>": ("hbm", S * (h_i * d_i + 4 * h_i + 4 * h_i + 4 * d_i + 16), 0),
         "indexer_tile_kernel<fp8, 4, split>": ("mfma", 0, 2 * h_i * d_i * pairs),
         "topk_kernel": ("hbm", 4 * pairs + 4 * K * S, 0),
-        "sparse_mla_fwd_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * K * S + 2 * H * dv * S + 4 * H * S,
+        "sparse_mla_fwd_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * Ka * S + 2 * H * dv * S + 4 * H * S,
                                        2 * H * (dq + dv) * P),
         "sparse_mla_fwd_exact_kernel<fixup>": ("hbm", 4 * H * S, 0),
         "bwd_delta_kernel": ("hbm", 2 * (2 * H * dv * S) + 4 * H * S, 0),
         # Q, dO, gathered rows, indices, G written, mass, (max, sum, delta)
-        "bwd_sdp_kernel": ("hbm", 2 * H * dq * S + 2 * H * dv * S + 2 * dq * P + 4 * K * S + 2 * gw * P + 4 * K * S
+        "bwd_sdp_kernel": ("hbm", 2 * H * dq * S + 2 * H * dv * S + 2 * dq * P + 4 * Ka * S + 2 * gw * P + 4 * Ka * S
                            + 12 * H * S, 2 * H * (dq + dv) * P),
         # gathered rows, indices, dS half of G, dQ written
-        "bwd_dqk_kernel": ("hbm", 2 * dq * P + 4 * K * S + 2 * (gw // 2) * P + 2 * H * dq * S, 2 * H * dq * P),
+        "bwd_dqk_kernel": ("hbm", 2 * dq * P + 4 * Ka * S + 2 * (gw // 2) * P + 2 * H * dq * S, 2 * H * dq * P),
         # G, X = [Q; dO], indices, C written
-        "bwd_contrib_kernel<2>": ("hbm", 2 * gw * P + 2 * H * (dq + dv) * S + 4 * K * S + 2 * dq * P,
+        "bwd_contrib_kernel<2>": ("hbm", 2 * gw * P + 2 * H * (dq + dv) * S + 4 * Ka * S + 2 * dq * P,
                                   2 * P * (gw * dv + (gw // 2) * (dq - dv))),
         "zero_i32_kernel": ("hbm", 4 * (s_kv + 1) + 4 * (s_ki + 1), 0),
-        "csr_count_kernel<count>": ("hbm", 8 * K * S, 0),
-        "csr_count_kernel<fill>": ("hbm", 8 * K * S + 8 * P, 0),
+        "csr_count_kernel<count>": ("hbm", 8 * Ka * S, 0),
+        "csr_count_kernel<fill>": ("hbm", 8 * Ka * S + 8 * P, 0),
         "csr_scan_kernel": ("hbm", 12 * (s_kv + s_ki), 0),
         "csr_seg_key_kernel": ("hbm", 8 * (s_kv + s_ki), 0),
         # C rows read, pair list, fp32 dKV written
@@ -382,6 +385,12 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128):
         "dkv_reduce_kernel<16>": ("hbm", 2 * d_i * P + 4 * P + 4 * d_i * s_ki, 0),
         "compressor_kernel": ("hbm", 0, 0),  # per-call bytes depend on the block geometry; see kernels
     }
+    if dq != 576:  # the rope-less variants' names
+        for name in ("sparse_mla_fwd_bf16_kernel", "bwd_sdp_kernel", "bwd_dqk_kernel"):
+            w[f"{name}<{dq}>"] = w.pop(name)
+        w[f"bwd_contrib_kernel<2,{dq}>"] = w.pop("bwd_contrib_kernel<2>")
+        w[f"dkv_reduce_kernel<{dq // 8}>"] = w.pop("dkv_reduce_kernel<72>")
+    return w
 
 
 def kernel_table(ktimes, work, steps, traffic_of=None):
@@ -654,10 +663,10 @@ def main():
     phases = timer.averages_ms()
     if wl == "v4":
         # slots per row: the window (min(128, s + 1) rows) plus the valid compressed picks;
-        # rows are 512 wide, padded to the 576-column kernels' layout
+        # rows are 512 wide (the kernels' rope-less variant)
         win = sum(min(128, s + 1) for s in range(S))
-        work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs)
-        work = algorithmic_work(S, H, K + 128, None, causal_pairs=pairs, sum_keff=work["sum_keff"] + win)
+        work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs, d_qk=512)
+        work = algorithmic_work(S, H, K + 128, None, causal_pairs=pairs, sum_keff=work["sum_keff"] + win, d_qk=512)
     else:
         work = algorithmic_work(S, H, K, res["idx"], causal_pairs=pairs)
     del res
@@ -665,7 +674,7 @@ def main():
     fwd_ms = phases["attn_fwd"]
     bwd_ms = phases["attn_bwd"]
     if wl == "v4":
-        kwork = {}
+        kwork = step_kernel_work(S, H, K, work["sum_keff"], pairs, S + S // 4, S // 4, d_qk=512, k_attn=K + 128)
     else:
         s_kv = S // 4 if wl == "c4" else S
         kwork = step_kernel_work(S, H, K, work["sum_keff"], pairs if pairs is not None else S * (S + 1) // 2, s_kv)
@@ -698,7 +707,7 @@ def main():
         algorithmic_bytes=attn_bytes,
     )
     roof_pair["frac"] = roof_pair["achieved"] / roof_pair["peak"]
-    cfg.update(heads=H, d_qk=576, d_v=512, topk=K, index_heads=64, index_dim=128, sum_k_eff=work["sum_keff"],
+    cfg.update(heads=H, d_qk=512 if wl == "v4" else 576, d_v=512, topk=K, index_heads=64, index_dim=128, sum_k_eff=work["sum_keff"],
                indexer_pairs=pairs if pairs is not None else S * (S + 1) // 2)
     metric = "sparse-attn fwd+bwd tokens/s @S=8K,top-k 2048; % HBM / MFMA roofline"
     if wl != "c3":

@@ -185,7 +185,9 @@ int dsa_lightning_indexer(const void* q, const float* q_scale, const void* k, co
  *   out      [B, S, H, D_v]
  *   softmax_max [B, S, H] fp32: max_j scale*q.k_j (natural-log units), -inf if no valid slot
  *   softmax_sum [B, S, H] fp32: sum_j exp(scale*q.k_j - softmax_max)
- * dtype DSA_BF16: MFMA path (requires D_qk = 576, D_v = 512); DSA_F32: exact fp32 path.
+ * dtype DSA_BF16: MFMA path (requires D_v = 512 and D_qk = 576, the DeepSeek-V3.2 latent +
+ * rope rows, or D_qk = 512, the rope-less DeepSeek-V4 rows where v = the whole row);
+ * DSA_F32: exact fp32 path.
  */
 int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, void* out, float* softmax_max,
                        float* softmax_sum, int dtype, int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
@@ -203,7 +205,7 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, vo
  *             sparse_flash_mla_grad returns the same quantity, converters/kernels/npu_smla.py:540-568)
  *   workspace  device scratch of workspace_bytes (dsa_sparse_mla_bwd_workspace_size() gives the
  *              default; a smaller one processes query rows in more chunks); fp32 dtype needs none
- * The bf16 path needs D_qk = 576, D_v = 512, H <= 128.  dKV is reduced per key through a
+ * The bf16 path needs D_qk = 576 or 512, D_v = 512, H <= 128.  dKV is reduced per key through a
  * key-major CSR of the bf16 per-(row, slot) contributions, summed in fp32; only a key whose
  * list straddles two reduction segments adds its partial sums with fp32 atomics, so dKV
  * is reproducible to fp32 rounding, not bit for bit.

@@ -173,3 +173,29 @@ def test_host_tensors_are_refused_before_any_launch():
         ops._rope_args(torch.polar(torch.ones(4, 32), torch.zeros(4, 32)), 64, torch.device("cpu"))[0].data_ptr() \
             and _lib.ptr(ops._rope_args(torch.polar(torch.ones(4, 32), torch.zeros(4, 32)), 64,
                                         torch.device("cpu"))[0])
+
+
+def test_host_ints_reads_a_device_tensor_once_per_version():
+    """The cu_seqlens read-back cache: a hit needs the same tensor object and version, and
+    the entry goes when the tensor is freed.  (A CPU tensor that reports is_cuda stands in
+    for a device tensor.)"""
+    import gc
+
+    from torchtitan_npu_simulator_amd import _lib
+
+    class Dev(torch.Tensor):
+        @property
+        def is_cuda(self):
+            return True
+
+    cu = torch.tensor([0, 100, 250], dtype=torch.int32).as_subclass(Dev)
+    twin = torch.tensor([0, 100, 250], dtype=torch.int32).as_subclass(Dev)  # equal values, other object
+    first = _lib.host_ints(cu)
+    assert first == [0, 100, 250] and _lib.host_ints(cu) is first
+    assert _lib.host_ints(twin) == first and _lib.host_ints(twin) is not first
+    cu[2] = 260
+    assert _lib.host_ints(cu) == [0, 100, 260]
+    n = len(_lib._host_cache)
+    del cu, twin
+    gc.collect()
+    assert len(_lib._host_cache) == n - 2

@@ -55,6 +55,28 @@ def test_bwd_bf16_parity(S, H, K, q_offset, seed, shuffle, holes):
     assert rel_err(dq, adq) <= BF16_TOL and rel_err(dkv, adkv) <= BF16_TOL
 
 
+@pytest.mark.parametrize(
+    "S,H,K,q_offset,seed,holes,workspace",
+    [
+        (256, 128, 128, 0, 31, 0.0, None),
+        (160, 128, 96, 32, 32, 0.2, None),  # -1 holes, CP shard offset
+        (128, 16, 64, 0, 33, 0.0, None),  # one partial head group
+        (96, 72, 40, 0, 34, 0.1, 40 * (256 * 2 + 512 * 2 + 4) * 24 + 3 * 97 * 4 + 8192),  # row chunks
+    ],
+)
+def test_bwd_bf16_rows_of_512_columns(S, H, K, q_offset, seed, holes, workspace):
+    """The rope-less variant (DeepSeek-V4 rows, d_qk = d_v = 512): dQ and dKV, with the
+    contribution rows and the key-major reduction 512 wide."""
+    q, kv, dout, scale = attn_inputs(S, H, q_offset=q_offset, seed=seed, d_qk=512)
+    idx = rand_indices(S, K, q_offset=q_offset, seed=seed, shuffle=True, holes=holes)
+    out, smax, ssum, dq, dkv = _gpu_fwd_bwd(q, kv, idx, dout, scale, q_offset, workspace_bytes=workspace)
+    assert dq.shape == q.shape and dkv.shape == kv.shape
+    _, ref_lse = O.sparse_mla_fwd(q, kv, idx, scale, q_offset=q_offset)
+    rdq, rdkv, _ = O.sparse_mla_bwd_closed_form(q, kv, idx, out, ref_lse, dout, scale, q_offset=q_offset)
+    assert rel_err(dq, rdq) <= BF16_TOL, rel_err(dq, rdq)
+    assert rel_err(dkv, rdkv) <= BF16_TOL, rel_err(dkv, rdkv)
+
+
 @pytest.mark.parametrize("K", [96, 99])
 def test_bwd_long_kv_spans_several_counting_ranges(K):
     """A KV prefix of 40000 rows: the key-major CSR behind dKV counts keys in 16384-key

@@ -52,6 +52,21 @@ def test_fwd_bf16_parity(S, H, K, q_offset, seed):
     _check(q, kv, idx, scale, q_offset, BF16_TOL)
 
 
+@pytest.mark.parametrize(
+    "S,H,K,q_offset,seed,holes",
+    [
+        (256, 128, 128, 0, 21, 0.0),
+        (160, 64, 96, 32, 22, 0.2),  # -1 holes, CP shard offset
+        (96, 40, 48, 0, 23, 0.0),  # head count not a multiple of 32
+    ],
+)
+def test_fwd_bf16_rows_of_512_columns(S, H, K, q_offset, seed, holes):
+    """The rope-less variant (DeepSeek-V4 rows): d_qk = d_v = 512, v = the whole key row."""
+    q, kv, _, scale = attn_inputs(S, H, q_offset=q_offset, seed=seed, d_qk=512)
+    idx = rand_indices(S, K, q_offset=q_offset, seed=seed, shuffle=True, holes=holes)
+    _check(q, kv, idx, scale, q_offset, BF16_TOL)
+
+
 def test_fwd_bf16_shuffled_slots_and_holes():
     S, H, K = 160, 128, 96
     q, kv, _, scale = attn_inputs(S, H, seed=7, logit_std=3.0)

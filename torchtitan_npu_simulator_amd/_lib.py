@@ -178,7 +178,16 @@ class kernel_timing:
 # host copies of device integer tensors (cu_seqlens and the like), keyed by the tensor and
 # valid while its version counter is unchanged: the ops of one step that share a device
 # cu_seqlens tensor read it back once, not once per op
-_host_cache: "weakref.WeakKeyDictionary[torch.Tensor, tuple[int, list[int]]]" = weakref.WeakKeyDictionary()
+# keyed by id(tensor): a WeakKeyDictionary would compare two weak references to the same
+# live tensor with the tensor's own (elementwise) ==.  Each entry holds a weak reference,
+# checked by identity, and is dropped when its tensor is freed.
+_host_cache: dict[int, tuple["weakref.ref[torch.Tensor]", int, list[int]]] = {}
+
+
+def _drop_host_entry(key: int, r: "weakref.ref[torch.Tensor]") -> None:
+    entry = _host_cache.get(key)
+    if entry is not None and entry[0] is r:  # (the id may have been reused since)
+        del _host_cache[key]
 
 
 def host_ints(values) -> list[int]:
@@ -186,11 +195,13 @@ def host_ints(values) -> list[int]:
     tensor is read back once per version of that tensor."""
     if isinstance(values, torch.Tensor):
         if values.is_cuda:
-            hit = _host_cache.get(values)
-            if hit is not None and hit[0] == values._version:
-                return hit[1]
+            key = id(values)
+            hit = _host_cache.get(key)
+            if hit is not None and hit[0]() is values and hit[1] == values._version:
+                return hit[2]
             lst = [int(v) for v in values.detach().to("cpu", torch.int64).tolist()]
-            _host_cache[values] = (values._version, lst)
+            r = weakref.ref(values, lambda ref_, k=key: _drop_host_entry(k, ref_))
+            _host_cache[key] = (r, values._version, lst)
             return lst
         return [int(v) for v in values.tolist()]
     return [int(v) for v in values]

@@ -185,7 +185,8 @@ __global__ void __launch_bounds__(1024) csr_scan_kernel(const int* __restrict__ 
 // key lies wholly inside the segment (sole owner), else with fp32 atomic adds (only keys
 // that straddle a segment boundary, at most two partial sums per segment).
 // 576-wide rows (72 chunks): lane l owns chunk l, and chunk 64 + (l & 7) is loaded by every
-// lane (one 128-byte line per instruction) and stored by lanes 0..7.  128-wide rows
+// lane (one 128-byte line per instruction) and stored by lanes 0..7; 512-wide rows (64
+// chunks): lane l owns chunk l.  128-wide rows
 // (16 chunks): lanes 16s .. 16s+15 own the row of pair 4g + s of each group of 4 (four
 // streams), combined with two lane exchanges at the flush.
 constexpr int kSegPairs = 256;
@@ -226,7 +227,7 @@ template <int kChunks>
 __global__ void __launch_bounds__(256)
 dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row_ptr, const int* __restrict__ pairs,
                   const int* __restrict__ seg_key, float* __restrict__ acc_out, int s_kv, int rows, int K, int b) {
-  static_assert(kChunks == 72 || kChunks == 16, "row widths of the attention and indexer reductions");
+  static_assert(kChunks == 72 || kChunks == 64 || kChunks == 16, "row widths of the attention and indexer reductions");
   constexpr int kWidth = kChunks * 8;
   constexpr int kGroup = 8;
   const int seg = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
@@ -245,12 +246,14 @@ dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row
   auto flush = [&]() {
     const bool sole = kbeg >= seg0 && kend <= seg1;
     float* d = dbase + (int64_t)k * kWidth;
-    if constexpr (kChunks == 72) {
+    if constexpr (kChunks >= 64) {
       flush8(d + 8 * lane, acc, sole);
-      if (lane < kChunks - 64) flush8(d + 512 + 8 * lane, acc2, sole);
-      else
+      if constexpr (kChunks == 72) {
+        if (lane < kChunks - 64) flush8(d + 512 + 8 * lane, acc2, sole);
+        else
 #pragma unroll
-        for (int r = 0; r < 8; ++r) acc2[r] = 0.f;
+          for (int r = 0; r < 8; ++r) acc2[r] = 0.f;
+      }
     } else {
 #pragma unroll
       for (int r = 0; r < 8; ++r) acc[r] = xor32_sum(xor16_sum(acc[r]));
@@ -265,12 +268,12 @@ dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) pr[u] = pairs[min(p + u, seg1 - 1)];
     u32x4 v[kGroup], w[kGroup];
-    if constexpr (kChunks == 72) {
+    if constexpr (kChunks >= 64) {
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
         const uint16_t* row = cb + (int64_t)pr[u] * kWidth;
         v[u] = *reinterpret_cast<const u32x4*>(row + 8 * lane);
-        w[u] = *reinterpret_cast<const u32x4*>(row + 512 + 8 * (lane & 7));
+        if constexpr (kChunks == 72) w[u] = *reinterpret_cast<const u32x4*>(row + 512 + 8 * (lane & 7));
       }
     } else {
 #pragma unroll
@@ -289,9 +292,9 @@ dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row
         kbeg = kend;
         kend = row_ptr[k + 1];
       }
-      if constexpr (kChunks == 72) {
+      if constexpr (kChunks >= 64) {
         add_bf16x8(acc, v[u]);
-        add_bf16x8(acc2, w[u]);
+        if constexpr (kChunks == 72) add_bf16x8(acc2, w[u]);
       } else {
         // four pairs per load group: stream s adds its row when q is pair 4 (u / 4) + s
         if (stream == (u & 3)) add_bf16x8(acc, v[u >> 2]);
@@ -343,9 +346,14 @@ inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, 
     csr_seg_key_kernel<<<ceil_div(s_kv, 256), 256, 0, st>>>(row_ptr, seg_key, s_kv);
   }
   const unsigned rgrid = ceil_div(ceil_div((int64_t)rows * K, kSegPairs), 4);
-  const TimedLaunch tl(row_chunks == 72 ? "dkv_reduce_kernel<72>" : "dkv_reduce_kernel<16>", st);
+  const TimedLaunch tl(row_chunks == 72   ? "dkv_reduce_kernel<72>"
+                       : row_chunks == 64 ? "dkv_reduce_kernel<64>"
+                                          : "dkv_reduce_kernel<16>",
+                       st);
   if (row_chunks == 72)
     dkv_reduce_kernel<72><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, s_kv, rows, K, b);
+  else if (row_chunks == 64)
+    dkv_reduce_kernel<64><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, s_kv, rows, K, b);
   else if (row_chunks == 16)
     dkv_reduce_kernel<16><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, s_kv, rows, K, b);
   else

@@ -1,11 +1,12 @@
 // Gathered KV-row pipeline shared by the sparse-attention kernels (gfx950).
 //
-// A block is kBN = 32 selected latent-KV rows of 576 bf16 (1152 B).  Its LDS tile holds
-// the rows row-major with 16-byte chunk c of row r at chunk c ^ swz_kv(r), and is filled by
-// 36 wave-wide DMA instructions (global_load_lds, 16 B per lane): instruction J covers
-// tile positions [64J, 64J+64), position p = r*72 + (c ^ swz_kv(r)); wave w issues
-// J = w, w + W, ...  Unused slots (-1, past the causal limit, past K) load row 0 and are
-// masked by the block's validity bits.
+// A block is kBN = 32 selected latent-KV rows of 576 bf16 (1152 B; 512 bf16 = 1024 B for
+// the rope-less DeepSeek-V4 rows).  Its LDS tile holds the rows row-major with 16-byte chunk
+// c of row r at chunk c ^ swz_kv(r), and is filled by 36 (32) wave-wide DMA instructions
+// (global_load_lds, 16 B per lane): instruction J covers tile positions [64J, 64J+64),
+// position p = r*72 + (c ^ swz_kv(r)) (r*64 + ...); wave w issues J = w, w + W, ...
+// Unused slots (-1, past the causal limit, past K) load row 0 and are masked by the
+// block's validity bits.
 //
 // Tiles are triple-buffered: while block b computes, block b+1 has landed or is landing
 // and block b+2 is being issued, so a gather has two block times to arrive.  The slot
@@ -26,17 +27,20 @@ namespace dsa {
 
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4_t;
 
-struct GatherGeom {
-  static constexpr int kDqk = 576;
-  static constexpr int kRowChunks = kDqk / 8;           // 72
-  static constexpr int kRowBytes = kRowChunks * 16;     // 1152
+// row width kDqkT: 576 (latent 512 + rope 64, DeepSeek-V3.2 MLA) or 512 (DeepSeek-V4 rows)
+template <int kDqkT>
+struct GatherGeomT {
+  static constexpr int kDqk = kDqkT;
+  static constexpr int kRowChunks = kDqk / 8;           // 72 | 64
+  static constexpr int kRowBytes = kRowChunks * 16;     // 1152 | 1024
   static constexpr int kBN = 32;                        // rows per block
-  static constexpr int kTileChunks = kBN * kRowChunks;  // 2304 x 16 B
-  static constexpr int kTileBytes = kTileChunks * 16;   // 36864
-  static constexpr int kTileInstr = kTileChunks / 64;   // 36 wave-wide DMA instructions
+  static constexpr int kTileChunks = kBN * kRowChunks;  // 2304 | 2048 x 16 B
+  static constexpr int kTileBytes = kTileChunks * 16;   // 36864 | 32768
+  static constexpr int kTileInstr = kTileChunks / 64;   // 36 | 32 wave-wide DMA instructions
   static constexpr int kRing = 4;
   static constexpr int64_t kMaxRows = (int64_t)UINT32_MAX / kRowBytes - 1;  // 32-bit byte offsets
 };
+using GatherGeom = GatherGeomT<576>;
 
 // slot value v of a row whose causal limit is `limit` is a usable key
 __device__ __forceinline__ bool slot_ok(int v, int s_kv, int64_t limit) {
@@ -81,9 +85,9 @@ __device__ __forceinline__ uint32_t gather_limit(int64_t tok_limit, int s_kv) {
   return l < 0 ? 0u : (uint32_t)l;
 }
 
-template <int kWaves>
+template <int kWaves, int kDqkT = 576>
 struct RowGather {
-  using G = GatherGeom;
+  using G = GatherGeomT<kDqkT>;
   static constexpr int kMaxPerWave = (G::kTileInstr + kWaves - 1) / kWaves;
   static constexpr int kFullWaves = G::kTileInstr % kWaves == 0 ? kWaves : G::kTileInstr % kWaves;
   static constexpr int kRingInts = 64;  // one dword per lane; lanes 32..63 repeat 0..31

@@ -31,12 +31,7 @@ namespace {
 
 constexpr int kDqk = 576;
 constexpr int kDv = 512;
-constexpr int kRowChunks = kDqk / 8;
-constexpr int kRowBytes = kRowChunks * 16;
 constexpr int kBN = 32;
-constexpr int kTileChunks = kBN * kRowChunks;
-constexpr int kTileBytes = kTileChunks * 16;
-constexpr int kTileInstr = kTileChunks / 64;  // 36
 constexpr int kHG = 64;                       // heads per G head group (one 128-entry half of a G row)
 constexpr int kGW = 256;                      // G row width: (dS | P) x 128 heads
 constexpr int kHeadsMax = 128;
@@ -67,17 +62,21 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // aligned rows x 4 pieces distinct (the flush's transposed reads)
 __device__ __forceinline__ int g2_swz(int r) { return (r >> 2) & 7; }
 
+template <int kD>  // row width of Q and KV: 576 (latent + rope) or 512 (no rope)
 __global__ void __launch_bounds__(256, 1)
 bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
                const uint16_t* __restrict__ dout, const float* __restrict__ smax, const float* __restrict__ ssum,
                const float* __restrict__ dbuf, uint16_t* __restrict__ gbuf, float* __restrict__ mass, int S, int s_kv,
                int H, int K, float scale, int64_t q_offset, int row0) {
-  using Gather = RowGather<4>;
+  using Gather = RowGather<4, kD>;
+  using Geo = GatherGeomT<kD>;
   constexpr int kPer = Gather::kMaxPerWave;
-  constexpr int kLat = kDv / 16;   // 32 latent k-steps
-  constexpr int kSteps = kDqk / 16;  // 36
-  __shared__ u32x4 tile[2][kTileChunks];
-  __shared__ u32x4 qpe[kHeadsMax][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
+  constexpr int kLat = kDv / 16;     // 32 latent k-steps
+  constexpr int kSteps = kD / 16;    // 36 | 32
+  constexpr bool kRope = kSteps > kLat;
+  constexpr int kRB = Geo::kRowBytes;
+  __shared__ u32x4 tile[2][Geo::kTileChunks];
+  __shared__ u32x4 qpe[kRope ? kHeadsMax : 1][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
   __shared__ uint2 gst[2][kGW][kBN / 4];  // [parity][G entry][piece of 4 slots ^ g2_swz(entry)]
   __shared__ float pst[2][4][kBN];
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
@@ -92,7 +91,7 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   const int64_t hrow = row_id * H + (hok ? hl : 0);
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
-  const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
+  const uint16_t* kvb = kv + (int64_t)b * s_kv * kD;
   uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)g_slots(K) * kGW;
   float* mrow = mass ? mass + row_id * K : nullptr;
 
@@ -105,14 +104,14 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   // latent Q and dO of head hl: k-step s holds columns 16s + 8h .. +8 (B operands)
   u32x4 qb[kLat], db[kLat], qr[4];
   {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kD);
     const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
 #pragma unroll
     for (int st = 0; st < kLat; ++st) qb[st] = qh[2 * st + h];
 #pragma unroll
     for (int st = 0; st < kLat; ++st) db[st] = dh[2 * st + h];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qr[j] = qh[64 + 4 * h + j];
+    for (int j = 0; j < 4; ++j) qr[j] = kRope ? qh[64 + 4 * h + j] : (u32x4){0u, 0u, 0u, 0u};
   }
   const float mx = smax[hrow], sm = ssum[hrow];
   const float dlt = dbuf[((int64_t)b * gridDim.x + lr) * H + (hok ? hl : 0)];
@@ -130,10 +129,12 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) qr[j] = (u32x4){0u, 0u, 0u, 0u};
   }
+  if constexpr (kRope) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int ch = 4 * h + j;
-    qpe[hl][ch ^ ((hl >> 1) & 7)] = qr[j];
+    for (int j = 0; j < 4; ++j) {
+      const int ch = 4 * h + j;
+      qpe[hl][ch ^ ((hl >> 1) & 7)] = qr[j];
+    }
   }
   const float lse2 = (hok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0
   const float delta = hok ? dlt : 0.f;
@@ -145,7 +146,7 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
 
   uint32_t ka_off[4];  // A operand (K row n, chunk (2s + h) ^ swz_kv(n)), s = 4u + s0 -> + 128 u
 #pragma unroll
-  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRowBytes + 16 * ((2 * s0 + h) ^ swz_kv(n));
+  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRB + 16 * ((2 * s0 + h) ^ swz_kv(n));
   const lds_char* qpe_b = lds_bytes(&qpe[0][0]);
   // G entries of head hl: dS at 128 (hl / 64) + hl % 64, P 64 entries later
   const int e_ds = 128 * (hl >> 6) + (hl & 63), e_p = e_ds + 64;
@@ -190,7 +191,7 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   __syncthreads();
 
   constexpr int kQBatch = 4;
-  constexpr int kQB = kSteps / kQBatch;  // 9 batches
+  constexpr int kQB = kSteps / kQBatch;  // 9 | 8 batches
   static_assert(kQB >= kPer, "one row DMA per batch");
 
   // P / dS / G staging / mass of block pb (its S^T, dP^T in sp, pp; validity vm), in pieces
@@ -289,7 +290,7 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
     static_for<kQB>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
       if constexpr (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
-      if constexpr ((nb + 1) * kQBatch == kLat) {
+      if constexpr (kRope && (nb + 1) * kQBatch == kLat) {
 #pragma unroll
         for (int e = 0; e < kQBatch; ++e) rope[e] = lds_read16(qpe_b + hl * 128 + 16 * ((2 * e + h) ^ ((hl >> 1) & 7)));
       }
@@ -376,14 +377,18 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
 // --------------------------------------------------------------------------------------
 __device__ __forceinline__ int ds_swz(int r) { return 4 * (r & 3); }
 
+template <int kD>  // row width of KV and dQ: 576 or 512
 __global__ void __launch_bounds__(512, 1)
 bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf,
                uint16_t* __restrict__ dq, int S, int s_kv, int H, int K, int64_t q_offset, int row0) {
-  using Gather = RowGather<8>;
-  constexpr int kPer = Gather::kMaxPerWave;  // 5 row instructions per wave and block
-  constexpr int kDT = kDqk / 32;             // 18 d tiles
-  constexpr int kOwn = (kDT + 3) / 4;        // d tiles per wave (5; tile owners 2, 3 own 4)
-  __shared__ u32x4 tile[2][kTileChunks];
+  using Gather = RowGather<8, kD>;
+  using Geo = GatherGeomT<kD>;
+  constexpr int kPer = Gather::kMaxPerWave;  // 5 | 4 row instructions per wave and block
+  constexpr int kDT = kD / 32;               // 18 | 16 d tiles
+  constexpr int kOwn = (kDT + 3) / 4;        // d tiles per wave (576: 5, tile owners 2, 3 own 4; 512: 4)
+  constexpr int kRB = Geo::kRowBytes;
+  static_assert(kPer <= kOwn, "one row instruction per owned tile");
+  __shared__ u32x4 tile[2][Geo::kTileChunks];
   __shared__ u32x4 dsl[2][kBN * 16];  // dS tile: [slot][16 chunks of 8 heads ^ ds_swz(slot)]
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
   __shared__ int sh_last;
@@ -395,7 +400,7 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
-  const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
+  const uint16_t* kvb = kv + (int64_t)b * s_kv * kD;
   const uint16_t* grow = gbuf + ((int64_t)b * gridDim.x + lr) * (int64_t)g_slots(K) * kGW;
 
   int vidx[kIdxU];
@@ -407,8 +412,8 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (nblk == 0) {  // no usable key: dQ = 0
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    for (int i = tid; i < H * (kDqk / 2); i += 512)
-      reinterpret_cast<uint32_t*>(dq + row_id * H * kDqk)[i] = 0u;
+    for (int i = tid; i < H * (kD / 2); i += 512)
+      reinterpret_cast<uint32_t*>(dq + row_id * H * kD)[i] = 0u;
     return;
   }
   const uint32_t lim = gather_limit(limit, s_kv);
@@ -427,7 +432,7 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
 #pragma unroll
       for (int d0 = 0; d0 < 2; ++d0) {
         const int ch = 4 * d0 + 2 * (G & 1) + ((c & 3) >> 1);
-        tr_off[x][d0] = r * kRowBytes + 16 * (ch ^ swz_kv(r)) + 8 * (c & 1);
+        tr_off[x][d0] = r * kRB + 16 * (ch ^ swz_kv(r)) + 8 * (c & 1);
       }
 #pragma unroll
       for (int gg = 0; gg < 2; ++gg) {
@@ -481,7 +486,7 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
     auto read_kt = [&](u32x4 (&dst)[2], int dt) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const lds_char* base = vb + kk * 16 * kRowBytes + 128 * (dt >> 1);
+        const lds_char* base = vb + kk * 16 * kRB + 128 * (dt >> 1);
         dst[kk] = lds_read_tr_pair(base + tr_off[0][dt & 1], base + tr_off[1][dt & 1]);
       }
     };
@@ -544,7 +549,7 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
     for (int gg = 0; gg < 2; ++gg) {
       const int hd = 32 * (2 * hh2 + gg) + n;
       if (hd >= H) continue;
-      uint2* drow = reinterpret_cast<uint2*>(dq + (row_id * H + hd) * kDqk);
+      uint2* drow = reinterpret_cast<uint2*>(dq + (row_id * H + hd) * kD);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         uint2 w;
@@ -560,12 +565,14 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
 // (beta) C[token][slot] = G[token][slot] . X_token,  X = [(Q, dO) per head group]
 // rows of X: k = 128 hg + 64 type + i  ->  type 0: q[64hg + i], type 1: dout[64hg + i]
 //
-// One workgroup per token, 12 waves; wave w owns the 48 output columns 48w .. 48w+47
-// (three 16-column MFMA tiles) and keeps its slice of X transposed in VGPRs for the whole
-// token (A operand of C^T = X^T G^T, 96 VGPRs).  G is streamed through a double-buffered
-// LDS tile of 64 slots x 256 (DMA), so G, X and C each cross HBM exactly once.  The C rows
-// of each 32-slot step are assembled in a double-buffered LDS stage (every wave adds its
-// 48 columns) and leave as whole 1152-byte rows, 16 bytes per lane: the MFMA output layout
+// One workgroup per token, 12 waves; the output columns form 16-column MFMA tiles (36 of
+// a 576-wide row, 32 of a 512-wide one), three per wave at 576 columns (wave w: columns
+// 48w .. 48w+47) and at 512 three for waves 0..7, two for waves 8..11 (8 tiles per SIMD
+// either way).  Each wave keeps its slice of X transposed in VGPRs for the whole token (A
+// operand of C^T = X^T G^T, 96 VGPRs).  G is streamed through a double-buffered LDS tile of
+// 64 slots x 256 (DMA), so G, X and C each cross HBM exactly once.  The C rows of each
+// 32-slot step are assembled in a double-buffered LDS stage (every wave adds its columns)
+// and leave as whole 1152- (1024-) byte rows, 16 bytes per lane: the MFMA output layout
 // alone would give 8-byte pieces scattered over 16 rows per store instruction.
 // --------------------------------------------------------------------------------------
 constexpr int kCW = 12;                     // waves
@@ -573,19 +580,30 @@ constexpr int kCThreads = kCW * 64;
 constexpr int kCT = 64;                     // slots per G tile
 constexpr int kGTChunks = kCT * (kGW / 8);  // 2048 16-byte chunks (32 KB)
 constexpr int kCS = 32;                     // slots per step (C stage rows)
-constexpr int kStChunks = kCS * kRowChunks; // 2304 chunks (36 KB)
 constexpr int kXK = 64;                     // X rows staged per chunk while loading X
-constexpr int kXChunks = kXK * kRowChunks;  // 4608 chunks (73.7 KB)
-static_assert(2 * kGTChunks + 2 * kStChunks >= kXChunks, "X staging reuses the tile space");
+template <int kD>
+struct ContribGeom {
+  static constexpr int kRC = kD / 8;           // 16-byte chunks per C row (72 | 64)
+  static constexpr int kStChunks = kCS * kRC;  // C stage: 2304 | 2048 chunks
+  static constexpr int kXChunks = kXK * kRC;   // X staging: 4608 | 4096 chunks
+  static constexpr int kNT = kD / 16;          // 16-column tiles (36 | 32)
+  static constexpr int kFull = kNT - 2 * kCW;  // waves owning three tiles (12 | 8); the rest own two
+  static_assert(kFull > 0 && kFull <= kCW, "two or three tiles per wave");
+  static_assert(2 * kGTChunks + 2 * kStChunks >= kXChunks, "X staging reuses the tile space");
+  // first tile of wave w
+  static __device__ __forceinline__ int tile0(int w) { return w < kFull ? 3 * w : 3 * kFull + 2 * (w - kFull); }
+};
 
 // C stage layout: row r (slot), 16-byte chunk c stored at c ^ ((r >> 1) & 7)
 __device__ __forceinline__ int stage_swz(int r) { return (r >> 1) & 7; }
 
-template <int kHGroups>
+template <int kHGroups, int kD>
 __global__ void __launch_bounds__(kCThreads, 1)
 bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ dout,
                    const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf, uint16_t* __restrict__ cbuf,
                    int S, int s_kv, int H, int K, int64_t q_offset, int row0, int rows) {
+  using CG = ContribGeom<kD>;
+  constexpr int kRC = CG::kRC, kStChunks = CG::kStChunks, kXChunks = CG::kXChunks;
   constexpr int kKSteps = 4 * kHGroups;                // 32-row k steps of X (128 rows per head group)
   __shared__ u32x4 lds[2 * kGTChunks + 2 * kStChunks];  // X staging at start; then G tiles + C stages
   __shared__ int sh_last;
@@ -602,10 +620,12 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   if (nblk == 0) return;
   const int nslots = min(K, nblk * kBN);
   const uint16_t* grow = gbuf + ((int64_t)b * rows + lr) * (int64_t)g_slots(K) * kGW;
-  uint16_t* crow = cbuf + ((int64_t)b * rows + lr) * (int64_t)K * kDqk;
+  uint16_t* crow = cbuf + ((int64_t)b * rows + lr) * (int64_t)K * kD;
   const lds_char* lb = lds_bytes(&lds[0]);
+  const int t0w = CG::tile0(wave);               // the wave's first 16-column tile
+  const bool three = CG::kFull == kCW || wave < CG::kFull;  // (wave-uniform) it owns three tiles
 
-  // ---- X^T slice into VGPRs: xa[t][ks] = X[32 ks + 8g .. +8][48w + 16t + col] ----
+  // ---- X^T slice into VGPRs: xa[t][ks] = X[32 ks + 8g .. +8][16 (t0w + t) + col] ----
   // (rows of dO at the rope columns are zero, so every MFMA below runs unconditionally)
   u32x4 xa[3][kKSteps];
   const int tr_row = 8 * g + (col >> 2);  // source row within a 32-row k step (+4 second read)
@@ -614,14 +634,14 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     __syncthreads();
     const int hgk = kc >> 1, type = kc & 1;
     for (int i = tid; i < kXChunks; i += kCThreads) {
-      const int row = i / kRowChunks, c = i - row * kRowChunks;
+      const int row = i / kRC, c = i - row * kRC;
       const int head = hgk * kHG + row;
       u32x4 v = (u32x4){0u, 0u, 0u, 0u};
       if (head < H) {
-        if (type == 0) v = *reinterpret_cast<const u32x4*>(q + (row_id * H + head) * kDqk + c * 8);
+        if (type == 0) v = *reinterpret_cast<const u32x4*>(q + (row_id * H + head) * kD + c * 8);
         else if (c < kDv / 8) v = *reinterpret_cast<const u32x4*>(dout + (row_id * H + head) * kDv + c * 8);
       }
-      lds[row * kRowChunks + (c ^ swz8(row))] = v;
+      lds[row * kRC + (c ^ swz8(row))] = v;
     }
     __syncthreads();
 #pragma unroll
@@ -630,9 +650,9 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
       const int r1 = 32 * kl + tr_row, r2 = r1 + 4;
 #pragma unroll
       for (int t = 0; t < 3; ++t) {
-        const int c0 = (48 * wave + 16 * t) / 8 + ((col & 3) >> 1);
-        const lds_char* a1 = lb + 16 * (r1 * kRowChunks + (c0 ^ swz8(r1))) + 8 * (col & 1);
-        const lds_char* a2 = lb + 16 * (r2 * kRowChunks + (c0 ^ swz8(r2))) + 8 * (col & 1);
+        const int c0 = 2 * min(t0w + t, CG::kNT - 1) + ((col & 3) >> 1);  // (a two-tile wave's third: unused)
+        const lds_char* a1 = lb + 16 * (r1 * kRC + (c0 ^ swz8(r1))) + 8 * (col & 1);
+        const lds_char* a2 = lb + 16 * (r2 * kRC + (c0 ^ swz8(r2))) + 8 * (col & 1);
         xa[t][ks] = lds_read_tr_pair(a1, a2);
       }
     }
@@ -706,34 +726,40 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
-          for (int t = 0; t < 3; ++t)
+          for (int t = 0; t < 2; ++t)
             acc[h2][t] = mfma16x16x32(as_bf16x8(xa[t][ks]), as_bf16x8(bg[ks & 1][h2]), acc[h2][t]);
+        if (three) {
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+            acc[h2][2] = mfma16x16x32(as_bf16x8(xa[2][ks]), as_bf16x8(bg[ks & 1][h2]), acc[h2][2]);
+        }
       }
-      // lane (slot 16 h2 + col, g) holds columns 48w + 16t + 4g + r: 8 bytes at chunk
-      // 6w + 2t + g/2, half g & 1 of the stage row
+      // lane (slot 16 h2 + col, g) holds columns 16 (t0w + t) + 4g + r: 8 bytes at chunk
+      // 2 (t0w + t) + g/2, half g & 1 of the stage row
       lds_char* stg = stage + (step & 1) * (kStChunks * 16);
 #pragma unroll
       for (int h2 = 0; h2 < 2; ++h2) {
         const int r = 16 * h2 + col;
 #pragma unroll
         for (int t = 0; t < 3; ++t) {
+          if (t == 2 && !three) break;
           typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
           const u32x2 w2 = {pack_bf16x2(acc[h2][t][0], acc[h2][t][1]), pack_bf16x2(acc[h2][t][2], acc[h2][t][3])};
-          const int c = 6 * wave + 2 * t + (g >> 1);
-          *(__attribute__((address_space(3))) u32x2*)(stg + r * (kRowChunks * 16) + 16 * (c ^ stage_swz(r)) + 8 * (g & 1)) = w2;
+          const int c = 2 * (t0w + t) + (g >> 1);
+          *(__attribute__((address_space(3))) u32x2*)(stg + r * (kRC * 16) + 16 * (c ^ stage_swz(r)) + 8 * (g & 1)) = w2;
         }
       }
       __syncthreads();  // the step's C rows are complete in the stage
-      // whole rows out: thread chunk i -> row i / 72, chunk i % 72
+      // whole rows out: thread chunk i -> row i / kRC, chunk i % kRC
       int t_ = tid;
       asm volatile("" : "+v"(t_));
 #pragma unroll
-      for (int m = 0; m < kStChunks / kCThreads; ++m) {
+      for (int m = 0; m < (kStChunks + kCThreads - 1) / kCThreads; ++m) {
         const int i = t_ + kCThreads * m;
-        const int r = i / kRowChunks, c = i - r * kRowChunks;
-        if (s0 + r < nslots) {
-          const u32x4 v = lds_read16(stg + r * (kRowChunks * 16) + 16 * (c ^ stage_swz(r)));
-          *reinterpret_cast<u32x4*>(crow + (int64_t)(s0 + r) * kDqk + 8 * c) = v;
+        const int r = i / kRC, c = i - r * kRC;
+        if ((kStChunks % kCThreads == 0 || i < kStChunks) && s0 + r < nslots) {
+          const u32x4 v = lds_read16(stg + r * (kRC * 16) + 16 * (c ^ stage_swz(r)));
+          *reinterpret_cast<u32x4*>(crow + (int64_t)(s0 + r) * kD + 8 * c) = v;
         }
       }
     }
@@ -833,17 +859,17 @@ struct BwdPlan {
   int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, delta_bytes, total;
 };
 
-// Scratch per chunk: G and C (bf16), the CSR pair list and offsets, and delta (fp32 per
-// row and head).
-BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget) {
+// Scratch per chunk: G and C (bf16, C rows `width` columns), the CSR pair list and
+// offsets, and delta (fp32 per row and head).
+BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget, int64_t width) {
   BwdPlan p{};
-  const int64_t per_row = batch * g_slots(topk) * kGW * 2 + batch * topk * (int64_t)(kDqk * 2 + 4) +
+  const int64_t per_row = batch * g_slots(topk) * kGW * 2 + batch * topk * (int64_t)(width * 2 + 4) +
                           batch * kHeadsMax * 4;
   int64_t rows = s_q;
   if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
   p.rows = rows;
   p.g_bytes = batch * rows * g_slots(topk) * kGW * 2;
-  p.c_bytes = batch * rows * topk * kDqk * 2;
+  p.c_bytes = batch * rows * topk * width * 2;
   p.pairs_bytes = rows * topk * 4;
   p.csr_bytes = csr_ws_bytes(s_kv, rows, topk);
   p.delta_bytes = batch * rows * kHeadsMax * 4;
@@ -860,9 +886,9 @@ constexpr int64_t kDefaultBudget = 32LL << 30;  // scratch for the G / C chunks 
 extern "C" int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
                                                      int64_t d_qk, int64_t topk) {
   (void)n_heads;
-  (void)d_qk;
   if (batch <= 0 || s_q <= 0 || s_kv <= 0 || topk <= 0) return 0;
-  return dsa::plan_bwd(batch, s_q, s_kv, topk, dsa::kDefaultBudget).total;
+  const int64_t width = d_qk == dsa::kDv ? dsa::kDv : dsa::kDqk;  // C row width of the bf16 path
+  return dsa::plan_bwd(batch, s_q, s_kv, topk, dsa::kDefaultBudget, width).total;
 }
 
 extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out,
@@ -895,15 +921,16 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
     return check_launch("dsa_sparse_mla_bwd(f32)");
   }
   if (dtype != DSA_BF16) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: dtype %d", dtype);
-  if (d_qk != kDqk || d_v != kDv)
-    return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: bf16 path needs d_qk=576, d_v=512");
+  if ((d_qk != kDqk && d_qk != kDv) || d_v != kDv)
+    return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: bf16 path needs d_qk = 576 or 512, d_v = 512");
   if (n_heads > kHeadsMax) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: bf16 path needs H <= 128");
-  if (s_kv > GatherGeom::kMaxRows)
-    return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: S_kv > %lld", (long long)GatherGeom::kMaxRows);
+  const bool rope = d_qk == kDqk;
+  const int64_t max_rows = rope ? GatherGeom::kMaxRows : GatherGeomT<kDv>::kMaxRows;
+  if (s_kv > max_rows) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_bwd: S_kv > %lld", (long long)max_rows);
   if (!workspace) return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: workspace required");
   // choose the largest chunk whose scratch fits the given workspace
-  BwdPlan plan = plan_bwd(batch, s_q, s_kv, topk, workspace_bytes);
-  while (plan.total > workspace_bytes && plan.rows > 1) plan = plan_bwd(batch, plan.rows - 1, s_kv, topk, 0);
+  BwdPlan plan = plan_bwd(batch, s_q, s_kv, topk, workspace_bytes, d_qk);
+  while (plan.total > workspace_bytes && plan.rows > 1) plan = plan_bwd(batch, plan.rows - 1, s_kv, topk, 0, d_qk);
   if (plan.total > workspace_bytes)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: workspace of %lld bytes is too small",
                      (long long)workspace_bytes);
@@ -927,34 +954,34 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
     }
     dim3 ga((unsigned)rows, 1, (unsigned)batch);
     {
-      const TimedLaunch tl("bwd_sdp_kernel", st);
-      bwd_sdp_kernel<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout,
-                                         softmax_max, softmax_sum, dbuf, gbuf, mass, (int)s_q, (int)s_kv,
-                                         (int)n_heads, (int)topk, scale, q_offset, (int)r0);
+      const TimedLaunch tl(rope ? "bwd_sdp_kernel" : "bwd_sdp_kernel<512>", st);
+      auto* kern = rope ? bwd_sdp_kernel<kDqk> : bwd_sdp_kernel<kDv>;
+      kern<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout, softmax_max,
+                               softmax_sum, dbuf, gbuf, mass, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale,
+                               q_offset, (int)r0);
     }
     if (int rc = check_launch("dsa_sparse_mla_bwd(sdp)")) return rc;
     {
-      const TimedLaunch tl("bwd_dqk_kernel", st);
-      bwd_dqk_kernel<<<ga, 512, 0, st>>>((const uint16_t*)kv, indices, gbuf, (uint16_t*)dq, (int)s_q, (int)s_kv,
-                                         (int)n_heads, (int)topk, q_offset, (int)r0);
+      const TimedLaunch tl(rope ? "bwd_dqk_kernel" : "bwd_dqk_kernel<512>", st);
+      auto* kern = rope ? bwd_dqk_kernel<kDqk> : bwd_dqk_kernel<kDv>;
+      kern<<<ga, 512, 0, st>>>((const uint16_t*)kv, indices, gbuf, (uint16_t*)dq, (int)s_q, (int)s_kv, (int)n_heads,
+                               (int)topk, q_offset, (int)r0);
     }
     if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
     dim3 gb((unsigned)rows, (unsigned)batch);
     {
-      const TimedLaunch tl(hgroups == 1 ? "bwd_contrib_kernel<1>" : "bwd_contrib_kernel<2>", st);
-      if (hgroups == 1)
-        bwd_contrib_kernel<1><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf,
-                                                        cbuf, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset,
-                                                        (int)r0, rows);
-      else
-        bwd_contrib_kernel<2><<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf,
-                                                        cbuf, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, q_offset,
-                                                        (int)r0, rows);
+      static const char* const names[2][2] = {{"bwd_contrib_kernel<1,512>", "bwd_contrib_kernel<2,512>"},
+                                              {"bwd_contrib_kernel<1>", "bwd_contrib_kernel<2>"}};
+      const TimedLaunch tl(names[rope][hgroups == 1 ? 0 : 1], st);
+      auto* kern = rope ? (hgroups == 1 ? bwd_contrib_kernel<1, kDqk> : bwd_contrib_kernel<2, kDqk>)
+                        : (hgroups == 1 ? bwd_contrib_kernel<1, kDv> : bwd_contrib_kernel<2, kDv>);
+      kern<<<gb, kCThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)dout, indices, gbuf, cbuf, (int)s_q,
+                                     (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0, rows);
     }
     if (int rc = check_launch("dsa_sparse_mla_bwd(contrib)")) return rc;
     for (int b = 0; b < (int)batch; ++b)
       if (int rc = csr_reduce(indices, cbuf, dkv_accum, pairs, counts, (int)s_q, (int)s_kv, (int)topk, q_offset,
-                              (int)r0, rows, b, kRowChunks, st))
+                              (int)r0, rows, b, (int)(d_qk / 8), st))
         return rc;
   }
   return DSA_OK;

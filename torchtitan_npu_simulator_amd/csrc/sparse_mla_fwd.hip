@@ -49,15 +49,20 @@ typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 
+template <int kD>  // row width of Q and KV: 576 (latent + rope) or 512 (no rope)
 __global__ void __launch_bounds__(kFwdThreads, 1)
 sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv,
                            const int32_t* __restrict__ idx, uint16_t* __restrict__ out, float* __restrict__ smax,
                            float* __restrict__ ssum, int S, int s_kv, int H, int K, float scale_log2,
                            int64_t q_offset) {
-  using Gather = RowGather<kFwdWaves>;
+  using Gather = RowGather<kFwdWaves, kD>;
+  using Geo = GatherGeomT<kD>;
   constexpr int kPer = Gather::kMaxPerWave;
-  __shared__ u32x4 tile[3][kTileChunks];
-  __shared__ u32x4 qpe[kFwdHeads][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
+  constexpr int kTC = Geo::kTileChunks, kRB = Geo::kRowBytes;
+  constexpr int kKS = kD / 16;                // MFMA k-steps of S^T (36 | 32)
+  constexpr bool kRope = kKS > kLatSteps;     // the rope columns 512..575 exist
+  __shared__ u32x4 tile[3][kTC];
+  __shared__ u32x4 qpe[kRope ? kFwdHeads : 1][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
   __shared__ int sh_last;
 
@@ -71,7 +76,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   const int64_t orow = row_id * H + (hok ? head : 0);
   const int32_t* ridx = idx + row_id * K;
   const int64_t limit = tok + q_offset;
-  const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
+  const uint16_t* kvb = kv + (int64_t)b * s_kv * kD;
 
   // the row's slot indices (block count), the index ring entries of blocks 0..2 (wave 0,
   // DMA) and the row's Q are requested together; the block count waits only for the indices
@@ -88,11 +93,11 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   // zeroed after it)
   u32x4 qb[kLatSteps], qr[4];
   {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + orow * kDqk);
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + orow * kD);
 #pragma unroll
     for (int s = 0; s < kLatSteps; ++s) qb[s] = qh[2 * s + h];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qr[j] = qh[64 + 4 * h + j];  // rope chunks 64 + 4h ..
+    for (int j = 0; j < 4; ++j) qr[j] = kRope ? qh[64 + 4 * h + j] : (u32x4){0u, 0u, 0u, 0u};  // rope chunks 64 + 4h ..
   }
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (nblk == 0) {
@@ -115,10 +120,12 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
 #pragma unroll
     for (int j = 0; j < 4; ++j) qr[j] = (u32x4){0u, 0u, 0u, 0u};
   }
+  if constexpr (kRope) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {  // rope chunks 64..71: lane h writes 4h .. 4h+3
-    const int ch = 4 * h + j;
-    qpe[hl][ch ^ ((hl >> 1) & 7)] = qr[j];
+    for (int j = 0; j < 4; ++j) {  // rope chunks 64..71: lane h writes 4h .. 4h+3
+      const int ch = 4 * h + j;
+      qpe[hl][ch ^ ((hl >> 1) & 7)] = qr[j];
+    }
   }
 #pragma unroll
   for (int s = 0; s < kLatSteps; ++s) asm volatile("" : "+v"(qb[s]));  // landed before any DMA
@@ -128,7 +135,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   // XOR only touches bits 0..2 of 8u + 2s0 + h, so offset = ka_off[s0] + 128 u.
   uint32_t ka_off[4];
 #pragma unroll
-  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRowBytes + 16 * ((2 * s0 + h) ^ swz_kv(n));
+  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRB + 16 * ((2 * s0 + h) ^ swz_kv(n));
   // rope B operand, step 32 + e: head row hl, chunk (2e + h) ^ ((hl >> 1) & 7)
   const lds_char* qpe_b = lds_bytes(&qpe[0][0]);
   // Transposed V reads for O^T[32 dv x 32 heads] += V^T . P^T, dv tile dt, key step kk:
@@ -147,7 +154,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
 #pragma unroll
       for (int d0 = 0; d0 < 2; ++d0) {
         const int ch = 4 * d0 + 2 * (G & 1) + ((c & 3) >> 1);
-        tr_off[x][d0] = r * kRowBytes + 16 * (ch ^ swz_kv(r)) + 8 * (c & 1);
+        tr_off[x][d0] = r * kRB + 16 * (ch ^ swz_kv(r)) + 8 * (c & 1);
       }
     }
   }
@@ -167,7 +174,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
   if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
   __syncthreads();                                                  // publishes them and qpe
-  for (int i = tid; i < kTileChunks; i += kFwdThreads) tile[2][i] = (u32x4){0u, 0u, 0u, 0u};
+  for (int i = tid; i < kTC; i += kFwdThreads) tile[2][i] = (u32x4){0u, 0u, 0u, 0u};
   uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
 #pragma unroll
   for (int i = 0; i < kPer; ++i) Gather::issue_slot(kvb, &tile[0][0], i, wave, Gather::ring_slot(sidx[0], i, gl), gl, lim, K);
@@ -175,9 +182,10 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   __syncthreads();
 
   constexpr int kQBatch = 4;                  // k-steps per QK batch
-  constexpr int kQB = kKSteps / kQBatch;      // 9 QK batches
+  constexpr int kQB = kKS / kQBatch;          // 9 | 8 QK batches
   static_assert(kQB >= kPer, "one row DMA per QK batch");
-  static_assert(kLatSteps % kQBatch == 0 && kKSteps - kLatSteps == kQBatch, "rope steps form the last QK batch");
+  static_assert(kLatSteps % kQBatch == 0 && (kKS - kLatSteps == kQBatch || kKS == kLatSteps),
+                "rope steps form the last QK batch");
   constexpr int kVB = kDv / 32;               // 16 PV batches (one dv tile, two key steps)
   u32x4 bp_prev[2] = {(u32x4){0u, 0u, 0u, 0u}, (u32x4){0u, 0u, 0u, 0u}};
 
@@ -201,7 +209,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
     static_for<kQB>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
       if constexpr (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
-      if constexpr ((nb + 1) * kQBatch == kLatSteps) {  // rope B operands one batch ahead
+      if constexpr (kRope && (nb + 1) * kQBatch == kLatSteps) {  // rope B operands one batch ahead
 #pragma unroll
         for (int e = 0; e < kQBatch; ++e) rope[e] = lds_read16(qpe_b + hl * 128 + 16 * ((2 * e + h) ^ ((hl >> 1) & 7)));
       }
@@ -242,7 +250,7 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   auto read_v = [&](const lds_char* vb, u32x4 (&dst)[2], int dt) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const lds_char* base = vb + kk * 16 * kRowBytes + 128 * (dt >> 1);
+      const lds_char* base = vb + kk * 16 * kRB + 128 * (dt >> 1);
       dst[kk] = lds_read_tr_pair(base + tr_off[0][dt & 1], base + tr_off[1][dt & 1]);
     }
   };
@@ -688,17 +696,23 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
     return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: topk <= 16384 supported (got %lld)", (long long)topk);
   const size_t sc_bytes = (size_t)topk * sizeof(float);
   if (dtype == DSA_BF16) {
-    if (d_qk != kDqk || d_v != kDv)
-      return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: bf16 path needs d_qk=576, d_v=512 (got %lld/%lld)",
-                       (long long)d_qk, (long long)d_v);
-    if (s_kv > GatherGeom::kMaxRows)
-      return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: S_kv > %lld", (long long)GatherGeom::kMaxRows);
+    if ((d_qk != kDqk && d_qk != kDv) || d_v != kDv)
+      return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: bf16 path needs d_qk = 576 or 512, d_v = 512 "
+                       "(got %lld/%lld)", (long long)d_qk, (long long)d_v);
+    const bool rope = d_qk == kDqk;
+    const int64_t max_rows = rope ? GatherGeom::kMaxRows : GatherGeomT<kDv>::kMaxRows;
+    if (s_kv > max_rows) return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: S_kv > %lld", (long long)max_rows);
     dim3 grid((unsigned)s_q, ceil_div(n_heads, kFwdHeads), (unsigned)batch);
     {
-      const TimedLaunch tl("sparse_mla_fwd_bf16_kernel", st);
-      sparse_mla_fwd_bf16_kernel<<<grid, kFwdThreads, 0, st>>>(
-          (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
-          (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
+      const TimedLaunch tl(rope ? "sparse_mla_fwd_bf16_kernel" : "sparse_mla_fwd_bf16_kernel<512>", st);
+      if (rope)
+        sparse_mla_fwd_bf16_kernel<kDqk><<<grid, kFwdThreads, 0, st>>>(
+            (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
+            (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
+      else
+        sparse_mla_fwd_bf16_kernel<kDv><<<grid, kFwdThreads, 0, st>>>(
+            (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
+            (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
     }
     if (int rc = check_launch("dsa_sparse_mla_fwd(bf16)")) return rc;
     dim3 fgrid((unsigned)s_q, 1, (unsigned)batch);

@@ -797,8 +797,9 @@ def _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, o
 
 def _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, cmp_ratio, ori_win_left, ori_win_right):
     """Kernel operands of the shared-KV attention: query and cat(ori_kv, cmp_kv) rows as the
-    gathered-attention kernels take them (bf16: 576-column rows, the value columns first and
-    zeros after; fp32: as given) and the [B,S,W(+K)] slot indices over the concatenated rows."""
+    gathered-attention kernels take them (bf16: 512-column rows, the kernels' rope-less
+    width, zero-padded when D < 512; fp32: as given) and the [B,S,W(+K)] slot indices over
+    the concatenated rows."""
     B, S, H, D = query.shape
     ori = ori_kv.reshape(ori_kv.shape[0], ori_kv.shape[1], ori_kv.shape[-1])
     cmp = None if cmp_kv is None else cmp_kv.reshape(cmp_kv.shape[0], cmp_kv.shape[1], cmp_kv.shape[-1])
@@ -812,9 +813,9 @@ def _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, cmp_ratio, ori_
     bf16 = query.dtype == torch.bfloat16
     if bf16 and D > 512:
         raise NotImplementedError(f"bf16 shared-KV attention needs head_dim <= 512 (got {D})")
-    # bf16: rows padded to the kernel's 576 = 512 value columns + 64 (zero) columns; k = v
-    # = the whole row.  fp32: the exact kernel takes any width.
-    dqk, dv = (576, 512) if bf16 else (D, D)
+    # bf16: 512-column rows (k = v = the whole row; the kernels' d_qk = d_v = 512 variant,
+    # no rope columns).  fp32: the exact kernel takes any width.
+    dqk, dv = (512, 512) if bf16 else (D, D)
     return dict(q=_pad_rows(query, dqk), kv=_pad_rows(kv, dqk), idx=idx, D=D, dv=dv, s_ori=ori.shape[1],
                 has_cmp=cmp is not None)
 
@@ -974,7 +975,7 @@ class SparseAttnSharedKV(torch.autograd.Function):
             max_seq_len_kv, 0, topk, cmp_ratio, ori_mask_mode, cmp_mask_mode, ori_win_left, ori_win_right, layout_q,
             layout_kv, ori_kv is not None, cmp_kv is not None, device=query.device)
         _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, ori_win_right)
-        # the kernels' operands are kept for backward (the bf16 path pads query rows to 576)
+        # the kernels' operands are kept for backward (the bf16 path pads query rows to 512)
         prep = _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, int(cmp_ratio), ori_win_left,
                                  ori_win_right)
         sk = None if sinks is None else sinks.float().contiguous()
