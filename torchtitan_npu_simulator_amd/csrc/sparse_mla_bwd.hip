@@ -689,10 +689,27 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     }
   };
   load_g(0, 0);
+  // C-row store instructions a wave issues per step: one per 768-chunk slice of the stage
+  // that holds any of its chunks (576 columns: 3 for every wave; 512: 3 for waves 0..7, 2
+  // for waves 8..11)
+  constexpr int kStSlices = (kStChunks + kCThreads - 1) / kCThreads;
+  const bool last_slice = kStChunks % kCThreads == 0 || wave * 64 < kStChunks % kCThreads;
   int step = 0;
   for (int tl = 0; tl < ntiles; ++tl) {
     const int buf = tl & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's part of tile tl (and its stores) done
+    // this wave's part of tile tl landed.  Its DMA was issued before the C-row stores of
+    // tile tl-1's two steps (every row of a tile before the last exists, so every store
+    // instruction of those steps issues); vector memory operations retire in issue order,
+    // so waiting until only those stores are outstanding covers the DMA and leaves the
+    // stores in flight
+    if (tl == 0) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (last_slice) {
+      static_assert(kStSlices == 3, "the counted waits below assume three stage slices");
+      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    }
     __syncthreads();  // every wave's part landed; the other G buffer is free
     if (tl + 1 < ntiles) load_g(tl + 1, buf ^ 1);
     const lds_char* gb = gtile + buf * (kGTChunks * 16);

@@ -7,8 +7,10 @@
 //
 // One 256-thread workgroup per row.  A row is read in segments of 1024·kR scores: thread t
 // holds float4 chunks j = 0..kR-1 at positions 4(t + 256 j), so a segment is one coalesced
-// sweep and index order is (segment, j, thread, element).  Rows of one segment stay in
-// registers for every pass; longer rows are re-read per pass (from L2 / MALL).
+// sweep and index order is (segment, j, thread, element).  The scores become order keys
+// once, as they are loaded; rows of one segment stay in registers for every pass, longer
+// rows are re-read per pass (from L2 / MALL).  A chunk that starts past the row's valid
+// prefix (causal rows) is skipped by the whole workgroup, in every pass.
 //   pass 0   count of candidates, min and max key
 //   pass 1.. histogram of the next 11 bits of (key - min) below the current bin; the bin
 //            holding the k-th largest key becomes the new prefix.  Digits start at the
@@ -17,7 +19,8 @@
 //            exactly the remaining quota or the bin is a single key value.
 //   compact  key > T is taken; key == T is taken for the first need_eq such keys in index
 //            order.  Output position = (#taken-above before it) + min(#equal before it,
-//            need_eq), from wave ballots and per-(wave, chunk) totals.
+//            need_eq), from wave ballots and per-(wave, chunk) totals (the key == T ballots
+//            only when the threshold has ties).
 #include "dsa_common.h"
 
 namespace dsa {
@@ -73,7 +76,9 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   __shared__ uint32_t tot[2][kR][kWaves];  // per-(chunk, wave) counts of key > T and key == T
   __shared__ uint32_t sh_bin[3];
 
-  const int s = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  // rows are dispatched last-first: under the causal rule the later rows hold the longest
+  // valid prefixes, so the slowest workgroups start first instead of forming the tail
+  const int s = S - 1 - (int)blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int64_t row = (int64_t)b * S + s;
   const float* src = scores + row * ld;
@@ -82,46 +87,40 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   const int nseg = kSingle ? 1 : (nv + kSeg - 1) / kSeg;
   const int s_k4 = s_k & ~3;  // scores [0, s_k4) are covered by whole float4 loads
 
-  float x[kR][4];
-  // positions past the row's valid prefix become NaN (not candidates)
+  // chunk j of segment sg covers positions [sg kSeg + 1024 j, +1024): it holds a valid
+  // position iff it starts below nv (workgroup-uniform), so chunks past the row's valid
+  // prefix are neither loaded nor examined
+  auto live = [&](int sg, int j) { return sg * kSeg + kThreads * 4 * j < nv; };
+  // order keys of the thread's scores; positions past the valid prefix and NaN scores are
+  // key 0 (not candidates)
+  uint32_t key[kR][4];
   auto load_seg = [&](int sg) {
-    if (kVec) {
 #pragma unroll
-      for (int j = 0; j < kR; ++j) {
-        const int base = sg * kSeg + 4 * (t + kThreads * j);
-        const int at = min(base, s_k4 - 4);  // in bounds; used only when at == base
-        // only the row's valid prefix is read: scores at or past nv may be unwritten
-        const float4 v = base < nv ? *reinterpret_cast<const float4*>(src + at) : make_float4(0.f, 0.f, 0.f, 0.f);
-        x[j][0] = v.x;
-        x[j][1] = v.y;
-        x[j][2] = v.z;
-        x[j][3] = v.w;
-      }
+    for (int j = 0; j < kR; ++j) {
+      const int base = sg * kSeg + 4 * (t + kThreads * j);
+      float x[4] = {0.f, 0.f, 0.f, 0.f};
+      if (live(sg, j)) {
+        if (kVec) {
+          const int at = min(base, s_k4 - 4);  // in bounds; used only when at == base
+          // only the row's valid prefix is read: scores at or past nv may be unwritten
+          if (base < nv) {
+            const float4 v = *reinterpret_cast<const float4*>(src + at);
+            x[0] = v.x;
+            x[1] = v.y;
+            x[2] = v.z;
+            x[3] = v.w;
+          }
+          if (base >= s_k4 && base < nv) {  // the partial last chunk of a row whose length is not a multiple of 4
 #pragma unroll
-      for (int j = 0; j < kR; ++j) {
-        const int base = sg * kSeg + 4 * (t + kThreads * j);
-        if (base >= s_k4 && base < nv) {  // the partial last chunk of a row whose length is not a multiple of 4
+            for (int e = 0; e < 4; ++e) x[e] = base + e < nv ? src[base + e] : 0.f;
+          }
+        } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) x[j][e] = base + e < nv ? src[base + e] : 0.f;
+          for (int e = 0; e < 4; ++e) x[e] = src[min(base + e, nv - 1)];
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (base + e >= nv) x[j][e] = __builtin_nanf("");
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < kR; ++j) {
-        const int base = sg * kSeg + 4 * (t + kThreads * j);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) x[j][e] = src[min(base + e, nv - 1)];
       }
 #pragma unroll
-      for (int j = 0; j < kR; ++j) {
-        const int base = sg * kSeg + 4 * (t + kThreads * j);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (base + e >= nv) x[j][e] = __builtin_nanf("");
-      }
+      for (int e = 0; e < 4; ++e) key[j][e] = base + e < nv ? order_key(x[e]) : 0u;
     }
   };
 
@@ -140,16 +139,16 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   for (int sg = 0; sg < nseg; ++sg) {
     load_seg(sg);
 #pragma unroll
-    for (int j = 0; j < kR; ++j)
+    for (int j = 0; j < kR; ++j) {
+      if (!live(sg, j)) continue;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t key = order_key(x[j][e]);
-        if (key) {
-          ++cnt;
-          kmin = min(kmin, key);
-          kmax = max(kmax, key);
-        }
+        const uint32_t kv = key[j][e];
+        cnt += kv != 0u;
+        kmin = min(kmin, kv ? kv : 0xffffffffu);
+        kmax = max(kmax, kv);
       }
+    }
   }
   cnt = wave_sum_u(cnt);
   kmin = wave_min_u(kmin);
@@ -172,7 +171,7 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   uint32_t T = 0u, need_eq = 0u;  // n_cand <= k: every candidate (key > 0)
   if (n_cand > (uint32_t)k) {
     const uint32_t range = kmax - kmin;
-    int sh = range ? 32 - __clz(range) : 0;  // the current bin is rel in [lo, lo + 2^sh)
+    int sh = range ? 32 - __clz(range) : 0;  // the current bin is rel = key - kmin in [lo, lo + 2^sh)
     uint32_t lo = 0u, rem = (uint32_t)k;
     bool whole_bin = false;
     while (sh > 0) {
@@ -180,16 +179,23 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
       const int nb = 1 << (sh - nsh);
       for (int i = t; i < nb; i += kThreads) hist[i] = 0u;
       __syncthreads();
+      // a candidate is in the bin iff key - (kmin + lo) <= span in 32-bit arithmetic: keys
+      // below the bin, key 0 (not a candidate) included, wrap to at least 2^32 - (kmin + lo),
+      // which the span never reaches once it is clamped to 2^32 - 1 - (kmin + lo); the clamp
+      // drops no candidate (candidate keys are at most order_key(+inf) = 0xff800000)
+      const uint32_t base_key = kmin + lo;
+      const uint32_t span = min(sh >= 32 ? 0xffffffffu : (1u << sh) - 1u, 0xffffffffu - base_key);
       for (int sg = 0; sg < nseg; ++sg) {
         if (!kSingle) load_seg(sg);
 #pragma unroll
-        for (int j = 0; j < kR; ++j)
+        for (int j = 0; j < kR; ++j) {
+          if (!live(sg, j)) continue;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const uint32_t key = order_key(x[j][e]);
-            const uint64_t d = (uint64_t)(key - kmin) - lo;  // wraps far above the bin when rel < lo
-            if (key && d < (1ull << sh)) atomicAdd(&hist[(uint32_t)(d >> nsh)], 1u);
+            const uint32_t d = key[j][e] - base_key;
+            if (d <= span) atomicAdd(&hist[d >> nsh], 1u);
           }
+        }
       }
       __syncthreads();
       // thread t sums bins [nb - 8(t+1), nb - 8t) (from the top); exclusive scan in thread
@@ -241,67 +247,91 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   }
 
   // ---- compaction in index order ----
-  uint32_t gt_base = 0, eq_base = 0;
-  for (int sg = 0; sg < nseg; ++sg) {
-    if (!kSingle) load_seg(sg);
-    uint32_t pg[kR], pe[kR], mg[kR], me[kR];  // lanes-below counts and this lane's flag bits
+  // (no tie at the threshold, the usual case: key > T alone decides, one ballot per score,
+  // in a code path of its own so that it holds no tie state)
+  auto compact = [&](auto ties_c) {
+    constexpr bool kTies = decltype(ties_c)::value;
+    uint32_t gt_base = 0, eq_base = 0;
+    for (int sg = 0; sg < nseg; ++sg) {
+      if (!kSingle) load_seg(sg);
+      // per chunk j: lanes-below counts (< 256: 8 bits, four chunks per word) and this lane's
+      // flag bits (4 bits, eight chunks per word), packed so that the compaction holds few
+      // registers besides the keys
+      constexpr int kW8 = (kR + 3) / 4, kW4 = (kR + 7) / 8;
+      uint32_t pg[kW8], pe[kW8], mg[kW4], me[kW4];
 #pragma unroll
-    for (int j = 0; j < kR; ++j) {
-      uint32_t below_g = 0, below_e = 0, wg = 0, we = 0, fg = 0, fe = 0;
+      for (int i = 0; i < kW8; ++i) pg[i] = pe[i] = 0u;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t key = order_key(x[j][e]);
-        const bool g = key > T;
-        const bool q = key == T && key != 0u;
-        const uint64_t bg = __ballot(g), bq = __ballot(q);
-        below_g += lanes_below(bg);
-        below_e += lanes_below(bq);
-        wg += (uint32_t)__popcll(bg);
-        we += (uint32_t)__popcll(bq);
-        fg |= (uint32_t)g << e;
-        fe |= (uint32_t)q << e;
-      }
-      pg[j] = below_g;
-      pe[j] = below_e;
-      mg[j] = fg;
-      me[j] = fe;
-      if (lane == 0) {
-        tot[0][j][wave] = wg;
-        tot[1][j][wave] = we;
-      }
-    }
-    __syncthreads();
-    uint32_t run_g = gt_base, run_e = eq_base;  // counts before chunk j of this segment
+      for (int i = 0; i < kW4; ++i) mg[i] = me[i] = 0u;
 #pragma unroll
-    for (int j = 0; j < kR; ++j) {
-      uint32_t bg = run_g + pg[j], be = run_e + pe[j];
+      for (int j = 0; j < kR; ++j) {
+        if (!live(sg, j)) continue;
+        uint32_t below_g = 0, below_e = 0, wg = 0, we = 0, fg = 0, fe = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        if (w < wave) {
-          bg += tot[0][j][w];
-          be += tot[1][j][w];
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t kv = key[j][e];
+          const bool g = kv > T;
+          const uint64_t bg = __ballot(g);
+          below_g += lanes_below(bg);
+          wg += (uint32_t)__popcll(bg);
+          fg |= (uint32_t)g << e;
+          if constexpr (kTies) {
+            const bool q = kv == T && kv != 0u;
+            const uint64_t bq = __ballot(q);
+            below_e += lanes_below(bq);
+            we += (uint32_t)__popcll(bq);
+            fe |= (uint32_t)q << e;
+          }
         }
-        run_g += tot[0][j][w];
-        run_e += tot[1][j][w];
-      }
-      const int base = sg * kSeg + 4 * (t + kThreads * j);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool g = (mg[j] >> e) & 1u, q = (me[j] >> e) & 1u;
-        const bool take = g || (q && be < need_eq);
-        const uint32_t pos = bg + min(be, need_eq);
-        if (take && pos < (uint32_t)k) {  // (always < k: the threshold admits exactly min(n_cand, k))
-          oi[pos] = (int32_t)(base + e + index_offset);
-          if (ov) ov[pos] = x[j][e];
+        pg[j >> 2] |= below_g << (8 * (j & 3));
+        pe[j >> 2] |= below_e << (8 * (j & 3));
+        mg[j >> 3] |= fg << (4 * (j & 7));
+        me[j >> 3] |= fe << (4 * (j & 7));
+        if (lane == 0) {
+          tot[0][j][wave] = wg;
+          tot[1][j][wave] = we;
         }
-        bg += g;
-        be += q;
       }
+      __syncthreads();
+      uint32_t run_g = gt_base, run_e = eq_base;  // counts before chunk j of this segment
+#pragma unroll
+      for (int j = 0; j < kR; ++j) {
+        if (!live(sg, j)) continue;
+        uint32_t bg = run_g + ((pg[j >> 2] >> (8 * (j & 3))) & 0xffu), be = run_e + ((pe[j >> 2] >> (8 * (j & 3))) & 0xffu);
+        const uint32_t fgj = mg[j >> 3] >> (4 * (j & 7)), fej = me[j >> 3] >> (4 * (j & 7));
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const uint32_t tg = tot[0][j][w], te = kTies ? tot[1][j][w] : 0u;
+          if (w < wave) {
+            bg += tg;
+            be += te;
+          }
+          run_g += tg;
+          run_e += te;
+        }
+        const int base = sg * kSeg + 4 * (t + kThreads * j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool g = (fgj >> e) & 1u, q = kTies && ((fej >> e) & 1u);
+          const bool take = g || (q && be < need_eq);
+          const uint32_t pos = bg + (kTies ? min(be, need_eq) : 0u);
+          if (take && pos < (uint32_t)k) {  // (always < k: the threshold admits exactly min(n_cand, k))
+            oi[pos] = (int32_t)(base + e + index_offset);
+            if (ov) ov[pos] = src[base + e];  // (the score as given: -0.0 keeps its sign)
+          }
+          bg += g;
+          be += q;
+        }
+      }
+      gt_base = run_g;
+      eq_base = run_e;
+      if (!kSingle) __syncthreads();  // tot is rewritten by the next segment
     }
-    gt_base = run_g;
-    eq_base = run_e;
-    if (!kSingle) __syncthreads();  // tot is rewritten by the next segment
-  }
+  };
+  if (need_eq != 0u)  // workgroup-uniform
+    compact(std::true_type{});
+  else
+    compact(std::false_type{});
   const uint32_t taken = min(n_cand, (uint32_t)k);
   for (int j = (int)taken + t; j < k; j += kThreads) {
     oi[j] = -1;
