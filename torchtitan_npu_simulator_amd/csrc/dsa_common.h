@@ -170,24 +170,35 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// LDS chunk swizzles.  gfx950's LDS has 64 banks of 4 bytes (256 B per clock): a b128
-// read is served 16 lanes per clock and a b64 read 32 lanes per clock, and each of those
-// lane groups must cover distinct banks.
+// LDS chunk swizzles.  Conflict rules of gfx950's LDS, measured per instruction with the
+// bank-conflict counter over full-wave address patterns (a group of lanes is served
+// together and must hit distinct slots of the period; equal addresses broadcast):
+//   ds_read_b128            4 groups of 16 lanes: each half-wave split by the parity of
+//                           lane bits 2..4; 16-byte slots of a 256-byte period
+//   ds_read_b64, ..._tr_b16 half-waves; 8-byte slots of a 256-byte period
+//   ds_read_b32             half-waves; 4-byte slots of a 128-byte period
+//   ds_write_b128           8-lane groups; 16-byte slots of a 128-byte period
+//   ds_write_b64            16-lane groups; 8-byte slots of a 128-byte period
+// Each swizzle below was chosen by exhaustive search over the linear (XOR) maps of the row
+// bits against every access pattern of the kernels that use it.
 //
 // swz8: 16-byte chunk c of row r lives at chunk c ^ swz8(r); any 8 consecutive rows get
-// distinct values (rows whose stride is a multiple of 256 B, read 8 rows at a time).
+// distinct values.
 __device__ __forceinline__ int swz8(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
-// swz_kv: for tiles of 1152-byte latent-KV rows (72 chunks; a row starts on bank 0 or 32
-// by parity).  The XOR value is row bits 1, 2, 3 reversed (period 16), chosen (by
-// exhaustive check over the linear swizzles) so that all four read patterns of the
-// attention kernels are conflict-free: b128 reads of one chunk column by 16 aligned rows
-// (each parity class takes all 8 values), and transposed b64 reads of 4 rows x 4 chunks
-// (rows 4q and 4q+2 differ in bit 2) or 8 rows x 2 chunks per 32 lanes.  Values are < 8,
-// so XOR keeps a chunk inside its aligned group of 8.
+// swz_kv: tiles of 1152-byte latent-KV rows (72 chunks; rows alternate between the two
+// 128-byte halves of the period): row bits 1, 2, 3 reversed, so the A-operand b128 reads
+// of one chunk column by 32 rows and the transposed b64 reads of 4 rows x 4 chunks are
+// conflict-free.  Values are < 8, so XOR keeps a chunk inside its aligned group of 8 and
+// commutes with the kernels' +8-chunk offsets; it ignores row bit 4.  (On 1024-byte rows
+// the b128 reads keep a 2-way conflict: a 16-row read group needs 16 distinct values.)
 __device__ __forceinline__ int swz_kv(int r) { return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
 // swz16: for rows whose stride is a multiple of 256 B with >= 16 chunks: 16 consecutive
-// rows reading one chunk column hit 16 distinct 16-byte bank groups.
+// rows reading one chunk column hit 16 distinct 16-byte slots.
 __device__ __forceinline__ int swz16(int r) { return r & 15; }
+// swz_kl: 256-byte rows of 16 chunks read both ways (the indexer KL key tile and q): b128
+// reads of one chunk column (4c + lane / 16) by 16 consecutive rows, and transposed b64
+// reads of rows 8g + 0..3 (+4) by the two lane quarters of a half-wave.
+__device__ __forceinline__ int swz_kl(int r) { return ((r & 7) << 1) ^ (((r >> 3) & 1) * 9); }
 
 // 16-byte-per-lane DMA from global memory straight into LDS (global_load_lds_dwordx4):
 // lane i reads gbase + voff and writes LDS byte lds_base + 16 i.  gbase and lds_base must

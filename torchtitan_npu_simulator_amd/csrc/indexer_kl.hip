@@ -16,7 +16,8 @@
 //            dk^T[128 d x 16 slots of wave w] = q^T E over all 64 heads (q^T operands read
 //            transposed from q staged in LDS once per row), written as bf16 whole rows
 //            through a wave-private LDS stage and reduced per key by the shared CSR pass.
-// LDS key rows use the swz8 chunk swizzle (conflict-free b128 and transposed reads).
+// LDS key rows (and q, staged once per row) use the swz_kl chunk swizzle: the b128 column
+// reads of 16 rows and the transposed b64 reads are both conflict-free.
 // A generic fp32 kernel (any H, D) handles shapes outside the MFMA tile.
 #include <algorithm>
 
@@ -84,7 +85,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const float gsc = grad_scale_dev ? grad_scale * grad_scale_dev[0] : grad_scale;
 
   // Key-row gather, 64 rows x 256 B per block: 4 DMA instructions per wave, instruction
-  // J = 4 wave + i covering tile chunks [64J, 64J+64) (row p / 16, chunk (p % 16) ^ swz8(row)).
+  // J = 4 wave + i covering tile chunks [64J, 64J+64) (row p / 16, chunk (p % 16) ^ swz_kl(row)).
   // The block's slot indices reach an LDS ring by DMA (wave 0, one dword per lane) two
   // blocks ahead, and every DMA is inline assembly (the compiler neither waits for it before
   // LDS reads nor counts it), so the only wait is the explicit one at the top of each block.
@@ -100,7 +101,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       const int J = wave * 4 + i;
       const int p = J * 64 + lane;
       const int row = p >> 4, pos = p & 15;
-      const int chunk = pos ^ swz8(row);
+      const int chunk = pos ^ swz_kl(row);
       const int slot = blk * kB + row;
       const int vi = ring[blk & 3][row];
       const int r = (slot < K && ok_slot(vi, s_k, limit)) ? vi : 0;
@@ -258,7 +259,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     u32x4 bk[kD / 32];
 #pragma unroll
     for (int c = 0; c < kD / 32; ++c)
-      bk[c] = *(const lds_u32x4*)(uintptr_t)(tb + 16 * (row * kRowC + ((4 * c + g) ^ swz8(row))));
+      bk[c] = *(const lds_u32x4*)(uintptr_t)(tb + 16 * (row * kRowC + ((4 * c + g) ^ swz_kl(row))));
 #pragma unroll
     for (int c = 0; c < kD / 32; ++c) acc = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk[c]), acc);
     return acc;
@@ -273,14 +274,14 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const int tr_row = 8 * g + (col >> 2);
   if (gs != 0.f) {  // block-uniform
     // q^T for dk (A of 16x16x32 over heads): tile dt covers d = 16 dt + col, k-step ks
-    // heads 32 ks + 8g .. +7; q [64 heads x 128 d] is staged row-major in kt[1] (swz8) and
+    // heads 32 ks + 8g .. +7; q [64 heads x 128 d] is staged row-major in kt[1] (swz_kl) and
     // read transposed (source lane col supplies head row 32 ks + 8g + col/4 (+4 second
     // read), d columns 16 dt + 4 (col % 4))
     u32x4 qtr[kD / 16][2];
     __syncthreads();  // phase 1 is done with kt
     for (int i = tid; i < kH * kRowC; i += 256) {
       const int h = i >> 4, c = i & 15;
-      kt[1][h * kRowC + (c ^ swz8(h))] = *reinterpret_cast<const u32x4*>(qi + (row_id * kH + h) * kD + 8 * c);
+      kt[1][h * kRowC + (c ^ swz_kl(h))] = *reinterpret_cast<const u32x4*>(qi + (row_id * kH + h) * kD + 8 * c);
     }
     __syncthreads();
     {
@@ -291,8 +292,8 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
         for (int ks = 0; ks < 2; ++ks) {
           const int r1 = 32 * ks + tr_row, r2 = r1 + 4;
           const int c0 = 2 * dt + ((col & 3) >> 1);
-          qtr[dt][ks] = lds_read_tr_pair(qb + 16 * (r1 * kRowC + (c0 ^ swz8(r1))) + 8 * (col & 1),
-                                         qb + 16 * (r2 * kRowC + (c0 ^ swz8(r2))) + 8 * (col & 1));
+          qtr[dt][ks] = lds_read_tr_pair(qb + 16 * (r1 * kRowC + (c0 ^ swz_kl(r1))) + 8 * (col & 1),
+                                         qb + 16 * (r2 * kRowC + (c0 ^ swz_kl(r2))) + 8 * (col & 1));
         }
     }
     __syncthreads();  // kt[1] is a gather target again
@@ -341,8 +342,8 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
 #pragma unroll
         for (int dt = 0; dt < kD / 16; ++dt) {
           const int c0 = 2 * dt + ((col & 3) >> 1);
-          const uint32_t a1 = tb + 16 * (r1 * kRowC + (c0 ^ swz8(r1))) + 8 * (col & 1);
-          const uint32_t a2 = tb + 16 * (r2 * kRowC + (c0 ^ swz8(r2))) + 8 * (col & 1);
+          const uint32_t a1 = tb + 16 * (r1 * kRowC + (c0 ^ swz_kl(r1))) + 8 * (col & 1);
+          const uint32_t a2 = tb + 16 * (r2 * kRowC + (c0 ^ swz_kl(r2))) + 8 * (col & 1);
           const u32x4 av = lds_read_tr_pair((const lds_char*)(uintptr_t)a1, (const lds_char*)(uintptr_t)a2);
           dqa[dt] = mfma16x16x32(as_bf16x8(av), as_bf16x8(eb), dqa[dt]);
         }

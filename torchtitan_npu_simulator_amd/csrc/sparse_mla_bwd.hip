@@ -57,10 +57,10 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // lanes, then the 4 waves).  No dQ here: with no dQ accumulators the wave holds 32 heads,
 // so each K element read from LDS serves twice the heads of the one-kernel backward.
 // --------------------------------------------------------------------------------------
-// piece swizzle of the 256-entry transposed stage (64-byte rows): (r & 3, swz) injective
-// over 32 consecutive rows (the write of one piece by a wave's 32 head lanes), and 4
-// aligned rows x 4 pieces distinct (the flush's transposed reads)
-__device__ __forceinline__ int g2_swz(int r) { return (r >> 2) & 7; }
+// piece swizzle of the 256-entry transposed stage (64-byte rows): the b64 writes of one
+// piece by 16 consecutive head rows, and the flush's transposed reads (4 aligned rows x 4
+// pieces per lane quarter), are conflict-free
+__device__ __forceinline__ int g2_swz(int r) { return (r >> 1) & 7; }
 
 template <int kD>  // row width of Q and KV: 576 (latent + rope) or 512 (no rope)
 __global__ void __launch_bounds__(256, 1)
