@@ -64,10 +64,11 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
                        int s_k, int K, int64_t q_offset, float loss_scale, float eps, float grad_scale,
                        const float* __restrict__ grad_scale_dev, int row0) {
   __shared__ u32x4 kt[2][kTileC];           // gathered key rows [64][16 chunks], swizzled
-  __shared__ float iv[kMaxK];               // I_j, then g_j
+  __shared__ u32x4 qs[kH * kRowC];          // q of the row [64 heads][16 chunks] (phase 3), swizzled
+  extern __shared__ float iv[];             // I_j, then g_j: K rounded up to whole blocks
   __shared__ uint16_t es[kB][kH + 8];       // E as [slot][head]
   __shared__ uint16_t eh[kH][kB + 8];       // E as [head][slot]
-  __shared__ float red[4];
+  __shared__ float red[12];
   __shared__ int ring[4][kB];                 // slot indices of blocks b & 3
 
   const int lr = blockIdx.x, b = blockIdx.y;
@@ -183,19 +184,27 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
 
   // ---------------- phase 2: row statistics ----------------
   // each thread keeps its slots' validity, target mass and score in registers (one batch
-  // of loads instead of a dependent load per pass)
+  // of loads instead of a dependent load per pass); slot groups u with 256 u >= K are
+  // skipped (workgroup-uniform).  Two block reductions: (max, sum of exp at that max, Z)
+  // merged as running (max, sum) pairs, then (loss part, T).  exp and log use the hardware
+  // base-2 instructions.
   constexpr int kPer = kMaxK / 256;
   float mv[kPer], xv[kPer];
   bool okv[kPer];
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
     const int j = tid + 256 * u;
-    okv[u] = j < K && ok_slot(ridx[min(j, K - 1)], s_k, limit);
-    mv[u] = j < K ? mrow[j] : 0.f;
+    okv[u] = false;
+    mv[u] = xv[u] = 0.f;
+    if (256 * u < K) {
+      okv[u] = j < K && ok_slot(ridx[min(j, K - 1)], s_k, limit);
+      mv[u] = j < K ? mrow[j] : 0.f;
+    }
   }
   float lmax = -INFINITY, zsum = 0.f;
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
+    if (256 * u >= K) continue;
     const int j = tid + 256 * u;
     xv[u] = j < K ? iv[j] : 0.f;
     if (okv[u]) {
@@ -203,35 +212,73 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       zsum += fmaxf(mv[u], 0.f);
     }
   }
-  const float imax = block_reduce(lmax, red, true);
-  const float Z = block_reduce(zsum, red, false);
   float esum = 0.f;
 #pragma unroll
   for (int u = 0; u < kPer; ++u)
-    if (okv[u]) esum += expf(xv[u] - imax);
-  const float E = block_reduce(esum, red, false);
+    if (256 * u < K && okv[u]) esum += __builtin_amdgcn_exp2f((xv[u] - lmax) * kLog2e);
+  // (max, sum) pairs: s_a e^(m_a - m) + s_b e^(m_b - m) at m = max(m_a, m_b); a side with
+  // no valid slot has m = -inf, s = 0 and contributes 0
+  auto merge = [](float& m, float& se, float mo, float so) {
+    const float mn = fmaxf(m, mo);
+    const float a = m == -INFINITY ? 0.f : se * __builtin_amdgcn_exp2f((m - mn) * kLog2e);
+    const float b = mo == -INFINITY ? 0.f : so * __builtin_amdgcn_exp2f((mo - mn) * kLog2e);
+    m = mn;
+    se = a + b;
+  };
+#pragma unroll
+  for (int msk = 32; msk >= 1; msk >>= 1) {
+    const float mo = __shfl_xor(lmax, msk, 64), so = __shfl_xor(esum, msk, 64);
+    merge(lmax, esum, mo, so);
+    zsum += __shfl_xor(zsum, msk, 64);
+  }
+  if (lane == 0) {
+    red[wave] = lmax;
+    red[4 + wave] = esum;
+    red[8 + wave] = zsum;
+  }
+  __syncthreads();
+  float imax = red[0], E = red[4], Z = red[8];
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    merge(imax, E, red[i], red[4 + i]);
+    Z += red[8 + i];
+  }
   const bool valid_row = Z > eps;
-  const float lse = imax + logf(E);
-  const float zc = fmaxf(Z, eps);
+  const float lse = imax + __builtin_amdgcn_logf(E) * kLn2;
+  const float zc = fmaxf(Z, eps), rzc = 1.f / zc;
+  const float ls_uniform = -__builtin_amdgcn_logf((float)K) * kLn2;
   float lpart = 0.f, tpos = 0.f;
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
-    const float t = okv[u] ? fmaxf(mv[u], 0.f) / zc : 0.f;
+    if (256 * u >= K) continue;
+    const float t = okv[u] ? fmaxf(mv[u], 0.f) * rzc : 0.f;
     if (t > 0.f) {
-      const float ls = valid_row ? (xv[u] - lse) : -logf((float)K);
-      lpart += t * (logf(fmaxf(t, eps)) - ls);
+      const float ls = valid_row ? (xv[u] - lse) : ls_uniform;
+      lpart += t * (__builtin_amdgcn_logf(fmaxf(t, eps)) * kLn2 - ls);
       tpos += t;
     }
   }
-  const float lrow = block_reduce(lpart, red, false);
-  const float T = block_reduce(tpos, red, false);
+#pragma unroll
+  for (int msk = 32; msk >= 1; msk >>= 1) {
+    lpart += __shfl_xor(lpart, msk, 64);
+    tpos += __shfl_xor(tpos, msk, 64);
+  }
+  __syncthreads();  // red is rewritten
+  if (lane == 0) {
+    red[wave] = lpart;
+    red[4 + wave] = tpos;
+  }
+  __syncthreads();
+  const float lrow = (red[0] + red[1]) + (red[2] + red[3]);
+  const float T = (red[4] + red[5]) + (red[6] + red[7]);
   if (tid == 0) loss_rows[row_id] = Z * lrow * loss_scale;
   const float gs = valid_row ? Z * loss_scale * gsc : 0.f;
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
+    if (256 * u >= K) continue;
     const int j = tid + 256 * u;
-    const float t = okv[u] ? fmaxf(mv[u], 0.f) / zc : 0.f;
-    const float sm = okv[u] ? expf(xv[u] - lse) : 0.f;
+    const float t = okv[u] ? fmaxf(mv[u], 0.f) * rzc : 0.f;
+    const float sm = okv[u] ? __builtin_amdgcn_exp2f((xv[u] - lse) * kLog2e) : 0.f;
     if (j < K) iv[j] = gs * (sm * T - t);
   }
 
@@ -253,16 +300,25 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   for (int c = 0; c < kD / 32; ++c) asm volatile("" : "+v"(qa[c]));
 #pragma unroll
   for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(wr[r]));
-  auto s_tile = [&](uint32_t tb, int st) -> f32x4 {  // S tile (16 heads x 16 slots) of slot tile st
-    f32x4 acc = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const int row = 16 * st + col;
-    u32x4 bk[kD / 32];
+  // S tiles (16 heads x 16 slots) of the block's four slot tiles: every operand read is
+  // issued first, then the four accumulation chains run interleaved (the compiler would
+  // otherwise issue each read just before its MFMA and wait for it there)
+  auto s_tiles = [&](uint32_t tb, f32x4 (&sv)[4]) {
+    u32x4 bk[4][kD / 32];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int row = 16 * st + col;
+#pragma unroll
+      for (int c = 0; c < kD / 32; ++c)
+        bk[st][c] = *(const lds_u32x4*)(uintptr_t)(tb + 16 * (row * kRowC + ((4 * c + g) ^ swz_kl(row))));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) sv[st] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < kD / 32; ++c)
-      bk[c] = *(const lds_u32x4*)(uintptr_t)(tb + 16 * (row * kRowC + ((4 * c + g) ^ swz_kl(row))));
 #pragma unroll
-    for (int c = 0; c < kD / 32; ++c) acc = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk[c]), acc);
-    return acc;
+      for (int st = 0; st < 4; ++st) sv[st] = mfma16x16x32(as_bf16x8(qa[c]), as_bf16x8(bk[st][c]), sv[st]);
   };
   f32x4 dqa[kD / 16];
 #pragma unroll
@@ -274,30 +330,22 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const int tr_row = 8 * g + (col >> 2);
   if (gs != 0.f) {  // block-uniform
     // q^T for dk (A of 16x16x32 over heads): tile dt covers d = 16 dt + col, k-step ks
-    // heads 32 ks + 8g .. +7; q [64 heads x 128 d] is staged row-major in kt[1] (swz_kl) and
-    // read transposed (source lane col supplies head row 32 ks + 8g + col/4 (+4 second
-    // read), d columns 16 dt + 4 (col % 4))
-    u32x4 qtr[kD / 16][2];
-    __syncthreads();  // phase 1 is done with kt
+    // heads 32 ks + 8g .. +7; q [64 heads x 128 d] stays staged row-major in qs (swz_kl) for
+    // the whole phase and is read transposed per block (source lane col supplies head row
+    // 32 ks + 8g + col/4 (+4 second read), d columns 16 dt + 4 (col % 4)), which keeps 64
+    // registers free for the S tiles' operand reads
     for (int i = tid; i < kH * kRowC; i += 256) {
       const int h = i >> 4, c = i & 15;
-      kt[1][h * kRowC + (c ^ swz_kl(h))] = *reinterpret_cast<const u32x4*>(qi + (row_id * kH + h) * kD + 8 * c);
+      qs[h * kRowC + (c ^ swz_kl(h))] = *reinterpret_cast<const u32x4*>(qi + (row_id * kH + h) * kD + 8 * c);
     }
-    __syncthreads();
-    {
-      const lds_char* qb = lds_bytes(&kt[1][0]);
-#pragma unroll
-      for (int dt = 0; dt < kD / 16; ++dt)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const int r1 = 32 * ks + tr_row, r2 = r1 + 4;
-          const int c0 = 2 * dt + ((col & 3) >> 1);
-          qtr[dt][ks] = lds_read_tr_pair(qb + 16 * (r1 * kRowC + (c0 ^ swz_kl(r1))) + 8 * (col & 1),
-                                         qb + 16 * (r2 * kRowC + (c0 ^ swz_kl(r2))) + 8 * (col & 1));
-        }
-    }
-    __syncthreads();  // kt[1] is a gather target again
-    start_pass();
+    const lds_char* qsb = lds_bytes(&qs[0]);
+    auto read_qtr = [&](int dt, int ks) {
+      const int r1 = 32 * ks + tr_row, r2 = r1 + 4;
+      const int c0 = 2 * dt + ((col & 3) >> 1);
+      return lds_read_tr_pair(qsb + 16 * (r1 * kRowC + (c0 ^ swz_kl(r1))) + 8 * (col & 1),
+                              qsb + 16 * (r2 * kRowC + (c0 ^ swz_kl(r2))) + 8 * (col & 1));
+    };
+    start_pass();  // (its barrier also publishes qs)
     for (int blk = 0; blk < nblocks; ++blk) {
       const int buf = blk & 1;
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -305,9 +353,13 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       if (blk + 1 < nblocks) gather(blk + 1, buf ^ 1);
       if (blk + 2 < nblocks) load_idx(blk + 2);
       const uint32_t tb = kt_base + buf * (kTileC * 16);
-      f32x4 sv[4];
+      // g_j of the lane's four slots, read before the S tiles so that the reads overlap the
+      // MFMAs (unconditional reads inside iv, slots past K select 0 afterwards)
+      float gjv[4];
 #pragma unroll
-      for (int st = 0; st < 4; ++st) sv[st] = s_tile(tb, st);
+      for (int st = 0; st < 4; ++st) gjv[st] = iv[blk * kB + 16 * st + col];  // (iv spans whole blocks)
+      f32x4 sv[4];
+      s_tiles(tb, sv);
       // E = g_j w_h [S > 0] in bf16: es[slot][head] takes the lane's four heads as one 8-byte
       // store; for eh[head][slot] the lanes of adjacent slots (col, col ^ 1) swap two values
       // so that each writes two whole dwords (slot pair, one head each)
@@ -316,7 +368,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       for (int st = 0; st < 4; ++st) {
         const int sl = 16 * st + col;
         const int slot = blk * kB + sl;
-        const float gj = slot < K ? iv[slot] : 0.f;
+        const float gj = slot < K ? gjv[st] : 0.f;
         float e[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -335,18 +387,22 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       }
       __syncthreads();
       // dq^T[16 d x 16 heads] += k^T[16 d x 32 slots] E^T[32 slots x 16 heads], two k-steps
+      // (per k-step all eight operand reads first, then the eight MFMAs)
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const u32x4 eb = *reinterpret_cast<const u32x4*>(&eh[head_a][32 * ks + 8 * g]);
         const int r1 = 32 * ks + tr_row, r2 = r1 + 4;
+        u32x4 av[kD / 16];
 #pragma unroll
         for (int dt = 0; dt < kD / 16; ++dt) {
           const int c0 = 2 * dt + ((col & 3) >> 1);
           const uint32_t a1 = tb + 16 * (r1 * kRowC + (c0 ^ swz_kl(r1))) + 8 * (col & 1);
           const uint32_t a2 = tb + 16 * (r2 * kRowC + (c0 ^ swz_kl(r2))) + 8 * (col & 1);
-          const u32x4 av = lds_read_tr_pair((const lds_char*)(uintptr_t)a1, (const lds_char*)(uintptr_t)a2);
-          dqa[dt] = mfma16x16x32(as_bf16x8(av), as_bf16x8(eb), dqa[dt]);
+          av[dt] = lds_read_tr_pair((const lds_char*)(uintptr_t)a1, (const lds_char*)(uintptr_t)a2);
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int dt = 0; dt < kD / 16; ++dt) dqa[dt] = mfma16x16x32(as_bf16x8(av[dt]), as_bf16x8(eb), dqa[dt]);
       }
       // dk^T[128 d x 16 slots of this wave] = q^T[d x 64 heads] . E[64 heads x slots 16w ..];
       // the wave's rows of es / eh are read by this wave only, so once its MFMA operands are
@@ -364,13 +420,18 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
         typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
+          u32x4 qt[kD / 32][2];  // the half's q^T operands, read before its MFMAs
+#pragma unroll
+          for (int d4 = 0; d4 < kD / 32; ++d4)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) qt[d4][ks] = read_qtr(4 * half + d4, ks);
+          __builtin_amdgcn_sched_barrier(0);
           f32x4 c4[kD / 32];
 #pragma unroll
           for (int d4 = 0; d4 < kD / 32; ++d4) {
-            const int dt = 4 * half + d4;
             c4[d4] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) c4[d4] = mfma16x16x32(as_bf16x8(qtr[dt][ks]), as_bf16x8(eo[ks]), c4[d4]);
+            for (int ks = 0; ks < 2; ++ks) c4[d4] = mfma16x16x32(as_bf16x8(qt[d4][ks]), as_bf16x8(eo[ks]), c4[d4]);
           }
 #pragma unroll
           for (int d4 = 0; d4 < kD / 32; ++d4) {
@@ -575,7 +636,9 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
     dim3 grid((unsigned)rows_c, (unsigned)batch);
     {
       const TimedLaunch tl("indexer_kl_mfma_kernel", st);
-      indexer_kl_mfma_kernel<<<grid, 256, 0, st>>>((const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass,
+      // iv: one float per slot of whole 64-slot blocks (dynamic LDS)
+      const size_t iv_bytes = (size_t)((topk + kB - 1) / kB * kB) * sizeof(float);
+      indexer_kl_mfma_kernel<<<grid, 256, iv_bytes, st>>>((const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass,
                                                    dq_idx, dw, loss_rows, ck, (int)s_q, (int)s_k, (int)topk, q_offset,
                                                    loss_scale, eps, grad_scale, grad_scale_dev, (int)r0);
     }
