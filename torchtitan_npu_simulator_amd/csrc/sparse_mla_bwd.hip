@@ -740,6 +740,9 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) bg[(ks + 1) & 1][h2] = lds_read16(gl[h2] + 16 * ((4 * (ks + 1) + g) ^ sw[h2]));
         }
+        // (the next k-step's reads stay ahead of this step's MFMAs; left to itself the
+        // compiler issues each read just before its MFMA and waits for it there)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int h2 = 0; h2 < 2; ++h2)
 #pragma unroll
