@@ -26,8 +26,9 @@
  *   dsa_quantize_fp8_rows        the fp8-e4m3 per-row quantisation this build adds in front of
  *                                npu_lightning_indexer (the reference indexes in bf16 and marks fp8
  *                                as a QAT step: models/deepseek_v4/model.py:646, :822)
- *   dsa_attn_sink_fold +
- *   dsa_attn_sink_grad           the per-head sink of SparseAttention.forward (models/deepseek_v4/
+ *   dsa_sparse_mla_{fwd,bwd}_sink
+ *   (and dsa_attn_sink_fold +
+ *   dsa_attn_sink_grad)          the per-head sink of SparseAttention.forward (models/deepseek_v4/
  *                                model.py:573-623) inside npu_sparse_attn_shared_kv{,_grad}
  *                                (converters/kernels/npu_smla.py:351-400;
  *                                 ops/aclnn/sparse_attn_sharedkv/binding.cpp:30-88)
@@ -217,6 +218,29 @@ int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, co
                        void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q,
                        int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
                        int64_t q_offset, void* stream);
+
+/*
+ * dsa_sparse_mla_fwd / dsa_sparse_mla_bwd with the DeepSeek-V4 per-head attention sink folded
+ * in (reference: SparseAttention.forward's attn_sink, models/deepseek_v4/model.py:573-623,
+ * passed as `sinks` to npu_sparse_attn_shared_kv{,_grad}, converters/kernels/npu_smla.py:351-400).
+ * The forward's epilogue does what dsa_attn_sink_fold does after the plain forward: out is
+ * normalised by s2 = l e^(m - m2) + e^(sink - m2), m2 = max(m, sink[h]), and (m2, s2) are written
+ * as the statistics (a row with no valid slot gets out = 0, (sink[h], 1)).  The backward takes
+ * those statistics and also adds to dsink_accum[h] (fp32, caller zeroes it) the sink's gradient
+ * - sum over rows of e^(sink - m2) / s2 * sum_d dout * out, from the delta pass it already makes.
+ *   sinks [H] fp32 (required; NULL is an error)
+ * Same shapes, dtypes, workspace and limits as the entry points without the sink.
+ */
+int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* indices, const float* sinks, void* out,
+                            float* softmax_max, float* softmax_sum, int dtype, int64_t batch, int64_t s_q,
+                            int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
+                            int64_t q_offset, void* stream);
+int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* indices, const void* out,
+                            const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
+                            float* dkv_accum, float* mass, const float* sinks, float* dsink_accum, void* workspace,
+                            int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
+                            int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale, int64_t q_offset,
+                            void* stream);
 
 /*
  * Head-summed attention probability at each selected slot (reference: get_attn_scores,

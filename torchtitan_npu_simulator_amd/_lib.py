@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -53,6 +53,15 @@ _SIGNATURES = {
     "dsa_sparse_mla_bwd": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
          _f32, _i64, _vp],
+        _i32,
+    ),
+    "dsa_sparse_mla_fwd_sink": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _vp],
+        _i32,
+    ),
+    "dsa_sparse_mla_bwd_sink": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i64, _i64, _i64, _i64, _i64,
+         _i64, _i64, _f32, _i64, _vp],
         _i32,
     ),
     "dsa_attn_mass": (

@@ -793,7 +793,8 @@ __global__ void __launch_bounds__(256)
 bwd_exact_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, const int32_t* __restrict__ idx,
                      const float* __restrict__ out, const float* __restrict__ dout, const float* __restrict__ smax,
                      const float* __restrict__ ssum, float* __restrict__ dq, float* __restrict__ dkv, int S,
-                     int s_kv, int H, int K, int dqk, int dv, float scale, int64_t q_offset) {
+                     int s_kv, int H, int K, int dqk, int dv, float scale, int64_t q_offset,
+                     const float* __restrict__ sinks, float* __restrict__ dsink) {
   extern __shared__ float ds[];  // K
   __shared__ float red[256];
   const int tok = blockIdx.x, head = blockIdx.y, b = blockIdx.z, tid = threadIdx.x;
@@ -815,6 +816,7 @@ bwd_exact_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, 
   const float delta = red[0];
   const float sm = ssum[hr];
   const float lse = sm > 0.f ? smax[hr] + logf(sm) : INFINITY;
+  if (sinks && tid == 0) atomicAdd(&dsink[head], -expf(sinks[head] - lse) * delta);  // (one per token and head)
   __syncthreads();
   for (int j = tid; j < K; j += 256) {
     const int v = ridx[j];
@@ -846,10 +848,13 @@ bwd_exact_f32_kernel(const float* __restrict__ q, const float* __restrict__ kv, 
 }
 
 // delta[b][lr][h] = sum_d dO[row, h, d] * O[row, h, d] (fp32) for the chunk's rows: one
-// 16-lane group per (row, head), 32 columns per lane (four 16-byte loads of each tensor)
+// 16-lane group per (row, head), 32 columns per lane (four 16-byte loads of each tensor).
+// With a per-head sink it also writes pd[b][lr][h] = -p_sink delta, p_sink = e^(sink - m2) /
+// s2 from the row statistics (which include the sink): the sink's gradient summed over rows.
 __global__ void __launch_bounds__(256)
 bwd_delta_kernel(const uint16_t* __restrict__ out, const uint16_t* __restrict__ dout, float* __restrict__ delta,
-                 int64_t n, int S, int H, int row0, int rows) {
+                 int64_t n, int S, int H, int row0, int rows, const float* __restrict__ sinks,
+                 const float* __restrict__ smax, const float* __restrict__ ssum, float* __restrict__ pd) {
   const int64_t grp = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;  // (b, lr, h) flattened, n of them
   const int l = threadIdx.x & 15;
   const int64_t g = grp < n ? grp : n - 1;
@@ -871,12 +876,34 @@ bwd_delta_kernel(const uint16_t* __restrict__ out, const uint16_t* __restrict__ 
       part += bf16_lo(dv[c][r]) * bf16_lo(ov[c][r]) + bf16_hi(dv[c][r]) * bf16_hi(ov[c][r]);
 #pragma unroll
   for (int m = 8; m >= 1; m >>= 1) part += __shfl_xor(part, m, 64);
-  if (l == 0 && grp < n) delta[g] = part;
+  if (l == 0 && grp < n) {
+    delta[g] = part;
+    if (sinks) {
+      const float ps = expf(sinks[rem % H] - smax[hr]) / ssum[hr];
+      pd[g] = -ps * part;
+    }
+  }
+}
+
+// dsink[h] += sum over the chunk's rows of pd[row][h]: one workgroup per head
+__global__ void __launch_bounds__(256)
+sink_colsum_kernel(const float* __restrict__ pd, int64_t nrows, int H, float* __restrict__ dsink) {
+  __shared__ float red[256];
+  const int h = blockIdx.x, t = threadIdx.x;
+  float acc = 0.f;
+  for (int64_t r = t; r < nrows; r += 256) acc += pd[r * H + h];
+  red[t] = acc;
+  __syncthreads();
+  for (int st = 128; st > 0; st >>= 1) {
+    if (t < st) red[t] += red[t + st];
+    __syncthreads();
+  }
+  if (t == 0) dsink[h] += red[0];
 }
 
 struct BwdPlan {
   int64_t rows;  // query rows per chunk
-  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, delta_bytes, total;
+  int64_t g_bytes, c_bytes, pairs_bytes, csr_bytes, delta_bytes, total;  // (delta twice: delta and the sink part)
 };
 
 // Scratch per chunk: G and C (bf16, C rows `width` columns), the CSR pair list and
@@ -884,7 +911,7 @@ struct BwdPlan {
 BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget, int64_t width) {
   BwdPlan p{};
   const int64_t per_row = batch * g_slots(topk) * kGW * 2 + batch * topk * (int64_t)(width * 2 + 4) +
-                          batch * kHeadsMax * 4;
+                          2 * batch * kHeadsMax * 4;
   int64_t rows = s_q;
   if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
   p.rows = rows;
@@ -894,7 +921,7 @@ BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t
   p.csr_bytes = csr_ws_bytes(s_kv, rows, topk);
   p.delta_bytes = batch * rows * kHeadsMax * 4;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
-  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + al(p.delta_bytes);
+  p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + 2 * al(p.delta_bytes);
   return p;
 }
 
@@ -911,13 +938,13 @@ extern "C" int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q,
   return dsa::plan_bwd(batch, s_q, s_kv, topk, dsa::kDefaultBudget, width).total;
 }
 
-extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out,
-                                  const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
-                                  float* dkv_accum, float* mass, void* workspace, int64_t workspace_bytes, int dtype,
-                                  int64_t batch,
-                                  int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
-                                  int64_t topk, float scale, int64_t q_offset, void* stream) {
-  using namespace dsa;
+namespace dsa {
+static int sparse_mla_bwd_impl(const void* q, const void* kv, const int32_t* indices, const void* out,
+                               const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
+                               float* dkv_accum, float* mass, void* workspace, int64_t workspace_bytes, int dtype,
+                               int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
+                               int64_t topk, float scale, int64_t q_offset, const float* sinks, float* dsink,
+                               void* stream) {
   if (!q || !kv || !indices || !out || !dout || !softmax_max || !softmax_sum || !dq || !dkv_accum)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: null pointer");
   if (batch <= 0 || s_q <= 0 || s_kv <= 0 || n_heads <= 0 || topk <= 0 || d_v <= 0 || d_qk < d_v)
@@ -936,7 +963,8 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
       const TimedLaunch tl("bwd_exact_f32_kernel", st);
       bwd_exact_f32_kernel<<<grid, 256, topk * 4, st>>>(
           (const float*)q, (const float*)kv, indices, (const float*)out, (const float*)dout, softmax_max, softmax_sum,
-          (float*)dq, dkv_accum, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset);
+          (float*)dq, dkv_accum, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset,
+          sinks, dsink);
     }
     return check_launch("dsa_sparse_mla_bwd(f32)");
   }
@@ -961,6 +989,7 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
   int* pairs = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes));
   int* counts = (int*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes));
   float* dbuf = (float*)(ws + al(plan.g_bytes) + al(plan.c_bytes) + al(plan.pairs_bytes) + al(plan.csr_bytes));
+  float* pdbuf = (float*)((char*)dbuf + al(plan.delta_bytes));  // the sink's per-(row, head) gradient parts
   const unsigned hgroups = ceil_div(n_heads, kHG);
 
   for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
@@ -969,8 +998,14 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
       const int64_t groups = batch * rows * n_heads;
       const TimedLaunch tl("bwd_delta_kernel", st);
       bwd_delta_kernel<<<(unsigned)((groups * 16 + 255) / 256), 256, 0, st>>>(
-          (const uint16_t*)out, (const uint16_t*)dout, dbuf, groups, (int)s_q, (int)n_heads, (int)r0, rows);
+          (const uint16_t*)out, (const uint16_t*)dout, dbuf, groups, (int)s_q, (int)n_heads, (int)r0, rows, sinks,
+          softmax_max, softmax_sum, pdbuf);
       if (int rc = check_launch("dsa_sparse_mla_bwd(delta)")) return rc;
+    }
+    if (sinks) {
+      const TimedLaunch tl("sink_colsum_kernel", st);
+      sink_colsum_kernel<<<(unsigned)n_heads, 256, 0, st>>>(pdbuf, batch * rows, (int)n_heads, dsink);
+      if (int rc = check_launch("dsa_sparse_mla_bwd(sink)")) return rc;
     }
     dim3 ga((unsigned)rows, 1, (unsigned)batch);
     {
@@ -1006,3 +1041,28 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
   }
   return DSA_OK;
 }
+}  // namespace dsa
+
+extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out,
+                                  const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
+                                  float* dkv_accum, float* mass, void* workspace, int64_t workspace_bytes, int dtype,
+                                  int64_t batch,
+                                  int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
+                                  int64_t topk, float scale, int64_t q_offset, void* stream) {
+  return dsa::sparse_mla_bwd_impl(q, kv, indices, out, dout, softmax_max, softmax_sum, dq, dkv_accum, mass, workspace,
+                                  workspace_bytes, dtype, batch, s_q, s_kv, n_heads, d_qk, d_v, topk, scale, q_offset,
+                                  nullptr, nullptr, stream);
+}
+
+extern "C" int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* indices, const void* out,
+                                       const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
+                                       float* dkv_accum, float* mass, const float* sinks, float* dsink_accum,
+                                       void* workspace, int64_t workspace_bytes, int dtype, int64_t batch,
+                                       int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
+                                       int64_t topk, float scale, int64_t q_offset, void* stream) {
+  if (!sinks || !dsink_accum) return dsa::set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd_sink: null sinks / dsink");
+  return dsa::sparse_mla_bwd_impl(q, kv, indices, out, dout, softmax_max, softmax_sum, dq, dkv_accum, mass, workspace,
+                                  workspace_bytes, dtype, batch, s_q, s_kv, n_heads, d_qk, d_v, topk, scale, q_offset,
+                                  sinks, dsink_accum, stream);
+}
+

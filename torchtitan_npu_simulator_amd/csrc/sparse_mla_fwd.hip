@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(kFwdThreads, 1)
 sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv,
                            const int32_t* __restrict__ idx, uint16_t* __restrict__ out, float* __restrict__ smax,
                            float* __restrict__ ssum, int S, int s_kv, int H, int K, float scale_log2,
-                           int64_t q_offset) {
+                           int64_t q_offset, const float* __restrict__ sinks) {
   using Gather = RowGather<kFwdWaves, kD>;
   using Geo = GatherGeomT<kD>;
   constexpr int kPer = Gather::kMaxPerWave;
@@ -105,9 +105,9 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
     if (hok) {
       uint32_t* o32 = reinterpret_cast<uint32_t*>(out + orow * kDv);
       for (int i = h; i < kDv / 2; i += 2) o32[i] = 0u;
-      if (h == 0) {
-        smax[orow] = -INFINITY;
-        ssum[orow] = 0.f;
+      if (h == 0) {  // (with a sink the row's only logit is the sink's)
+        smax[orow] = sinks ? sinks[head] : -INFINITY;
+        ssum[orow] = sinks ? 1.f : 0.f;
       }
     }
     return;
@@ -334,7 +334,13 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
   // ---- epilogue: lane holds dv = 32 dt + 8 j + 4 h + i of its head ----
   const float ls = xor32_sum(lsum);
   if (!hok) return;
-  const float inv = ls > 0.f ? 1.f / ls : 0.f;
+  // a per-head sink (a logit with no value, natural-log units of the scaled score) joins
+  // the row's denominator: O = acc / (ls + 2^(sink2 - m_ref)), and the row statistics
+  // become (m2, s2) = (max(m, sink), sum e^(x - m2) + e^(sink - m2)); with no valid key
+  // (m_ref = -inf) the sink term is +inf and O stays 0
+  const float sk2 = sinks ? sinks[head] * kLog2e : -INFINITY;
+  const float den = sinks ? ls + exp2f(sk2 - m_ref) : ls;
+  const float inv = den > 0.f ? 1.f / den : 0.f;
   uint2* orp = reinterpret_cast<uint2*>(out + orow * kDv);
 #pragma unroll
   for (int dt = 0; dt < kDv / 32; ++dt)
@@ -346,9 +352,15 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
       orp[(32 * dt + 8 * j + 4 * h) / 4] = w;
     }
   if (h == 0) {
-    smax[orow] = m_true * kLn2;
+    const float l_true = ls > 0.f ? ls * exp2f(m_ref - m_true) : 0.f;  // sum at the true max
+    float m_out = m_true, l_out = l_true;
+    if (sinks) {
+      m_out = fmaxf(m_true, sk2);
+      l_out = (l_true > 0.f ? l_true * exp2f(m_true - m_out) : 0.f) + exp2f(sk2 - m_out);
+    }
+    smax[orow] = m_out * kLn2;
     // a negative sum marks a row whose logits outgrew the headroom; the fixup pass redoes it
-    ssum[orow] = clamped ? -1.f : ls * exp2f(m_ref - m_true);
+    ssum[orow] = clamped ? -1.f : l_out;
   }
 }
 
@@ -540,7 +552,8 @@ template <typename T>
 __global__ void __launch_bounds__(256)
 sparse_mla_fwd_exact_kernel(const T* __restrict__ q, const T* __restrict__ kv, const int32_t* __restrict__ idx,
                             T* __restrict__ out, float* __restrict__ smax, float* __restrict__ ssum, int S,
-                            int s_kv, int H, int K, int dqk, int dv, float scale, int64_t q_offset, int fixup) {
+                            int s_kv, int H, int K, int dqk, int dv, float scale, int64_t q_offset, int fixup,
+                            const float* __restrict__ sinks) {
   extern __shared__ float sc[];
   __shared__ float red[256];
   const int tok = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
@@ -592,7 +605,16 @@ sparse_mla_fwd_exact_kernel(const T* __restrict__ q, const T* __restrict__ kv, c
       __syncthreads();
     }
     const float l = red[0];
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    // per-head sink: O scaled by a / s2 with a = l e^(m - m2), s2 = a + e^(sink - m2)
+    float m_out = m, l_out = l, fold = 1.f;
+    if (sinks) {
+      const float sk = sinks[head];
+      m_out = fmaxf(m, sk);
+      const float a = l > 0.f ? l * expf(m - m_out) : 0.f;
+      l_out = a + expf(sk - m_out);
+      fold = a / l_out;
+    }
+    const float inv = l > 0.f ? fold / l : 0.f;
     T* orow = out + hr * dv;
     for (int d = tid; d < dv; d += 256) {
       float acc = 0.f;
@@ -604,8 +626,8 @@ sparse_mla_fwd_exact_kernel(const T* __restrict__ q, const T* __restrict__ kv, c
     }
     __syncthreads();  // sc / red reused by the next head
     if (tid == 0) {
-      smax[hr] = m;
-      ssum[hr] = l;
+      smax[hr] = m_out;
+      ssum[hr] = l_out;
     }
   }
 }
@@ -679,11 +701,11 @@ extern "C" int dsa_attn_mass(const void* q, const void* kv, const int32_t* indic
   return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: dtype %d", dtype);
 }
 
-extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, void* out, float* softmax_max,
-                                  float* softmax_sum, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
-                                  int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
-                                  int64_t q_offset, void* stream) {
-  using namespace dsa;
+namespace dsa {
+static int sparse_mla_fwd_impl(const void* q, const void* kv, const int32_t* indices, const float* sinks, void* out,
+                               float* softmax_max, float* softmax_sum, int dtype, int64_t batch, int64_t s_q,
+                               int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
+                               int64_t q_offset, void* stream) {
   if (!q || !kv || !indices || !out || !softmax_max || !softmax_sum)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_fwd: null pointer");
   if (batch <= 0 || s_q <= 0 || s_kv <= 0 || n_heads <= 0 || topk <= 0 || d_v <= 0 || d_qk < d_v)
@@ -708,18 +730,18 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
       if (rope)
         sparse_mla_fwd_bf16_kernel<kDqk><<<grid, kFwdThreads, 0, st>>>(
             (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
-            (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
+            (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset, sinks);
       else
         sparse_mla_fwd_bf16_kernel<kDv><<<grid, kFwdThreads, 0, st>>>(
             (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
-            (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
+            (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset, sinks);
     }
     if (int rc = check_launch("dsa_sparse_mla_fwd(bf16)")) return rc;
     dim3 fgrid((unsigned)s_q, 1, (unsigned)batch);
     const TimedLaunch tl("sparse_mla_fwd_exact_kernel<fixup>", st);
     sparse_mla_fwd_exact_kernel<uint16_t><<<fgrid, 256, sc_bytes, st>>>(
         (const uint16_t*)q, (const uint16_t*)kv, indices, (uint16_t*)out, softmax_max, softmax_sum, (int)s_q,
-        (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset, 1);
+        (int)s_kv, (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset, 1, sinks);
     return check_launch("dsa_sparse_mla_fwd(bf16 fixup)");
   }
   if (dtype == DSA_F32) {
@@ -727,8 +749,26 @@ extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* 
     const TimedLaunch tl("sparse_mla_fwd_exact_kernel<float>", st);
     sparse_mla_fwd_exact_kernel<float><<<grid, 256, sc_bytes, st>>>(
         (const float*)q, (const float*)kv, indices, (float*)out, softmax_max, softmax_sum, (int)s_q, (int)s_kv,
-        (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset, 0);
+        (int)n_heads, (int)topk, (int)d_qk, (int)d_v, scale, q_offset, 0, sinks);
     return check_launch("dsa_sparse_mla_fwd(f32)");
   }
   return set_error(DSA_ERR_UNSUPPORTED, "dsa_sparse_mla_fwd: dtype %d not supported", dtype);
+}
+}  // namespace dsa
+
+extern "C" int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, void* out, float* softmax_max,
+                                  float* softmax_sum, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
+                                  int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
+                                  int64_t q_offset, void* stream) {
+  return dsa::sparse_mla_fwd_impl(q, kv, indices, nullptr, out, softmax_max, softmax_sum, dtype, batch, s_q, s_kv,
+                                  n_heads, d_qk, d_v, topk, scale, q_offset, stream);
+}
+
+extern "C" int dsa_sparse_mla_fwd_sink(const void* q, const void* kv, const int32_t* indices, const float* sinks,
+                                       void* out, float* softmax_max, float* softmax_sum, int dtype, int64_t batch,
+                                       int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
+                                       int64_t topk, float scale, int64_t q_offset, void* stream) {
+  if (!sinks) return dsa::set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_fwd_sink: null sinks");
+  return dsa::sparse_mla_fwd_impl(q, kv, indices, sinks, out, softmax_max, softmax_sum, dtype, batch, s_q, s_kv,
+                                  n_heads, d_qk, d_v, topk, scale, q_offset, stream);
 }

@@ -370,10 +370,12 @@ def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sp
 # ---------------------------------------------------------------------------
 # gathered sparse MLA attention
 # ---------------------------------------------------------------------------
-def sparse_mla_fwd(q, kv, indices, scale, *, d_v=512, q_offset=0):
+def sparse_mla_fwd(q, kv, indices, scale, *, d_v=512, q_offset=0, sinks=None):
     """(out [B,S,H,d_v], softmax_max [B,S,H], softmax_sum [B,S,H]) from dsa_sparse_mla_fwd.
 
     q [B,S,H,D_qk] bf16/fp32, kv [B,S_kv,D_qk] (v = kv[..., :d_v]), indices [B,S,K] int32.
+    ``sinks`` [H] (DeepSeek-V4's per-head attention sink) selects dsa_sparse_mla_fwd_sink: the
+    sink joins every row's softmax with no value, and the statistics returned include it.
     """
     lib = load_library()
     require_gpu_tensor(q, "q")
@@ -386,6 +388,15 @@ def sparse_mla_fwd(q, kv, indices, scale, *, d_v=512, q_offset=0):
     out = torch.empty(B, S, H, d_v, dtype=q.dtype, device=q.device)
     smax = torch.empty(B, S, H, dtype=torch.float32, device=q.device)
     ssum = torch.empty(B, S, H, dtype=torch.float32, device=q.device)
+    if sinks is not None:
+        sk = _sink_vector(sinks, H, q.device)
+        check(
+            lib.dsa_sparse_mla_fwd_sink(ptr(q), ptr(kv), ptr(indices), ptr(sk), ptr(out), ptr(smax), ptr(ssum),
+                                        _lib.dtype_code(q.dtype), B, S, s_kv, H, D, d_v, K, float(scale),
+                                        int(q_offset), stream_of(q.device)),
+            "dsa_sparse_mla_fwd_sink",
+        )
+        return out, smax, ssum
     check(
         lib.dsa_sparse_mla_fwd(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(smax), ptr(ssum), _lib.dtype_code(q.dtype),
                                B, S, s_kv, H, D, d_v, K, float(scale), int(q_offset), stream_of(q.device)),
@@ -394,11 +405,20 @@ def sparse_mla_fwd(q, kv, indices, scale, *, d_v=512, q_offset=0):
     return out, smax, ssum
 
 
+def _sink_vector(sinks, H, device):
+    sk = sinks.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if sk.numel() != H:
+        raise ValueError(f"sinks has {sk.numel()} entries, the call has {H} heads")
+    return sk
+
+
 def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, workspace_bytes=None,
-                   return_mass=False):
+                   return_mass=False, sinks=None):
     """(dq like q, dkv fp32 [B,S_kv,D_qk]) from dsa_sparse_mla_bwd, plus the head-summed
     attention mass [B,S,K] fp32 when ``return_mass`` (bf16 path; the same quantity as
-    ``attn_mass``, taken from the probabilities the backward recomputes anyway).
+    ``attn_mass``, taken from the probabilities the backward recomputes anyway), plus
+    d sinks [H] fp32 last when ``sinks`` is given (dsa_sparse_mla_bwd_sink; smax / ssum must
+    then be the statistics sparse_mla_fwd returned with the same sinks).
 
     ``workspace_bytes`` caps the scratch (fewer bytes -> more query-row chunks).
     """
@@ -416,13 +436,25 @@ def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, 
     if workspace_bytes is not None:
         ws_bytes = int(workspace_bytes)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    res = (dq, dkv, mass) if return_mass else (dq, dkv)
+    if sinks is not None:
+        sk = _sink_vector(sinks, H, q.device)
+        dsink = torch.zeros(H, dtype=torch.float32, device=q.device)
+        check(
+            lib.dsa_sparse_mla_bwd_sink(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax), ptr(ssum),
+                                        ptr(dq), ptr(dkv), ptr(mass), ptr(sk), ptr(dsink), ptr(ws), ws_bytes,
+                                        _lib.dtype_code(q.dtype), B, S, s_kv, H, D, d_v, K, float(scale),
+                                        int(q_offset), stream_of(q.device)),
+            "dsa_sparse_mla_bwd_sink",
+        )
+        return res + (dsink,)
     check(
         lib.dsa_sparse_mla_bwd(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax), ptr(ssum), ptr(dq),
                                ptr(dkv), ptr(mass), ptr(ws), ws_bytes, _lib.dtype_code(q.dtype), B, S, s_kv, H, D, d_v,
                                K, float(scale), int(q_offset), stream_of(q.device)),
         "dsa_sparse_mla_bwd",
     )
-    return (dq, dkv, mass) if return_mass else (dq, dkv)
+    return res
 
 
 def attn_mass(q, kv, indices, smax, ssum, scale, *, q_offset=0):
@@ -684,17 +716,6 @@ def _pad_rows(x: torch.Tensor, width: int) -> torch.Tensor:
     return torch.cat([x, pad], dim=-1).contiguous()
 
 
-def _sink_fold(smax, ssum, sinks):
-    """Fold a per-head sink logit into the row statistics: returns (m2, s2, factor) with
-    m2 = max(smax, sink), s2 = ssum e^(smax-m2) + e^(sink-m2) and factor = the share of
-    the probability mass on the keys (the output scale)."""
-    sk = sinks.float().view(*([1] * (smax.dim() - 1)), -1)
-    m2 = torch.maximum(smax, sk)
-    a = torch.where(ssum > 0, ssum * torch.exp(smax - m2), torch.zeros_like(ssum))
-    s2 = a + torch.exp(sk - m2)
-    return m2, s2, a / s2
-
-
 def attn_sink_fold_(out, smax, ssum, sinks):
     """In place (dsa_attn_sink_fold): out [.., H, d_v] *= a / s2 and (smax, ssum) <- (m2, s2)
     with m2 = max(smax, sink), a = ssum e^(smax - m2), s2 = a + e^(sink - m2)."""
@@ -822,11 +843,8 @@ def _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, cmp_ratio, ori_
 
 def _sharedkv_forward(prep, sinks, scale):
     """(out [B,S,H,dv] with the sink folded in, m2, s2): the row statistics include the sink."""
-    out, smax, ssum = sparse_mla_fwd(prep["q"], prep["kv"], prep["idx"], scale, d_v=prep["dv"],
-                                     q_offset=_NO_MASK_OFFSET)
-    if sinks is not None:
-        out, smax, ssum = attn_sink_fold_(out, smax, ssum, sinks)
-    return out, smax, ssum
+    return sparse_mla_fwd(prep["q"], prep["kv"], prep["idx"], scale, d_v=prep["dv"], q_offset=_NO_MASK_OFFSET,
+                          sinks=sinks)
 
 
 def _sharedkv_backward(prep, out, dout, m2, s2, sinks, scale):
@@ -834,10 +852,12 @@ def _sharedkv_backward(prep, out, dout, m2, s2, sinks, scale):
     D, dv = prep["D"], prep["dv"]
     dout = _pad_rows(dout.to(out.dtype), dv) if dv != D else dout.contiguous().to(out.dtype)
     # P_j = exp(x_j - lse) with lse = m2 + log s2 includes the sink, and the kernel's
-    # delta = rowsum(dO * O) uses the sink-scaled O: dQ and dKV are exact
-    dq, dkv = sparse_mla_bwd(prep["q"], prep["kv"], prep["idx"], out, dout, m2, s2, scale, q_offset=_NO_MASK_OFFSET)
-    # the sink has no value: d sink = -sum over rows of p_sink * rowsum(dO o O)
-    dsink = attn_sink_grad(out, dout, m2, s2, sinks) if sinks is not None else None
+    # delta = rowsum(dO * O) uses the sink-scaled O: dQ and dKV are exact.  The sink has no
+    # value: d sink = -sum over rows of p_sink * rowsum(dO o O), from the same delta pass.
+    res = sparse_mla_bwd(prep["q"], prep["kv"], prep["idx"], out, dout, m2, s2, scale, q_offset=_NO_MASK_OFFSET,
+                         sinks=sinks)
+    dq, dkv = res[0], res[1]
+    dsink = res[2] if sinks is not None else None
     dkv = dkv[..., :D]
     s_ori = prep["s_ori"]
     return dq[..., :D], dkv[:, :s_ori], (dkv[:, s_ori:] if prep["has_cmp"] else None), dsink
@@ -1079,8 +1099,8 @@ def v4_indexer_kl_grad(q, kv, kv_compress, attn_sink, q_indexer, k_indexer, weig
     dqk, dv = (576, 512) if bf16 else (D, D)
     q_ext = _pad_rows(q.detach(), dqk)
     kv_ext = _pad_rows(torch.cat([kv.detach(), kv_compress.detach()], dim=1), dqk)
-    _, smax, ssum = sparse_mla_fwd(q_ext, kv_ext, idx, softmax_scale, d_v=dv, q_offset=_NO_MASK_OFFSET)
-    m2, s2, _ = _sink_fold(smax, ssum, attn_sink.detach())
+    _, m2, s2 = sparse_mla_fwd(q_ext, kv_ext, idx, softmax_scale, d_v=dv, q_offset=_NO_MASK_OFFSET,
+                               sinks=attn_sink.detach())
     mass = attn_mass(q_ext, kv_ext, idx, m2, s2, softmax_scale, q_offset=_NO_MASK_OFFSET)
     dist = (mass[..., W:] / H).contiguous()
     return indexer_kl_grad_from_mass(q_indexer, k_indexer, weights, local, dist, q_offset=_NO_MASK_OFFSET,
