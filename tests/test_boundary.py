@@ -67,7 +67,9 @@ def test_sharedkv_metadata_record_and_check():
 def test_sharedkv_rejects_what_it_does_not_support():
     q = torch.randn(1, 8, 2, 16)
     kv = torch.randn(1, 8, 1, 16)
-    with pytest.raises(NotImplementedError, match="BSND"):
+    with pytest.raises(NotImplementedError, match="layouts"):
+        ops.npu_sparse_attn_sharedkv(q, kv, layout_q="TND", layout_kv="BSND")
+    with pytest.raises(ValueError, match="cu_seqlens_q"):
         ops.npu_sparse_attn_sharedkv(q, kv, layout_q="TND", layout_kv="TND")
     with pytest.raises(NotImplementedError, match="band"):
         ops.npu_sparse_attn_sharedkv(q, kv, ori_sparse_indices=torch.zeros(1, 8, 1, 4, dtype=torch.int32))

@@ -336,8 +336,7 @@ def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sp
     n_seq = len(cu_q) - 1
     res = None
     if cmp_residual_k is not None:
-        res = [int(v) for v in (cmp_residual_k.tolist() if isinstance(cmp_residual_k, torch.Tensor)
-                                else cmp_residual_k)]
+        res = list(_lib.host_ints(cmp_residual_k))  # a device tensor is read back once per version
         if len(res) != n_seq:
             raise ValueError("cmp_residual_k needs one entry per sequence")
     q = query.contiguous()
@@ -709,6 +708,61 @@ def v4_attention_indices(B, S, device, *, win_left=127, win_right=0, cmp_ratio=1
     return idx.to(torch.int32).contiguous()
 
 
+def _cu_device(cu, device) -> torch.Tensor:
+    """int64 device copy of a cu_seqlens-style tensor or list (no host read of a device tensor)."""
+    if isinstance(cu, torch.Tensor):
+        return cu.to(device=device, dtype=torch.int64).reshape(-1)
+    return torch.tensor([int(v) for v in cu], dtype=torch.int64, device=device)
+
+
+def sharedkv_tnd_indices(cu_seqlens_q, cu_seqlens_ori_kv, T, T_ori, device, *, win_left=127, win_right=0,
+                         cmp_ratio=1, cu_seqlens_cmp_kv=None, cmp_residual_kv=None, cmp_indices=None, max_cmp=0,
+                         window=True):
+    """int32 [T, W(+K)] slot indices of a packed ("TND") shared-KV batch over the rows of
+    cat(ori_kv [T_ori], cmp_kv), -1 = empty; built on the device from the cu_seqlens tensors
+    (no host read).
+
+    Query t of sequence i (position p = t - cu_seqlens_q[i]) sees the ori rows of its own
+    sequence at positions [p - win_left, p + win_right] (ori_mask_mode 4; ori and query
+    tokens are the same positions, as in the reference's global TND batch) and, with
+    compressed keys (cmp_ratio > 1, cmp_mask_mode 3), the compressed rows c of its sequence
+    with c < (p + 1 + o_i) // cmp_ratio, o_i = max(0, cmp_ratio * n_i + residual_i - len_i)
+    (n_i compressed rows, residual_i original tokens after the last whole block): for ratio 4
+    the entries of ``cmp_indices`` [T, K] (sequence-local, as the indexer returns them; -1
+    and entries outside that rule stay empty), otherwise every such row, in ``max_cmp``
+    (>= the longest compressed sequence) slots.  The same rules over one sequence are what
+    ``v4_attention_indices`` builds for a BSND batch.  ``window=False`` leaves the window
+    columns out (the compressed rows alone, numbered from ``T_ori``).
+    """
+    cu_q = _cu_device(cu_seqlens_q, device)
+    cu_o = _cu_device(cu_seqlens_ori_kv if cu_seqlens_ori_kv is not None else cu_seqlens_q, device)
+    t = torch.arange(T, device=device)
+    seq = torch.searchsorted(cu_q[1:].contiguous(), t, right=True).clamp_(max=cu_q.numel() - 2)
+    pos = t - cu_q[seq]
+    len_o = (cu_o[seq + 1] - cu_o[seq]).view(T, 1)
+    W = int(win_left) + int(win_right) + 1
+    j = pos.view(T, 1) - int(win_left) + torch.arange(W, device=device).view(1, W)
+    win = torch.where((j >= 0) & (j < len_o), cu_o[seq].view(T, 1) + j, torch.full_like(j, -1))
+    if not window:
+        win = win[:, :0]
+    if cmp_ratio <= 1 or cu_seqlens_cmp_kv is None:
+        return win.to(torch.int32).contiguous()
+    r = int(cmp_ratio)
+    cu_c = _cu_device(cu_seqlens_cmp_kv, device)
+    n_c = cu_c[seq + 1] - cu_c[seq]
+    res = _cu_device(cmp_residual_kv, device)[seq] if cmp_residual_kv is not None else torch.zeros_like(n_c)
+    len_q = cu_q[seq + 1] - cu_q[seq]
+    off = (r * n_c + res - len_q).clamp(min=0)
+    lim = torch.minimum((pos + 1 + off) // r, n_c).view(T, 1)
+    base = (int(T_ori) + cu_c[seq]).view(T, 1)
+    if cmp_indices is not None:
+        c = cmp_indices.reshape(T, -1).to(torch.int64)
+    else:
+        c = torch.arange(int(max_cmp), device=device).view(1, -1).expand(T, -1)
+    cmp = torch.where((c >= 0) & (c < lim), base + c, torch.full_like(c, -1))
+    return torch.cat([win, cmp], dim=1).to(torch.int32).contiguous()
+
+
 def _pad_rows(x: torch.Tensor, width: int) -> torch.Tensor:
     if x.shape[-1] == width:
         return x.contiguous()
@@ -808,7 +862,11 @@ def _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, o
     rec = getattr(metadata, "_dsa_record", None) if metadata is not None else None
     if rec is None:
         return
-    B, S, H, D = query.shape
+    if query.dim() == 3:  # TND: [T, N, D]; the record's batch size counts sequences
+        H, D = query.shape[1:]
+        B = rec[5]
+    else:
+        B, S, H, D = query.shape
     want = dict(num_heads_q=(2, H), head_dim=(4, D), batch_size=(5, B), cmp_ratio=(10, cmp_ratio),
                 ori_win_left=(13, ori_win_left), ori_win_right=(14, ori_win_right), has_cmp_kv=(18, int(cmp_kv is not None)))
     for name, (i, v) in want.items():
@@ -816,20 +874,41 @@ def _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, o
             raise ValueError(f"metadata was built for {name}={rec[i]}, the call has {v}")
 
 
-def _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, cmp_ratio, ori_win_left, ori_win_right):
+def _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, cmp_ratio, ori_win_left, ori_win_right, tnd=None):
     """Kernel operands of the shared-KV attention: query and cat(ori_kv, cmp_kv) rows as the
     gathered-attention kernels take them (bf16: 512-column rows, the kernels' rope-less
     width, zero-padded when D < 512; fp32: as given) and the [B,S,W(+K)] slot indices over
-    the concatenated rows."""
-    B, S, H, D = query.shape
-    ori = ori_kv.reshape(ori_kv.shape[0], ori_kv.shape[1], ori_kv.shape[-1])
-    cmp = None if cmp_kv is None else cmp_kv.reshape(cmp_kv.shape[0], cmp_kv.shape[1], cmp_kv.shape[-1])
-    if cmp_sparse_indices is not None and cmp_sparse_indices.dim() == 4:
-        cmp_sparse_indices = cmp_sparse_indices.squeeze(2)
-    n_cmp = 0 if cmp is None else cmp.shape[1]
-    idx = v4_attention_indices(B, S, query.device, win_left=int(ori_win_left), win_right=int(ori_win_right),
-                               cmp_ratio=int(cmp_ratio), n_cmp=n_cmp,
-                               cmp_indices=cmp_sparse_indices if cmp_ratio == 4 else None)
+    the concatenated rows.  ``tnd`` (a dict of cu_seqlens_q / cu_seqlens_ori_kv /
+    cu_seqlens_cmp_kv / cmp_residual_kv / max_cmp) marks a packed batch: query [T,N,D],
+    ori_kv [T_ori,(1,)D], cmp_kv [T_c,(1,)D], cmp_sparse_indices [T,(1,)K] sequence-local;
+    it runs as one [1,T] batch whose slot indices keep every query inside its sequence."""
+    if tnd is not None:
+        T, H, D = query.shape
+        ori = ori_kv.reshape(1, ori_kv.shape[0], ori_kv.shape[-1])
+        cmp = None if cmp_kv is None else cmp_kv.reshape(1, cmp_kv.shape[0], cmp_kv.shape[-1])
+        cmp_ratio = int(cmp_ratio) if cmp is not None else 1
+        ci = None
+        if cmp_ratio == 4:
+            if cmp_sparse_indices is None:
+                raise ValueError("cmp_ratio 4 needs cmp_sparse_indices")
+            ci = cmp_sparse_indices.reshape(T, -1)
+        idx = sharedkv_tnd_indices(tnd["cu_seqlens_q"], tnd.get("cu_seqlens_ori_kv"), T, ori.shape[1], query.device,
+                                   win_left=int(ori_win_left), win_right=int(ori_win_right), cmp_ratio=cmp_ratio,
+                                   cu_seqlens_cmp_kv=tnd.get("cu_seqlens_cmp_kv"),
+                                   cmp_residual_kv=tnd.get("cmp_residual_kv"), cmp_indices=ci,
+                                   max_cmp=int(tnd.get("max_cmp", 0)))
+        query = query.reshape(1, T, H, D)
+        idx = idx.unsqueeze(0)
+    else:
+        B, S, H, D = query.shape
+        ori = ori_kv.reshape(ori_kv.shape[0], ori_kv.shape[1], ori_kv.shape[-1])
+        cmp = None if cmp_kv is None else cmp_kv.reshape(cmp_kv.shape[0], cmp_kv.shape[1], cmp_kv.shape[-1])
+        if cmp_sparse_indices is not None and cmp_sparse_indices.dim() == 4:
+            cmp_sparse_indices = cmp_sparse_indices.squeeze(2)
+        n_cmp = 0 if cmp is None else cmp.shape[1]
+        idx = v4_attention_indices(B, S, query.device, win_left=int(ori_win_left), win_right=int(ori_win_right),
+                                   cmp_ratio=int(cmp_ratio), n_cmp=n_cmp,
+                                   cmp_indices=cmp_sparse_indices if cmp_ratio == 4 else None)
     kv = ori if cmp is None else torch.cat([ori, cmp], dim=1)
     bf16 = query.dtype == torch.bfloat16
     if bf16 and D > 512:
@@ -837,8 +916,9 @@ def _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, cmp_ratio, ori_
     # bf16: 512-column rows (k = v = the whole row; the kernels' d_qk = d_v = 512 variant,
     # no rope columns).  fp32: the exact kernel takes any width.
     dqk, dv = (512, 512) if bf16 else (D, D)
+    W = int(ori_win_left) + int(ori_win_right) + 1
     return dict(q=_pad_rows(query, dqk), kv=_pad_rows(kv, dqk), idx=idx, D=D, dv=dv, s_ori=ori.shape[1],
-                has_cmp=cmp is not None)
+                has_cmp=cmp is not None, W=W, tnd=tnd is not None)
 
 
 def _sharedkv_forward(prep, sinks, scale):
@@ -847,35 +927,54 @@ def _sharedkv_forward(prep, sinks, scale):
                           sinks=sinks)
 
 
-def _sharedkv_backward(prep, out, dout, m2, s2, sinks, scale):
-    """(dq [B,S,H,D], d_ori [B,S_ori,D], d_cmp [B,S_c,D] or None, d_sink [H] or None), fp32 dKV."""
+def _sharedkv_backward(prep, out, dout, m2, s2, sinks, scale, *, return_cmp_mass=False):
+    """(dq [B,S,H,D], d_ori [B,S_ori,D], d_cmp [B,S_c,D] or None, d_sink [H] or None), fp32 dKV;
+    with ``return_cmp_mass`` also the head-summed probability [B,S,K] at the compressed slots
+    (from the probabilities the bf16 backward recomputes; dsa_attn_mass on the fp32 path)."""
     D, dv = prep["D"], prep["dv"]
-    dout = _pad_rows(dout.to(out.dtype), dv) if dv != D else dout.contiguous().to(out.dtype)
+    dout = _pad_rows(dout.reshape(out.shape[:-1] + dout.shape[-1:]).to(out.dtype), dv) if dv != D else \
+        dout.reshape(out.shape).contiguous().to(out.dtype)
     # P_j = exp(x_j - lse) with lse = m2 + log s2 includes the sink, and the kernel's
     # delta = rowsum(dO * O) uses the sink-scaled O: dQ and dKV are exact.  The sink has no
     # value: d sink = -sum over rows of p_sink * rowsum(dO o O), from the same delta pass.
+    bf16 = prep["q"].dtype == torch.bfloat16
+    fused_mass = return_cmp_mass and bf16
     res = sparse_mla_bwd(prep["q"], prep["kv"], prep["idx"], out, dout, m2, s2, scale, q_offset=_NO_MASK_OFFSET,
-                         sinks=sinks)
+                         sinks=sinks, return_mass=fused_mass)
     dq, dkv = res[0], res[1]
-    dsink = res[2] if sinks is not None else None
+    mass = res[2] if fused_mass else None
+    dsink = res[-1] if sinks is not None else None
+    if return_cmp_mass and mass is None:
+        mass = attn_mass(prep["q"], prep["kv"], prep["idx"], m2, s2, scale, q_offset=_NO_MASK_OFFSET)
     dkv = dkv[..., :D]
     s_ori = prep["s_ori"]
-    return dq[..., :D], dkv[:, :s_ori], (dkv[:, s_ori:] if prep["has_cmp"] else None), dsink
+    out4 = (dq[..., :D], dkv[:, :s_ori], (dkv[:, s_ori:] if prep["has_cmp"] else None), dsink)
+    if return_cmp_mass:
+        return out4 + (mass[..., prep["W"]:],)
+    return out4
 
 
 def _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, block_tables, seq_tensors, ori_mask_mode,
                          cmp_mask_mode):
-    if layout_q != "BSND" or layout_kv != "BSND":
-        raise NotImplementedError(f"layouts {layout_q}/{layout_kv}: BSND only (the reference's shared-KV wrapper "
-                                  "passes BSND and no cu_seqlens)")
+    """Returns True for a packed (TND) call: both layouts TND and cu_seqlens_q given (the
+    first of ``seq_tensors``); BSND takes no cu_seqlens / seqused tensors."""
+    if (layout_q, layout_kv) not in (("BSND", "BSND"), ("TND", "TND")):
+        raise NotImplementedError(f"layouts {layout_q}/{layout_kv}: BSND/BSND or TND/TND")
     if ori_sparse_indices is not None:
         raise NotImplementedError("ori_sparse_indices: the window over ori_kv is the band of ori_mask_mode 4")
     if any(t is not None for t in block_tables):
         raise NotImplementedError("paged KV (block tables) is not supported")
-    if any(t is not None and t.numel() for t in seq_tensors):
-        raise NotImplementedError("cu_seqlens / seqused arguments need layout TND, which is not supported here")
     if ori_mask_mode != 4 or cmp_mask_mode != 3:
         raise NotImplementedError("mask modes: band window (4) over ori_kv, causal (3) over cmp_kv")
+    if layout_q == "TND":
+        if seq_tensors[0] is None:
+            raise ValueError("layout TND needs cu_seqlens_q")
+        if any(t is not None and t.numel() for t in seq_tensors[3:]):
+            raise NotImplementedError("seqused_* (per-sequence used lengths) is not supported")
+        return True
+    if any(t is not None and t.numel() for t in seq_tensors):
+        raise NotImplementedError("cu_seqlens / seqused arguments need layout TND")
+    return False
 
 
 def npu_sparse_attn_sharedkv(
@@ -914,25 +1013,50 @@ def npu_sparse_attn_sharedkv(
     LiCompute returns them (-1 empty; ratio 4 only, every causal block t < (s+1)//r
     otherwise); sinks [N] fp32 (a per-head logit with no value) or None.  Each query sees
     the ori tokens of its band [s - ori_win_left, s + ori_win_right] and its compressed rows.
-    Returns (attn_out like query, softmax_lse fp32 [B,S,N,1] = the natural-log logsumexp of
-    every logit of the row including the sink, or None without ``return_softmax_lse``).
-    Not differentiable by itself: ``npu_sparse_attn_sharedkv_grad`` is its backward.
+    Layout TND (packed sequences, ``cu_seqlens_q`` / ``cu_seqlens_ori_kv`` /
+    ``cu_seqlens_cmp_kv``): query [T,N,D], ori_kv [T,1,D], cmp_kv [T_c,1,D],
+    cmp_sparse_indices [T,1,K] sequence-local; the same rules hold inside each sequence
+    (``sharedkv_tnd_indices``).  Returns (attn_out like query, softmax_lse fp32 [B,S,N,1]
+    (TND: [T,N,1]) = the natural-log logsumexp of every logit of the row including the
+    sink, or None without ``return_softmax_lse``).  Not differentiable by itself:
+    ``npu_sparse_attn_sharedkv_grad`` is its backward.
     """
-    _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, (ori_block_table, cmp_block_table),
-                         (cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, seqused_q, seqused_kv), ori_mask_mode,
-                         cmp_mask_mode)
+    tnd = _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, (ori_block_table, cmp_block_table),
+                               (cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, seqused_q, seqused_kv),
+                               ori_mask_mode, cmp_mask_mode)
     if ori_kv is None:
         raise NotImplementedError("ori_kv is required (the window keys)")
     require_gpu_tensor(query, "query")
     _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, ori_win_right)
+    geo = _sharedkv_tnd_args(cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, None, cmp_kv, cmp_ratio) if tnd else None
     prep = _sharedkv_prepare(query.contiguous(), ori_kv.contiguous(), cmp_kv, cmp_sparse_indices, int(cmp_ratio),
-                             ori_win_left, ori_win_right)
+                             ori_win_left, ori_win_right, tnd=geo)
     sk = None if sinks is None else sinks.float().contiguous()
     out, m2, s2 = _sharedkv_forward(prep, sk, float(softmax_scale))
     D = prep["D"]
     out = out[..., :D].contiguous() if prep["dv"] != D else out
     lse = (m2 + torch.log(s2)).unsqueeze(-1) if return_softmax_lse else None
+    if tnd:
+        out = out.reshape(query.shape)
+        lse = None if lse is None else lse.reshape(*query.shape[:2], 1)
     return out, lse
+
+
+def _sharedkv_tnd_args(cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, cmp_residual_kv, cmp_kv, cmp_ratio,
+                       max_cmp=None):
+    """The ``tnd`` argument of _sharedkv_prepare; ``max_cmp`` (the longest compressed
+    sequence, the slot count of the every-causal-block rule) is read from cu_seqlens_cmp_kv
+    when not given (a device tensor is read back once per version)."""
+    geo = dict(cu_seqlens_q=cu_seqlens_q, cu_seqlens_ori_kv=cu_seqlens_ori_kv, cu_seqlens_cmp_kv=cu_seqlens_cmp_kv,
+               cmp_residual_kv=cmp_residual_kv, max_cmp=0)
+    if cmp_kv is not None and int(cmp_ratio) > 1:
+        if cu_seqlens_cmp_kv is None:
+            raise ValueError("compressed KV in layout TND needs cu_seqlens_cmp_kv")
+        if max_cmp is None:
+            cu = _lib.host_ints(cu_seqlens_cmp_kv)
+            max_cmp = max([b - a for a, b in zip(cu[:-1], cu[1:])] or [0])
+        geo["max_cmp"] = int(max_cmp)
+    return geo
 
 
 def npu_sparse_attn_sharedkv_grad(
@@ -961,21 +1085,39 @@ def npu_sparse_attn_sharedkv_grad(
     the forward's output and softmax_lse, returns (d_query like query, d_ori_kv like ori_kv,
     d_cmp_kv like cmp_kv or None, d_sinks like sinks), allocated in the inputs' dtypes as the
     binding does."""
-    _check_sharedkv_args(layout, layout, ori_sparse_indices, (), (cu_seqlens_q, cu_seqlens_ori_kv,
-                                                                 cu_seqlens_cmp_kv), ori_mask_mode, cmp_mask_mode)
+    tnd = _check_sharedkv_args(layout, layout, ori_sparse_indices, (), (cu_seqlens_q, cu_seqlens_ori_kv,
+                                                                       cu_seqlens_cmp_kv), ori_mask_mode, cmp_mask_mode)
     if d_out is None or out is None or lse is None or sinks is None:
         raise ValueError("d_out, out, lse and sinks are required")
+    geo = _sharedkv_tnd_args(cu_seqlens_q, cu_seqlens_ori_kv, cu_seqlens_cmp_kv, None, cmp_kv, cmp_ratio) if tnd else None
+    res = _sharedkv_grad(query, ori_kv, cmp_kv, d_out, out, lse, cmp_sparse_indices, sinks, scale_value, cmp_ratio,
+                         ori_win_left, ori_win_right, geo)
+    return res[:4]
+
+
+def _sharedkv_grad(query, ori_kv, cmp_kv, d_out, out, lse, cmp_sparse_indices, sinks, scale_value, cmp_ratio,
+                   ori_win_left, ori_win_right, geo, return_cmp_mass=False):
+    """npu_sparse_attn_sharedkv_grad's work (BSND, or TND with ``geo``); with
+    ``return_cmp_mass`` also the head-summed probability at each compressed slot, fp32
+    [B,S,K] (TND: [T,K])."""
     prep = _sharedkv_prepare(query.contiguous(), ori_kv.contiguous(), cmp_kv, cmp_sparse_indices, int(cmp_ratio),
-                             ori_win_left, ori_win_right)
+                             ori_win_left, ori_win_right, tnd=geo)
     D, dv = prep["D"], prep["dv"]
-    o = _pad_rows(out.to(prep["q"].dtype), dv) if dv != D else out.contiguous().to(prep["q"].dtype)
-    m2 = lse.reshape(lse.shape[:3]).float().contiguous()
+    shp = prep["q"].shape[:-1]
+    o = out.reshape(*shp, out.shape[-1]).to(prep["q"].dtype)
+    o = _pad_rows(o, dv) if dv != D else o.contiguous()
+    m2 = lse.reshape(shp).float().contiguous()
     s2 = torch.ones_like(m2)
-    dq, d_ori, d_cmp, dsink = _sharedkv_backward(prep, o, d_out, m2, s2, sinks.float().contiguous(),
-                                                 float(scale_value))
+    res = _sharedkv_backward(prep, o, d_out.reshape(*shp, d_out.shape[-1]), m2, s2, sinks.float().contiguous(),
+                             float(scale_value), return_cmp_mass=return_cmp_mass)
+    dq, d_ori, d_cmp, dsink = res[:4]
     d_ori = d_ori.reshape(ori_kv.shape).to(ori_kv.dtype)
     d_cmp = None if d_cmp is None or cmp_ratio <= 1 else d_cmp.reshape(cmp_kv.shape).to(cmp_kv.dtype)
-    return dq.to(query.dtype), d_ori, d_cmp, dsink.reshape(sinks.shape).to(sinks.dtype)
+    out4 = (dq.reshape(query.shape).to(query.dtype), d_ori, d_cmp, dsink.reshape(sinks.shape).to(sinks.dtype))
+    if return_cmp_mass:
+        mass = res[4]
+        return out4 + (mass.reshape(query.shape[0], -1) if geo is not None else mass,)
+    return out4
 
 
 class SparseAttnSharedKV(torch.autograd.Function):
@@ -988,31 +1130,37 @@ class SparseAttnSharedKV(torch.autograd.Function):
                 cmp_sparse_indices, sinks, softmax_scale, cmp_ratio, ori_mask_mode, cmp_mask_mode, ori_win_left,
                 ori_win_right, num_heads_q, num_heads_kv, head_dim, batch_size, max_seq_len_q, max_seq_len_kv, topk,
                 layout_q, layout_kv):
-        _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, (),
-                             (cu_seq_lens_q, cu_seq_lens_ori_kv, cu_seq_lens_cmp_kv), ori_mask_mode, cmp_mask_mode)
+        tnd = _check_sharedkv_args(layout_q, layout_kv, ori_sparse_indices, (),
+                                   (cu_seq_lens_q, cu_seq_lens_ori_kv, cu_seq_lens_cmp_kv), ori_mask_mode,
+                                   cmp_mask_mode)
         metadata = npu_sparse_attn_sharedkv_metadata(
             cu_seq_lens_q, None, None, None, None, num_heads_q, num_heads_kv, head_dim, batch_size, max_seq_len_q,
             max_seq_len_kv, 0, topk, cmp_ratio, ori_mask_mode, cmp_mask_mode, ori_win_left, ori_win_right, layout_q,
             layout_kv, ori_kv is not None, cmp_kv is not None, device=query.device)
         _check_sharedkv_metadata(metadata, query, cmp_kv, cmp_ratio, ori_win_left, ori_win_right)
         # the kernels' operands are kept for backward (the bf16 path pads query rows to 512)
+        geo = _sharedkv_tnd_args(cu_seq_lens_q, cu_seq_lens_ori_kv, cu_seq_lens_cmp_kv, None, cmp_kv,
+                                 cmp_ratio) if tnd else None
         prep = _sharedkv_prepare(query, ori_kv, cmp_kv, cmp_sparse_indices, int(cmp_ratio), ori_win_left,
-                                 ori_win_right)
+                                 ori_win_right, tnd=geo)
         sk = None if sinks is None else sinks.float().contiguous()
         out, m2, s2 = _sharedkv_forward(prep, sk, float(softmax_scale))
         ctx.prep = prep
+        ctx.q_shape = query.shape
         ctx.save_for_backward(out, m2, s2, sk)
         ctx.softmax_scale = float(softmax_scale)
         ctx.in_dtypes = (ori_kv.dtype, None if cmp_kv is None else cmp_kv.dtype, None if sinks is None else sinks.dtype)
         ctx.shapes = (ori_kv.shape, None if cmp_kv is None else cmp_kv.shape, None if sinks is None else sinks.shape)
         ctx.cmp_ratio = int(cmp_ratio)
         D = prep["D"]
-        return out[..., :D] if prep["dv"] != D else out
+        res = out[..., :D] if prep["dv"] != D else out
+        return res.reshape(query.shape)
 
     @staticmethod
     def backward(ctx, grad_output):
         out, m2, s2, sk = ctx.saved_tensors
         dq, d_ori, d_cmp, dsink = _sharedkv_backward(ctx.prep, out, grad_output, m2, s2, sk, ctx.softmax_scale)
+        dq = dq.reshape(ctx.q_shape)
         ori_dt, cmp_dt, sink_dt = ctx.in_dtypes
         ori_shape, cmp_shape, sink_shape = ctx.shapes
         d_ori = d_ori.reshape(ori_shape).to(ori_dt)
