@@ -207,9 +207,10 @@ int dsa_sparse_mla_fwd(const void* q, const void* kv, const int32_t* indices, vo
  *   workspace  device scratch of workspace_bytes (dsa_sparse_mla_bwd_workspace_size() gives the
  *              default; a smaller one processes query rows in more chunks); fp32 dtype needs none
  * The bf16 path needs D_qk = 576 or 512, D_v = 512, H <= 128.  dKV is reduced per key through a
- * key-major CSR of the bf16 per-(row, slot) contributions, summed in fp32; only a key whose
- * list straddles two reduction segments adds its partial sums with fp32 atomics, so dKV
- * is reproducible to fp32 rounding, not bit for bit.
+ * key-major CSR of the bf16 per-(row, slot) contributions, summed in fp32 in a fixed order
+ * (no float atomics), so the same inputs and workspace size give the same dKV bit for bit;
+ * another workspace size (another row chunking) changes the summation order.  The fp32
+ * path scatters with fp32 atomics and is reproducible to rounding only.
  */
 int64_t dsa_sparse_mla_bwd_workspace_size(int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads,
                                           int64_t d_qk, int64_t topk);

@@ -125,6 +125,13 @@ def test_kl_op_cmp_ratio_dtypes_and_deterministic_warning():
     assert any("deterministic" in str(x.message) for x in ws)
 
 
+def test_kl_deterministic_flag_is_met_on_the_mfma_shapes():
+    """H_I = 64, D_I = 128 runs the KL MFMA kernel, whose d_key_index is bitwise reproducible:
+    deterministic=True gives no warning there."""
+    assert ops._kl_mfma_shape(torch.empty(1, 4, 64, 128), torch.empty(1, 4, 1, 128))
+    assert not ops._kl_mfma_shape(torch.empty(1, 4, 8, 16), torch.empty(1, 4, 1, 16))
+
+
 def test_custom_ops_fake_shapes_and_autograd_on_meta():
     from torchtitan_npu_simulator_amd import library  # noqa: F401  (registers dsa_mi355x::*)
 

@@ -48,6 +48,16 @@ def test_indexer_kl_parity(S, H, D, K, q_offset, holes):
     assert rel_err(dw, 2.0 * rdw) <= 1e-2, rel_err(dw, 2.0 * rdw)
 
 
+def test_indexer_kl_dk_is_bitwise_reproducible():
+    """dk_idx sums each key's contributions in a fixed order: two runs give the same bits
+    (key lists of ~250-500 pairs straddle the 256-pair reduction segments)."""
+    qi, ki, w, idx, mass = _case(768, 64, 128, 384, seed=5, holes=0.02)
+    a = _gpu(qi, ki, w, idx, mass)
+    b = _gpu(qi, ki, w, idx, mass)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
 def test_indexer_kl_zero_when_distributions_match():
     """If softmax(I) over the selected keys equals the target, loss and gradients vanish."""
     S, H, D, K = 64, 64, 128, 32

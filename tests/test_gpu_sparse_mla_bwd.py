@@ -116,6 +116,25 @@ def test_bwd_bf16_chunked_workspace_matches_single_pass():
     assert rel_err(dkv2, dkv1) <= 1e-6
 
 
+@pytest.mark.parametrize("d_qk,chunk_bytes", [(576, None), (512, None), (576, 40 << 20)])
+def test_bwd_dkv_is_bitwise_reproducible(d_qk, chunk_bytes):
+    """dKV sums every key's contributions in a fixed order (key lists placed row by row, the
+    partial sums of keys that straddle reduction segments added in segment order): three runs
+    of the same backward give the same bits.  The keys' lists here (~450 pairs) all straddle
+    256-pair segments; the chunked case also adds over several row chunks."""
+    S, H, K = 1024, 32, 512
+    q, kv, dout, scale = attn_inputs(S, H, seed=12, d_qk=d_qk)
+    idx = rand_indices(S, K, seed=12, shuffle=True, holes=0.05)
+    ops = _ops()
+    qd, kvd, idd, dod = q.to(DEV), kv.to(DEV), idx.to(DEV), dout.to(DEV)
+    out, smax, ssum = ops.sparse_mla_fwd(qd, kvd, idd, scale)
+    runs = [ops.sparse_mla_bwd(qd, kvd, idd, out, dod, smax, ssum, scale, workspace_bytes=chunk_bytes)
+            for _ in range(3)]
+    for dq, dkv in runs[1:]:
+        assert torch.equal(dq, runs[0][0])
+        assert torch.equal(dkv, runs[0][1])
+
+
 def test_bwd_dense_special_case_matches_sdpa_autograd():
     S, H = 96, 32
     q, kv, dout, scale = attn_inputs(S, H, seed=6)

@@ -3,15 +3,20 @@
 //
 // The pairs of a query-row chunk are counted per key with LDS-privatised histograms (one
 // workgroup per block of query rows and 16384-key range, the ranges of one row block
-// adjacent in launch order so they share its index rows in L2), scanned into row_ptr, and
-// placed by a second pass that reserves one contiguous range per (workgroup, key).  The
-// row block grows with the key count (about four pairs per key and workgroup), so the
-// global atomics of the histogram flush and the range reservation stay well below one
-// per pair also for long KV prefixes.  The reduction
-// then gives every key a single owner that sums its pairs' bf16 contribution rows in
-// fp32 and adds the result to the caller's accumulator with plain loads/stores, so no
-// float atomics are issued.  Order within a key's list varies run to run, so fp32 sums
-// may differ in the last bits between runs.
+// adjacent in launch order so they share its index rows in L2) stored as a [row block][key]
+// count table; a two-level column scan of that table gives every (row block, key) its
+// offset inside the key's list, a scan of the key totals gives row_ptr, and a second pass
+// places each row block's pairs at row_ptr + its offset, row by row.  No global atomics are
+// issued, and the order of a key's list is the same in every run (rows in order within each
+// span of up to 2048 slots; only a key repeated inside one row has its entries for that row
+// placed in either order, which top-k output never has).
+// The row block grows with the key count (about four pairs per key and workgroup), which
+// keeps the count table about the size of the pair list.  The reduction then gives every
+// key a single owner that sums its pairs' bf16 contribution rows in fp32 and adds the
+// result to the caller's accumulator with plain loads/stores; a key whose list straddles
+// reduction segments has each segment's partial sum stored apart and added, in segment
+// order, by a fix-up pass.  No float atomics are issued and every sum is taken in a fixed
+// order, so the accumulator's result is the same bit for bit in every run.
 #pragma once
 #include "dsa_common.h"
 
@@ -22,6 +27,13 @@ constexpr int kCsrRowsMin = 16;   // query rows per counting workgroup: at least
 constexpr int kCsrRowsMax = 512;  // and at most
 constexpr int kCsrRowBatch = 8;   // index rows loaded together
 constexpr int kLdsKeys = 16384;  // keys privatised in LDS
+constexpr int kColChunk = 32;    // row blocks per chunk of the count table's column scan
+
+// query rows per counting workgroup: about four pairs per key of a range
+inline int csr_rows_per_wg(int64_t s_kv, int64_t K) {
+  const int64_t want = 4 * s_kv / (K > 0 ? K : 1);
+  return (int)(want < kCsrRowsMin ? kCsrRowsMin : want > kCsrRowsMax ? kCsrRowsMax : want);
+}
 
 __device__ __forceinline__ bool csr_slot_ok(int v, int s_kv, int64_t limit) {
   return v >= 0 && v < s_kv && (int64_t)v <= limit;
@@ -29,7 +41,9 @@ __device__ __forceinline__ bool csr_slot_ok(int v, int s_kv, int64_t limit) {
 
 // Calls f(key - key0, pair) for every valid slot of query rows [r0, r1) whose key lies in
 // [key0, key0 + nkeys); the index rows of kCsrRowBatch rows are loaded before any is used.
-template <bool kVec, typename F>
+// kOrdered: a workgroup barrier after each row's calls, so the calls of row r all come
+// before those of row r + 1 (every thread of the workgroup must call this).
+template <bool kVec, bool kOrdered = false, typename F>
 __device__ __forceinline__ void csr_for_pairs(const int32_t* __restrict__ idx, int S, int s_kv, int K, int64_t q_offset,
                                               int row0, int r0, int r1, int b, int key0, int nkeys, F&& f) {
   constexpr int kPer = kVec ? 2 : 8;  // loads per row and chunk (int4 or int)
@@ -56,7 +70,7 @@ __device__ __forceinline__ void csr_for_pairs(const int32_t* __restrict__ idx, i
 #pragma unroll
       for (int a = 0; a < kCsrRowBatch; ++a) {
         const int lr = lr0 + a;
-        if (lr >= r1) break;
+        if (lr >= r1) break;  // (uniform over the workgroup)
         const int64_t limit = (int64_t)(row0 + lr) + q_offset;
 #pragma unroll
         for (int u = 0; u < kPer; ++u)
@@ -67,57 +81,98 @@ __device__ __forceinline__ void csr_for_pairs(const int32_t* __restrict__ idx, i
             if (j < K && csr_slot_ok(key, s_kv, limit) && (unsigned)(key - key0) < (unsigned)nkeys)
               f(key - key0, lr * K + j);
           }
+        if constexpr (kOrdered) __syncthreads();
       }
     }
   }
 }
 
+// Count pass (kFill = false): table[rb][key] = the number of pairs of row block rb with
+// that key, for every key of the workgroup's range (zeros included), plain stores.
+// Fill pass: a key's pairs of row block rb start at row_ptr[key] + chunk_off[rb / kColChunk]
+// [key] + table[rb][key] (the table then holding offsets inside the column chunk) and are
+// placed row by row.
 template <bool kFill, bool kVec>
 __global__ void __launch_bounds__(256)
-csr_count_kernel(const int32_t* __restrict__ idx, int* __restrict__ counts, int* __restrict__ cursor,
-                 int* __restrict__ pairs, int S, int s_kv, int K, int64_t q_offset, int row0, int rows, int b,
-                 int n_ranges, int rows_per_wg) {
+csr_count_kernel(const int32_t* __restrict__ idx, int* __restrict__ table, const int* __restrict__ chunk_off,
+                 const int* __restrict__ row_ptr, int* __restrict__ pairs, int S, int s_kv, int K, int64_t q_offset,
+                 int row0, int rows, int b, int n_ranges, int rows_per_wg) {
   extern __shared__ int hist[];
   const int rb = blockIdx.x / n_ranges, kr = blockIdx.x - rb * n_ranges;
   const int key0 = kr * kLdsKeys, nkeys = min(kLdsKeys, s_kv - key0);
   const int r0 = rb * rows_per_wg;
   const int r1 = min(rows, r0 + rows_per_wg);
-  for (int j = threadIdx.x; j < nkeys; j += 256) hist[j] = 0;
-  __syncthreads();
-  csr_for_pairs<kVec>(idx, S, s_kv, K, q_offset, row0, r0, r1, b, key0, nkeys,
-                      [&](int u, int) { atomicAdd(&hist[u], 1); });
-  __syncthreads();
+  int* trow = table + (int64_t)rb * s_kv + key0;
   if (!kFill) {
-    for (int j = threadIdx.x; j < nkeys; j += 256)
-      if (hist[j]) atomicAdd(&counts[key0 + j], hist[j]);
+    for (int j = threadIdx.x; j < nkeys; j += 256) hist[j] = 0;
+    __syncthreads();
+    csr_for_pairs<kVec>(idx, S, s_kv, K, q_offset, row0, r0, r1, b, key0, nkeys,
+                        [&](int u, int) { atomicAdd(&hist[u], 1); });
+    __syncthreads();
+    for (int j = threadIdx.x; j < nkeys; j += 256) trow[j] = hist[j];
     return;
   }
-  // fill: reserve this workgroup's range per key, then place pairs
-  for (int j = threadIdx.x; j < nkeys; j += 256) {
-    const int c = hist[j];
-    hist[j] = c ? atomicAdd(&cursor[key0 + j], c) : 0;
-  }
+  const int* coff = chunk_off + (int64_t)(rb / kColChunk) * s_kv + key0;
+  for (int j = threadIdx.x; j < nkeys; j += 256) hist[j] = row_ptr[key0 + j] + coff[j] + trow[j];
   __syncthreads();
-  csr_for_pairs<kVec>(idx, S, s_kv, K, q_offset, row0, r0, r1, b, key0, nkeys,
-                      [&](int u, int pair) { pairs[atomicAdd(&hist[u], 1)] = pair; });
+  csr_for_pairs<kVec, true>(idx, S, s_kv, K, q_offset, row0, r0, r1, b, key0, nkeys,
+                            [&](int u, int pair) { pairs[atomicAdd(&hist[u], 1)] = pair; });
 }
 
 template <bool kFill>
-void launch_csr_count(bool vec, unsigned grid, size_t lds, hipStream_t st, const int32_t* idx, int* counts,
-                      int* cursor, int* pairs, int S, int s_kv, int K, int64_t q_offset, int row0, int rows, int b,
-                      int n_ranges, int rows_per_wg) {
+void launch_csr_count(bool vec, unsigned grid, size_t lds, hipStream_t st, const int32_t* idx, int* table,
+                      const int* chunk_off, const int* row_ptr, int* pairs, int S, int s_kv, int K, int64_t q_offset,
+                      int row0, int rows, int b, int n_ranges, int rows_per_wg) {
   const TimedLaunch tl(kFill ? "csr_count_kernel<fill>" : "csr_count_kernel<count>", st);
   if (vec)
-    csr_count_kernel<kFill, true><<<grid, 256, lds, st>>>(idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
-                                                          rows, b, n_ranges, rows_per_wg);
+    csr_count_kernel<kFill, true><<<grid, 256, lds, st>>>(idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
+                                                          q_offset, row0, rows, b, n_ranges, rows_per_wg);
   else
-    csr_count_kernel<kFill, false><<<grid, 256, lds, st>>>(idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
-                                                           rows, b, n_ranges, rows_per_wg);
+    csr_count_kernel<kFill, false><<<grid, 256, lds, st>>>(idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
+                                                           q_offset, row0, rows, b, n_ranges, rows_per_wg);
 }
 
-__global__ void zero_i32_kernel(int* __restrict__ p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
+// Column scan of the count table, first level: within each chunk of kColChunk row blocks,
+// table[rb][key] <- exclusive prefix over the chunk's earlier row blocks, and
+// chunk_off[c][key] <- the chunk's total.  One thread per (key, chunk); its loads are
+// issued together.
+__global__ void __launch_bounds__(256)
+csr_colscan_kernel(int* __restrict__ table, int* __restrict__ chunk_off, int s_kv, int n_rb) {
+  const int key = blockIdx.x * 256 + threadIdx.x;
+  const int c = blockIdx.y;
+  if (key >= s_kv) return;
+  const int rb0 = c * kColChunk, n = min(kColChunk, n_rb - rb0);
+  int* col = table + (int64_t)rb0 * s_kv + key;
+  int v[kColChunk];
+#pragma unroll
+  for (int i = 0; i < kColChunk; ++i) v[i] = i < n ? col[(int64_t)i * s_kv] : 0;
+  int run = 0;
+#pragma unroll
+  for (int i = 0; i < kColChunk; ++i) {
+    if (i < n) col[(int64_t)i * s_kv] = run;
+    run += v[i];
+  }
+  chunk_off[(int64_t)c * s_kv + key] = run;
+}
+
+// Second level: chunk_off[c][key] <- exclusive prefix over the earlier chunks, and
+// counts[key] <- the key's total.  One thread per key.
+__global__ void __launch_bounds__(256)
+csr_chunkscan_kernel(int* __restrict__ chunk_off, int* __restrict__ counts, int s_kv, int n_chunks) {
+  const int key = blockIdx.x * 256 + threadIdx.x;
+  if (key >= s_kv) return;
+  int run = 0;
+  for (int c0 = 0; c0 < n_chunks; c0 += 16) {
+    int v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = c0 + i < n_chunks ? chunk_off[(int64_t)(c0 + i) * s_kv + key] : 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (c0 + i < n_chunks) chunk_off[(int64_t)(c0 + i) * s_kv + key] = run;
+      run += v[i];
+    }
+  }
+  counts[key] = run;
 }
 
 // exclusive scan of counts -> row_ptr (s_kv + 1 entries) and cursor = row_ptr; one
@@ -166,7 +221,7 @@ __global__ void __launch_bounds__(1024) csr_scan_kernel(const int* __restrict__ 
     for (int u = 0; u < kScanPer; ++u) {
       if (j0 + u < s_kv) {
         row_ptr[j0 + u] = run;
-        cursor[j0 + u] = run;
+        if (cursor) cursor[j0 + u] = run;
       }
       run += v[u];
     }
@@ -198,18 +253,17 @@ __device__ __forceinline__ void add_bf16x8(float (&acc)[8], const u32x4& v) {
     acc[2 * r + 1] += bf16_hi(v[r]);
   }
 }
+// sole owner: d += acc (read-add-write); a straddling key's segment partial: d = acc
 __device__ __forceinline__ void flush8(float* d, float (&acc)[8], bool sole) {
+  float4* d4 = reinterpret_cast<float4*>(d);
+  float4 x = make_float4(acc[0], acc[1], acc[2], acc[3]), y = make_float4(acc[4], acc[5], acc[6], acc[7]);
   if (sole) {
-    float4* d4 = reinterpret_cast<float4*>(d);
-    float4 x = d4[0], y = d4[1];
-    x.x += acc[0]; x.y += acc[1]; x.z += acc[2]; x.w += acc[3];
-    y.x += acc[4]; y.y += acc[5]; y.z += acc[6]; y.w += acc[7];
-    d4[0] = x;
-    d4[1] = y;
-  } else {
-#pragma unroll
-    for (int r = 0; r < 8; ++r) atomicAdd(d + r, acc[r]);
+    const float4 a = d4[0], c = d4[1];
+    x.x += a.x; x.y += a.y; x.z += a.z; x.w += a.w;
+    y.x += c.x; y.y += c.y; y.z += c.z; y.w += c.w;
   }
+  d4[0] = x;
+  d4[1] = y;
 #pragma unroll
   for (int r = 0; r < 8; ++r) acc[r] = 0.f;
 }
@@ -226,7 +280,8 @@ csr_seg_key_kernel(const int* __restrict__ row_ptr, int* __restrict__ seg_key, i
 template <int kChunks>
 __global__ void __launch_bounds__(256)
 dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row_ptr, const int* __restrict__ pairs,
-                  const int* __restrict__ seg_key, float* __restrict__ acc_out, int s_kv, int rows, int K, int b) {
+                  const int* __restrict__ seg_key, float* __restrict__ acc_out, float* __restrict__ part, int s_kv,
+                  int rows, int K, int b) {
   static_assert(kChunks == 72 || kChunks == 64 || kChunks == 16, "row widths of the attention and indexer reductions");
   constexpr int kWidth = kChunks * 8;
   constexpr int kGroup = 8;
@@ -239,13 +294,15 @@ dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row
   const uint16_t* cb = cbuf + (int64_t)b * rows * K * kWidth;
   float* dbase = acc_out + (int64_t)b * s_kv * kWidth;
   int k = seg_key[seg];
+  const int k_first = k;
   int kbeg = row_ptr[k], kend = row_ptr[k + 1];
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float acc2[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // 72-chunk rows: chunk 64 + (lane & 7)
   const int stream = lane >> 4, c16 = lane & 15;               // 16-chunk rows
   auto flush = [&]() {
+    // a straddling key is the segment's first key (partial slot 0) or its last (slot 1)
     const bool sole = kbeg >= seg0 && kend <= seg1;
-    float* d = dbase + (int64_t)k * kWidth;
+    float* d = sole ? dbase + (int64_t)k * kWidth : part + ((int64_t)seg * 2 + (k == k_first ? 0 : 1)) * kWidth;
     if constexpr (kChunks >= 64) {
       flush8(d + 8 * lane, acc, sole);
       if constexpr (kChunks == 72) {
@@ -304,10 +361,43 @@ dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row
   flush();
 }
 
-// Bytes of the CSR workspace csr_reduce needs: counts, row_ptr, cursor (s_kv + 1 ints
-// each) and the segment table (one int per kSegPairs pairs of the chunk).
-inline int64_t csr_ws_bytes(int64_t s_kv, int64_t rows, int64_t K) {
-  return (3 * (s_kv + 1) + (rows * K + kSegPairs - 1) / kSegPairs) * 4;
+// A straddling key: acc_out[k] += its segments' partial sums, in segment order (partial slot
+// 0 where k is the segment's first key, else slot 1).  One wave per key.
+template <int kWidth>
+__global__ void __launch_bounds__(256)
+csr_partial_fixup_kernel(const int* __restrict__ row_ptr, const int* __restrict__ seg_key,
+                         const float* __restrict__ part, float* __restrict__ acc_out, int s_kv, int b) {
+  const int k = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (k >= s_kv) return;
+  const int kbeg = row_ptr[k], kend = row_ptr[k + 1];
+  if (kend <= kbeg) return;
+  const int s0 = kbeg / kSegPairs, s1 = (kend - 1) / kSegPairs;
+  if (s0 == s1) return;  // inside one segment: its owner added it
+  constexpr int kPer = kWidth / 64;
+  float acc[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) acc[i] = 0.f;
+  for (int sg = s0; sg <= s1; ++sg) {
+    const float* src = part + ((int64_t)sg * 2 + (seg_key[sg] == k ? 0 : 1)) * kWidth;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) acc[i] += src[lane + 64 * i];
+  }
+  float* d = acc_out + ((int64_t)b * s_kv + k) * kWidth;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) d[lane + 64 * i] += acc[i];
+}
+
+// Bytes of the CSR workspace csr_reduce needs for contribution rows of `width` floats:
+// counts and row_ptr (s_kv + 1 ints each), the segment table (one int per kSegPairs pairs
+// of the chunk), the [row block][key] count table, the [column chunk][key] chunk offsets
+// and two partial-sum rows per segment (at a 16-byte boundary).
+inline int64_t csr_ws_bytes(int64_t s_kv, int64_t rows, int64_t K, int64_t width) {
+  const int64_t n_rb = (rows + csr_rows_per_wg(s_kv, K) - 1) / csr_rows_per_wg(s_kv, K);
+  const int64_t n_chunks = (n_rb + kColChunk - 1) / kColChunk;
+  const int64_t n_seg = (rows * K + kSegPairs - 1) / kSegPairs;
+  const int64_t ints = 2 * (s_kv + 1) + n_seg + (n_rb + n_chunks) * s_kv;
+  return (ints + 3) / 4 * 16 + n_seg * 2 * width * 4;
 }
 
 // Build the CSR for query rows [row0, row0 + rows) of batch element b and reduce the
@@ -316,31 +406,41 @@ inline int64_t csr_ws_bytes(int64_t s_kv, int64_t rows, int64_t K) {
 inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, int* pairs, int* csr_ws, int S,
                       int s_kv, int K, int64_t q_offset, int row0, int rows, int b, int row_chunks, hipStream_t st) {
   if (s_kv <= 0 || rows <= 0) return DSA_OK;  // no pairs: the accumulator keeps its contents
+  const int rows_per_wg = csr_rows_per_wg(s_kv, K);
+  const int64_t n_rb = ceil_div(rows, rows_per_wg);
+  const int64_t n_chunks = ceil_div(n_rb, kColChunk);
   int* counts = csr_ws;
   int* row_ptr = counts + (s_kv + 1);
-  int* cursor = row_ptr + (s_kv + 1);
-  int* seg_key = cursor + (s_kv + 1);
+  int* seg_key = row_ptr + (s_kv + 1);
+  const int64_t n_seg = ceil_div((int64_t)rows * K, kSegPairs);
+  int* table = seg_key + n_seg;
+  int* chunk_off = table + n_rb * s_kv;
+  const int64_t n_ints = 2 * (s_kv + 1) + n_seg + (n_rb + n_chunks) * s_kv;
+  float* part = reinterpret_cast<float*>(csr_ws + (n_ints + 3) / 4 * 4);
   const int n_ranges = (int)ceil_div(s_kv, kLdsKeys);
   const size_t hist_bytes = (size_t)(s_kv < kLdsKeys ? s_kv : kLdsKeys) * 4;
-  // about four pairs per key of a range per workgroup
-  const int64_t want = 4 * (int64_t)s_kv / (K > 0 ? K : 1);
-  const int rows_per_wg = (int)(want < kCsrRowsMin ? kCsrRowsMin : want > kCsrRowsMax ? kCsrRowsMax : want);
-  {
-    const TimedLaunch tl("zero_i32_kernel", st);
-    zero_i32_kernel<<<ceil_div(s_kv + 1, 256), 256, 0, st>>>(counts, s_kv + 1);
-  }
-  const int64_t cgrid = ceil_div(rows, rows_per_wg) * (int64_t)n_ranges;
-  if (cgrid > 2147483647LL) return set_error(DSA_ERR_INVALID_ARG, "csr_reduce: too many rows x keys");
+  const int64_t cgrid = n_rb * (int64_t)n_ranges;
+  if (cgrid > 2147483647LL || n_chunks > 65535)
+    return set_error(DSA_ERR_INVALID_ARG, "csr_reduce: too many rows x keys");
   const int64_t row_base = (int64_t)b * S + row0;  // int4 loads need 16-byte aligned index rows
   const bool vec = K % 4 == 0 && ((uintptr_t)(idx + row_base * K) % 16) == 0;
-  launch_csr_count<false>(vec, (unsigned)cgrid, hist_bytes, st, idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
-                          rows, b, n_ranges, rows_per_wg);
+  launch_csr_count<false>(vec, (unsigned)cgrid, hist_bytes, st, idx, table, nullptr, nullptr, pairs, S, s_kv, K,
+                          q_offset, row0, rows, b, n_ranges, rows_per_wg);
+  {
+    const TimedLaunch tl("csr_colscan_kernel", st);
+    csr_colscan_kernel<<<dim3((unsigned)ceil_div(s_kv, 256), (unsigned)n_chunks), 256, 0, st>>>(table, chunk_off,
+                                                                                                 s_kv, (int)n_rb);
+  }
+  {
+    const TimedLaunch tl("csr_chunkscan_kernel", st);
+    csr_chunkscan_kernel<<<(unsigned)ceil_div(s_kv, 256), 256, 0, st>>>(chunk_off, counts, s_kv, (int)n_chunks);
+  }
   {
     const TimedLaunch tl("csr_scan_kernel", st);
-    csr_scan_kernel<<<1, 1024, 0, st>>>(counts, row_ptr, cursor, s_kv);
+    csr_scan_kernel<<<1, 1024, 0, st>>>(counts, row_ptr, nullptr, s_kv);
   }
-  launch_csr_count<true>(vec, (unsigned)cgrid, hist_bytes, st, idx, counts, cursor, pairs, S, s_kv, K, q_offset, row0,
-                         rows, b, n_ranges, rows_per_wg);
+  launch_csr_count<true>(vec, (unsigned)cgrid, hist_bytes, st, idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
+                         q_offset, row0, rows, b, n_ranges, rows_per_wg);
   {
     const TimedLaunch tl("csr_seg_key_kernel", st);
     csr_seg_key_kernel<<<ceil_div(s_kv, 256), 256, 0, st>>>(row_ptr, seg_key, s_kv);
@@ -351,14 +451,25 @@ inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, 
                                           : "dkv_reduce_kernel<16>",
                        st);
   if (row_chunks == 72)
-    dkv_reduce_kernel<72><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, s_kv, rows, K, b);
+    dkv_reduce_kernel<72><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, part, s_kv, rows, K, b);
   else if (row_chunks == 64)
-    dkv_reduce_kernel<64><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, s_kv, rows, K, b);
+    dkv_reduce_kernel<64><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, part, s_kv, rows, K, b);
   else if (row_chunks == 16)
-    dkv_reduce_kernel<16><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, s_kv, rows, K, b);
+    dkv_reduce_kernel<16><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, part, s_kv, rows, K, b);
   else
     return set_error(DSA_ERR_UNSUPPORTED, "csr_reduce: row width %d chunks", row_chunks);
-  return check_launch("csr_reduce");
+  if (int rc = check_launch("csr_reduce")) return rc;
+  {
+    const TimedLaunch tl2("csr_partial_fixup_kernel", st);
+    const unsigned fgrid = (unsigned)ceil_div(s_kv, 4);
+    if (row_chunks == 72)
+      csr_partial_fixup_kernel<576><<<fgrid, 256, 0, st>>>(row_ptr, seg_key, part, acc_out, s_kv, b);
+    else if (row_chunks == 64)
+      csr_partial_fixup_kernel<512><<<fgrid, 256, 0, st>>>(row_ptr, seg_key, part, acc_out, s_kv, b);
+    else
+      csr_partial_fixup_kernel<128><<<fgrid, 256, 0, st>>>(row_ptr, seg_key, part, acc_out, s_kv, b);
+  }
+  return check_launch("csr_reduce(fix-up)");
 }
 
 }  // namespace

@@ -574,7 +574,7 @@ KlPlan plan_kl(int64_t batch, int64_t rows, int64_t s_k, int64_t topk) {
   p.rows = rows;
   p.ck_bytes = batch * rows * topk * kD * 2;
   p.pairs_bytes = rows * topk * 4;
-  p.csr_bytes = csr_ws_bytes(s_k, rows, topk);
+  p.csr_bytes = csr_ws_bytes(s_k, rows, topk, 128);
   p.total = al(p.ck_bytes) + al(p.pairs_bytes) + al(p.csr_bytes);
   return p;
 }

@@ -911,14 +911,14 @@ struct BwdPlan {
 BwdPlan plan_bwd(int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk, int64_t budget, int64_t width) {
   BwdPlan p{};
   const int64_t per_row = batch * g_slots(topk) * kGW * 2 + batch * topk * (int64_t)(width * 2 + 4) +
-                          2 * batch * kHeadsMax * 4;
+                          2 * batch * kHeadsMax * 4 + topk * width / 32;  // (last: CSR segment partials)
   int64_t rows = s_q;
   if (budget > 0) rows = std::max<int64_t>(1, std::min<int64_t>(s_q, budget / per_row));
   p.rows = rows;
   p.g_bytes = batch * rows * g_slots(topk) * kGW * 2;
   p.c_bytes = batch * rows * topk * width * 2;
   p.pairs_bytes = rows * topk * 4;
-  p.csr_bytes = csr_ws_bytes(s_kv, rows, topk);
+  p.csr_bytes = csr_ws_bytes(s_kv, rows, topk, width);
   p.delta_bytes = batch * rows * kHeadsMax * 4;
   auto al = [](int64_t x) { return (x + 255) / 256 * 256; };
   p.total = al(p.g_bytes) + al(p.c_bytes) + al(p.pairs_bytes) + al(p.csr_bytes) + 2 * al(p.delta_bytes);

@@ -1292,13 +1292,13 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     (the caller divides by B*S, reference dsa.py:73).  ``cmp_ratio`` > 1: key / key_index
     are compressed rows (binding.cpp:17) and sparse_indices come from the indexer's
     compressed rule t < (s+1)//r, so the -1 slots carry the validity and no causal test is
-    applied on top.  ``deterministic``: d_key_index sums each key's contributions in
-    fp32 in an order that can change from run to run (a key-major list built with atomics,
-    and fp32 atomic adds for keys whose list straddles two reduction segments), so results
-    are reproducible to fp32 rounding, not bit for bit; ``deterministic=True`` warns once that
-    this build does not offer the bitwise mode.
+    applied on top.  ``deterministic``: always met on the MFMA path - d_key_index sums each
+    key's contributions in fp32 in a fixed order (the key-major pair list is placed row by
+    row, and the partial sums of keys that straddle reduction segments are added in segment
+    order), with no float atomics, so equal inputs give equal bits; the exact fp32 kernel of
+    other shapes scatters with fp32 atomics, so ``deterministic=True`` warns there.
     """
-    if deterministic:
+    if deterministic and not _kl_mfma_shape(query_index, key_index):
         _warn_nondeterministic()
     out_dtypes = (query_index.dtype, key_index.dtype, weight.dtype)
     if layout == "TND":
@@ -1340,13 +1340,19 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
 _warned_nondeterministic = False
 
 
+def _kl_mfma_shape(query_index, key_index) -> bool:
+    """The KL MFMA kernel's shapes (H_I = 64, D_I = 128), whose d_key_index is bitwise
+    reproducible; other shapes take the exact fp32 kernel."""
+    return query_index.shape[-2] == 64 and query_index.shape[-1] == 128 and key_index.shape[-1] == 128
+
+
 def _warn_nondeterministic():
     global _warned_nondeterministic
     if not _warned_nondeterministic:
         _warned_nondeterministic = True
-        warnings.warn("npu_sparse_lightning_indexer_grad_kl_loss(deterministic=True): d_key_index is reproducible "
-                      "to fp32 rounding only (per-key sums in a run-dependent order); there is no bitwise mode",
-                      stacklevel=3)
+        warnings.warn("npu_sparse_lightning_indexer_grad_kl_loss(deterministic=True): shapes other than H_I=64, "
+                      "D_I=128 run the exact fp32 kernel, whose d_key_index is reproducible to fp32 rounding only "
+                      "(fp32 atomics)", stacklevel=3)
 
 
 def _grad_scale_args(grad_scale, device):
