@@ -94,7 +94,9 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   // order keys of the thread's scores; positions past the valid prefix and NaN scores are
   // key 0 (not candidates)
   uint32_t key[kR][4];
-  auto load_seg = [&](int sg) {
+  // (the lambdas are forced inline: called from several loops, an out-of-line copy would take
+  // `key` by reference and put it in scratch memory)
+  auto load_seg = [&](int sg) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kR; ++j) {
       const int base = sg * kSeg + 4 * (t + kThreads * j);
@@ -249,7 +251,7 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   // ---- compaction in index order ----
   // (no tie at the threshold, the usual case: key > T alone decides, one ballot per score,
   // in a code path of its own so that it holds no tie state)
-  auto compact = [&](auto ties_c) {
+  auto compact = [&](auto ties_c) __attribute__((always_inline)) {
     constexpr bool kTies = decltype(ties_c)::value;
     uint32_t gt_base = 0, eq_base = 0;
     for (int sg = 0; sg < nseg; ++sg) {
@@ -374,7 +376,7 @@ extern "C" int dsa_topk(const float* scores, int32_t* indices, float* values, in
     launch_topk<8, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
   else if (s_k <= 16384)
     launch_topk<16, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
-  else
-    launch_topk<16, false>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
+  else  // long rows: 8192-score segments re-read per pass; 61 VGPRs, seven waves per SIMD in flight
+    launch_topk<8, false>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
   return check_launch("dsa_topk");
 }
