@@ -97,6 +97,16 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     }
   };
   auto gather = [&](int blk, int buf) {
+    // the four ring entries are read (and waited for) together before the first DMA: each
+    // DMA's inline asm orders memory, so a read left between two of them is a round trip
+    int vi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = ((wave * 4 + i) * 64 + lane) >> 4;
+      vi[i] = ring[blk & 3][row];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(vi[i]));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int J = wave * 4 + i;
@@ -104,8 +114,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
       const int row = p >> 4, pos = p & 15;
       const int chunk = pos ^ swz_kl(row);
       const int slot = blk * kB + row;
-      const int vi = ring[blk & 3][row];
-      const int r = (slot < K && ok_slot(vi, s_k, limit)) ? vi : 0;
+      const int r = (slot < K && ok_slot(vi[i], s_k, limit)) ? vi[i] : 0;
       dma16_to_lds(kb, (uint32_t)r * (kD * 2) + chunk * 16, (uint32_t)(uintptr_t)&kt[buf][J * 64]);
     }
   };

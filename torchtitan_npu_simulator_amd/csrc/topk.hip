@@ -12,14 +12,12 @@
 // rows are re-read per pass (from L2 / MALL).  A chunk that starts past the row's valid
 // prefix (causal rows) is skipped by the whole workgroup, in every pass.
 //   (a row with at most k valid positions takes every candidate: no pass)
-//   pass 1   histogram of the top 11 bits of every key; bin 0 holds exactly the
-//            non-candidates (key 0: NaN or past the valid prefix; real scores have keys
-//            >= 2^21), so the candidate count is the total minus bin 0, and a row with at
-//            most k candidates stops here
-//   pass 2.. histogram of the next 11 (then 10) bits below the current bin; the bin holding
-//            the k-th largest key becomes the new prefix.  Stops when the bin's keys are
-//            exactly the remaining quota or the bin is a single key value (at most three
-//            passes, each one sweep of the row).
+//   pass 0   count of candidates, min and max key
+//   pass 1.. histogram of the next 11 bits of (key - min) below the current bin; the bin
+//            holding the k-th largest key becomes the new prefix.  Digits start at the
+//            highest set bit of (max - min), so clustered scores (all of one exponent)
+//            spread over the bins from the first pass on.  Stops when the bin's keys are
+//            exactly the remaining quota or the bin is a single key value.
 //   compact  key > T is taken; key == T is taken for the first need_eq such keys in index
 //            order.  Output position = (#taken-above before it) + min(#equal before it,
 //            need_eq), from wave ballots and per-(wave, chunk) totals (the key == T ballots
@@ -41,6 +39,21 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = min(v, (uint32_t)__shfl_xor(v, m, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)__shfl_xor(v, m, 64));
+  return v;
+}
 __device__ __forceinline__ uint32_t wave_scan_incl_u(uint32_t v, int lane) {
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -60,7 +73,7 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
             int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio, int64_t index_offset) {
   constexpr int kSeg = kThreads * 4 * kR;
   __shared__ uint32_t hist[kBins];
-  __shared__ uint32_t red[kWaves];  // per-wave totals of the histogram scan
+  __shared__ uint32_t red[3][kWaves];
   __shared__ uint32_t tot[2][kR][kWaves];  // per-(chunk, wave) counts of key > T and key == T
   __shared__ uint32_t sh_bin[3];
 
@@ -124,96 +137,120 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
     return;
   }
 
-  if (kSingle) load_seg(0);  // (the whole row: its keys stay in registers for every pass)
-
-  // ---- threshold: take key > T, and key == T for the first need_eq in index order ----
+  // ---- a row with at most k valid positions: every candidate, no pass ----
   uint32_t T = 0u, need_eq = 0u;  // (T = 0, need_eq = 0: every candidate, key > 0)
-  if (nv > k) {
-    int sh = 32;  // the current bin is keys in [lo, lo + 2^sh)
-    uint32_t lo = 0u, rem = (uint32_t)k;
-    bool whole_bin = false, all_fit = false;
-    while (sh > 0) {
-      const int nsh = max(sh - kDigitBits, 0);
-      const int nb = 1 << (sh - nsh);
-      for (int i = t; i < nb; i += kThreads) hist[i] = 0u;
-      __syncthreads();
-      // a key is in the bin iff key - lo <= span in 32-bit arithmetic: after the first pass
-      // (lo >= 2^21) keys below the bin, key 0 included, wrap to at least 2^32 - lo, which the
-      // span never reaches once it is clamped to 2^32 - 1 - lo; the clamp drops no candidate
-      // (candidate keys are at most order_key(+inf) = 0xff800000).  The first pass counts
-      // every key of the live chunks, key 0 in bin 0.
-      const uint32_t base_key = lo;
-      const uint32_t span = min(sh >= 32 ? 0xffffffffu : (1u << sh) - 1u, 0xffffffffu - base_key);
-      for (int sg = 0; sg < nseg; ++sg) {
-        if (!kSingle) load_seg(sg);
+  if (nv <= k) {
+    if (kSingle) load_seg(0);
+  } else {
+    // ---- pass 0: candidates, min and max key ----
+    uint32_t cnt = 0, kmin = 0xffffffffu, kmax = 0u;
+    for (int sg = 0; sg < nseg; ++sg) {
+      load_seg(sg);
 #pragma unroll
-        for (int j = 0; j < kR; ++j) {
-          if (!live(sg, j)) continue;
+      for (int j = 0; j < kR; ++j) {
+        if (!live(sg, j)) continue;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t d = key[j][e] - base_key;
-            if (d <= span) atomicAdd(&hist[d >> nsh], 1u);
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t kv = key[j][e];
+          cnt += kv != 0u;
+          kmin = min(kmin, kv ? kv : 0xffffffffu);
+          kmax = max(kmax, kv);
+        }
+      }
+    }
+    cnt = wave_sum_u(cnt);
+    kmin = wave_min_u(kmin);
+    kmax = wave_max_u(kmax);
+    if (lane == 0) {
+      red[0][wave] = cnt;
+      red[1][wave] = kmin;
+      red[2][wave] = kmax;
+    }
+    __syncthreads();
+    uint32_t n_cand = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      n_cand += red[0][w];
+      kmin = min(kmin, red[1][w]);
+      kmax = max(kmax, red[2][w]);
+    }
+
+    // ---- threshold: take key > T, and key == T for the first need_eq in index order ----
+    if (n_cand > (uint32_t)k) {
+      const uint32_t range = kmax - kmin;
+      int sh = range ? 32 - __clz(range) : 0;  // the current bin is rel = key - kmin in [lo, lo + 2^sh)
+      uint32_t lo = 0u, rem = (uint32_t)k;
+      bool whole_bin = false;
+      while (sh > 0) {
+        const int nsh = max(sh - kDigitBits, 0);
+        const int nb = 1 << (sh - nsh);
+        for (int i = t; i < nb; i += kThreads) hist[i] = 0u;
+        __syncthreads();
+        // a candidate is in the bin iff key - (kmin + lo) <= span in 32-bit arithmetic: keys
+        // below the bin, key 0 (not a candidate) included, wrap to at least 2^32 - (kmin + lo),
+        // which the span never reaches once it is clamped to 2^32 - 1 - (kmin + lo); the clamp
+        // drops no candidate (candidate keys are at most order_key(+inf) = 0xff800000)
+        const uint32_t base_key = kmin + lo;
+        const uint32_t span = min(sh >= 32 ? 0xffffffffu : (1u << sh) - 1u, 0xffffffffu - base_key);
+        for (int sg = 0; sg < nseg; ++sg) {
+          if (!kSingle) load_seg(sg);
+#pragma unroll
+          for (int j = 0; j < kR; ++j) {
+            if (!live(sg, j)) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t d = key[j][e] - base_key;
+              if (d <= span) atomicAdd(&hist[d >> nsh], 1u);
+            }
           }
         }
-      }
-      __syncthreads();
-      // thread t sums bins [nb - 8(t+1), nb - 8t) (from the top); exclusive scan in thread
-      // order = keys in bins above its range
-      const int hi = nb - kBinsPerThread * t;
-      uint32_t c[kBinsPerThread], my = 0;
-#pragma unroll
-      for (int i = 0; i < kBinsPerThread; ++i) {
-        const int bin = hi - 1 - i;
-        c[i] = bin >= 0 ? hist[bin] : 0u;
-        my += c[i];
-      }
-      const uint32_t incl = wave_scan_incl_u(my, lane);
-      if (lane == 63) red[wave] = incl;
-      __syncthreads();
-      uint32_t above = incl - my;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w)
-        if (w < wave) above += red[w];
-      if (sh == 32) {  // first pass: candidates = every key counted but those in bin 0
-        uint32_t total = 0;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) total += red[w];
-        if (total - hist[0] <= (uint32_t)k) {  // (workgroup-uniform)
-          all_fit = true;
-          break;
-        }
-      }
-      if (above < rem && rem <= above + my) {  // exactly one thread
+        __syncthreads();
+        // thread t sums bins [nb - 8(t+1), nb - 8t) (from the top); exclusive scan in thread
+        // order = keys in bins above its range
+        const int hi = nb - kBinsPerThread * t;
+        uint32_t c[kBinsPerThread], my = 0;
 #pragma unroll
         for (int i = 0; i < kBinsPerThread; ++i) {
-          if (above < rem && rem <= above + c[i]) {
-            sh_bin[0] = (uint32_t)(hi - 1 - i);
-            sh_bin[1] = above;
-            sh_bin[2] = c[i];
-          }
-          above += c[i];
+          const int bin = hi - 1 - i;
+          c[i] = bin >= 0 ? hist[bin] : 0u;
+          my += c[i];
         }
+        const uint32_t incl = wave_scan_incl_u(my, lane);
+        if (lane == 63) red[0][wave] = incl;
+        __syncthreads();
+        uint32_t above = incl - my;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+          if (w < wave) above += red[0][w];
+        if (above < rem && rem <= above + my) {  // exactly one thread
+#pragma unroll
+          for (int i = 0; i < kBinsPerThread; ++i) {
+            if (above < rem && rem <= above + c[i]) {
+              sh_bin[0] = (uint32_t)(hi - 1 - i);
+              sh_bin[1] = above;
+              sh_bin[2] = c[i];
+            }
+            above += c[i];
+          }
+        }
+        __syncthreads();
+        const uint32_t bin = sh_bin[0], n_above = sh_bin[1], n_bin = sh_bin[2];
+        lo += bin << nsh;
+        rem -= n_above;
+        sh = nsh;
+        if (n_bin == rem) {
+          whole_bin = true;
+          break;
+        }
+        __syncthreads();  // sh_bin and red are rewritten by the next pass
       }
-      __syncthreads();
-      const uint32_t bin = sh_bin[0], n_above = sh_bin[1], n_bin = sh_bin[2];
-      lo += bin << nsh;
-      rem -= n_above;
-      sh = nsh;
-      if (n_bin == rem) {
-        whole_bin = true;
-        break;
+      if (whole_bin) {
+        T = kmin + lo - 1u;  // lo >= 1 here: lo == 0 would take every candidate (n_cand == k)
+        need_eq = 0u;
+      } else {
+        T = kmin + lo;
+        need_eq = rem;
       }
-      __syncthreads();  // sh_bin and red are rewritten by the next pass
-    }
-    if (all_fit) {
-      T = 0u;
-      need_eq = 0u;
-    } else if (whole_bin) {
-      T = lo - 1u;  // lo >= 2^21 here (the k-th largest candidate is above bin 0)
-      need_eq = 0u;
-    } else {
-      T = lo;
-      need_eq = rem;
     }
   }
 
