@@ -131,49 +131,104 @@ def test_npu_dsa_converter_skips_other_models():
     assert not hasattr(model.layers["0"].attention.inner_attention, "layer_number")
 
 
-def test_dsa_forward_plumbing_and_loss_deferral():
-    B, H, S, K, HI, DI = 1, 4, 8, 4, 2, 16
+def _dsa_case(B=1, H=4, S=8, HI=2, DI=16):
     self_ = SimpleNamespace(config=SimpleNamespace(kv_lora_rank=512, qk_rope_head_dim=64), layer_number=0,
                             num_layers=1, compute_dsa_indexer_loss=dsa_mod.SparseLightningIndexerKLLoss())
     q = torch.randn(B, H, S, 576)
     kv = torch.randn(B, 1, S, 576)
-    v = kv[..., :512]
     qi, ki, w = torch.randn(B, S, HI, DI, requires_grad=True), torch.randn(B, S, 1, DI), torch.rand(B, S, HI)
+    return self_, q, kv, qi, ki, w
+
+
+class _FakeLinkedAttention(torch.autograd.Function):
+    """Stands in for the linked attention op: its backward hands a mass to the link."""
+
+    @staticmethod
+    def forward(ctx, q_nope, after, link, mass):
+        ctx.link, ctx.mass = link, mass
+        link.fwd = ("q", "kv", "idx", "smax", "ssum", 0.1, 0)
+        return q_nope.new_zeros(q_nope.shape)
+
+    @staticmethod
+    def backward(ctx, dout):
+        ctx.link.mass = ctx.mass
+        return dout, torch.zeros(()), None, None
+
+
+def test_dsa_forward_plumbing_and_loss_deferral():
+    B, H, S, K, HI, DI = 1, 4, 8, 4, 2, 16
+    self_, q, kv, qi, ki, w = _dsa_case(B, H, S, HI, DI)
     seen = {}
 
     def fake_li(q_, k_, w_, **kw):
         seen["li"] = kw
         return torch.zeros(B, S, 1, K, dtype=torch.int32), None
 
-    def fake_sfa(q_nope, k_nope, v_, **kw):
-        seen["sfa"] = dict(q_nope=q_nope, k_nope=k_nope, **kw)
+    def fake_sfa(q_, k_, idx, scale, after, link, d_v=512):
+        seen["sfa"] = dict(q=q_, k=k_, idx=idx, scale=scale, d_v=d_v)
+        link.fwd = ("q", "kv", "idx", "smax", "ssum", scale, 0)
         return torch.zeros(B, S, H, 512), torch.zeros(B, S, H), torch.ones(B, S, H)
 
     with patch.object(dsa_mod.npu, "npu_lightning_indexer", side_effect=fake_li), \
-            patch.object(dsa_mod.npu, "npu_sparse_flash_attention", side_effect=fake_sfa):
-        loss, out = dsa_mod.dsa_forward(self_, q, kv, v, None, 0.1, qi, ki, w, None, K)
+            patch.object(dsa_mod.npu, "sparse_flash_attention_linked", side_effect=fake_sfa):
+        loss, out = dsa_mod.dsa_forward(self_, q, kv, kv[..., :512], None, 0.1, qi, ki, w, None, K)
     assert seen["li"]["sparse_count"] == K and seen["li"]["sparse_mode"] == 3
     s = seen["sfa"]
-    assert s["q_nope"].shape == (B, S, H, 512) and s["query_rope"].shape == (B, S, H, 64)
-    assert s["key_rope"].shape == (B, S, 1, 64) and s["sparse_indices"].dtype == torch.int32
-    assert s["attention_mode"] == 2 and s["sparse_mode"] == 3 and s["scale_value"] == 0.1
+    assert s["q"].shape == (B, S, H, 576) and s["k"].shape == (B, S, 1, 576) and s["d_v"] == 512
+    assert s["idx"].shape == (B, S, 1, K) and s["scale"] == 0.1
     assert out.shape == (B, H, S, 512)
-    assert float(loss) == 0.0  # deferred to backward
+    assert float(loss.detach()) == 0.0  # deferred to backward
 
-    # backward runs the fused KL op with the upstream grad as its grad_scale (a tensor, so the
-    # op scales on the device without a host round trip) and logs loss/(B*S)
-    def fake_kl(*a, **kw):
-        g = kw["grad_scale"]
-        seen["grad_scale"] = g
-        return torch.ones(B, S, HI, DI) * g, torch.ones(B, S, 1, DI) * g, torch.ones(B, S, HI) * g, torch.tensor([8.0])
+    # backward of the loss alone: the attention node is not on the path, so the loss
+    # recomputes the mass from the forward statistics; the upstream grad scales the KL
+    # gradients as a tensor (no host round trip) and loss/(B*S) is logged
+    def fake_mass(q_, kv_, idx_, smax_, ssum_, scale_, *, q_offset=0):
+        seen["mass_args"] = (q_, kv_, idx_, smax_, ssum_, scale_, q_offset)
+        return torch.rand(B, S, K)
+
+    def fake_kl(qi_, ki_, w_, idx_, mass_, *, q_offset=0, loss_scale=1.0, eps=1e-8, grad_scale=1.0):
+        seen["grad_scale"] = grad_scale
+        g = grad_scale
+        return (torch.ones(B, S, HI, DI) * g, torch.ones(B, S, DI) * g, torch.ones(B, S, HI) * g,
+                torch.full((B, S), 1.0))
 
     DSAIndexerLossLoggingHelper.tracker.clear()
-    with patch.object(dsa_mod.npu, "npu_sparse_lightning_indexer_grad_kl_loss", side_effect=fake_kl):
+    with patch.object(dsa_mod.npu, "attn_mass", side_effect=fake_mass), \
+            patch.object(dsa_mod.npu, "indexer_kl_grad_from_mass", side_effect=fake_kl):
         (loss * 3.0).backward()
-    # d(loss/(B*S))/d(LILossTrain) = 1/(B*S), times 3
+    assert seen["mass_args"][:5] == ("q", "kv", "idx", "smax", "ssum")
+    # d(loss/(B*S))/d(z) = 1/(B*S), times 3
     torch.testing.assert_close(qi.grad, torch.full_like(qi, 3.0 / (B * S)))
     assert isinstance(seen["grad_scale"], torch.Tensor)
-    assert DSAIndexerLossLoggingHelper.tracker["values"][0].item() == pytest.approx(8.0 / (B * S))
+    assert DSAIndexerLossLoggingHelper.tracker["values"][0].item() == pytest.approx(S / (B * S))
+
+
+def test_dsa_loss_backward_waits_for_the_attention_mass():
+    """The loss's output is an input of the attention op, so in a backward through both the
+    attention backward runs first and its mass reaches the loss (no recompute)."""
+    B, H, S, K, HI, DI = 1, 4, 8, 4, 2, 16
+    self_, q, kv, qi, ki, w = _dsa_case(B, H, S, HI, DI)
+    mass = torch.rand(B, S, K)
+    seen = {}
+
+    def fake_li(q_, k_, w_, **kw):
+        return torch.zeros(B, S, 1, K, dtype=torch.int32), None
+
+    def fake_sfa(q_, k_, idx, scale, after, link, d_v=512):
+        out = _FakeLinkedAttention.apply(q_[..., :d_v].detach().requires_grad_(True), after, link, mass)
+        return out, None, None
+
+    def fake_kl(qi_, ki_, w_, idx_, mass_, **kw):
+        seen["mass"] = mass_
+        return torch.zeros(B, S, HI, DI), torch.zeros(B, S, DI), torch.zeros(B, S, HI), torch.zeros(B, S)
+
+    with patch.object(dsa_mod.npu, "npu_lightning_indexer", side_effect=fake_li), \
+            patch.object(dsa_mod.npu, "sparse_flash_attention_linked", side_effect=fake_sfa):
+        loss, out = dsa_mod.dsa_forward(self_, q, kv, kv[..., :512], None, 0.1, qi, ki, w, None, K)
+    with patch.object(dsa_mod.npu, "attn_mass", side_effect=AssertionError("mass recomputed")), \
+            patch.object(dsa_mod.npu, "indexer_kl_grad_from_mass", side_effect=fake_kl):
+        (out.sum() + loss).backward()
+    assert seen["mass"] is mass
 
 
 def test_dsa_forward_rejects_multi_kv_heads():

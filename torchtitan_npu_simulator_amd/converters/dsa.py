@@ -7,6 +7,13 @@ Drop-in for the reference's converters/kernels/dsa.py:
   indexer gradients in backward, scaled by the incoming gradient; the token-sum loss
   divided by B*S goes to the logging tracker.
 * ``SparseLightningIndexerKLLoss`` (dsa.py:22-73) returns ``LILossTrain(...) / (B*S)``.
+
+Inside ``dsa_forward`` the installed loss module is run through ``_LinkedIndexerLoss``, the
+same deferred loss whose backward takes the main-attention mass from the layer's attention
+backward (fused into dsa_sparse_mla_bwd) instead of recomputing it from the softmax
+statistics: the loss node's zero output is an input of the attention op, so autograd runs
+the attention backward first.  Called on its own, the module keeps the reference's
+interface and recomputes the mass.
 * ``NpuDSAConverter`` / ``DSAModelConfig`` registered as ``"npu_dsa"`` (dsa.py:283-309).
 """
 
@@ -67,6 +74,42 @@ class LILossTrain(torch.autograd.Function):
                 *([None] * 14))
 
 
+class _LinkedIndexerLoss(torch.autograd.Function):
+    """LILossTrain for a layer's own attention (BSND, sparse_mode 3): zero in forward; in
+    backward the KL loss and the indexer gradients, scaled by the upstream gradient, with the
+    target mass from ``link`` (set by the attention backward; recomputed from the saved
+    forward statistics only if that backward has not run)."""
+
+    @staticmethod
+    def forward(ctx, query_indexer, key_indexer, weights, sparse_indices, link, layer_number, num_layers):
+        ctx.save_for_backward(query_indexer, key_indexer, weights, sparse_indices)
+        ctx.link = link
+        ctx.layer_number = layer_number
+        ctx.num_layers = num_layers
+        return torch.zeros((), dtype=torch.float32, device=query_indexer.device)
+
+    @staticmethod
+    def backward(ctx, grad):
+        query_indexer, key_indexer, weights, sparse_indices = ctx.saved_tensors
+        link = ctx.link
+        q, kv3, idx, smax, ssum, scale, q_off = link.fwd
+        mass = link.mass
+        if mass is None:  # (a backward of the loss alone: the attention node did not run)
+            mass = npu.attn_mass(q, kv3, idx, smax, ssum, scale, q_offset=q_off)
+        link.mass = None
+        link.fwd = None
+        ctx.link = None
+        g = grad if isinstance(grad, torch.Tensor) else float(grad)
+        dq_i, dk_i, dw, loss_rows = npu.indexer_kl_grad_from_mass(query_indexer, key_indexer, weights, idx, mass,
+                                                                  q_offset=q_off, loss_scale=1.0, eps=1e-8,
+                                                                  grad_scale=g)
+        bsz, sq = query_indexer.shape[0], query_indexer.shape[1]
+        DSAIndexerLossLoggingHelper.save_loss_to_tracker(loss_rows.sum() / (bsz * sq), ctx.layer_number,
+                                                         ctx.num_layers)
+        return (dq_i.to(query_indexer.dtype), dk_i.reshape(key_indexer.shape).to(key_indexer.dtype),
+                dw.to(weights.dtype), None, None, None, None)
+
+
 class SparseLightningIndexerKLLoss(torch.nn.Module):
     """Indexer KL loss module installed as ``inner_attention.compute_dsa_indexer_loss``."""
 
@@ -93,6 +136,17 @@ def dsa_forward(self, q, k, v, attn_mask=None, scale=None, q_indexer=None, k_ind
     k = k.transpose(1, 2)
     v = v.transpose(1, 2)
     nope, rope = self.config.kv_lora_rank, self.config.qk_rope_head_dim
+    if type(self.compute_dsa_indexer_loss) is SparseLightningIndexerKLLoss:
+        # the loss first (zero, deferred), then the attention with the loss's output as an
+        # input: its backward runs before the loss's and hands over the attention mass.  The
+        # attention takes the whole [nope | rope] rows (v = the first kv_lora_rank columns of
+        # k, the absorb-mode alias), so no split / re-concatenation is made either way.
+        bsz, sq = q.shape[0], q.shape[1]
+        link = npu.MassLink()
+        z = _LinkedIndexerLoss.apply(q_indexer, k_indexer, weights, topk_indices.to(torch.int32), link,
+                                     self.layer_number, self.num_layers)
+        output, _, _ = npu.sparse_flash_attention_linked(q, k, topk_indices, scale, z, link, d_v=nope)
+        return z / (bsz * sq), output.transpose(1, 2)
     q_nope, q_pe = torch.split(q, [nope, rope], dim=-1)
     k_nope, k_pe = torch.split(k, [nope, rope], dim=-1)
     output, softmax_max, softmax_sum = npu.npu_sparse_flash_attention(

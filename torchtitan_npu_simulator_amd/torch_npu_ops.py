@@ -600,6 +600,62 @@ class _SparseFlashAttention(torch.autograd.Function):
         return dq[..., :dnope], dkv[..., :dnope], dq[..., dnope:], dkv[..., dnope:], None, None, None
 
 
+class MassLink:
+    """Hands the head-summed attention mass [B,S,K] from a layer's attention backward to the
+    same layer's indexer-loss backward, so the loss's target is not recomputed.  ``fwd``
+    keeps what a recompute would need (q, kv, indices, softmax_max, softmax_sum, scale,
+    q_offset) for a backward in which the attention node does not run first."""
+
+    __slots__ = ("mass", "fwd")
+
+    def __init__(self):
+        self.mass = None
+        self.fwd = None
+
+
+class _SparseFlashAttentionLinked(torch.autograd.Function):
+    """Absorb-mode attention on whole 576-column rows (query [B,S,H,576], key [B,S_kv,1,576],
+    any strides: each becomes one contiguous copy at most, no split and re-concatenation)
+    whose backward also produces the attention mass (the fused output of
+    dsa_sparse_mla_bwd) into ``link``.  ``after`` is the indexer loss's (zero) output: as an
+    input here it makes the loss node's backward wait for this one."""
+
+    @staticmethod
+    def forward(ctx, query, key, indices, scale, q_offset, d_v, after, link):
+        q = query.contiguous()
+        kv3 = key.reshape(key.shape[0], key.shape[1], key.shape[-1]).contiguous()
+        out, smax, ssum = sparse_mla_fwd(q, kv3, indices, scale, d_v=d_v, q_offset=q_offset)
+        ctx.save_for_backward(q, kv3, indices, out, smax, ssum)
+        ctx.scale = scale
+        ctx.q_offset = q_offset
+        ctx.kv_shape = key.shape
+        ctx.link = link
+        link.fwd = (q, kv3, indices, smax, ssum, scale, q_offset)
+        ctx.mark_non_differentiable(smax, ssum)
+        return out, smax, ssum
+
+    @staticmethod
+    def backward(ctx, dout, _dmax, _dsum):
+        q, kv3, indices, out, smax, ssum = ctx.saved_tensors
+        dq, dkv, mass = sparse_mla_bwd(q, kv3, indices, out, dout.contiguous(), smax, ssum, ctx.scale,
+                                       q_offset=ctx.q_offset, return_mass=True)
+        ctx.link.mass = mass
+        ctx.link = None
+        return dq, dkv.to(kv3.dtype).reshape(ctx.kv_shape), None, None, None, None, None, None
+
+
+def sparse_flash_attention_linked(query, key, sparse_indices, scale_value, after, link, *, d_v=512, sparse_mode=3):
+    """Absorb-mode sparse attention (``npu_sparse_flash_attention`` semantics, BSND) on whole
+    rows - query [B,S,H,576] = [q_nope | q_pe], key [B,S_kv,1,576] = [k_nope | k_pe], the value
+    being the first ``d_v`` columns of the key - for a layer whose indexer loss takes its
+    target from this attention's backward: returns (out [B,S,H,d_v], softmax_max,
+    softmax_sum) and, in backward, leaves the head-summed mass [B,S,K] in ``link.mass`` (a
+    ``MassLink``).  ``after`` is the loss's output tensor (see _SparseFlashAttentionLinked)."""
+    q_off = _resolve_q_offset(sparse_mode, query.shape[1], key.shape[1], None)
+    idx = sparse_indices.reshape(query.shape[0], query.shape[1], -1).to(torch.int32).contiguous()
+    return _SparseFlashAttentionLinked.apply(query, key, idx, float(scale_value), q_off, int(d_v), after, link)
+
+
 class _SparseFlashAttentionTND(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q_nope, k_nope, q_pe, k_pe, indices, scale, cu_q, cu_k):
