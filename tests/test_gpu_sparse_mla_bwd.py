@@ -158,9 +158,19 @@ def test_bwd_fp32_parity():
     assert rel_err(dq, adq) <= 1e-5 and rel_err(dkv, adkv) <= 1e-5
 
 
-@pytest.mark.parametrize("S,H,K,q_offset", [(200, 128, 128, 0), (64, 16, 32, 16), (80, 128, 40, 0)])
-def test_attn_mass_parity(S, H, K, q_offset):
-    q, kv, _, scale = attn_inputs(S, H, q_offset=q_offset, seed=10)
+@pytest.mark.parametrize(
+    "S,H,K,q_offset,d_qk",
+    [
+        (200, 128, 128, 0, 576),
+        (64, 16, 32, 16, 576),  # one partial head group, CP shard offset
+        (80, 128, 40, 0, 576),  # top-k not a multiple of the 32-slot block
+        (64, 160, 96, 0, 576),  # two head groups adding into one row
+        (96, 72, 40, 8, 512),  # rope-less 512-column rows (DeepSeek-V4)
+        (48, 128, 2048, 2200, 576),  # 64 blocks per row, most slots usable
+    ],
+)
+def test_attn_mass_parity(S, H, K, q_offset, d_qk):
+    q, kv, _, scale = attn_inputs(S, H, q_offset=q_offset, seed=10, d_qk=d_qk)
     idx = rand_indices(S, K, q_offset=q_offset, seed=10, holes=0.1)
     ops = _ops()
     out, smax, ssum = ops.sparse_mla_fwd(q.to(DEV), kv.to(DEV), idx.to(DEV), scale, q_offset=q_offset)

@@ -28,25 +28,13 @@ namespace {
 
 constexpr int kDqk = 576;
 constexpr int kDv = 512;
-constexpr int kRowChunks = kDqk / 8;           // 16-byte chunks per KV row (72)
-constexpr int kRowBytes = kRowChunks * 16;     // 1152
 constexpr int kBN = 32;                        // keys per block
-constexpr int kTileChunks = kBN * kRowChunks;  // 2304
-constexpr int kTileBytes = kTileChunks * 16;   // 36864
 constexpr float kHeadroom = 64.0f;             // log2 units of P above the reference max
 constexpr int kFwdWaves = 4;
 constexpr int kFwdThreads = kFwdWaves * 64;
 constexpr int kFwdHeads = 32 * kFwdWaves;      // heads per workgroup
-constexpr int kKSteps = kDqk / 16;             // 36 MFMA k-steps of 16 columns (32x32x16)
 constexpr int kLatSteps = kDv / 16;            // 32 latent k-steps (Q in registers)
-// mass kernel (8 waves: 4 head groups x 2 contraction halves, 32x32x16 tiles)
-constexpr int kWaves = 8;
-constexpr int kThreads = kWaves * 64;
-constexpr int kHeadsPerWG = 128;
-constexpr int kHalfSteps = 16;                 // latent MFMA steps per contraction half
 
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 
 template <int kD>  // row width of Q and KV: 576 (latent + rope) or 512 (no rope)
@@ -366,176 +354,197 @@ sparse_mla_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __res
 
 // Head-summed softmax mass at the selected slots (target of the indexer KL loss):
 //   mass[s, j] = sum_h exp2(S[h, j] * scale * log2e - lse2[h]),  lse2 from softmax_max/sum.
-// Same token-per-workgroup gather as the forward, 8 waves (4 head groups x 2 contraction
-// halves exchanging partial S through LDS); each wave sums P over its 32 heads with a
-// 5-step butterfly (16 shuffles), the four head groups are added in LDS and one 128-byte
-// row segment is stored per block.
-__global__ void __launch_bounds__(kThreads, 1)
+// The forward's gather and QK pipeline without its PV half: one workgroup = one token x
+// up to 128 heads on 4 waves (32 heads each, v_mfma_f32_32x32x16_bf16); S^T of block blk
+// on tile blk & 1 while block blk+1's rows are DMA'd into the other tile (two tiles
+// suffice: a block is not read after its QK).  The whole Q row of the wave's heads
+// (latent and rope) stays in VGPRs, so the LDS holds little more than the two tiles and
+// two workgroups share a CU.  Each wave sums P over its 32 heads (permlane16 swap, then
+// DPP exchanges), the four waves' sums meet in LDS behind the block's barrier, and wave 0
+// stores the block's 128-byte row segment at the start of the next iteration.
+template <int kD>  // row width of Q and KV: 576 (latent + rope) or 512 (no rope)
+__global__ void __launch_bounds__(kFwdThreads, 2)
 attn_mass_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv,
                       const int32_t* __restrict__ idx, const float* __restrict__ smax, const float* __restrict__ ssum,
                       float* __restrict__ mass, int S, int s_kv, int H, int K, float scale_log2, int64_t q_offset) {
-  __shared__ u32x4 tile[3][kTileChunks];
-  __shared__ u32x4 qpe[kHeadsPerWG][(kDqk - kDv) / 8];
-  __shared__ f32x4 xs[kWaves][4][64];
-  using Gather = RowGather<kWaves>;
-  __shared__ float macc[2][kBN];
-  __shared__ uint32_t vmask[3];
+  using Gather = RowGather<kFwdWaves, kD>;
+  using Geo = GatherGeomT<kD>;
+  constexpr int kPer = Gather::kMaxPerWave;
+  constexpr int kTC = Geo::kTileChunks, kRB = Geo::kRowBytes;
+  constexpr int kKS = kD / 16;  // MFMA k-steps of S^T (36 | 32)
+  __shared__ u32x4 tile[2][kTC];
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
-  __shared__ int last_slot;
+  __shared__ float part[2][kFwdWaves][kBN];  // [block parity][wave][key]: per-wave head sums
+  __shared__ int sh_last;
 
   const int tok = blockIdx.x, b = blockIdx.z, tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, n = lane & 31, hh = lane >> 5;
-  const int grp = wave & 3, half = wave >> 2;
-  const int head = blockIdx.y * kHeadsPerWG + grp * 32 + n;
-  const bool head_ok = head < H;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int n = lane & 31, h = lane >> 5;  // MFMA column (head / key row) and k half
+  const int head = blockIdx.y * kFwdHeads + wave * 32 + n;
+  const bool hok = head < H;
   const int64_t row_id = (int64_t)b * S + tok;
+  const int64_t hrow = row_id * H + (hok ? head : 0);
   const int32_t* ridx = idx + row_id * K;
-  const int64_t limit = tok + q_offset;
-  const uint32_t lim = gather_limit(limit, s_kv);
-  const uint16_t* kvb = kv + (int64_t)b * s_kv * kDqk;
-  const int64_t hrow = row_id * H + (head_ok ? head : 0);
   float* mrow = mass + row_id * K;
+  const int64_t limit = tok + q_offset;
+  const uint16_t* kvb = kv + (int64_t)b * s_kv * kD;
 
-  if (tid == 0) last_slot = -1;
-  if (tid < 2 * kBN) macc[tid / kBN][tid % kBN] = 0.f;
-  __syncthreads();
-  {
-    int last = -1;
-    for (int j = tid; j < K; j += kThreads)
-      if (slot_ok(ridx[j], s_kv, limit)) last = j;
-    if (last >= 0) atomicMax(&last_slot, last);
+  // the row's slot indices (block count), the ring entries of blocks 0..2 (wave 0, DMA),
+  // the head's Q row and row statistics are requested together (unconditional loads from
+  // head 0's row for absent heads, whose lse2 is then +inf)
+  int vidx[kIdxU];
+  load_row_indices(ridx, K, vidx);
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);  // clamped to slot K-1
   }
-  __syncthreads();
-  const int nblk = (last_slot + kBN) / kBN;
-  if (blockIdx.y == 0)  // slots past the last usable block are zero
-    for (int j = nblk * kBN + tid; j < K; j += kThreads) mrow[j] = 0.f;
-  if (nblk == 0) return;
+  u32x4 qb[kKS];  // qb[s] = q[16s + 8h .. +8] of head `head`: B operand of k-step s
+  {
+    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kD);
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) qb[s] = qh[2 * s + h];
+  }
+  const float mx = smax[hrow], sm = ssum[hrow];
+  const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
+  if (blockIdx.y == 0)  // slots past the last usable block hold no mass
+    for (int j = nblk * kBN + tid; j < K; j += kFwdThreads) mrow[j] = 0.f;
+  if (nblk == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring DMA has landed before the LDS is released
+    return;
+  }
+  const uint32_t lim = gather_limit(limit, s_kv);
+  const float lse2 = (hok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0
+#pragma unroll
+  for (int s = 0; s < kKS; ++s) asm volatile("" : "+v"(qb[s]));  // landed before any DMA
 
-  float lse2;
-  {
-    const float sm = head_ok ? ssum[hrow] : 0.f;
-    lse2 = sm > 0.f ? (smax[hrow] + logf(sm)) * kLog2e : INFINITY;
-  }
-  u32x4 qr[kHalfSteps];
-  {
-    const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kDqk);
+  // A operand of k-step s: key row n, chunk (2s + h) ^ swz_kv(n) = ka_off[s % 4] + 128 (s / 4)
+  uint32_t ka_off[4];
 #pragma unroll
-    for (int c = 0; c < kHalfSteps; ++c)
-      qr[c] = head_ok ? qh[32 * half + 2 * c + hh] : (u32x4){0u, 0u, 0u, 0u};
-    if (half == 0) {
+  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRB + 16 * ((2 * s0 + h) ^ swz_kv(n));
+
+  const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
+  if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
+  __syncthreads();
+  uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int ch = 2 * c + hh;
-        qpe[grp * 32 + n][ch ^ (n & 7)] = head_ok ? qh[2 * (kDv / 16) + ch] : (u32x4){0u, 0u, 0u, 0u};
+  for (int i = 0; i < kPer; ++i) Gather::issue_slot(kvb, &tile[0][0], i, wave, Gather::ring_slot(sidx[0], i, gl), gl, lim, K);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  constexpr int kQBatch = 4;           // k-steps per QK batch
+  constexpr int kQB = kKS / kQBatch;   // 9 | 8 QK batches
+  static_assert(kQB >= kPer, "one row DMA per QK batch");
+
+  // S^T[32 keys x 32 heads] of one block, with the next block's rows DMA'd one
+  // instruction per batch (the forward's schedule); returns the next block's validity bits
+  auto qk = [&](const lds_char* tb, u32x4* dst_tile, const int* ring, int rows_left, f32x16& sacc)
+      __attribute__((always_inline)) {
+    const uint32_t vm_n = Gather::ring_valid(ring, lane, lim, rows_left);
+    uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
+    sacc = (f32x16){0.f};
+    u32x4 a[2][kQBatch];
+    auto read_a = [&](u32x4 (&dst)[kQBatch], int sb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < kQBatch; ++u) dst[u] = lds_read16(tb + ka_off[u] + 128 * (sb / kQBatch));
+    };
+    read_a(a[0], 0);
+    static_for<kQB>([&](auto nbc) {
+      constexpr int nb = decltype(nbc)::value;
+      if constexpr (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
+      if constexpr (nb < kPer) {
+        const uint32_t raw = raw_next;
+        if constexpr (nb + 1 < kPer) raw_next = Gather::ring_slot(ring, nb + 1, gl);
+        Gather::issue_slot(kvb, dst_tile, nb, wave, raw, gl, lim, rows_left);
       }
+#pragma unroll
+      for (int u = 0; u < kQBatch; ++u)
+        sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(qb[nb * kQBatch + u]), sacc);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);  // VALU / SALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x006, 6, 0);
+      __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // the row DMA
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    return vm_n;
+  };
+
+  // P of one block summed over the wave's 32 heads into part[pb][wave][*].  Lane holds keys
+  // 8j + 4h + i (value 4j + i) of head `head`; butterfly over the 32 head lanes: lane bits
+  // 4..1 halve the 16 values (bit 4 by one permlane16 swap, bits 3..1 by DPP), bit 0
+  // completes the sum, and lane l ends with value (l >> 1) & 15.  The halves are chosen by
+  // bit masks (a select between two array elements would become an indexed read).
+  auto block_mass = [&](const f32x16& sacc, uint32_t vm, int pb) __attribute__((always_inline)) {
+    const uint32_t vmh = vm >> (4 * h);  // bit 8j + i: key 8j + 4h + i
+    float pv[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const bool ok = (vmh >> (8 * (v >> 2) + (v & 3))) & 1u;
+      pv[v] = ok ? __builtin_amdgcn_exp2f(sacc[v] * scale_log2 - lse2) : 0.f;
     }
-  }
-  const int xsw = swz_kv(n);
-  uint32_t qk_off[4];
+    const bool odd = (lane >> 4) & 1;
 #pragma unroll
-  for (int c4 = 0; c4 < 4; ++c4) qk_off[c4] = n * kRowBytes + 512 * half + 16 * ((2 * c4 + hh) ^ xsw);
-  uint32_t pe_off[2];
+    for (int j = 0; j < 8; ++j) {  // even rows keep value j, odd rows j + 8
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(pv[j]), __float_as_uint(pv[j + 8]), false, false);
+      const float even_sum = pv[j] + __uint_as_float(r[1]), odd_sum = pv[j + 8] + __uint_as_float(r[0]);
+      pv[j] = odd ? odd_sum : even_sum;
+    }
+    auto bstep = [&](auto mc, int nh) __attribute__((always_inline)) {
+      constexpr int m = decltype(mc)::value;
+      const uint32_t up = ((lane & m) != 0) ? 0xffffffffu : 0u;
 #pragma unroll
-  for (int c = 0; c < 2; ++c) pe_off[c] = n * kRowBytes + 16 * ((64 + 4 * half + 2 * c + hh) ^ xsw);
-
-  // operands landed before the first DMA (a later wait would also wait for the DMAs)
-#pragma unroll
-  for (int c = 0; c < kHalfSteps; ++c) asm volatile("" : "+v"(qr[c]));
-  asm volatile("" : "+v"(lse2));
-
-  // block `fb`'s head-summed mass -> global (one iteration after it was accumulated,
-  // before the next row DMA, so the store never holds up a tile wait); clears the slot
-  auto flush = [&](int fb) {
-    if (tid < kBN) {
-      const int slot = fb * kBN + tid;
-      if (slot < K) {
-        if (gridDim.y == 1) mrow[slot] = macc[fb & 1][tid];
-        else atomicAdd(&mrow[slot], macc[fb & 1][tid]);
+      for (int j = 0; j < nh; ++j) {
+        const uint32_t a = __float_as_uint(pv[j]), c = __float_as_uint(pv[j + nh]);
+        const float send = __uint_as_float((a & up) | (c & ~up));
+        const float keep = __uint_as_float((c & up) | (a & ~up));
+        pv[j] = keep + lane_xor<m>(send);
       }
-      macc[fb & 1][tid] = 0.f;
+    };
+    bstep(std::integral_constant<int, 8>{}, 4);
+    bstep(std::integral_constant<int, 4>{}, 2);
+    bstep(std::integral_constant<int, 2>{}, 1);
+    const float tot = pv[0] + lane_xor<1>(pv[0]);
+    if ((lane & 1) == 0) {
+      const int r = (lane >> 1) & 15;
+      part[pb][wave][8 * (r >> 2) + 4 * h + (r & 3)] = tot;
     }
   };
 
-  const typename Gather::Lanes gl = Gather::lanes(wave, lane);
-  Gather::ring_init(sidx, ridx, K, nblk, wave, lane);
-  __syncthreads();
-  Gather::issue(kvb, tile[0], &vmask[0], sidx[0], 0, K, lim, wave, lane, gl);
-  if (nblk > 1) Gather::issue(kvb, tile[1], &vmask[1], sidx[1], 1, K, lim, wave, lane, gl);
-  Gather::wait_next(nblk > 1, wave);  // block 0 landed
-  __syncthreads();
+  // block fb's four wave sums -> global (its partials were published by the barrier that
+  // ended its iteration); several head groups add into a zeroed row
+  auto flush = [&](int fb) __attribute__((always_inline)) {
+    if (wave == 0 && lane < kBN) {
+      const int pb = fb & 1;
+      const float t = (part[pb][0][lane] + part[pb][1][lane]) + (part[pb][2][lane] + part[pb][3][lane]);
+      const int slot = fb * kBN + lane;
+      if (slot < K) {
+        if (gridDim.y == 1) mrow[slot] = t;
+        else atomicAdd(&mrow[slot], t);
+      }
+    }
+  };
+
+  // iteration blk: the store of block blk-1, S^T of block blk on tile blk & 1 while block
+  // blk+1's rows are DMA'd into the other tile, then P and the head sums of block blk; the
+  // iteration ends with its DMAs landed and one barrier
   for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk % 3;
-    const bool in_flight2 = blk + 2 < nblk;
     if (blk > 0) flush(blk - 1);
     if (wave == 0 && blk + 3 < nblk)
       Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
-    if (in_flight2) {
-      const int nb = (blk + 2) % 3;
-      Gather::issue(kvb, tile[nb], &vmask[nb], sidx[(blk + 2) & (GatherGeom::kRing - 1)], blk + 2, K, lim, wave, lane, gl);
-    }
-    const lds_char* tb = lds_bytes(&tile[buf][0]);
-    // operands fetched in batches of 6 ahead of their MFMAs (sched_barrier keeps each batch
-    // together so its LDS latency overlaps the previous batch's MFMAs)
-    f32x16 s = (f32x16){0};
-#pragma unroll
-    for (int cb = 0; cb < kHalfSteps + 2; cb += 6) {
-      u32x4 a[6], bq[6];
-#pragma unroll
-      for (int u = 0; u < 6; ++u) {
-        const int c = cb + u;
-        if (c < kHalfSteps) {
-          a[u] = lds_read16(tb + qk_off[c & 3] + 128 * (c >> 2));
-          bq[u] = qr[c];
-        } else {
-          a[u] = lds_read16(tb + pe_off[c - kHalfSteps]);
-          bq[u] = qpe[grp * 32 + n][(4 * half + 2 * (c - kHalfSteps) + hh) ^ (n & 7)];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 6; ++u) s = mfma32x32x16(as_bf16x8(a[u]), as_bf16x8(bq[u]), s);
-    }
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4)
-      xs[wave][r4][lane] = (f32x4){s[4 * r4], s[4 * r4 + 1], s[4 * r4 + 2], s[4 * r4 + 3]};
+    f32x16 sacc;
+    // ring entry blk+1 landed during iteration blk-2 (or before the loop)
+    const uint32_t vm_next = qk(lds_bytes(&tile[blk & 1][0]), &tile[(blk + 1) & 1][0],
+                                sidx[(blk + 1) & (GatherGeom::kRing - 1)], K - (blk + 1) * kBN, sacc);
+    block_mass(sacc, vm_cur, blk & 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
     __syncthreads();
-    if (half == 0) {
-      const uint32_t vm = vmask[buf];
-      float v[16];
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        const f32x4 other = xs[wave ^ 4][r4][lane];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int r = 4 * r4 + u;
-          const int key = 8 * (r >> 2) + 4 * hh + (r & 3);
-          const float x = s[r] + other[u];
-          v[r] = ((vm >> key) & 1u) ? exp2f(x * scale_log2 - lse2) : 0.f;
-        }
-      }
-      // butterfly over the 32 head lanes of this half-wave: after the steps on lane bits
-      // 4,3,2,1 lane l holds the partial for value (l >> 1) & 15; bit 0 completes the sum
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int lb = 4 - st, m = 1 << lb;
-        const bool up = (lane >> lb) & 1;
-        const int nh = 8 >> st;  // values kept after this step
-#pragma unroll
-        for (int j = 0; j < nh; ++j) {
-          const float send = up ? v[j] : v[j + nh];
-          const float keep = up ? v[j + nh] : v[j];
-          v[j] = keep + __shfl_xor(send, m, 64);
-        }
-      }
-      const float tot = v[0] + __shfl_xor(v[0], 1, 64);
-      if ((lane & 1) == 0) {
-        const int r = (lane >> 1) & 15;
-        const int key = 8 * (r >> 2) + 4 * hh + (r & 3);
-        atomicAdd(&macc[blk & 1][key], tot);
-      }
-    }
-    Gather::wait_next(in_flight2, wave);  // block blk+1 (and ring entry blk+3) landed
-    __syncthreads();
+    vm_cur = vm_next;
   }
   flush(nblk - 1);
 }
@@ -677,17 +686,19 @@ extern "C" int dsa_attn_mass(const void* q, const void* kv, const int32_t* indic
     return set_error(DSA_ERR_INVALID_ARG, "dsa_attn_mass: sizes out of range");
   hipStream_t st = (hipStream_t)stream;
   if (dtype == DSA_BF16) {
-    if (d_qk != kDqk) return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: bf16 path needs d_qk=576");
-    if (s_kv > GatherGeom::kMaxRows) return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: S_kv > %lld", (long long)GatherGeom::kMaxRows);
-    const unsigned hgroups = ceil_div(n_heads, kHeadsPerWG);
+    if (d_qk != kDqk && d_qk != kDv)
+      return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: bf16 path needs d_qk = 576 or 512 (got %lld)", (long long)d_qk);
+    const int64_t max_rows = d_qk == kDqk ? GatherGeomT<kDqk>::kMaxRows : GatherGeomT<kDv>::kMaxRows;
+    if (s_kv > max_rows) return set_error(DSA_ERR_UNSUPPORTED, "dsa_attn_mass: S_kv > %lld", (long long)max_rows);
+    const unsigned hgroups = ceil_div(n_heads, kFwdHeads);
     if (hgroups > 1) {  // partial sums from several head groups accumulate into a zeroed buffer
       if (hipMemsetAsync(mass, 0, (size_t)(batch * s_q * topk) * 4, st) != hipSuccess)
         return set_error(DSA_ERR_LAUNCH, "dsa_attn_mass: memset failed");
     }
     dim3 grid((unsigned)s_q, hgroups, (unsigned)batch);
-    attn_mass_bf16_kernel<<<grid, kThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, softmax_max,
-                                                     softmax_sum, mass, (int)s_q, (int)s_kv, (int)n_heads, (int)topk,
-                                                     scale * kLog2e, q_offset);
+    auto kern = d_qk == kDqk ? attn_mass_bf16_kernel<kDqk> : attn_mass_bf16_kernel<kDv>;
+    kern<<<grid, kFwdThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, softmax_max, softmax_sum, mass,
+                                       (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
     return check_launch("dsa_attn_mass(bf16)");
   }
   if (dtype == DSA_F32) {

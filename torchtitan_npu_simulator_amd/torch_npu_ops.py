@@ -1300,7 +1300,10 @@ def v4_indexer_kl_grad(q, kv, kv_compress, attn_sink, q_indexer, k_indexer, weig
                                cmp_indices=torch.where(local < 0, local, local + kv.shape[1]))
     W = window_size
     bf16 = q.dtype == torch.bfloat16
-    dqk, dv = (576, 512) if bf16 else (D, D)
+    if bf16 and D > 512:
+        raise NotImplementedError(f"bf16 DeepSeek-V4 indexer loss needs head_dim <= 512 (got {D})")
+    # bf16: the 512-column kernels (k = v = the whole row, no rope columns); fp32: any width
+    dqk, dv = (512, 512) if bf16 else (D, D)
     q_ext = _pad_rows(q.detach(), dqk)
     kv_ext = _pad_rows(torch.cat([kv.detach(), kv_compress.detach()], dim=1), dqk)
     _, m2, s2 = sparse_mla_fwd(q_ext, kv_ext, idx, softmax_scale, d_v=dv, q_offset=_NO_MASK_OFFSET,
