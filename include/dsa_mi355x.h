@@ -247,7 +247,8 @@ int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* indice
  * Head-summed attention probability at each selected slot (reference: get_attn_scores,
  * models/deepseek_v32/model.py:285-306, gathered/zeroed at :410-413):
  *   mass[b, s, j] = sum_h exp(scale*q[b,s,h].kv[idx_j] - lse[b,s,h]),  0 for unused slots,
- * with lse = softmax_max + log(softmax_sum) from dsa_sparse_mla_fwd.
+ * with lse = softmax_max + log(softmax_sum) from dsa_sparse_mla_fwd.  bf16 needs D_qk = 576 or
+ * 512 (the rope-less DeepSeek-V4 rows); fp32 takes any D_qk.
  */
 int dsa_attn_mass(const void* q, const void* kv, const int32_t* indices, const float* softmax_max,
                   const float* softmax_sum, float* mass, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
