@@ -38,12 +38,14 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", choices=("c3", "c4", "c5", "c5-long", "v4"), default="c3",
+    p.add_argument("--workload", choices=("c3", "c3-op", "c4", "c5", "c5-long", "v4"), default="c3",
                    help="c3 (default, the headline): dense-KV step at S=8192; c4: compressed-KV step "
                         "(block compressor r=4, indexer and attention over S/4 compressed rows, S=32768); "
                         "c5: 8 packed sequences of U[1024,32768] tokens through the varlen entry points; "
                         "c5-long: one 131072-token sequence; v4: DeepSeek-V4 shared-KV attention (128-token "
-                        "window + top-1024 of the S/4 compressed rows + per-head sink, 128 heads x 512) fwd+bwd")
+                        "window + top-1024 of the S/4 compressed rows + per-head sink, 128 heads x 512) fwd+bwd; "
+                        "c3-op: the C3 layer through the torch_npu op surface (bf16 indexer, the fused indexer "
+                        "KL op recomputing its target mass)")
     p.add_argument("--seq", type=int, default=None, help="query tokens (default: 8192, or 32768 for c4, "
                                                           "131072 for c5-long)")
     p.add_argument("--heads", type=int, default=128)
@@ -193,6 +195,26 @@ def dsa_step(inp, ops, timer):
     with timer("indexer_kl_grad"):
         dq_i, dk_i, dw, loss_rows = ops.indexer_kl_grad_from_mass(inp["q_idx"], inp["k_idx"], inp["w"], idx, mass)
     return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss_rows)
+
+
+def c3_op_step(inp, ops, timer):
+    """The C3 layer through the op surface that a converter written against torch_npu calls
+    (reference converters/kernels/dsa.py:159-177, :217-253): the bf16 lightning indexer with
+    its fused top-k, the sparse attention forward and backward, and the fused indexer KL op,
+    which recomputes its target mass from the forward statistics (dsa_attn_mass) as the
+    reference's npu_sparse_lightning_indexer_grad_kl_loss does."""
+    with timer("indexer_topk"):
+        idx, _ = ops.npu_lightning_indexer(inp["q_idx"], inp["k_idx"], inp["w"], sparse_count=inp["topk"],
+                                           sparse_mode=3)
+        idx = idx[:, :, 0]
+    with timer("attn_fwd"):
+        out, smax, ssum = ops.sparse_mla_fwd(inp["q"], inp["kv"], idx, inp["scale"])
+    with timer("attn_bwd"):
+        dq, dkv = ops.sparse_mla_bwd(inp["q"], inp["kv"], idx, out, inp["dout"], smax, ssum, inp["scale"])
+    with timer("indexer_kl_grad"):
+        dq_i, dk_i, dw, loss = ops.npu_sparse_lightning_indexer_grad_kl_loss(
+            inp["q"], inp["kv"], inp["q_idx"], inp["k_idx"], inp["w"], idx, smax, ssum, inp["scale"])
+    return dict(idx=idx, out=out, dq=dq, dkv=dkv, dq_i=dq_i, dk_i=dk_i, dw=dw, loss=loss)
 
 
 def c4_step(inp, comp, comp_i, ops, timer):
@@ -357,6 +379,11 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=5
         "quantize_fp8_kernel": ("hbm", (S * h_i + s_ki) * (2 * d_i + d_i + 4), 0),
         "indexer_lin_pieces_kernel<64>": ("hbm", S * (h_i * d_i + 4 * h_i + 4 * h_i + 4 * d_i + 16), 0),
         "indexer_tile_kernel<fp8, 4, split>": ("mfma", 0, 2 * h_i * d_i * pairs),
+        # bf16 indexer (the op surface without quantisation): against the fp8 peak x 1/2
+        "indexer_tile_kernel": ("mfma_bf16", 0, 2 * h_i * d_i * pairs),
+        # Q, gathered rows, indices, row statistics, mass written
+        "attn_mass_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * Ka * S + 8 * H * S + 4 * Ka * S,
+                                  2 * H * dq * P),
         "topk_kernel": ("hbm", 4 * pairs + 4 * K * S, 0),
         "sparse_mla_fwd_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * Ka * S + 2 * H * dv * S + 4 * H * S,
                                        2 * H * (dq + dv) * P),
@@ -384,7 +411,7 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=5
         "compressor_kernel": ("hbm", 0, 0),  # per-call bytes depend on the block geometry; see kernels
     }
     if dq != 576:  # the rope-less variants' names
-        for name in ("sparse_mla_fwd_bf16_kernel", "bwd_sdp_kernel", "bwd_dqk_kernel"):
+        for name in ("sparse_mla_fwd_bf16_kernel", "bwd_sdp_kernel", "bwd_dqk_kernel", "attn_mass_bf16_kernel"):
             w[f"{name}<{dq}>"] = w.pop(name)
         w[f"bwd_contrib_kernel<2,{dq}>"] = w.pop("bwd_contrib_kernel<2>")
         w[f"dkv_reduce_kernel<{dq // 8}>"] = w.pop("dkv_reduce_kernel<72>")
@@ -404,10 +431,11 @@ def kernel_table(ktimes, work, steps, traffic_of=None):
         if name in work:
             bound, nbytes, flops = work[name]
             b1, f1 = nbytes / per_step, flops / per_step
-            if bound == "mfma":
+            if bound in ("mfma", "mfma_bf16"):
                 ach = f1 / (avg * 1e-3) / 1e12
-                row.update(bound="mfma", algorithmic_flops=f1, achieved=ach, peak=FP8_PEAK_TFLOPS, unit="TFLOP/s",
-                           frac=ach / FP8_PEAK_TFLOPS)
+                peak = FP8_PEAK_TFLOPS if bound == "mfma" else BF16_PEAK_TFLOPS
+                row.update(bound="mfma", algorithmic_flops=f1, achieved=ach, peak=peak, unit="TFLOP/s",
+                           frac=ach / peak)
             elif nbytes:
                 ach = b1 / (avg * 1e-3) / 1e9
                 row.update(bound="hbm", algorithmic_bytes=b1, achieved=ach, peak=HBM_PEAK_GBPS, unit="GB/s",
@@ -603,7 +631,7 @@ def main():
     dev = torch.device("cuda:0")
     wl = args.workload
     H, K = args.heads, args.topk
-    S = args.seq or {"c3": 8192, "c4": 32768, "c5": 0, "c5-long": 131072, "v4": 8192}[wl]
+    S = args.seq or {"c3": 8192, "c3-op": 8192, "c4": 32768, "c5": 0, "c5-long": 131072, "v4": 8192}[wl]
     if args.copy_calibration:
         copy_calibration(torch, dev)
     pairs = None
@@ -611,6 +639,11 @@ def main():
         inp = make_inputs(S, H, K, args.seed, dev)
         step = lambda t: dsa_step(inp, ops, t)  # noqa: E731
         cfg = dict(workload="C3: DeepSeek-V3.2 DSA layer fwd+bwd", batch=1, seq_len=S)
+    elif wl == "c3-op":
+        inp = make_inputs(S, H, K, args.seed, dev)
+        step = lambda t: c3_op_step(inp, ops, t)  # noqa: E731
+        cfg = dict(workload="C3 through the torch_npu op surface: bf16 indexer + top-k, attention fwd+bwd, fused "
+                            "indexer KL op recomputing its target mass", batch=1, seq_len=S)
     elif wl == "c5-long":
         inp = make_inputs(S, H, K, args.seed, dev, on_device=True)
         step = lambda t: dsa_step(inp, ops, t)  # noqa: E731

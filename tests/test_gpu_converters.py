@@ -44,8 +44,11 @@ class _Model(torch.nn.Module):
         self.layers = torch.nn.ModuleDict({"0": _Block()})
 
 
-@pytest.mark.parametrize("S,H,K", [(256, 16, 64), (192, 128, 128)])
-def test_npu_dsa_end_to_end(S, H, K):
+@pytest.mark.parametrize("S,H,K,views", [(256, 16, 64, False), (192, 128, 128, False), (160, 128, 96, True)])
+def test_npu_dsa_end_to_end(S, H, K, views):
+    """views: q and k arrive as the reference model builds them, transposed views of
+    [B, S, H, D] tensors (models/deepseek_v32/model.py:526-535), with the gradients landing
+    in those tensors; otherwise as BHSD-contiguous tensors."""
     from torchtitan_npu_simulator_amd import converters as conv
     from torchtitan_npu_simulator_amd.converters.dsa_indexer_loss import DSAIndexerLossAutoScaler
 
@@ -63,8 +66,14 @@ def test_npu_dsa_end_to_end(S, H, K):
     dout = torch.randn(1, H, S, 512, generator=g)
     scale = 576 ** -0.5
 
-    qd = q.to(DEV).requires_grad_(True)
-    kvd = kv.to(DEV).requires_grad_(True)
+    if views:
+        q_leaf = q.transpose(1, 2).contiguous().to(DEV).requires_grad_(True)
+        kv_leaf = kv.transpose(1, 2).contiguous().to(DEV).requires_grad_(True)
+        qd, kvd = q_leaf.transpose(1, 2), kv_leaf.transpose(1, 2)
+    else:
+        qd = q.to(DEV).requires_grad_(True)
+        kvd = kv.to(DEV).requires_grad_(True)
+        q_leaf, kv_leaf = qd, kvd
     qid = qi.to(DEV).requires_grad_(True)
     kid = ki.to(DEV).requires_grad_(True)
     wd = w.to(DEV).requires_grad_(True)
@@ -89,8 +98,10 @@ def test_npu_dsa_end_to_end(S, H, K):
     ref_out, ref_lse = O.sparse_mla_fwd(q_b, kv_b, idx, scale)
     assert rel_err(out.detach().cpu().transpose(1, 2), ref_out) <= 2e-2
     dq, dkv = O.sparse_mla_bwd(q_b, kv_b, idx, dout.transpose(1, 2), scale)
-    assert rel_err(qd.grad.cpu().transpose(1, 2), dq) <= 2e-2
-    assert rel_err(kvd.grad.cpu()[:, 0], dkv) <= 2e-2
+    gq = q_leaf.grad.cpu() if views else q_leaf.grad.cpu().transpose(1, 2)
+    gkv = kv_leaf.grad.cpu()[:, :, 0] if views else kv_leaf.grad.cpu()[:, 0]
+    assert rel_err(gq, dq) <= 2e-2
+    assert rel_err(gkv, dkv) <= 2e-2
     rdq, rdk, rdw, rloss = O.indexer_kl_loss_grad(q_b, kv_b, qi, ki, w, idx, ref_lse, scale)
     n = S  # B*S
     assert rel_err(qid.grad.cpu(), rdq / n) <= 1e-2

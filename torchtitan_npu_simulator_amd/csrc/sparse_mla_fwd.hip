@@ -697,6 +697,7 @@ extern "C" int dsa_attn_mass(const void* q, const void* kv, const int32_t* indic
     }
     dim3 grid((unsigned)s_q, hgroups, (unsigned)batch);
     auto kern = d_qk == kDqk ? attn_mass_bf16_kernel<kDqk> : attn_mass_bf16_kernel<kDv>;
+    const TimedLaunch tl(d_qk == kDqk ? "attn_mass_bf16_kernel" : "attn_mass_bf16_kernel<512>", st);
     kern<<<grid, kFwdThreads, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, softmax_max, softmax_sum, mass,
                                        (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale * kLog2e, q_offset);
     return check_launch("dsa_attn_mass(bf16)");
