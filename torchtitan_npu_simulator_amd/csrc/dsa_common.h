@@ -205,17 +205,16 @@ __device__ __forceinline__ int swz_kl(int r) { return ((r & 7) << 1) ^ (((r >> 3
 // be wave-uniform.  Issued from inline assembly on purpose: the compiler then does not
 // treat every later LDS read as dependent on the DMA (it would otherwise wait for all DMAs
 // in flight before each ds_read), so the caller must wait for completion itself
-// (s_waitcnt vmcnt) before reading the destination.
+// (s_waitcnt vmcnt) before reading the destination.  The LDS address travels in M0, bound
+// by the "{m0}" operand constraint, so the compiler itself writes M0 and knows its value.
 __device__ __forceinline__ void dma16_to_lds(const void* gbase, uint32_t voff, uint32_t lds_base) {
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gbase), "s"(m0v)
-               : "memory", "m0");
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gbase), "{m0}"(m0v) : "memory");
 }
 // 4-byte-per-lane variant: lane i writes LDS byte lds_base + 4 i.
 __device__ __forceinline__ void dma4_to_lds(const void* gbase, uint32_t voff, uint32_t lds_base) {
   const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_base);
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(gbase), "s"(m0v)
-               : "memory", "m0");
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(gbase), "{m0}"(m0v) : "memory");
 }
 
 // compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1, expanded by the
