@@ -82,7 +82,7 @@ class _LinkedIndexerLoss(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query_indexer, key_indexer, weights, sparse_indices, link, layer_number, num_layers):
-        ctx.save_for_backward(query_indexer, key_indexer, weights, sparse_indices)
+        ctx.save_for_backward(query_indexer, key_indexer, weights)  # (the indices travel in ``link``)
         ctx.link = link
         ctx.layer_number = layer_number
         ctx.num_layers = num_layers
@@ -90,7 +90,7 @@ class _LinkedIndexerLoss(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad):
-        query_indexer, key_indexer, weights, sparse_indices = ctx.saved_tensors
+        query_indexer, key_indexer, weights = ctx.saved_tensors
         link = ctx.link
         q, kv3, idx, smax, ssum, scale, q_off = link.fwd
         mass = link.mass
