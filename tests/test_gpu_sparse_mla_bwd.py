@@ -183,6 +183,26 @@ def test_attn_mass_parity(S, H, K, q_offset, d_qk):
     assert torch.allclose(mass.sum(-1)[rows].double(), torch.full_like(mass.sum(-1)[rows].double(), H), rtol=1e-3)
 
 
+@pytest.mark.parametrize("d_qk", [576, 512])
+def test_attn_mass_batched(d_qk):
+    """Two batch elements in one call (grid z) with their own keys and indices, each against
+    the oracle."""
+    S, H, K = 72, 128, 48
+    parts = [attn_inputs(S, H, seed=20 + i, d_qk=d_qk) for i in range(2)]
+    scale = parts[0][3]
+    q = torch.cat([p[0] for p in parts])
+    kv = torch.cat([p[1] for p in parts])
+    idx = torch.cat([rand_indices(S, K, seed=20 + i, shuffle=True, holes=0.1) for i in range(2)])
+    ops = _ops()
+    qd, kvd, idxd = q.to(DEV), kv.to(DEV), idx.to(DEV)
+    out, smax, ssum = ops.sparse_mla_fwd(qd, kvd, idxd, scale, d_v=512)
+    mass = ops.attn_mass(qd, kvd, idxd, smax, ssum, scale).cpu()
+    lse = smax.cpu().double() + torch.log(ssum.cpu().double())
+    for b in range(2):
+        ref = O.attn_mass(q[b:b + 1], kv[b:b + 1], idx[b:b + 1], lse[b:b + 1], scale)
+        assert rel_err(mass[b:b + 1], ref) <= 1e-4
+
+
 @pytest.mark.parametrize("S,H,K,q_offset", [(200, 128, 128, 0), (64, 16, 32, 16), (96, 72, 40, 0)])
 def test_bwd_fused_mass_matches_attn_mass(S, H, K, q_offset):
     """The mass the backward returns (one or several head groups) equals dsa_attn_mass and the oracle."""
