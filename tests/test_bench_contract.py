@@ -60,3 +60,24 @@ def test_compressor_bytes_c4():
         assert b == 2 * 32768 * 2 * D * 4 + 4 * 2 * D * 4 + 8192 * D * 2
         total += b
     assert round(total / 1e8, 2) == 3.46
+
+
+def test_kernel_table_rooflines_per_bound():
+    """Per-kernel rows: HBM kernels against 8 TB/s, the fp8 indexer against the fp8 peak, the
+    bf16 indexer against the bf16 peak; the attention mass kernel's bytes follow its formula
+    (Q, the gathered rows, indices, row statistics, mass) and the 512-column names map."""
+    S, H, K, P, pairs = 8192, 128, 2048, 14_681_088, 8192 * 8193 // 2
+    w = bench.step_kernel_work(S, H, K, P, pairs, S)
+    bound, nbytes, flops = w["attn_mass_bf16_kernel"]
+    assert bound == "hbm" and flops == 2 * H * 576 * P
+    assert nbytes == 2 * H * 576 * S + 2 * 576 * P + 8 * K * S + 8 * H * S
+    w512 = bench.step_kernel_work(S, H, K, P, pairs, S, d_qk=512)
+    assert "attn_mass_bf16_kernel<512>" in w512 and w512["attn_mass_bf16_kernel<512>"][2] == 2 * H * 512 * P
+    ktimes = {"indexer_tile_kernel<fp8, 4, split>": (0.5, 2), "indexer_tile_kernel": (1.0, 2),
+              "attn_mass_bf16_kernel": (4.0, 2)}
+    rows = {r["kernel"]: r for r in bench.kernel_table(ktimes, w, steps=2)}
+    fp8, b16, mass = rows["indexer_tile_kernel<fp8, 4, split>"], rows["indexer_tile_kernel"], rows["attn_mass_bf16_kernel"]
+    assert fp8["peak"] == bench.FP8_PEAK_TFLOPS and b16["peak"] == bench.BF16_PEAK_TFLOPS
+    assert abs(b16["frac"] - 2 * 64 * 128 * pairs / 0.5e-3 / 1e12 / bench.BF16_PEAK_TFLOPS) < 1e-9
+    assert mass["unit"] == "GB/s" and abs(mass["achieved"] - nbytes / 2e-3 / 1e9) < 1e-6
+    assert rows["attn_mass_bf16_kernel"]["ms_per_step"] == 2.0
