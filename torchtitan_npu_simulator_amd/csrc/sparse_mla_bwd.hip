@@ -779,7 +779,10 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
         const int r = i / kRC, c = i - r * kRC;
         if ((kStChunks % kCThreads == 0 || i < kStChunks) && s0 + r < nslots) {
           const u32x4 v = lds_read16(stg + r * (kRC * 16) + 16 * (c ^ stage_swz(r)));
-          *reinterpret_cast<u32x4*>(crow + (int64_t)(s0 + r) * kD + 8 * c) = v;
+          // non-temporal: the rows are read back once, by the key-major reduction (with the
+          // reduction's non-temporal loads this makes that pass ≈4 % faster and this one ≈0.7 %
+          // slower)
+          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(crow + (int64_t)(s0 + r) * kD + 8 * c));
         }
       }
     }
