@@ -456,7 +456,8 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
           const int row = 4 * m + (lane >> 4), c = lane & 15;
           const u32x4 v = lds_read16(stg[row >> 3] + (row & 7) * 256 + 16 * (c ^ row));
           const int slot = blk * kB + 16 * wave + row;
-          if (slot < K) *reinterpret_cast<u32x4*>(ckrow + (int64_t)slot * kD + 8 * c) = v;
+          // (non-temporal: read back once, by the key-major reduction)
+          if (slot < K) __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(ckrow + (int64_t)slot * kD + 8 * c));
         }
       }
     }
