@@ -367,47 +367,61 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=5
     ``pairs`` = causal (query, key) pairs the indexer scores, s_kv attention keys, s_ki
     indexer keys (default s_kv), d_qk the attention row width (576: latent + rope; 512: the
     rope-less DeepSeek-V4 rows, whose kernels report a ``<512>`` name), k_attn the attention
-    slots per row (default K; V4: the 128-token window + K).  Bytes are the data each kernel
-    must move once (no cache hits assumed, gathered rows counted per pair); FLOPs count the
-    MFMA products.  Returns name -> (bound, bytes, flops).
+    slots per row (default K; V4: the 128-token window + K).  Returns name -> (bound, bytes,
+    flops, intermediate_bytes):
+
+    * ``bytes``: the operands of the op contract that the kernel must move once, counted as
+      the per-unit formulas of the survey's measurement table count them (Q, dO, O, the
+      gathered KV rows per pair, indices, row statistics, dQ, dKV; no cache hits assumed).
+      The dKV scatter-add payload (4 bytes per element and pair) is what the backward's
+      contribution rows cost here: written once in bf16 by the contribution kernel and read
+      once by the key-major reduction (2 + 2 bytes per element and pair);
+    * ``intermediate_bytes``: what this design adds between its kernels and the op contract
+      does not have: G (dS and P per head, bf16) written by the score kernel and read back by
+      the dQ and contribution kernels, the per-row delta, the head-summed mass handed to the
+      indexer loss, and the CSR pair lists;
+    * ``flops``: the MFMA products.
     """
     s_ki = s_kv if s_ki is None else s_ki
     Ka = K if k_attn is None else k_attn
     dq, dv, gw = d_qk, 512, 256  # row width, latent width, G row (dS | P) x 128 heads
     w = {
-        "quantize_fp8_kernel": ("hbm", (S * h_i + s_ki) * (2 * d_i + d_i + 4), 0),
-        "indexer_lin_pieces_kernel<64>": ("hbm", S * (h_i * d_i + 4 * h_i + 4 * h_i + 4 * d_i + 16), 0),
-        "indexer_tile_kernel<fp8, 4, split>": ("mfma", 0, 2 * h_i * d_i * pairs),
+        "quantize_fp8_kernel": ("hbm", (S * h_i + s_ki) * (2 * d_i + d_i + 4), 0, 0),
+        "indexer_lin_pieces_kernel<64>": ("hbm", 0, 0, S * (h_i * d_i + 4 * h_i + 4 * h_i + 4 * d_i + 16)),
+        "indexer_tile_kernel<fp8, 4, split>": ("mfma", 0, 2 * h_i * d_i * pairs, 0),
         # bf16 indexer (the op surface without quantisation): against the fp8 peak x 1/2
-        "indexer_tile_kernel": ("mfma_bf16", 0, 2 * h_i * d_i * pairs),
-        # Q, gathered rows, indices, row statistics, mass written
-        "attn_mass_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * Ka * S + 8 * H * S + 4 * Ka * S,
-                                  2 * H * dq * P),
-        "topk_kernel": ("hbm", 4 * pairs + 4 * K * S, 0),
-        "sparse_mla_fwd_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * Ka * S + 2 * H * dv * S + 4 * H * S,
-                                       2 * H * (dq + dv) * P),
-        "sparse_mla_fwd_exact_kernel<fixup>": ("hbm", 4 * H * S, 0),
-        "bwd_delta_kernel": ("hbm", 2 * (2 * H * dv * S) + 4 * H * S, 0),
-        # Q, dO, gathered rows, indices, G written, mass, (max, sum, delta)
-        "bwd_sdp_kernel": ("hbm", 2 * H * dq * S + 2 * H * dv * S + 2 * dq * P + 4 * Ka * S + 2 * gw * P + 4 * Ka * S
-                           + 12 * H * S, 2 * H * (dq + dv) * P),
-        # gathered rows, indices, dS half of G, dQ written
-        "bwd_dqk_kernel": ("hbm", 2 * dq * P + 4 * Ka * S + 2 * (gw // 2) * P + 2 * H * dq * S, 2 * H * dq * P),
-        # G, X = [Q; dO], indices, C written
-        "bwd_contrib_kernel<2>": ("hbm", 2 * gw * P + 2 * H * (dq + dv) * S + 4 * Ka * S + 2 * dq * P,
-                                  2 * P * (gw * dv + (gw // 2) * (dq - dv))),
-        "zero_i32_kernel": ("hbm", 4 * (s_kv + 1) + 4 * (s_ki + 1), 0),
-        "csr_count_kernel<count>": ("hbm", 8 * Ka * S, 0),
-        "csr_count_kernel<fill>": ("hbm", 8 * Ka * S + 8 * P, 0),
-        "csr_scan_kernel": ("hbm", 12 * (s_kv + s_ki), 0),
-        "csr_seg_key_kernel": ("hbm", 8 * (s_kv + s_ki), 0),
-        # C rows read, pair list, fp32 dKV written
-        "dkv_reduce_kernel<72>": ("hbm", 2 * dq * P + 4 * P + 4 * dq * s_kv, 0),
-        # q_I, gathered k_I rows, mass, weights, dq_I (fp32), dk_I contributions, dw, loss
-        "indexer_kl_mfma_kernel": ("hbm", S * (2 * h_i * d_i + 4 * K + 4 * h_i + 4 * h_i * d_i + 4 * h_i + 4)
-                                   + P * (2 * d_i + 2 * d_i), 2 * P * h_i * d_i * 3),
-        "dkv_reduce_kernel<16>": ("hbm", 2 * d_i * P + 4 * P + 4 * d_i * s_ki, 0),
-        "compressor_kernel": ("hbm", 0, 0),  # per-call bytes depend on the block geometry; see kernels
+        "indexer_tile_kernel": ("mfma_bf16", 0, 2 * h_i * d_i * pairs, 0),
+        # Q, gathered rows, indices, row statistics | mass written (the KL op's target)
+        "attn_mass_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * Ka * S + 8 * H * S, 2 * H * dq * P,
+                                  4 * Ka * S),
+        "topk_kernel": ("hbm", 4 * pairs + 4 * K * S, 0, 0),
+        "sparse_mla_fwd_bf16_kernel": ("hbm", 2 * H * dq * S + 2 * dq * P + 4 * Ka * S + 2 * H * dv * S + 8 * H * S,
+                                       2 * H * (dq + dv) * P, 0),
+        "sparse_mla_fwd_exact_kernel<fixup>": ("hbm", 4 * H * S, 0, 0),
+        # O, dO | delta written
+        "bwd_delta_kernel": ("hbm", 2 * (2 * H * dv * S), 0, 4 * H * S),
+        # Q, dO, gathered rows, indices, row statistics | G written, mass written, delta read
+        "bwd_sdp_kernel": ("hbm", 2 * H * dq * S + 2 * H * dv * S + 2 * dq * P + 4 * Ka * S + 8 * H * S,
+                           2 * H * (dq + dv) * P, 2 * gw * P + 4 * Ka * S + 4 * H * S),
+        # gathered rows, indices, dQ written | dS half of G read
+        "bwd_dqk_kernel": ("hbm", 2 * dq * P + 4 * Ka * S + 2 * H * dq * S, 2 * H * dq * P, 2 * (gw // 2) * P),
+        # X = [Q; dO], indices, contribution rows written (half the scatter payload) | G read
+        "bwd_contrib_kernel<2>": ("hbm", 2 * H * (dq + dv) * S + 4 * Ka * S + 2 * dq * P,
+                                  2 * P * (gw * dv + (gw // 2) * (dq - dv)), 2 * gw * P),
+        "zero_i32_kernel": ("hbm", 0, 0, 4 * (s_kv + 1) + 4 * (s_ki + 1)),
+        "csr_count_kernel<count>": ("hbm", 0, 0, 8 * Ka * S),
+        "csr_count_kernel<fill>": ("hbm", 0, 0, 8 * Ka * S + 8 * P),
+        "csr_scan_kernel": ("hbm", 0, 0, 12 * (s_kv + s_ki)),
+        "csr_seg_key_kernel": ("hbm", 0, 0, 8 * (s_kv + s_ki)),
+        # contribution rows read (the other half of the scatter payload), fp32 dKV written | pair list
+        "dkv_reduce_kernel<72>": ("hbm", 2 * dq * P + 4 * dq * s_kv, 0, 4 * P),
+        # q_I, gathered k_I rows, weights, dq_I (fp32), dk_I contributions (half the dk_I scatter
+        # payload), dw, loss | mass read, the key rows' second gather (the gradient pass)
+        "indexer_kl_mfma_kernel": ("hbm", S * (2 * h_i * d_i + 4 * h_i + 4 * h_i * d_i + 4 * h_i + 4)
+                                   + P * (2 * d_i + 2 * d_i), 2 * P * h_i * d_i * 3, 4 * K * S + 2 * d_i * P),
+        # dk_I contributions read (the other half of the payload), fp32 dk_I written | pair list
+        "dkv_reduce_kernel<16>": ("hbm", 2 * d_i * P + 4 * d_i * s_ki, 0, 4 * P),
+        "compressor_kernel": ("hbm", 0, 0, 0),  # per-call bytes depend on the block geometry; see kernels
     }
     if dq != 576:  # the rope-less variants' names
         for name in ("sparse_mla_fwd_bf16_kernel", "bwd_sdp_kernel", "bwd_dqk_kernel", "attn_mass_bf16_kernel"):
@@ -420,27 +434,31 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=5
 def kernel_table(ktimes, work, steps, traffic_of=None):
     """Per-kernel roofline rows, slowest first: average launch duration and launches per step
     from the kernel timing, the algorithmic bytes (or FLOPs for MFMA-bound kernels) per launch,
-    achieved rate and fraction of peak, MFMA fraction of the bf16 peak where the kernel runs
-    MFMAs, and the counter bytes per launch when a PMC summary has the kernel."""
+    achieved rate and ``frac`` of peak on those bytes alone; the design-intermediate bytes per
+    launch and ``frac_with_intermediates`` on both; the MFMA fraction of the bf16 peak where
+    the kernel runs MFMAs, and the counter bytes per launch when a PMC summary has the kernel."""
     rows = []
     for name, (total_ms, launches) in ktimes.items():
         per_step = launches / steps
         avg = total_ms / launches
         row = dict(kernel=name, avg_launch_ms=avg, launches_per_step=per_step, ms_per_step=total_ms / steps)
         if name in work:
-            bound, nbytes, flops = work[name]
-            b1, f1 = nbytes / per_step, flops / per_step
+            bound, nbytes, flops, inter = work[name]
+            b1, f1, i1 = nbytes / per_step, flops / per_step, inter / per_step
             if bound in ("mfma", "mfma_bf16"):
                 ach = f1 / (avg * 1e-3) / 1e12
                 peak = FP8_PEAK_TFLOPS if bound == "mfma" else BF16_PEAK_TFLOPS
                 row.update(bound="mfma", algorithmic_flops=f1, achieved=ach, peak=peak, unit="TFLOP/s",
                            frac=ach / peak)
-            elif nbytes:
+            elif nbytes or inter:
                 ach = b1 / (avg * 1e-3) / 1e9
                 row.update(bound="hbm", algorithmic_bytes=b1, achieved=ach, peak=HBM_PEAK_GBPS, unit="GB/s",
                            frac=ach / HBM_PEAK_GBPS)
                 if flops:
                     row["mfma_frac_bf16"] = f1 / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS
+            if inter and bound not in ("mfma", "mfma_bf16"):
+                row["intermediate_bytes"] = i1
+                row["frac_with_intermediates"] = (b1 + i1) / (avg * 1e-3) / 1e9 / HBM_PEAK_GBPS
         if traffic_of is not None:
             t = traffic_of(name)
             if t is not None:
@@ -723,6 +741,9 @@ def main():
                     share_of_step=dom["ms_per_step"] / ms_per_step)
         if dom["bound"] == "hbm":
             roof["algorithmic_bytes"] = dom["algorithmic_bytes"]
+            if "intermediate_bytes" in dom:  # the design's own intermediates, outside `achieved`
+                roof["intermediate_bytes"] = dom["intermediate_bytes"]
+                roof["frac_with_intermediates"] = dom["frac_with_intermediates"]
         else:
             roof["algorithmic_flops"] = dom["algorithmic_flops"]
     else:  # (v4: the attention forward as a whole)

@@ -278,6 +278,19 @@ int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, co
                         void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q, int64_t s_k,
                         int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset, float loss_scale,
                         float eps, float grad_scale, const float* grad_scale_dev, void* stream);
+/*
+ * dsa_indexer_kl_grad that also writes the indexer's softmax over the slots (reference: the
+ * softmax_out of cann_ops_transformer's sparse_lightning_indexer_kl_loss_grad,
+ * converters/kernels/npu_smla.py:584-602, which _compute_li_loss :405-420 logs):
+ *   softmax_out [B,S,K] fp32 (written): exp(I_j - logsumexp of the row's usable I) at usable
+ *   slots, 0 at the others.  softmax_out = NULL is dsa_indexer_kl_grad.
+ */
+int dsa_indexer_kl_grad_softmax(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
+                                const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
+                                float* softmax_out, void* workspace, int64_t workspace_bytes, int64_t batch,
+                                int64_t s_q, int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t topk,
+                                int64_t q_offset, float loss_scale, float eps, float grad_scale,
+                                const float* grad_scale_dev, void* stream);
 
 /*
  * Block KV compressor (reference: Compressor._forward_bsnd + overlap_transform,

@@ -82,3 +82,23 @@ def test_indexer_workspace_size(lib):
     assert lib.dsa_indexer_fwd_workspace_size(1, 8192, 64, 128, bf16) == 0
     assert lib.dsa_indexer_fwd_workspace_size(1, 8192, 32, 128, fp8) == 0
     assert lib.dsa_indexer_fwd_workspace_size(1, 0, 64, 128, fp8) == 0
+
+
+@pytest.mark.parametrize("B,S,s_k", [(2, 700, 700), (8, 512, 4096), (1, 700, 700)])
+def test_lightning_indexer_workspace_respects_the_score_budget(lib, B, S, s_k):
+    """The fused indexer's workspace stays within the score budget when all batches do not
+    fit at once (the C entry then goes batch by batch): scores of one budget's worth of rows
+    plus the fp8 split pieces of those rows."""
+    from torchtitan_npu_simulator_amd import _lib
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    fp8 = _lib.dtype_code(torch.float8_e4m3fn)
+    budget = S * s_k * 4  # exactly one batch of score rows
+    ws = ops.lightning_indexer_workspace_bytes(lib, B, S, s_k, 64, 128, fp8, budget=budget)
+    pieces = lib.dsa_indexer_fwd_workspace_size(1, S, 64, 128, fp8)
+    assert ws <= budget + 256 + pieces
+    if B > 1:
+        small = ops.lightning_indexer_workspace_bytes(lib, B, S, s_k, 64, 128, fp8, budget=budget - 4 * s_k)
+        assert small <= budget - 4 * s_k + 256 + pieces
+    big = ops.lightning_indexer_workspace_bytes(lib, B, S, s_k, 64, 128, fp8, budget=B * S * s_k * 4)
+    assert big >= B * S * s_k * 4  # everything in one pass when it fits

@@ -68,9 +68,9 @@ def test_kernel_table_rooflines_per_bound():
     (Q, the gathered rows, indices, row statistics, mass) and the 512-column names map."""
     S, H, K, P, pairs = 8192, 128, 2048, 14_681_088, 8192 * 8193 // 2
     w = bench.step_kernel_work(S, H, K, P, pairs, S)
-    bound, nbytes, flops = w["attn_mass_bf16_kernel"]
+    bound, nbytes, flops, inter = w["attn_mass_bf16_kernel"]
     assert bound == "hbm" and flops == 2 * H * 576 * P
-    assert nbytes == 2 * H * 576 * S + 2 * 576 * P + 8 * K * S + 8 * H * S
+    assert nbytes == 2 * H * 576 * S + 2 * 576 * P + 4 * K * S + 8 * H * S and inter == 4 * K * S
     w512 = bench.step_kernel_work(S, H, K, P, pairs, S, d_qk=512)
     assert "attn_mass_bf16_kernel<512>" in w512 and w512["attn_mass_bf16_kernel<512>"][2] == 2 * H * 512 * P
     ktimes = {"indexer_tile_kernel<fp8, 4, split>": (0.5, 2), "indexer_tile_kernel": (1.0, 2),
@@ -80,4 +80,32 @@ def test_kernel_table_rooflines_per_bound():
     assert fp8["peak"] == bench.FP8_PEAK_TFLOPS and b16["peak"] == bench.BF16_PEAK_TFLOPS
     assert abs(b16["frac"] - 2 * 64 * 128 * pairs / 0.5e-3 / 1e12 / bench.BF16_PEAK_TFLOPS) < 1e-9
     assert mass["unit"] == "GB/s" and abs(mass["achieved"] - nbytes / 2e-3 / 1e9) < 1e-6
+    assert abs(mass["frac_with_intermediates"] - (nbytes + inter) / 2e-3 / 1e9 / bench.HBM_PEAK_GBPS) < 1e-9
     assert rows["attn_mass_bf16_kernel"]["ms_per_step"] == 2.0
+
+
+def test_backward_bytes_split_into_contract_and_intermediate():
+    """The attention backward's per-kernel bytes: the survey's formula counts Q and dQ, O and
+    dO, the row statistics, the indices, the gathered rows and a 4-byte-per-element dKV
+    scatter payload; here the payload is the bf16 contribution rows written by the
+    contribution kernel and read by the reduction (2 + 2 bytes).  G (dS | P per head), the
+    delta, the mass and the pair lists are design intermediates, kept out of ``frac``."""
+    S, H, K, P, pairs = 8192, 128, 2048, 14_681_088, 8192 * 8193 // 2
+    w = bench.step_kernel_work(S, H, K, P, pairs, S)
+    G = 2 * 256 * P  # bf16 dS and P of 128 heads per (row, slot)
+    assert w["bwd_sdp_kernel"][3] == G + 4 * K * S + 4 * H * S
+    assert w["bwd_dqk_kernel"][3] == G // 2
+    assert w["bwd_contrib_kernel<2>"][3] == G
+    assert w["bwd_contrib_kernel<2>"][1] == 2 * H * (576 + 512) * S + 4 * K * S + 2 * 576 * P
+    assert w["dkv_reduce_kernel<72>"][1] == 2 * 576 * P + 4 * 576 * S
+    # the two halves of the contribution round trip are exactly the survey's scatter payload
+    payload = (w["bwd_contrib_kernel<2>"][1] - 2 * H * (576 + 512) * S - 4 * K * S) + \
+        (w["dkv_reduce_kernel<72>"][1] - 4 * 576 * S)
+    assert payload == 4 * 576 * P
+    assert all(w[k][1] == 0 for k in ("csr_count_kernel<count>", "csr_count_kernel<fill>", "csr_scan_kernel"))
+    ktimes = {"bwd_contrib_kernel<2>": (5.0, 1), "csr_count_kernel<fill>": (0.2, 1)}
+    rows = {r["kernel"]: r for r in bench.kernel_table(ktimes, w, steps=1)}
+    beta = rows["bwd_contrib_kernel<2>"]
+    assert beta["frac"] < beta["frac_with_intermediates"]
+    assert abs(beta["frac"] - w["bwd_contrib_kernel<2>"][1] / 5e-3 / 1e9 / bench.HBM_PEAK_GBPS) < 1e-9
+    assert rows["csr_count_kernel<fill>"]["frac"] == 0.0

@@ -208,3 +208,22 @@ def test_host_ints_reads_a_device_tensor_once_per_version():
     del cu, twin
     gc.collect()
     assert len(_lib._host_cache) == n - 2
+
+
+def test_band_rule_cuts_and_masks():
+    """pre_tokens / next_tokens: whether a band removes keys the mode admits, and the index
+    masking the KL op applies (band of row s: [a(s) - pre, a(s) + next], a(s) = s in
+    sparse_mode 0 and s + q_offset in sparse_mode 3)."""
+    from torchtitan_npu_simulator_amd.torch_npu_ops import _band_cuts, _band_mask_indices
+
+    # the reference's defaults never cut at the configs' lengths
+    assert not _band_cuts(3, 8192, 8192, 0, 65536, 65536)
+    assert not _band_cuts(3, 4096, 8192, 4096, (1 << 63) - 1, (1 << 63) - 1)
+    assert _band_cuts(3, 131072, 131072, 0, 65536, 65536)
+    assert _band_cuts(3, 16, 16, 0, 4, 0) and _band_cuts(3, 16, 16, 0, 100, -1)
+    assert not _band_cuts(0, 16, 16, 0, 15, 15) and _band_cuts(0, 16, 16, 0, 15, 14)
+    idx = torch.tensor([[[0, 3, 5, -1], [1, 2, 6, 7]]], dtype=torch.int32)  # rows 0, 1
+    m3 = _band_mask_indices(idx, 3, 6, 2, 0)  # a(s) = s + 6: rows see [4, 6] and [5, 7]
+    assert m3.tolist() == [[[-1, -1, 5, -1], [-1, -1, 6, 7]]]
+    m0 = _band_mask_indices(idx, 0, 0, 1, 1)  # a(s) = s: [-1, 1] and [0, 2]
+    assert m0.tolist() == [[[0, -1, -1, -1], [1, 2, -1, -1]]]

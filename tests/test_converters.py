@@ -8,6 +8,7 @@ shapes, -1 preservation, +offset, loss deferral and scaling, the registry.
 
 from __future__ import annotations
 
+import weakref
 from types import SimpleNamespace
 from unittest.mock import patch
 
@@ -141,12 +142,19 @@ def _dsa_case(B=1, H=4, S=8, HI=2, DI=16):
 
 
 class _FakeLinkedAttention(torch.autograd.Function):
-    """Stands in for the linked attention op: its backward hands a mass to the link."""
+    """Stands in for the linked attention op: it saves its forward statistics on its own node
+    (as the real op does), leaves only a weak reference to that node in the link, and its
+    backward hands a mass to the link."""
 
     @staticmethod
     def forward(ctx, q_nope, after, link, mass):
+        B, S, H, _ = q_nope.shape
+        K = mass.shape[-1] if mass is not None else 4
+        idx = torch.zeros(B, S, K, dtype=torch.int32)
+        ctx.save_for_backward(q_nope, q_nope, idx, q_nope, torch.zeros(B, S, H), torch.ones(B, S, H))
         ctx.link, ctx.mass = link, mass
-        link.fwd = ("q", "kv", "idx", "smax", "ssum", 0.1, 0)
+        link.attn = weakref.ref(ctx)
+        link.scale, link.q_offset = 0.1, 0
         return q_nope.new_zeros(q_nope.shape)
 
     @staticmethod
@@ -166,8 +174,9 @@ def test_dsa_forward_plumbing_and_loss_deferral():
 
     def fake_sfa(q_, k_, idx, scale, after, link, d_v=512):
         seen["sfa"] = dict(q=q_, k=k_, idx=idx, scale=scale, d_v=d_v)
-        link.fwd = ("q", "kv", "idx", "smax", "ssum", scale, 0)
-        return torch.zeros(B, S, H, 512), torch.zeros(B, S, H), torch.ones(B, S, H)
+        out = _FakeLinkedAttention.apply(torch.zeros(B, S, H, d_v, requires_grad=True), after, link, None)
+        seen["link"] = link
+        return out, torch.zeros(B, S, H), torch.ones(B, S, H)
 
     with patch.object(dsa_mod.npu, "npu_lightning_indexer", side_effect=fake_li), \
             patch.object(dsa_mod.npu, "sparse_flash_attention_linked", side_effect=fake_sfa):
@@ -178,10 +187,13 @@ def test_dsa_forward_plumbing_and_loss_deferral():
     assert s["idx"].shape == (B, S, 1, K) and s["scale"] == 0.1
     assert out.shape == (B, H, S, 512)
     assert float(loss.detach()) == 0.0  # deferred to backward
+    # the link holds no tensor between forward and backward (the attention node owns them)
+    link = seen["link"]
+    assert not any(isinstance(getattr(link, a), torch.Tensor) for a in type(link).__slots__)
 
     # backward of the loss alone: the attention node is not on the path, so the loss
-    # recomputes the mass from the forward statistics; the upstream grad scales the KL
-    # gradients as a tensor (no host round trip) and loss/(B*S) is logged
+    # recomputes the mass from the attention node's saved forward statistics; the upstream
+    # grad scales the KL gradients as a tensor (no host round trip) and loss/(B*S) is logged
     def fake_mass(q_, kv_, idx_, smax_, ssum_, scale_, *, q_offset=0):
         seen["mass_args"] = (q_, kv_, idx_, smax_, ssum_, scale_, q_offset)
         return torch.rand(B, S, K)
@@ -196,7 +208,8 @@ def test_dsa_forward_plumbing_and_loss_deferral():
     with patch.object(dsa_mod.npu, "attn_mass", side_effect=fake_mass), \
             patch.object(dsa_mod.npu, "indexer_kl_grad_from_mass", side_effect=fake_kl):
         (loss * 3.0).backward()
-    assert seen["mass_args"][:5] == ("q", "kv", "idx", "smax", "ssum")
+    assert seen["mass_args"][0].shape == (B, S, H, 512) and seen["mass_args"][5] == 0.1
+    assert torch.equal(seen["mass_args"][4], torch.ones(B, S, H))
     # d(loss/(B*S))/d(z) = 1/(B*S), times 3
     torch.testing.assert_close(qi.grad, torch.full_like(qi, 3.0 / (B * S)))
     assert isinstance(seen["grad_scale"], torch.Tensor)
@@ -229,6 +242,57 @@ def test_dsa_loss_backward_waits_for_the_attention_mass():
             patch.object(dsa_mod.npu, "indexer_kl_grad_from_mass", side_effect=fake_kl):
         (out.sum() + loss).backward()
     assert seen["mass"] is mass
+
+
+def test_dsa_linked_loss_second_backward_with_retain_graph():
+    """A graph kept with retain_graph=True backpropagates twice: the attention backward hands
+    the mass over again and the loss backward finds the link intact."""
+    B, H, S, K, HI, DI = 1, 4, 8, 4, 2, 16
+    self_, q, kv, qi, ki, w = _dsa_case(B, H, S, HI, DI)
+    mass = torch.rand(B, S, K)
+    calls = []
+
+    def fake_li(q_, k_, w_, **kw):
+        return torch.zeros(B, S, 1, K, dtype=torch.int32), None
+
+    def fake_sfa(q_, k_, idx, scale, after, link, d_v=512):
+        return _FakeLinkedAttention.apply(q_[..., :d_v].detach().requires_grad_(True), after, link, mass), None, None
+
+    def fake_kl(qi_, ki_, w_, idx_, mass_, **kw):
+        calls.append(mass_)
+        assert idx_.shape == (B, S, K) and idx_.dtype == torch.int32
+        return torch.ones(B, S, HI, DI), torch.zeros(B, S, DI), torch.zeros(B, S, HI), torch.zeros(B, S)
+
+    with patch.object(dsa_mod.npu, "npu_lightning_indexer", side_effect=fake_li), \
+            patch.object(dsa_mod.npu, "sparse_flash_attention_linked", side_effect=fake_sfa):
+        loss, out = dsa_mod.dsa_forward(self_, q, kv, kv[..., :512], None, 0.1, qi, ki, w, None, K)
+    with patch.object(dsa_mod.npu, "attn_mass", side_effect=AssertionError("mass recomputed")), \
+            patch.object(dsa_mod.npu, "indexer_kl_grad_from_mass", side_effect=fake_kl):
+        (out.sum() + loss).backward(retain_graph=True)
+        g1 = qi.grad.clone()
+        (out.sum() + loss).backward()
+    assert len(calls) == 2 and all(m is mass for m in calls)
+    torch.testing.assert_close(qi.grad, 2 * g1)
+
+
+def test_dsa_linked_loss_alone_without_attention_node_raises():
+    """With the attention output (and so its node) gone, a backward of the loss alone has no
+    forward statistics to recompute the target from: a clear error, not a silent zero."""
+    B, H, S, K, HI, DI = 1, 4, 8, 4, 2, 16
+    self_, q, kv, qi, ki, w = _dsa_case(B, H, S, HI, DI)
+
+    def fake_li(q_, k_, w_, **kw):
+        return torch.zeros(B, S, 1, K, dtype=torch.int32), None
+
+    def fake_sfa(q_, k_, idx, scale, after, link, d_v=512):
+        return _FakeLinkedAttention.apply(torch.zeros(B, S, H, d_v, requires_grad=True), after, link, None), None, None
+
+    with patch.object(dsa_mod.npu, "npu_lightning_indexer", side_effect=fake_li), \
+            patch.object(dsa_mod.npu, "sparse_flash_attention_linked", side_effect=fake_sfa):
+        loss, out = dsa_mod.dsa_forward(self_, q, kv, kv[..., :512], None, 0.1, qi, ki, w, None, K)
+    del out
+    with pytest.raises(RuntimeError, match="backpropagate through the attention output"):
+        loss.backward()
 
 
 def test_dsa_forward_rejects_multi_kv_heads():

@@ -182,3 +182,80 @@ def test_device_cu_seqlens_read_back_once_per_version():
     assert first == [0, 100, 250] and _lib.host_ints(cu) is first  # cached
     cu[2] = 260
     assert _lib.host_ints(cu) == [0, 100, 260]
+
+
+@pytest.mark.parametrize("mode,pre,nxt,s_kv", [(3, 100, 0, 384), (3, 40, -3, 384), (0, 50, 70, 384), (3, 200, 5, 512)])
+def test_lightning_indexer_band(mode, pre, nxt, s_kv):
+    """npu_lightning_indexer with a pre_tokens / next_tokens band (binding.cpp:12-16): bit-exact
+    against the oracle's top-k on the GPU's own scores with every key outside the row's band
+    [a(s) - pre, a(s) + next] (a(s) = s, or s + q_offset in sparse_mode 3) excluded."""
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    S, K, HI, DI = 256, 48, 64, 128
+    g = torch.Generator().manual_seed(pre + s_kv)
+    qi = torch.randn(1, S, HI, DI, generator=g).bfloat16().to(DEV)
+    ki = torch.randn(1, s_kv, DI, generator=g).bfloat16().to(DEV)
+    w = (torch.rand(1, S, HI, generator=g) * HI ** -0.5 * DI ** -0.5).to(DEV)
+    q_off = s_kv - S if mode == 3 else 0
+    idx, vals = ops.npu_lightning_indexer(qi, ki.unsqueeze(2), w, sparse_count=K, sparse_mode=mode, pre_tokens=pre,
+                                          next_tokens=nxt, return_value=True)
+    sc = ops.indexer_scores(qi, ki, w, q_offset=q_off if mode == 3 else ops._NO_MASK_OFFSET).cpu()[0].double()
+    t = torch.arange(s_kv).view(1, -1)
+    a = torch.arange(S).view(-1, 1) + q_off
+    ok = (t >= a - pre) & (t <= a + nxt)
+    if mode == 3:
+        ok &= t <= a
+    sc = sc.masked_fill(~ok, float("nan")).float().numpy()
+    ref = O.topk_select_numpy(sc, K)
+    assert torch.equal(idx[0, :, 0].cpu(), torch.from_numpy(ref).int())
+    assert (idx >= 0).any()
+
+
+def test_kl_loss_band_and_bsnd_lengths():
+    """npu_sparse_lightning_indexer_grad_kl_loss: (1) a pre_tokens band drops the selected keys
+    outside it from target and student alike - the same result as those slots set to -1;
+    (2) BSND with actual_seq_qlen / actual_seq_klen equals each batch's valid prefix run on
+    its own, with zero gradients on padded rows and keys."""
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+    from torchtitan_npu_simulator_amd.torch_npu_ops import _band_mask_indices
+
+    S, H, K, HI, DI = 192, 16, 32, 64, 128
+    q, kv, _, _ = attn_inputs(S, H, seed=3)
+    g = torch.Generator().manual_seed(4)
+    qi = torch.randn(2, S, HI, DI, generator=g).bfloat16()
+    ki = torch.randn(2, S, 1, DI, generator=g).bfloat16()
+    w = torch.rand(2, S, HI, generator=g) * HI ** -0.5 * DI ** -0.5
+    q2 = torch.cat([q, torch.randn_like(q.float()).bfloat16() / 24]).to(DEV)
+    kv2 = torch.cat([kv, torch.randn_like(kv.float()).bfloat16()]).to(DEV)
+    idx2 = torch.cat([rand_indices(S, K, seed=1), rand_indices(S, K, seed=2)]).to(DEV)
+    scale = 576 ** -0.5
+    _, smax, ssum = ops.sparse_mla_fwd(q2, kv2, idx2, scale)
+    common = dict(query_rope=q2[..., 512:], key_rope=kv2[..., 512:].unsqueeze(2))
+    args = (q2[..., :512], kv2[..., :512].unsqueeze(2), qi.to(DEV), ki.to(DEV), w.to(DEV))
+    # (1) the band
+    banded = ops.npu_sparse_lightning_indexer_grad_kl_loss(*args, idx2, smax, ssum, scale, pre_tokens=60, **common)
+    masked = _band_mask_indices(idx2, 3, 0, 60, 65536)
+    assert bool((masked != idx2).any())
+    ref = ops.npu_sparse_lightning_indexer_grad_kl_loss(*args, masked, smax, ssum, scale, **common)
+    for a_, b_ in zip(banded, ref):
+        assert torch.equal(a_, b_)
+    # (2) per-batch lengths: batch 0 keeps 150 rows / keys, batch 1 all of them
+    lq, lk = [150, S], [150, S]
+    got = ops.npu_sparse_lightning_indexer_grad_kl_loss(*args, idx2, smax, ssum, scale, actual_seq_qlen=lq,
+                                                        actual_seq_klen=lk, **common)
+    loss = 0.0
+    for b in range(2):
+        n = lq[b]
+        qb = q2[b:b + 1, :n].contiguous()
+        kvb = kv2[b:b + 1, :n].contiguous()
+        ib = idx2[b:b + 1, :n].contiguous()
+        _, mb, sb = ops.sparse_mla_fwd(qb, kvb, ib, scale)
+        one = ops.npu_sparse_lightning_indexer_grad_kl_loss(
+            qb[..., :512], kvb[..., :512].unsqueeze(2), qi[b:b + 1, :n].to(DEV), ki[b:b + 1, :n].to(DEV),
+            w[b:b + 1, :n].to(DEV), ib, mb, sb, scale, query_rope=qb[..., 512:], key_rope=kvb[..., 512:].unsqueeze(2))
+        torch.testing.assert_close(got[0][b:b + 1, :n], one[0], rtol=1e-5, atol=1e-7)
+        torch.testing.assert_close(got[1][b:b + 1, :n], one[1], rtol=1e-5, atol=1e-7)
+        torch.testing.assert_close(got[2][b:b + 1, :n], one[2], rtol=1e-5, atol=1e-7)
+        assert float(got[0][b, n:].abs().sum()) == 0.0 and float(got[1][b, n:].abs().sum()) == 0.0
+        loss += float(one[3])
+    assert abs(float(got[3]) - loss) <= 1e-5 * abs(loss)

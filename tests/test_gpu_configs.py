@@ -32,6 +32,7 @@ import pytest
 import torch
 
 from oracle import dsa_oracle as O
+from tests.attn_reference import attention_reference, chunk_rel_errors
 from tests.dsa_cases import rel_err
 
 pytestmark = pytest.mark.gpu
@@ -54,10 +55,10 @@ def _log(msg):
     print(f"[configs] {msg}", flush=True)
 
 
-def _draw(S, s_kv, seed, *, signed_w=False, d_kv=DQK):
+def _draw(S, s_kv, seed, *, signed_w=False, d_kv=DQK, d_q=DQK):
     g = torch.Generator(device=DEV).manual_seed(seed)
     bf = dict(device=DEV, dtype=torch.bfloat16, generator=g)
-    q = torch.randn(1, S, H, DQK, **bf)
+    q = torch.randn(1, S, H, d_q, **bf)
     kv = torch.randn(1, s_kv, d_kv, **bf) if s_kv else None
     qi = torch.randn(1, S, HI, DI, **bf)
     ki = torch.randn(1, s_kv, DI, **bf) if s_kv else None
@@ -177,7 +178,7 @@ def check_dkv_keys(res, q, kv, dout, scale, keys, chunk=256):
     for j in keys:
         rows = _rows_selecting(res["idx"], j)
         assert rows.numel() > 0, f"key {j} was never selected"
-        ref = torch.zeros(DQK, dtype=torch.float64)
+        ref = torch.zeros(kv.shape[-1], dtype=torch.float64)
         kv_j = kv[:, j : j + 1].cpu()
         for c0 in range(0, rows.numel(), chunk):
             r = rows[c0 : c0 + chunk]
@@ -192,6 +193,58 @@ def check_dkv_keys(res, q, kv, dout, scale, keys, chunk=256):
         worst = max(worst, e)
         assert e <= BF16_TOL, f"dKV of key {j} ({rows.numel()} rows): rel err {e:.3g}"
     _log(f"dKV sampled keys {list(keys)}: worst rel err {worst:.3g}")
+
+
+def spread_keys(idx, n=32):
+    """At least ``n`` distinct keys the GPU selected, spread from popular early keys to rare
+    late ones: the smallest, the middle and the largest selected key of rows spaced evenly
+    over the sequence (a row's largest key is selected by few rows, its smallest by many)."""
+    S = idx.shape[1]
+    rows = torch.linspace(0, S - 1, n).round().long().tolist()
+    picks = [(r, 0) for r in rows] + [(r, -1) for r in rows] + [(r, 1000) for r in rows[n // 2:]]
+    keys = selected_keys(idx, [(r, sl) for r, sl in picks if int((idx[0, r] >= 0).sum()) > 0])
+    assert len(keys) >= n, f"only {len(keys)} distinct keys"
+    return keys
+
+
+def check_full_reference(res, q, kv, dout, scale, q_off, *, sinks=None, row_chunk=64, key_block=256,
+                         d_keys=None):
+    """Every row and every key against the fp32 GPU reference (tests/attn_reference.py): out,
+    dQ and the head-summed mass per chunk of ``row_chunk`` rows, the LSE per element, dKV per
+    block of ``key_block`` keys (each block's error relative to that block's own norm), and
+    d sink; bf16 tolerance on each chunk / block."""
+    d_v = res["out"].shape[-1]
+    worst = dict(out=0.0, dq=0.0, mass=0.0, lse=0.0)
+
+    def dev_rel(a, b):  # on the device: the chunks stay on the GPU
+        a, b = a.double(), b.double()
+        return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+    def rows(r0, r1, ref):
+        worst["out"] = max(worst["out"], dev_rel(res["out"][0, r0:r1], ref["out"]))
+        worst["dq"] = max(worst["dq"], dev_rel(res["dq"][0, r0:r1], ref["dq"]))
+        if "mass" in res:
+            worst["mass"] = max(worst["mass"], dev_rel(res["mass"][0, r0:r1], ref["mass"]))
+        lse = res["smax"][0, r0:r1] + torch.log(res["ssum"][0, r0:r1])
+        fin = torch.isfinite(ref["lse"])
+        assert torch.equal(fin, torch.isfinite(lse)), f"rows {r0}-{r1}: rows without keys"
+        if bool(fin.any()):
+            worst["lse"] = max(worst["lse"], float((lse[fin] - ref["lse"][fin]).abs().max()))
+
+    ref = attention_reference(q, kv, res["idx"], dout, scale, d_v=d_v, q_offset=q_off, sinks=sinks,
+                              rows=row_chunk, on_rows=rows)
+    dkv = res["dkv"][0] if d_keys is None else d_keys
+    e_dkv = chunk_rel_errors(dkv, ref["dkv"], key_block)
+    msg = (f"full reference: worst {row_chunk}-row chunk out {worst['out']:.3g}, dq {worst['dq']:.3g}, "
+           f"mass {worst['mass']:.3g}, lse {worst['lse']:.3g}; dKV worst {key_block}-key block "
+           f"{float(e_dkv.max()):.3g} (median {float(e_dkv.median()):.3g})")
+    if sinks is not None:
+        e_sink = dev_rel(res["dsink"], ref["dsink"])
+        msg += f", d sink {e_sink:.3g}"
+        assert e_sink <= BF16_TOL, msg
+    _log(msg)
+    assert max(worst.values()) <= BF16_TOL, msg
+    assert float(e_dkv.max()) <= BF16_TOL, msg
 
 
 def check_kl_rows(res, qi, ki, w, blocks, q_off, eps=1e-8):
@@ -358,9 +411,12 @@ class TestC3Step:
         check_attention_rows(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, self.blocks(), 0)
 
     def test_dkv_sampled_keys(self, run):
-        # key 5: every row < 2048 selects it (popular key); the last row's largest key: few rows
-        keys = [5, 2047] + selected_keys(run["res"]["idx"], [(4096, 1000), (8000, -1), (8191, -1)])
+        # key 5: every row < 2048 selects it (popular key); a row's largest key: few rows
+        keys = sorted(set([5, 2047] + spread_keys(run["res"]["idx"])))
         check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, keys)
+
+    def test_full_reference(self, run):
+        check_full_reference(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, 0)
 
     def test_indexer_kl_rows_and_keys(self, run):
         check_kl_rows(run["res"], run["qi"], run["ki"], run["w"], self.blocks(), 0)
@@ -410,10 +466,13 @@ class TestC4CompressedStep:
             comp.append((kv_p, sc_p, ape, nw))
         pooled = [ops.compressor_pool(c[0], c[1], c[2], r) for c in comp]
         normed = [ops.compressor_pool(c[0], c[1], c[2], r, norm_weight=c[3]) for c in comp]
-        q, _, qi, _, w, dout = _draw(S, 0, self.SEED + 100)
+        # the compressed rows are k = v = the whole 512-column row (SparseAttention), so the
+        # attention runs on the kernels' 512-column variant with 512-column queries, as the
+        # benchmark's C4 step does
+        q, _, qi, _, w, dout = _draw(S, 0, self.SEED + 100, d_q=DV)
         ckv, cki = normed
-        kv = torch.nn.functional.pad(ckv, (0, DQK - DV))  # 512 value columns + 64 zero columns
-        res = run_dense_step(q, kv, qi, cki, w, dout, self.K, DQK ** -0.5, cmp_ratio=r, attn_q_offset=BIG)
+        kv = ckv
+        res = run_dense_step(q, kv, qi, cki, w, dout, self.K, DV ** -0.5, cmp_ratio=r, attn_q_offset=BIG)
         run = dict(comp=comp, pooled=pooled, normed=normed, q=q, kv=kv, qi=qi, ki=cki, w=w, dout=dout, res=res)
         yield run
         _free(run)
@@ -444,13 +503,17 @@ class TestC4CompressedStep:
         assert err <= IDX_TOL
 
     def test_attention_rows(self, run):
-        check_attention_rows(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, self.blocks(), BIG)
+        assert run["q"].shape[-1] == DV and run["kv"].shape[-1] == DV  # the 512-column kernels
+        check_attention_rows(run["res"], run["q"], run["kv"], run["dout"], DV ** -0.5, self.blocks(), BIG)
 
     def test_dkv_and_dk_i_sampled_keys(self, run):
         idx = run["res"]["idx"]
-        check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5,
-                       [0, 2047] + selected_keys(idx, [(24100, -1), (32767, -1)]))
+        check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], DV ** -0.5,
+                       sorted(set([0, 2047] + spread_keys(idx))))
         check_dk_i_keys(run["res"], run["qi"], run["ki"], run["w"], selected_keys(idx, [(24100, -1), (32767, -1)]))
+
+    def test_full_reference(self, run):
+        check_full_reference(run["res"], run["q"], run["kv"], run["dout"], DV ** -0.5, BIG)
 
     def test_indexer_kl_rows(self, run):
         check_kl_rows(run["res"], run["qi"], run["ki"], run["w"], self.blocks(), BIG)
@@ -493,8 +556,11 @@ class TestC5LongSequence:
     def test_dkv_and_dk_i_sampled_keys(self, run):
         idx = run["res"]["idx"]
         check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5,
-                       [1000] + selected_keys(idx, [(120100, -1), (131071, -1)]))
+                       sorted(set([1000] + spread_keys(idx))))
         check_dk_i_keys(run["res"], run["qi"], run["ki"], run["w"], selected_keys(idx, [(125100, -1), (131071, -1)]))
+
+    def test_full_reference(self, run):
+        check_full_reference(run["res"], run["q"], run["kv"], run["dout"], DQK ** -0.5, 0, row_chunk=128)
 
     def test_indexer_kl_rows(self, run):
         check_kl_rows(run["res"], run["qi"], run["ki"], run["w"], self.blocks(), 0)
@@ -558,3 +624,82 @@ class TestC5PackedVarlen:
 
     def test_full_size_identities(self, run):
         check_identities(run["res"], run["q"], run["kv"], run["dout"], run["qi"], run["ki"], run["w"])
+
+
+# ---------------------------------------------------------------------------
+# DeepSeek-V4 attention at the benchmark's shape: 128-token window + top-1024 of the S/4
+# compressed rows + per-head sink, 128 heads x 512 (reference models/deepseek_v4/model.py:573-623)
+# ---------------------------------------------------------------------------
+class TestV4SharedKV:
+    S, R, K, W, SEED = 8192, 4, 1024, 128, 6
+
+    @pytest.fixture(scope="class")
+    def run(self):
+        ops = _ops()
+        S, r = self.S, self.R
+        _log(f"V4: S={S} H={H} window {self.W} + top-{self.K} of {S // r} compressed rows + sink, fwd + bwd")
+        g = torch.Generator(device=DEV).manual_seed(self.SEED)
+        bf = dict(device=DEV, dtype=torch.bfloat16, generator=g)
+        q = torch.randn(1, S, H, DV, **bf)
+        ori = torch.randn(1, S, DV, **bf)
+        cmp = torch.randn(1, S // r, DV, **bf)
+        qi = torch.randn(1, S, HI, DI, **bf)
+        ki = torch.randn(1, S // r, DI, **bf)
+        w = torch.rand(1, S, HI, device=DEV, generator=g) * HI ** -0.5 * DI ** -0.5
+        sinks = torch.randn(H, device=DEV, generator=g)
+        dout = torch.randn(1, S, H, DV, **bf)
+        q8, qs = ops.quantize_fp8_per_row(qi)
+        k8, ks = ops.quantize_fp8_per_row(ki)
+        cidx, _ = ops.npu_lightning_indexer(q8, k8, w, sparse_count=self.K, sparse_mode=3, cmp_ratio=r,
+                                            query_scale=qs, key_scale=ks)
+        cidx = cidx[:, :, 0]
+        cidx = torch.where(cidx >= 0, cidx + S, cidx)  # rows of cat(ori_kv, cmp_kv)
+        scale = DV ** -0.5
+        # the path npu_sparse_attn_shared_kv takes (the bench's V4 step), with its row statistics
+        prep = ops._sharedkv_prepare(q, ori, cmp, cidx, r, self.W - 1, 0)
+        out, m2, s2 = ops._sharedkv_forward(prep, sinks, scale)
+        dq, d_ori, d_cmp, dsink = ops._sharedkv_backward(prep, out, dout, m2, s2, sinks, scale)
+        torch.cuda.synchronize()
+        res = dict(idx=prep["idx"], out=out, smax=m2, ssum=s2, dq=dq, dsink=dsink,
+                   dkv=torch.cat([d_ori, d_cmp], dim=1))
+        run = dict(q=q, kv=prep["kv"], dout=dout, sinks=sinks, res=res, scale=scale)
+        yield run
+        _free(run)
+
+    def test_index_layout(self, run):
+        idx = run["res"]["idx"][0]
+        S, W = self.S, self.W
+        assert idx.shape == (S, W + self.K)
+        s = torch.arange(S, device=DEV).view(-1, 1)
+        band = idx[:, :W].long()
+        assert bool(((band == -1) | ((band <= s) & (band > s - W))).all()), "window slots"
+        c = idx[:, W:].long()
+        assert bool(((c == -1) | ((c >= S) & (c - S < (s + 1) // self.R))).all()), "compressed slots"
+        assert int((c >= 0).sum(-1)[-1]) == self.K
+
+    def test_rows_against_oracle(self, run):
+        """Sampled rows against the fp64 oracle of SparseAttention.forward with the sink:
+        out, LSE and dQ (a row's dQ depends on its own inputs only)."""
+        res, kv_c = run["res"], run["kv"].cpu()
+        sk = run["sinks"].double().cpu()
+        worst = dict(out=0.0, lse=0.0, dq=0.0)
+        for a, b in _blocks([(0, 8), (4096, 4104), (8184, 8192)], self.S):
+            qb = run["q"][:, a:b].cpu().double().requires_grad_(True)
+            o, lse = O.sparse_attn_sink(qb, kv_c.double(), sk, res["idx"][:, a:b].cpu(), run["scale"])
+            o.backward(run["dout"][:, a:b].cpu().double())
+            glse = (res["smax"][:, a:b] + torch.log(res["ssum"][:, a:b])).cpu().double()
+            worst["out"] = max(worst["out"], rel_err(res["out"][:, a:b], o.detach()))
+            worst["lse"] = max(worst["lse"], float((glse - lse.detach()).abs().max()))
+            worst["dq"] = max(worst["dq"], rel_err(res["dq"][:, a:b], qb.grad))
+        _log(f"V4 rows: {worst}")
+        assert max(worst.values()) <= BF16_TOL, worst
+
+    def test_keys_against_oracle(self, run):
+        """dKV of 32+ sampled keys (window rows of ori_kv and compressed rows) over every row
+        that selected them, closed form with the GPU's sink-inclusive LSE."""
+        keys = spread_keys(run["res"]["idx"][:, :, self.W:])  # compressed rows (selected by the indexer)
+        keys += [5, 4000, self.S - 1]  # window keys: rows j .. j+127 select ori row j
+        check_dkv_keys(run["res"], run["q"], run["kv"], run["dout"], run["scale"], sorted(set(keys)))
+
+    def test_full_reference(self, run):
+        check_full_reference(run["res"], run["q"], run["kv"], run["dout"], run["scale"], BIG, sinks=run["sinks"])

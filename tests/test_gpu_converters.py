@@ -107,3 +107,59 @@ def test_npu_dsa_end_to_end(S, H, K, views):
     assert rel_err(qid.grad.cpu(), rdq / n) <= 1e-2
     assert rel_err(kid.grad.cpu()[:, :, 0], rdk / n) <= 1e-2
     assert rel_err(wd.grad.cpu(), rdw / n) <= 1e-2
+
+
+def test_npu_dsa_under_activation_checkpointing():
+    """The converted layer inside torch.utils.checkpoint (non-reentrant, as torchtitan's
+    activation checkpointing wraps each block): the same gradients as the plain run, bit for
+    bit, and the mass link holds no tensor between forward and backward (the attention node
+    owns its inputs through save_for_backward, so the checkpoint's hooks see them)."""
+    from unittest.mock import patch
+
+    from torch.utils.checkpoint import checkpoint
+
+    from torchtitan_npu_simulator_amd import converters as conv
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+    from torchtitan_npu_simulator_amd.converters import dsa as dsa_mod
+    from torchtitan_npu_simulator_amd.converters.dsa_indexer_loss import DSAIndexerLossAutoScaler
+
+    model = _Model()
+    conv.registry().converter_class("npu_dsa")(model_spec=SimpleNamespace(name="deepseek_v32")).convert(model)
+    sdpa = model.layers["0"].attention.inner_attention
+    S, H, K, HI, DI = 256, 32, 64, 64, 128
+    g = torch.Generator().manual_seed(11)
+    q = (torch.randn(1, H, S, 576, generator=g) / 24).bfloat16().to(DEV)
+    kv = torch.randn(1, 1, S, 576, generator=g).bfloat16().to(DEV)
+    qi = torch.randn(1, S, HI, DI, generator=g).bfloat16().to(DEV)
+    ki = torch.randn(1, S, 1, DI, generator=g).bfloat16().to(DEV)
+    w = (torch.rand(1, S, HI, generator=g) * HI ** -0.5 * DI ** -0.5).to(DEV)
+    dout = torch.randn(1, H, S, 512, generator=g).to(DEV)
+    links = []
+
+    class _Recorded(ops.MassLink):
+        __slots__ = ()
+
+        def __init__(self):
+            super().__init__()
+            links.append(self)
+
+    def run(ckpt):
+        leaves = [t.clone().requires_grad_(True) for t in (q, kv, qi, ki, w)]
+
+        def layer(qq, kk, qii, kii, ww):
+            loss, out = sdpa(qq, kk, kk[..., :512], None, 576 ** -0.5, qii, kii, ww, None, K)
+            return DSAIndexerLossAutoScaler.apply(out, loss)
+
+        y = checkpoint(layer, *leaves, use_reentrant=False) if ckpt else layer(*leaves)
+        link = links[-1]
+        assert not any(isinstance(getattr(link, a), torch.Tensor) for a in ops.MassLink.__slots__)
+        (y.float() * dout).sum().backward()
+        torch.cuda.synchronize()
+        return [t.grad for t in leaves]
+
+    with patch.object(dsa_mod.npu, "MassLink", _Recorded):
+        plain = run(False)
+        ckpt = run(True)
+    for a, b in zip(plain, ckpt):
+        assert torch.equal(a, b)
+    assert all(float(t.abs().sum()) > 0 for t in plain)

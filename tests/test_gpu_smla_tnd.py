@@ -221,3 +221,43 @@ def test_packed_lightning_indexer_module():
         pos = torch.arange(n).view(n, 1)
         ok = (rows < 0) | (rows < (pos + 1) // ratio)
         assert bool(ok.all())
+
+
+def test_packed_kl_loss_grad_returns_indexer_softmax():
+    """softmax_out of ``sparse_lightning_indexer_kl_loss_grad`` (reference npu_smla.py:584-602):
+    per row, the softmax of the indexer scores over the row's usable compressed slots (0 at
+    the others), against the oracle's scores gathered at the same slots; the logged loss the
+    converter builds from it (``_compute_li_loss``) equals the per-row losses the kernel
+    returns, mean over rows."""
+    from torchtitan_npu_simulator_amd import smla_ops
+    from torchtitan_npu_simulator_amd.converters.npu_smla import _compute_li_loss
+
+    ratio, K = 4, 16
+    lengths = [96, 300, 7, 161]
+    masks, cu_q, cu_c, n_cmp = _masks(lengths, ratio)
+    _, _, _, _, _, local, qi, ki, w = _case(lengths, ratio, 16, 512, K, torch.bfloat16, seed=5)
+    T = sum(lengths)
+    g = torch.Generator().manual_seed(9)
+    l1 = torch.rand(T, K, generator=g) * (local >= 0)
+    l1[3] = 0.0  # a row with no teacher mass
+    dq, dk, dw, sm, loss_rows = smla_ops.sparse_lightning_indexer_kl_loss_grad(
+        q=qi.to(DEV), k=ki.to(DEV).unsqueeze(1), w=w.to(DEV), sparse_indices=local.to(DEV),
+        attn_softmax_l1_norm=l1.to(DEV), cmp_residual_k=masks.cmp_residual_k[ratio], cu_seqlens_q=masks.cu_seqlens_q,
+        cu_seqlens_k=masks.cu_seqlens_cmp_kv[ratio], cmp_ratio=ratio, eps=1e-10, return_loss_rows=True)
+    sm = sm.cpu()
+    assert sm.shape == (T, K)
+    for i, n in enumerate(lengths):
+        s0, s1, c0, c1 = cu_q[i], cu_q[i + 1], cu_c[i], cu_c[i + 1]
+        if c1 == c0:
+            assert float(sm[s0:s1].abs().max()) == 0.0
+            continue
+        sc = O.indexer_scores(qi[s0:s1].unsqueeze(0), ki[c0:c1].unsqueeze(0), w[s0:s1].unsqueeze(0),
+                              cmp_ratio=ratio)[0].double()
+        lcl = local[s0:s1].long()
+        ok = lcl >= 0
+        sel = torch.gather(sc, 1, lcl.clamp_min(0)).masked_fill(~ok, float("-inf"))
+        ref = torch.softmax(sel, dim=-1).nan_to_num(0.0)  # rows with no usable slot: all 0
+        assert (sm[s0:s1].double() - ref).abs().max() <= 1e-5
+        assert float(sm[s0:s1][~ok].abs().max() if (~ok).any() else 0.0) == 0.0
+    logged = _compute_li_loss(sm.to(DEV), l1.to(DEV), 1.0)
+    assert abs(float(logged) - float(loss_rows.sum()) / T) <= 1e-4 * abs(float(loss_rows.sum()) / T) + 1e-7

@@ -68,3 +68,21 @@ def test_device_metadata_batch_rows_with_padding_and_mtp():
     bad = tnd.build_smla_attention_masks_device(pos.to(DEV), args)
     with pytest.raises(ValueError, match="contiguous before padding"):
         bad.host()
+
+
+def test_device_metadata_reference_known_answers():
+    """The device builder on the reference's own known-answer inputs
+    (tests/unit_tests/models/test_deepseek_v4_tnd.py:65-79 and :140-165), checked against
+    those answers directly rather than through the host builder."""
+    meta = tnd.build_smla_attention_masks_device(torch.tensor([0, 1, 2, 3, 0, 1, 2, 3], device=DEV),
+                                                 _args(ratios=(4, 128), mtp_ratio=1)).host()
+    torch.testing.assert_close(meta.block_starts_by_ratio[4].cpu().long(), torch.tensor([0, 4]))
+    assert meta.block_starts_by_ratio[128].numel() == 0
+    assert meta.max_seqlen_q == 4
+    assert meta.max_seqlen_cmp_kv == {4: 1, 128: 0}
+
+    meta = tnd.build_smla_attention_masks_device(torch.tensor([0, 1, 2, 3, 0, 1], dtype=torch.int32, device=DEV),
+                                                 _args(ratios=(1,), mtp_ratio=1)).host()
+    torch.testing.assert_close(meta.cu_seqlens_q.cpu().long(), torch.tensor([0, 4, 6]))
+    torch.testing.assert_close(meta.cu_seqlens_ori_kv.cpu().long(), torch.tensor([0, 4, 6]))
+    assert meta.batch_size == 2 and meta.seq_len == 6

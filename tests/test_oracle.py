@@ -213,9 +213,17 @@ def test_sparse_fwd_gathered_equals_dense_mask_form():
     w = torch.rand(1, S, HI, generator=g)
     loss, out, sel, valid = O.dsv32_sdpa_dense(q, k, v, qi, ki, w, K, 0.1)
     idx = torch.where(valid, sel, torch.full_like(sel, -1)).int()
-    out_g, _ = O.sparse_mla_fwd(q.transpose(1, 2), k[:, 0], idx, 0.1)
+    out_g, lse_g = O.sparse_mla_fwd(q.transpose(1, 2), k[:, 0], idx, 0.1)
     torch.testing.assert_close(out_g[0], out[0].transpose(0, 1))
-    assert torch.isfinite(loss)
+    assert torch.isfinite(loss) and float(loss) > 0
+    # the loss as the reference writes it (dense get_attn_scores, gather at the selection,
+    # DSAIndexerLoss mean over B*S tokens) equals the gathered form the GPU is checked with
+    # (mass from the sparse forward's LSE, KL summed over tokens) divided by B*S
+    _, _, _, loss_sum = O.indexer_kl_loss_grad(q.transpose(1, 2), k[:, 0], qi, ki[:, :, 0], w, idx, lse_g, 0.1)
+    torch.testing.assert_close(loss.double(), loss_sum.double() / (1 * S), rtol=2e-5, atol=0)
+    mass = O.attn_mass(q.transpose(1, 2), k[:, 0], idx, lse_g, 0.1)
+    _, _, _, loss_from_mass = O.indexer_kl_from_mass(qi, ki[:, :, 0], w, idx, mass)
+    torch.testing.assert_close(loss_from_mass, loss_sum)
 
 
 def test_sparse_bwd_gradcheck_and_closed_form():

@@ -219,3 +219,18 @@ def test_sharedkv_ops_accept_tnd_layout_arguments():
         ops._check_sharedkv_args("BSND", "BSND", None, (), (torch.tensor([0, 4]), None, None), 4, 3)
     with pytest.raises(NotImplementedError, match="layouts"):
         ops._check_sharedkv_args("TND", "BSND", None, (), (None,), 4, 3)
+
+
+def test_grad_metadata_record_kind_matches_on_host_and_device():
+    """The backward record says kind 2 in the host tuple and in the int32 record alike."""
+    from torchtitan_npu_simulator_amd import smla_ops
+
+    cu = torch.tensor([0, 5, 9], dtype=torch.int32)
+    kw = dict(cu_seqlens_q=cu, cu_seqlens_ori_kv=cu, batch_size=2, max_seqlen_q=5, max_seqlen_ori_kv=5,
+              num_heads_q=8, head_dim=512)
+    fwd = smla_ops.sparse_flash_mla_metadata(**kw)
+    bwd = smla_ops.sparse_flash_mla_grad_metadata(**kw)
+    assert fwd._dsa_record[1] == 1 and int(fwd[1]) == 1
+    assert bwd._dsa_record[1] == 2 and int(bwd[1]) == 2
+    assert bwd._dsa_record[2:] == fwd._dsa_record[2:]
+    assert torch.equal(bwd[2:], fwd[2:])

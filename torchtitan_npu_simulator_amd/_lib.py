@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -72,6 +72,11 @@ _SIGNATURES = {
     "dsa_indexer_kl_grad": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
          _f32, _f32, _vp, _vp],
+        _i32,
+    ),
+    "dsa_indexer_kl_grad_softmax": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _f32, _f32, _f32, _vp, _vp],
         _i32,
     ),
     "dsa_compressor_fwd": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _i64, _vp,

@@ -77,12 +77,12 @@ class LILossTrain(torch.autograd.Function):
 class _LinkedIndexerLoss(torch.autograd.Function):
     """LILossTrain for a layer's own attention (BSND, sparse_mode 3): zero in forward; in
     backward the KL loss and the indexer gradients, scaled by the upstream gradient, with the
-    target mass from ``link`` (set by the attention backward; recomputed from the saved
-    forward statistics only if that backward has not run)."""
+    target mass from ``link`` (set by the attention backward; recomputed from the attention
+    node's saved forward statistics only if that backward has not run)."""
 
     @staticmethod
     def forward(ctx, query_indexer, key_indexer, weights, sparse_indices, link, layer_number, num_layers):
-        ctx.save_for_backward(query_indexer, key_indexer, weights)  # (the indices travel in ``link``)
+        ctx.save_for_backward(query_indexer, key_indexer, weights, sparse_indices)
         ctx.link = link
         ctx.layer_number = layer_number
         ctx.num_layers = num_layers
@@ -90,18 +90,14 @@ class _LinkedIndexerLoss(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad):
-        query_indexer, key_indexer, weights = ctx.saved_tensors
+        query_indexer, key_indexer, weights, idx = ctx.saved_tensors
         link = ctx.link
-        q, kv3, idx, smax, ssum, scale, q_off = link.fwd
         mass = link.mass
         if mass is None:  # (a backward of the loss alone: the attention node did not run)
-            mass = npu.attn_mass(q, kv3, idx, smax, ssum, scale, q_offset=q_off)
-        link.mass = None
-        link.fwd = None
-        ctx.link = None
+            mass = link.recompute_mass()
         g = grad if isinstance(grad, torch.Tensor) else float(grad)
         dq_i, dk_i, dw, loss_rows = npu.indexer_kl_grad_from_mass(query_indexer, key_indexer, weights, idx, mass,
-                                                                  q_offset=q_off, loss_scale=1.0, eps=1e-8,
+                                                                  q_offset=link.q_offset, loss_scale=1.0, eps=1e-8,
                                                                   grad_scale=g)
         bsz, sq = query_indexer.shape[0], query_indexer.shape[1]
         DSAIndexerLossLoggingHelper.save_loss_to_tracker(loss_rows.sum() / (bsz * sq), ctx.layer_number,
@@ -143,8 +139,8 @@ def dsa_forward(self, q, k, v, attn_mask=None, scale=None, q_indexer=None, k_ind
         # k, the absorb-mode alias), so no split / re-concatenation is made either way.
         bsz, sq = q.shape[0], q.shape[1]
         link = npu.MassLink()
-        z = _LinkedIndexerLoss.apply(q_indexer, k_indexer, weights, topk_indices.to(torch.int32), link,
-                                     self.layer_number, self.num_layers)
+        idx3 = topk_indices.reshape(bsz, sq, -1).to(torch.int32)
+        z = _LinkedIndexerLoss.apply(q_indexer, k_indexer, weights, idx3, link, self.layer_number, self.num_layers)
         output, _, _ = npu.sparse_flash_attention_linked(q, k, topk_indices, scale, z, link, d_v=nope)
         return z / (bsz * sq), output.transpose(1, 2)
     q_nope, q_pe = torch.split(q, [nope, rope], dim=-1)

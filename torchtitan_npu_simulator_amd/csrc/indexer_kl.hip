@@ -62,7 +62,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
                        const int32_t* __restrict__ idx, const float* __restrict__ mass, float* __restrict__ dq,
                        float* __restrict__ dw, float* __restrict__ loss_rows, uint16_t* __restrict__ ck, int S,
                        int s_k, int K, int64_t q_offset, float loss_scale, float eps, float grad_scale,
-                       const float* __restrict__ grad_scale_dev, int row0) {
+                       const float* __restrict__ grad_scale_dev, int row0, float* __restrict__ softmax_out) {
   __shared__ u32x4 kt[2][kTileC];           // gathered key rows [64][16 chunks], swizzled
   __shared__ u32x4 qs[kH * kRowC];          // q of the row [64 heads][16 chunks] (phase 3), swizzled
   extern __shared__ float iv[];             // I_j, then g_j: K rounded up to whole blocks
@@ -288,7 +288,10 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     const int j = tid + 256 * u;
     const float t = okv[u] ? fmaxf(mv[u], 0.f) * rzc : 0.f;
     const float sm = okv[u] ? __builtin_amdgcn_exp2f((xv[u] - lse) * kLog2e) : 0.f;
-    if (j < K) iv[j] = gs * (sm * T - t);
+    if (j < K) {
+      iv[j] = gs * (sm * T - t);
+      if (softmax_out) softmax_out[row_id * K + j] = sm;  // the indexer's distribution over the slots
+    }
   }
 
   // ---------------- phase 3: gradients ----------------
@@ -495,7 +498,7 @@ indexer_kl_generic_kernel(const uint16_t* __restrict__ qi, const uint16_t* __res
                           const float* __restrict__ mass, float* __restrict__ dq, float* __restrict__ dk,
                           float* __restrict__ dw, float* __restrict__ loss_rows, int S, int s_k, int H, int D, int K,
                           int64_t q_offset, float loss_scale, float eps, float grad_scale,
-                          const float* __restrict__ grad_scale_dev) {
+                          const float* __restrict__ grad_scale_dev, float* __restrict__ softmax_out) {
   extern __shared__ float sh[];  // iv[K]
   __shared__ float red[4];
   const int tok = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
@@ -550,6 +553,7 @@ indexer_kl_generic_kernel(const uint16_t* __restrict__ qi, const uint16_t* __res
     const float t = ok ? fmaxf(mrow[j], 0.f) / zc : 0.f;
     const float sm = ok ? expf(iv[j] - lse) : 0.f;
     iv[j] = gs * (sm * T - t);
+    if (softmax_out) softmax_out[row_id * K + j] = sm;
   }
   __syncthreads();
   // dq[h][d], dw[h]: thread per (h, d); dk by atomics
@@ -610,6 +614,18 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
                                    int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset,
                                    float loss_scale, float eps, float grad_scale, const float* grad_scale_dev,
                                    void* stream) {
+  return dsa_indexer_kl_grad_softmax(q_idx, k_idx, w, indices, mass, dq_idx, dk_idx_accum, dw, loss_rows, nullptr,
+                                     workspace, workspace_bytes, batch, s_q, s_k, n_heads, head_dim, topk, q_offset,
+                                     loss_scale, eps, grad_scale, grad_scale_dev, stream);
+}
+
+extern "C" int dsa_indexer_kl_grad_softmax(const void* q_idx, const void* k_idx, const float* w,
+                                           const int32_t* indices, const float* mass, float* dq_idx,
+                                           float* dk_idx_accum, float* dw, float* loss_rows, float* softmax_out,
+                                           void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q,
+                                           int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t topk,
+                                           int64_t q_offset, float loss_scale, float eps, float grad_scale,
+                                           const float* grad_scale_dev, void* stream) {
   using namespace dsa;
   if (!q_idx || !k_idx || !w || !indices || !mass || !dq_idx || !dk_idx_accum || !dw || !loss_rows)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: null pointer");
@@ -625,7 +641,7 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
     indexer_kl_generic_kernel<<<grid, 256, topk * 4, st>>>(
         (const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass, dq_idx, dk_idx_accum, dw, loss_rows,
         (int)s_q, (int)s_k, (int)n_heads, (int)head_dim, (int)topk, q_offset, loss_scale, eps, grad_scale,
-        grad_scale_dev);
+        grad_scale_dev, softmax_out);
     return check_launch("dsa_indexer_kl_grad(generic)");
   }
   if (!workspace) return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: workspace required");
@@ -650,7 +666,8 @@ extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const f
       const size_t iv_bytes = (size_t)((topk + kB - 1) / kB * kB) * sizeof(float);
       indexer_kl_mfma_kernel<<<grid, 256, iv_bytes, st>>>((const uint16_t*)q_idx, (const uint16_t*)k_idx, w, indices, mass,
                                                    dq_idx, dw, loss_rows, ck, (int)s_q, (int)s_k, (int)topk, q_offset,
-                                                   loss_scale, eps, grad_scale, grad_scale_dev, (int)r0);
+                                                   loss_scale, eps, grad_scale, grad_scale_dev, (int)r0,
+                                                   softmax_out);
     }
     if (int rc = check_launch("dsa_indexer_kl_grad(mfma)")) return rc;
     for (int b = 0; b < (int)batch; ++b)

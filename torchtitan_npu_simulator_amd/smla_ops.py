@@ -88,11 +88,11 @@ def sparse_flash_mla_metadata(*, cu_seqlens_q=None, cu_seqlens_ori_kv=None, cu_s
                               max_seqlen_q=0, max_seqlen_ori_kv=0, max_seqlen_cmp_kv=0, num_heads_q=1,
                               num_heads_kv=1, head_dim=512, cmp_topk=0, cmp_ratio=1, ori_mask_mode=4, cmp_mask_mode=3,
                               ori_win_left=127, ori_win_right=0, layout_q="TND", layout_kv="TND", has_ori_kv=True,
-                              has_cmp_kv=False, ori_topk=None):
+                              has_cmp_kv=False, ori_topk=None, _kind=1):
     """Record of a packed attention problem (the keywords of the reference's
     ``_sparse_attention_metadata_kwargs``, npu_smla.py:165-189).  ``max_seqlen_cmp_kv`` is
     the slot count of the every-causal-block rule (ratio 128); it is read from
-    cu_seqlens_cmp_kv once when not given."""
+    cu_seqlens_cmp_kv once when not given.  (``_kind``: 1 forward, 2 backward record.)"""
     _check_tnd(layout_q, layout_kv)
     _check_masks(ori_mask_mode, cmp_mask_mode)
     if num_heads_kv != 1:
@@ -107,14 +107,13 @@ def sparse_flash_mla_metadata(*, cu_seqlens_q=None, cu_seqlens_ori_kv=None, cu_s
     fields = [num_heads_q, num_heads_kv, head_dim, batch_size, max_seqlen_q, max_seqlen_ori_kv, max_seqlen_cmp_kv,
               cmp_topk, cmp_ratio, ori_mask_mode, cmp_mask_mode, ori_win_left, ori_win_right, _LAYOUTS[layout_q],
               _LAYOUTS[layout_kv], int(bool(has_ori_kv)), int(bool(has_cmp_kv))]
-    return _record(1, fields, host, _device_of(cu_seqlens_q, cu_seqlens_ori_kv))
+    return _record(int(_kind), fields, host, _device_of(cu_seqlens_q, cu_seqlens_ori_kv))
 
 
 def sparse_flash_mla_grad_metadata(**kwargs):
-    """Record of the backward of the same problem (same keywords plus ``ori_topk``)."""
-    meta = sparse_flash_mla_metadata(**kwargs)
-    meta._dsa_record = (meta._dsa_record[0], 2) + meta._dsa_record[2:]
-    return meta
+    """Record of the backward of the same problem (same keywords plus ``ori_topk``): kind 2
+    in both the host tuple and the device record."""
+    return sparse_flash_mla_metadata(**kwargs, _kind=2)
 
 
 def _check_attn_metadata(metadata, query, cmp_ratio, ori_win_left, ori_win_right):
@@ -253,10 +252,11 @@ def sparse_lightning_indexer_kl_loss_grad(*, q, k, w, sparse_indices, attn_softm
     ``attn_softmax_l1_norm`` [T,K], row loss sum(l1) * KL(t || softmax(I)) (rows with
     sum(l1) <= eps add nothing) - DSAIndexerLoss with eps 1e-10 (dsa_indexer_loss.py:138-160),
     the form ``_compute_li_loss`` (npu_smla.py:405-420) logs.  ``grad_scale`` (a float or a
-    device scalar) multiplies the gradients inside the kernel.  ``softmax_out`` (the
-    indexer's distribution over the slots) is not formed by this build: it is None, and
-    ``return_loss_rows`` appends the per-row losses [T] fp32 instead (what the logged
-    loss is built from).  Gradients are fp32 in the shapes of q / k / w.
+    device scalar) multiplies the gradients inside the kernel.  ``softmax_out`` [T,K] fp32 is
+    the indexer's distribution over the slots, softmax of I over the usable slots and 0 at
+    the others (written by the KL kernel from the row statistics it forms anyway);
+    ``return_loss_rows`` appends the per-row losses [T] fp32.  Gradients are fp32 in the
+    shapes of q / k / w.
     """
     _check_tnd(layout_q, layout_k)
     if int(mask_mode) != 3:
@@ -269,9 +269,9 @@ def sparse_lightning_indexer_kl_loss_grad(*, q, k, w, sparse_indices, attn_softm
     gidx = npu.sharedkv_tnd_indices(cu_seqlens_q, cu_seqlens_q, T, 0, q.device, cmp_ratio=int(cmp_ratio),
                                     cu_seqlens_cmp_kv=cu_seqlens_k, cmp_residual_kv=cmp_residual_k, cmp_indices=idx,
                                     window=False)
-    dq, dk, dw, loss_rows = npu.indexer_kl_grad_from_mass(
+    dq, dk, dw, loss_rows, sm = npu.indexer_kl_grad_from_mass(
         q.unsqueeze(0), kc.unsqueeze(0), w.float().unsqueeze(0), gidx.unsqueeze(0),
         attn_softmax_l1_norm.float().reshape(1, T, -1).contiguous(), q_offset=npu._NO_MASK_OFFSET, loss_scale=1.0,
-        eps=eps, grad_scale=grad_scale)
-    res = (dq.reshape(q.shape), dk.reshape(k.shape), dw.reshape(w.shape), None)
+        eps=eps, grad_scale=grad_scale, return_softmax=True)
+    res = (dq.reshape(q.shape), dk.reshape(k.shape), dw.reshape(w.shape), sm.reshape(T, -1))
     return res + (loss_rows.reshape(T),) if return_loss_rows else res

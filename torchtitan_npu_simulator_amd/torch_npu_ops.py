@@ -27,8 +27,10 @@ get no selection (-1) and keys past its key length are never candidates.
 
 from __future__ import annotations
 
+import itertools
 import math
 import warnings
+import weakref
 
 import torch
 
@@ -80,6 +82,57 @@ def _resolve_q_offset(sparse_mode: int, s_q: int, s_k_tokens: int, q_offset: int
     if sparse_mode == 0:
         return _NO_MASK_OFFSET
     raise ValueError(f"sparse_mode={sparse_mode} is not supported (0 or 3)")
+
+
+def _band_cuts(sparse_mode: int, s_q: int, s_k: int, q_off: int, pre_tokens: int, next_tokens: int) -> bool:
+    """Whether the pre_tokens / next_tokens band removes any key the mode's own rule admits.
+
+    The band of query row s is t in [a(s) - pre_tokens, a(s) + next_tokens] with a(s) = s
+    (sparse_mode 0, top-left aligned) or s + q_off (sparse_mode 3, the bottom-right causal
+    diagonal, which also bounds t from above)."""
+    pre, nxt = int(pre_tokens), int(next_tokens)
+    if sparse_mode == 3:
+        return pre < s_q - 1 + q_off or nxt < 0
+    return pre < s_q - 1 or nxt < s_k - 1
+
+
+def _band_mask_indices(idx, sparse_mode: int, q_off: int, pre_tokens: int, next_tokens: int):
+    """Slot indices [B,S,K] with every key outside the row's band set to -1 (see _band_cuts)."""
+    S = idx.shape[1]
+    a = torch.arange(S, device=idx.device, dtype=torch.int64).view(1, S, 1)
+    if sparse_mode == 3:
+        a = a + int(q_off)
+    t = idx.long()
+    ok = (t >= a - int(pre_tokens)) & (t <= a + int(next_tokens))
+    return torch.where(ok, idx, torch.full_like(idx, -1))
+
+
+def _banded_indexer(query, k3, weights, K, query_scale, key_scale, sparse_mode, q_off, pre_tokens, next_tokens,
+                    index_offset, return_value):
+    """Indexer + top-k under a band that cuts keys: scores per row chunk (dsa_indexer_fwd_ws),
+    keys below the band's lower edge set to NaN (never a candidate), the upper edge given to
+    dsa_topk as its causal offset."""
+    B, S = query.shape[:2]
+    s_k = k3.shape[1]
+    pre, nxt = int(pre_tokens), int(next_tokens)
+    up_off = min(q_off, q_off + nxt) if sparse_mode == 3 else min(nxt, _NO_MASK_OFFSET)
+    lo_off = (q_off if sparse_mode == 3 else 0) - pre
+    idx = torch.empty(B, S, K, dtype=torch.int32, device=query.device)
+    vals = torch.empty(B, S, K, dtype=torch.float32, device=query.device) if return_value else None
+    rows = max(1, min(S, _SCORE_BUDGET_BYTES // (4 * max(1, s_k) * B)))
+    t = torch.arange(s_k, device=query.device).view(1, 1, s_k)
+    for r0 in range(0, S, rows):
+        r1 = min(S, r0 + rows)
+        qs = None if query_scale is None else query_scale[:, r0:r1]
+        sc = indexer_scores(query[:, r0:r1], k3, weights[:, r0:r1], q_scale=qs, k_scale=key_scale,
+                            q_offset=r0 + up_off)
+        lo = torch.arange(r0, r1, device=query.device).view(1, -1, 1) + lo_off
+        sc.masked_fill_(t < lo, float("nan"))
+        i_c, v_c = topk_select(sc, K, q_offset=r0 + up_off, index_offset=index_offset, return_values=return_value)
+        idx[:, r0:r1] = i_c
+        if return_value:
+            vals[:, r0:r1] = v_c
+    return idx, vals
 
 
 def to_cu_seqlens(cu_seqlens=None, actual_seq_lengths=None, total=None) -> list[int]:
@@ -240,10 +293,27 @@ def npu_lightning_indexer(
     B, S, H, D = query.shape
     s_k = k3.shape[1]
     q_off = _resolve_q_offset(sparse_mode, S, s_k * cmp_ratio, q_offset)
-    idx, vals = lightning_indexer(query, k3, weights, int(sparse_count), query_scale=query_scale,
-                                  key_scale=key_scale, q_offset=q_off, cmp_ratio=cmp_ratio, index_offset=index_offset,
-                                  return_value=return_value)
+    if _band_cuts(sparse_mode, S, s_k, q_off, pre_tokens, next_tokens):
+        if int(cmp_ratio) != 1:
+            raise NotImplementedError("a pre_tokens / next_tokens band over compressed keys (cmp_ratio > 1)")
+        idx, vals = _banded_indexer(query, k3, weights, int(sparse_count), query_scale, key_scale, sparse_mode, q_off,
+                                    pre_tokens, next_tokens, index_offset, return_value)
+    else:
+        idx, vals = lightning_indexer(query, k3, weights, int(sparse_count), query_scale=query_scale,
+                                      key_scale=key_scale, q_offset=q_off, cmp_ratio=cmp_ratio,
+                                      index_offset=index_offset, return_value=return_value)
     return idx.unsqueeze(2), (vals.to(_values_dtype(query)).unsqueeze(2) if return_value else None)
+
+
+def lightning_indexer_workspace_bytes(lib, B, S, s_k, H, D, dt, budget=None) -> int:
+    """Workspace of one dsa_lightning_indexer call under a score budget (default
+    ``_SCORE_BUDGET_BYTES``): every row of every batch at once when they fit, else one batch
+    at a time in chunks of as many rows as fit (the C entry picks the same split from the
+    workspace size it is given)."""
+    budget = _SCORE_BUDGET_BYTES if budget is None else int(budget)
+    if B * S * s_k * 4 <= budget:
+        return int(lib.dsa_lightning_indexer_workspace_size(B, S, s_k, H, D, dt, S))
+    return int(lib.dsa_lightning_indexer_workspace_size(1, S, s_k, H, D, dt, max(1, budget // (4 * s_k))))
 
 
 def lightning_indexer(query, key, weights, k, *, query_scale=None, key_scale=None, q_offset=0, cmp_ratio=1,
@@ -269,8 +339,7 @@ def lightning_indexer(query, key, weights, k, *, query_scale=None, key_scale=Non
     dt = _lib.dtype_code(q.dtype)
     idx = torch.empty(B, S, k, dtype=torch.int32, device=q.device)
     vals = torch.empty(B, S, k, dtype=torch.float32, device=q.device) if return_value else None
-    max_rows = S if B * S * s_k * 4 <= _SCORE_BUDGET_BYTES else max(1, _SCORE_BUDGET_BYTES // (4 * s_k))
-    ws_bytes = int(lib.dsa_lightning_indexer_workspace_size(B, S, s_k, H, D, dt, max_rows))
+    ws_bytes = lightning_indexer_workspace_bytes(lib, B, S, s_k, H, D, dt)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     check(
         lib.dsa_lightning_indexer(ptr(q), ptr(qs), ptr(kk), ptr(ks), ptr(w), ptr(idx), ptr(vals), dt, B, S, s_k, H, D,
@@ -602,15 +671,31 @@ class _SparseFlashAttention(torch.autograd.Function):
 
 class MassLink:
     """Hands the head-summed attention mass [B,S,K] from a layer's attention backward to the
-    same layer's indexer-loss backward, so the loss's target is not recomputed.  ``fwd``
-    keeps what a recompute would need (q, kv, indices, softmax_max, softmax_sum, scale,
-    q_offset) for a backward in which the attention node does not run first."""
+    same layer's indexer-loss backward, so the loss's target is not recomputed.
 
-    __slots__ = ("mass", "fwd")
+    The link holds no tensor between forward and backward: the attention node owns its
+    inputs through ``save_for_backward`` (so saved-tensor hooks, and with them activation
+    checkpointing, see them), and ``attn`` is only a weak reference to that node, through
+    which a backward of the loss alone (attention node not run) reaches the saved forward
+    statistics.  ``mass`` is set by each run of the attention backward and kept until the
+    graph is freed, so a second backward with ``retain_graph=True`` finds it again."""
+
+    __slots__ = ("mass", "attn", "scale", "q_offset")
 
     def __init__(self):
         self.mass = None
-        self.fwd = None
+        self.attn = None
+        self.scale = None
+        self.q_offset = 0
+
+    def recompute_mass(self):
+        """The mass from the attention node's saved forward statistics (``dsa_attn_mass``)."""
+        node = self.attn() if self.attn is not None else None
+        if node is None:
+            raise RuntimeError("the indexer loss of this DSA layer takes its target from the layer's attention, "
+                               "whose autograd node is gone; backpropagate through the attention output as well")
+        q, kv3, indices, _out, smax, ssum = node.saved_tensors
+        return attn_mass(q, kv3, indices, smax, ssum, self.scale, q_offset=self.q_offset)
 
 
 class _SparseFlashAttentionLinked(torch.autograd.Function):
@@ -630,7 +715,9 @@ class _SparseFlashAttentionLinked(torch.autograd.Function):
         ctx.q_offset = q_offset
         ctx.kv_shape = key.shape
         ctx.link = link
-        link.fwd = (q, kv3, indices, smax, ssum, scale, q_offset)
+        link.attn = weakref.ref(ctx)  # (the node itself; no tensor is kept in the link)
+        link.scale = scale
+        link.q_offset = q_offset
         ctx.mark_non_differentiable(smax, ssum)
         return out, smax, ssum
 
@@ -640,7 +727,6 @@ class _SparseFlashAttentionLinked(torch.autograd.Function):
         dq, dkv, mass = sparse_mla_bwd(q, kv3, indices, out, dout.contiguous(), smax, ssum, ctx.scale,
                                        q_offset=ctx.q_offset, return_mass=True)
         ctx.link.mass = mass
-        ctx.link = None
         return dq, dkv.to(kv3.dtype).reshape(ctx.kv_shape), None, None, None, None, None, None
 
 
@@ -1378,7 +1464,9 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     if layout != "BSND":
         raise NotImplementedError(f"layout {layout} (BSND or TND)")
     if actual_seq_qlen is not None or actual_seq_klen is not None:
-        raise NotImplementedError("BSND with actual_seq_*: pack the batch as TND instead")
+        return _kl_loss_bsnd_lengths(query, key, query_index, key_index, weight, sparse_indices, softmax_max,
+                                     softmax_sum, scale_value, query_rope, key_rope, actual_seq_qlen, actual_seq_klen,
+                                     sparse_mode, cmp_ratio, q_offset, loss_scale, eps, grad_scale, out_dtypes)
     q = _cat_last(query, query_rope) if query_rope is not None else query.contiguous()
     kv = _cat_last(key, key_rope) if key_rope is not None else key.contiguous()
     B, S, H, D = q.shape
@@ -1389,10 +1477,63 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     else:
         q_off = _resolve_q_offset(sparse_mode, S, s_kv, q_offset)
     idx = sparse_indices.reshape(B, S, -1).to(torch.int32).contiguous()
+    if int(cmp_ratio) == 1 and _band_cuts(sparse_mode, S, s_kv, q_off, pre_tokens, next_tokens):
+        # selected keys outside the band count as unusable slots in the target and the student
+        idx = _band_mask_indices(idx, sparse_mode, q_off, pre_tokens, next_tokens).contiguous()
+    elif int(cmp_ratio) != 1 and (int(pre_tokens) < s_kv * int(cmp_ratio) or int(next_tokens) < 0):
+        raise NotImplementedError("a pre_tokens / next_tokens band over compressed keys (cmp_ratio > 1)")
     mass = attn_mass(q, kv3, idx, softmax_max, softmax_sum, scale_value, q_offset=q_off)
     dq_i, dk_i, dw, loss_rows = indexer_kl_grad_from_mass(query_index, key_index, weight, idx, mass, q_offset=q_off,
                                                           loss_scale=loss_scale, eps=eps, grad_scale=grad_scale)
     return (dq_i.to(out_dtypes[0]), dk_i.reshape(key_index.shape).to(out_dtypes[1]), dw.to(out_dtypes[2]),
+            loss_rows.sum().reshape(1))
+
+
+def _kl_loss_bsnd_lengths(query, key, query_index, key_index, weight, sparse_indices, softmax_max, softmax_sum,
+                          scale_value, query_rope, key_rope, len_q, len_k, sparse_mode, cmp_ratio, q_offset,
+                          loss_scale, eps, grad_scale, out_dtypes):
+    """BSND with per-batch valid lengths (``actual_seq_qlen`` / ``actual_seq_klen``, the
+    binding's actual_seq_lengths_query / _key): batch b is one sequence of its first len_q[b]
+    query rows and len_k[b] key rows, causal bottom-right within those lengths (sparse_mode 3).
+    The valid rows are packed into one TND batch for the varlen kernels and the gradients
+    scattered back; padded query rows and keys get zero gradients and add no loss."""
+    if sparse_mode != 3 or q_offset is not None or int(cmp_ratio) != 1:
+        raise NotImplementedError("BSND with actual sequence lengths runs the per-sequence causal rule "
+                                  "(sparse_mode=3, cmp_ratio=1) only")
+    q = _cat_last(query, query_rope) if query_rope is not None else query.contiguous()
+    kv = _cat_last(key, key_rope) if key_rope is not None else key.contiguous()
+    B, S, H, D = q.shape
+    kv3 = kv.reshape(B, kv.shape[1], D)
+    s_k = kv3.shape[1]
+    ki3 = key_index.reshape(B, key_index.shape[1], key_index.shape[-1])
+
+    def _lens(v, n):
+        vals = [n] * B if v is None else [int(x) for x in (v.tolist() if isinstance(v, torch.Tensor) else v)]
+        if len(vals) != B or any(not 0 <= x <= n for x in vals):
+            raise ValueError(f"actual sequence lengths {vals} do not fit B={B}, length {n}")
+        return vals
+
+    lq, lk = _lens(len_q, S), _lens(len_k, s_k)
+    rows_q = torch.cat([torch.arange(n, device=q.device) + b * S for b, n in enumerate(lq)])
+    rows_k = torch.cat([torch.arange(n, device=q.device) + b * s_k for b, n in enumerate(lk)])
+    cu_q = torch.tensor([0] + list(itertools.accumulate(lq)), dtype=torch.int32, device=q.device)
+    cu_k = torch.tensor([0] + list(itertools.accumulate(lk)), dtype=torch.int32, device=q.device)
+    idx = sparse_indices.reshape(B * S, -1).to(torch.int32)
+    flat = lambda t, n: t.reshape(B * n, *t.shape[2:])  # noqa: E731
+    qt, kvt = flat(q, S)[rows_q], kv3.reshape(B * s_k, D)[rows_k]
+    it = idx[rows_q].contiguous()
+    mass = attn_mass_varlen(qt, kvt, it, flat(softmax_max, S)[rows_q], flat(softmax_sum, S)[rows_q], scale_value,
+                            cu_q, cu_k)
+    dq_t, dk_t, dw_t, loss_rows = indexer_kl_grad_from_mass_varlen(
+        flat(query_index, S)[rows_q], ki3.reshape(B * ki3.shape[1], -1)[rows_k], flat(weight, S)[rows_q], it, mass,
+        cu_q, cu_k, loss_scale=loss_scale, eps=eps, grad_scale=grad_scale)
+    dq_i = torch.zeros(B * S, *query_index.shape[2:], dtype=out_dtypes[0], device=q.device)
+    dk_i = torch.zeros(B * ki3.shape[1], ki3.shape[-1], dtype=out_dtypes[1], device=q.device)
+    dw = torch.zeros(B * S, *weight.shape[2:], dtype=out_dtypes[2], device=q.device)
+    dq_i[rows_q] = dq_t.to(out_dtypes[0])
+    dk_i[rows_k] = dk_t.to(out_dtypes[1])
+    dw[rows_q] = dw_t.to(out_dtypes[2])
+    return (dq_i.reshape(query_index.shape), dk_i.reshape(key_index.shape), dw.reshape(weight.shape),
             loss_rows.sum().reshape(1))
 
 
@@ -1424,9 +1565,11 @@ def _grad_scale_args(grad_scale, device):
 
 
 def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, q_offset=0, loss_scale=1.0, eps=1e-8,
-                              grad_scale=1.0):
+                              grad_scale=1.0, return_softmax=False):
     """(dq_idx fp32, dk_idx fp32 [B,S_k,D_I], dw fp32, loss_rows fp32 [B,S]) given the target mass;
-    ``grad_scale`` (a float or a device scalar tensor) multiplies the gradients."""
+    ``grad_scale`` (a float or a device scalar tensor) multiplies the gradients.  With
+    ``return_softmax`` a fifth tensor follows: the indexer's softmax over the slots [B,S,K]
+    fp32 (0 at unusable slots; dsa_indexer_kl_grad_softmax)."""
     lib = load_library()
     ki = key_index.squeeze(2) if key_index.dim() == 4 else key_index
     qi = query_index.to(torch.bfloat16).contiguous()
@@ -1445,13 +1588,14 @@ def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, 
     ws_bytes = int(lib.dsa_indexer_kl_grad_workspace_size(B, S, s_k, HI, DI, K))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     gsf, gsd = _grad_scale_args(grad_scale, dev)
+    sm = torch.empty(B, S, K, dtype=torch.float32, device=dev) if return_softmax else None
     check(
-        lib.dsa_indexer_kl_grad(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i), ptr(dw),
-                                ptr(loss_rows), ptr(ws), ws_bytes, B, S, s_k, HI, DI, K, int(q_offset),
-                                float(loss_scale), float(eps), gsf, ptr(gsd), stream_of(dev)),
+        lib.dsa_indexer_kl_grad_softmax(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i), ptr(dw),
+                                        ptr(loss_rows), ptr(sm), ptr(ws), ws_bytes, B, S, s_k, HI, DI, K,
+                                        int(q_offset), float(loss_scale), float(eps), gsf, ptr(gsd), stream_of(dev)),
         "dsa_indexer_kl_grad",
     )
-    return dq_i, dk_i, dw, loss_rows
+    return (dq_i, dk_i, dw, loss_rows, sm) if return_softmax else (dq_i, dk_i, dw, loss_rows)
 
 
 def indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, indices, mass, cu_seqlens_q, cu_seqlens_k, *,
