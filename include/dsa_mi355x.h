@@ -242,6 +242,19 @@ int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* indice
                             int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
                             int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale, int64_t q_offset,
                             void* stream);
+/*
+ * dsa_sparse_mla_bwd / dsa_sparse_mla_bwd_sink in one entry (sinks = NULL: no sink) that can
+ * reduce dKV with a prebuilt pair CSR (dsa_pair_csr_build from the same indices, s_kv and
+ * q_offset; NULL = build one).  The CSR is used when the workspace holds every query row in
+ * one chunk and ignored otherwise.  No counterpart in the reference's op (see
+ * dsa_pair_csr_build).
+ */
+int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* indices, const void* out, const void* dout,
+                          const float* softmax_max, const float* softmax_sum, void* dq, float* dkv_accum, float* mass,
+                          const float* sinks, float* dsink_accum, const void* pair_csr, int64_t pair_csr_bytes,
+                          void* workspace, int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q,
+                          int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
+                          int64_t q_offset, void* stream);
 
 /*
  * Head-summed attention probability at each selected slot (reference: get_attn_scores,
@@ -279,18 +292,43 @@ int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, co
                         int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset, float loss_scale,
                         float eps, float grad_scale, const float* grad_scale_dev, void* stream);
 /*
- * dsa_indexer_kl_grad that also writes the indexer's softmax over the slots (reference: the
- * softmax_out of cann_ops_transformer's sparse_lightning_indexer_kl_loss_grad,
- * converters/kernels/npu_smla.py:584-602, which _compute_li_loss :405-420 logs):
- *   softmax_out [B,S,K] fp32 (written): exp(I_j - logsumexp of the row's usable I) at usable
- *   slots, 0 at the others.  softmax_out = NULL is dsa_indexer_kl_grad.
+ * dsa_indexer_kl_grad with two optional extras (NULL = without them):
+ *   softmax_out [B,S,K] fp32 (written): the indexer's softmax over the slots, exp(I_j -
+ *     logsumexp of the row's usable I) at usable slots and 0 at the others (reference: the
+ *     softmax_out of cann_ops_transformer's sparse_lightning_indexer_kl_loss_grad,
+ *     converters/kernels/npu_smla.py:584-602, which _compute_li_loss :405-420 logs);
+ *   pair_csr / pair_csr_bytes: a CSR built by dsa_pair_csr_build from the same indices,
+ *     s_k and q_offset (the caller guarantees it), reduced with instead of building one; used
+ *     when the workspace holds every query row in one chunk, ignored otherwise.  No
+ *     counterpart in the reference's op: it lets the attention backward and this op share
+ *     one key-major pair list per step.
  */
-int dsa_indexer_kl_grad_softmax(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
-                                const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
-                                float* softmax_out, void* workspace, int64_t workspace_bytes, int64_t batch,
-                                int64_t s_q, int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t topk,
-                                int64_t q_offset, float loss_scale, float eps, float grad_scale,
-                                const float* grad_scale_dev, void* stream);
+int dsa_indexer_kl_grad_ex(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
+                           const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
+                           float* softmax_out, const void* pair_csr, int64_t pair_csr_bytes, void* workspace,
+                           int64_t workspace_bytes, int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
+                           int64_t head_dim, int64_t topk, int64_t q_offset, float loss_scale, float eps,
+                           float grad_scale, const float* grad_scale_dev, void* stream);
+
+/*
+ * Key-major CSR of the usable (query row, slot) pairs of an index tensor (no counterpart in
+ * the reference: the closed CANN ops scatter with atomics).  indices [B,S,K] int32; slot j of
+ * row s is usable iff 0 <= idx < s_k and idx <= s + q_offset.  The buffer (256-byte aligned,
+ * dsa_pair_csr_size() bytes) holds, per batch element, the pair list sorted by key (rows in
+ * order within each key) with its key pointers and segment table; dsa_sparse_mla_bwd_ex and
+ * dsa_indexer_kl_grad_ex reduce their per-pair contribution rows with it, so the attention
+ * backward's dKV and the indexer loss's dK_index, which use the same indices, build it once.
+ */
+int64_t dsa_pair_csr_size(int64_t batch, int64_t s_q, int64_t s_k, int64_t topk);
+/* query rows per chunk that a workspace of workspace_bytes gives dsa_sparse_mla_bwd{,_ex}
+ * (bf16 path) / dsa_indexer_kl_grad{,_ex} (H_I = 64, D_I = 128); s_q means one chunk, where a
+ * prebuilt pair CSR is used; 0 = the workspace is too small */
+int64_t dsa_sparse_mla_bwd_chunk_rows(int64_t batch, int64_t s_q, int64_t s_kv, int64_t d_qk, int64_t topk,
+                                      int64_t workspace_bytes);
+int64_t dsa_indexer_kl_grad_chunk_rows(int64_t batch, int64_t s_q, int64_t s_k, int64_t topk,
+                                       int64_t workspace_bytes);
+int dsa_pair_csr_build(const int32_t* indices, int64_t batch, int64_t s_q, int64_t s_k, int64_t topk,
+                       int64_t q_offset, void* csr, int64_t csr_bytes, void* stream);
 
 /*
  * Block KV compressor (reference: Compressor._forward_bsnd + overlap_transform,

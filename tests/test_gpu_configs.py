@@ -195,13 +195,15 @@ def check_dkv_keys(res, q, kv, dout, scale, keys, chunk=256):
     _log(f"dKV sampled keys {list(keys)}: worst rel err {worst:.3g}")
 
 
-def spread_keys(idx, n=32):
+def spread_keys(idx, n=32, popular=4):
     """At least ``n`` distinct keys the GPU selected, spread from popular early keys to rare
-    late ones: the smallest, the middle and the largest selected key of rows spaced evenly
-    over the sequence (a row's largest key is selected by few rows, its smallest by many)."""
-    S = idx.shape[1]
+    late ones: the middle and the largest selected key of rows spaced evenly over the
+    sequence (a row's largest key is selected by few rows, its middle one by more) and the
+    smallest key of the first ``popular`` of those rows (selected by the most rows; each
+    costs the oracle one closed form per selecting row)."""
+    S, K = idx.shape[1], idx.shape[2]
     rows = torch.linspace(0, S - 1, n).round().long().tolist()
-    picks = [(r, 0) for r in rows] + [(r, -1) for r in rows] + [(r, 1000) for r in rows[n // 2:]]
+    picks = [(r, -1) for r in rows] + [(r, K // 2) for r in rows] + [(r, 0) for r in rows[:popular]]
     keys = selected_keys(idx, [(r, sl) for r, sl in picks if int((idx[0, r] >= 0).sum()) > 0])
     assert len(keys) >= n, f"only {len(keys)} distinct keys"
     return keys

@@ -222,3 +222,42 @@ def test_bwd_fused_mass_matches_attn_mass(S, H, K, q_offset):
     assert rel_err(mass.cpu(), ref) <= 1e-4
     assert rel_err(mass.cpu(), standalone.cpu()) <= 1e-4
     assert float(mass.cpu()[idx < 0].abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize("d_qk,s_kv_extra", [(576, 0), (512, 96)])
+def test_shared_pair_csr_matches_per_op_builds(d_qk, s_kv_extra):
+    """The attention backward and the indexer KL op reduce with one key-major pair CSR built
+    once per index tensor (dsa_pair_csr_build): the KL op reuses the backward's (no second
+    build) and both results are bit-identical to each op building its own CSR inside the
+    library call (the same list order and segment sums)."""
+    S, H, K, HI, DI = 768, 32, 256, 64, 128
+    q, kv, dout, scale = attn_inputs(S, H, seed=21, d_qk=d_qk, q_offset=s_kv_extra)
+    idx = rand_indices(S, K, q_offset=s_kv_extra, seed=21, holes=0.05)
+    g = torch.Generator().manual_seed(22)
+    s_k = S + s_kv_extra
+    qi = torch.randn(1, S, HI, DI, generator=g).bfloat16().to(DEV)
+    ki = torch.randn(1, s_k, DI, generator=g).bfloat16().to(DEV)
+    w = (torch.rand(1, S, HI, generator=g) * HI ** -0.5 * DI ** -0.5).to(DEV)
+    ops = _ops()
+    qd, kvd, idd, dod = q.to(DEV), kv.to(DEV), idx.to(DEV), dout.to(DEV)
+    out, smax, ssum = ops.sparse_mla_fwd(qd, kvd, idd, scale, q_offset=s_kv_extra)
+
+    def step():
+        dq, dkv, mass = ops.sparse_mla_bwd(qd, kvd, idd, out, dod, smax, ssum, scale, q_offset=s_kv_extra,
+                                           return_mass=True)
+        built = ops._pair_csr_entry
+        kl = ops.indexer_kl_grad_from_mass(qi, ki, w, idd, mass, q_offset=s_kv_extra)
+        return (dq, dkv, mass) + tuple(kl), built
+
+    ops._pair_csr_entry = None
+    shared, built = step()
+    assert built is not None and ops._pair_csr_entry is built  # the KL op found the backward's CSR
+    try:
+        ops._share_pair_csr = False
+        ops._pair_csr_entry = None
+        own, none = step()
+        assert none is None and ops._pair_csr_entry is None
+    finally:
+        ops._share_pair_csr = True
+    for a, b in zip(shared, own):
+        assert torch.equal(a, b)

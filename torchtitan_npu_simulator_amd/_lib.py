@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -64,6 +64,11 @@ _SIGNATURES = {
          _i64, _i64, _f32, _i64, _vp],
         _i32,
     ),
+    "dsa_sparse_mla_bwd_ex": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i32, _i64, _i64, _i64,
+         _i64, _i64, _i64, _i64, _f32, _i64, _vp],
+        _i32,
+    ),
     "dsa_attn_mass": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _i64, _vp],
         _i32,
@@ -74,11 +79,15 @@ _SIGNATURES = {
          _f32, _f32, _vp, _vp],
         _i32,
     ),
-    "dsa_indexer_kl_grad_softmax": (
-        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-         _f32, _f32, _f32, _vp, _vp],
+    "dsa_indexer_kl_grad_ex": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _i64, _f32, _f32, _f32, _vp, _vp],
         _i32,
     ),
+    "dsa_pair_csr_size": ([_i64, _i64, _i64, _i64], _i64),
+    "dsa_sparse_mla_bwd_chunk_rows": ([_i64, _i64, _i64, _i64, _i64, _i64], _i64),
+    "dsa_indexer_kl_grad_chunk_rows": ([_i64, _i64, _i64, _i64, _i64], _i64),
+    "dsa_pair_csr_build": ([_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp], _i32),
     "dsa_compressor_fwd": ([_vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _f32, _vp, _i64, _i64, _vp,
                             _vp], _i32),
     "dsa_compressor_fwd_tnd": (

@@ -395,20 +395,30 @@ csr_partial_fixup_kernel(const int* __restrict__ row_ptr, const int* __restrict_
 // counts and row_ptr (s_kv + 1 ints each), the segment table (one int per kSegPairs pairs
 // of the chunk), the [row block][key] count table, the [column chunk][key] chunk offsets
 // and two partial-sum rows per segment (at a 16-byte boundary).
-inline int64_t csr_ws_bytes(int64_t s_kv, int64_t rows, int64_t K, int64_t width) {
+inline int64_t csr_ws_ints(int64_t s_kv, int64_t rows, int64_t K) {
   const int64_t n_rb = (rows + csr_rows_per_wg(s_kv, K) - 1) / csr_rows_per_wg(s_kv, K);
   const int64_t n_chunks = (n_rb + kColChunk - 1) / kColChunk;
   const int64_t n_seg = (rows * K + kSegPairs - 1) / kSegPairs;
-  const int64_t ints = 2 * (s_kv + 1) + n_seg + (n_rb + n_chunks) * s_kv;
-  return (ints + 3) / 4 * 16 + n_seg * 2 * width * 4;
+  return (2 * (s_kv + 1) + n_seg + (n_rb + n_chunks) * s_kv + 3) / 4 * 4;
+}
+inline int64_t csr_part_bytes(int64_t rows, int64_t K, int64_t width) {
+  return (rows * K + kSegPairs - 1) / kSegPairs * 2 * width * 4;
+}
+inline int64_t csr_ws_bytes(int64_t s_kv, int64_t rows, int64_t K, int64_t width) {
+  return csr_ws_ints(s_kv, rows, K) * 4 + csr_part_bytes(rows, K, width);
 }
 
-// Build the CSR for query rows [row0, row0 + rows) of batch element b and reduce the
-// contribution rows cbuf[b][row][slot][8 * row_chunks] into acc_out[b][key][...].
-// csr_ws holds csr_ws_bytes(s_kv, rows, K) bytes.
-inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, int* pairs, int* csr_ws, int S,
-                      int s_kv, int K, int64_t q_offset, int row0, int rows, int b, int row_chunks, hipStream_t st) {
-  if (s_kv <= 0 || rows <= 0) return DSA_OK;  // no pairs: the accumulator keeps its contents
+// A built CSR: the key-sorted pair list with its key pointers and segment table.
+struct CsrView {
+  const int* pairs;
+  const int* row_ptr;
+  const int* seg_key;
+};
+
+// Build the CSR of query rows [row0, row0 + rows) of batch element b: `pairs` holds
+// rows * K ints, csr_ws csr_ws_ints(s_kv, rows, K) ints.
+inline int csr_build(const int32_t* idx, int* pairs, int* csr_ws, int S, int s_kv, int K, int64_t q_offset, int row0,
+                     int rows, int b, hipStream_t st, CsrView* view) {
   const int rows_per_wg = csr_rows_per_wg(s_kv, K);
   const int64_t n_rb = ceil_div(rows, rows_per_wg);
   const int64_t n_chunks = ceil_div(n_rb, kColChunk);
@@ -418,8 +428,6 @@ inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, 
   const int64_t n_seg = ceil_div((int64_t)rows * K, kSegPairs);
   int* table = seg_key + n_seg;
   int* chunk_off = table + n_rb * s_kv;
-  const int64_t n_ints = 2 * (s_kv + 1) + n_seg + (n_rb + n_chunks) * s_kv;
-  float* part = reinterpret_cast<float*>(csr_ws + (n_ints + 3) / 4 * 4);
   const int n_ranges = (int)ceil_div(s_kv, kLdsKeys);
   const size_t hist_bytes = (size_t)(s_kv < kLdsKeys ? s_kv : kLdsKeys) * 4;
   const int64_t cgrid = n_rb * (int64_t)n_ranges;
@@ -448,17 +456,27 @@ inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, 
     const TimedLaunch tl("csr_seg_key_kernel", st);
     csr_seg_key_kernel<<<ceil_div(s_kv, 256), 256, 0, st>>>(row_ptr, seg_key, s_kv);
   }
+  view->pairs = pairs;
+  view->row_ptr = row_ptr;
+  view->seg_key = seg_key;
+  return check_launch("csr_reduce(build)");
+}
+
+// Reduce the contribution rows cbuf[b][row][slot][8 * row_chunks] of the rows a built CSR
+// covers into acc_out[b][key][...]; `part` holds csr_part_bytes(rows, K, 8 * row_chunks).
+inline int csr_reduce_built(const CsrView& v, const uint16_t* cbuf, float* acc_out, float* part, int s_kv, int rows,
+                            int K, int b, int row_chunks, hipStream_t st) {
   const unsigned rgrid = ceil_div(ceil_div((int64_t)rows * K, kSegPairs), 4);
   const TimedLaunch tl(row_chunks == 72   ? "dkv_reduce_kernel<72>"
                        : row_chunks == 64 ? "dkv_reduce_kernel<64>"
                                           : "dkv_reduce_kernel<16>",
                        st);
   if (row_chunks == 72)
-    dkv_reduce_kernel<72><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, part, s_kv, rows, K, b);
+    dkv_reduce_kernel<72><<<rgrid, 256, 0, st>>>(cbuf, v.row_ptr, v.pairs, v.seg_key, acc_out, part, s_kv, rows, K, b);
   else if (row_chunks == 64)
-    dkv_reduce_kernel<64><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, part, s_kv, rows, K, b);
+    dkv_reduce_kernel<64><<<rgrid, 256, 0, st>>>(cbuf, v.row_ptr, v.pairs, v.seg_key, acc_out, part, s_kv, rows, K, b);
   else if (row_chunks == 16)
-    dkv_reduce_kernel<16><<<rgrid, 256, 0, st>>>(cbuf, row_ptr, pairs, seg_key, acc_out, part, s_kv, rows, K, b);
+    dkv_reduce_kernel<16><<<rgrid, 256, 0, st>>>(cbuf, v.row_ptr, v.pairs, v.seg_key, acc_out, part, s_kv, rows, K, b);
   else
     return set_error(DSA_ERR_UNSUPPORTED, "csr_reduce: row width %d chunks", row_chunks);
   if (int rc = check_launch("csr_reduce")) return rc;
@@ -466,13 +484,45 @@ inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, 
     const TimedLaunch tl2("csr_partial_fixup_kernel", st);
     const unsigned fgrid = (unsigned)ceil_div(s_kv, 4);
     if (row_chunks == 72)
-      csr_partial_fixup_kernel<576><<<fgrid, 256, 0, st>>>(row_ptr, seg_key, part, acc_out, s_kv, b);
+      csr_partial_fixup_kernel<576><<<fgrid, 256, 0, st>>>(v.row_ptr, v.seg_key, part, acc_out, s_kv, b);
     else if (row_chunks == 64)
-      csr_partial_fixup_kernel<512><<<fgrid, 256, 0, st>>>(row_ptr, seg_key, part, acc_out, s_kv, b);
+      csr_partial_fixup_kernel<512><<<fgrid, 256, 0, st>>>(v.row_ptr, v.seg_key, part, acc_out, s_kv, b);
     else
-      csr_partial_fixup_kernel<128><<<fgrid, 256, 0, st>>>(row_ptr, seg_key, part, acc_out, s_kv, b);
+      csr_partial_fixup_kernel<128><<<fgrid, 256, 0, st>>>(v.row_ptr, v.seg_key, part, acc_out, s_kv, b);
   }
   return check_launch("csr_reduce(fix-up)");
+}
+
+// Build the CSR for query rows [row0, row0 + rows) of batch element b and reduce the
+// contribution rows cbuf[b][row][slot][8 * row_chunks] into acc_out[b][key][...].
+// csr_ws holds csr_ws_bytes(s_kv, rows, K) bytes.
+inline int csr_reduce(const int32_t* idx, const uint16_t* cbuf, float* acc_out, int* pairs, int* csr_ws, int S,
+                      int s_kv, int K, int64_t q_offset, int row0, int rows, int b, int row_chunks, hipStream_t st) {
+  if (s_kv <= 0 || rows <= 0) return DSA_OK;  // no pairs: the accumulator keeps its contents
+  CsrView v;
+  if (int rc = csr_build(idx, pairs, csr_ws, S, s_kv, K, q_offset, row0, rows, b, st, &v)) return rc;
+  float* part = reinterpret_cast<float*>(csr_ws + csr_ws_ints(s_kv, rows, K));
+  return csr_reduce_built(v, cbuf, acc_out, part, s_kv, rows, K, b, row_chunks, st);
+}
+
+// A prebuilt CSR of every query row of every batch element, shared by the reductions of one
+// index tensor (the attention backward's dKV and the indexer KL op's dK_index): per batch
+// element, rows * K pair ints then csr_ws_ints of key pointers, segment table and the build's
+// scratch tables.
+inline int64_t pair_csr_batch_ints(int64_t s_kv, int64_t rows, int64_t K) {
+  return (rows * K + 3) / 4 * 4 + csr_ws_ints(s_kv, rows, K);
+}
+inline int64_t pair_csr_bytes_of(int64_t batch, int64_t s_q, int64_t s_kv, int64_t K) {
+  return batch * pair_csr_batch_ints(s_kv, s_q, K) * 4;
+}
+inline CsrView pair_csr_view(const void* csr, int64_t s_kv, int64_t rows, int64_t K, int b) {
+  const int* base = reinterpret_cast<const int*>(csr) + (int64_t)b * pair_csr_batch_ints(s_kv, rows, K);
+  const int* ws = base + (rows * K + 3) / 4 * 4;
+  CsrView v;
+  v.pairs = base;
+  v.row_ptr = ws + (s_kv + 1);
+  v.seg_key = ws + 2 * (s_kv + 1);
+  return v;
 }
 
 }  // namespace

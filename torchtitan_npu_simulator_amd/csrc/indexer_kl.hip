@@ -608,25 +608,39 @@ extern "C" int64_t dsa_indexer_kl_grad_workspace_size(int64_t batch, int64_t s_q
   return plan_kl(batch, rows, s_k, topk).total;
 }
 
+extern "C" int64_t dsa_indexer_kl_grad_chunk_rows(int64_t batch, int64_t s_q, int64_t s_k, int64_t topk,
+                                                  int64_t workspace_bytes) {
+  using namespace dsa;
+  if (batch <= 0 || s_q <= 0 || s_k <= 0 || topk <= 0 || workspace_bytes <= 0) return 0;
+  const int64_t per_row = batch * topk * kD * 2 + topk * 4;
+  const int64_t rows = std::max<int64_t>(1, std::min<int64_t>(s_q, workspace_bytes / per_row));
+  KlPlan plan = plan_kl(batch, rows, s_k, topk);
+  while (plan.total > workspace_bytes && plan.rows > 1) plan = plan_kl(batch, plan.rows - 1, s_k, topk);
+  return plan.total > workspace_bytes ? 0 : plan.rows;
+}
+
 extern "C" int dsa_indexer_kl_grad(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
                                    const float* mass, float* dq_idx, float* dk_idx_accum, float* dw, float* loss_rows,
                                    void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q, int64_t s_k,
                                    int64_t n_heads, int64_t head_dim, int64_t topk, int64_t q_offset,
                                    float loss_scale, float eps, float grad_scale, const float* grad_scale_dev,
                                    void* stream) {
-  return dsa_indexer_kl_grad_softmax(q_idx, k_idx, w, indices, mass, dq_idx, dk_idx_accum, dw, loss_rows, nullptr,
-                                     workspace, workspace_bytes, batch, s_q, s_k, n_heads, head_dim, topk, q_offset,
-                                     loss_scale, eps, grad_scale, grad_scale_dev, stream);
+  return dsa_indexer_kl_grad_ex(q_idx, k_idx, w, indices, mass, dq_idx, dk_idx_accum, dw, loss_rows, nullptr, nullptr,
+                                0, workspace, workspace_bytes, batch, s_q, s_k, n_heads, head_dim, topk, q_offset,
+                                loss_scale, eps, grad_scale, grad_scale_dev, stream);
 }
 
-extern "C" int dsa_indexer_kl_grad_softmax(const void* q_idx, const void* k_idx, const float* w,
-                                           const int32_t* indices, const float* mass, float* dq_idx,
-                                           float* dk_idx_accum, float* dw, float* loss_rows, float* softmax_out,
-                                           void* workspace, int64_t workspace_bytes, int64_t batch, int64_t s_q,
-                                           int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t topk,
-                                           int64_t q_offset, float loss_scale, float eps, float grad_scale,
-                                           const float* grad_scale_dev, void* stream) {
+extern "C" int dsa_indexer_kl_grad_ex(const void* q_idx, const void* k_idx, const float* w, const int32_t* indices,
+                                      const float* mass, float* dq_idx, float* dk_idx_accum, float* dw,
+                                      float* loss_rows, float* softmax_out, const void* pair_csr,
+                                      int64_t pair_csr_bytes, void* workspace, int64_t workspace_bytes, int64_t batch,
+                                      int64_t s_q, int64_t s_k, int64_t n_heads, int64_t head_dim, int64_t topk,
+                                      int64_t q_offset, float loss_scale, float eps, float grad_scale,
+                                      const float* grad_scale_dev, void* stream) {
   using namespace dsa;
+  if (pair_csr && pair_csr_bytes < pair_csr_bytes_of(batch, s_q, s_k, topk))
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad_ex: pair CSR of %lld bytes is too small",
+                     (long long)pair_csr_bytes);
   if (!q_idx || !k_idx || !w || !indices || !mass || !dq_idx || !dk_idx_accum || !dw || !loss_rows)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_indexer_kl_grad: null pointer");
   if (batch <= 0 || s_q <= 0 || s_k <= 0 || n_heads <= 0 || head_dim <= 0 || topk <= 0 || topk > kMaxK)
@@ -670,10 +684,20 @@ extern "C" int dsa_indexer_kl_grad_softmax(const void* q_idx, const void* k_idx,
                                                    softmax_out);
     }
     if (int rc = check_launch("dsa_indexer_kl_grad(mfma)")) return rc;
-    for (int b = 0; b < (int)batch; ++b)
-      if (int rc = csr_reduce(indices, ck, dk_idx_accum, pairs, csr, (int)s_q, (int)s_k, (int)topk, q_offset, (int)r0,
-                              rows_c, b, kRowC, st))
+    // a prebuilt CSR of every row (the one the attention backward reduced dKV with) serves a
+    // one-chunk plan; otherwise each chunk builds its own
+    const bool prebuilt = pair_csr && rows_c == s_q;
+    for (int b = 0; b < (int)batch; ++b) {
+      if (prebuilt) {
+        float* part = reinterpret_cast<float*>(csr + csr_ws_ints(s_k, rows_c, topk));
+        if (int rc = csr_reduce_built(pair_csr_view(pair_csr, s_k, rows_c, topk, b), ck, dk_idx_accum, part, (int)s_k,
+                                      rows_c, (int)topk, b, kRowC, st))
+          return rc;
+      } else if (int rc = csr_reduce(indices, ck, dk_idx_accum, pairs, csr, (int)s_q, (int)s_k, (int)topk, q_offset,
+                                     (int)r0, rows_c, b, kRowC, st)) {
         return rc;
+      }
+    }
   }
   return DSA_OK;
 }

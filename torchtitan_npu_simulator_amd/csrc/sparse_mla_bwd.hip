@@ -366,11 +366,12 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
 // (alpha-2) bwd_dqk_kernel: dQ = (dS * scale) K for a token, all heads in one workgroup
 //
 // The forward's P.V structure with P := the staged dS of bwd_sdp_kernel and V := the whole
-// 576-column K row: dQ^T[32 d x 32 heads] += K^T dS^T on v_mfma_f32_32x32x16_bf16.  Eight
-// waves (two per SIMD): wave w owns the d tiles w % 4, w % 4 + 4, .. (of 18) for the two
-// 32-head groups of half w / 4, so each K^T operand read from LDS feeds 4 MFMAs (2 head
-// groups x 2 key steps) and the tile is read twice per workgroup instead of once per head
-// group; dQ^T (up to 5 x 2 x 16 fp32 per lane) stays in the accumulation registers.  The dS columns of each slot's G row (two 128-byte pieces) are
+// 576-column K row: dQ^T[32 d x 32 heads] += K^T dS^T on v_mfma_f32_32x32x16_bf16.  Twelve
+// waves (three per SIMD; eight for 512-column rows): wave w owns the d tiles w % 6,
+// w % 6 + 6, w % 6 + 12 (of 18; w % 4 + 4i of 16) for the two 32-head groups of half
+// w / 6 (w / 4), so each K^T operand read from LDS feeds 4 MFMAs (2 head groups x 2 key
+// steps) and the tile is read twice per workgroup instead of once per head group; dQ^T
+// (3 x 2 x 16 fp32 per lane) stays in the accumulation registers.  The dS columns of each slot's G row (two 128-byte pieces) are
 // DMA'd into a [slot][128 heads] tile (16-byte chunk c of slot r at c ^ 4 (r & 3)) and read
 // back transposed with the forward's V^T lane pattern, so both operands share the k order.
 // Keys that are not valid contribute 0.
@@ -378,16 +379,27 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
 __device__ __forceinline__ int ds_swz(int r) { return 4 * (r & 3); }
 
 template <int kD>  // row width of KV and dQ: 576 or 512
-__global__ void __launch_bounds__(512, 1)
+struct DqkShape {
+  static constexpr int kDT = kD / 32;                 // 18 | 16 d tiles
+  static constexpr int kPh = kD == 576 ? 6 : 4;       // d-tile owners per head half (18 = 6 x 3, 16 = 4 x 4)
+  static constexpr int kWaves = 2 * kPh;              // 12 | 8 waves: three | two per SIMD
+  static constexpr int kOwn = (kDT + kPh - 1) / kPh;  // d tiles per wave: 3 | 4
+};
+
+template <int kD>  // row width of KV and dQ: 576 or 512
+__global__ void __launch_bounds__(DqkShape<kD>::kWaves * 64, 1)
 bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx, const uint16_t* __restrict__ gbuf,
                uint16_t* __restrict__ dq, int S, int s_kv, int H, int K, int64_t q_offset, int row0) {
-  using Gather = RowGather<8, kD>;
+  using Shape = DqkShape<kD>;
+  constexpr int kWaves = Shape::kWaves, kPh = Shape::kPh;
+  using Gather = RowGather<kWaves, kD>;
   using Geo = GatherGeomT<kD>;
-  constexpr int kPer = Gather::kMaxPerWave;  // 5 | 4 row instructions per wave and block
-  constexpr int kDT = kD / 32;               // 18 | 16 d tiles
-  constexpr int kOwn = (kDT + 3) / 4;        // d tiles per wave (576: 5, tile owners 2, 3 own 4; 512: 4)
+  constexpr int kPer = Gather::kMaxPerWave;  // 3 | 4 row instructions per wave and block
+  constexpr int kDT = Shape::kDT;
+  constexpr int kOwn = Shape::kOwn;
   constexpr int kRB = Geo::kRowBytes;
   static_assert(kPer <= kOwn, "one row instruction per owned tile");
+  static_assert(kWaves >= 8, "eight waves issue the dS tile DMA");
   __shared__ u32x4 tile[2][Geo::kTileChunks];
   __shared__ u32x4 dsl[2][kBN * 16];  // dS tile: [slot][16 chunks of 8 heads ^ ds_swz(slot)]
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
@@ -395,7 +407,7 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
 
   const int lr = blockIdx.x, tok = row0 + lr, b = blockIdx.z, tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int wt = wave & 3, hh2 = wave >> 2;  // d-tile owner, head half (groups 2 hh2, 2 hh2 + 1)
+  const int wt = wave % kPh, hh2 = wave / kPh;  // d-tile owner, head half (groups 2 hh2, 2 hh2 + 1)
   const int n = lane & 31, h = lane >> 5;
   const int64_t row_id = (int64_t)b * S + tok;
   const int32_t* ridx = idx + row_id * K;
@@ -412,7 +424,7 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (nblk == 0) {  // no usable key: dQ = 0
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    for (int i = tid; i < H * (kD / 2); i += 512)
+    for (int i = tid; i < H * (kD / 2); i += kWaves * 64)
       reinterpret_cast<uint32_t*>(dq + row_id * H * kD)[i] = 0u;
     return;
   }
@@ -445,12 +457,15 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
   // slot 4J + lane/16, stored chunk lane % 16 = source chunk (lane % 16) ^ ds_swz(slot);
   // source chunk c < 8: dS entries 8c .. (head group 0), else 128 + 8 (c - 8) (group 1)
   auto issue_ds = [&](int blk, int buf) {
-    {
+    if (wave < 8) {  // (wave-uniform) eight instructions of 1 KB cover the 32 slots
       const int J = wave;
       const int r = 4 * J + (lane >> 4);
       const int c = (lane & 15) ^ ds_swz(r);
       const int eo = c < 8 ? 8 * c : 128 + 8 * (c - 8);
-      const int slot = min(blk * kBN + r, K - 1);
+      // (G rows are padded to whole 32-slot blocks, and the score kernel writes exact zeros
+      // at the padding slots past K, as at every unusable slot: no clamp to slot K - 1, whose
+      // dS would otherwise stand in for them)
+      const int slot = blk * kBN + r;
       dma16_to_lds(grow, (uint32_t)(slot * kGW + eo) * 2u, (uint32_t)(uintptr_t)&dsl[buf][J * 64]);
     }
   };
@@ -464,7 +479,6 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
   const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
   if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
   __syncthreads();
-  uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
 #pragma unroll
   for (int i = 0; i < kPer; ++i)
     Gather::issue_slot(kvb, &tile[0][0], i, wave, Gather::ring_slot(sidx[0], i, gl), gl, lim, K);
@@ -481,7 +495,6 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
     u32x4* dst_tile = &tile[buf ^ 1][0];
     const int* ring = sidx[(blk + 1) & (GatherGeom::kRing - 1)];
     const int rows_left = K - (blk + 1) * kBN;
-    const uint32_t vm_next = Gather::ring_valid(ring, lane, lim, rows_left);
     if (blk + 1 < nblk) issue_ds(blk + 1, buf ^ 1);
     auto read_kt = [&](u32x4 (&dst)[2], int dt) {
 #pragma unroll
@@ -492,23 +505,15 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
     };
     u32x4 av[2][2];
     read_kt(av[0], wt);
-    // dS^T operands of the wave's two head groups (masked to the block's valid keys)
-    const uint32_t vmh = vm_cur >> (4 * h);
+    // dS^T operands of the wave's two head groups.  No masking: the score kernel stores
+    // dS = P (dP - delta) with P = 0 exactly at every unusable slot and absent head, and the
+    // rows gathered for those slots (row 0) are finite, so they add exact zeros.
     u32x4 bs[2][2];
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        u32x4 v = lds_read_tr_pair(db + ds_off[gg][0] + kk * 16 * 256, db + ds_off[gg][1] + kk * 16 * 256);
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {  // dword q4: keys 16kk + 8 (q4 / 2) + 4h + 2 (q4 % 2) + {0, 1}
-          const int k0 = 16 * kk + 8 * (q4 >> 1) + 2 * (q4 & 1);
-          const uint32_t lo = ((vmh >> k0) & 1u) ? 0x0000ffffu : 0u;
-          const uint32_t hi = ((vmh >> (k0 + 1)) & 1u) ? 0xffff0000u : 0u;
-          v[q4] &= lo | hi;
-        }
-        bs[gg][kk] = v;
-      }
+      for (int kk = 0; kk < 2; ++kk)
+        bs[gg][kk] = lds_read_tr_pair(db + ds_off[gg][0] + kk * 16 * 256, db + ds_off[gg][1] + kk * 16 * 256);
     uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
     auto issue_rows = [&](auto tc) {  // one row instruction per tile
       constexpr int nb = decltype(tc)::value;
@@ -520,9 +525,9 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
     };
     static_for<kOwn>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
-      const int dt = wt + 4 * t;  // wave-uniform
+      const int dt = wt + kPh * t;  // wave-uniform
       if (dt < kDT) {
-        if (t + 1 < kOwn && dt + 4 < kDT) read_kt(av[(t + 1) & 1], dt + 4);
+        if (t + 1 < kOwn && dt + kPh < kDT) read_kt(av[(t + 1) & 1], dt + kPh);
         issue_rows(tc);  // block blk+1's rows
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg)
@@ -536,14 +541,13 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
     });
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // block blk+1 (rows, dS) and ring entry blk+3 landed
     __syncthreads();
-    vm_cur = vm_next;
   }
 
   // ---- epilogue: tile t, group gg: lane holds d = 32 dt + 8 j + 4 h + i of head
   // 32 (2 hh2 + gg) + n (dS was pre-scaled) ----
 #pragma unroll
   for (int t = 0; t < kOwn; ++t) {
-    const int dt = wt + 4 * t;
+    const int dt = wt + kPh * t;
     if (dt >= kDT) break;
 #pragma unroll
     for (int gg = 0; gg < 2; ++gg) {
@@ -947,7 +951,7 @@ static int sparse_mla_bwd_impl(const void* q, const void* kv, const int32_t* ind
                                float* dkv_accum, float* mass, void* workspace, int64_t workspace_bytes, int dtype,
                                int64_t batch, int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t d_qk, int64_t d_v,
                                int64_t topk, float scale, int64_t q_offset, const float* sinks, float* dsink,
-                               void* stream) {
+                               const void* csr, void* stream) {
   if (!q || !kv || !indices || !out || !dout || !softmax_max || !softmax_sum || !dq || !dkv_accum)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd: null pointer");
   if (batch <= 0 || s_q <= 0 || s_kv <= 0 || n_heads <= 0 || topk <= 0 || d_v <= 0 || d_qk < d_v)
@@ -1022,8 +1026,9 @@ static int sparse_mla_bwd_impl(const void* q, const void* kv, const int32_t* ind
     {
       const TimedLaunch tl(rope ? "bwd_dqk_kernel" : "bwd_dqk_kernel<512>", st);
       auto* kern = rope ? bwd_dqk_kernel<kDqk> : bwd_dqk_kernel<kDv>;
-      kern<<<ga, 512, 0, st>>>((const uint16_t*)kv, indices, gbuf, (uint16_t*)dq, (int)s_q, (int)s_kv, (int)n_heads,
-                               (int)topk, q_offset, (int)r0);
+      const int threads = 64 * (rope ? DqkShape<kDqk>::kWaves : DqkShape<kDv>::kWaves);
+      kern<<<ga, threads, 0, st>>>((const uint16_t*)kv, indices, gbuf, (uint16_t*)dq, (int)s_q, (int)s_kv,
+                                   (int)n_heads, (int)topk, q_offset, (int)r0);
     }
     if (int rc = check_launch("dsa_sparse_mla_bwd(dq)")) return rc;
     dim3 gb((unsigned)rows, (unsigned)batch);
@@ -1037,13 +1042,70 @@ static int sparse_mla_bwd_impl(const void* q, const void* kv, const int32_t* ind
                                      (int)s_kv, (int)n_heads, (int)topk, q_offset, (int)r0, rows);
     }
     if (int rc = check_launch("dsa_sparse_mla_bwd(contrib)")) return rc;
-    for (int b = 0; b < (int)batch; ++b)
-      if (int rc = csr_reduce(indices, cbuf, dkv_accum, pairs, counts, (int)s_q, (int)s_kv, (int)topk, q_offset,
-                              (int)r0, rows, b, (int)(d_qk / 8), st))
+    // a prebuilt CSR of every row serves a one-chunk plan; otherwise each chunk builds its own
+    const bool prebuilt = csr && rows == s_q;
+    for (int b = 0; b < (int)batch; ++b) {
+      if (prebuilt) {
+        float* part = reinterpret_cast<float*>(counts + csr_ws_ints(s_kv, rows, topk));
+        if (int rc = csr_reduce_built(pair_csr_view(csr, s_kv, rows, topk, b), cbuf, dkv_accum, part, (int)s_kv, rows,
+                                      (int)topk, b, (int)(d_qk / 8), st))
+          return rc;
+      } else if (int rc = csr_reduce(indices, cbuf, dkv_accum, pairs, counts, (int)s_q, (int)s_kv, (int)topk, q_offset,
+                                     (int)r0, rows, b, (int)(d_qk / 8), st)) {
         return rc;
+      }
+    }
   }
   return DSA_OK;
 }
+
+// a prebuilt CSR's size against the call that wants to use it
+static int check_pair_csr(const void* csr, int64_t csr_bytes, int64_t batch, int64_t s_q, int64_t s_kv, int64_t topk,
+                          const char* what) {
+  if (!csr) return DSA_OK;
+  if (csr_bytes < pair_csr_bytes_of(batch, s_q, s_kv, topk))
+    return set_error(DSA_ERR_INVALID_ARG, "%s: pair CSR of %lld bytes is too small", what, (long long)csr_bytes);
+  return DSA_OK;
+}
+}  // namespace dsa
+
+extern "C" int64_t dsa_sparse_mla_bwd_chunk_rows(int64_t batch, int64_t s_q, int64_t s_kv, int64_t d_qk,
+                                                 int64_t topk, int64_t workspace_bytes) {
+  using namespace dsa;
+  if (batch <= 0 || s_q <= 0 || s_kv <= 0 || topk <= 0 || workspace_bytes <= 0) return 0;
+  BwdPlan plan = plan_bwd(batch, s_q, s_kv, topk, workspace_bytes, d_qk);
+  while (plan.total > workspace_bytes && plan.rows > 1) plan = plan_bwd(batch, plan.rows - 1, s_kv, topk, 0, d_qk);
+  return plan.total > workspace_bytes ? 0 : plan.rows;
+}
+
+extern "C" int64_t dsa_pair_csr_size(int64_t batch, int64_t s_q, int64_t s_k, int64_t topk) {
+  if (batch <= 0 || s_q <= 0 || s_k <= 0 || topk <= 0) return 0;
+  return dsa::pair_csr_bytes_of(batch, s_q, s_k, topk);
+}
+
+extern "C" int dsa_pair_csr_build(const int32_t* indices, int64_t batch, int64_t s_q, int64_t s_k, int64_t topk,
+                                  int64_t q_offset, void* csr, int64_t csr_bytes, void* stream) {
+  using namespace dsa;
+  if (!indices || !csr) return set_error(DSA_ERR_INVALID_ARG, "dsa_pair_csr_build: null pointer");
+  if (batch <= 0 || s_q <= 0 || s_k <= 0 || topk <= 0 || s_q > 2147483647LL || s_k > 2147483647LL || batch > 65535 ||
+      topk > (1 << 20))
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_pair_csr_build: bad sizes");
+  if ((uintptr_t)csr % 256) return set_error(DSA_ERR_INVALID_ARG, "dsa_pair_csr_build: buffer must be 256-byte aligned");
+  if (csr_bytes < pair_csr_bytes_of(batch, s_q, s_k, topk))
+    return set_error(DSA_ERR_INVALID_ARG, "dsa_pair_csr_build: buffer of %lld bytes, %lld needed", (long long)csr_bytes,
+                     (long long)pair_csr_bytes_of(batch, s_q, s_k, topk));
+  hipStream_t st = (hipStream_t)stream;
+  for (int b = 0; b < (int)batch; ++b) {
+    int* base = reinterpret_cast<int*>(csr) + (int64_t)b * pair_csr_batch_ints(s_k, s_q, topk);
+    int* ws = base + (s_q * topk + 3) / 4 * 4;
+    CsrView v;
+    if (int rc = csr_build(indices, base, ws, (int)s_q, (int)s_k, (int)topk, q_offset, 0, (int)s_q, b, st, &v))
+      return rc;
+  }
+  return DSA_OK;
+}
+
+namespace dsa {
 }  // namespace dsa
 
 extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* indices, const void* out,
@@ -1054,7 +1116,7 @@ extern "C" int dsa_sparse_mla_bwd(const void* q, const void* kv, const int32_t* 
                                   int64_t topk, float scale, int64_t q_offset, void* stream) {
   return dsa::sparse_mla_bwd_impl(q, kv, indices, out, dout, softmax_max, softmax_sum, dq, dkv_accum, mass, workspace,
                                   workspace_bytes, dtype, batch, s_q, s_kv, n_heads, d_qk, d_v, topk, scale, q_offset,
-                                  nullptr, nullptr, stream);
+                                  nullptr, nullptr, nullptr, stream);
 }
 
 extern "C" int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int32_t* indices, const void* out,
@@ -1066,6 +1128,21 @@ extern "C" int dsa_sparse_mla_bwd_sink(const void* q, const void* kv, const int3
   if (!sinks || !dsink_accum) return dsa::set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd_sink: null sinks / dsink");
   return dsa::sparse_mla_bwd_impl(q, kv, indices, out, dout, softmax_max, softmax_sum, dq, dkv_accum, mass, workspace,
                                   workspace_bytes, dtype, batch, s_q, s_kv, n_heads, d_qk, d_v, topk, scale, q_offset,
-                                  sinks, dsink_accum, stream);
+                                  sinks, dsink_accum, nullptr, stream);
+}
+
+extern "C" int dsa_sparse_mla_bwd_ex(const void* q, const void* kv, const int32_t* indices, const void* out,
+                                     const void* dout, const float* softmax_max, const float* softmax_sum, void* dq,
+                                     float* dkv_accum, float* mass, const float* sinks, float* dsink_accum,
+                                     const void* pair_csr, int64_t pair_csr_bytes, void* workspace,
+                                     int64_t workspace_bytes, int dtype, int64_t batch, int64_t s_q, int64_t s_kv,
+                                     int64_t n_heads, int64_t d_qk, int64_t d_v, int64_t topk, float scale,
+                                     int64_t q_offset, void* stream) {
+  if (sinks && !dsink_accum) return dsa::set_error(DSA_ERR_INVALID_ARG, "dsa_sparse_mla_bwd_ex: sinks without dsink");
+  if (int rc = dsa::check_pair_csr(pair_csr, pair_csr_bytes, batch, s_q, s_kv, topk, "dsa_sparse_mla_bwd_ex"))
+    return rc;
+  return dsa::sparse_mla_bwd_impl(q, kv, indices, out, dout, softmax_max, softmax_sum, dq, dkv_accum, mass, workspace,
+                                  workspace_bytes, dtype, batch, s_q, s_kv, n_heads, d_qk, d_v, topk, scale, q_offset,
+                                  sinks, sinks ? dsink_accum : nullptr, pair_csr, stream);
 }
 

@@ -480,6 +480,35 @@ def _sink_vector(sinks, H, device):
     return sk
 
 
+_pair_csr_entry = None  # (key, the index tensor, CSR buffer)
+_share_pair_csr = True  # False: each reduction builds its own CSR inside the library call
+
+
+def pair_csr(indices, s_k, q_offset=0):
+    """The key-major CSR of the usable (row, slot) pairs of ``indices`` [B,S,K] int32 over s_k
+    keys (dsa_pair_csr_build), shared by the attention backward's dKV reduction and the
+    indexer KL op's dK_index reduction, which use the same index tensor.  One CSR is kept,
+    with a reference to the index tensor it was built from (so that storage cannot be freed
+    and its address reused while the entry lives); it is rebuilt when the index data (address,
+    shape, strides or version, which views of one storage share), the key count or the offset
+    changes."""
+    global _pair_csr_entry
+    lib = load_library()
+    B, S, K = indices.shape
+    key = (indices.data_ptr(), indices._version, tuple(indices.shape), tuple(indices.stride()), indices.device,
+           int(s_k), int(q_offset))
+    e = _pair_csr_entry
+    if e is not None and e[0] == key:
+        return e[2]
+    _pair_csr_entry = None  # (the old buffer goes before the new one is allocated)
+    nbytes = int(lib.dsa_pair_csr_size(B, S, s_k, K))
+    csr = torch.empty(nbytes, dtype=torch.uint8, device=indices.device)
+    check(lib.dsa_pair_csr_build(ptr(indices), B, S, s_k, K, int(q_offset), ptr(csr), nbytes,
+                                 stream_of(indices.device)), "dsa_pair_csr_build")
+    _pair_csr_entry = (key, indices, csr)
+    return csr
+
+
 def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, workspace_bytes=None,
                    return_mass=False, sinks=None):
     """(dq like q, dkv fp32 [B,S_kv,D_qk]) from dsa_sparse_mla_bwd, plus the head-summed
@@ -505,24 +534,23 @@ def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, 
         ws_bytes = int(workspace_bytes)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
     res = (dq, dkv, mass) if return_mass else (dq, dkv)
+    # one chunk of rows: the dKV reduction takes the shared pair CSR (also the indexer loss's)
+    csr = None
+    if _share_pair_csr and q.dtype == torch.bfloat16 and \
+            int(lib.dsa_sparse_mla_bwd_chunk_rows(B, S, s_kv, D, K, ws_bytes)) >= S:
+        csr = pair_csr(indices, s_kv, q_offset)
+    sk = dsink = None
     if sinks is not None:
         sk = _sink_vector(sinks, H, q.device)
         dsink = torch.zeros(H, dtype=torch.float32, device=q.device)
-        check(
-            lib.dsa_sparse_mla_bwd_sink(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax), ptr(ssum),
-                                        ptr(dq), ptr(dkv), ptr(mass), ptr(sk), ptr(dsink), ptr(ws), ws_bytes,
-                                        _lib.dtype_code(q.dtype), B, S, s_kv, H, D, d_v, K, float(scale),
-                                        int(q_offset), stream_of(q.device)),
-            "dsa_sparse_mla_bwd_sink",
-        )
-        return res + (dsink,)
     check(
-        lib.dsa_sparse_mla_bwd(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax), ptr(ssum), ptr(dq),
-                               ptr(dkv), ptr(mass), ptr(ws), ws_bytes, _lib.dtype_code(q.dtype), B, S, s_kv, H, D, d_v,
-                               K, float(scale), int(q_offset), stream_of(q.device)),
+        lib.dsa_sparse_mla_bwd_ex(ptr(q), ptr(kv), ptr(indices), ptr(out), ptr(dout), ptr(smax), ptr(ssum), ptr(dq),
+                                  ptr(dkv), ptr(mass), ptr(sk), ptr(dsink), ptr(csr),
+                                  0 if csr is None else csr.numel(), ptr(ws), ws_bytes, _lib.dtype_code(q.dtype), B,
+                                  S, s_kv, H, D, d_v, K, float(scale), int(q_offset), stream_of(q.device)),
         "dsa_sparse_mla_bwd",
     )
-    return res
+    return res + (dsink,) if sinks is not None else res
 
 
 def attn_mass(q, kv, indices, smax, ssum, scale, *, q_offset=0):
@@ -1589,10 +1617,16 @@ def indexer_kl_grad_from_mass(query_index, key_index, weight, indices, mass, *, 
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     gsf, gsd = _grad_scale_args(grad_scale, dev)
     sm = torch.empty(B, S, K, dtype=torch.float32, device=dev) if return_softmax else None
+    # one chunk of rows: the dK_index reduction takes the shared pair CSR (the attention
+    # backward's, when it ran on the same indices)
+    csr = None
+    if _share_pair_csr and ws_bytes > 0 and int(lib.dsa_indexer_kl_grad_chunk_rows(B, S, s_k, K, ws_bytes)) >= S:
+        csr = pair_csr(idx, s_k, q_offset)
     check(
-        lib.dsa_indexer_kl_grad_softmax(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i), ptr(dw),
-                                        ptr(loss_rows), ptr(sm), ptr(ws), ws_bytes, B, S, s_k, HI, DI, K,
-                                        int(q_offset), float(loss_scale), float(eps), gsf, ptr(gsd), stream_of(dev)),
+        lib.dsa_indexer_kl_grad_ex(ptr(qi), ptr(ki), ptr(w), ptr(idx), ptr(mass), ptr(dq_i), ptr(dk_i), ptr(dw),
+                                   ptr(loss_rows), ptr(sm), ptr(csr), 0 if csr is None else csr.numel(), ptr(ws),
+                                   ws_bytes, B, S, s_k, HI, DI, K, int(q_offset), float(loss_scale), float(eps), gsf,
+                                   ptr(gsd), stream_of(dev)),
         "dsa_indexer_kl_grad",
     )
     return (dq_i, dk_i, dw, loss_rows, sm) if return_softmax else (dq_i, dk_i, dw, loss_rows)
