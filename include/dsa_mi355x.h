@@ -155,6 +155,19 @@ int dsa_indexer_fwd_noalloc(const void* q, const float* q_scale, const void* k, 
 int dsa_topk(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
              int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset,
              void* stream);
+/*
+ * dsa_topk with a workspace (dsa_topk_workspace_size() bytes, 16-byte aligned; 0 bytes when
+ * s_k <= 16384): rows longer than 16384 keys are read once into per-row candidate lists -
+ * every key at or above a threshold estimated from a sample of the row, which at least k
+ * keys reach, in index order - and selected from those; a row whose list would miss a key
+ * or overflow is selected from its scores as dsa_topk does.  Same contract and results as
+ * dsa_topk (bit for bit).  No counterpart in the reference (its top-k is fused into the
+ * closed indexer op); the fused lightning indexer uses it for its long rows.
+ */
+int64_t dsa_topk_workspace_size(int64_t batch, int64_t s_q, int64_t s_k, int64_t k);
+int dsa_topk_ws(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
+                int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset,
+                void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * The fused lightning indexer (reference: npu_lightning_indexer, ops/aclnn/lightning_indexer/

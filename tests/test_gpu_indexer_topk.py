@@ -208,3 +208,46 @@ def test_lightning_indexer_op_end_to_end():
     sel = idx[:, :, 0].cpu()
     ref_vals = torch.gather(scores, -1, sel.clamp_min(0).long()).masked_fill(sel < 0, float("-inf"))
     assert torch.equal(vals[:, :, 0].cpu(), ref_vals.to(torch.bfloat16))
+
+
+def _long_rows_case(kind, S, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "normal":
+        return torch.randn(1, S, n, generator=g)
+    if kind == "rising":  # scores grow along the row: the sample must span it, not only its start
+        return torch.randn(1, S, n, generator=g) + torch.linspace(0, 6, n)
+    if kind == "clustered":  # one exponent, 22 significant key bits, runs of equal values
+        m = torch.randint(0, 1 << 22, (1, S, n), generator=g)
+        m[:, :, ::5] = m[:, :, :1]
+        return (1.0 + m.double() * 2.0 ** -23).float()
+    if kind == "plateau":  # a constant row with a few outliers: the list would overflow -> fallback
+        x = torch.full((1, S, n), 0.5)
+        x[:, :, torch.randint(0, n, (50,), generator=g)] = torch.randn(50, generator=g) * 1e30
+        return x
+    if kind == "special":  # ties, signed zeros, NaN, infinities
+        x = torch.randint(-3, 4, (1, S, n), generator=g).float()
+        x[0, :, ::7] = -0.0
+        x[0, 1:, 1::13] = float("nan")
+        x[0, 2:, 2::17] = float("inf")
+        x[0, 3:, 4::19] = float("-inf")
+        return x
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind,n,k", [("normal", 40003, 2048), ("normal", 131072, 2048), ("rising", 65536, 2048),
+                                      ("clustered", 50000, 1000), ("plateau", 30000, 2048), ("special", 20000, 2048),
+                                      ("normal", 40000, 4096), ("normal", 17000, 64)])
+@pytest.mark.parametrize("candidates", [True, False])
+def test_topk_long_rows_candidate_lists(kind, n, k, candidates):
+    """Rows longer than 16384 keys: the candidate-list path (one read of the row, selection
+    over the keys at or above a sampled threshold, fallback to the multi-pass selection when
+    the list would miss a key or overflow) and the multi-pass path, bit-exact against the
+    oracle; causal rows of several lengths (the last rows the longest), values bit for bit."""
+    S = 5
+    scores = _long_rows_case(kind, S, n, seed=n + k)
+    q_off = n - S - 2 * 4096  # rows of n - 8196 .. n - 8192 valid keys (more than the 4096-entry lists)
+    idx, vals = _ops().topk_select(scores.to(DEV), k, q_offset=q_off, return_values=True, candidates=candidates)
+    ref = _oracle_topk(scores, k, q_off)
+    assert torch.equal(idx.cpu(), ref)
+    ref_vals = torch.where(ref >= 0, torch.gather(scores, -1, ref.clamp_min(0).long()), torch.tensor(float("-inf")))
+    assert torch.equal(vals.cpu().view(torch.int32), ref_vals.view(torch.int32))

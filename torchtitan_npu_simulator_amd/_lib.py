@@ -42,6 +42,8 @@ _SIGNATURES = {
     "dsa_attn_sink_fold": ([_vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp], _i32),
     "dsa_attn_sink_grad": ([_vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _vp], _i32),
     "dsa_topk": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp], _i32),
+    "dsa_topk_workspace_size": ([_i64, _i64, _i64, _i64], _i64),
+    "dsa_topk_ws": ([_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp], _i32),
     "dsa_lightning_indexer_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _i32, _i64], _i64),
     "dsa_lightning_indexer": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                _i64, _vp, _i64, _vp], _i32),

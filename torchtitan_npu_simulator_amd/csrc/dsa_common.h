@@ -26,6 +26,14 @@ constexpr float kLn2 = 0.6931471805599453f;
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// per-row top-k (topk.hip): dsa_topk with an optional candidate workspace of
+// topk_cand_bytes(batch * s_q, k) bytes, which rows longer than 16384 keys use to select
+// from one read of their scores
+int topk_rows(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
+              int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset, void* cand_ws,
+              void* stream);
+int64_t topk_cand_bytes(int64_t rows, int64_t k);
+
 // ----- lightning-indexer scores shared by the entry points (host) -----
 // dsa_indexer_fwd_ws's work; fill_masked = false leaves the key spans that lie past every
 // query's causal frontier of a tile unwritten (for consumers that read only each row's

@@ -20,9 +20,16 @@ int64_t idx_elem_bytes(int dtype) { return dtype == DSA_F32 ? 4 : dtype == DSA_B
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// bytes of one chunk of `rows` query rows over `nb` batches
+// long rows (more than 16384 keys) select through per-row candidate lists (k <= 4096)
+int64_t cand_bytes(int64_t nb, int64_t rows, int64_t s_k) {
+  return s_k > 16384 ? align256(topk_cand_bytes(nb * rows, 4096)) : 0;
+}
+
+// bytes of one chunk of `rows` query rows over `nb` batches: the score rows, the
+// linear-split pieces, the top-k candidate lists
 int64_t chunk_bytes(int64_t nb, int64_t rows, int64_t s_k, int64_t n_heads, int64_t head_dim, int dtype) {
-  return align256(nb * rows * s_k * 4) + dsa_indexer_fwd_workspace_size(nb, rows, n_heads, head_dim, dtype);
+  return align256(nb * rows * s_k * 4) + align256(dsa_indexer_fwd_workspace_size(nb, rows, n_heads, head_dim, dtype)) +
+         cand_bytes(nb, rows, s_k);
 }
 
 }  // namespace
@@ -69,6 +76,9 @@ extern "C" int dsa_lightning_indexer(const void* q, const float* q_scale, const 
       const int64_t row = b0 * s_q + r0;  // first (batch, row) of the chunk
       const int64_t lin_bytes = dsa_indexer_fwd_workspace_size(nb, nr, n_heads, head_dim, dtype);
       void* lin_ws = lin_bytes ? (void*)((char*)workspace + align256(nb * nr * s_k * 4)) : nullptr;
+      void* cand_ws = cand_bytes(nb, nr, s_k)
+                          ? (void*)((char*)workspace + align256(nb * nr * s_k * 4) + align256(lin_bytes))
+                          : nullptr;
       // (with one batch per pass the chunk's rows are contiguous in q, w and the outputs)
       const char* qc = (const char*)q + row * n_heads * head_dim * es;
       if (int rc = indexer_fwd(qc, q_scale ? q_scale + row * n_heads : nullptr,
@@ -76,8 +86,8 @@ extern "C" int dsa_lightning_indexer(const void* q, const float* q_scale, const 
                                w + row * n_heads, scores, dtype, nb, nr, s_k, n_heads, head_dim, s_k, q_offset + r0,
                                cmp_ratio, lin_ws, lin_bytes, stream, false))
         return rc;
-      if (int rc = dsa_topk(scores, indices + row * topk, values ? values + row * topk : nullptr, nb, nr, s_k, s_k,
-                            topk, q_offset + r0, cmp_ratio, index_offset, stream))
+      if (int rc = topk_rows(scores, indices + row * topk, values ? values + row * topk : nullptr, nb, nr, s_k, s_k,
+                             topk, q_offset + r0, cmp_ratio, index_offset, cand_ws, stream))
         return rc;
     }
   }

@@ -81,18 +81,26 @@ extern "C" int dsa_lightning_indexer_varlen(const void* q, const float* q_scale,
     if (res < 0) return set_error(DSA_ERR_INVALID_ARG, "%s: cmp_residual_k[%lld] < 0", what, (long long)i);
     const int64_t q_off = sparse_mode == 3 ? std::max<int64_t>(0, cmp_ratio * lk + res - lq) : (int64_t)1 << 40;
     // per chunk row: its fp32 scores, plus (fp8, H_I = 64) the linear-split pieces placed after
-    // the chunk's scores at a 256-byte boundary
+    // the chunk's scores at a 256-byte boundary, plus (rows longer than 16384 keys) the top-k
+    // candidate list after those
     const int64_t lin_bytes = dsa_indexer_fwd_workspace_size(1, 1, n_heads, head_dim, dtype);
-    const int64_t row_bytes = 4 * std::max<int64_t>(lk, 1) + lin_bytes;
-    const int64_t rows = std::min<int64_t>(lq, std::max<int64_t>(0, ws_bytes - (lin_bytes ? 256 : 0)) / row_bytes);
+    const bool long_rows = lk > 16384;
+    const int64_t cand_row = long_rows ? topk_cand_bytes(1, topk) - 256 : 0;
+    const int64_t row_bytes = 4 * std::max<int64_t>(lk, 1) + lin_bytes + cand_row;
+    const int64_t rows =
+        std::min<int64_t>(lq, std::max<int64_t>(0, ws_bytes - (lin_bytes ? 256 : 0) - (long_rows ? 512 : 0)) /
+                                  row_bytes);
     if (rows <= 0)
       return set_error(DSA_ERR_INVALID_ARG, "%s: score scratch of %lld bytes holds no row of sequence %lld", what,
                        (long long)ws_bytes, (long long)i);
     for (int64_t r0 = 0; r0 < lq; r0 += rows) {
       const int64_t nr = std::min(rows, lq - r0);
       const int64_t row = q0 + r0;
+      void* lin_ws = lin_bytes ? (void*)((char*)scores_ws + (rows * 4 * lk + 255) / 256 * 256) : nullptr;
+      void* cand_ws = long_rows ? (void*)((char*)scores_ws + (rows * 4 * lk + 255) / 256 * 256 +
+                                          (rows * lin_bytes + 255) / 256 * 256)
+                                : nullptr;
       if (lk > 0) {
-        void* lin_ws = lin_bytes ? (void*)((char*)scores_ws + (rows * 4 * lk + 255) / 256 * 256) : nullptr;
         // (spans past every frontier stay unwritten: the top-k reads only valid prefixes)
         if (int rc = indexer_fwd(at(q, row * n_heads * head_dim * es), at(q_scale, row * n_heads * 4),
                                  at(k, k0 * head_dim * es), at(k_scale, k0 * 4), at(w, row * n_heads * 4), scores_ws,
@@ -101,8 +109,8 @@ extern "C" int dsa_lightning_indexer_varlen(const void* q, const float* q_scale,
           return rc;
       }
       // with no keys the selection sees no candidate and pads the rows with -1
-      if (int rc = dsa_topk(scores_ws, at(indices, row * topk * 4), at(values, row * topk * 4), 1, nr, lk, lk, topk,
-                            q_off + r0, cmp_ratio, index_offset, stream))
+      if (int rc = topk_rows(scores_ws, at(indices, row * topk * 4), at(values, row * topk * 4), 1, nr, lk, lk, topk,
+                             q_off + r0, cmp_ratio, index_offset, cand_ws, stream))
         return rc;
     }
   }

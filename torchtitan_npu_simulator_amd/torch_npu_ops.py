@@ -211,8 +211,10 @@ def indexer_scores(q_idx, k_idx, weights, *, q_scale=None, k_scale=None, q_offse
     return out
 
 
-def topk_select(scores, k, *, q_offset=0, cmp_ratio=1, index_offset=0, return_values=False):
-    """int32 [B,S,k] top-k indices (ascending index order, -1 padded) of fp32 scores."""
+def topk_select(scores, k, *, q_offset=0, cmp_ratio=1, index_offset=0, return_values=False, candidates=True):
+    """int32 [B,S,k] top-k indices (ascending index order, -1 padded) of fp32 scores.  Rows
+    longer than 16384 keys go through candidate lists (dsa_topk_ws) unless ``candidates`` is
+    False (dsa_topk's multi-pass selection; the same result)."""
     lib = load_library()
     require_gpu_tensor(scores, "scores")
     B, S, s_k = scores.shape
@@ -220,9 +222,18 @@ def topk_select(scores, k, *, q_offset=0, cmp_ratio=1, index_offset=0, return_va
         scores = scores.contiguous()
     idx = torch.empty(B, S, k, dtype=torch.int32, device=scores.device)
     vals = torch.empty(B, S, k, dtype=torch.float32, device=scores.device) if return_values else None
+    if not candidates:
+        check(
+            lib.dsa_topk(ptr(scores), ptr(idx), ptr(vals), B, S, s_k, scores.stride(1), k, int(q_offset),
+                         int(cmp_ratio), int(index_offset), stream_of(scores.device)),
+            "dsa_topk",
+        )
+        return idx, vals
+    ws_bytes = int(lib.dsa_topk_workspace_size(B, S, s_k, k))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=scores.device) if ws_bytes else None
     check(
-        lib.dsa_topk(ptr(scores), ptr(idx), ptr(vals), B, S, s_k, scores.stride(1), k, int(q_offset), int(cmp_ratio),
-                     int(index_offset), stream_of(scores.device)),
+        lib.dsa_topk_ws(ptr(scores), ptr(idx), ptr(vals), B, S, s_k, scores.stride(1), k, int(q_offset),
+                        int(cmp_ratio), int(index_offset), ptr(ws), ws_bytes, stream_of(scores.device)),
         "dsa_topk",
     )
     return idx, vals
@@ -419,9 +430,12 @@ def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sp
     max_k = max(max(b - a for a, b in zip(cu_k[:-1], cu_k[1:])), 1)
     max_q = max(max(b - a for a, b in zip(cu_q[:-1], cu_q[1:])), 1)
     rows = max(1, min(max_q, _SCORE_BUDGET_BYTES // (4 * max_k)))
-    # + the linear-split pieces of the chunk's rows (fp8, H_I=64), after a 256-byte boundary
+    # + the linear-split pieces of the chunk's rows (fp8, H_I=64), after a 256-byte boundary,
+    # + for rows longer than 16384 keys the top-k candidate lists (8 bytes per entry, twice K
+    # rounded to 4096 or 8192 entries, and a count per row), after another
     lin = int(lib.dsa_indexer_fwd_workspace_size(1, 1, H, D, _lib.dtype_code(q.dtype)))
-    ws = torch.empty(rows * max_k + (rows * lin + 256) // 4 if lin else rows * max_k, dtype=torch.float32,
+    cand = rows * (8 * (4096 if K <= 2048 else 8192) + 4) + 768 if max_k > 16384 else 0
+    ws = torch.empty(rows * max_k + ((rows * lin + 256) // 4 if lin else 0) + cand // 4, dtype=torch.float32,
                      device=q.device)
     if T == 0:
         return idx, vals
