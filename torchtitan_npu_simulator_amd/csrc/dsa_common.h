@@ -200,6 +200,10 @@ __device__ __forceinline__ int swz8(int r) { return ((r & 3) << 1) | ((r >> 2) &
 // commutes with the kernels' +8-chunk offsets; it ignores row bit 4.  (On 1024-byte rows
 // the b128 reads keep a 2-way conflict: a 16-row read group needs 16 distinct values.)
 __device__ __forceinline__ int swz_kv(int r) { return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
+// swz_a16: the same 1152-byte KV rows read as A operands of v_mfma_f32_16x16x32 (16-lane
+// group g reads chunk 4s + g of rows 16x + 0..15): row bits 1, 2 kept in place, which makes
+// those b128 reads conflict-free; values < 8 as for swz_kv.
+__device__ __forceinline__ int swz_a16(int r) { return r & 6; }
 // swz16: for rows whose stride is a multiple of 256 B with >= 16 chunks: 16 consecutive
 // rows reading one chunk column hit 16 distinct 16-byte slots.
 __device__ __forceinline__ int swz16(int r) { return r & 15; }

@@ -85,7 +85,8 @@ __device__ __forceinline__ uint32_t gather_limit(int64_t tok_limit, int s_kv) {
   return l < 0 ? 0u : (uint32_t)l;
 }
 
-template <int kWaves, int kDqkT = 576>
+// kA16: tile chunks swizzled by swz_a16 (tiles read as 16x16x32 A operands) instead of swz_kv
+template <int kWaves, int kDqkT = 576, bool kA16 = false>
 struct RowGather {
   using G = GatherGeomT<kDqkT>;
   static constexpr int kMaxPerWave = (G::kTileInstr + kWaves - 1) / kWaves;
@@ -107,7 +108,7 @@ struct RowGather {
       const int p = J * 64 + lane;
       const int row = p / G::kRowChunks, pos = p - row * G::kRowChunks;
       L.row[i] = row;
-      L.cbyte[i] = (uint32_t)((pos ^ swz_kv(row)) * 16);
+      L.cbyte[i] = (uint32_t)((pos ^ (kA16 ? swz_a16(row) : swz_kv(row))) * 16);
     }
     return L;
   }

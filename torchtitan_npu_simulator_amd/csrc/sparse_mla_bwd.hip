@@ -5,12 +5,12 @@
 // the backward reduces dKV through a key-major pass instead:
 //
 //   (delta) bwd_delta_kernel: delta = rowsum(dO o O) per (token, head), one streaming pass.
-//   (alpha) bwd_sdp_kernel, workgroup = token x 128 heads, 4 waves x 32 heads (the
-//           forward's gather pipeline): S^T = K Q^T and dP^T = V dO^T as two
-//           v_mfma_f32_32x32x16_bf16 chains sharing every K operand read, P = exp2(S*scale*
+//   (alpha) bwd_sdp_kernel, workgroup = token x 128 heads, 8 waves x 16 heads (the
+//           forward's gather pipeline): S^T = K Q^T and dP^T = V dO^T on
+//           v_mfma_f32_16x16x32_bf16 chains sharing every K operand read, P = exp2(S*scale*
 //           log2e - lse2), dS = P (dP - delta); G[token][slot][128 hg + (0..63 | 64..127)] =
 //           (dS * scale | P) in bf16 and the head-summed P (attention mass) per slot.
-//           bwd_dqk_kernel, workgroup = token x 128 heads, 8 waves: dQ^T += K^T dS^T with
+//           bwd_dqk_kernel, workgroup = token x 128 heads, 12 waves: dQ^T += K^T dS^T with
 //           each wave owning d tiles for two 32-head groups (K read transposed, dS^T from
 //           the G rows staged in LDS).
 //   (beta)  bwd_contrib_kernel, workgroup = token, 12 waves (X slice in VGPRs, G streamed):
@@ -47,45 +47,54 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // --------------------------------------------------------------------------------------
 // (alpha-1) bwd_sdp_kernel: G and the attention mass of a token, all heads in one workgroup
 //
-// The forward kernel's gather pipeline and layout, 4 waves x 32 heads: per 32-key block
-// S^T = K Q^T and dP^T = V dO^T as two v_mfma_f32_32x32x16_bf16 chains that share every K
-// operand read (v = k_nope: the first 32 k-steps serve both; latent Q and dO of the wave's
-// heads stay in VGPRs, rope Q in LDS).  Lane (head n, h) then holds keys 8j + 4h + i of its
-// head: P = exp2(S*scale*log2e - lse2), dS = P (dP - delta); G = (dS * scale | P) is staged
-// transposed in LDS (8-byte pieces of 4 slots, four per type and lane) and leaves as whole
-// 512-byte slot rows; the mass sums P over the 128 heads (butterfly over a wave's 32 head
-// lanes, then the 4 waves).  No dQ here: with no dQ accumulators the wave holds 32 heads,
-// so each K element read from LDS serves twice the heads of the one-kernel backward.
+// The forward's gather pipeline (block of 32 selected KV rows DMA'd into a swizzled LDS
+// tile, double-buffered) with 8 waves x 16 heads, two waves per SIMD: wave w owns heads
+// 16w .. 16w+15 on v_mfma_f32_16x16x32_bf16, S^T = K Q^T and dP^T = V dO^T as two 16-key
+// halves each (four independent accumulation chains that share every K operand read;
+// v = k_nope), so one wave's MFMAs run while the other waits on LDS, exponentials or the
+// barrier.  Latent Q and dO of the wave's heads stay in AGPRs as B operands (lane (head c,
+// group g) holds columns 32s + 8g .. +8 of k-step s), rope Q in LDS; A operands are the
+// tile's K rows 16x + c, chunk 4s + g (swz_a16 keeps those reads conflict-free).  Lane
+// (c, g) then holds keys 16x + 4g + r (r < 4) of head 16w + c: P = exp2(S*scale*log2e -
+// lse2), dS = P (dP - delta); G = (dS * scale | P) is staged transposed in LDS (8-byte
+// pieces of 4 slots) and leaves as whole 512-byte slot rows; the mass sums P over the 128
+// heads (DPP butterfly over a wave's 16 head lanes, then the 8 waves).  No dQ here: with no
+// dQ accumulators Q and dO of 16 heads fit beside two waves per SIMD.  Each K operand read
+// serves 16 heads (twice the LDS reads of a 32-head wave), which the doubled wave count
+// absorbs: b128 read throughput per CU grows with the waves issuing them.
 // --------------------------------------------------------------------------------------
 // piece swizzle of the 256-entry transposed stage (64-byte rows): the b64 writes of one
 // piece by 16 consecutive head rows, and the flush's transposed reads (4 aligned rows x 4
 // pieces per lane quarter), are conflict-free
 __device__ __forceinline__ int g2_swz(int r) { return (r >> 1) & 7; }
 
+constexpr int kSdpWaves = 8;
+
 template <int kD>  // row width of Q and KV: 576 (latent + rope) or 512 (no rope)
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(64 * kSdpWaves, 1)
 bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
-               const uint16_t* __restrict__ dout, const float* __restrict__ smax, const float* __restrict__ ssum,
-               const float* __restrict__ dbuf, uint16_t* __restrict__ gbuf, float* __restrict__ mass, int S, int s_kv,
-               int H, int K, float scale, int64_t q_offset, int row0) {
-  using Gather = RowGather<4, kD>;
+                const uint16_t* __restrict__ dout, const float* __restrict__ smax, const float* __restrict__ ssum,
+                const float* __restrict__ dbuf, uint16_t* __restrict__ gbuf, float* __restrict__ mass, int S,
+                int s_kv, int H, int K, float scale, int64_t q_offset, int row0) {
+  constexpr int kW = kSdpWaves;
+  using Gather = RowGather<kW, kD, true>;
   using Geo = GatherGeomT<kD>;
   constexpr int kPer = Gather::kMaxPerWave;
-  constexpr int kLat = kDv / 16;     // 32 latent k-steps
-  constexpr int kSteps = kD / 16;    // 36 | 32
-  constexpr bool kRope = kSteps > kLat;
+  constexpr int kLat = kDv / 32;     // 16 latent k-steps of 32 columns (dP has only these)
+  constexpr int kSteps = kD / 32;    // 18 | 16
   constexpr int kRB = Geo::kRowBytes;
+  constexpr bool kRope = kSteps > kLat;
   __shared__ u32x4 tile[2][Geo::kTileChunks];
   __shared__ u32x4 qpe[kRope ? kHeadsMax : 1][8];  // rope Q, [head][16 B chunk ^ ((head >> 1) & 7)]
   __shared__ uint2 gst[2][kGW][kBN / 4];  // [parity][G entry][piece of 4 slots ^ g2_swz(entry)]
-  __shared__ float pst[2][4][kBN];
+  __shared__ float pst[2][kW][kBN];
   __shared__ int sidx[GatherGeom::kRing][Gather::kRingInts];
   __shared__ int sh_last;
 
   const int lr = blockIdx.x, tok = row0 + lr, b = blockIdx.z, tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int n = lane & 31, h = lane >> 5;
-  const int hl = wave * 32 + n;  // head (the workgroup holds all heads)
+  const int c = lane & 15, g = lane >> 4;  // MFMA column (head) and k group; A row c
+  const int hl = wave * 16 + c;            // head (the workgroup holds all heads)
   const bool hok = hl < H;
   const int64_t row_id = (int64_t)b * S + tok;
   const int64_t hrow = row_id * H + (hok ? hl : 0);
@@ -101,23 +110,24 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
 #pragma unroll
     for (int i = 0; i < 3; ++i) Gather::issue_idx(ridx, K, i, sidx[i], lane);
   }
-  // latent Q and dO of head hl: k-step s holds columns 16s + 8h .. +8 (B operands)
-  u32x4 qb[kLat], db[kLat], qr[4];
+  // latent Q and dO of head hl: k-step s holds columns 32s + 8g .. +8; lane group g also
+  // loads rope chunks 2g, 2g + 1 for the LDS copy (step kLat + j reads chunk 4j + g)
+  u32x4 qb[kLat], db[kLat], qr[2];
   {
     const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kD);
     const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
 #pragma unroll
-    for (int st = 0; st < kLat; ++st) qb[st] = qh[2 * st + h];
+    for (int st = 0; st < kLat; ++st) qb[st] = qh[4 * st + g];
 #pragma unroll
-    for (int st = 0; st < kLat; ++st) db[st] = dh[2 * st + h];
+    for (int st = 0; st < kLat; ++st) db[st] = dh[4 * st + g];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qr[j] = kRope ? qh[64 + 4 * h + j] : (u32x4){0u, 0u, 0u, 0u};
+    for (int j = 0; j < 2; ++j) qr[j] = kRope ? qh[64 + 2 * g + j] : (u32x4){0u, 0u, 0u, 0u};
   }
   const float mx = smax[hrow], sm = ssum[hrow];
   const float dlt = dbuf[((int64_t)b * gridDim.x + lr) * H + (hok ? hl : 0)];
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (mrow)  // slots past the last usable block carry no mass
-    for (int j = nblk * kBN + tid; j < K; j += 256) mrow[j] = 0.f;
+    for (int j = nblk * kBN + tid; j < K; j += 64 * kW) mrow[j] = 0.f;
   if (nblk == 0) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the ring DMA has landed before the LDS is released
     return;
@@ -127,60 +137,60 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
 #pragma unroll
     for (int st = 0; st < kLat; ++st) qb[st] = db[st] = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qr[j] = (u32x4){0u, 0u, 0u, 0u};
+    for (int j = 0; j < 2; ++j) qr[j] = (u32x4){0u, 0u, 0u, 0u};
   }
   if constexpr (kRope) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ch = 4 * h + j;
+    for (int j = 0; j < 2; ++j) {  // rope chunks 64..71: lane group g writes 2g, 2g + 1
+      const int ch = 2 * g + j;
       qpe[hl][ch ^ ((hl >> 1) & 7)] = qr[j];
     }
   }
   const float lse2 = (hok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0
   const float delta = hok ? dlt : 0.f;
   const float scale_log2 = scale * kLog2e;
+  // landed before any DMA; held in AGPRs, which the MFMAs read directly as B operands
 #pragma unroll
-  // landed before any DMA; held in AGPRs, which the MFMAs read directly as B operands, so
-  // the VGPRs stay free for the softmax and for prefetching the K operands from LDS
   for (int st = 0; st < kLat; ++st) asm volatile("" : "+a"(qb[st]), "+a"(db[st]));
 
-  uint32_t ka_off[4];  // A operand (K row n, chunk (2s + h) ^ swz_kv(n)), s = 4u + s0 -> + 128 u
+  // A operand of half x, k-step s = 2u + s0: K row 16x + c, chunk (4s + g) = 8u + (4 s0 + g),
+  // swizzled inside its group of 8 -> ka_off[x][s0] + 128 u
+  uint32_t ka_off[2][2];
 #pragma unroll
-  for (int s0 = 0; s0 < 4; ++s0) ka_off[s0] = n * kRB + 16 * ((2 * s0 + h) ^ swz_kv(n));
-  const lds_char* qpe_b = lds_bytes(&qpe[0][0]);
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int s0 = 0; s0 < 2; ++s0) ka_off[x][s0] = (16 * x + c) * kRB + 16 * ((4 * s0 + g) ^ swz_a16(16 * x + c));
   // G entries of head hl: dS at 128 (hl / 64) + hl % 64, P 64 entries later
   const int e_ds = 128 * (hl >> 6) + (hl & 63), e_p = e_ds + 64;
 
   // G rows and mass of block fb from stage fb & 1 -> global, in three parts.  G part u:
-  // slots 16u .. 16u+15; lane group (wave, G) takes entry octets oct and oct + 16
-  // (oct = 4 wave + G); two transposed reads give lane c the octet's 8 values of slot
-  // 16u + c (source lane c supplies entry row 8 oct + 4x + c/4, slots 16u + 4(c % 4) ..+3).
+  // slots 16u .. 16u+15; lane group (wave, G) takes entry octet oct = 4 wave + G; two
+  // transposed reads give lane c the octet's 8 values of slot 16u + c.
   auto flush_part = [&](int fb, int part) {
     const int sb = fb & 1;
     if (part == 2) {
       if (mrow && tid < kBN && fb * kBN + tid < K)
-        mrow[fb * kBN + tid] = (pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid]);
+        mrow[fb * kBN + tid] = ((pst[sb][0][tid] + pst[sb][1][tid]) + (pst[sb][2][tid] + pst[sb][3][tid])) +
+                               ((pst[sb][4][tid] + pst[sb][5][tid]) + (pst[sb][6][tid] + pst[sb][7][tid]));
       return;
     }
     const int c16 = lane & 15;
     const lds_char* gb = lds_bytes(&gst[sb][0][0]);
     const int slot = fb * kBN + 16 * part + c16;
+    const int oct = 4 * wave + (lane >> 4);
+    const lds_char* a[2];
 #pragma unroll
-    for (int o2 = 0; o2 < 2; ++o2) {
-      const int oct = 4 * wave + (lane >> 4) + 16 * o2;
-      const lds_char* a[2];
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        const int row = 8 * oct + 4 * x + (c16 >> 2);
-        const int piece = 4 * part + (c16 & 3);
-        a[x] = gb + row * (kBN * 2) + 8 * (piece ^ g2_swz(row));
-      }
-      const u32x4 v = lds_read_tr_pair(a[0], a[1]);
-      *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 8 * oct) = v;  // (rows padded to whole blocks)
+    for (int x = 0; x < 2; ++x) {
+      const int row = 8 * oct + 4 * x + (c16 >> 2);
+      const int piece = 4 * part + (c16 & 3);
+      a[x] = gb + row * (kBN * 2) + 8 * (piece ^ g2_swz(row));
     }
+    const u32x4 v = lds_read_tr_pair(a[0], a[1]);
+    *reinterpret_cast<u32x4*>(grow + (int64_t)slot * kGW + 8 * oct) = v;  // (rows padded to whole blocks)
   };
 
   const typename Gather::PackedLanes gl = Gather::packed_lanes(wave, lane);
+  const lds_char* qpe_b = lds_bytes(&qpe[0][0]);
   if (wave == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // ring entries 0..2 landed
   __syncthreads();                                                  // publishes them and qpe
   uint32_t vm_cur = Gather::ring_valid(sidx[0], lane, lim, K);
@@ -190,64 +200,62 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
-  constexpr int kQBatch = 4;
-  constexpr int kQB = kSteps / kQBatch;  // 9 | 8 batches
+  constexpr int kQBatch = 1;             // k-steps per batch
+  constexpr int kQB = kSteps / kQBatch;  // 18 | 16 batches
   static_assert(kQB >= kPer, "one row DMA per batch");
 
-  // P / dS / G staging / mass of block pb (its S^T, dP^T in sp, pp; validity vm), in pieces
-  // so they can be spread over the next block's MFMA batches:
-  //   0: P and dS (16 values),  1: stage dS,  2: stage P,  3: mass butterfly + partial
-  float pv[16], dv[16];
-  auto pds_piece = [&](int piece, const f32x16& sp, const f32x16& pp, uint32_t vm, int pb) {
-    const uint32_t vmh = vm >> (4 * h);  // bit 8j + i: key 8j + 4h + i
+  // P / dS / G staging / mass of block pb (S^T, dP^T halves sp, pp; validity vm), in pieces
+  // spread over the next block's MFMA batches:
+  //   0: P (8 values) and its stage,  1: dS and its stage,  3: mass butterfly + partial
+  // value 4x + r of a lane: key 16x + 4g + r
+  float pv[8];
+  auto stage = [&](int sb, int e, const float (&src)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int pc = 4 * x + g;  // slots 16x + 4g .. +3
+      gst[sb][e][pc ^ g2_swz(e)] = make_uint2(pack_bf16x2(src[4 * x], src[4 * x + 1]),
+                                              pack_bf16x2(src[4 * x + 2], src[4 * x + 3]));
+    }
+  };
+  auto pds_piece = [&](int piece, const f32x4 (&sp)[2], const f32x4 (&pp)[2], uint32_t vm, int pb) {
     const int sb = pb & 1;
     if (piece == 0) {
       if (vm == 0xffffffffu) {  // (wave-uniform) every key of the block is valid: no masking
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float p = __builtin_amdgcn_exp2f(sp[v] * scale_log2 - lse2);
-          pv[v] = p;
-          dv[v] = p * (pp[v] - delta) * scale;
-        }
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pv[4 * x + r] = __builtin_amdgcn_exp2f(sp[x][r] * scale_log2 - lse2);
       } else {
+        const uint32_t vmg = vm >> (4 * g);  // bit 16x + r: key 16x + 4g + r
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const bool ok = (vmh >> (8 * (v >> 2) + (v & 3))) & 1u;
-          const float p = ok ? __builtin_amdgcn_exp2f(sp[v] * scale_log2 - lse2) : 0.f;
-          pv[v] = p;
-          dv[v] = p * (pp[v] - delta) * scale;
-        }
-      }
-    } else if (piece == 1 || piece == 2) {
-      const float* src = piece == 1 ? dv : pv;
-      const int e = piece == 1 ? e_ds : e_p;
+        for (int x = 0; x < 2; ++x)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int pc = 2 * j + h;  // slots 8j + 4h .. +3
-        gst[sb][e][pc ^ g2_swz(e)] = make_uint2(pack_bf16x2(src[4 * j], src[4 * j + 1]),
-                                                pack_bf16x2(src[4 * j + 2], src[4 * j + 3]));
+          for (int r = 0; r < 4; ++r) {
+            const bool ok = (vmg >> (16 * x + r)) & 1u;
+            pv[4 * x + r] = ok ? __builtin_amdgcn_exp2f(sp[x][r] * scale_log2 - lse2) : 0.f;
+          }
       }
-    } else {
-      // mass: butterfly over the 32 head lanes (lane bits 4..1 halve the 16 values, bit 0
-      // completes the sum); lane l ends with value (l >> 1) & 15.  Step bit 4 exchanges
-      // rows of 16 lanes with one permlane16 swap; bits 3..0 use DPP.  The halves are
-      // chosen by bit masks (a select between two array elements would become an indexed
-      // read).
-      const bool odd = (lane >> 4) & 1;
+      stage(sb, e_p, pv);
+    } else if (piece == 1) {
+      float dv[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {  // even rows keep value j, odd rows j + 8
-        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(pv[j]), __float_as_uint(pv[j + 8]), false, false);
-        const float even_sum = pv[j] + __uint_as_float(r[1]), odd_sum = pv[j + 8] + __uint_as_float(r[0]);
-        pv[j] = odd ? odd_sum : even_sum;
-      }
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dv[4 * x + r] = pv[4 * x + r] * (pp[x][r] - delta) * scale;
+      stage(sb, e_ds, dv);
+    } else if (piece == 3) {
+      // mass: butterfly over the 16 head lanes of a lane group (lane bits 3..1 halve the 8
+      // values, bit 0 completes the sum); lane c ends with value (c >> 1) & 7.  The halves
+      // are chosen by bit masks (a select between two array elements would become an
+      // indexed read).
       auto bstep = [&](auto mc, int nh) {
         constexpr int m = decltype(mc)::value;
         const uint32_t up = ((lane & m) != 0) ? 0xffffffffu : 0u;
 #pragma unroll
         for (int j = 0; j < nh; ++j) {
-          const uint32_t a = __float_as_uint(pv[j]), b = __float_as_uint(pv[j + nh]);
-          const float send = __uint_as_float((a & up) | (b & ~up));
-          const float keep = __uint_as_float((b & up) | (a & ~up));
+          const uint32_t a = __float_as_uint(pv[j]), bb = __float_as_uint(pv[j + nh]);
+          const float send = __uint_as_float((a & up) | (bb & ~up));
+          const float keep = __uint_as_float((bb & up) | (a & ~up));
           pv[j] = keep + lane_xor<m>(send);
         }
       };
@@ -256,8 +264,8 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
       bstep(std::integral_constant<int, 2>{}, 1);
       const float tot = pv[0] + lane_xor<1>(pv[0]);
       if ((lane & 1) == 0) {
-        const int r = (lane >> 1) & 15;
-        pst[sb][wave][8 * (r >> 2) + 4 * h + (r & 3)] = tot;
+        const int v = (c >> 1) & 7;
+        pst[sb][wave][16 * (v >> 2) + 4 * g + (v & 3)] = tot;
       }
     }
   };
@@ -266,11 +274,14 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   // DMA'd into the other tile, with P / dS / G / mass of block blk-1 and the G and mass
   // stores of block blk-2 spread over its MFMA batches; the iteration ends with its DMAs
   // landed and one barrier (which also publishes blk-1's stage for its flush).
-  // (the loop below is unrolled by two so that block blk's accumulators and block blk-1's
-  // alternate between two register sets instead of being copied every block)
-  f32x16 s_a = (f32x16){0.f}, p_a = (f32x16){0.f}, s_b = (f32x16){0.f}, p_b = (f32x16){0.f};
+  // (unrolled by two so that block blk's accumulators and block blk-1's alternate between
+  // two register sets instead of being copied every block)
+  f32x4 s_a[2], p_a[2], s_b[2], p_b[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) s_a[x] = p_a[x] = s_b[x] = p_b[x] = (f32x4){0.f, 0.f, 0.f, 0.f};
   uint32_t vm_prev = 0u;
-  auto block_iter = [&](int blk, f32x16& sacc, f32x16& pacc, const f32x16& sprev, const f32x16& pprev) {
+  auto block_iter = [&](int blk, f32x4 (&sacc)[2], f32x4 (&pacc)[2], const f32x4 (&sprev)[2],
+                        const f32x4 (&pprev)[2]) {
     if (wave == 0 && blk + 3 < nblk)
       Gather::issue_idx(ridx, K, blk + 3, sidx[(blk + 3) & (GatherGeom::kRing - 1)], lane);
     const lds_char* tb = lds_bytes(&tile[blk & 1][0]);
@@ -279,20 +290,24 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
     const int rows_left = K - (blk + 1) * kBN;
     const uint32_t vm_next = Gather::ring_valid(ring, lane, lim, rows_left);
     uint32_t raw_next = Gather::ring_slot(ring, 0, gl);
-    sacc = (f32x16){0.f};
-    pacc = (f32x16){0.f};
-    u32x4 a[2][kQBatch], rope[kQBatch];
-    auto read_a = [&](u32x4 (&dst)[kQBatch], int sb) {
 #pragma unroll
-      for (int u = 0; u < kQBatch; ++u) dst[u] = lds_read16(tb + ka_off[u] + 128 * (sb / kQBatch));
+    for (int x = 0; x < 2; ++x) sacc[x] = pacc[x] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    u32x4 a[2][kQBatch][2];  // [buffer][step of the batch][half]
+    u32x4 rope[2];  // rope B operands of steps kLat, kLat + 1 (chunk 4j + g of the rope)
+    auto read_a = [&](u32x4 (&dst)[kQBatch][2], int sb) {  // steps sb .. sb + kQBatch - 1
+#pragma unroll
+      for (int u = 0; u < kQBatch; ++u)
+#pragma unroll
+        for (int x = 0; x < 2; ++x) dst[u][x] = lds_read16(tb + ka_off[x][(sb + u) & 1] + 128 * ((sb + u) >> 1));
     };
     read_a(a[0], 0);
     static_for<kQB>([&](auto nbc) {
       constexpr int nb = decltype(nbc)::value;
+      constexpr int s0 = nb * kQBatch;
       if constexpr (nb + 1 < kQB) read_a(a[(nb + 1) & 1], (nb + 1) * kQBatch);
-      if constexpr (kRope && (nb + 1) * kQBatch == kLat) {
-#pragma unroll
-        for (int e = 0; e < kQBatch; ++e) rope[e] = lds_read16(qpe_b + hl * 128 + 16 * ((2 * e + h) ^ ((hl >> 1) & 7)));
+      if constexpr (kRope && nb + 1 >= kLat && nb + 1 < kSteps) {  // rope B operand one batch ahead
+        constexpr int j = nb + 1 - kLat;
+        rope[j] = lds_read16(qpe_b + hl * 128 + 16 * ((4 * j + g) ^ ((hl >> 1) & 7)));
       }
       if constexpr (nb < kPer) {
         const uint32_t raw = raw_next;
@@ -301,38 +316,37 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
       }
 #pragma unroll
       for (int u = 0; u < kQBatch; ++u) {
-        constexpr int s0 = nb * kQBatch;
+        const u32x4 bq = s0 + u < kLat ? qb[(s0 + u) % kLat] : rope[(s0 + u - kLat) & 1];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) sacc[x] = mfma16x16x32(as_bf16x8(a[nb & 1][u][x]), as_bf16x8(bq), sacc[x]);
         if constexpr (s0 < kLat) {
-          sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(qb[s0 + u]), sacc);
-          pacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(db[s0 + u]), pacc);
-        } else {
-          sacc = mfma32x32x16(as_bf16x8(a[nb & 1][u]), as_bf16x8(rope[u]), sacc);
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+            pacc[x] = mfma16x16x32(as_bf16x8(a[nb & 1][u][x]), as_bf16x8(db[s0 + u]), pacc[x]);
         }
       }
-      // the four pieces go to every other batch so that their VALU work spreads over the
-      // block's MFMAs
-      if constexpr (nb % 2 == 0 && nb / 2 < 4) {
-        if (blk > 0) pds_piece(nb / 2, sprev, pprev, vm_prev, blk - 1);
+      // the pieces of block blk-1 and the flush of block blk-2 (after the block's last row
+      // DMA) are spread over the block's MFMAs
+      if constexpr (nb == 1 || nb == 4 || nb == 7) {
+        if (blk > 0) pds_piece(nb == 1 ? 0 : nb == 4 ? 1 : 3, sprev, pprev, vm_prev, blk - 1);
       }
-      // one wave per SIMD issues in order: put the batch's VALU, LDS and memory work in the
-      // gaps between its MFMAs, not after them
-      static_for<(nb * kQBatch < kLat ? 2 * kQBatch : kQBatch)>([&](auto) {
+      if constexpr (nb >= kPer && (nb == 9 || nb == 11 || nb == 13)) {
+        if (blk > 1) flush_part(blk - 2, (nb - 9) / 2);
+      }
+      static_for<(s0 < kLat ? 4 * kQBatch : 2 * kQBatch)>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
         __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
-        __builtin_amdgcn_sched_group_barrier(0x006, 6, 0);  // VALU / SALU
+        __builtin_amdgcn_sched_group_barrier(0x006, 4, 0);  // VALU / SALU
         __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // VMEM (row DMA, G stores)
       });
       __builtin_amdgcn_sched_barrier(0);
     });
-    // block blk-2's G and mass stores go out after the block's last row DMA; at least four
-    // store instructions follow that DMA (two per G part, unconditional), so vmcnt(4) waits
-    // for every DMA (they retire in order) but not for the stores
+    // block blk-2's G and mass stores went out after the block's last row DMA; two store
+    // instructions follow that DMA unconditionally (one per G part), so vmcnt(2) waits for
+    // every DMA (they retire in order) but not for the stores
     if (blk > 1) {
-      flush_part(blk - 2, 0);
-      flush_part(blk - 2, 1);
-      flush_part(blk - 2, 2);
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
+      asm volatile("s_waitcnt vmcnt(2)" ::: "memory");  // block blk+1 and ring entry blk+3 landed
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
@@ -348,9 +362,14 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   if (blk < nblk) block_iter(blk, s_a, p_a, s_b, p_b);
   // the last block's P / dS / G / mass, the stores of the one before, then its own stores
   const bool last_a = nblk & 1;
-  const f32x16 s_last = last_a ? s_a : s_b, p_last = last_a ? p_a : p_b;
+  f32x4 s_last[2], p_last[2];
 #pragma unroll
-  for (int piece = 0; piece < 4; ++piece) pds_piece(piece, s_last, p_last, vm_prev, nblk - 1);
+  for (int x = 0; x < 2; ++x) {
+    s_last[x] = last_a ? s_a[x] : s_b[x];
+    p_last[x] = last_a ? p_a[x] : p_b[x];
+  }
+#pragma unroll
+  for (int piece = 0; piece < 4; ++piece) pds_piece(piece, s_last, p_last, vm_prev, nblk - 1);  // (2: none)
   if (nblk > 1) {
     flush_part(nblk - 2, 0);
     flush_part(nblk - 2, 1);
@@ -1018,7 +1037,7 @@ static int sparse_mla_bwd_impl(const void* q, const void* kv, const int32_t* ind
     {
       const TimedLaunch tl(rope ? "bwd_sdp_kernel" : "bwd_sdp_kernel<512>", st);
       auto* kern = rope ? bwd_sdp_kernel<kDqk> : bwd_sdp_kernel<kDv>;
-      kern<<<ga, 256, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout, softmax_max,
+      kern<<<ga, 64 * kSdpWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout, softmax_max,
                                softmax_sum, dbuf, gbuf, mass, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale,
                                q_offset, (int)r0);
     }
