@@ -70,6 +70,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   __shared__ uint16_t eh[kH][kB + 8];       // E as [head][slot]
   __shared__ float red[12];
   __shared__ int ring[4][kB];                 // slot indices of blocks b & 3
+  __shared__ int sh_last;
 
   const int lr = blockIdx.x, b = blockIdx.y;
   const int tok = row0 + lr;
@@ -80,7 +81,19 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   const int64_t limit = tok + q_offset;
   const uint16_t* kb = ki + (int64_t)b * s_k * kD;
   const int head_a = 16 * wave + col;  // A-operand row (head) of this lane
-  const int nblocks = (K + kB - 1) / kB;
+  // slots past the row's last usable one (the causal limit cuts early rows short) hold no
+  // valid key: phases 1 and 3 stop at the block that holds it
+  if (tid == 0) sh_last = -1;
+  __syncthreads();
+  {
+    int last = -1;
+    for (int j = tid; j < K; j += 256)
+      if (ok_slot(ridx[j], s_k, limit)) last = j;
+    if (last >= 0) atomicMax(&sh_last, last);
+  }
+  __syncthreads();
+  const int n_used = sh_last + 1;  // slots [0, n_used) hold every valid slot
+  const int nblocks = (n_used + kB - 1) / kB;
 
   // the upstream gradient may live on the device (no host round trip for the caller)
   const float gsc = grad_scale_dev ? grad_scale * grad_scale_dev[0] : grad_scale;
@@ -145,7 +158,7 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
 #pragma unroll
       for (int r = 0; r < 4; ++r) wall[ht][r] = w[row_id * kH + 16 * ht + 4 * g + r];
     }
-    const int nsb = (K + 15) / 16;  // 16-slot groups
+    const int nsb = (n_used + 15) / 16;  // 16-slot groups up to the last usable slot
     auto slot_of = [&](int i) { return 16 * i + col; };  // group i = 4 blk + wave
     auto load_idx1 = [&](int i) -> int {
       const int sl = slot_of(i);
