@@ -411,6 +411,9 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=5
         "zero_i32_kernel": ("hbm", 0, 0, 4 * (s_kv + 1) + 4 * (s_ki + 1)),
         "csr_count_kernel<count>": ("hbm", 0, 0, 8 * Ka * S),
         "csr_count_kernel<fill>": ("hbm", 0, 0, 8 * Ka * S + 8 * P),
+        # (the same list, staged per key in LDS and written as 32-byte sectors)
+        "csr_fill_staged_kernel": ("hbm", 0, 0, 8 * Ka * S + 8 * P),
+        "csr_count_kernel<fill, repair>": ("hbm", 0, 0, 0),
         "csr_scan_kernel": ("hbm", 0, 0, 12 * (s_kv + s_ki)),
         "csr_seg_key_kernel": ("hbm", 0, 0, 8 * (s_kv + s_ki)),
         # contribution rows read (the other half of the scatter payload), fp32 dKV written | pair list

@@ -102,7 +102,8 @@ def test_backward_bytes_split_into_contract_and_intermediate():
     payload = (w["bwd_contrib_kernel<2>"][1] - 2 * H * (576 + 512) * S - 4 * K * S) + \
         (w["dkv_reduce_kernel<72>"][1] - 4 * 576 * S)
     assert payload == 4 * 576 * P
-    assert all(w[k][1] == 0 for k in ("csr_count_kernel<count>", "csr_count_kernel<fill>", "csr_scan_kernel"))
+    assert all(w[k][1] == 0 for k in ("csr_count_kernel<count>", "csr_count_kernel<fill>", "csr_fill_staged_kernel",
+                                      "csr_scan_kernel"))
     ktimes = {"bwd_contrib_kernel<2>": (5.0, 1), "csr_count_kernel<fill>": (0.2, 1)}
     rows = {r["kernel"]: r for r in bench.kernel_table(ktimes, w, steps=1)}
     beta = rows["bwd_contrib_kernel<2>"]

@@ -104,6 +104,45 @@ def test_bwd_long_kv_spans_several_counting_ranges(K):
     assert float(dkv[0, ~touched].abs().sum()) == 0.0
 
 
+@pytest.mark.parametrize("s_kv", [3584, 12000])
+def test_bwd_staged_pair_fill_key_ranges(s_kv):
+    """Key spaces of up to four 3584-key ranges take the staged CSR fill (pairs staged per
+    key in LDS and written as 32-byte sectors of the key's list): one range exactly, and
+    four with a partial last one; slots at the range edges in every row."""
+    S, H, K = 160, 16, 256
+    q_offset = s_kv - S
+    q, kv, dout, scale = attn_inputs(S, H, q_offset=q_offset, seed=23)
+    g = torch.Generator().manual_seed(23)
+    edge = torch.tensor([e for e in (0, 3583, 3584, 7167, 7168, 10751, 10752, s_kv - S) if e < s_kv - S + 1])
+    idx = torch.empty(1, S, K, dtype=torch.int32)
+    for s in range(S):
+        pick = torch.randperm(s + q_offset + 1, generator=g)[: 2 * K]
+        pick = pick[~torch.isin(pick, edge)][: K - len(edge)]
+        idx[0, s] = torch.sort(torch.cat([edge, pick])).values.int()
+    out, smax, ssum, dq, dkv = _gpu_fwd_bwd(q, kv, idx, dout, scale, q_offset)
+    _, ref_lse = O.sparse_mla_fwd(q, kv, idx, scale, q_offset=q_offset)
+    rdq, rdkv, _ = O.sparse_mla_bwd_closed_form(q, kv, idx, out, ref_lse, dout, scale, q_offset=q_offset)
+    assert rel_err(dq, rdq) <= BF16_TOL, rel_err(dq, rdq)
+    assert rel_err(dkv, rdkv) <= BF16_TOL, rel_err(dkv, rdkv)
+
+
+def test_bwd_key_repeated_inside_a_row():
+    """A key selected twice by one row (never the case for top-k output) counts twice, as the
+    oracle's scatter-add does: the staged CSR fill detects the repeat and the unstaged fill
+    redoes the pair list."""
+    S, H, K = 128, 16, 64
+    q, kv, dout, scale = attn_inputs(S, H, seed=24)
+    idx = rand_indices(S, K, seed=24)
+    for s in (40, 77, 127):  # rows with more than K causal keys: every slot valid
+        idx[0, s, 1] = idx[0, s, 0]
+        idx[0, s, 9] = idx[0, s, 5]
+    out, smax, ssum, dq, dkv = _gpu_fwd_bwd(q, kv, idx, dout, scale)
+    _, ref_lse = O.sparse_mla_fwd(q, kv, idx, scale)
+    rdq, rdkv, _ = O.sparse_mla_bwd_closed_form(q, kv, idx, out, ref_lse, dout, scale)
+    assert rel_err(dq, rdq) <= BF16_TOL, rel_err(dq, rdq)
+    assert rel_err(dkv, rdkv) <= BF16_TOL, rel_err(dkv, rdkv)
+
+
 def test_bwd_bf16_chunked_workspace_matches_single_pass():
     """A workspace that only fits a few query rows gives the same gradients (row chunking)."""
     S, H, K = 128, 32, 64

@@ -96,8 +96,17 @@ template <bool kFill, bool kVec>
 __global__ void __launch_bounds__(256)
 csr_count_kernel(const int32_t* __restrict__ idx, int* __restrict__ table, const int* __restrict__ chunk_off,
                  const int* __restrict__ row_ptr, int* __restrict__ pairs, int S, int s_kv, int K, int64_t q_offset,
-                 int row0, int rows, int b, int n_ranges, int rows_per_wg) {
+                 int row0, int rows, int b, int n_ranges, int rows_per_wg, int* __restrict__ dup_flag) {
   extern __shared__ int hist[];
+  // dup_flag (when given): the count pass clears it; the fill then runs only if the staged
+  // fill before it raised it
+  if (dup_flag) {
+    if (!kFill) {
+      if (blockIdx.x == 0 && threadIdx.x == 0) *dup_flag = 0;
+    } else if (*dup_flag == 0) {
+      return;
+    }
+  }
   const int rb = blockIdx.x / n_ranges, kr = blockIdx.x - rb * n_ranges;
   const int key0 = kr * kLdsKeys, nkeys = min(kLdsKeys, s_kv - key0);
   const int r0 = rb * rows_per_wg;
@@ -119,17 +128,149 @@ csr_count_kernel(const int32_t* __restrict__ idx, int* __restrict__ table, const
                             [&](int u, int pair) { pairs[atomicAdd(&hist[u], 1)] = pair; });
 }
 
+// Staged fill (key spaces of at most kFillKeys * kFillRangesMax keys): workgroup = kFillRB
+// consecutive row blocks of the count pass x a kFillKeys-key range.  A key's pairs from those
+// row blocks are contiguous in its list (row blocks in order, rows in order within each),
+// starting at row_ptr[key] + chunk_off[rb0 / kColChunk][key] + table[rb0][key].  They are
+// staged per key in LDS one aligned 8-pair (32-byte) sector of the list at a time, and a
+// sector whose pairs are all this workgroup's leaves as one 32-byte write once its last pair
+// is placed; the first sector of a key's run (shared with the run before it) and its last
+// open sector go out pair by pair.  Scattered 4-byte stores would each leave L2 as a 32-byte
+// write: the lines of a list are evicted before the neighbouring runs reach them.  Each row's
+// positions are handed out (LDS atomics) and its pairs staged, then (after a barrier) its
+// completed sectors are written, then (after another) the next row may reuse their slots.
+// That needs each key at most once per row, which top-k output is; a workgroup that meets a
+// key twice in one row raises *dup_flag, and the unstaged fill (csr_count_kernel<true>, which
+// runs after this one only when the flag is set) redoes the whole list.
+constexpr int kFillKeys = 3584;
+constexpr int kFillRangesMax = 4;
+constexpr int kFillRB = 4;          // count-pass row blocks per fill workgroup
+constexpr int kFillThreads = 512;
+
+template <bool kVec>
+__global__ void __launch_bounds__(kFillThreads)
+csr_fill_staged_kernel(const int32_t* __restrict__ idx, const int* __restrict__ table,
+                       const int* __restrict__ chunk_off, const int* __restrict__ row_ptr, int* __restrict__ pairs,
+                       int* __restrict__ dup_flag, int S, int s_kv, int K, int64_t q_offset, int row0, int rows, int b,
+                       int n_franges, int rows_per_rb, int n_rb) {
+  __shared__ int cur[kFillKeys];             // next list position of each key of the range
+  __shared__ int first[kFillKeys];           // the workgroup's first list position of each key
+  __shared__ int4 stg[kFillKeys][2];         // the open sector of each key (pair at position & 7)
+  __shared__ int seen[kFillKeys];            // the last row (within the workgroup) that placed the key
+  __shared__ int dup;
+  // the n_franges workgroups of one row group read the same index rows: they run on one XCD
+  // (workgroups go to the 8 XCDs round-robin by id), in consecutive dispatch slots, so the
+  // rows come from that XCD's L2 after the first read.  Group g runs on XCD g % 8; the grid
+  // holds 8 * n_franges * ceil(groups / 8) workgroups and the surplus ones return.
+  const int xcd = (int)blockIdx.x % 8, slot = (int)blockIdx.x / 8;
+  const int grp = xcd + 8 * (slot / n_franges), kr = slot % n_franges;
+  const int rb0 = grp * kFillRB;
+  if (rb0 >= n_rb) return;
+  const int key0 = kr * kFillKeys, nkeys = min(kFillKeys, s_kv - key0);
+  const int r0 = rb0 * rows_per_rb, r1 = min(rows, min(rb0 + kFillRB, n_rb) * rows_per_rb);
+  const int t = threadIdx.x;
+  {
+    const int* trow = table + (int64_t)rb0 * s_kv + key0;
+    const int* coff = chunk_off + (int64_t)(rb0 / kColChunk) * s_kv + key0;
+    for (int j = t; j < nkeys; j += kFillThreads) {
+      const int p0 = row_ptr[key0 + j] + coff[j] + trow[j];
+      cur[j] = p0;
+      first[j] = p0;
+      seen[j] = -1;
+    }
+    if (t == 0) dup = 0;
+  }
+  __syncthreads();
+  int* const stg_i = reinterpret_cast<int*>(&stg[0][0]);
+  constexpr int kW = kVec ? 4 : 1;
+  constexpr int kPer = (2048 + kFillThreads * kW - 1) / (kFillThreads * kW);  // loads per row and chunk
+  constexpr int kP = kPer * kW;                                                // pairs per thread and row
+  for (int lr0 = r0; lr0 < r1; lr0 += kCsrRowBatch) {
+    for (int j0 = 0; j0 < K; j0 += kFillThreads * kPer * kW) {
+      int v[kCsrRowBatch][kPer][kW];
+#pragma unroll
+      for (int a = 0; a < kCsrRowBatch; ++a) {
+        const int lr = min(lr0 + a, r1 - 1);
+        const int32_t* ridx = idx + ((int64_t)b * S + row0 + lr) * K;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+          const int j = j0 + kW * (t + kFillThreads * u);
+          if constexpr (kVec) {
+            const int4 w = *reinterpret_cast<const int4*>(ridx + min(j, K - 4));
+            v[a][u][0] = w.x, v[a][u][1] = w.y, v[a][u][2] = w.z, v[a][u][3] = w.w;
+          } else {
+            v[a][u][0] = ridx[min(j, K - 1)];
+          }
+        }
+      }
+#pragma unroll
+      for (int a = 0; a < kCsrRowBatch; ++a) {
+        const int lr = lr0 + a;
+        if (lr >= r1) break;  // (uniform over the workgroup)
+        const int64_t limit = (int64_t)(row0 + lr) + q_offset;
+        const int tag = lr;
+        int dk[kP], dp[kP];  // key and position of each pair that completed a sector (else -1)
+#pragma unroll
+        for (int u = 0; u < kPer; ++u)
+#pragma unroll
+          for (int e = 0; e < kW; ++e) {
+            const int j = j0 + kW * (t + kFillThreads * u) + e;
+            const int key = v[a][u][e];
+            dk[kW * u + e] = -1;
+            if (j < K && csr_slot_ok(key, s_kv, limit) && (unsigned)(key - key0) < (unsigned)nkeys) {
+              const int k = key - key0;
+              if (atomicExch(&seen[k], tag) == tag) dup = 1;
+              const int pos = atomicAdd(&cur[k], 1);
+              stg_i[8 * k + (pos & 7)] = lr * K + j;
+              if ((pos & 7) == 7) {
+                dk[kW * u + e] = k;
+                dp[kW * u + e] = pos;
+              }
+            }
+          }
+        __syncthreads();  // the row's pairs are staged
+        if (dup) {  // (workgroup-uniform) a key twice in one row: the unstaged fill takes over
+          if (t == 0) *dup_flag = 1;
+          return;
+        }
+#pragma unroll
+        for (int i = 0; i < kP; ++i) {
+          const int k = dk[i];
+          if (k < 0) continue;
+          const int base = dp[i] - 7;
+          if (base >= first[k]) {
+            int4* dst = reinterpret_cast<int4*>(pairs + base);
+            dst[0] = stg[k][0];
+            dst[1] = stg[k][1];
+          } else {
+            for (int q = first[k]; q <= dp[i]; ++q) pairs[q] = stg_i[8 * k + (q & 7)];
+          }
+        }
+        __syncthreads();  // the written sectors' slots may be restaged by the next row
+      }
+    }
+  }
+  // each key's open sector: its positions [max(first, end & ~7), end)
+  for (int k = t; k < nkeys; k += kFillThreads) {
+    const int e = cur[k];
+    if ((e & 7) == 0) continue;
+    for (int q = max(first[k], e & ~7); q < e; ++q) pairs[q] = stg_i[8 * k + (q & 7)];
+  }
+}
+
 template <bool kFill>
 void launch_csr_count(bool vec, unsigned grid, size_t lds, hipStream_t st, const int32_t* idx, int* table,
                       const int* chunk_off, const int* row_ptr, int* pairs, int S, int s_kv, int K, int64_t q_offset,
-                      int row0, int rows, int b, int n_ranges, int rows_per_wg) {
-  const TimedLaunch tl(kFill ? "csr_count_kernel<fill>" : "csr_count_kernel<count>", st);
+                      int row0, int rows, int b, int n_ranges, int rows_per_wg, int* dup_flag) {
+  const TimedLaunch tl(kFill ? (dup_flag ? "csr_count_kernel<fill, repair>" : "csr_count_kernel<fill>")
+                             : "csr_count_kernel<count>",
+                       st);
   if (vec)
     csr_count_kernel<kFill, true><<<grid, 256, lds, st>>>(idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
-                                                          q_offset, row0, rows, b, n_ranges, rows_per_wg);
+                                                          q_offset, row0, rows, b, n_ranges, rows_per_wg, dup_flag);
   else
     csr_count_kernel<kFill, false><<<grid, 256, lds, st>>>(idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
-                                                           q_offset, row0, rows, b, n_ranges, rows_per_wg);
+                                                           q_offset, row0, rows, b, n_ranges, rows_per_wg, dup_flag);
 }
 
 // Column scan of the count table, first level: within each chunk of kColChunk row blocks,
@@ -399,7 +540,7 @@ inline int64_t csr_ws_ints(int64_t s_kv, int64_t rows, int64_t K) {
   const int64_t n_rb = (rows + csr_rows_per_wg(s_kv, K) - 1) / csr_rows_per_wg(s_kv, K);
   const int64_t n_chunks = (n_rb + kColChunk - 1) / kColChunk;
   const int64_t n_seg = (rows * K + kSegPairs - 1) / kSegPairs;
-  return (2 * (s_kv + 1) + n_seg + (n_rb + n_chunks) * s_kv + 3) / 4 * 4;
+  return (2 * (s_kv + 1) + n_seg + (n_rb + n_chunks) * s_kv + 3) / 4 * 4 + 4;  // (+4: the fill's dup flag last)
 }
 inline int64_t csr_part_bytes(int64_t rows, int64_t K, int64_t width) {
   return (rows * K + kSegPairs - 1) / kSegPairs * 2 * width * 4;
@@ -435,8 +576,11 @@ inline int csr_build(const int32_t* idx, int* pairs, int* csr_ws, int S, int s_k
     return set_error(DSA_ERR_INVALID_ARG, "csr_reduce: too many rows x keys");
   const int64_t row_base = (int64_t)b * S + row0;  // int4 loads need 16-byte aligned index rows
   const bool vec = K % 4 == 0 && ((uintptr_t)(idx + row_base * K) % 16) == 0;
+  const int n_franges = (int)ceil_div(s_kv, kFillKeys);
+  const bool staged = n_franges <= kFillRangesMax;
+  int* dup_flag = staged ? csr_ws + csr_ws_ints(s_kv, rows, K) - 1 : nullptr;
   launch_csr_count<false>(vec, (unsigned)cgrid, hist_bytes, st, idx, table, nullptr, nullptr, pairs, S, s_kv, K,
-                          q_offset, row0, rows, b, n_ranges, rows_per_wg);
+                          q_offset, row0, rows, b, n_ranges, rows_per_wg, dup_flag);
   {
     const TimedLaunch tl("csr_colscan_kernel", st);
     csr_colscan_kernel<<<dim3((unsigned)ceil_div(s_kv, 256), (unsigned)n_chunks), 256, 0, st>>>(table, chunk_off,
@@ -450,8 +594,26 @@ inline int csr_build(const int32_t* idx, int* pairs, int* csr_ws, int S, int s_k
     const TimedLaunch tl("csr_scan_kernel", st);
     csr_scan_kernel<<<1, 1024, 0, st>>>(counts, row_ptr, nullptr, s_kv);
   }
-  launch_csr_count<true>(vec, (unsigned)cgrid, hist_bytes, st, idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
-                         q_offset, row0, rows, b, n_ranges, rows_per_wg);
+  if (staged) {
+    const unsigned fgrid = (unsigned)(8 * n_franges * ceil_div(ceil_div(n_rb, kFillRB), 8));
+    {
+      const TimedLaunch tl("csr_fill_staged_kernel", st);
+      if (vec)
+        csr_fill_staged_kernel<true><<<fgrid, kFillThreads, 0, st>>>(idx, table, chunk_off, row_ptr, pairs, dup_flag, S,
+                                                                    s_kv, K, q_offset, row0, rows, b, n_franges,
+                                                                    rows_per_wg, (int)n_rb);
+      else
+        csr_fill_staged_kernel<false><<<fgrid, kFillThreads, 0, st>>>(idx, table, chunk_off, row_ptr, pairs, dup_flag,
+                                                                     S, s_kv, K, q_offset, row0, rows, b, n_franges,
+                                                                     rows_per_wg, (int)n_rb);
+    }
+    // (returns at once unless a key repeated inside a row made the staged fill give up)
+    launch_csr_count<true>(vec, (unsigned)cgrid, hist_bytes, st, idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
+                           q_offset, row0, rows, b, n_ranges, rows_per_wg, dup_flag);
+  } else {
+    launch_csr_count<true>(vec, (unsigned)cgrid, hist_bytes, st, idx, table, chunk_off, row_ptr, pairs, S, s_kv, K,
+                           q_offset, row0, rows, b, n_ranges, rows_per_wg, nullptr);
+  }
   {
     const TimedLaunch tl("csr_seg_key_kernel", st);
     csr_seg_key_kernel<<<ceil_div(s_kv, 256), 256, 0, st>>>(row_ptr, seg_key, s_kv);
