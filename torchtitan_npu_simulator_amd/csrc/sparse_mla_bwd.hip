@@ -612,7 +612,7 @@ struct ContribGeom {
   static constexpr int kNT = kD / 16;          // 16-column tiles (36 | 32)
   static constexpr int kFull = kNT - 2 * kCW;  // waves owning three tiles (12 | 8); the rest own two
   static_assert(kFull > 0 && kFull <= kCW, "two or three tiles per wave");
-  static_assert(2 * kGTChunks + 2 * kStChunks >= kXChunks, "X staging reuses the tile space");
+  static_assert(2 * kGTChunks + 2 * kStChunks >= kGTChunks + kXChunks, "X staging reuses the tile space after G tile 0");
   // first tile of wave w
   static __device__ __forceinline__ int tile0(int w) { return w < kFull ? 3 * w : 3 * kFull + 2 * (w - kFull); }
 };
@@ -648,44 +648,6 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   const int t0w = CG::tile0(wave);               // the wave's first 16-column tile
   const bool three = CG::kFull == kCW || wave < CG::kFull;  // (wave-uniform) it owns three tiles
 
-  // ---- X^T slice into VGPRs: xa[t][ks] = X[32 ks + 8g .. +8][16 (t0w + t) + col] ----
-  // (rows of dO at the rope columns are zero, so every MFMA below runs unconditionally)
-  u32x4 xa[3][kKSteps];
-  const int tr_row = 8 * g + (col >> 2);  // source row within a 32-row k step (+4 second read)
-#pragma unroll
-  for (int kc = 0; kc < 2 * kHGroups; ++kc) {
-    __syncthreads();
-    const int hgk = kc >> 1, type = kc & 1;
-    for (int i = tid; i < kXChunks; i += kCThreads) {
-      const int row = i / kRC, c = i - row * kRC;
-      const int head = hgk * kHG + row;
-      u32x4 v = (u32x4){0u, 0u, 0u, 0u};
-      if (head < H) {
-        if (type == 0) v = *reinterpret_cast<const u32x4*>(q + (row_id * H + head) * kD + c * 8);
-        else if (c < kDv / 8) v = *reinterpret_cast<const u32x4*>(dout + (row_id * H + head) * kDv + c * 8);
-      }
-      lds[row * kRC + (c ^ swz8(row))] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kl = 0; kl < 2; ++kl) {  // two 32-row k steps per staged chunk
-      const int ks = 2 * kc + kl;
-      const int r1 = 32 * kl + tr_row, r2 = r1 + 4;
-#pragma unroll
-      for (int t = 0; t < 3; ++t) {
-        const int c0 = 2 * min(t0w + t, CG::kNT - 1) + ((col & 3) >> 1);  // (a two-tile wave's third: unused)
-        const lds_char* a1 = lb + 16 * (r1 * kRC + (c0 ^ swz8(r1))) + 8 * (col & 1);
-        const lds_char* a2 = lb + 16 * (r2 * kRC + (c0 ^ swz8(r2))) + 8 * (col & 1);
-        xa[t][ks] = lds_read_tr_pair(a1, a2);
-      }
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < 3; ++t)
-#pragma unroll
-    for (int ks = 0; ks < kKSteps; ++ks) asm volatile("" : "+v"(xa[t][ks]));  // landed before the DMAs
-  __syncthreads();
-
   // ---- stream G tiles; per 32-slot step C^T[16 cols x 16 slots] = X^T . G^T on six tiles ----
   // G tile DMA: instruction J = wave + 12 i covers tile chunks [64J, 64J+64), chunk
   // p = slot*32 + (c ^ swz16(slot))
@@ -712,6 +674,66 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
     }
   };
   load_g(0, 0);
+
+  // ---- X^T slice into VGPRs: xa[t][ks] = X[32 ks + 8g .. +8][16 (t0w + t) + col] ----
+  // (rows of dO at the rope columns are zero, so every MFMA below runs unconditionally)
+  // G tile 0 is requested first: its DMA lands in tile buffer 0 while X is staged through
+  // the LDS after it.  X is staged in 2 * kHGroups chunks of 64 rows; every chunk's loads
+  // are issued before the first is staged, so the chunks cost one memory round trip, not
+  // one each.
+  u32x4 xa[3][kKSteps];
+  const int tr_row = 8 * g + (col >> 2);  // source row within a 32-row k step (+4 second read)
+  constexpr int kXPer = (kXChunks + kCThreads - 1) / kCThreads;  // staged chunks per thread and X chunk
+  u32x4 xraw[2 * kHGroups][kXPer];
+#pragma unroll
+  for (int kc = 0; kc < 2 * kHGroups; ++kc) {
+    const int hgk = kc >> 1, type = kc & 1;
+#pragma unroll
+    for (int m = 0; m < kXPer; ++m) {
+      // (no load under a lane-dependent branch, which would make the compiler wait for each
+      // load before the next: addresses are clamped into the tensors and the chunks outside
+      // them zeroed after the load)
+      const int i = tid + kCThreads * m;
+      const int ic = min(i, kXChunks - 1);
+      const int row = ic / kRC, c = ic - row * kRC;
+      const int head = hgk * kHG + row;
+      const int64_t hrow = row_id * H + min(head, H - 1);
+      const u32x4 v = type == 0 ? *reinterpret_cast<const u32x4*>(q + hrow * kD + c * 8)
+                                : *reinterpret_cast<const u32x4*>(dout + hrow * kDv + min(c, kDv / 8 - 1) * 8);
+      const bool ok = i < kXChunks && head < H && (type == 0 || c < kDv / 8);
+      xraw[kc][m] = ok ? v : (u32x4){0u, 0u, 0u, 0u};
+    }
+  }
+  u32x4* const xst = &lds[kGTChunks];  // X staging: after G tile 0
+#pragma unroll
+  for (int kc = 0; kc < 2 * kHGroups; ++kc) {
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < kXPer; ++m) {
+      const int i = tid + kCThreads * m;
+      const int row = i / kRC, c = i - row * kRC;
+      if (i < kXChunks) xst[row * kRC + (c ^ swz8(row))] = xraw[kc][m];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kl = 0; kl < 2; ++kl) {  // two 32-row k steps per staged chunk
+      const int ks = 2 * kc + kl;
+      const int r1 = 32 * kl + tr_row, r2 = r1 + 4;
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        const int c0 = 2 * min(t0w + t, CG::kNT - 1) + ((col & 3) >> 1);  // (a two-tile wave's third: unused)
+        const lds_char* a1 = lb + 16 * (kGTChunks + r1 * kRC + (c0 ^ swz8(r1))) + 8 * (col & 1);
+        const lds_char* a2 = lb + 16 * (kGTChunks + r2 * kRC + (c0 ^ swz8(r2))) + 8 * (col & 1);
+        xa[t][ks] = lds_read_tr_pair(a1, a2);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+#pragma unroll
+    for (int ks = 0; ks < kKSteps; ++ks) asm volatile("" : "+v"(xa[t][ks]));  // landed before the DMAs
+  __syncthreads();
+
   // C-row store instructions a wave issues per step: one per 768-chunk slice of the stage
   // that holds any of its chunks (576 columns: 3 for every wave; 512: 3 for waves 0..7, 2
   // for waves 8..11)
