@@ -213,14 +213,26 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   constexpr int kPer = kMaxK / 256;
   float mv[kPer], xv[kPer];
   bool okv[kPer];
+  // (the loads are unconditional, at slots clamped into the row, and their results selected
+  // afterwards: under a lane-dependent branch the compiler waits for each load before the
+  // next, one memory round trip per 256 slots)
+  int vi[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {  // (groups past K re-read slot K - 1: cache hits, unused)
+    const int jc = min(tid + 256 * u, K - 1);
+    vi[u] = ridx[jc];
+    mv[u] = mrow[jc];
+  }
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
     const int j = tid + 256 * u;
     okv[u] = false;
-    mv[u] = xv[u] = 0.f;
+    xv[u] = 0.f;
     if (256 * u < K) {
-      okv[u] = j < K && ok_slot(ridx[min(j, K - 1)], s_k, limit);
-      mv[u] = j < K ? mrow[j] : 0.f;
+      okv[u] = j < K && ok_slot(vi[u], s_k, limit);
+      mv[u] = j < K ? mv[u] : 0.f;
+    } else {
+      mv[u] = 0.f;
     }
   }
   float lmax = -INFINITY, zsum = 0.f;

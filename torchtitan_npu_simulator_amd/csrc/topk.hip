@@ -115,6 +115,9 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   // order keys of the thread's scores; positions past the valid prefix and NaN scores are
   // key 0 (not candidates)
   uint32_t key[kR][4];
+  // (candidate lists: each candidate's position in the row, read with its key so that the
+  // output pass issues no load under its per-lane branches)
+  uint32_t cpos[kMode == 1 ? kR : 1][4];
   // Every load of a segment is issued before any key is formed and no load sits under a
   // lane-dependent branch, so a wave has all of them in flight at once (a branch per lane
   // would make the compiler wait for each load before the next); chunks past the valid
@@ -130,7 +133,11 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
         const int base = sg * kSeg + 4 * (t + kThreads * j);
         if (live(sg, j)) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) key[j][e] = crow[min(base + e, last)].x;
+          for (int e = 0; e < 4; ++e) {
+            const uint2 cv = crow[min(base + e, last)];
+            key[j][e] = cv.x;
+            cpos[j][e] = cv.y;
+          }
         }
       }
 #pragma unroll
@@ -379,7 +386,8 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
           const bool take = g || (q && be < need_eq);
           const uint32_t pos = bg + (kTies ? min(be, need_eq) : 0u);
           if (take && pos < (uint32_t)k) {  // (always < k: the threshold admits at most k)
-            const int at = kMode == 1 ? (int)crow[base + e].y : base + e;  // position in the row
+            int at = base + e;  // position in the row
+            if constexpr (kMode == 1) at = (int)cpos[j][e];
             oi[pos] = (int32_t)(at + index_offset);
             if (ov) ov[pos] = src[at];  // (the score as given: -0.0 keeps its sign)
           }
