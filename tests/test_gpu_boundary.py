@@ -259,3 +259,61 @@ def test_kl_loss_band_and_bsnd_lengths():
         assert float(got[0][b, n:].abs().sum()) == 0.0 and float(got[1][b, n:].abs().sum()) == 0.0
         loss += float(one[3])
     assert abs(float(got[3]) - loss) <= 1e-5 * abs(loss)
+
+
+def test_kl_op_takes_the_attention_backward_mass(monkeypatch):
+    """The op-level route as the reference's dsa.py calls it (converters/kernels/dsa.py:238-253,
+    then :159-177): npu_sparse_flash_attention on q_nope / q_pe and k_nope / k_pe split views,
+    its backward, then npu_sparse_lightning_indexer_grad_kl_loss on the same (detached)
+    pieces, indices and statistics.  The backward's mass reaches the KL op (dsa_attn_mass is
+    not called), the results equal a recomputed target's bit for bit, the entry is used
+    once, and an in-place change of the statistics makes the op recompute."""
+    from torchtitan_npu_simulator_amd import torch_npu_ops as ops
+
+    S, H, K, HI, DI = 192, 16, 32, 64, 128
+    q, kv, dout, scale = attn_inputs(S, H, seed=7)
+    g = torch.Generator().manual_seed(8)
+    qi = torch.randn(1, S, HI, DI, generator=g).bfloat16().to(DEV)
+    ki = torch.randn(1, S, 1, DI, generator=g).bfloat16().to(DEV)
+    w = (torch.rand(1, S, HI, generator=g) * HI ** -0.5 * DI ** -0.5).to(DEV)
+    q = q.to(DEV).requires_grad_()
+    k = kv.to(DEV).unsqueeze(2).requires_grad_()  # [1,S,1,576]
+    idx = rand_indices(S, K, seed=9).to(DEV).unsqueeze(2)  # [1,S,1,K]
+    q_nope, q_pe = torch.split(q, [512, 64], dim=-1)
+    k_nope, k_pe = torch.split(k, [512, 64], dim=-1)
+    out, smax, ssum = ops.npu_sparse_flash_attention(q_nope, k_nope, k_nope, idx, query_rope=q_pe, key_rope=k_pe,
+                                                     scale_value=scale)
+    (out.float() * dout.to(DEV).float()).sum().backward()
+    args = (q_nope.detach(), k_nope.detach(), qi, ki, w, idx, smax, ssum, scale)
+    kw = dict(query_rope=q_pe.detach(), key_rope=k_pe.detach())
+    assert ops._attn_mass_entry is not None
+
+    def no_recompute(*a, **k_):
+        raise AssertionError("the KL op recomputed a mass the backward had left for it")
+
+    real_attn_mass = ops.attn_mass
+    monkeypatch.setattr(ops, "attn_mass", no_recompute)
+    taken = ops.npu_sparse_lightning_indexer_grad_kl_loss(*args, **kw)
+    assert ops._attn_mass_entry is None
+    monkeypatch.setattr(ops, "attn_mass", real_attn_mass)
+    recomputed = ops.npu_sparse_lightning_indexer_grad_kl_loss(*args, **kw)
+    for a_, b_ in zip(taken, recomputed):
+        assert torch.equal(a_, b_)
+    assert float(taken[3]) > 0.0
+
+    # a statistics tensor changed in place after the backward: the kept mass is not used
+    out2, smax2, ssum2 = ops.npu_sparse_flash_attention(q_nope, k_nope, k_nope, idx, query_rope=q_pe,
+                                                        key_rope=k_pe, scale_value=scale)
+    (out2.float() * dout.to(DEV).float()).sum().backward()
+    assert ops._attn_mass_entry is not None
+    ssum2.mul_(2.0)
+    calls = []
+
+    def counting(*a, **k_):
+        calls.append(1)
+        return real_attn_mass(*a, **k_)
+
+    monkeypatch.setattr(ops, "attn_mass", counting)
+    ops.npu_sparse_lightning_indexer_grad_kl_loss(q_nope.detach(), k_nope.detach(), qi, ki, w, idx, smax2, ssum2,
+                                                  scale, **kw)
+    assert calls == [1]

@@ -459,6 +459,8 @@ def sparse_mla_fwd(q, kv, indices, scale, *, d_v=512, q_offset=0, sinks=None):
     ``sinks`` [H] (DeepSeek-V4's per-head attention sink) selects dsa_sparse_mla_fwd_sink: the
     sink joins every row's softmax with no value, and the statistics returned include it.
     """
+    global _attn_mass_entry
+    _attn_mass_entry = None  # a mass kept by the last backward (take_attn_mass) is not for this call
     lib = load_library()
     require_gpu_tensor(q, "q")
     B, S, H, D = q.shape
@@ -523,6 +525,37 @@ def pair_csr(indices, s_k, q_offset=0):
     return csr
 
 
+_attn_mass_entry = None  # (key, the tensors the mass came from, mass [B,S,K] fp32)
+_share_attn_mass = True  # False: the indexer KL op always recomputes its target mass
+
+
+def _attn_mass_key(q, kv, indices, smax, ssum, scale, q_offset):
+    # address, version (shared by every view of a storage), shape, strides and dtype of each
+    # input, so a different view, a copy or an in-place change of any of them misses
+    return tuple((t.data_ptr(), t._version, tuple(t.shape), tuple(t.stride()), t.dtype)
+                 for t in (q, kv, indices, smax, ssum)) + (q.device, float(scale), int(q_offset))
+
+
+def take_attn_mass(q, kv, indices, smax, ssum, scale, q_offset=0):
+    """The head-summed attention mass that the last op-level attention backward left for
+    exactly these inputs (same tensors, unchanged since), or None; the entry is used once.
+
+    ``npu_sparse_flash_attention``'s backward forms P for every (row, head, slot) anyway, so
+    it keeps the mass (``bwd_sdp_kernel`` writes it; bitwise equal to ``dsa_attn_mass`` on
+    the same inputs) for the indexer KL op that a torch_npu-style layer calls next with the
+    same query, key, indices and softmax statistics (reference converters/kernels/dsa.py:
+    159-177 after :238-253).  The entry holds the index and statistics tensors it was made
+    for (so their addresses cannot be reused while it lives; softmax statistics belong to
+    one query / key pair) but not the query and key, and it is dropped by the next attention
+    forward or replaced by the next backward."""
+    global _attn_mass_entry
+    e = _attn_mass_entry
+    if e is None or e[0] != _attn_mass_key(q, kv, indices, smax, ssum, scale, q_offset):
+        return None
+    _attn_mass_entry = None
+    return e[2]
+
+
 def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, workspace_bytes=None,
                    return_mass=False, sinks=None):
     """(dq like q, dkv fp32 [B,S_kv,D_qk]) from dsa_sparse_mla_bwd, plus the head-summed
@@ -533,16 +566,24 @@ def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, 
 
     ``workspace_bytes`` caps the scratch (fewer bytes -> more query-row chunks).
     """
+    global _attn_mass_entry
     lib = load_library()
     B, S, H, D = q.shape
     s_kv = kv.shape[1]
     K = indices.shape[-1]
     d_v = out.shape[-1]
-    q, kv, out, dout = (t.contiguous() for t in (q, kv, out, dout))
     indices = indices.reshape(B, S, K).to(torch.int32).contiguous()
+    # without return_mass the bf16 path still writes the mass (a few % of the score kernel)
+    # and keeps it for the indexer KL op of the same layer (take_attn_mass)
+    keep = _share_attn_mass and not return_mass and sinks is None and q.dtype == torch.bfloat16
+    if keep:
+        _attn_mass_entry = None  # (the old mass goes before the new one is allocated)
+        keep_key = _attn_mass_key(q, kv, indices, smax, ssum, scale, q_offset)
+        keep_refs = (indices, smax, ssum)
+    q, kv, out, dout = (t.contiguous() for t in (q, kv, out, dout))
     dq = torch.empty_like(q)
     dkv = torch.zeros(B, s_kv, D, dtype=torch.float32, device=q.device)
-    mass = torch.empty(B, S, K, dtype=torch.float32, device=q.device) if return_mass else None
+    mass = torch.empty(B, S, K, dtype=torch.float32, device=q.device) if (return_mass or keep) else None
     ws_bytes = int(lib.dsa_sparse_mla_bwd_workspace_size(B, S, s_kv, H, D, K))
     if workspace_bytes is not None:
         ws_bytes = int(workspace_bytes)
@@ -564,6 +605,8 @@ def sparse_mla_bwd(q, kv, indices, out, dout, smax, ssum, scale, *, q_offset=0, 
                                   S, s_kv, H, D, d_v, K, float(scale), int(q_offset), stream_of(q.device)),
         "dsa_sparse_mla_bwd",
     )
+    if keep:
+        _attn_mass_entry = (keep_key, keep_refs, mass)
     return res + (dsink,) if sinks is not None else res
 
 
@@ -1524,7 +1567,9 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
         idx = _band_mask_indices(idx, sparse_mode, q_off, pre_tokens, next_tokens).contiguous()
     elif int(cmp_ratio) != 1 and (int(pre_tokens) < s_kv * int(cmp_ratio) or int(next_tokens) < 0):
         raise NotImplementedError("a pre_tokens / next_tokens band over compressed keys (cmp_ratio > 1)")
-    mass = attn_mass(q, kv3, idx, softmax_max, softmax_sum, scale_value, q_offset=q_off)
+    mass = take_attn_mass(q, kv3, idx, softmax_max, softmax_sum, scale_value, q_off)
+    if mass is None:
+        mass = attn_mass(q, kv3, idx, softmax_max, softmax_sum, scale_value, q_offset=q_off)
     dq_i, dk_i, dw, loss_rows = indexer_kl_grad_from_mass(query_index, key_index, weight, idx, mass, q_offset=q_off,
                                                           loss_scale=loss_scale, eps=eps, grad_scale=grad_scale)
     return (dq_i.to(out_dtypes[0]), dk_i.reshape(key_index.shape).to(out_dtypes[1]), dw.to(out_dtypes[2]),
