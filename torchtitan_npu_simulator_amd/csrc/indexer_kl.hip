@@ -86,9 +86,15 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
   if (tid == 0) sh_last = -1;
   __syncthreads();
   {
+    // (every index load issued before the first test: a loop of load-then-test waits for
+    // each load in turn; slots past K re-read slot K - 1 and are not counted)
+    int vs[kMaxK / 256];
+#pragma unroll
+    for (int u = 0; u < kMaxK / 256; ++u) vs[u] = ridx[min(tid + 256 * u, K - 1)];
     int last = -1;
-    for (int j = tid; j < K; j += 256)
-      if (ok_slot(ridx[j], s_k, limit)) last = j;
+#pragma unroll
+    for (int u = 0; u < kMaxK / 256; ++u)
+      if (tid + 256 * u < K && ok_slot(vs[u], s_k, limit)) last = tid + 256 * u;
     if (last >= 0) atomicMax(&sh_last, last);
   }
   __syncthreads();
@@ -371,9 +377,18 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     // the whole phase and is read transposed per block (source lane col supplies head row
     // 32 ks + 8g + col/4 (+4 second read), d columns 16 dt + 4 (col % 4)), which keeps 64
     // registers free for the S tiles' operand reads
-    for (int i = tid; i < kH * kRowC; i += 256) {
-      const int h = i >> 4, c = i & 15;
-      qs[h * kRowC + (c ^ swz_kl(h))] = *reinterpret_cast<const u32x4*>(qi + (row_id * kH + h) * kD + 8 * c);
+    {  // (all four loads in flight before the first store)
+      u32x4 qv[kH * kRowC / 256];
+#pragma unroll
+      for (int u = 0; u < kH * kRowC / 256; ++u) {
+        const int i = tid + 256 * u, h = i >> 4, c = i & 15;
+        qv[u] = *reinterpret_cast<const u32x4*>(qi + (row_id * kH + h) * kD + 8 * c);
+      }
+#pragma unroll
+      for (int u = 0; u < kH * kRowC / 256; ++u) {
+        const int i = tid + 256 * u, h = i >> 4, c = i & 15;
+        qs[h * kRowC + (c ^ swz_kl(h))] = qv[u];
+      }
     }
     const lds_char* qsb = lds_bytes(&qs[0]);
     auto read_qtr = [&](int dt, int ks) {
