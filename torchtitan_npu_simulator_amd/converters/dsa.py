@@ -13,7 +13,8 @@ same deferred loss whose backward takes the main-attention mass from the layer's
 backward (fused into dsa_sparse_mla_bwd) instead of recomputing it from the softmax
 statistics: the loss node's zero output is an input of the attention op, so autograd runs
 the attention backward first.  Called on its own, the module keeps the reference's
-interface and recomputes the mass.
+interface and takes the mass through the KL op (kept by the op-level attention backward
+for the same tensors, or recomputed).
 * ``NpuDSAConverter`` / ``DSAModelConfig`` registered as ``"npu_dsa"`` (dsa.py:283-309).
 """
 

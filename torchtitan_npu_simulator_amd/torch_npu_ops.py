@@ -1517,8 +1517,10 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
     gradients in the dtypes of query_index / key_index / weight as the binding allocates them
     (sparse_lightning_indexer_grad_kl_loss/binding.cpp:26-29).
 
-    The main-attention target mass is recomputed from (query || query_rope, key ||
-    key_rope, softmax_max, softmax_sum) at the selected keys; ``loss`` is the token SUM
+    The main-attention target mass at the selected keys is the one the op-level attention
+    backward left for exactly these query / key, indices and statistics (take_attn_mass),
+    or else recomputed from (query || query_rope, key || key_rope, softmax_max,
+    softmax_sum) - bitwise the same mass either way; ``loss`` is the token SUM
     (the caller divides by B*S, reference dsa.py:73).  ``cmp_ratio`` > 1: key / key_index
     are compressed rows (binding.cpp:17) and sparse_indices come from the indexer's
     compressed rule t < (s+1)//r, so the -1 slots carry the validity and no causal test is
