@@ -739,18 +739,39 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   // for waves 8..11)
   constexpr int kStSlices = (kStChunks + kCThreads - 1) / kCThreads;
   const bool last_slice = kStChunks % kCThreads == 0 || wave * 64 < kStChunks % kCThreads;
+  // the C rows of step n leave the stage during step n+1's MFMAs (one slice of row stores
+  // per two k-steps), so the stores overlap matrix work instead of following a barrier
+  auto store_rows = [&](int m, int ps0, int pstep) __attribute__((always_inline)) {
+    const lds_char* pst = stage + (pstep & 1) * (kStChunks * 16);
+    int t_ = tid;
+    asm volatile("" : "+v"(t_));
+    const int i = t_ + kCThreads * m;
+    const int r = i / kRC, c = i - r * kRC;
+    if ((kStChunks % kCThreads == 0 || i < kStChunks) && ps0 + r < nslots) {
+      const u32x4 v = lds_read16(pst + r * (kRC * 16) + 16 * (c ^ stage_swz(r)));
+      // non-temporal: the rows are read back once, by the key-major reduction (with the
+      // reduction's non-temporal loads this makes that pass ≈4 % faster and this one ≈0.7 %
+      // slower)
+      __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(crow + (int64_t)(ps0 + r) * kD + 8 * c));
+    }
+  };
   int step = 0;
+  int prev_s0 = -1;  // first slot of the step whose rows wait in the stage (-1: none)
   for (int tl = 0; tl < ntiles; ++tl) {
     const int buf = tl & 1;
-    // this wave's part of tile tl landed.  Its DMA was issued before the C-row stores of
-    // tile tl-1's two steps (every row of a tile before the last exists, so every store
-    // instruction of those steps issues); vector memory operations retire in issue order,
-    // so waiting until only those stores are outstanding covers the DMA and leaves the
-    // stores in flight
+    // this wave's part of tile tl landed.  Its DMA was issued before the C-row stores
+    // that tile tl-1's two steps issue: those of the step before tile tl-1 and of tile
+    // tl-1's first step (none for tile 0's first step).  Every row of a tile before the
+    // last exists, so every store instruction of those steps issues; vector memory
+    // operations retire in issue order, so waiting until only those stores are outstanding
+    // covers the DMA and leaves the stores in flight
+    static_assert(kStSlices == 3, "the counted waits below assume three stage slices");
     if (tl == 0) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else if (tl == 1) {  // (only step 0's rows have gone out since: tile 0's second step)
+      if (last_slice) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     } else if (last_slice) {
-      static_assert(kStSlices == 3, "the counted waits below assume three stage slices");
       asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
@@ -798,6 +819,11 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
           for (int h2 = 0; h2 < 2; ++h2)
             acc[h2][2] = mfma16x16x32(as_bf16x8(xa[2][ks]), as_bf16x8(bg[ks & 1][h2]), acc[h2][2]);
         }
+        if (prev_s0 >= 0) {  // slice m after k-step 2m + 1 (with four k-steps: the last two after the last)
+#pragma unroll
+          for (int m = 0; m < kStSlices; ++m)
+            if (ks == min(2 * m + 1, kKSteps - 1)) store_rows(m, prev_s0, step - 1);
+        }
       }
       // lane (slot 16 h2 + col, g) holds columns 16 (t0w + t) + 4g + r: 8 bytes at chunk
       // 2 (t0w + t) + g/2, half g & 1 of the stage row
@@ -815,22 +841,13 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
         }
       }
       __syncthreads();  // the step's C rows are complete in the stage
-      // whole rows out: thread chunk i -> row i / kRC, chunk i % kRC
-      int t_ = tid;
-      asm volatile("" : "+v"(t_));
-#pragma unroll
-      for (int m = 0; m < (kStChunks + kCThreads - 1) / kCThreads; ++m) {
-        const int i = t_ + kCThreads * m;
-        const int r = i / kRC, c = i - r * kRC;
-        if ((kStChunks % kCThreads == 0 || i < kStChunks) && s0 + r < nslots) {
-          const u32x4 v = lds_read16(stg + r * (kRC * 16) + 16 * (c ^ stage_swz(r)));
-          // non-temporal: the rows are read back once, by the key-major reduction (with the
-          // reduction's non-temporal loads this makes that pass ≈4 % faster and this one ≈0.7 %
-          // slower)
-          __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(crow + (int64_t)(s0 + r) * kD + 8 * c));
-        }
-      }
+      prev_s0 = s0;
     }
+  }
+  // the last step's rows
+  if (prev_s0 >= 0) {
+#pragma unroll
+    for (int m = 0; m < kStSlices; ++m) store_rows(m, prev_s0, step - 1);
   }
 }
 
