@@ -400,8 +400,16 @@ indexer_kl_mfma_kernel(const uint16_t* __restrict__ qi, const uint16_t* __restri
     start_pass();  // (its barrier also publishes qs)
     for (int blk = 0; blk < nblocks; ++blk) {
       const int buf = blk & 1;
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();  // tile[buf] and ring entry blk+1 landed; es / eh free
+      // tile[buf] and ring entry blk+1 landed.  Their DMAs were issued before the previous
+      // block's four dk row stores (every slot of a block before the last exists, so all
+      // four issue); vector memory operations retire in issue order, so waiting until only
+      // those stores are outstanding covers the DMAs and leaves the stores in flight
+      if (blk == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      }
+      __syncthreads();  // es / eh free
       if (blk + 1 < nblocks) gather(blk + 1, buf ^ 1);
       if (blk + 2 < nblocks) load_idx(blk + 2);
       const uint32_t tb = kt_base + buf * (kTileC * 16);
