@@ -631,7 +631,7 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   __shared__ u32x4 lds[2 * kGTChunks + 2 * kStChunks];  // X staging at start; then G tiles + C stages
   __shared__ int sh_last;
 
-  const int lr = blockIdx.x;  // local row in chunk
+  const int lr = launch_row();  // local row in chunk
   const int tok = row0 + lr, b = blockIdx.y;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
