@@ -359,7 +359,7 @@ def measured_traffic(kernel, S, H, K):
     return k["fetch_bytes"] + k["write_bytes"]
 
 
-def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=576, k_attn=None):
+def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=576, k_attn=None, sink=False):
     """Algorithmic work of one launch-set per step of every kernel in the DSA step, keyed by
     the name the library's kernel timing reports (dsa_kernel_timing).
 
@@ -367,7 +367,9 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=5
     ``pairs`` = causal (query, key) pairs the indexer scores, s_kv attention keys, s_ki
     indexer keys (default s_kv), d_qk the attention row width (576: latent + rope; 512: the
     rope-less DeepSeek-V4 rows, whose kernels report a ``<512>`` name), k_attn the attention
-    slots per row (default K; V4: the 128-token window + K).  Returns name -> (bound, bytes,
+    slots per row (default K; V4: the 128-token window + K), ``sink`` whether the attention
+    has a per-head sink (then a separate pass forms delta = rowsum(dO o O) for the score
+    kernel; without one the score kernel reads O itself).  Returns name -> (bound, bytes,
     flops, intermediate_bytes):
 
     * ``bytes``: the operands of the op contract that the kernel must move once, counted as
@@ -400,9 +402,10 @@ def step_kernel_work(S, H, K, P, pairs, s_kv, s_ki=None, h_i=64, d_i=128, d_qk=5
         "sparse_mla_fwd_exact_kernel<fixup>": ("hbm", 4 * H * S, 0, 0),
         # O, dO | delta written
         "bwd_delta_kernel": ("hbm", 2 * (2 * H * dv * S), 0, 4 * H * S),
-        # Q, dO, gathered rows, indices, row statistics | G written, mass written, delta read
-        "bwd_sdp_kernel": ("hbm", 2 * H * dq * S + 2 * H * dv * S + 2 * dq * P + 4 * Ka * S + 8 * H * S,
-                           2 * H * (dq + dv) * P, 2 * gw * P + 4 * Ka * S + 4 * H * S),
+        # Q, dO, O (delta formed here when there is no sink), gathered rows, indices, row
+        # statistics | G written, mass written, delta read (with a sink)
+        "bwd_sdp_kernel": ("hbm", 2 * H * dq * S + 2 * H * dv * S * (1 if sink else 2) + 2 * dq * P + 4 * Ka * S
+                           + 8 * H * S, 2 * H * (dq + dv) * P, 2 * gw * P + 4 * Ka * S + (4 * H * S if sink else 0)),
         # gathered rows, indices, dQ written | dS half of G read
         "bwd_dqk_kernel": ("hbm", 2 * dq * P + 4 * Ka * S + 2 * H * dq * S, 2 * H * dq * P, 2 * (gw // 2) * P),
         # X = [Q; dO], indices, contribution rows written (half the scatter payload) | G read
@@ -727,7 +730,8 @@ def main():
     fwd_ms = phases["attn_fwd"]
     bwd_ms = phases["attn_bwd"]
     if wl == "v4":
-        kwork = step_kernel_work(S, H, K, work["sum_keff"], pairs, S + S // 4, S // 4, d_qk=512, k_attn=K + 128)
+        kwork = step_kernel_work(S, H, K, work["sum_keff"], pairs, S + S // 4, S // 4, d_qk=512, k_attn=K + 128,
+                                 sink=True)
     else:
         s_kv = S // 4 if wl == "c4" else S
         kwork = step_kernel_work(S, H, K, work["sum_keff"], pairs if pairs is not None else S * (S + 1) // 2, s_kv,

@@ -93,7 +93,13 @@ def test_backward_bytes_split_into_contract_and_intermediate():
     S, H, K, P, pairs = 8192, 128, 2048, 14_681_088, 8192 * 8193 // 2
     w = bench.step_kernel_work(S, H, K, P, pairs, S)
     G = 2 * 256 * P  # bf16 dS and P of 128 heads per (row, slot)
-    assert w["bwd_sdp_kernel"][3] == G + 4 * K * S + 4 * H * S
+    # with no sink the score kernel forms delta from O itself: O is its contract read, no
+    # delta buffer; with a sink the delta pass reads O and dO and the score kernel the delta
+    assert w["bwd_sdp_kernel"][3] == G + 4 * K * S
+    assert w["bwd_sdp_kernel"][1] == 2 * H * 576 * S + 2 * 2 * H * 512 * S + 2 * 576 * P + 4 * K * S + 8 * H * S
+    ws = bench.step_kernel_work(S, H, K, P, pairs, S, sink=True)
+    assert ws["bwd_sdp_kernel"][3] == G + 4 * K * S + 4 * H * S
+    assert ws["bwd_sdp_kernel"][1] + ws["bwd_delta_kernel"][1] == w["bwd_sdp_kernel"][1] + 2 * H * 512 * S
     assert w["bwd_dqk_kernel"][3] == G // 2
     assert w["bwd_contrib_kernel<2>"][3] == G
     assert w["bwd_contrib_kernel<2>"][1] == 2 * H * (576 + 512) * S + 4 * K * S + 2 * 576 * P

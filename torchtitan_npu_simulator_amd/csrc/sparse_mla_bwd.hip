@@ -4,7 +4,9 @@
 // per clock), far too slow for the dKV scatter-add (576 fp32 per (token, key) pair), so
 // the backward reduces dKV through a key-major pass instead:
 //
-//   (delta) bwd_delta_kernel: delta = rowsum(dO o O) per (token, head), one streaming pass.
+//   (delta) delta = rowsum(dO o O) per (token, head): formed by bwd_sdp_kernel from the O
+//           rows it reads beside dO, or, with a per-head sink (whose gradient needs it for
+//           every row), by bwd_delta_kernel in one streaming pass; the same fp32 sum either way.
 //   (alpha) bwd_sdp_kernel, workgroup = token x 128 heads, 8 waves x 16 heads (the
 //           forward's gather pipeline): S^T = K Q^T and dP^T = V dO^T on
 //           v_mfma_f32_16x16x32_bf16 chains sharing every K operand read, P = exp2(S*scale*
@@ -70,12 +72,15 @@ __device__ __forceinline__ int g2_swz(int r) { return (r >> 1) & 7; }
 
 constexpr int kSdpWaves = 8;
 
-template <int kD>  // row width of Q and KV: 576 (latent + rope) or 512 (no rope)
+// kD: row width of Q and KV, 576 (latent + rope) or 512 (no rope).  kOwnDelta: delta =
+// rowsum(dO o O) of each head is formed here from O (read beside dO, in dO's lane layout,
+// then summed over the head's four lane groups) instead of read from dbuf
+template <int kD, bool kOwnDelta>
 __global__ void __launch_bounds__(64 * kSdpWaves, 1)
 bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
-                const uint16_t* __restrict__ dout, const float* __restrict__ smax, const float* __restrict__ ssum,
-                const float* __restrict__ dbuf, uint16_t* __restrict__ gbuf, float* __restrict__ mass, int S,
-                int s_kv, int H, int K, float scale, int64_t q_offset, int row0) {
+                const uint16_t* __restrict__ dout, const uint16_t* __restrict__ out, const float* __restrict__ smax,
+                const float* __restrict__ ssum, const float* __restrict__ dbuf, uint16_t* __restrict__ gbuf,
+                float* __restrict__ mass, int S, int s_kv, int H, int K, float scale, int64_t q_offset, int row0) {
   constexpr int kW = kSdpWaves;
   using Gather = RowGather<kW, kD, true>;
   using Geo = GatherGeomT<kD>;
@@ -113,6 +118,7 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
   // latent Q and dO of head hl: k-step s holds columns 32s + 8g .. +8; lane group g also
   // loads rope chunks 2g, 2g + 1 for the LDS copy (step kLat + j reads chunk 4j + g)
   u32x4 qb[kLat], db[kLat], qr[2];
+  u32x4 ob[kOwnDelta ? kLat : 1];  // O in dO's layout (kOwnDelta)
   {
     const u32x4* qh = reinterpret_cast<const u32x4*>(q + hrow * kD);
     const u32x4* dh = reinterpret_cast<const u32x4*>(dout + hrow * kDv);
@@ -122,9 +128,15 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
     for (int st = 0; st < kLat; ++st) db[st] = dh[4 * st + g];
 #pragma unroll
     for (int j = 0; j < 2; ++j) qr[j] = kRope ? qh[64 + 2 * g + j] : (u32x4){0u, 0u, 0u, 0u};
+    if constexpr (kOwnDelta) {
+      const u32x4* oh = reinterpret_cast<const u32x4*>(out + hrow * kDv);
+#pragma unroll
+      for (int st = 0; st < kLat; ++st) ob[st] = oh[4 * st + g];
+    }
   }
   const float mx = smax[hrow], sm = ssum[hrow];
-  const float dlt = dbuf[((int64_t)b * gridDim.x + lr) * H + (hok ? hl : 0)];
+  float dlt;
+  if constexpr (!kOwnDelta) dlt = dbuf[((int64_t)b * gridDim.x + lr) * H + (hok ? hl : 0)];
   const int nblk = count_row_blocks(ridx, K, s_kv, limit, vidx, &sh_last);
   if (mrow)  // slots past the last usable block carry no mass
     for (int j = nblk * kBN + tid; j < K; j += 64 * kW) mrow[j] = 0.f;
@@ -147,6 +159,27 @@ bwd_sdp_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kv, 
     }
   }
   const float lse2 = (hok && sm > 0.f) ? (mx + logf(sm)) * kLog2e : INFINITY;  // +inf -> P = 0
+  if constexpr (kOwnDelta) {
+    // The same fp32 sum as bwd_delta_kernel, bit for bit (so results do not depend on which
+    // of the two formed delta): its lane l of a head sums 16-byte chunks l + 16 j (j = 0..3,
+    // in order), which this lane group g holds for l = 4a + g as chunks 4 (a + 4j) + g; its
+    // xor tree over l (8, 4, 2, 1) is a's two bits here, then g's across the lanes 32 and 16
+    // apart (each step adds a value and its partner's, which commutes)
+    static_assert(kLat == 16, "four chunks per lane of the delta pass");
+    float sa[4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          part += bf16_lo(db[a + 4 * j][r]) * bf16_lo(ob[a + 4 * j][r]) +
+                  bf16_hi(db[a + 4 * j][r]) * bf16_hi(ob[a + 4 * j][r]);
+      sa[a] = part;
+    }
+    dlt = xor16_sum(xor32_sum((sa[0] + sa[2]) + (sa[1] + sa[3])));
+  }
   const float delta = hok ? dlt : 0.f;
   const float scale_log2 = scale * kLog2e;
   // landed before any DMA; held in AGPRs, which the MFMAs read directly as B operands
@@ -1059,7 +1092,7 @@ static int sparse_mla_bwd_impl(const void* q, const void* kv, const int32_t* ind
 
   for (int64_t r0 = 0; r0 < s_q; r0 += plan.rows) {
     const int rows = (int)std::min<int64_t>(plan.rows, s_q - r0);
-    {
+    if (sinks) {
       const int64_t groups = batch * rows * n_heads;
       const TimedLaunch tl("bwd_delta_kernel", st);
       bwd_delta_kernel<<<(unsigned)((groups * 16 + 255) / 256), 256, 0, st>>>(
@@ -1075,10 +1108,12 @@ static int sparse_mla_bwd_impl(const void* q, const void* kv, const int32_t* ind
     dim3 ga((unsigned)rows, 1, (unsigned)batch);
     {
       const TimedLaunch tl(rope ? "bwd_sdp_kernel" : "bwd_sdp_kernel<512>", st);
-      auto* kern = rope ? bwd_sdp_kernel<kDqk> : bwd_sdp_kernel<kDv>;
-      kern<<<ga, 64 * kSdpWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout, softmax_max,
-                               softmax_sum, dbuf, gbuf, mass, (int)s_q, (int)s_kv, (int)n_heads, (int)topk, scale,
-                               q_offset, (int)r0);
+      // with no sink, delta is formed inside (the sink's gradient needs the delta pass)
+      auto* kern = sinks ? (rope ? bwd_sdp_kernel<kDqk, false> : bwd_sdp_kernel<kDv, false>)
+                         : (rope ? bwd_sdp_kernel<kDqk, true> : bwd_sdp_kernel<kDv, true>);
+      kern<<<ga, 64 * kSdpWaves, 0, st>>>((const uint16_t*)q, (const uint16_t*)kv, indices, (const uint16_t*)dout,
+                                          (const uint16_t*)out, softmax_max, softmax_sum, dbuf, gbuf, mass, (int)s_q,
+                                          (int)s_kv, (int)n_heads, (int)topk, scale, q_offset, (int)r0);
     }
     if (int rc = check_launch("dsa_sparse_mla_bwd(sdp)")) return rc;
     {
