@@ -428,7 +428,7 @@ dkv_reduce_kernel(const uint16_t* __restrict__ cbuf, const int* __restrict__ row
                   int rows, int K, int b) {
   static_assert(kChunks == 72 || kChunks == 64 || kChunks == 16, "row widths of the attention and indexer reductions");
   constexpr int kWidth = kChunks * 8;
-  constexpr int kGroup = 8;
+  constexpr int kGroup = kChunks == 16 ? 16 : 8;  // pairs per load group (16-chunk rows: four per load)
   const int seg = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int n_pairs = row_ptr[s_kv];
