@@ -91,11 +91,64 @@ quantize_fp8_kernel(const T* __restrict__ x, uint8_t* __restrict__ q, float* __r
   }
 }
 
+// Rows of exactly 8 G elements (one 16-byte chunk per lane, bf16): each lane group takes
+// kRows rows a grid apart and issues all their loads before the first use, so a wave keeps
+// kRows loads in flight and the launch has a quarter of the waves.  Per row the arithmetic
+// is quantize_fp8_kernel's, so the bytes are the same.
+constexpr int kRows = 4;
+__global__ void __launch_bounds__(kThreads)
+quantize_fp8_rows_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q, float* __restrict__ scale,
+                         int64_t rows, int lg) {
+  const int G = 1 << lg, D = 8 << lg;
+  const int64_t g0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> lg;
+  const int64_t ng = ((int64_t)gridDim.x * kThreads) >> lg;
+  const int l = threadIdx.x & (G - 1);
+  uint4 w[kRows];
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const int64_t row = g0 + i * ng;
+    const int64_t r = row < rows ? row : rows - 1;  // (idle groups re-read the last row)
+    w[i] = *reinterpret_cast<const uint4*>(x + r * D + 8 * l);
+  }
+#pragma unroll
+  for (int i = 0; i < kRows; ++i) {
+    const int64_t row = g0 + i * ng;
+    const uint32_t p[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = __uint_as_float(p[e] << 16);
+      v[2 * e + 1] = __uint_as_float(p[e] & 0xffff0000u);
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = max_mag(amax, v[e]);
+    for (int m = G >> 1; m >= 1; m >>= 1) amax = max_mag(amax, __shfl_xor(amax, m, 64));
+    float s = amax / 448.0f;
+    s = s < 1e-12f ? 1e-12f : s;  // (keeps NaN)
+    if (row >= rows) continue;  // (uniform over the lane group)
+    if (l == 0) scale[row] = s;
+    uint32_t b[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[e] = e4m3fn_rne(v[e] / s);
+    const uint2 o = {b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24)};
+    *reinterpret_cast<uint2*>(q + row * D + 8 * l) = o;
+  }
+}
+
 template <typename T>
 void launch_quantize(bool vec, const void* x, uint8_t* q, float* scale, int64_t rows, int D, int lg, hipStream_t st) {
   const int64_t threads = rows << lg;
   const dim3 grid((unsigned)((threads + kThreads - 1) / kThreads));
   const TimedLaunch tl("quantize_fp8_kernel", st);
+  if constexpr (sizeof(T) == 2) {
+    if (vec && D == (8 << lg)) {
+      const int64_t groups = (rows + kRows - 1) / kRows;
+      const dim3 g4((unsigned)(((groups << lg) + kThreads - 1) / kThreads));
+      quantize_fp8_rows_kernel<<<g4, kThreads, 0, st>>>(static_cast<const uint16_t*>(x), q, scale, rows, lg);
+      return;
+    }
+  }
   if (vec)
     quantize_fp8_kernel<T, true><<<grid, kThreads, 0, st>>>(static_cast<const T*>(x), q, scale, rows, D, lg);
   else
