@@ -626,15 +626,15 @@ bwd_dqk_kernel(const uint16_t* __restrict__ kv, const int32_t* __restrict__ idx,
 // 48w .. 48w+47) and at 512 three for waves 0..7, two for waves 8..11 (8 tiles per SIMD
 // either way).  Each wave keeps its slice of X transposed in VGPRs for the whole token (A
 // operand of C^T = X^T G^T, 96 VGPRs).  G is streamed through a double-buffered LDS tile of
-// 64 slots x 256 (DMA), so G, X and C each cross HBM exactly once.  The C rows of each
+// 32 slots x 256 (DMA), so G, X and C each cross HBM exactly once.  The C rows of each
 // 32-slot step are assembled in a double-buffered LDS stage (every wave adds its columns)
 // and leave as whole 1152- (1024-) byte rows, 16 bytes per lane: the MFMA output layout
 // alone would give 8-byte pieces scattered over 16 rows per store instruction.
 // --------------------------------------------------------------------------------------
 constexpr int kCW = 12;                     // waves
 constexpr int kCThreads = kCW * 64;
-constexpr int kCT = 64;                     // slots per G tile
-constexpr int kGTChunks = kCT * (kGW / 8);  // 2048 16-byte chunks (32 KB)
+constexpr int kCT = 32;                     // slots per G tile: one step (64 measured 1 % slower)
+constexpr int kGTChunks = kCT * (kGW / 8);  // 1024 16-byte chunks (16 KB)
 constexpr int kCS = 32;                     // slots per step (C stage rows)
 constexpr int kXK = 64;                     // X rows staged per chunk while loading X
 template <int kD>
@@ -792,22 +792,18 @@ bwd_contrib_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ 
   int prev_s0 = -1;  // first slot of the step whose rows wait in the stage (-1: none)
   for (int tl = 0; tl < ntiles; ++tl) {
     const int buf = tl & 1;
-    // this wave's part of tile tl landed.  Its DMA was issued before the C-row stores
-    // that tile tl-1's two steps issue: those of the step before tile tl-1 and of tile
-    // tl-1's first step (none for tile 0's first step).  Every row of a tile before the
-    // last exists, so every store instruction of those steps issues; vector memory
-    // operations retire in issue order, so waiting until only those stores are outstanding
-    // covers the DMA and leaves the stores in flight
-    static_assert(kStSlices == 3, "the counted waits below assume three stage slices");
-    if (tl == 0) {
+    // this wave's part of tile tl landed.  Its DMA was issued before the C-row stores that
+    // tile tl-1's step issues, those of step tl-2 (none when tl-1 is step 0).  Every row of
+    // a step before the last exists, so every store instruction of that step issues; vector
+    // memory operations retire in issue order, so waiting until only those stores are
+    // outstanding covers the DMA and leaves the stores in flight
+    static_assert(kStSlices == 3 && kCT == kCS, "the counted waits below assume three stage slices, one step per tile");
+    if (tl <= 1) {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    } else if (tl == 1) {  // (only step 0's rows have gone out since: tile 0's second step)
-      if (last_slice) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     } else if (last_slice) {
-      asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
     } else {
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     }
     __syncthreads();  // every wave's part landed; the other G buffer is free
     if (tl + 1 < ntiles) load_g(tl + 1, buf ^ 1);
