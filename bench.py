@@ -50,6 +50,9 @@ def parse_args():
     p.add_argument("--heads", type=int, default=128)
     p.add_argument("--topk", type=int, default=2048)
     p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--varlen-bounds", choices=("host", "device"), default="host",
+                   help="c5: sequence bounds as a host list (one launch per sequence) or a device tensor (one "
+                        "launch per op over the whole batch, no host read)")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="target CPU time of the baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration", action="store_true",
@@ -248,10 +251,15 @@ def c4_step(inp, comp, comp_i, ops, timer):
 
 def c5_step(inp, ops, timer):
     """One layer over a packed varlen batch (config C5 ii) through the ``_varlen`` entry
-    points: each sequence attends causally to its own tokens only."""
-    cu = [0]
-    for n in inp["lens_q"]:
-        cu.append(cu[-1] + n)
+    points: each sequence attends causally to its own tokens only.  The sequence bounds are a
+    device tensor (``inp["cu_dev"]``, the form a trainer's packed batch carries them in: the ops
+    then read them on the device; ``--varlen-bounds device``) or a host list (the ops schedule
+    one launch per sequence; the default)."""
+    cu = inp.get("cu_dev")
+    if cu is None:
+        cu = [0]
+        for n in inp["lens_q"]:
+            cu.append(cu[-1] + n)
     q, kv, qi, ki, w, do = (inp[k][0] for k in ("q", "kv", "q_idx", "k_idx", "w", "dout"))
     with timer("quantize"):
         q8, qs = ops.quantize_fp8_per_row(qi)
@@ -694,10 +702,15 @@ def main():
         lens = torch.randint(1024, 32769, (8,), generator=g).tolist()
         S = sum(lens)
         inp = _device_inputs(S, H, K, args.seed, dev, lens, lens)
+        if args.varlen_bounds == "device":
+            bounds = [0]
+            for n in lens:
+                bounds.append(bounds[-1] + n)
+            inp["cu_dev"] = torch.tensor(bounds, dtype=torch.int32, device=dev)
         step = lambda t: c5_step(inp, ops, t)  # noqa: E731
         pairs = sum(n * (n + 1) // 2 for n in lens)
         cfg = dict(workload="C5(ii): 8 packed sequences (TND), varlen entry points, fwd+bwd", tokens=S,
-                   seq_lens=lens)
+                   seq_lens=lens, seq_bounds=args.varlen_bounds)
     timer = PhaseTimer(torch)
     for _ in range(args.warmup):
         res = step(timer)

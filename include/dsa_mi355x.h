@@ -508,6 +508,45 @@ int dsa_indexer_kl_grad_varlen(const void* q_idx, const void* k_idx, const float
                                int64_t topk, float loss_scale, float eps, float grad_scale,
                                const float* grad_scale_dev, void* stream);
 
+/*
+ * Packed varlen batches with DEVICE cu_seqlens (no host copy of the lengths, so no host
+ * synchronisation per batch).  Same contracts as the _varlen entry points above (reference:
+ * npu_lightning_indexer / npu_sparse_flash_attention / npu_sparse_lightning_indexer_grad_kl_loss
+ * with layout TND and actual_seq_lengths as tensors, ops/aclnn/lightning_indexer/binding.cpp:14,
+ * converters/kernels/dsa.py:159-177, :238-253), except that the lengths are not validated on
+ * the host: every window is clamped into the key tensor, and a sequence with queries and no
+ * keys gives its rows no candidate instead of an error.
+ */
+
+/* Workspace of one dsa_lightning_indexer_tnd call whose row chunks hold up to max_rows rows
+ * (0 if the shape has no tile kernel: D_I must be 128, H_I a multiple of 16 up to 128, bf16 or
+ * fp8).  Per chunk: fp32 score rows of t_k (rounded up to 4) columns, the linear-split pieces
+ * (fp8, H_I = 64), the top-k candidate lists (t_k > 16384) and the row geometry. */
+int64_t dsa_lightning_indexer_tnd_workspace_size(int64_t t_q, int64_t t_k, int64_t n_heads, int64_t head_dim,
+                                                 int dtype, int64_t topk, int64_t max_rows);
+/* dsa_lightning_indexer_varlen with device cu_seqlens_q / cu_seqlens_k (int32 [n_seq + 1]) and
+ * cmp_residual_k (device int32 [n_seq] or NULL): query rows are taken in chunks of as many
+ * rows as the workspace holds; per chunk a geometry kernel reads each row's key window from
+ * the device lengths, the persistent score kernels walk the (query group, key span) pairs
+ * that hold work, and the top-k selects each row's window.  Indices are sequence-local (+
+ * index_offset), -1 padded, bit-identical to dsa_lightning_indexer_varlen's. */
+int dsa_lightning_indexer_tnd(const void* q, const float* q_scale, const void* k, const float* k_scale,
+                              const float* w, int32_t* indices, float* values, int dtype,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              const int32_t* cmp_residual_k, int64_t n_seq, int64_t t_q, int64_t t_k,
+                              int64_t n_heads, int64_t head_dim, int64_t topk, int64_t cmp_ratio, int64_t sparse_mode,
+                              int64_t index_offset, void* workspace, int64_t workspace_bytes, void* stream);
+/* Sequence-local slot indices [t_q, topk] -> global key rows (cu_seqlens_k[i] + v), keeping a
+ * slot iff it passes the per-sequence causal rule of the _varlen attention entry points
+ * (0 <= v < len_k_i, v <= s - cu_seqlens_q[i] + max(0, len_k_i - len_q_i)), else -1.  The
+ * fixed-length attention, mass and indexer KL entry points then take the whole batch as one
+ * [1, t_q] problem with q_offset >= t_k (no causal test): dsa_sparse_mla_fwd(_varlen)
+ * results are bit-identical per row; dKV and dk_I sum the same contributions in another
+ * fp32 grouping. */
+int dsa_tnd_global_indices(const int32_t* indices, int32_t* out, const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqlens_k, int64_t n_seq, int64_t t_q, int64_t t_k, int64_t topk,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

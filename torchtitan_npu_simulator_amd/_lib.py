@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libdsa_mi355x.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 DSA_F32, DSA_BF16, DSA_FP8_E4M3 = 0, 1, 2
 
@@ -120,6 +120,14 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
         _i32,
     ),
+    # packed varlen with device cu_seqlens (device int32 pointers)
+    "dsa_lightning_indexer_tnd_workspace_size": ([_i64, _i64, _i64, _i64, _i32, _i64, _i64], _i64),
+    "dsa_lightning_indexer_tnd": (
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+         _vp, _i64, _vp],
+        _i32,
+    ),
+    "dsa_tnd_global_indices": ([_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp], _i32),
     "dsa_indexer_kl_grad_varlen_workspace_size": ([_vp, _vp, _i64, _i64, _i64, _i64], _i64),
     "dsa_indexer_kl_grad_varlen": (
         [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _f32, _f32,

@@ -137,4 +137,4 @@ extern "C" int dsa_kernel_timing_get(int i, char* name, int64_t name_cap, double
 
 extern "C" const char* dsa_last_error(void) { return dsa::g_last_error.c_str(); }
 
-extern "C" int dsa_abi_version(void) { return 16; }
+extern "C" int dsa_abi_version(void) { return 17; }

@@ -29,9 +29,12 @@ int check_launch(const char* what);
 // per-row top-k (topk.hip): dsa_topk with an optional candidate workspace of
 // topk_cand_bytes(batch * s_q, k) bytes, which rows longer than 16384 keys use to select
 // from one read of their scores
+// With ``win`` (device int32 [2 * win_rows]: each row's first valid key, then the end of its
+// window, the layout indexer_fwd_tnd writes) row r's valid prefix is win[win_rows + r] -
+// win[r] instead of the causal rule.
 int topk_rows(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
               int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset, void* cand_ws,
-              void* stream);
+              void* stream, const int* win = nullptr, int64_t win_rows = 0);
 int64_t topk_cand_bytes(int64_t rows, int64_t k);
 
 // ----- lightning-indexer scores shared by the entry points (host) -----
@@ -42,6 +45,16 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
                 float* scores, int dtype, int64_t batch, int64_t s_q, int64_t s_k, int64_t n_heads,
                 int64_t head_dim, int64_t ld_scores, int64_t q_offset, int64_t cmp_ratio, void* workspace,
                 int64_t workspace_bytes, void* stream, bool fill_masked);
+
+// Packed rows with their key windows on the device (indexer_tile_kernel's kTnd mode): the
+// tiling of the tile kernel that dsa_indexer_fwd would run for this shape (query rows per
+// group, keys per span; false if the shape has no tile kernel), and the scores of ``rows``
+// rows from the geometry array ``tnd`` of ``ngroups`` groups (layout in indexer.hip).
+bool indexer_tnd_tiling(int dtype, int64_t n_heads, int64_t head_dim, int* group_rows, int* span_keys);
+int indexer_fwd_tnd(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
+                    float* scores, int dtype, int64_t rows, int64_t s_k, int64_t n_heads, int64_t head_dim,
+                    int64_t ld_scores, const int* tnd, int64_t ngroups, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 // ----- optional per-kernel timing (host) -----
 // While dsa_kernel_timing(1) is in force, a TimedLaunch scope around a kernel launch
@@ -250,5 +263,35 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 inline unsigned ceil_div(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+// ----- packed ("TND") batches with device cu_seqlens -----
+// Row s of a packed batch belongs to sequence i with cu_q[i] <= s < cu_q[i+1]; its keys are
+// the sequence's [cu_k[i], cu_k[i+1]) and, under sparse_mode 3, the first
+// (s - cu_q[i] + off + 1) / cmp_ratio of them with off = max(0, cmp_ratio * len_k +
+// residual - len_q) (the bottom-right causal rule of one sequence, as the host schedule
+// applies it per sequence).  Everything is clamped into [0, t_k) so that garbage lengths
+// cannot address outside the key tensor.
+__device__ __forceinline__ void tnd_row_window(const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
+                                               const int32_t* __restrict__ res, int n_seq, int64_t s, int cmp_ratio,
+                                               bool causal, int t_k, int& first, int& end) {
+  int lo = 0, hi = n_seq - 1;  // the last sequence whose start is <= s
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (cu_q[mid] <= s) lo = mid;
+    else hi = mid - 1;
+  }
+  const int64_t q0 = cu_q[lo], q1 = cu_q[lo + 1];
+  const int64_t k0 = min<int64_t>(max<int64_t>(cu_k[lo], 0), t_k);
+  const int64_t lk = min<int64_t>(max<int64_t>((int64_t)cu_k[lo + 1] - k0, 0), t_k - k0);
+  int64_t nv = 0;
+  if (s >= q0 && s < q1) {
+    const int64_t r = res ? max<int64_t>(res[lo], 0) : 0;
+    const int64_t off = causal ? max<int64_t>(0, cmp_ratio * lk + r - (q1 - q0)) : ((int64_t)1 << 40);
+    nv = min<int64_t>(max<int64_t>((s - q0 + off + 1) / cmp_ratio, 0), lk);
+  }
+  first = (int)k0;
+  end = (int)(k0 + nv);
+}
+
 
 }  // namespace dsa

@@ -160,12 +160,21 @@ indexer_lin_pieces_kernel(const uint8_t* __restrict__ q, const float* __restrict
   }
 }
 
-template <bool kFp8, int kHeadTiles, bool kLin>
+// kTnd: packed rows whose key windows come from the device (row geometry of a packed batch,
+// see tnd_layout): ``tnd`` holds, for the S rows of the call, each row's first valid key
+// [S] and the end of its window [S], then per query group (kQ rows) the first key of its
+// spans [ngroups], the end of its work [ngroups] and the exclusive prefix of its span
+// counts [ngroups + 1].  The workgroups are persistent: each walks (group, span) items
+// blockIdx.x, blockIdx.x + gridDim.x, ... up to the total, so the launch needs no host copy
+// of the geometry.  A row's score for key t goes to column t - (its first key): row s holds
+// its window's scores in [0, end - first), every other column is left unwritten.
+template <bool kFp8, int kHeadTiles, bool kLin, bool kTnd = false>
 __global__ void __launch_bounds__(kThreads, 2)
 indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_scale, const uint8_t* __restrict__ k,
                     const float* __restrict__ k_scale, const float* __restrict__ w, float* __restrict__ scores,
                     int S, int s_k, int64_t ld, int64_t q_offset, int cmp_ratio,
-                    const uint8_t* __restrict__ lin_pieces, const float* __restrict__ lin_scale, int fill_masked) {
+                    const uint8_t* __restrict__ lin_pieces, const float* __restrict__ lin_scale, int fill_masked,
+                    const int* __restrict__ tnd = nullptr, int ngroups = 0) {
   using T = IdxTile<kFp8, kHeadTiles>;
   static_assert(!kLin || (kFp8 && T::kQw == 2), "the linear split pairs two fp8 queries per wave");
   constexpr int H = kHeadTiles * 16;
@@ -175,11 +184,26 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
   __shared__ float stage[T::kQ + 1][kK];  // + a spare row for duplicate lanes
   __shared__ float ksc[2][kK];
   __shared__ int nv_rows[T::kQ];
+  __shared__ int kl_rows[kTnd ? T::kQ : 1];
   const int b = blockIdx.z;
-  const int s0 = blockIdx.x * T::kQ;
-  const int t0 = blockIdx.y * T::kSpan;
   const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int col = lane & 15, g = lane >> 4;
+  const int n_items = kTnd ? tnd[2 * S + 3 * ngroups] : 1;
+  for (int item = kTnd ? (int)blockIdx.x : 0; item < n_items; item += kTnd ? (int)gridDim.x : 1) {
+  int qg = blockIdx.x, t0 = blockIdx.y * T::kSpan, grp_end = 0;
+  if constexpr (kTnd) {  // the item's group: the last one whose prefix is <= item
+    const int* pfx = tnd + 2 * S + 2 * ngroups;
+    int lo = 0, hi = ngroups - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (pfx[mid] <= item) lo = mid;
+      else hi = mid - 1;
+    }
+    qg = lo;
+    t0 = tnd[2 * S + qg] + (item - pfx[qg]) * T::kSpan;
+    grp_end = tnd[2 * S + ngroups + qg];
+  }
+  const int s0 = qg * T::kQ;
   const int t_end = min(s_k, t0 + T::kSpan);
   const int nrows = min(T::kQ, S - s0);
 
@@ -188,13 +212,13 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
     const int64_t v = (s + q_offset + 1) / cmp_ratio;
     return (int)max((int64_t)0, min((int64_t)s_k, v));
   };
-  const int nv_max = nvalid(s0 + nrows - 1);  // last (largest) frontier of the workgroup
+  const int nv_max = kTnd ? grp_end : nvalid(s0 + nrows - 1);  // last (largest) frontier of the workgroup
   const int t_work = min(t_end, nv_max);      // keys below t_work need MFMA work
   const int64_t q_row0 = (int64_t)b * S;
 
   if (t_work <= t0) {  // the whole key span lies past every query's frontier
     if (fill_masked) fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0, t_end, tid);
-    return;
+    continue;
   }
   const int nsub = (t_work - t0 + kK - 1) / kK;  // key tiles with work
 
@@ -293,7 +317,14 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
 #pragma unroll
       for (int r = 0; r < 4; ++r) asm volatile("" : "+v"(wv[j][ht][r]));
     }
-  if (tid < T::kQ) nv_rows[tid] = s0 + tid < S ? nvalid(s0 + tid) : 0;
+  if (tid < T::kQ) {
+    if constexpr (kTnd) {  // the row's window [first key, end)
+      kl_rows[tid] = s0 + tid < S ? tnd[s0 + tid] : 0;
+      nv_rows[tid] = s0 + tid < S ? tnd[S + s0 + tid] : 0;
+    } else {
+      nv_rows[tid] = s0 + tid < S ? nvalid(s0 + tid) : 0;
+    }
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's tile-0 DMA landed
   __syncthreads();
 
@@ -384,9 +415,12 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
     // one 16-key tile: kQw items, each item's reduction behind the next item's MFMAs; raw
     // head sums are staged (key scale and causal mask are applied when the rows are stored)
     f32x4 cq[2][kHeadTiles];
-    auto tile = [&](int kt, const uint32_t (&kb_cur)[T::kRegsPerTile], uint32_t (&kb_nxt)[T::kRegsPerTile],
-                    const f32x4& cl_cur, f32x4& cl_nxt) {
-      read_b(min(kt + 1, ntiles - 1), kb_nxt);  // (the last tile re-reads itself)
+    // B operands are read kAhead tiles before their first MFMA: two for fp8 (8 registers a
+    // tile; three register sets rotate), one for bf16 (16 registers a tile, two sets)
+    constexpr int kAhead = kFp8 ? 2 : 1;
+    auto tile = [&](int kt, const uint32_t (&kb_cur)[T::kRegsPerTile], const uint32_t (&kb_nxt)[T::kRegsPerTile],
+                    uint32_t (&kb_load)[T::kRegsPerTile], const f32x4& cl_cur, f32x4& cl_nxt) {
+      read_b(min(kt + kAhead, ntiles - 1), kb_load);  // (the last tiles re-read the last one)
       float pe = 0.f;
 #pragma unroll
       for (int j = 0; j < kQw; ++j) {
@@ -421,15 +455,33 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
 #pragma unroll
         for (int ht = 0; ht < kHeadTiles; ++ht) cq[0][ht] = cq[1][ht];
       }
+      if constexpr (kFp8) {
+        // each MFMA followed by VALU work of the reductions (left to itself the scheduler
+        // issues a tile's first item as one run of MFMAs)
+#pragma unroll
+        for (int i = 0; i < kQw * kHeadTiles + (kLin ? 1 : 0); ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+        }
+      }
     };
-    uint32_t kb_a[T::kRegsPerTile], kb_b[T::kRegsPerTile];
-    f32x4 cl_a = (f32x4){0.f, 0.f, 0.f, 0.f}, cl_b = cl_a;
+    uint32_t kb_a[T::kRegsPerTile], kb_b[T::kRegsPerTile], kb_c[kAhead > 1 ? T::kRegsPerTile : 1];
+    f32x4 cl_a = (f32x4){0.f, 0.f, 0.f, 0.f}, cl_b = cl_a, cl_c = cl_a;
     read_b(0, kb_a);
+    if constexpr (kAhead > 1) read_b(min(1, ntiles - 1), kb_b);
     mfma_q(0, kb_a, cq[0]);
     mfma_lin(kb_a, cl_a);
-    for (int kt = 0; kt < ntiles; kt += 2) {  // two tiles per trip: the B registers alternate
-      tile(kt, kb_a, kb_b, cl_a, cl_b);
-      if (kt + 1 < ntiles) tile(kt + 1, kb_b, kb_a, cl_b, cl_a);
+    if constexpr (kAhead > 1) {
+      for (int kt = 0; kt < ntiles; kt += 3) {  // three tiles per trip: the B registers rotate
+        tile(kt, kb_a, kb_b, kb_c, cl_a, cl_b);
+        if (kt + 1 < ntiles) tile(kt + 1, kb_b, kb_c, kb_a, cl_b, cl_c);
+        if (kt + 2 < ntiles) tile(kt + 2, kb_c, kb_a, kb_b, cl_c, cl_a);
+      }
+    } else {
+      for (int kt = 0; kt < ntiles; kt += 2) {  // two tiles per trip: the B registers alternate
+        tile(kt, kb_a, kb_b, kb_b, cl_a, cl_b);
+        if (kt + 1 < ntiles) tile(kt + 1, kb_b, kb_a, kb_a, cl_b, cl_a);
+      }
     }
     __syncthreads();  // the tile's scores are staged
 
@@ -460,6 +512,15 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
       const int qi = i / (kK / 4), kk = 4 * (i % (kK / 4));
       const int t = tb + kk;
       if (qi >= nrows || t >= t_end) continue;
+      if constexpr (kTnd) {  // keys of the row's window only, at column key - first key
+        const int kl = kl_rows[qi], end = nv_rows[qi];
+        float* rowp = scores + (q_row0 + s0 + qi) * ld;
+        const float vv[4] = {v[it].x, v[it].y, v[it].z, v[it].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (t + e >= kl && t + e < end) rowp[t + e - kl] = vv[e];
+        continue;
+      }
       float* dst = scores + (q_row0 + s0 + qi) * ld + t;
       if (t + 4 <= t_end && (((uintptr_t)dst) & 15) == 0) {
         *reinterpret_cast<float4*>(dst) = v[it];
@@ -471,6 +532,8 @@ indexer_tile_kernel(const uint8_t* __restrict__ q, const float* __restrict__ q_s
   }
   // key tiles of the span past every frontier
   if (fill_masked) fill_neg_inf(scores, q_row0 + s0, nrows, ld, t0 + nsub * kK, t_end, tid);
+  if constexpr (kTnd) __syncthreads();  // the next item rewrites the row windows and tiles
+  }
 }
 
 // Generic path (any H, D; fp32 arithmetic): one thread per (query, key).
@@ -620,6 +683,95 @@ int indexer_fwd(const void* q, const float* q_scale, const void* k, const float*
       return set_error(DSA_ERR_UNSUPPORTED, "dsa_indexer_fwd: dtype %d", dtype);
   }
   return check_launch("dsa_indexer_fwd(generic)");
+}
+
+// ----- packed rows with device geometry -----
+bool indexer_tnd_tiling(int dtype, int64_t n_heads, int64_t head_dim, int* group_rows, int* span_keys) {
+  if (head_dim != kD || n_heads % 16 != 0 || n_heads > 128 || (dtype != DSA_FP8_E4M3 && dtype != DSA_BF16))
+    return false;
+  const int ht = (int)(n_heads / 16);
+  const bool fp8 = dtype == DSA_FP8_E4M3;
+  // IdxTile<fp8, ht>: kQ = 4 * kQw, kSpan = 4 * (32768 / row bytes)
+  const int qw = fp8 ? (8 / ht > 0 ? 8 / ht : 1) : (4 / ht > 0 ? 4 / ht : 1);
+  *group_rows = 4 * qw;
+  *span_keys = 4 * (32768 / (kD * (fp8 ? 1 : 2)));
+  return true;
+}
+
+namespace {
+// persistent workgroups of the packed-row launches: two per CU (the tile kernels' occupancy)
+int tnd_workgroups(hipStream_t st) {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipStreamGetDevice(st, &dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return 2 * cus[dev];
+}
+}  // namespace
+
+int indexer_fwd_tnd(const void* q, const float* q_scale, const void* k, const float* k_scale, const float* w,
+                    float* scores, int dtype, int64_t rows, int64_t s_k, int64_t n_heads, int64_t head_dim,
+                    int64_t ld_scores, const int* tnd, int64_t ngroups, void* workspace, int64_t workspace_bytes,
+                    void* stream) {
+  const char* what = "dsa_lightning_indexer_tnd";
+  int gr = 0, sk = 0;
+  if (!indexer_tnd_tiling(dtype, n_heads, head_dim, &gr, &sk))
+    return set_error(DSA_ERR_UNSUPPORTED, "%s: H_I=%lld, D_I=%lld, dtype %d has no tile kernel (H_I a multiple of 16 "
+                     "up to 128, D_I 128, bf16 or fp8)", what, (long long)n_heads, (long long)head_dim, dtype);
+  if (!q || !k || !w || !scores || !tnd) return set_error(DSA_ERR_INVALID_ARG, "%s: null pointer", what);
+  if (rows <= 0 || s_k <= 0 || ld_scores < s_k || rows > 2147483647LL || s_k > 2147483647LL ||
+      ngroups != (rows + gr - 1) / gr)
+    return set_error(DSA_ERR_INVALID_ARG, "%s: bad sizes", what);
+  const int64_t key_row_bytes = head_dim * (dtype == DSA_FP8_E4M3 ? 1 : 2);
+  if (s_k > (int64_t)(0xffffffffu / key_row_bytes))
+    return set_error(DSA_ERR_UNSUPPORTED, "%s: %lld keys exceed the tile kernels' 32-bit key offsets", what,
+                     (long long)s_k);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)tnd_workgroups(st), 1, 1);
+  const uint8_t* qp = (const uint8_t*)q;
+  const uint8_t* kp = (const uint8_t*)k;
+  const int S = (int)rows, n = (int)s_k, G = (int)ngroups;
+  if (lin_split_shape(dtype, n_heads, head_dim)) {
+    if (!workspace || workspace_bytes < rows * kLinRowBytes)
+      return set_error(DSA_ERR_INVALID_ARG, "%s: workspace of %lld bytes, %lld needed for the linear split", what,
+                       (long long)workspace_bytes, (long long)(rows * kLinRowBytes));
+    uint8_t* pieces = (uint8_t*)workspace;
+    float* pscale = (float*)(pieces + rows * kLinPieces * kD);
+    {
+      const TimedLaunch tl("indexer_lin_pieces_kernel<64>", st);
+      indexer_lin_pieces_kernel<64><<<(unsigned)ceil_div(rows, kThreads / 64), kThreads, 0, st>>>(qp, q_scale, w,
+                                                                                                 pieces, pscale, rows);
+    }
+    const TimedLaunch tl("indexer_tile_kernel<fp8, 4, split, tnd>", st);
+    indexer_tile_kernel<true, 4, true, true><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, S, n,
+                                                                        ld_scores, 0, 1, pieces, pscale, 0, tnd, G);
+    return check_launch("dsa_lightning_indexer_tnd(linear split)");
+  }
+#define DSA_IDX_TND(FP8, HT)                                                                                      \
+  do {                                                                                                             \
+    const TimedLaunch tl("indexer_tile_kernel<tnd>", st);                                                          \
+    indexer_tile_kernel<FP8, HT, false, true><<<grid, kThreads, 0, st>>>(qp, q_scale, kp, k_scale, w, scores, S, n, \
+                                                                         ld_scores, 0, 1, nullptr, nullptr, 0, tnd, \
+                                                                         G);                                       \
+  } while (0)
+  const bool fp8 = dtype == DSA_FP8_E4M3;
+  switch ((int)(n_heads / 16) * 2 + (fp8 ? 1 : 0)) {
+    case 2: DSA_IDX_TND(false, 1); break;
+    case 3: DSA_IDX_TND(true, 1); break;
+    case 4: DSA_IDX_TND(false, 2); break;
+    case 5: DSA_IDX_TND(true, 2); break;
+    case 8: DSA_IDX_TND(false, 4); break;
+    case 9: DSA_IDX_TND(true, 4); break;
+    case 16: DSA_IDX_TND(false, 8); break;
+    case 17: DSA_IDX_TND(true, 8); break;
+    default: return set_error(DSA_ERR_UNSUPPORTED, "%s: H_I=%lld", what, (long long)n_heads);
+  }
+#undef DSA_IDX_TND
+  return check_launch("dsa_lightning_indexer_tnd");
 }
 
 }  // namespace dsa

@@ -81,7 +81,8 @@ template <int kR, bool kSingle, bool kVec, int kMode = 0>
 __global__ void __launch_bounds__(kThreads)
 topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, float* __restrict__ out_val, int S,
             int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio, int64_t index_offset,
-            const uint2* __restrict__ cand = nullptr, const int* __restrict__ cand_cnt = nullptr, int cap = 0) {
+            const uint2* __restrict__ cand = nullptr, const int* __restrict__ cand_cnt = nullptr, int cap = 0,
+            const int* __restrict__ win = nullptr, int64_t win_rows = 0) {
   static_assert(kMode != 1 || kSingle, "a candidate list is one segment");
   constexpr int kSeg = kThreads * 4 * kR;
   __shared__ uint32_t hist[kBins];
@@ -95,7 +96,7 @@ topk_kernel(const float* __restrict__ scores, int32_t* __restrict__ out_idx, flo
   const int lane = t & 63, wave = t >> 6;
   const int64_t row = (int64_t)b * S + s;
   const float* src = scores + row * ld;
-  const int64_t nv64 = (s + q_offset + 1) / cmp_ratio;
+  const int64_t nv64 = win ? (int64_t)(win[win_rows + row] - win[row]) : (s + q_offset + 1) / cmp_ratio;
   int nv = (int)max((int64_t)0, min((int64_t)s_k, nv64));
   const uint2* crow = kMode == 1 ? cand + row * (int64_t)cap : nullptr;
   if constexpr (kMode == 1) {
@@ -423,7 +424,8 @@ constexpr int kCandChunks = 8;
 template <bool kVec>
 __global__ void __launch_bounds__(kThreads)
 topk_cand_kernel(const float* __restrict__ scores, uint2* __restrict__ cand, int* __restrict__ cand_cnt, int cap,
-                 int S, int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio) {
+                 int S, int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio,
+                 const int* __restrict__ win = nullptr, int64_t win_rows = 0) {
   constexpr int kR = 8, kSeg = kThreads * 4 * kR;  // 8192-score segments
   __shared__ uint32_t hist[kBins];
   __shared__ uint32_t red[3][kWaves];
@@ -434,7 +436,7 @@ topk_cand_kernel(const float* __restrict__ scores, uint2* __restrict__ cand, int
   const int lane = t & 63, wave = t >> 6;
   const int64_t row = (int64_t)b * S + s;
   const float* src = scores + row * ld;
-  const int64_t nv64 = (s + q_offset + 1) / cmp_ratio;
+  const int64_t nv64 = win ? (int64_t)(win[win_rows + row] - win[row]) : (s + q_offset + 1) / cmp_ratio;
   const int nv = (int)max((int64_t)0, min((int64_t)s_k, nv64));
   const int s_k4 = s_k & ~3;
   uint2* crow = cand + row * (int64_t)cap;
@@ -645,14 +647,17 @@ topk_cand_kernel(const float* __restrict__ scores, uint2* __restrict__ cand, int
 
 template <int kR, bool kSingle>
 void launch_topk(bool vec, dim3 grid, hipStream_t st, const float* scores, int32_t* indices, float* values, int S,
-                 int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio, int64_t index_offset) {
+                 int s_k, int64_t ld, int k, int64_t q_offset, int cmp_ratio, int64_t index_offset, const int* win,
+                 int64_t win_rows) {
   const TimedLaunch tl("topk_kernel", st);
   if (vec)
     topk_kernel<kR, kSingle, true><<<grid, kThreads, 0, st>>>(scores, indices, values, S, s_k, ld, k, q_offset,
-                                                              cmp_ratio, index_offset);
+                                                              cmp_ratio, index_offset, nullptr, nullptr, 0, win,
+                                                              win_rows);
   else
     topk_kernel<kR, kSingle, false><<<grid, kThreads, 0, st>>>(scores, indices, values, S, s_k, ld, k, q_offset,
-                                                               cmp_ratio, index_offset);
+                                                               cmp_ratio, index_offset, nullptr, nullptr, 0, win,
+                                                               win_rows);
 }
 
 }  // namespace
@@ -668,7 +673,7 @@ int64_t topk_cand_bytes(int64_t rows, int64_t k) { return rows * (int64_t)topk_c
 // candidate pass, selection over the candidate lists, the fallback rows from their scores.
 int topk_long_cand(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
                    int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset,
-                   void* cand_ws, hipStream_t st) {
+                   void* cand_ws, hipStream_t st, const int* win, int64_t win_rows) {
   const int cap = topk_cand_cap(k);
   uint2* cand = (uint2*)cand_ws;
   int* cnt = (int*)((char*)cand_ws + batch * s_q * (int64_t)cap * 8);
@@ -678,27 +683,33 @@ int topk_long_cand(const float* scores, int32_t* indices, float* values, int64_t
   {
     const TimedLaunch tl("topk_cand_kernel", st);
     if (vec)
-      topk_cand_kernel<true><<<grid, kThreads, 0, st>>>(scores, cand, cnt, cap, S, n, ld_scores, kk, q_offset, r);
+      topk_cand_kernel<true><<<grid, kThreads, 0, st>>>(scores, cand, cnt, cap, S, n, ld_scores, kk, q_offset, r,
+                                                        win, win_rows);
     else
-      topk_cand_kernel<false><<<grid, kThreads, 0, st>>>(scores, cand, cnt, cap, S, n, ld_scores, kk, q_offset, r);
+      topk_cand_kernel<false><<<grid, kThreads, 0, st>>>(scores, cand, cnt, cap, S, n, ld_scores, kk, q_offset, r,
+                                                         win, win_rows);
   }
   {
     const TimedLaunch tl("topk_kernel<cand>", st);
     if (cap == 4096)
       topk_kernel<4, true, false, 1><<<grid, kThreads, 0, st>>>(scores, indices, values, S, n, ld_scores, kk,
-                                                                q_offset, r, index_offset, cand, cnt, cap);
+                                                                q_offset, r, index_offset, cand, cnt, cap, win,
+                                                                win_rows);
     else
       topk_kernel<8, true, false, 1><<<grid, kThreads, 0, st>>>(scores, indices, values, S, n, ld_scores, kk,
-                                                                q_offset, r, index_offset, cand, cnt, cap);
+                                                                q_offset, r, index_offset, cand, cnt, cap, win,
+                                                                win_rows);
   }
   {
     const TimedLaunch tl("topk_kernel<fallback>", st);
     if (vec)
       topk_kernel<8, false, true, 2><<<grid, kThreads, 0, st>>>(scores, indices, values, S, n, ld_scores, kk,
-                                                                q_offset, r, index_offset, cand, cnt, cap);
+                                                                q_offset, r, index_offset, cand, cnt, cap, win,
+                                                                win_rows);
     else
       topk_kernel<8, false, false, 2><<<grid, kThreads, 0, st>>>(scores, indices, values, S, n, ld_scores, kk,
-                                                                 q_offset, r, index_offset, cand, cnt, cap);
+                                                                 q_offset, r, index_offset, cand, cnt, cap, win,
+                                                                 win_rows);
   }
   return check_launch("dsa_topk(candidates)");
 }
@@ -733,7 +744,7 @@ extern "C" int dsa_topk_ws(const float* scores, int32_t* indices, float* values,
 namespace dsa {
 int topk_rows(const float* scores, int32_t* indices, float* values, int64_t batch, int64_t s_q, int64_t s_k,
               int64_t ld_scores, int64_t k, int64_t q_offset, int64_t cmp_ratio, int64_t index_offset, void* cand_ws,
-              void* stream) {
+              void* stream, const int* win, int64_t win_rows) {
   if (!scores || !indices) return set_error(DSA_ERR_INVALID_ARG, "dsa_topk: null pointer");
   if (batch <= 0 || s_q <= 0 || s_k < 0 || k <= 0 || k > 4096 || ld_scores < s_k || cmp_ratio <= 0)
     return set_error(DSA_ERR_INVALID_ARG, "dsa_topk: bad sizes (B=%lld S=%lld S_k=%lld ld=%lld k=%lld r=%lld)",
@@ -747,14 +758,17 @@ int topk_rows(const float* scores, int32_t* indices, float* values, int64_t batc
   const bool vec = s_k >= 4 && (ld_scores % 4) == 0 && ((uintptr_t)scores % 16) == 0;
   const int S = (int)s_q, n = (int)s_k, kk = (int)k, r = (int)cmp_ratio;
   if (s_k <= 8192)
-    launch_topk<8, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
+    launch_topk<8, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset, win,
+                         win_rows);
   else if (s_k <= 16384)
-    launch_topk<16, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
+    launch_topk<16, true>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset, win,
+                          win_rows);
   else if (cand_ws)  // long rows: one read into candidate lists, selection over those
     return topk_long_cand(scores, indices, values, batch, s_q, s_k, ld_scores, k, q_offset, cmp_ratio, index_offset,
-                          cand_ws, st);
+                          cand_ws, st, win, win_rows);
   else  // long rows: 8192-score segments re-read per pass; 61 VGPRs, seven waves per SIMD in flight
-    launch_topk<8, false>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset);
+    launch_topk<8, false>(vec, grid, st, scores, indices, values, S, n, ld_scores, kk, q_offset, r, index_offset, win,
+                          win_rows);
   return check_launch("dsa_topk");
 }
 }  // namespace dsa

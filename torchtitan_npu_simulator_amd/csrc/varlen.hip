@@ -239,3 +239,51 @@ extern "C" int dsa_indexer_kl_grad_varlen(const void* q_idx, const void* k_idx, 
   }
   return DSA_OK;
 }
+
+// ----- packed batches with device cu_seqlens: one launch over all rows -----
+// The attention, its mass and the indexer KL take a packed batch as one [1, T] problem when
+// its slot indices are global key rows: row s of sequence i keeps local slot v iff
+// 0 <= v < (its causal count under the per-sequence rule of the host schedule above:
+// min(len_k, s - cu_q[i] + max(0, len_k - len_q) + 1)), as cu_k[i] + v, and -1 otherwise.
+// Run with the causal test off (q_offset past every key), the fixed-length kernels then
+// compute each row from exactly the rows the per-sequence launch would gather, in the same
+// order; only the key-major reductions (dKV, dk_I) group their fp32 sums differently.
+namespace dsa {
+namespace {
+__global__ void __launch_bounds__(256)
+tnd_global_indices_kernel(const int32_t* __restrict__ idx, int32_t* __restrict__ out,
+                          const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k, int n_seq, int t_q,
+                          int t_k, int topk) {
+  const int s = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (s >= t_q) return;  // whole waves
+  int first, end;
+  tnd_row_window(cu_q, cu_k, nullptr, n_seq, s, 1, true, t_k, first, end);
+  const int n = end - first;
+  const int32_t* src = idx + (int64_t)s * topk;
+  int32_t* dst = out + (int64_t)s * topk;
+  for (int j = lane; j < topk; j += 64) {
+    const int v = src[j];
+    dst[j] = (v >= 0 && v < n) ? first + v : -1;
+  }
+}
+}  // namespace
+}  // namespace dsa
+
+extern "C" int dsa_tnd_global_indices(const int32_t* indices, int32_t* out, const int32_t* cu_seqlens_q,
+                                      const int32_t* cu_seqlens_k, int64_t n_seq, int64_t t_q, int64_t t_k,
+                                      int64_t topk, void* stream) {
+  using namespace dsa;
+  const char* what = "dsa_tnd_global_indices";
+  if (!indices || !out || !cu_seqlens_q || !cu_seqlens_k) return set_error(DSA_ERR_INVALID_ARG, "%s: null pointer", what);
+  if (n_seq <= 0 || t_q < 0 || t_k < 0 || topk <= 0 || n_seq > 2147483646LL || t_q > 2147483647LL ||
+      t_k > 2147483647LL || topk > 2147483647LL)
+    return set_error(DSA_ERR_INVALID_ARG, "%s: bad sizes", what);
+  if (t_q == 0) return DSA_OK;
+  hipStream_t st = (hipStream_t)stream;
+  {
+    const TimedLaunch tl("tnd_global_indices_kernel", st);
+    tnd_global_indices_kernel<<<ceil_div(t_q, 4), 256, 0, st>>>(indices, out, cu_seqlens_q, cu_seqlens_k,
+                                                                (int)n_seq, (int)t_q, (int)t_k, (int)topk);
+  }
+  return check_launch(what);
+}

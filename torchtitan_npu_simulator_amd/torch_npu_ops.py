@@ -153,6 +153,37 @@ def to_cu_seqlens(cu_seqlens=None, actual_seq_lengths=None, total=None) -> list[
     return cu
 
 
+def _on_device(x) -> bool:
+    return isinstance(x, torch.Tensor) and x.is_cuda
+
+
+def seq_bounds(cu_seqlens=None, actual_seq_lengths=None, total=None):
+    """Sequence boundaries of a packed batch: a GPU tensor stays on the device (int32
+    [0, end_0, end_1, ...], built there from ``cu_seqlens`` or from the cumulative ends
+    ``actual_seq_lengths`` without reading them, so the ops take their device paths with no
+    host synchronisation); anything else becomes the validated host list of
+    ``to_cu_seqlens``."""
+    src = cu_seqlens if cu_seqlens is not None else actual_seq_lengths
+    if _on_device(src):
+        t = src.reshape(-1).to(torch.int32)
+        if cu_seqlens is None:
+            t = torch.cat([t.new_zeros(1), t])
+        return t.contiguous()
+    return to_cu_seqlens(cu_seqlens, actual_seq_lengths, total)
+
+
+def _device_bounds(*bounds, device):
+    """Each of ``bounds`` (host list, CPU or GPU tensor, or None) as a device int32 tensor."""
+    out = []
+    for b in bounds:
+        if b is None or _on_device(b):
+            out.append(None if b is None else b.reshape(-1).to(device=device, dtype=torch.int32).contiguous())
+        else:
+            vals = b.tolist() if isinstance(b, torch.Tensor) else list(b)
+            out.append(torch.tensor(vals, dtype=torch.int32, device=device))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # lightning indexer + top-k
 # ---------------------------------------------------------------------------
@@ -288,8 +319,8 @@ def npu_lightning_indexer(
         raise NotImplementedError(f"layouts {layout_query}/{layout_key} (BSND/BSND or TND/TND)")
     if layout_query == "TND":
         kt = key.reshape(key.shape[0], key.shape[-1])
-        cu_q = to_cu_seqlens(cu_seqlens_q, actual_seq_lengths_query, query.shape[0])
-        cu_k = to_cu_seqlens(cu_seqlens_k, actual_seq_lengths_key, kt.shape[0])
+        cu_q = seq_bounds(cu_seqlens_q, actual_seq_lengths_query, query.shape[0])
+        cu_k = seq_bounds(cu_seqlens_k, actual_seq_lengths_key, kt.shape[0])
         idx, vals = lightning_indexer_varlen(query, kt, weights, cu_q, cu_k, sparse_count, sparse_mode=sparse_mode,
                                              cmp_ratio=cmp_ratio, cmp_residual_k=cmp_residual_k,
                                              return_value=return_value, query_scale=query_scale, key_scale=key_scale,
@@ -409,6 +440,11 @@ def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sp
     T_k = key.shape[0]
     if query.dtype != key.dtype:
         raise ValueError("query and key must share a dtype")
+    if any(_on_device(b) for b in (cu_seqlens_q, cu_seqlens_k, cmp_residual_k)):
+        res = _lightning_indexer_tnd(query, key, weights, cu_seqlens_q, cu_seqlens_k, sparse_count, sparse_mode,
+                                     cmp_ratio, cmp_residual_k, return_value, query_scale, key_scale, index_offset)
+        if res is not None:
+            return res
     cu_q = to_cu_seqlens(cu_seqlens_q, None, T)
     cu_k = to_cu_seqlens(cu_seqlens_k, None, T_k)
     if len(cu_q) != len(cu_k):
@@ -447,6 +483,85 @@ def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sp
         "dsa_lightning_indexer_varlen",
     )
     return idx, vals
+
+
+def _lightning_indexer_tnd(query, key, weights, cu_seqlens_q, cu_seqlens_k, sparse_count, sparse_mode, cmp_ratio,
+                           cmp_residual_k, return_value, query_scale, key_scale, index_offset):
+    """lightning_indexer_varlen with device sequence bounds (dsa_lightning_indexer_tnd): the
+    windows are read on the device, so nothing is copied back.  None if the shape has no tile
+    kernel (the host schedule then serves it)."""
+    lib = load_library()
+    T, H, D = query.shape
+    T_k = key.shape[0]
+    K = int(sparse_count)
+    dt = _lib.dtype_code(query.dtype)
+    ld = (T_k + 3) // 4 * 4
+    max_rows = max(1, _SCORE_BUDGET_BYTES // (4 * ld))
+    ws_bytes = int(lib.dsa_lightning_indexer_tnd_workspace_size(max(T, 1), T_k, H, D, dt, K, max_rows))
+    if ws_bytes <= 0:
+        return None
+    dev = query.device
+    cu_q, cu_k, res = _device_bounds(cu_seqlens_q, cu_seqlens_k, cmp_residual_k, device=dev)
+    if cu_q.numel() != cu_k.numel() or cu_q.numel() < 2:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k describe different numbers of sequences")
+    n_seq = cu_q.numel() - 1
+    if res is not None and res.numel() != n_seq:
+        raise ValueError("cmp_residual_k needs one entry per sequence")
+    q = query.contiguous()
+    k = key.contiguous()
+    w = weights.float().contiguous()
+    qs = None if query_scale is None else query_scale.float().contiguous()
+    ks = None if key_scale is None else key_scale.float().contiguous()
+    idx = torch.empty(T, K, dtype=torch.int32, device=dev)
+    vals = torch.empty(T, K, dtype=torch.float32, device=dev) if return_value else None
+    if T == 0:
+        return idx, vals
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    check(
+        lib.dsa_lightning_indexer_tnd(ptr(q), ptr(qs), ptr(k), ptr(ks), ptr(w), ptr(idx), ptr(vals), dt, ptr(cu_q),
+                                      ptr(cu_k), ptr(res), n_seq, T, T_k, H, D, K, int(cmp_ratio), int(sparse_mode),
+                                      int(index_offset), ptr(ws), ws_bytes, stream_of(dev)),
+        "dsa_lightning_indexer_tnd",
+    )
+    return idx, vals
+
+
+_global_idx_entry = None  # (key, source tensors, global indices [T,K] int32)
+
+
+def tnd_global_indices(indices, cu_seqlens_q, cu_seqlens_k, t_k):
+    """Sequence-local slot indices [T,K] of a packed batch as global key rows
+    (dsa_tnd_global_indices): slot v of a row of sequence i becomes cu_seqlens_k[i] + v if it
+    passes that sequence's causal rule, else -1, so the fixed-length kernels run the batch
+    as one [1, T] problem with no causal test.  ``cu_seqlens_*`` are device int32 tensors.
+    The last result is kept (with the tensors it came from, so their addresses cannot be
+    reused while it lives) for the other ops of the same step: forward, backward, mass and
+    indexer KL all take the same indices."""
+    global _global_idx_entry
+    lib = load_library()
+    key = tuple((t.data_ptr(), t._version, tuple(t.shape), tuple(t.stride())) for t in
+                (indices, cu_seqlens_q, cu_seqlens_k)) + (indices.device, int(t_k))
+    e = _global_idx_entry
+    if e is not None and e[0] == key:
+        return e[2]
+    _global_idx_entry = None
+    T, K = indices.shape
+    out = torch.empty(T, K, dtype=torch.int32, device=indices.device)
+    check(lib.dsa_tnd_global_indices(ptr(indices), ptr(out), ptr(cu_seqlens_q), ptr(cu_seqlens_k),
+                                     cu_seqlens_q.numel() - 1, T, int(t_k), K, stream_of(indices.device)),
+          "dsa_tnd_global_indices")
+    _global_idx_entry = (key, (indices, cu_seqlens_q, cu_seqlens_k), out)
+    return out
+
+
+def _varlen_global(indices, cu_seqlens_q, cu_seqlens_kv, T, T_kv, device):
+    """Global indices [T,K] when the sequence bounds are on the device, else None."""
+    if not (_on_device(cu_seqlens_q) or _on_device(cu_seqlens_kv)):
+        return None
+    cu_q, cu_k = _device_bounds(cu_seqlens_q, cu_seqlens_kv, device=device)
+    if cu_q.numel() != cu_k.numel() or cu_q.numel() < 2:
+        raise ValueError("cu_seqlens_q and cu_seqlens_kv describe different numbers of sequences")
+    return tnd_global_indices(indices.reshape(T, -1).to(torch.int32).contiguous(), cu_q, cu_k, T_kv)
 
 
 # ---------------------------------------------------------------------------
@@ -644,6 +759,11 @@ def sparse_mla_fwd_varlen(q, kv, indices, scale, cu_seqlens_q, cu_seqlens_kv, *,
     require_gpu_tensor(q, "q")
     T, H, D = q.shape
     kv = kv.reshape(kv.shape[0], kv.shape[-1]).contiguous()
+    g = _varlen_global(indices, cu_seqlens_q, cu_seqlens_kv, T, kv.shape[0], q.device)
+    if g is not None:  # device bounds: one launch over the batch
+        out, smax, ssum = sparse_mla_fwd(q.unsqueeze(0), kv.unsqueeze(0), g.unsqueeze(0), scale, d_v=d_v,
+                                         q_offset=_NO_MASK_OFFSET)
+        return out[0], smax[0], ssum[0]
     cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, kv.shape[0])
     K = indices.shape[-1]
     q = q.contiguous()
@@ -669,6 +789,12 @@ def sparse_mla_bwd_varlen(q, kv, indices, out, dout, smax, ssum, scale, cu_seqle
     T, H, D = q.shape
     kv = kv.reshape(kv.shape[0], kv.shape[-1]).contiguous()
     T_kv = kv.shape[0]
+    g = _varlen_global(indices, cu_seqlens_q, cu_seqlens_kv, T, T_kv, q.device)
+    if g is not None:  # device bounds: one launch over the batch
+        res = sparse_mla_bwd(q.unsqueeze(0), kv.unsqueeze(0), g.unsqueeze(0), out.unsqueeze(0), dout.unsqueeze(0),
+                             smax.unsqueeze(0), ssum.unsqueeze(0), scale, q_offset=_NO_MASK_OFFSET,
+                             workspace_bytes=workspace_bytes, return_mass=return_mass)
+        return tuple(t[0] for t in res)
     cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, T_kv)
     K = indices.shape[-1]
     d_v = out.shape[-1]
@@ -698,6 +824,10 @@ def attn_mass_varlen(q, kv, indices, smax, ssum, scale, cu_seqlens_q, cu_seqlens
     lib = load_library()
     T, H, D = q.shape
     kv = kv.reshape(kv.shape[0], kv.shape[-1]).contiguous()
+    g = _varlen_global(indices, cu_seqlens_q, cu_seqlens_kv, T, kv.shape[0], q.device)
+    if g is not None:  # device bounds: one launch over the batch
+        return attn_mass(q.unsqueeze(0), kv.unsqueeze(0), g.unsqueeze(0), smax.unsqueeze(0), ssum.unsqueeze(0), scale,
+                         q_offset=_NO_MASK_OFFSET)[0]
     cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, kv.shape[0])
     K = indices.shape[-1]
     q = q.contiguous()
@@ -896,8 +1026,8 @@ def npu_sparse_flash_attention(
     if layout_query == "TND":
         if sparse_mode != 3 or q_offset is not None:
             raise NotImplementedError("TND runs the per-sequence causal rule (sparse_mode=3) only")
-        cu_q = to_cu_seqlens(cu_seqlens_q, actual_seq_lengths_query, query.shape[0])
-        cu_k = to_cu_seqlens(cu_seqlens_kv, actual_seq_lengths_kv, key.shape[0])
+        cu_q = seq_bounds(cu_seqlens_q, actual_seq_lengths_query, query.shape[0])
+        cu_k = seq_bounds(cu_seqlens_kv, actual_seq_lengths_kv, key.shape[0])
         idx = sparse_indices.reshape(query.shape[0], -1)
         return _SparseFlashAttentionTND.apply(query, key, query_rope, key_rope, idx, float(scale_value), cu_q, cu_k)
     if actual_seq_lengths_query is not None or actual_seq_lengths_kv is not None:
@@ -1539,8 +1669,8 @@ def npu_sparse_lightning_indexer_grad_kl_loss(
         q = _cat_last(query, query_rope) if query_rope is not None else query.contiguous()
         kv = _cat_last(key, key_rope) if key_rope is not None else key.contiguous()
         kv2 = kv.reshape(kv.shape[0], kv.shape[-1])
-        cu_q = to_cu_seqlens(cu_seqlens_q, actual_seq_qlen, q.shape[0])
-        cu_k = to_cu_seqlens(cu_seqlens_k, actual_seq_klen, kv2.shape[0])
+        cu_q = seq_bounds(cu_seqlens_q, actual_seq_qlen, q.shape[0])
+        cu_k = seq_bounds(cu_seqlens_k, actual_seq_klen, kv2.shape[0])
         idx = sparse_indices.reshape(q.shape[0], -1).to(torch.int32).contiguous()
         mass = attn_mass_varlen(q, kv2, idx, softmax_max, softmax_sum, scale_value, cu_q, cu_k)
         dq_i, dk_i, dw, loss_rows = indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, idx, mass, cu_q,
@@ -1705,6 +1835,12 @@ def indexer_kl_grad_from_mass_varlen(query_index, key_index, weight, indices, ma
     w = weight.float().contiguous()
     T, HI, DI = qi.shape
     T_k = ki.shape[0]
+    g = _varlen_global(indices, cu_seqlens_q, cu_seqlens_k, T, T_k, qi.device)
+    if g is not None:  # device bounds: one launch over the batch
+        res = indexer_kl_grad_from_mass(qi.unsqueeze(0), ki.unsqueeze(0), w.unsqueeze(0), g.unsqueeze(0),
+                                        mass.reshape(T, -1).unsqueeze(0), q_offset=_NO_MASK_OFFSET,
+                                        loss_scale=loss_scale, eps=eps, grad_scale=grad_scale)
+        return tuple(t[0] for t in res)
     cu_q, cu_k, n_seq = _varlen_seqs(cu_seqlens_q, cu_seqlens_k, T, T_k)
     idx = indices.reshape(T, -1).to(torch.int32).contiguous()
     K = idx.shape[-1]
