@@ -300,3 +300,44 @@ def test_shared_pair_csr_matches_per_op_builds(d_qk, s_kv_extra):
         ops._share_pair_csr = True
     for a, b in zip(shared, own):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize(
+    "S,K,s_kv,windows",
+    [
+        # 512-row counting blocks, four 16384-key ranges: block b keeps to range b % 3
+        (3000, 64, 50000, [(100, 2100), (16484, 18484), (32868, 34868)]),
+        # 78-row blocks (34 of them: two column-scan chunks of 32), two ranges: even blocks in
+        # range 0, odd blocks in range 1
+        (2600, 1024, 20000, [(100, 8000), (16500, 19900)]),
+    ],
+)
+def test_bwd_pair_fill_row_blocks_without_keys_in_a_range(S, K, s_kv, windows):
+    """Key spaces past 14336 keys take the unstaged CSR fill, which skips the (row block,
+    16384-key range) pairs that hold no pair.  Here every counting row block keeps its slots
+    inside one range, so most pairs are skipped, including blocks next to a column-scan chunk
+    edge: dQ and dKV equal the fp32 GPU reference (dKV per 256-key block), keys no row selects
+    stay exactly zero, and a second run gives the same bits."""
+    from tests.attn_reference import attention_reference, chunk_rel_errors
+
+    H = 16
+    q_offset = s_kv - S
+    rows_per_block = max(16, min(512, 4 * s_kv // K))  # the counting workgroup's rows
+    q, kv, dout, scale = attn_inputs(S, H, q_offset=q_offset, seed=45)
+    g = torch.Generator().manual_seed(45)
+    idx = torch.empty(1, S, K, dtype=torch.int32)
+    for s in range(S):
+        lo, hi = windows[(s // rows_per_block) % len(windows)]
+        idx[0, s] = torch.sort(lo + torch.randperm(hi - lo, generator=g)[:K]).values.int()
+    idx[0, ::7, ::5] = -1
+    runs = [_gpu_fwd_bwd(q, kv, idx, dout, scale, q_offset) for _ in range(2)]
+    out, _, _, dq, dkv = runs[0]
+    assert torch.equal(runs[1][4], dkv) and torch.equal(runs[1][3], dq)
+    ref = attention_reference(q.to(DEV), kv.to(DEV), idx.to(DEV), dout.to(DEV), scale, q_offset=q_offset)
+    assert rel_err(dq, ref["dq"].cpu()) <= BF16_TOL, rel_err(dq, ref["dq"].cpu())
+    e = chunk_rel_errors(dkv[0], ref["dkv"].cpu(), 256)
+    assert float(e.max()) <= BF16_TOL, float(e.max())
+    touched = torch.zeros(s_kv, dtype=torch.bool)
+    sel = idx.flatten().long()
+    touched[sel[sel >= 0]] = True
+    assert float(dkv[0, ~touched].abs().sum()) == 0.0

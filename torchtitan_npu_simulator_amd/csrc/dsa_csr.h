@@ -122,8 +122,21 @@ csr_count_kernel(const int32_t* __restrict__ idx, int* __restrict__ table, const
     return;
   }
   const int* coff = chunk_off + (int64_t)(rb / kColChunk) * s_kv + key0;
-  for (int j = threadIdx.x; j < nkeys; j += 256) hist[j] = row_ptr[key0 + j] + coff[j] + trow[j];
-  __syncthreads();
+  // The column scan left table[rb][key] = the pairs of the row blocks before rb in its chunk of
+  // kColChunk, so where rb + 1 lies in the same chunk, table[rb + 1][key] - table[rb][key] is
+  // rb's own count: a row block with no pair in this key range places nothing here and skips
+  // the walk over its index rows (a packed batch on global key rows keeps each row's keys in
+  // its own sequence; causal rows keep theirs below the row).  The last row block of a chunk
+  // always walks.
+  const int n_rb = (int)gridDim.x / n_ranges;
+  const bool next_in_chunk = (rb + 1) % kColChunk != 0 && rb + 1 < n_rb;
+  int any = next_in_chunk ? 0 : 1;
+  for (int j = threadIdx.x; j < nkeys; j += 256) {
+    const int c = trow[j];
+    hist[j] = row_ptr[key0 + j] + coff[j] + c;
+    if (next_in_chunk) any |= trow[s_kv + j] - c;
+  }
+  if (!__syncthreads_or(any)) return;
   csr_for_pairs<kVec, true>(idx, S, s_kv, K, q_offset, row0, r0, r1, b, key0, nkeys,
                             [&](int u, int pair) { pairs[atomicAdd(&hist[u], 1)] = pair; });
 }
