@@ -431,6 +431,12 @@ def lightning_indexer_varlen(query, key, weights, cu_seqlens_q, cu_seqlens_k, sp
     indices are sequence-local (+ index_offset), -1 padded.  With compressed keys
     (cmp_ratio > 1), ``cmp_residual_k[i]`` original tokens follow the last whole block.
     Returns (indices int32 [T,K], values fp32 [T,K] or None).
+
+    Bounds given as GPU tensors are read on the device (dsa_lightning_indexer_tnd: no host
+    synchronisation, the same indices bit for bit) when the shape has a tile kernel (D_I
+    128, H_I a multiple of 16 up to 128, bf16 or fp8); otherwise, and for host bounds, the
+    host schedule (dsa_lightning_indexer_varlen) runs, reading GPU bounds back once per
+    tensor version.
     """
     lib = load_library()
     for t, n in ((query, "query"), (key, "key"), (weights, "weights")):
@@ -754,7 +760,9 @@ def _varlen_seqs(cu_seqlens_q, cu_seqlens_kv, T, T_kv):
 
 def sparse_mla_fwd_varlen(q, kv, indices, scale, cu_seqlens_q, cu_seqlens_kv, *, d_v=512):
     """Packed varlen forward (dsa_sparse_mla_fwd_varlen): q [T,H,D_qk], kv [T_kv,D_qk],
-    indices [T,K] sequence-local; returns (out [T,H,d_v], softmax_max [T,H], softmax_sum [T,H])."""
+    indices [T,K] sequence-local; returns (out [T,H,d_v], softmax_max [T,H], softmax_sum [T,H]).
+    With GPU-tensor bounds the batch runs as one launch on global key rows
+    (tnd_global_indices), with no host read; with host bounds, one launch per sequence."""
     lib = load_library()
     require_gpu_tensor(q, "q")
     T, H, D = q.shape
