@@ -66,7 +66,7 @@ def test_device_metadata_batch_rows_with_padding_and_mtp():
         meta = tnd.build_smla_attention_masks_device(p.to(DEV), args)
         _same(meta.host(), tnd.build_smla_attention_masks(p.to(DEV), args))
     bad = tnd.build_smla_attention_masks_device(pos.to(DEV), args)
-    with pytest.raises(ValueError, match="contiguous before padding"):
+    with pytest.raises(ValueError, match="padding must come after"):
         bad.host()
 
 

@@ -92,11 +92,11 @@ def test_padding_rules_and_errors():
     # padding after the valid tokens is dropped; the MTP column is not part of the sequence
     m = tnd.build_smla_attention_masks(torch.tensor([[0, 1, 2, 0, 1, -1, 7]]), _args((1,), n_mtp=1))
     assert m.cu_seqlens_q.tolist() == [0, 3, 5]
-    with pytest.raises(ValueError, match="contiguous before padding"):
+    with pytest.raises(ValueError, match="padding must come after"):
         tnd.build_smla_attention_masks(torch.tensor([[0, 1, -1, 3]]), _args((1,)))
-    with pytest.raises(ValueError, match="no valid tokens"):
+    with pytest.raises(ValueError, match="no entry is a valid"):
         tnd.build_smla_attention_masks(torch.tensor([[-1, -1, 5]]), _args((1,), n_mtp=1))
-    with pytest.raises(ValueError, match="batch size"):
+    with pytest.raises(ValueError, match="rows for an input batch"):
         tnd.build_smla_attention_masks(torch.zeros(2, 4, dtype=torch.long), _args((1,)), batch_size=3)
     # a first request that does not start at position 0 still starts a sequence
     m = tnd.build_smla_attention_masks(torch.tensor([5, 6, 7, 0, 1]), _args((4,)))
