@@ -44,6 +44,10 @@
  *                                lightning_indexer (converters/kernels/npu_smla.py:754-768),
  *                                sparse_flash_mla{,_grad} (:457-479, :540-568),
  *                                sparse_lightning_indexer_kl_loss_grad (:584-598)
+ *   dsa_lightning_indexer_tnd,   the same packed batches with cu_seqlens on the device (no host read):
+ *   dsa_tnd_global_indices       npu_lightning_indexer with actual_seq_lengths tensors
+ *                                (ops/aclnn/lightning_indexer/binding.cpp:14), and sequence-local
+ *                                slots as global key rows for the fixed-length attention / KL calls
  */
 #ifndef DSA_MI355X_H
 #define DSA_MI355X_H
